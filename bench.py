@@ -1,0 +1,196 @@
+"""Benchmark of the DSA hot path on one MI355X (the driver's contract).
+
+Workload (the one its metric is quoted on): bf16 DSA forward+backward
+over T = 16384 packed tokens in 4 causal documents (cu_seqlens 0/10363/15340/15537/16384),
+128 query heads over one shared 576-wide latent KV head (d_v 512, scale 1/sqrt(192)), indexer
+64 heads x 128, top-k 2048.  One step = lightning-indexer scores + top-k + sparse MLA forward
++ sparse MLA backward, all in the HIP kernels of libdsa_amd.so, inputs resident in HBM.
+
+value = algorithmic FLOPs of the step / step time:
+  sparse fwd 2176*H*N_sel + sparse bwd 5504*H*N_sel + indexer 2*Di*Hi*N_pairs
+(N_sel = sum_q min(K, visible keys) = 27,602,695; N_pairs = causally visible pairs).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "mcore-bridge_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "DSA sparse-attn fwd+bwd ms & TFLOP/s at S=16k, topk=2048; % of roofline"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def _cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(torch):
+    """Reference algorithm class on the host (oracle/dsa_oracle.py naive fp32 compositions):
+    dense indexer scores + full-row top-k, dense index-masked attention forward, autograd
+    backward; bounded sample of the same workload, algorithmic FLOPs / wall time."""
+    from oracle import dsa_oracle as O
+    from mcore_bridge_amd import workloads as W
+    S, H, Hi, Di, K = 2048, 16, 64, 128, 512
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(S, 1, H, 576, generator=g) * 0.1
+    kv = torch.randn(S, 1, 576, generator=g) * 0.1
+    qi = torch.randn(S, 1, Hi, Di, generator=g) * 0.1
+    ki = torch.randn(S, 1, Di, generator=g) * 0.1
+    w = torch.randn(S, 1, Hi, generator=g) / 8
+    dout = torch.randn(S, 1, H * 512, generator=g) * 0.01
+    mask = torch.triu(torch.full((S, S), float("-inf")), 1)[None]
+
+    def run():
+        _, ti = O.naive_fused_qk_topk_fp32(qi, ki, w, K, mask)
+        qq = q.clone().requires_grad_()
+        kk = kv.clone().requires_grad_()
+        o = O.naive_unfused_sparse_attn_fp32(qq, kk, ti, W.SM_SCALE)
+        o.backward(dout)
+        return o
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    nsel = W.n_sel([0, S], K)
+    flops = 7680 * H * nsel + 2 * Di * Hi * W.n_pairs([0, S])
+    return {
+        "value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one causal document S={S}, H={H} of 128 heads, Hi={Hi}, Di={Di}, top-k={K}: dense fp32 "
+                   f"indexer + full-row top-k, dense index-masked attention fwd + autograd bwd "
+                   f"(reference algorithm class), median of 3 = {t * 1e3:.0f} ms; cpu {_cpu_model()}, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build runs the DSA path on a single MI355X); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mcore_bridge_amd import ops, workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = W.CONFIGS["cfg3"]
+    T, H, K = cfg.S, cfg.H, cfg.K
+    cu = cfg.cu_seqlens
+    max_seqlen = max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    x = W.make_prefill(cfg, device=dev)
+    q, kv = x["q"].bfloat16(), x["kv"].bfloat16()
+    qi, ki, w = x["q_idx"].bfloat16(), x["k_idx"].bfloat16(), x["w"]
+    dout = x["dout"].bfloat16()
+    cu_t = x["cu_seqlens"]
+    del x
+    scale = W.SM_SCALE
+
+    ev = {k: [] for k in ("indexer_topk", "sparse_fwd", "sparse_bwd")}
+
+    def step(record: bool):
+        def mark():
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            return e
+        e0 = mark() if record else None
+        idx = ops.indexer_topk(qi, ki, w, K, cu_t, True, max_seqlen)
+        e1 = mark() if record else None
+        out, lse = ops.sparse_mla_fwd(q, kv, idx, scale, True)
+        e2 = mark() if record else None
+        dq, dkv = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, scale, True)
+        e3 = mark() if record else None
+        if record:
+            ev["indexer_topk"].append((e0, e1))
+            ev["sparse_fwd"].append((e1, e2))
+            ev["sparse_bwd"].append((e2, e3))
+        return dq, dkv
+
+    for i in range(args.warmup):
+        step(False)
+        print(f"[bench] warmup step {i + 1}/{args.warmup} done", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall / args.steps * 1e3
+    print(f"[bench] {args.steps} timed steps: {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    def avg_ms(name):
+        return statistics.mean(a.elapsed_time(b) for a, b in ev[name])
+
+    nsel = W.n_sel(cu, K)
+    npairs = W.n_pairs(cu)
+    fl_fwd = 2176 * H * nsel
+    fl_bwd = 5504 * H * nsel
+    fl_idx = 2 * cfg.Di * cfg.Hi * npairs
+    total = fl_fwd + fl_bwd + fl_idx
+    value = total / (ms_step * 1e-3) / 1e12
+    t_fwd, t_bwd, t_idx = avg_ms("sparse_fwd"), avg_ms("sparse_bwd"), avg_ms("indexer_topk")
+    # dominant single kernel measured live: the sparse MLA forward (one launch per step)
+    achieved = fl_fwd / (t_fwd * 1e-3) / 1e12
+    res = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "cfg3: bf16 DSA fwd+bwd, T=16384 packed varlen (cu_seqlens 0/10363/15340/15537/16384, "
+                        "causal per document), H=128, d_qk=576, d_v=512, indexer 64x128, top-k 2048",
+            "global_batch": 1, "seq_len": T, "parallelism": "single GPU",
+        },
+        "breakdown_ms": {"indexer_topk": round(t_idx, 3), "sparse_fwd": round(t_fwd, 3),
+                         "sparse_bwd": round(t_bwd, 3)},
+        "breakdown_tflops": {"indexer": round(fl_idx / t_idx / 1e9, 2), "sparse_fwd": round(fl_fwd / t_fwd / 1e9, 2),
+                             "sparse_bwd": round(fl_bwd / t_bwd / 1e9, 2),
+                             "sparse_fwd_bwd": round((fl_fwd + fl_bwd) / (t_fwd + t_bwd) / 1e9, 2)},
+        "roofline": {"bound": "mfma", "kernel": "sparse_mla_fwd_kernel", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

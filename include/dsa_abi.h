@@ -1,0 +1,107 @@
+/*
+ * dsa_abi.h -- C ABI of libdsa_amd.so, the MI355X (gfx950) DSA sparse-attention hot path.
+ *
+ * The reference (maomaocun/mcore-bridge) reaches this arithmetic through Python calls into
+ * Megatron-Core's DSA module; each entry point below replaces one of those calls:
+ *
+ *   dsa_indexer_scores + dsa_topk
+ *       replace fused_qk_topk_naive(q, k, weights, index_topk, mask), called from
+ *       DSAIndexer.forward_with_scores, reference src/mcore_bridge/patcher.py:349-358
+ *       (returns index_scores [B,S,S] and topk_indices [B,S,min(K,S)], patcher.py:357).
+ *   dsa_sparse_mla_fwd
+ *       replaces the un-fused sparse attention of DSAttention, invoked through
+ *       self.core_attention(...) at src/mcore_bridge/model/modules/multi_latent_attention.py:262-270.
+ *   dsa_sparse_mla_bwd
+ *       replaces torch autograd through that un-fused attention (the reference defines no
+ *       custom backward; multi_latent_attention.py:262-270 is the forward call site).
+ *
+ * Conventions
+ *   - All pointers are device pointers on the current HIP device, except where noted.
+ *   - Tensors are dense, row-major, and 16-byte aligned: q [T, H, 576] bf16, kv [N, 576] bf16,
+ *     out [T, H, 512] bf16, lse [T, H] fp32 (natural log), idx [T, K] int32.
+ *   - Indices are global row ids into kv (packed THD tokens, or cache rows); -1 = no key.
+ *   - Documents: cu_seqlens [n_seq + 1] int32 on the device, cu[0] = 0, cu[n_seq] = T.
+ *   - The caller owns every buffer, including workspaces; the library allocates nothing,
+ *     keeps no pointer past the call, and launches everything on `stream` (hipStream_t,
+ *     NULL = default stream) without synchronising the host.
+ *   - Return 0 on success, a negative dsa_status otherwise; dsa_strerror() explains it.
+ *     No C++ exception crosses the ABI.  Argument checks run before any device work, so an
+ *     error return means nothing was launched.
+ */
+#ifndef DSA_ABI_H_
+#define DSA_ABI_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  DSA_OK = 0,
+  DSA_ERR_INVALID_ARG = -1,   /* null pointer, bad shape, misaligned buffer, bad stride */
+  DSA_ERR_UNSUPPORTED = -2,   /* valid request this build does not implement (e.g. d_qk != 576) */
+  DSA_ERR_WORKSPACE = -3,     /* workspace missing or smaller than *_workspace_size() */
+  DSA_ERR_LAUNCH = -4,        /* a kernel launch failed (HIP error) */
+  DSA_ERR_DEVICE = -5         /* no usable gfx950 device */
+} dsa_status;
+
+typedef enum { DSA_BF16 = 0, DSA_FP8_E4M3 = 1 } dsa_dtype;
+
+/* ABI version (major * 100 + minor). */
+int dsa_abi_version(void);
+/* Static description of a status code. */
+const char* dsa_strerror(int status);
+
+/* Per-query visible-key rows of packed prefill tokens: row_base[t] = start of t's document,
+ * row_len[t] = t - start + 1 (causal) or the document length.  Feeds the indexer and top-k.
+ * Replaces the dense [B,S,S] causal float mask built by DSAttention before the indexer call
+ * (mask argument of fused_qk_topk_naive, patcher.py:358). */
+int dsa_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal,
+                   int32_t* row_base, int32_t* row_len, void* stream);
+
+/* Lightning-indexer scores (scoring half of fused_qk_topk_naive, patcher.py:358):
+ *   scores[t, j] = sum_h w[t,h] * relu(q[t,h,:] . k[row_base[t] + j, :]),  j < row_len[t].
+ * q [total_q, n_heads, head_dim], k [n_k, head_dim] in bf16 or OCP e4m3fn (then q_scale
+ * [total_q, n_heads] and k_scale [n_k] fp32 dequantise: x = x8 * scale); w [total_q, n_heads]
+ * fp32.  n_heads <= 64, head_dim in {64, 128}.  scores [total_q, pitch] fp32, pitch >=
+ * max_row_len; with fill_masked the columns [row_len, pitch) are set to -inf (the reference's
+ * masked layout). */
+int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const void* k, int k_dtype,
+                       const float* k_scale, const float* w, const int32_t* row_base,
+                       const int32_t* row_len, int total_q, int n_k, int n_heads, int head_dim,
+                       int max_row_len, float* scores, int64_t pitch, int fill_masked, void* stream);
+
+/* Top-k selection half of fused_qk_topk_naive (patcher.py:358): for each row the min(topk,
+ * row_len) largest scores (ties -> lower key), emitted as key ids row_base + j in ascending
+ * order, padded with -1.  out_idx [rows, topk] int32; out_count [rows] (nullable). */
+int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const int32_t* row_len,
+             int rows, int topk, int32_t* out_idx, int32_t* out_count, void* stream);
+
+/* Sparse MLA forward (DSAttention's un-fused sparse attention, multi_latent_attention.py:262-270),
+ * absorbed MQA-latent form: out[t,h] = softmax_j(sm_scale * q[t,h] . kv[idx[t,j]]) kv[idx[t,j], :512],
+ * lse[t,h] = ln sum_j exp(sm_scale * q[t,h] . kv[idx[t,j]]).  d_qk must be 576, d_v 512.
+ * causal != 0 additionally ignores indices > t (the reference's triu mask).  A row without
+ * a valid index yields out = 0, lse = -inf. */
+int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv,
+                       int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
+                       void* out, float* lse, void* stream);
+
+/* Workspace bytes for dsa_sparse_mla_bwd. */
+size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk);
+
+/* Sparse MLA backward (autograd of dsa_sparse_mla_fwd; replaces torch autograd through the
+ * un-fused attention called at multi_latent_attention.py:262-270).  Writes dq [T, H, 576] bf16
+ * and dkv [n_kv, 576] fp32 (every row written; rows no query selected are zero).
+ * n_heads <= 128 and a multiple of 16. */
+int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const void* out,
+                       const void* dout, const float* lse, int total_q, int n_kv, int n_heads,
+                       int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_ABI_H_ */

@@ -1,0 +1,161 @@
+// C-ABI entry points of libdsa_amd.so: argument validation, workspace carving, launch.
+// Declarations and the reference interfaces they replace: include/dsa_abi.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/dsa_abi.h"
+#include "dsa_kernels.h"
+
+namespace {
+
+constexpr int kDqk = 576;
+constexpr int kDv = 512;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+int topk_pad(int topk) { return (topk + 31) / 32 * 32; }
+
+size_t align_up(size_t x) { return (x + 255) / 256 * 256; }
+
+struct BwdLayout {
+  size_t p_stage, ds_stage, g_stage, pair_pos, offsets, counts, total;
+};
+
+BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
+  BwdLayout L{};
+  const size_t stage = align_up(sizeof(uint16_t) * (size_t)total_q * n_heads * topk_pad(topk));
+  size_t off = 0;
+  L.p_stage = off; off += stage;
+  L.ds_stage = off; off += stage;
+  L.g_stage = off; off += align_up(sizeof(uint16_t) * (size_t)total_q * topk * kDqk);
+  L.pair_pos = off; off += align_up(sizeof(int64_t) * (size_t)total_q * topk);
+  L.offsets = off; off += align_up(sizeof(int64_t) * ((size_t)n_kv + 1));
+  L.counts = off; off += align_up(sizeof(int32_t) * (size_t)n_kv);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_abi_version(void) { return 100; }
+
+const char* dsa_strerror(int status) {
+  switch (status) {
+    case DSA_OK: return "ok";
+    case DSA_ERR_INVALID_ARG: return "invalid argument (null pointer, shape, alignment or stride)";
+    case DSA_ERR_UNSUPPORTED: return "unsupported configuration for this build";
+    case DSA_ERR_WORKSPACE: return "workspace missing or too small";
+    case DSA_ERR_LAUNCH: return "kernel launch failed";
+    case DSA_ERR_DEVICE: return "no usable gfx950 device";
+    default: return "unknown dsa status";
+  }
+}
+
+int dsa_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,
+                   int32_t* row_len, void* stream) {
+  if (!cu_seqlens || !row_base || !row_len || n_seq < 1 || total_q < 0) return DSA_ERR_INVALID_ARG;
+  return dsa::launch_build_rows(cu_seqlens, n_seq, total_q, causal, row_base, row_len, as_stream(stream));
+}
+
+int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const void* k, int k_dtype,
+                       const float* k_scale, const float* w, const int32_t* row_base, const int32_t* row_len,
+                       int total_q, int n_k, int n_heads, int head_dim, int max_row_len, float* scores,
+                       int64_t pitch, int fill_masked, void* stream) {
+  if (total_q < 0 || n_k < 0 || n_heads < 1 || max_row_len < 0 || pitch < max_row_len) return DSA_ERR_INVALID_ARG;
+  if (total_q == 0) return DSA_OK;
+  if (!q || !k || !w || !row_base || !row_len || !scores) return DSA_ERR_INVALID_ARG;
+  if (q_dtype != k_dtype || (q_dtype != DSA_BF16 && q_dtype != DSA_FP8_E4M3)) return DSA_ERR_UNSUPPORTED;
+  const bool fp8 = q_dtype == DSA_FP8_E4M3;
+  if (fp8 && (!q_scale || !k_scale)) return DSA_ERR_INVALID_ARG;
+  if (n_heads > 64 || (head_dim != 64 && head_dim != 128)) return DSA_ERR_UNSUPPORTED;
+  if (!aligned16(q) || !aligned16(k)) return DSA_ERR_INVALID_ARG;
+  dsa::IndexerParams p{};
+  p.q = q; p.q_scale = q_scale; p.k = k; p.k_scale = k_scale; p.w = w;
+  p.row_base = row_base; p.row_len = row_len; p.scores = scores;
+  p.total_q = total_q; p.n_heads = n_heads; p.head_dim = head_dim; p.fp8 = fp8 ? 1 : 0;
+  p.max_row_len = max_row_len; p.pitch = pitch; p.fill_masked = fill_masked ? 1 : 0;
+  return dsa::launch_indexer_scores(p, as_stream(stream));
+}
+
+int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const int32_t* row_len, int rows,
+             int topk, int32_t* out_idx, int32_t* out_count, void* stream) {
+  if (rows < 0 || topk < 1 || pitch < 0) return DSA_ERR_INVALID_ARG;
+  if (rows == 0) return DSA_OK;
+  if (!scores || !row_base || !row_len || !out_idx) return DSA_ERR_INVALID_ARG;
+  dsa::TopkParams p{};
+  p.scores = scores; p.row_base = row_base; p.row_len = row_len; p.out_idx = out_idx; p.out_count = out_count;
+  p.rows = rows; p.topk = topk; p.pitch = pitch;
+  return dsa::launch_topk(p, as_stream(stream));
+}
+
+int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv, int n_heads,
+                       int d_qk, int d_v, int topk, float sm_scale, int causal, void* out, float* lse,
+                       void* stream) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
+  if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
+  if (total_q == 0) return DSA_OK;
+  if (!q || !kv || !idx || !out || !lse || n_kv < 1) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out)) return DSA_ERR_INVALID_ARG;
+  dsa::SparseFwdParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.kv = static_cast<const dsa::bf16_t*>(kv);
+  p.idx = idx;
+  p.out = static_cast<dsa::bf16_t*>(out);
+  p.lse = lse;
+  p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.causal = causal ? 1 : 0;
+  p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
+  p.out_stride_t = (int64_t)n_heads * kDv; p.lse_stride_t = n_heads;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  return dsa::launch_sparse_mla_fwd(p, as_stream(stream));
+}
+
+size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1) return 0;
+  return bwd_layout(total_q, n_kv, n_heads, topk).total;
+}
+
+int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
+                       const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
+                       float sm_scale, int causal, void* dq, float* dkv, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
+  if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
+  if (n_heads > 128 || n_heads % 16 != 0) return DSA_ERR_UNSUPPORTED;
+  if (!q || !kv || !idx || !out || !dout || !lse || !dq || !dkv) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(dout) || !aligned16(dq) || !aligned16(dkv))
+    return DSA_ERR_INVALID_ARG;
+  const BwdLayout L = bwd_layout(total_q, n_kv, n_heads, topk);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  dsa::SparseBwdParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.kv = static_cast<const dsa::bf16_t*>(kv);
+  p.idx = idx;
+  p.out = static_cast<const dsa::bf16_t*>(out);
+  p.dout = static_cast<const dsa::bf16_t*>(dout);
+  p.lse = lse;
+  p.dq = static_cast<dsa::bf16_t*>(dq);
+  p.dkv = dkv;
+  p.p_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.p_stage);
+  p.ds_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.ds_stage);
+  p.g_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.g_stage);
+  p.pair_pos = reinterpret_cast<int64_t*>(ws + L.pair_pos);
+  p.csr_offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
+  p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);
+  p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.topk_pad = topk_pad(topk);
+  p.causal = causal ? 1 : 0;
+  p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
+  p.out_stride_t = (int64_t)n_heads * kDv; p.dout_stride_t = (int64_t)n_heads * kDv;
+  p.lse_stride_t = n_heads; p.dq_stride_t = (int64_t)n_heads * kDqk; p.dkv_stride = kDqk;
+  p.scale = sm_scale;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  if (total_q == 0) return DSA_OK;
+  return dsa::launch_sparse_mla_bwd(p, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+// Shared device helpers for the gfx950 DSA kernels (CDNA4, wave64).
+//
+// MFMA operand layouts used throughout (checked on the device by tests/test_gpu_kernels.py
+// through the parity tests, and by construction below):
+//   v_mfma_f32_32x32x16_bf16  C[32x32] += A[32x16] * B[16x32]
+//     A: lane l holds A[row = l%32][k = (l/32)*8 + 0..7]
+//     B: lane l holds B[k = (l/32)*8 + 0..7][col = l%32]
+//     C: lane l holds C[row = (i/4)*8 + (l/32)*4 + i%4][col = l%32], i = 0..15
+//   v_mfma_f32_16x16x32_bf16  C[16x16] += A[16x32] * B[32x16]
+//     A: lane l holds A[row = l%16][k = (l/16)*8 + 0..7]
+//     B: lane l holds B[k = (l/16)*8 + 0..7][col = l%16]
+//     C: lane l holds C[row = (l/16)*4 + i][col = l%16], i = 0..3
+// The order of the k index inside one MFMA is free as long as A and B agree; the kernels
+// use that freedom to feed the C layout of one product straight into the next one.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define DSA_DEV __device__ __forceinline__
+
+namespace dsa {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+DSA_DEV f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+DSA_DEV f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+DSA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16-byte LDS / global access helpers.
+DSA_DEV u32x4 lds_load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+DSA_DEV void lds_store16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+DSA_DEV u32x4 gload16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+DSA_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+DSA_DEV u32x4 as_u32x4(const bf16x8& v) { return __builtin_bit_cast(u32x4, v); }
+
+// Pack two floats into one dword of two bf16 (round to nearest even).
+DSA_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  bf16_t a = (bf16_t)lo, b = (bf16_t)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+DSA_DEV float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
+DSA_DEV float bf16_hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xffff0000u); }
+
+// 8x8 transpose of 16-bit elements held as 8 rows x 4 dwords (row r = 8 consecutive
+// elements of one source row).  Output operand t (t = 0..7) gathers element t of each row:
+//   out[t].dword[n] = (row[2n].elem[t], row[2n+1].elem[t]).
+// v_perm_b32 selector 0x05040100 keeps the low halves, 0x07060302 the high halves.
+DSA_DEV void transpose8x8_b16(const u32x4 (&row)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const uint32_t a = row[2 * n][m];
+      const uint32_t b = row[2 * n + 1][m];
+      out[2 * m][n] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+      out[2 * m + 1][n] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+    }
+  }
+}
+
+// One output operand of the transpose above (lets the caller interleave with MFMAs).
+DSA_DEV u32x4 transpose8x8_b16_col(const u32x4 (&row)[8], int t) {
+  const int m = t >> 1;
+  const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+  u32x4 o;
+#pragma unroll
+  for (int n = 0; n < 4; ++n) o[n] = __builtin_amdgcn_perm(row[2 * n + 1][m], row[2 * n][m], sel);
+  return o;
+}
+
+// wave64 reductions (xor butterflies through ds_swizzle/dpp chosen by the compiler)
+DSA_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+DSA_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+DSA_DEV int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+DSA_DEV int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Combine a per-lane value with the lane 32 apart (same MFMA column, other row half).
+DSA_DEV float xor32_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
+DSA_DEV float xor32_sum(float v) { return v + __shfl_xor(v, 32, 64); }
+
+// Asynchronous 16-byte global -> LDS copy (gfx950 global_load_lds_dwordx4).  Lane i of the
+// wave writes 16 bytes at lds_wave_base + 16*i; lds_wave_base must be wave-uniform.
+DSA_DEV void async_copy16(const void* gsrc, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(const_cast<void*>(gsrc),
+                                   (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): all of this wave's vector-memory loads (including LDS-direct ones) done.
+DSA_DEV void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// XCD-aware remap of a 1-D grid: consecutive workgroup ids are spread round-robin over the
+// 8 XCDs, so give each XCD a contiguous run of work items (neighbouring query tokens share
+// most of their selected KV rows, and then share that XCD's L2).
+DSA_DEV int xcd_remap(int bid, int n_items) {
+  const int per = (n_items + 7) >> 3;
+  return (bid & 7) * per + (bid >> 3);
+}
+
+}  // namespace dsa

@@ -1,0 +1,316 @@
+// K1: lightning-indexer scores, K2: per-row top-k selection (gfx950).
+//
+// Replaces fused_qk_topk_naive(q, k, weights, index_topk, mask) as called from
+// DSAIndexer.forward_with_scores (reference src/mcore_bridge/patcher.py:358):
+//   I[t, s] = sum_h w[t,h] * relu(q[t,h,:] . k[s,:])      (fp32 accumulate)
+//   topk_indices[t] = the min(K, n_t) largest I[t, .] over the visible keys, ties -> lower key.
+// A query row is described by (row_base, row_len): its visible keys are row_base + [0, row_len).
+// Prefill with documents: row_base = document start, row_len = t - start + 1 (causal) or the
+// document length; decode: row_base = cache offset, row_len = cache length.  Scores are written
+// row-major with column j <-> key row_base + j, which is also the layout of the reference's
+// returned index_scores when there is one document.
+//
+// K1: one wave = one (query, 2048-key chunk).  Q[64 heads x 128] stays in registers as the A
+// operand (row = head), key rows are the B operand loaded straight from global memory (256 B
+// per key, shared by the 4 waves of a workgroup through L1/L2); C[heads x 32 keys] is reduced
+// over heads in registers: each lane holds 16 heads of one key, so ReLU * w and the head sum
+// are lane-local plus one exchange with the lane 32 apart.
+// fp8 (OCP e4m3fn, gfx950 MFMA native): I = k_scale[s] * sum_h (w * q_scale)[t,h] *
+// relu(q8 . k8) -- valid because ReLU is positive-homogeneous and both scales are > 0.
+//
+// K2: one workgroup per row.  4 passes of 8-bit MSB-first radix select over order-preserving
+// uint32 keys (LDS histograms) find the exact K-th largest value; one stable compaction pass
+// (block-wide prefix sums) then emits every larger key plus the lowest-index ties, in ascending
+// key order, -1 padded.
+#include "dsa_common.h"
+#include "dsa_kernels.h"
+
+namespace dsa {
+
+namespace {
+constexpr int kIdxChunk = 2048;   // keys per wave work item
+constexpr int kMaxHi = 64;        // indexer heads handled by the register tiling
+}  // namespace
+
+template <bool FP8>
+__global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= p.total_q) return;
+  const int len = p.row_len[t];
+  const int c0 = blockIdx.y * kIdxChunk;
+  if (c0 >= len) return;
+  const int c1 = min(len, c0 + kIdxChunk);
+  const int base = p.row_base[t];
+  const int hb = lane >> 5, hl = lane & 31;
+  const int Di = p.head_dim;        // 64 or 128
+  const int nks = Di / 16;          // 4 or 8 k-steps of 16
+
+  // per-lane weights for the 16 head rows of each of the 2 row tiles (heads >= n_heads -> 0)
+  float wr[2][16];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int h = 32 * mt + (i >> 2) * 8 + 4 * hb + (i & 3);
+      float w = h < p.n_heads ? p.w[(int64_t)t * p.n_heads + h] : 0.f;
+      if (FP8 && h < p.n_heads) w *= p.q_scale[(int64_t)t * p.n_heads + h];
+      wr[mt][i] = w;
+    }
+  }
+  if (!FP8) {
+    const bf16_t* q = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)t * p.n_heads * Di;
+    const bf16_t* k = reinterpret_cast<const bf16_t*>(p.k);
+    u32x4 qa[2][8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int h = 32 * mt + hl;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        qa[mt][ks] = (h < p.n_heads && ks < nks) ? gload16(q + (int64_t)h * Di + 16 * ks + 8 * hb) : u32x4{0, 0, 0, 0};
+    }
+    for (int k0 = c0; k0 < c1; k0 += 32) {
+      const int j = k0 + hl;
+      const int key = base + (j < c1 ? j : c0);
+      const bf16_t* krow = k + (int64_t)key * Di + 8 * hb;
+      u32x4 kb[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) kb[ks] = ks < nks ? gload16(krow + 16 * ks) : u32x4{0, 0, 0, 0};
+      f32x16 c0a = f32x16{}, c1a = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        c0a = mfma32x32x16(as_bf16x8(qa[0][ks]), as_bf16x8(kb[ks]), c0a);
+        c1a = mfma32x32x16(as_bf16x8(qa[1][ks]), as_bf16x8(kb[ks]), c1a);
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc += wr[0][i] * fmaxf(c0a[i], 0.f) + wr[1][i] * fmaxf(c1a[i], 0.f);
+      acc = xor32_sum(acc);
+      if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc;
+    }
+  } else {
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(p.q) + (int64_t)t * p.n_heads * Di;
+    const uint8_t* k = reinterpret_cast<const uint8_t*>(p.k);
+    long qa[2][8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int h = 32 * mt + hl;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        qa[mt][ks] = (h < p.n_heads && ks < nks) ? *reinterpret_cast<const long*>(q + (int64_t)h * Di + 16 * ks + 8 * hb) : 0l;
+    }
+    for (int k0 = c0; k0 < c1; k0 += 32) {
+      const int j = k0 + hl;
+      const int key = base + (j < c1 ? j : c0);
+      const uint8_t* krow = k + (int64_t)key * Di + 8 * hb;
+      long kb[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) kb[ks] = ks < nks ? *reinterpret_cast<const long*>(krow + 16 * ks) : 0l;
+      f32x16 c0a = f32x16{}, c1a = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        c0a = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qa[0][ks], kb[ks], c0a, 0, 0, 0);
+        c1a = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qa[1][ks], kb[ks], c1a, 0, 0, 0);
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc += wr[0][i] * fmaxf(c0a[i], 0.f) + wr[1][i] * fmaxf(c1a[i], 0.f);
+      acc = xor32_sum(acc);
+      if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc * p.k_scale[key];
+    }
+  }
+}
+
+// Fill the masked tail [row_len, pitch) of each score row with -inf (only when the caller
+// wants the reference's dense [S, S] index_scores).
+__global__ void scores_fill_masked_kernel(float* scores, int64_t pitch, const int32_t* row_len, int rows) {
+  const int t = blockIdx.x;
+  if (t >= rows) return;
+  for (int64_t j = row_len[t] + threadIdx.x; j < pitch; j += blockDim.x) scores[(int64_t)t * pitch + j] = -INFINITY;
+}
+
+int launch_indexer_scores(const IndexerParams& p, hipStream_t stream) {
+  if (p.n_heads > kMaxHi || (p.head_dim != 128 && p.head_dim != 64)) return -2;
+  int max_len = p.max_row_len;
+  const dim3 grid((p.total_q + 3) / 4, (max_len + kIdxChunk - 1) / kIdxChunk);
+  if (grid.y == 0) return 0;
+  if (p.fp8)
+    hipLaunchKernelGGL(indexer_scores_kernel<true>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(indexer_scores_kernel<false>, grid, dim3(256), 0, stream, p);
+  if (p.fill_masked)
+    hipLaunchKernelGGL(scores_fill_masked_kernel, dim3(p.total_q), dim3(256), 0, stream, p.scores, p.pitch,
+                       p.row_len, p.total_q);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// ------------------------------------------------------------------------------------------
+// K2: top-k
+// ------------------------------------------------------------------------------------------
+namespace {
+constexpr int kTopkThreads = 512;
+constexpr int kCacheElems = 16384;  // rows up to this length are cached in LDS (64 KB)
+
+DSA_DEV uint32_t order_key(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u << 1) == 0) u = 0;  // -0.0 -> +0.0 (equal values must tie)
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Block-wide exclusive scan of one int per thread (kTopkThreads threads); returns the prefix
+// and writes the total to *total.
+DSA_DEV int block_exclusive_scan(int v, int* sh, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += n;
+  }
+  if (lane == 63) sh[wave] = incl;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < kTopkThreads / 64; ++w) {
+      const int x = sh[w];
+      sh[w] = run;
+      run += x;
+    }
+    sh[kTopkThreads / 64] = run;
+  }
+  __syncthreads();
+  const int res = sh[wave] + incl - v;
+  *total = sh[kTopkThreads / 64];
+  __syncthreads();
+  return res;
+}
+}  // namespace
+
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
+  __shared__ uint32_t cache[kCacheElems];
+  __shared__ int hist[256];
+  __shared__ int sh[kTopkThreads / 64 + 1];
+  __shared__ uint32_t sel_prefix;
+  __shared__ int sel_need;
+  const int row = blockIdx.x;
+  if (row >= p.rows) return;
+  const int n = p.row_len[row];
+  const int base = p.row_base[row];
+  const int K = p.topk;
+  int32_t* out = p.out_idx + (int64_t)row * K;
+  const float* sc = p.scores + (int64_t)row * p.pitch;
+
+  if (n <= K) {  // everything visible is selected
+    for (int j = threadIdx.x; j < K; j += blockDim.x) out[j] = j < n ? base + j : -1;
+    if (p.out_count && threadIdx.x == 0) p.out_count[row] = n;
+    return;
+  }
+  const bool cached = n <= kCacheElems;
+  if (cached)
+    for (int j = threadIdx.x; j < n; j += blockDim.x) cache[j] = order_key(sc[j]);
+  auto key_at = [&](int j) -> uint32_t { return cached ? cache[j] : order_key(sc[j]); };
+
+  // ---- radix select: find the K-th largest key (prefix over the top 32 bits)
+  uint32_t prefix = 0, pmask = 0;
+  int need = K;  // still to take from the keys matching the current prefix
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) hist[b] = 0;
+    __syncthreads();
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+      const uint32_t u = key_at(j);
+      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {  // one wave: suffix scan of 256 bins, 4 per lane (lane 0 = top bins)
+      const int l = threadIdx.x;
+      const int b0 = 255 - 4 * l;
+      const int c0 = hist[b0], c1 = hist[b0 - 1], c2 = hist[b0 - 2], c3 = hist[b0 - 3];
+      const int tot = c0 + c1 + c2 + c3;
+      int incl = tot;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if (l >= o) incl += v;
+      }
+      const int excl = incl - tot;  // keys in bins above b0
+      if (excl < need && need <= incl) {
+        int above = excl, bin = b0;
+        const int cs[4] = {c0, c1, c2, c3};
+        for (int q = 0; q < 4; ++q) {
+          if (above + cs[q] >= need) { bin = b0 - q; break; }
+          above += cs[q];
+        }
+        sel_prefix = prefix | ((uint32_t)bin << shift);
+        sel_need = need - above;
+      }
+    }
+    __syncthreads();
+    prefix = sel_prefix;
+    need = sel_need;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  const uint32_t thr = prefix;  // exact K-th largest key; take `need` of the keys equal to it
+
+  // ---- stable compaction in ascending index order
+  const int per = (n + kTopkThreads - 1) / kTopkThreads;
+  const int a = min(n, (int)threadIdx.x * per), b = min(n, a + per);
+  int c_gt = 0, c_eq = 0;
+  for (int j = a; j < b; ++j) {
+    const uint32_t u = key_at(j);
+    c_gt += u > thr;
+    c_eq += u == thr;
+  }
+  int tot_gt, tot_eq;
+  const int gt_before = block_exclusive_scan(c_gt, sh, &tot_gt);
+  const int eq_before = block_exclusive_scan(c_eq, sh, &tot_eq);
+  int pos = gt_before + min(eq_before, need);
+  int eq_rank = eq_before;
+  for (int j = a; j < b; ++j) {
+    const uint32_t u = key_at(j);
+    bool take = u > thr;
+    if (u == thr) {
+      take = eq_rank < need;
+      ++eq_rank;
+    }
+    if (take) out[pos++] = base + j;
+  }
+  if (p.out_count && threadIdx.x == 0) p.out_count[row] = K;
+}
+
+int launch_topk(const TopkParams& p, hipStream_t stream) {
+  if (p.rows == 0) return 0;
+  hipLaunchKernelGGL(topk_kernel, dim3(p.rows), dim3(kTopkThreads), 0, stream, p);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace dsa
+
+// ------------------------------------------------------------------------------------------
+// Row descriptors of packed prefill queries from cu_seqlens (documents, causal or not).
+// ------------------------------------------------------------------------------------------
+namespace dsa {
+
+__global__ void build_rows_kernel(const int32_t* cu_seqlens, int n_seq, int total_q, int causal,
+                                  int32_t* row_base, int32_t* row_len) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= total_q) return;
+  int lo = 0, hi = n_seq;  // find document d with cu[d] <= t < cu[d+1]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cu_seqlens[mid] <= t) lo = mid; else hi = mid;
+  }
+  const int start = cu_seqlens[lo], end = cu_seqlens[lo + 1];
+  row_base[t] = start;
+  row_len[t] = causal ? t - start + 1 : end - start;
+}
+
+int launch_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,
+                      int32_t* row_len, hipStream_t stream) {
+  if (total_q == 0) return 0;
+  hipLaunchKernelGGL(build_rows_kernel, dim3((total_q + 255) / 256), dim3(256), 0, stream, cu_seqlens, n_seq,
+                     total_q, causal, row_base, row_len);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace dsa

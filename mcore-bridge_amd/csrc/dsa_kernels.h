@@ -1,0 +1,75 @@
+// Internal launch interface between the C-ABI layer (dsa_abi.cpp) and the HIP kernels.
+// Pointers are device pointers; strides are in elements.  The C-ABI validates every field
+// before a launcher is called, so the kernels may assume the documented shapes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsa {
+
+typedef __bf16 bf16_t;
+
+struct SparseFwdParams {
+  const bf16_t* q;      // [total_q, n_heads, 576], token stride q_stride_t
+  const bf16_t* kv;     // [n_kv, 576], row stride kv_stride
+  const int32_t* idx;   // [total_q, topk] global kv row ids, -1 = none
+  bf16_t* out;          // [total_q, n_heads, 512], token stride out_stride_t
+  float* lse;           // [total_q, n_heads] natural-log LSE, token stride lse_stride_t
+  int total_q, n_heads, n_kv, topk, causal;
+  int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, lse_stride_t;
+  float scale_log2;     // softmax scale * log2(e)
+};
+
+struct SparseBwdParams {
+  const bf16_t* q;      // [total_q, n_heads, 576]
+  const bf16_t* kv;     // [n_kv, 576]
+  const int32_t* idx;   // [total_q, topk]
+  const bf16_t* out;    // [total_q, n_heads, 512]
+  const bf16_t* dout;   // [total_q, n_heads, 512]
+  const float* lse;     // [total_q, n_heads]
+  bf16_t* dq;           // [total_q, n_heads, 576]
+  float* dkv;           // [n_kv, 576] fp32 (fully written, no accumulation into old contents)
+  // workspace (carved by the C-ABI from one caller buffer)
+  bf16_t* p_stage;      // [total_q, n_heads, topk_pad]  P
+  bf16_t* ds_stage;     // [total_q, n_heads, topk_pad]  scale * dS
+  bf16_t* g_stage;      // [n_pairs, 576] per-pair dKV partial rows in key-major order
+  int64_t* pair_pos;    // [total_q, topk] row of G for each pair (-1 = not selected)
+  int64_t* csr_offsets; // [n_kv + 1]
+  int32_t* csr_counts;  // [n_kv] counts, then per-key cursor
+  int total_q, n_heads, n_kv, topk, topk_pad, causal;
+  int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, dout_stride_t, lse_stride_t, dq_stride_t, dkv_stride;
+  float scale, scale_log2;
+};
+
+struct IndexerParams {
+  const void* q;        // [total_q, n_heads, head_dim] bf16 or e4m3fn
+  const float* q_scale; // [total_q, n_heads] (fp8 only) or null
+  const void* k;        // [n_k, head_dim] bf16 or e4m3fn
+  const float* k_scale; // [n_k] (fp8 only) or null
+  const float* w;       // [total_q, n_heads]
+  const int32_t* row_base;  // per query: key id of score column 0
+  const int32_t* row_len;   // per query: number of visible keys
+  float* scores;        // [total_q, pitch]; column j <-> key row_base[t] + j
+  int total_q, n_heads, head_dim, fp8, max_row_len;
+  int64_t pitch;
+  int fill_masked;      // also write -inf into columns [row_len, pitch)
+};
+
+struct TopkParams {
+  const float* scores;       // [rows, pitch]
+  const int32_t* row_base;   // per row: key id of column 0
+  const int32_t* row_len;    // per row: number of valid columns
+  int32_t* out_idx;          // [rows, topk] key ids, ascending, -1 padded
+  int32_t* out_count;        // [rows] number selected, or null
+  int rows, topk;
+  int64_t pitch;
+};
+
+int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
+int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream);
+int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
+int launch_topk(const TopkParams& p, hipStream_t stream);
+int launch_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,
+                      int32_t* row_len, hipStream_t stream);
+
+}  // namespace dsa

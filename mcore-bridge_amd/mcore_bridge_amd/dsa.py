@@ -1,0 +1,105 @@
+"""Megatron-compatible entry points of the DSA hot path (sequence-first ``sbhd`` layouts).
+
+``fused_qk_topk_naive`` keeps the name, argument order, layouts and return values of the
+function that reference ``DSAIndexer.forward_with_scores`` imports and calls at
+src/mcore_bridge/patcher.py:349-358, so reassigning
+``megatron.core.transformer.experimental_attention_variant.dsa.fused_qk_topk_naive`` to it
+swaps the implementation without model-code changes (see ``patch.py``).
+
+``sparse_mla_attention`` is the absorbed-layout counterpart of the un-fused sparse attention
+that DSAttention runs on the indexer output (call site
+src/mcore_bridge/model/modules/multi_latent_attention.py:262-270): one shared 576-wide latent KV
+head, ``v = kv[..., :512]``, causal ``triu`` mask applied on top of the index mask.
+
+Both run entirely in the HIP kernels of libdsa_amd.so; torch ops here only reshape, cast and
+reorder indices.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import ops
+
+
+def _is_causal_mask(mask: Tensor) -> bool:
+    """True if ``mask`` [B, S, S] is the float causal mask DSAttention builds (0 on/below the
+    diagonal, -inf above)."""
+    S = mask.shape[-1]
+    if mask.shape[-2] != S:
+        return False
+    ref = torch.triu(torch.full((S, S), float("-inf"), device=mask.device, dtype=mask.dtype), diagonal=1)
+    return bool(torch.equal(mask, ref.expand_as(mask)))
+
+
+def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
+                        mask: Optional[Tensor] = None, *, causal: Optional[bool] = None,
+                        return_scores: bool = True, q_scale: Optional[Tensor] = None,
+                        k_scale: Optional[Tensor] = None) -> Tuple[Optional[Tensor], Tensor]:
+    """Drop-in for Megatron's ``fused_qk_topk_naive`` (called at reference patcher.py:358).
+
+    ``q [S, B, Hi, Di]``, ``k [S, B, Di]``, ``weights [S, B, Hi]``, ``mask [B, S, S]`` float
+    (0 / -inf) or None.  Returns ``(index_scores [B, S, S] fp32, topk_indices [B, S, min(K, S)]
+    int64)`` with ``index_scores[b,t,s] = sum_h weights[t,b,h] relu(q[t,b,h] . k[s,b]) + mask``
+    and the indices ordered like ``torch.topk`` (score descending) with the tie rule made
+    explicit: equal scores -- including the ``-inf`` of masked keys -- go to the lower index.
+
+    Keyword extensions: ``causal`` skips the mask inspection (True = the triu mask);
+    ``return_scores=False`` skips materialising the ``[B, S, S]`` scores (first output None);
+    ``q_scale [S, B, Hi]`` / ``k_scale [S, B]`` with float8_e4m3fn ``q`` / ``k``.
+    """
+    S, B, Hi, Di = q.shape
+    kk = min(index_topk, S)
+    if causal is None:
+        causal = mask is not None and _is_causal_mask(mask)
+    general_mask = mask is not None and not causal
+    scores_out = torch.empty(B, S, S, dtype=torch.float32, device=q.device) if (return_scores or general_mask) else None
+    idx_out = torch.empty(B, S, kk, dtype=torch.int64, device=q.device)
+    cu = torch.tensor([0, S], dtype=torch.int32, device=q.device)
+    for b in range(B):
+        qb, kb, wb = q[:, b].contiguous(), k[:, b].contiguous(), weights[:, b].to(torch.float32).contiguous()
+        qs = q_scale[:, b].contiguous() if q_scale is not None else None
+        ks = k_scale[:, b].contiguous() if k_scale is not None else None
+        base, ln = ops.build_rows(cu, S, bool(causal))
+        need_scores = scores_out is not None
+        sc = ops.indexer_scores(qb, kb, wb, base, ln, S, S, qs, ks, need_scores)
+        if general_mask:
+            sc = sc + mask[b].to(torch.float32)
+        idx = ops.topk(sc, base, ln, kk).to(torch.int64)            # ascending key ids, -1 pad
+        if causal:
+            # masked (-inf) keys of row t are t+1, t+2, ...: a stable top-k takes them in order,
+            # so the padding slot j holds key j.
+            slot = torch.arange(kk, device=q.device).expand_as(idx)
+            idx = torch.where(idx < 0, slot, idx)
+        # reference order: score descending, ties to the lower index (stable sort of an
+        # ascending-index list)
+        vals = torch.gather(sc, 1, idx.clamp(min=0))
+        vals = torch.where(idx < 0, torch.full_like(vals, float("-inf")), vals)
+        order = torch.sort(vals, dim=1, descending=True, stable=True).indices
+        idx_out[b] = torch.gather(idx, 1, order)
+        if scores_out is not None:
+            scores_out[b] = sc
+    return (scores_out if return_scores else None), idx_out
+
+
+def sparse_mla_attention(query: Tensor, kv: Tensor, topk_indices: Tensor, softmax_scale: float,
+                         d_v: int = 512, causal: bool = True) -> Tensor:
+    """Absorbed sparse MLA attention in Megatron's sequence-first layout.
+
+    ``query [S, B, H, 576]`` bf16, ``kv [S, B, 576]`` bf16 (the shared latent head, ``v =
+    kv[..., :d_v]``), ``topk_indices [B, S, K]`` (per-batch key positions; negative = none).
+    Returns ``[S, B, H * d_v]`` like the un-fused reference attention; differentiable w.r.t.
+    ``query`` and ``kv``.  ``causal`` applies the reference's ``triu`` mask on top of the index
+    mask.
+    """
+    S, B, H, D = query.shape
+    assert d_v == ops.D_V and D == ops.D_QK, "absorbed MLA layout: 576-wide q/kv, d_v = 512"
+    q_thd = query.transpose(0, 1).reshape(B * S, H, D)
+    kv_thd = kv.transpose(0, 1).reshape(B * S, D)
+    off = (torch.arange(B, device=query.device, dtype=torch.int64) * S).view(B, 1, 1)
+    ti = topk_indices.to(torch.int64)
+    idx = torch.where(ti >= 0, ti + off, torch.full_like(ti, -1)).reshape(B * S, -1).to(torch.int32)
+    out = ops.sparse_mla(q_thd, kv_thd, idx, softmax_scale, causal)     # [B*S, H, 512]
+    return out.reshape(B, S, H * d_v).transpose(0, 1)

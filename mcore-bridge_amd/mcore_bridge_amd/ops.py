@@ -1,0 +1,224 @@
+"""PyTorch custom ops over the C ABI (include/dsa_abi.h).
+
+These are the kernel-native ops in the packed THD layout:
+  q [T, H, 576] bf16, kv [N, 576] bf16, idx [T, K] int32 (global kv row ids, -1 pad),
+  out [T, H, 512] bf16, lse [T, H] fp32.
+PyTorch only supplies device memory (caching allocator) and the current stream; every op
+launches the HIP kernels of libdsa_amd.so and raises if a tensor is not on the GPU.  The
+Megatron-compatible call signatures (sbhd layouts, ``fused_qk_topk_naive``) are in ``dsa.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+D_QK = 576
+D_V = 512
+
+
+def _p(t: Optional[Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _require_gpu(*ts: Optional[Tensor]) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"dsa_amd ops run on the GPU (gfx950) only; got a tensor on {t.device}")
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AssertionError(msg)
+
+
+# --------------------------------------------------------------------------------------
+# row descriptors (documents -> per-query visible key ranges)
+# --------------------------------------------------------------------------------------
+@torch.library.custom_op("dsa_amd::build_rows", mutates_args=())
+def build_rows(cu_seqlens: Tensor, total_q: int, causal: bool) -> Tuple[Tensor, Tensor]:
+    """Per-token ``(row_base, row_len)`` int32 from ``cu_seqlens`` (int32, on the GPU)."""
+    _require_gpu(cu_seqlens)
+    cu = cu_seqlens.to(torch.int32).contiguous()
+    base = torch.empty(total_q, dtype=torch.int32, device=cu.device)
+    ln = torch.empty(total_q, dtype=torch.int32, device=cu.device)
+    with torch.cuda.device(cu.device):
+        _lib.call("dsa_build_rows", _p(cu), cu.numel() - 1, total_q, int(causal), _p(base), _p(ln), _stream(cu.device))
+    return base, ln
+
+
+@build_rows.register_fake
+def _(cu_seqlens, total_q, causal):
+    return (cu_seqlens.new_empty(total_q, dtype=torch.int32), cu_seqlens.new_empty(total_q, dtype=torch.int32))
+
+
+# --------------------------------------------------------------------------------------
+# K1 indexer scores
+# --------------------------------------------------------------------------------------
+@torch.library.custom_op("dsa_amd::indexer_scores", mutates_args=())
+def indexer_scores(q: Tensor, k: Tensor, w: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
+                   pitch: int, q_scale: Optional[Tensor] = None, k_scale: Optional[Tensor] = None,
+                   fill_masked: bool = False) -> Tensor:
+    """``scores[t, j] = sum_h w[t,h] relu(q[t,h] . k[row_base[t] + j])`` for ``j < row_len[t]``.
+
+    ``q [T, Hi, Di]``, ``k [N, Di]`` bf16 or float8_e4m3fn (then ``q_scale [T, Hi]`` and
+    ``k_scale [N]`` fp32), ``w [T, Hi]``.  Returns fp32 ``[T, pitch]``; columns past ``row_len``
+    are ``-inf`` when ``fill_masked`` and unspecified otherwise."""
+    _require_gpu(q, k, w, row_base, row_len, q_scale, k_scale)
+    T, Hi, Di = q.shape
+    fp8 = q.dtype == torch.float8_e4m3fn
+    _require(k.dtype == q.dtype and k.dim() == 2 and k.shape[1] == Di, "k must be [N, Di] with q's dtype")
+    _require(q.dtype in (torch.bfloat16, torch.float8_e4m3fn), "q must be bf16 or float8_e4m3fn")
+    _require(not fp8 or (q_scale is not None and k_scale is not None), "fp8 inputs need q_scale and k_scale")
+    q = q.contiguous()
+    k = k.contiguous()
+    w = w.to(torch.float32).contiguous()
+    qs = q_scale.to(torch.float32).contiguous() if fp8 else None
+    ks = k_scale.to(torch.float32).contiguous() if fp8 else None
+    scores = torch.empty(T, pitch, dtype=torch.float32, device=q.device)
+    dt = _lib.DSA_FP8_E4M3 if fp8 else _lib.DSA_BF16
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_indexer_scores", _p(q), dt, _p(qs), _p(k), dt, _p(ks), _p(w), _p(row_base.contiguous()),
+                  _p(row_len.contiguous()), T, k.shape[0], Hi, Di, max_row_len, _p(scores), pitch,
+                  int(fill_masked), _stream(q.device))
+    return scores
+
+
+@indexer_scores.register_fake
+def _(q, k, w, row_base, row_len, max_row_len, pitch, q_scale=None, k_scale=None, fill_masked=False):
+    return q.new_empty(q.shape[0], pitch, dtype=torch.float32)
+
+
+# --------------------------------------------------------------------------------------
+# K2 top-k
+# --------------------------------------------------------------------------------------
+@torch.library.custom_op("dsa_amd::topk", mutates_args=())
+def topk(scores: Tensor, row_base: Tensor, row_len: Tensor, k: int) -> Tensor:
+    """Per row the ``min(k, row_len)`` largest scores (ties -> lower key) as ascending key ids
+    ``row_base + j``, ``-1`` padded.  int32 ``[rows, k]``."""
+    _require_gpu(scores, row_base, row_len)
+    _require(scores.dtype == torch.float32 and scores.dim() == 2, "scores must be fp32 [rows, pitch]")
+    s = scores if scores.stride(1) == 1 else scores.contiguous()
+    rows = s.shape[0]
+    out = torch.empty(rows, k, dtype=torch.int32, device=s.device)
+    with torch.cuda.device(s.device):
+        _lib.call("dsa_topk", _p(s), s.stride(0), _p(row_base.contiguous()), _p(row_len.contiguous()), rows, k,
+                  _p(out), ctypes.c_void_p(0), _stream(s.device))
+    return out
+
+
+@topk.register_fake
+def _(scores, row_base, row_len, k):
+    return scores.new_empty(scores.shape[0], k, dtype=torch.int32)
+
+
+def indexer_topk(q: Tensor, k: Tensor, w: Tensor, index_topk: int, cu_seqlens: Optional[Tensor] = None,
+                 causal: bool = True, max_seqlen: Optional[int] = None, q_scale: Optional[Tensor] = None,
+                 k_scale: Optional[Tensor] = None, return_scores: bool = False):
+    """K1 + K2 over packed documents.  Returns ``idx [T, index_topk]`` int32 (global key ids,
+    ascending, ``-1`` pad) and, with ``return_scores``, the fp32 scores ``[T, max_seqlen]``
+    (column j <-> key ``doc_start(t) + j``)."""
+    T = q.shape[0]
+    if cu_seqlens is None:
+        cu_seqlens = torch.tensor([0, T], dtype=torch.int32, device=q.device)
+        max_seqlen = T
+    if max_seqlen is None:
+        max_seqlen = int((cu_seqlens[1:] - cu_seqlens[:-1]).max().item())
+    base, ln = build_rows(cu_seqlens.to(torch.int32), T, causal)
+    pitch = max(4, (max_seqlen + 3) // 4 * 4)
+    sc = indexer_scores(q, k, w, base, ln, max_seqlen, pitch, q_scale, k_scale, return_scores)
+    idx = topk(sc, base, ln, index_topk)
+    return (idx, sc) if return_scores else idx
+
+
+# --------------------------------------------------------------------------------------
+# K3 / K4 sparse MLA
+# --------------------------------------------------------------------------------------
+def _check_attn(q: Tensor, kv: Tensor, idx: Tensor) -> None:
+    _require_gpu(q, kv, idx)
+    _require(q.dim() == 3 and q.shape[-1] == D_QK, f"q must be [T, H, {D_QK}]")
+    _require(kv.dim() == 2 and kv.shape[-1] == D_QK, f"kv must be [N, {D_QK}]")
+    _require(idx.dim() == 2 and idx.shape[0] == q.shape[0], "idx must be [T, K]")
+    _require(q.dtype == torch.bfloat16 and kv.dtype == torch.bfloat16, "q and kv must be bf16")
+
+
+@torch.library.custom_op("dsa_amd::sparse_mla_fwd", mutates_args=())
+def sparse_mla_fwd(q: Tensor, kv: Tensor, idx: Tensor, sm_scale: float, causal: bool = False) -> Tuple[Tensor, Tensor]:
+    """Absorbed sparse MLA forward: ``(out [T,H,512] bf16, lse [T,H] fp32)``."""
+    _check_attn(q, kv, idx)
+    q = q.contiguous()
+    kv = kv.contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, H, _ = q.shape
+    out = torch.empty(T, H, D_V, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_sparse_mla_fwd", _p(q), _p(kv), _p(idx), T, kv.shape[0], H, D_QK, D_V, idx.shape[1],
+                  float(sm_scale), int(causal), _p(out), _p(lse), _stream(q.device))
+    return out, lse
+
+
+@sparse_mla_fwd.register_fake
+def _(q, kv, idx, sm_scale, causal=False):
+    T, H, _ = q.shape
+    return q.new_empty(T, H, D_V), q.new_empty(T, H, dtype=torch.float32)
+
+
+def bwd_workspace_bytes(total_q: int, n_kv: int, n_heads: int, topk_: int) -> int:
+    return int(_lib.load().dsa_sparse_mla_bwd_workspace_size(total_q, n_kv, n_heads, topk_))
+
+
+@torch.library.custom_op("dsa_amd::sparse_mla_bwd", mutates_args=())
+def sparse_mla_bwd(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sm_scale: float,
+                   causal: bool = False) -> Tuple[Tensor, Tensor]:
+    """Gradients of ``sparse_mla_fwd``: ``(dq [T,H,576] bf16, dkv [N,576] fp32)``."""
+    _check_attn(q, kv, idx)
+    _require_gpu(out, dout, lse)
+    q, kv, out, lse = q.contiguous(), kv.contiguous(), out.contiguous(), lse.contiguous()
+    dout = dout.to(torch.bfloat16).contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, H, _ = q.shape
+    N, K = kv.shape[0], idx.shape[1]
+    dq = torch.empty_like(q)
+    dkv = torch.empty(N, D_QK, dtype=torch.float32, device=q.device)
+    ws_bytes = bwd_workspace_bytes(T, N, H, K)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_sparse_mla_bwd", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), T, N, H, D_QK, D_V, K,
+                  float(sm_scale), int(causal), _p(dq), _p(dkv), _p(ws), ws_bytes, _stream(q.device))
+    return dq, dkv
+
+
+@sparse_mla_bwd.register_fake
+def _(q, kv, idx, out, dout, lse, sm_scale, causal=False):
+    return torch.empty_like(q), kv.new_empty(kv.shape[0], D_QK, dtype=torch.float32)
+
+
+def _fwd_setup(ctx, inputs, output):
+    q, kv, idx, sm_scale, causal = inputs
+    out, lse = output
+    ctx.save_for_backward(q, kv, idx, out, lse)
+    ctx.sm_scale = sm_scale
+    ctx.causal = causal
+
+
+def _fwd_backward(ctx, dout, dlse):
+    q, kv, idx, out, lse = ctx.saved_tensors
+    dq, dkv = sparse_mla_bwd(q, kv, idx, out, dout, lse, ctx.sm_scale, ctx.causal)
+    return dq, dkv.to(kv.dtype), None, None, None
+
+
+torch.library.register_autograd("dsa_amd::sparse_mla_fwd", _fwd_backward, setup_context=_fwd_setup)
+
+
+def sparse_mla(q: Tensor, kv: Tensor, idx: Tensor, sm_scale: float, causal: bool = False) -> Tensor:
+    """Differentiable sparse MLA attention output ``[T, H, 512]``."""
+    return sparse_mla_fwd(q, kv, idx, sm_scale, causal)[0]

@@ -1,0 +1,349 @@
+"""CPU oracle for the DSA sparse-attention hot path (TEST INFRASTRUCTURE ONLY).
+
+This module is the checker, never the product: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The shipped path (``mcore-bridge_amd``) never calls into it and
+raises when its HIP library is missing.
+
+It restates, in float64 PyTorch on the CPU, the arithmetic that
+mcore-bridge routes through Megatron-Core's DSA module:
+
+* ``DSAIndexer.forward_with_scores`` (reference ``src/mcore_bridge/patcher.py:326-360``)
+  calls ``fused_qk_topk_naive(q, k, weights, index_topk, mask)`` (``patcher.py:358``),
+  which lives in the third-party dependency ``megatron-core>=0.16,<0.19``
+  (``requirements.txt:1``; 0.17.1 recommended at ``README.md:113``), module
+  ``megatron.core.transformer.experimental_attention_variant.dsa``.  That package is
+  not vendored under the reference and not installed here, so its published algorithm
+  is restated: ``I[t,s] = sum_h w[t,h] * relu(q[t,h,:] . k[s,:]) + mask[t,s]`` followed by
+  ``topk(I, min(K, S))``.  The same formula is spelled out by the in-container
+  third-party analog ``transformers/models/deepseek_v32/modeling_deepseek_v32.py:240-256``.
+* ``DSAttention`` (called from ``src/mcore_bridge/model/modules/multi_latent_attention.py:262-270``)
+  runs Megatron's un-fused sparse attention: dense ``q.k`` scores, a ``-inf`` mask that
+  is ``0`` only at the top-k indices, the causal ``triu`` mask, fp32 softmax and ``P.V``.
+  Restated here in gather form (``sparse_mla_fwd``) and in the dense masked form
+  (``sparse_mla_fwd_dense``).  Backward is plain autograd in the reference; restated
+  here as the closed-form gradient (``sparse_mla_bwd``).
+
+Layouts follow the build's absorbed MQA-latent form (one shared 576-wide KV row per
+token, ``v = kv[:, :512]``), packed THD: ``q [T, H, 576]``, ``kv [T, 576]``,
+``idx [T, K]`` of global token ids with ``-1`` padding, ``out [T, H, 512]``,
+``lse [T, H]``.  Documents are given by ``cu_seqlens`` (``None`` means one
+document of length T); "causal" means key ``s`` is visible from query ``t`` iff
+``doc_start(t) <= s <= t``.
+
+Pinning (each function is checked by tests/test_oracle.py against something that is
+not its own formula): brute-force loops, the Hadamard invariance of the indexer
+(``patcher.py:292-293``), positive homogeneity of ReLU (fp8 scale folding), the HF
+third-party indexer, the dense masked form, ``scaled_dot_product_attention`` when
+``K >= S``, the MLA absorption identity, autograd/gradcheck for the backward, the
+per-document split for varlen and the last prefill row for decode.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+NEG_INF = float("-inf")
+
+
+# --------------------------------------------------------------------------------------
+# documents / visibility
+# --------------------------------------------------------------------------------------
+def doc_bounds(T: int, cu_seqlens: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-token ``(doc_start, doc_end)`` from ``cu_seqlens`` ([n+1] int, cu[0]=0, cu[-1]=T)."""
+    if cu_seqlens is None:
+        cu = torch.tensor([0, T], dtype=torch.int64)
+    else:
+        cu = cu_seqlens.to(torch.int64).cpu()
+    assert int(cu[0]) == 0 and int(cu[-1]) == T, "cu_seqlens must start at 0 and end at T"
+    start = torch.empty(T, dtype=torch.int64)
+    end = torch.empty(T, dtype=torch.int64)
+    for i in range(cu.numel() - 1):
+        a, b = int(cu[i]), int(cu[i + 1])
+        start[a:b] = a
+        end[a:b] = b
+    return start, end
+
+
+def visibility_mask(T: int, cu_seqlens: Optional[torch.Tensor] = None, causal: bool = True) -> torch.Tensor:
+    """Boolean ``[T, T]``: True where key s is visible from query t."""
+    start, end = doc_bounds(T, cu_seqlens)
+    s = torch.arange(T)[None, :]
+    vis = (s >= start[:, None]) & (s < end[:, None])
+    if causal:
+        vis &= s <= torch.arange(T)[:, None]
+    return vis
+
+
+# --------------------------------------------------------------------------------------
+# lightning indexer  (fused_qk_topk_naive scoring half, called at patcher.py:358)
+# --------------------------------------------------------------------------------------
+def indexer_scores(q_idx: torch.Tensor, k_idx: torch.Tensor, w: torch.Tensor,
+                   cu_seqlens: Optional[torch.Tensor] = None, causal: bool = True,
+                   q_scale: Optional[torch.Tensor] = None, k_scale: Optional[torch.Tensor] = None,
+                   mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense ``[T, T]`` float64 index scores, ``-inf`` where the key is not visible.
+
+    ``I[t,s] = sum_h w[t,h] * relu(qd[t,h,:] . kd[s,:])`` with ``qd = q_idx * q_scale[t,h]``
+    and ``kd = k_idx * k_scale[s]`` when fp8 scales are given (per-(token, head) block scale
+    for q, per-token scale for k).  ``mask`` (optional ``[T, T]`` additive float) is added
+    like the reference's ``mask`` argument of ``fused_qk_topk_naive``.
+    """
+    T, Hi, Di = q_idx.shape
+    qd = q_idx.to(torch.float64)
+    kd = k_idx.to(torch.float64)
+    if q_scale is not None:
+        qd = qd * q_scale.to(torch.float64)[:, :, None]
+    if k_scale is not None:
+        kd = kd * k_scale.to(torch.float64)[:, None]
+    logits = torch.einsum("thd,sd->ths", qd, kd)           # [T, Hi, T]
+    scores = (torch.relu(logits) * w.to(torch.float64)[:, :, None]).sum(dim=1)  # [T, T]
+    vis = visibility_mask(T, cu_seqlens, causal)
+    scores = scores.masked_fill(~vis, NEG_INF)
+    if mask is not None:
+        scores = scores + mask.to(torch.float64)
+    return scores
+
+
+def indexer_scores_bruteforce(q_idx, k_idx, w, cu_seqlens=None, causal=True):
+    """Triple loop restatement of ``indexer_scores`` for tiny shapes (pins the einsum)."""
+    T, Hi, Di = q_idx.shape
+    vis = visibility_mask(T, cu_seqlens, causal)
+    out = torch.full((T, T), NEG_INF, dtype=torch.float64)
+    q = q_idx.to(torch.float64).tolist()
+    k = k_idx.to(torch.float64).tolist()
+    ww = w.to(torch.float64).tolist()
+    for t in range(T):
+        for s in range(T):
+            if not vis[t, s]:
+                continue
+            acc = 0.0
+            for h in range(Hi):
+                dot = 0.0
+                for d in range(Di):
+                    dot += q[t][h][d] * k[s][d]
+                acc += ww[t][h] * max(dot, 0.0)
+            out[t, s] = acc
+    return out
+
+
+# --------------------------------------------------------------------------------------
+# top-k  (fused_qk_topk_naive selection half)
+# --------------------------------------------------------------------------------------
+def topk_reference_order(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Top ``min(k, #finite)`` keys per row ordered by (score desc, index asc); ``-1`` pad.
+
+    This is ``torch.topk(scores, min(k, S))`` with the tie rule made explicit (ties go to
+    the lower index) and masked (``-inf``) keys never selected.
+    """
+    T, S = scores.shape
+    kk = min(k, S)
+    out = torch.full((T, kk), -1, dtype=torch.int64)
+    idx = torch.arange(S)
+    for t in range(T):
+        row = scores[t]
+        fin = torch.isfinite(row)
+        cand = idx[fin]
+        vals = row[fin]
+        # stable sort on (-score, index): sort by index first (already), then stable by -score
+        order = torch.sort(-vals, stable=True).indices
+        sel = cand[order][:kk]
+        out[t, : sel.numel()] = sel
+    return out
+
+
+def topk_indices(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Canonical kernel order: the same selected set as ``topk_reference_order``, ascending
+    index, ``-1`` padding at the end."""
+    ref = topk_reference_order(scores, k)
+    big = torch.iinfo(torch.int64).max
+    srt = torch.where(ref < 0, torch.full_like(ref, big), ref).sort(dim=1).values
+    return torch.where(srt == big, torch.full_like(srt, -1), srt)
+
+
+def topk_bruteforce(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Python ``sorted`` restatement of ``topk_indices`` (pins the tie rule)."""
+    T, S = scores.shape
+    kk = min(k, S)
+    out = torch.full((T, kk), -1, dtype=torch.int64)
+    for t in range(T):
+        items = [(-float(scores[t, s]), s) for s in range(S) if math.isfinite(float(scores[t, s]))]
+        items.sort()
+        sel = sorted(s for _, s in items[:kk])
+        out[t, : len(sel)] = torch.tensor(sel, dtype=torch.int64)
+    return out
+
+
+# --------------------------------------------------------------------------------------
+# sparse MLA attention (DSAttention's un-fused sparse attention, caller multi_latent_attention.py:262-270)
+# --------------------------------------------------------------------------------------
+def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, sm_scale: float,
+                   d_v: int = 512, chunk: int = 256) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gather-form sparse MQA over the latent KV.
+
+    ``out[t,h] = sum_{j: idx[t,j] >= 0} softmax_j(sm_scale * q[t,h] . kv[idx[t,j]]) kv[idx[t,j], :d_v]``
+    and ``lse[t,h] = log sum_j exp(sm_scale * q[t,h] . kv[idx[t,j]])`` (natural log).  A row
+    with no valid index yields ``out = 0`` and ``lse = -inf``.
+    """
+    T, H, D = q.shape
+    out = torch.zeros(T, H, d_v, dtype=torch.float64)
+    lse = torch.full((T, H), NEG_INF, dtype=torch.float64)
+    kv64 = kv.to(torch.float64)
+    for a in range(0, T, chunk):
+        b = min(T, a + chunk)
+        ii = idx[a:b].to(torch.int64)
+        valid = ii >= 0
+        g = kv64[ii.clamp(min=0)]                               # [c, K, D]
+        s = torch.einsum("thd,tkd->thk", q[a:b].to(torch.float64), g) * sm_scale
+        s = s.masked_fill(~valid[:, None, :], NEG_INF)
+        m = s.amax(dim=-1, keepdim=True)
+        m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+        p = torch.exp(s - m)
+        l = p.sum(dim=-1, keepdim=True)
+        o = torch.einsum("thk,tkd->thd", p, g[..., :d_v])
+        nz = l > 0
+        out[a:b] = torch.where(nz, o / torch.where(nz, l, torch.ones_like(l)), torch.zeros_like(o))
+        lse[a:b] = torch.where(nz[..., 0], (m + torch.log(l))[..., 0], torch.full_like(l[..., 0], NEG_INF))
+    return out, lse
+
+
+def sparse_mla_fwd_dense(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, sm_scale: float,
+                         d_v: int = 512, cu_seqlens: Optional[torch.Tensor] = None,
+                         causal: bool = True) -> torch.Tensor:
+    """Dense masked restatement of Megatron's un-fused sparse attention.
+
+    Scores for all ``[T, T]`` pairs, an index mask that is ``0`` at the selected keys and
+    ``-inf`` elsewhere, plus the causal / document mask, float softmax, then ``P V``.
+    Differentiable (used with autograd to pin ``sparse_mla_bwd``).
+    """
+    T, H, D = q.shape
+    sel = torch.zeros(T, T, dtype=torch.bool)
+    ii = idx.to(torch.int64)
+    rows = torch.arange(T)[:, None].expand_as(ii)
+    ok = ii >= 0
+    sel[rows[ok], ii[ok]] = True
+    sel &= visibility_mask(T, cu_seqlens, causal)
+    s = torch.einsum("thd,sd->hts", q, kv) * sm_scale          # [H, T, T]
+    s = s.masked_fill(~sel[None], NEG_INF)
+    p = torch.softmax(s, dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)
+    return torch.einsum("hts,sd->thd", p, kv[:, :d_v])
+
+
+def sparse_mla_bwd(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, out: torch.Tensor,
+                   dout: torch.Tensor, lse: torch.Tensor, sm_scale: float, d_v: int = 512,
+                   chunk: int = 256) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Closed-form gradients of ``sparse_mla_fwd``.
+
+    ``P = exp(sm_scale*S - lse)``, ``dP = dO . V^T``, ``Delta = rowsum(dO * O)``,
+    ``dS = P * (dP - Delta)``; ``dQ = sm_scale * dS . K``;
+    ``dKV[s] += sm_scale * dS^T Q`` (all 576 columns) ``+ P^T dO`` (first ``d_v`` columns),
+    summed over every (query, head) that selected key ``s``.
+    """
+    T, H, D = q.shape
+    q64, kv64 = q.to(torch.float64), kv.to(torch.float64)
+    do64, o64 = dout.to(torch.float64), out.to(torch.float64)
+    dq = torch.zeros(T, H, D, dtype=torch.float64)
+    dkv = torch.zeros(kv.shape[0], D, dtype=torch.float64)
+    delta = (do64 * o64).sum(-1)                                    # [T, H]
+    for a in range(0, T, chunk):
+        b = min(T, a + chunk)
+        ii = idx[a:b].to(torch.int64)
+        valid = ii >= 0
+        ic = ii.clamp(min=0)
+        g = kv64[ic]                                               # [c, K, D]
+        s = torch.einsum("thd,tkd->thk", q64[a:b], g) * sm_scale
+        l = lse[a:b].to(torch.float64)[..., None]
+        p = torch.where(valid[:, None, :] & torch.isfinite(l), torch.exp(s - l), torch.zeros_like(s))
+        dp = torch.einsum("thv,tkv->thk", do64[a:b], g[..., :d_v])
+        ds = p * (dp - delta[a:b, :, None])
+        dq[a:b] = sm_scale * torch.einsum("thk,tkd->thd", ds, g)
+        contrib = sm_scale * torch.einsum("thk,thd->tkd", ds, q64[a:b])
+        contrib[..., :d_v] += torch.einsum("thk,thv->tkv", p, do64[a:b])
+        contrib = contrib * valid[..., None]
+        dkv.index_add_(0, ic.reshape(-1), contrib.reshape(-1, D))
+    return dq, dkv
+
+
+# --------------------------------------------------------------------------------------
+# decode (no reference counterpart: the reference has no DSA cache, patcher.py:256)
+# --------------------------------------------------------------------------------------
+def decode_indexer_scores(q_idx: torch.Tensor, k_cache: torch.Tensor, w: torch.Tensor,
+                          cache_offsets: torch.Tensor, cache_lens: torch.Tensor,
+                          q_scale=None, k_scale=None) -> torch.Tensor:
+    """Per-sequence scores of one new query (position L_b - 1) over its whole cache.
+
+    ``q_idx [B, Hi, Di]``, ``k_cache [sum L, Di]`` (rows ``offset_b .. offset_b + L_b``),
+    ``w [B, Hi]`` -> ``[B, max L]`` float64 with ``-inf`` beyond ``L_b``.
+    """
+    B = q_idx.shape[0]
+    Lmax = int(cache_lens.max())
+    out = torch.full((B, Lmax), NEG_INF, dtype=torch.float64)
+    for b in range(B):
+        o, L = int(cache_offsets[b]), int(cache_lens[b])
+        kd = k_cache[o:o + L].to(torch.float64)
+        if k_scale is not None:
+            kd = kd * k_scale[o:o + L].to(torch.float64)[:, None]
+        qd = q_idx[b].to(torch.float64)
+        if q_scale is not None:
+            qd = qd * q_scale[b].to(torch.float64)[:, None]
+        lg = qd @ kd.T                                            # [Hi, L]
+        out[b, :L] = (torch.relu(lg) * w[b].to(torch.float64)[:, None]).sum(0)
+    return out
+
+
+def sparse_mla_decode(q: torch.Tensor, kv_cache: torch.Tensor, idx: torch.Tensor, sm_scale: float,
+                      d_v: int = 512) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Decode attention: ``q [B, H, 576]`` over rows ``kv_cache[idx[b]]`` (global cache row
+    ids, ``-1`` pad).  Same arithmetic as ``sparse_mla_fwd`` with one query per sequence."""
+    return sparse_mla_fwd(q, kv_cache, idx, sm_scale, d_v=d_v, chunk=8)
+
+
+# --------------------------------------------------------------------------------------
+# the reference's own naive compositions, fp32 (the CPU baseline that bench.py times)
+# --------------------------------------------------------------------------------------
+def naive_fused_qk_topk_fp32(q_sbhd: torch.Tensor, k_sbd: torch.Tensor, w_sbh: torch.Tensor,
+                             index_topk: int, mask: Optional[torch.Tensor]):
+    """Shape-for-shape fp32 restatement of ``fused_qk_topk_naive(q, k, weights, index_topk, mask)``
+    as called at ``patcher.py:358``: materialises ``[S, B, Hi, S]`` logits, then a full-row
+    ``topk``.  Returns ``(index_scores [B,S,S], topk_indices [B,S,min(K,S)])``."""
+    logits = torch.einsum("sbhd,tbd->sbht", q_sbhd.float(), k_sbd.float())
+    scores = (torch.relu(logits) * w_sbh.float().unsqueeze(-1)).sum(dim=2).transpose(0, 1)
+    if mask is not None:
+        scores = scores + mask
+    kk = min(index_topk, scores.shape[-1])
+    return scores, scores.topk(kk, dim=-1).indices
+
+
+def naive_unfused_sparse_attn_fp32(q_sbhd: torch.Tensor, kv_sbd: torch.Tensor, topk_idx: torch.Tensor,
+                                   sm_scale: float, d_v: int = 512) -> torch.Tensor:
+    """Shape-for-shape fp32 restatement of Megatron's un-fused sparse attention in the absorbed
+    layout: dense ``[B*H, S, S]`` scores, index mask scattered to 0 at ``topk_idx``, causal
+    ``triu`` mask, float softmax, ``P V``.  ``q [S,B,H,576]``, ``kv [S,B,576]`` -> ``[S,B,H*d_v]``."""
+    S, B, H, D = q_sbhd.shape
+    qf = q_sbhd.float().permute(1, 2, 0, 3)                          # [B, H, S, D]
+    kf = kv_sbd.float().permute(1, 0, 2)                             # [B, S, D]
+    s = torch.matmul(qf, kf.transpose(1, 2).unsqueeze(1)) * sm_scale  # [B, H, S, S]
+    imask = torch.full((B, S, S), NEG_INF)
+    imask.scatter_(-1, topk_idx, 0.0)
+    imask = imask + torch.triu(torch.full((S, S), NEG_INF), diagonal=1)[None]
+    p = torch.softmax(s + imask[:, None], dim=-1)
+    o = torch.matmul(p, kf[:, None, :, :d_v])                        # [B, H, S, d_v]
+    return o.permute(2, 0, 1, 3).reshape(S, B, H * d_v)
+
+
+# --------------------------------------------------------------------------------------
+# fp8 (OCP e4m3fn) quantisation used by config 4
+# --------------------------------------------------------------------------------------
+E4M3_MAX = 448.0
+
+
+def quantize_e4m3_rows(x: torch.Tensor):
+    """Absmax-per-last-dim quantisation to ``torch.float8_e4m3fn``: ``scale = absmax/448``
+    (``1`` for an all-zero row); returns ``(x_fp8, scale)`` with ``x ~= x_fp8 * scale``."""
+    amax = x.abs().amax(dim=-1).to(torch.float32)
+    scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+    xq = (x.to(torch.float32) / scale[..., None]).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return xq, scale

@@ -1,0 +1,89 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/dsa_abi.h declares,
+and rejects invalid arguments before touching a device (so these run without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from mcore_bridge_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsa_abi.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 8
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_version_and_strerror():
+    lib = _lib.load()
+    assert lib.dsa_abi_version() >= 100
+    for code in (0, -1, -2, -3, -4, -5):
+        assert len(_lib.strerror(code)) >= 2
+    assert "unknown" in _lib.strerror(-99)
+
+
+N = ctypes.c_void_p(0)
+P = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+
+
+def test_invalid_arguments_rejected_before_launch():
+    lib = _lib.load()
+    # d_qk must be 576
+    assert lib.dsa_sparse_mla_fwd(P, P, P, 4, 4, 16, 512, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_UNSUPPORTED
+    # null pointer
+    assert lib.dsa_sparse_mla_fwd(N, P, P, 4, 4, 16, 576, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
+    # misaligned
+    assert lib.dsa_sparse_mla_fwd(ctypes.c_void_p(4098), P, P, 4, 4, 16, 576, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
+    # non-finite scale
+    assert lib.dsa_sparse_mla_fwd(P, P, P, 4, 4, 16, 576, 512, 8, float("nan"), 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
+    # zero-size work is a no-op
+    assert lib.dsa_sparse_mla_fwd(N, N, N, 0, 4, 16, 576, 512, 8, 0.1, 1, N, N, N) == _lib.DSA_OK
+    # indexer: too many heads / bad head_dim / dtype mismatch / fp8 without scales
+    args = lambda hi, di, qd, kd, qs: (P, qd, qs, P, kd, qs, P, P, P, 4, 4, hi, di, 4, P, 4, 0, N)
+    assert lib.dsa_indexer_scores(*args(65, 128, 0, 0, P)) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_indexer_scores(*args(64, 96, 0, 0, P)) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_indexer_scores(*args(64, 128, 0, 1, P)) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_indexer_scores(*args(64, 128, 1, 1, N)) == _lib.DSA_ERR_INVALID_ARG
+    # pitch smaller than the longest row
+    assert lib.dsa_indexer_scores(P, 0, N, P, 0, N, P, P, P, 4, 4, 4, 64, 9, P, 8, 0, N) == _lib.DSA_ERR_INVALID_ARG
+    # top-k: k < 1, null output
+    assert lib.dsa_topk(P, 8, P, P, 4, 0, P, N, N) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_topk(P, 8, P, P, 4, 2, N, N, N) == _lib.DSA_ERR_INVALID_ARG
+    # backward: heads not a multiple of 16, workspace too small
+    assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 24, 576, 512, 8, 0.1, 1, P, P, P, 1 << 30, N) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 32, 576, 512, 8, 0.1, 1, P, P, P, 16, N) == _lib.DSA_ERR_WORKSPACE
+    # rows: bad n_seq
+    assert lib.dsa_build_rows(P, 0, 4, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
+
+
+def test_bwd_workspace_size_formula():
+    lib = _lib.load()
+    T, N, H, K = 16384, 16384, 128, 2048
+    ws = lib.dsa_sparse_mla_bwd_workspace_size(T, N, H, K)
+    stage = T * H * K * 2
+    assert ws >= 2 * stage + T * K * 576 * 2 + T * K * 8
+    assert ws < 2 * stage + T * K * 576 * 2 + T * K * 8 + 64 * N + 4096
+    assert lib.dsa_sparse_mla_bwd_workspace_size(-1, N, H, K) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    from mcore_bridge_amd import ops
+    q = torch.zeros(4, 16, 576, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 576, dtype=torch.bfloat16)
+    idx = torch.zeros(4, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.sparse_mla_fwd(q, kv, idx, 0.1, True)
