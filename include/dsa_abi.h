@@ -20,6 +20,8 @@
  *   - Tensors are dense, row-major, and 16-byte aligned: q [T, H, 576] bf16, kv [N, 576] bf16,
  *     out [T, H, 512] bf16, lse [T, H] fp32 (natural log), idx [T, K] int32.
  *   - Indices are global row ids into kv (packed THD tokens, or cache rows); -1 = no key.
+ *     The valid indices of one row must be distinct (a top-k never repeats a key); ids outside
+ *     [0, n_kv) are treated like -1.
  *   - Documents: cu_seqlens [n_seq + 1] int32 on the device, cu[0] = 0, cu[n_seq] = T.
  *   - The caller owns every buffer, including workspaces; the library allocates nothing,
  *     keeps no pointer past the call, and launches everything on `stream` (hipStream_t,

