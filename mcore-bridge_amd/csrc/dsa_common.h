@@ -116,6 +116,27 @@ DSA_DEV void async_copy16(const void* gsrc, void* lds_wave_base) {
                                    (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
 }
 
+// LDS byte address of a pointer into __shared__ memory.
+DSA_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// The same copy issued through inline asm (M0 = wave-uniform LDS base).  The compiler does not
+// model it, so it neither serialises later LDS reads against it nor waits for it: the caller
+// owns completion (s_waitcnt vmcnt(N) + barrier) -- that is what lets a multi-stage gather ring
+// overlap the MFMA work on earlier stages.
+DSA_DEV void async_copy16_unordered(const void* gsrc, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(gsrc)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | expcnt=7 | lgkmcnt=15 | vmcnt[5:4] << 14).
+template <int N>
+DSA_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | 0xF00 | ((N >> 4) << 14));
+}
+
 // s_waitcnt vmcnt(0): all of this wave's vector-memory loads (including LDS-direct ones) done.
 DSA_DEV void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

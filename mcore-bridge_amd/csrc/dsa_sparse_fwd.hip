@@ -8,21 +8,23 @@
 // Work decomposition (one workgroup = one query token, up to 128 heads):
 //   * wave w owns 32 heads.  Q[32 heads x 576] sits in registers for the whole key loop (the B
 //     operand of S^T = K . Q^T, 144 VGPRs), the output accumulator O^T[512 x 32 heads] in fp32
-//     (256 registers, AGPR-backed).  Keeping O transposed puts all accumulators of one lane on a
-//     single head, so the online-softmax rescale needs no cross-lane traffic.
-//   * selected KV rows are gathered 32 at a time straight into LDS with global_load_lds (16 B per
-//     lane, no VGPR staging), double buffered: row pitch 73 x 16 B (one pad chunk) makes the
-//     32-row column reads of the QK product bank-conflict free.
-//   * QK: 36 MFMA 32x32x16 per 32-key block; PV: O^T += V^T . P^T, where the V^T operand comes
-//     from ds_read_b64_tr_b16 (hardware 16-bit transpose on the LDS read) and P^T is the S^T
-//     accumulator converted to bf16 in place (the k order inside each MFMA is permuted to
-//     match the S^T C layout, so no shuffle is needed).
+//     (256 AGPRs).  Keeping O transposed puts all accumulators of one lane on a single head.
+//   * the query's index row is staged once in LDS; selected KV rows are gathered 32 at a time
+//     straight into LDS with global_load_lds (16 B per lane, no VGPR staging, swizzled tile of
+//     dsa_kvtile.h) through a 3-stage ring, so block j+2 streams in while block j is
+//     multiplied.  The copies are issued through inline asm and completed with explicit
+//     s_waitcnt vmcnt(G) + barrier (every wave issues the same G copies per block).
+//   * QK: 36 MFMA 32x32x16 per 32-key block, A operands prefetched 3 MFMAs ahead;
+//     PV: O^T += V^T . P^T, V^T from ds_read_b64_tr_b16 (hardware 16-bit transpose on the LDS
+//     read), P^T is the S^T accumulator converted to bf16 in place (the k order inside each
+//     MFMA is permuted to match the S^T C layout, so no shuffle is needed).
 //   * softmax in the exp2 domain against a per-head reference max fixed by the first valid
 //     block (2^64 headroom), so the O accumulators are never rescaled (a rescale would pull the
 //     256 AGPR accumulators through VGPRs).  A query whose scores overshoot the headroom is
 //     recomputed once with its exact row max.
 #include "dsa_common.h"
 #include "dsa_kernels.h"
+#include "dsa_kvtile.h"
 
 namespace dsa {
 
@@ -30,12 +32,11 @@ namespace {
 
 constexpr int kDqk = 576;
 constexpr int kDv = 512;
-constexpr int kChunks = kDqk / 8;       // 72 16-byte chunks per latent row
-constexpr int kPitch = kChunks + 1;     // LDS row pitch in chunks (pad = bank-conflict free)
-constexpr int kBK = 32;                 // keys per block (lane l%32 holds the index of key l%32)
-constexpr int kGatherInstr = (kBK * kPitch + 63) / 64;   // 37 wave-instructions per block
-constexpr int kBufBytes = kGatherInstr * 1024;
+constexpr int kBK = kTileKeys;          // keys per block (lane l%32 <-> key l%32)
+constexpr int kStages = 3;
+constexpr int kMaxTopk = 8192;
 constexpr float kHeadroom = 64.0f;      // log2 headroom above the reference max
+constexpr int kPre = 3;                 // LDS operand prefetch distance (MFMAs)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -45,46 +46,28 @@ DSA_DEV u32x2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-// Issue the LDS-direct gather of one 32-key block.  Slot p (16 B) of the buffer holds
-// row p / 73, chunk p % 73 (chunk 72 is the pad; slots past the last row are filler).
-// Wave-instruction n covers slots 64n..64n+63.
-DSA_DEV void gather_block(char* buf, const bf16_t* kv, int64_t kv_stride, int row_id_lane,
-                          int wave, int nwaves, int lane) {
-  for (int n = wave; n < kGatherInstr; n += nwaves) {
-    const int p = n * 64 + lane;
-    const int r = p / kPitch;
-    const int c = p - r * kPitch;
-    const int row = __shfl(row_id_lane, r & 31, 64);
-    const bf16_t* src = kv;
-    if (r < kBK && row >= 0 && c < kChunks) src = kv + (int64_t)row * kv_stride + c * 8;
-    async_copy16(src, buf + n * 1024);
-  }
-}
+struct FwdSmem {
+  char tile[kStages][kTileBytes];
+  int32_t idx[kMaxTopk];
+  int red[4];
+  int redo_flag;
+};
 
 }  // namespace
 
-__global__ __launch_bounds__(256, 1) void sparse_mla_fwd_kernel(SparseFwdParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kBufBytes];
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdParams p) {
+  constexpr int G = tile_copies_per_wave<NW>();
+  __shared__ __attribute__((aligned(16))) FwdSmem sm;
 
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
   const int hb = lane >> 5;          // row half of the MFMA C layout
   const int hl = lane & 31;          // head within the wave
   const int head = blockIdx.y * 128 + wave * 32 + hl;
   const bool head_ok = head < p.n_heads;
-  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
-
-  // ---- number of key blocks: up to the last valid index of the row
-  int last = -1;
-  for (int j = lane; j < p.topk; j += 64) {
-    const int v = idx_row[j];
-    if (v >= 0 && v < p.n_kv && (!p.causal || v <= t)) last = j;
-  }
-  last = wave_max_i(last);
-  const int nblk = (last + kBK) / kBK;
 
   // ---- Q fragments: lane holds q[t, head, 16*ks + 8*hb .. +7] for ks = 0..35
   u32x4 qf[kDqk / 16];
@@ -97,56 +80,83 @@ __global__ __launch_bounds__(256, 1) void sparse_mla_fwd_kernel(SparseFwdParams 
     }
   }
 
+  // ---- stage the index row (invalid -> -1) and find the last valid position
+  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
+  const int kpad = (p.topk + kBK - 1) / kBK * kBK;
+  int last = -1;
+  for (int j = threadIdx.x; j < kpad; j += NW * 64) {
+    int v = j < p.topk ? idx_row[j] : -1;
+    if (v < 0 || v >= p.n_kv || (p.causal && v > t)) v = -1;
+    sm.idx[j] = v;
+    if (v >= 0) last = j;
+  }
+  last = wave_max_i(last);
+  if (lane == 0) sm.red[wave] = last;
+  wait_vmcnt0();  // Q and index loads retired: nothing compiler-visible stays in flight
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) last = max(last, sm.red[w]);
+  const int nblk = __builtin_amdgcn_readfirstlane((last + kBK) / kBK);
+
   f32x16 o[kDv / 32];
-  // Softmax reference: m_ref (log2 units of scale*s) is the max of the first block that has a
-  // valid key for this head; later blocks are taken relative to it with 2^kHeadroom of
-  // headroom, so O never needs rescaling.  If any score overshoots the headroom the whole query
-  // is recomputed once with the exact row max (m_seen), which cannot overshoot.
-  float m_ref = -INFINITY;
-  float m_seen = -INFINITY;
-  float l_run = 0.f;
-  __shared__ int redo_flag;
+  float m_ref = -INFINITY, m_seen = -INFINITY, l_run = 0.f;
 
-  const int g = lane >> 4;  // 16-lane group (ds_read_tr operand rows)
-  const int gi = lane & 15;
-  const int tr_key = 4 * (g >> 1) + (gi >> 2);       // key row this lane feeds into ds_read_tr
-  const int tr_dv = 16 * (g & 1) + 4 * (gi & 3);     // dv column this lane feeds into ds_read_tr
-
-  auto load_idx = [&](int blk) -> int {
-    const int j = blk * kBK + (lane & 31);
-    if (blk >= nblk || j >= p.topk) return -1;
-    const int v = idx_row[j];
-    return (v >= 0 && v < p.n_kv) ? v : -1;
-  };
+  // QK operand addresses: lane reads row hl, chunk 2*ks + hb (see tile_off): V part at
+  // qk_v ^ (32*ks) for ks < 32, rope part at qk_r ^ (32*(ks-32)).
+  const uint32_t qk_v = hl * 1024u + 16u * (hb ^ kv_swz(hl));
+  const uint32_t qk_r = kTileVBytes + hl * 128u + 16u * (hb ^ ((hl >> 1) & 7u));
+  // PV operand addresses (ds_read_tr): lane feeds key 16a + 8h + 4(g/2) + gi/4 (the S^T C-layout
+  // key order) and dv 32m + 16(g%2) + 4(gi%4): byte pv[a][h] ^ (64*m).
+  uint32_t pv[2][2];
+  {
+    const int g = lane >> 4, gi = lane & 15;
+    const uint32_t cl = 2 * (g & 1) + ((gi & 3) >> 1);
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t key = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
+        pv[a][h] = key * 1024u + 8u * (gi & 1) + 16u * (cl ^ kv_swz(key));
+      }
+  }
 
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int m = 0; m < kDv / 32; ++m) o[m] = f32x16{};
     l_run = 0.f;
-    int idx_cur = load_idx(0);
-    int idx_nxt = load_idx(1);
-    if (nblk > 0) gather_block(smem, p.kv, p.kv_stride, idx_cur, wave, nwaves, lane);
+    if (nblk > 0) gather_tile<NW>(sm.tile[0], sm.idx[lane & 31], p.kv, wave, lane);
+    if (nblk > 1) gather_tile<NW>(sm.tile[1], sm.idx[kBK + (lane & 31)], p.kv, wave, lane);
 
     for (int blk = 0; blk < nblk; ++blk) {
-      wait_vmcnt0();
+      if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
       __syncthreads();
-      if (blk + 1 < nblk)
-        gather_block(smem + ((blk + 1) & 1) * kBufBytes, p.kv, p.kv_stride, idx_nxt, wave, nwaves, lane);
-      const int idx_nn = load_idx(blk + 2);
-      const char* buf = smem + (blk & 1) * kBufBytes;
+      if (blk + 2 < nblk)
+        gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
+      const char* buf = sm.tile[blk % kStages];
+      uint32_t qv = qk_v, qr = qk_r;
+      uint32_t pv00 = pv[0][0], pv01 = pv[0][1], pv10 = pv[1][0], pv11 = pv[1][1];
+      // opaque per iteration: the swizzled operand addresses are recomputed (one v_xor each)
+      // right before use instead of being hoisted into ~100 loop-invariant VGPRs
+      asm volatile("" : "+v"(qv), "+v"(qr), "+v"(pv00), "+v"(pv01), "+v"(pv10), "+v"(pv11));
+      const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
-      const bool kvalid = idx_cur >= 0 && (!p.causal || idx_cur <= t);
-      const uint32_t vmask = (uint32_t)__ballot(kvalid);
-
-      // ---- S^T[32 keys x 32 heads] = K . Q^T
-      f32x16 s = f32x16{};
+      // ---- S^T[32 keys x 32 heads] = K . Q^T  (two accumulator chains, A prefetched)
+      f32x16 s;
       {
-        const char* a0 = buf + (hl * kPitch + hb) * 16;
+        auto qk_addr = [&](int ks) { return buf + (ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
+        u32x4 a[kPre];
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) a[i] = lds_load16(qk_addr(i));
+        f32x16 sa = f32x16{}, sb = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < kDqk / 16; ++ks) {
-          s = mfma32x32x16(as_bf16x8(lds_load16(a0 + ks * 32)), as_bf16x8(qf[ks]), s);
-          if ((ks & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          const u32x4 cur = a[ks % kPre];
+          if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
+          if (ks & 1) sb = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sb);
+          else sa = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sa);
+          __builtin_amdgcn_sched_barrier(0);
         }
+        s = sa + sb;
       }
 
       // ---- softmax numerator; key of s[i] = (i/4)*8 + 4*hb + i%4
@@ -180,32 +190,37 @@ __global__ __launch_bounds__(256, 1) void sparse_mla_fwd_kernel(SparseFwdParams 
       }
       l_run += xor32_sum(rs);
 
-      // ---- O^T[512 x 32 heads] += V^T . P^T   (V^T via transposing LDS reads)
+      // ---- O^T[512 x 32 heads] += V^T . P^T   (V^T via transposing LDS reads, prefetched)
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        const int kb = 16 * a + tr_key;
-        const char* r0 = buf + (kb * kPitch) * 16 + tr_dv * 2;
-        const char* r1 = r0 + 8 * kPitch * 16;
+        const uint32_t r0 = a ? pv10 : pv00, r1 = a ? pv11 : pv01;
         const bf16x8 b = as_bf16x8(pb[a]);
+        u32x4 v[kPre];
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+          const u32x2 lo = lds_read_tr16(buf + (r0 ^ (64u * i))), hi = lds_read_tr16(buf + (r1 ^ (64u * i)));
+          v[i] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
 #pragma unroll
         for (int m = 0; m < kDv / 32; ++m) {
-          const u32x2 lo = lds_read_tr16(r0 + m * 64);
-          const u32x2 hi = lds_read_tr16(r1 + m * 64);
-          const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-          o[m] = mfma32x32x16(as_bf16x8(av), b, o[m]);
-          if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+          const u32x4 cur = v[m % kPre];
+          if (m + kPre < kDv / 32) {
+            const u32x2 lo = lds_read_tr16(buf + (r0 ^ (64u * (m + kPre))));
+            const u32x2 hi = lds_read_tr16(buf + (r1 ^ (64u * (m + kPre))));
+            v[m % kPre] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          }
+          o[m] = mfma32x32x16(as_bf16x8(cur), b, o[m]);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-      idx_cur = idx_nxt;
-      idx_nxt = idx_nn;
     }
     // ---- did any head overshoot its reference?  (workgroup-uniform decision)
     const bool over = m_seen > m_ref + kHeadroom;
-    if (threadIdx.x == 0) redo_flag = 0;
+    if (threadIdx.x == 0) sm.redo_flag = 0;
     __syncthreads();
-    if (__any(over) && lane == 0) redo_flag = 1;
+    if (__any(over) && lane == 0) sm.redo_flag = 1;
     __syncthreads();
-    if (!redo_flag) break;
+    if (!sm.redo_flag) break;
     m_ref = m_seen;
   }
 
@@ -231,9 +246,15 @@ __global__ __launch_bounds__(256, 1) void sparse_mla_fwd_kernel(SparseFwdParams 
 }
 
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
-  const int nwaves = p.n_heads >= 128 ? 4 : (p.n_heads + 31) / 32;
-  dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
-  hipLaunchKernelGGL(sparse_mla_fwd_kernel, grid, dim3(64 * nwaves), 0, stream, p);
+  if (p.topk > kMaxTopk) return -2;
+  const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
+  const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
+  if (nw == 4)
+    hipLaunchKernelGGL(sparse_mla_fwd_kernel<4>, grid, dim3(256), 0, stream, p);
+  else if (nw == 2)
+    hipLaunchKernelGGL(sparse_mla_fwd_kernel<2>, grid, dim3(128), 0, stream, p);
+  else
+    hipLaunchKernelGGL(sparse_mla_fwd_kernel<1>, grid, dim3(64), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
