@@ -30,7 +30,7 @@ BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
   size_t off = 0;
   L.p_stage = off; off += stage;
   L.ds_stage = off; off += stage;
-  L.g_stage = off; off += align_up(sizeof(uint16_t) * (size_t)total_q * topk * kDqk);
+  L.g_stage = off; off += align_up(sizeof(uint16_t) * ((size_t)total_q * topk + 1) * kDqk);
   L.pair_pos = off; off += align_up(sizeof(int64_t) * (size_t)total_q * topk);
   L.offsets = off; off += align_up(sizeof(int64_t) * ((size_t)n_kv + 1));
   L.counts = off; off += align_up(sizeof(int32_t) * (size_t)n_kv);
@@ -144,6 +144,7 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
   p.p_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.p_stage);
   p.ds_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.ds_stage);
   p.g_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.g_stage);
+  p.g_sink_row = (int64_t)total_q * topk;
   p.pair_pos = reinterpret_cast<int64_t*>(ws + L.pair_pos);
   p.csr_offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
   p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);

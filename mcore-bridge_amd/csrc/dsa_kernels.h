@@ -32,7 +32,8 @@ struct SparseBwdParams {
   // workspace (carved by the C-ABI from one caller buffer)
   bf16_t* p_stage;      // [total_q, n_heads, topk_pad]  P
   bf16_t* ds_stage;     // [total_q, n_heads, topk_pad]  scale * dS
-  bf16_t* g_stage;      // [n_pairs, 576] per-pair dKV partial rows in key-major order
+  bf16_t* g_stage;      // [total_q * topk + 1, 576] per-pair dKV partial rows, key-major order
+  int64_t g_sink_row;   // last row of g_stage: write target of pairs that select nothing
   int64_t* pair_pos;    // [total_q, topk] row of G for each pair (-1 = not selected)
   int64_t* csr_offsets; // [n_kv + 1]
   int32_t* csr_counts;  // [n_kv] counts, then per-key cursor

@@ -17,14 +17,21 @@
 //   B1 bwd_sp_kernel   per query: recompute S, P, dP (shared K/V operand reads), Delta fused;
 //                      stage P and scale*dS (bf16, [t][h][j]).
 //   B2 bwd_dq_kernel   per query: dQ^T += K^T . dS^T over the gathered rows (K^T via transposing
-//                      LDS reads, dS^T straight from the staging buffer).
-//   B3 bwd_g_kernel    per query: G^T[576 x keys] = Q^T . dS + dO^T . P contracted over all 128
+//                      LDS reads, dS^T tile copied into LDS next to the KV tile).
+//   B3 bwd_g_kernel    per query: G^T[576 x keys] = Q^T . dS + dO^T . P contracted over all
 //                      heads (Q^T / dO^T held in registers), written as bf16 rows at the pair's
 //                      key-major position.
 //   B4 csr_*           key-major order of the selected pairs: count, scan, position.
 //   B5 bwd_dkv_reduce  per key: fp32 sum of its contiguous G rows -> dKV.
+// B1-B3 stream their per-block operands into LDS through 3-stage rings of asynchronous
+// global_load_lds copies (see dsa_kvtile.h) completed by explicit s_waitcnt vmcnt + barrier.
+// vmcnt counts every vector-memory instruction of the wave in issue order, so each wave issues
+// a fixed number of copies and stores per block and the waits count them exactly.
+#include <algorithm>
+
 #include "dsa_common.h"
 #include "dsa_kernels.h"
+#include "dsa_kvtile.h"
 
 namespace dsa {
 
@@ -32,11 +39,10 @@ namespace {
 
 constexpr int kDqk = 576;
 constexpr int kDv = 512;
-constexpr int kChunks = kDqk / 8;
-constexpr int kPitch = kChunks + 1;
-constexpr int kBK = 32;
-constexpr int kGatherInstr = (kBK * kPitch + 63) / 64;
-constexpr int kBufBytes = kGatherInstr * 1024;
+constexpr int kBK = kTileKeys;
+constexpr int kStages = 3;
+constexpr int kMaxTopkBwd = 4096;
+constexpr int kPre = 3;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -46,35 +52,27 @@ DSA_DEV u32x2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-DSA_DEV void gather_block(char* buf, const bf16_t* kv, int64_t kv_stride, int row_id_lane,
-                          int wave, int nwaves, int lane) {
-  for (int n = wave; n < kGatherInstr; n += nwaves) {
-    const int p = n * 64 + lane;
-    const int r = p / kPitch;
-    const int c = p - r * kPitch;
-    const int row = __shfl(row_id_lane, r & 31, 64);
-    const bf16_t* src = kv;
-    if (r < kBK && row >= 0 && c < kChunks) src = kv + (int64_t)row * kv_stride + c * 8;
-    async_copy16(src, buf + n * 1024);
-  }
-}
-
-// Number of 32-key blocks of a query row: up to its last valid index (same rule as the forward).
-DSA_DEV int count_blocks(const int32_t* idx_row, int topk, int n_kv, int causal, int t, int lane) {
+// Stage the query's index row in LDS (invalid -> -1); returns the number of 32-key blocks up
+// to the last valid entry (workgroup-uniform).  Also retires every outstanding load.
+template <int NW>
+DSA_DEV int stage_index_row(int32_t* idx_s, int* red, const int32_t* idx_row, int topk, int n_kv, int causal,
+                            int t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kpad = (topk + kBK - 1) / kBK * kBK;
   int last = -1;
-  for (int j = lane; j < topk; j += 64) {
-    const int v = idx_row[j];
-    if (v >= 0 && v < n_kv && (!causal || v <= t)) last = j;
+  for (int j = threadIdx.x; j < kpad; j += NW * 64) {
+    int v = j < topk ? idx_row[j] : -1;
+    if (v < 0 || v >= n_kv || (causal && v > t)) v = -1;
+    idx_s[j] = v;
+    if (v >= 0) last = j;
   }
   last = wave_max_i(last);
-  return (last + kBK) / kBK;
-}
-
-DSA_DEV int load_idx(const int32_t* idx_row, int blk, int nblk, int topk, int n_kv, int lane) {
-  const int j = blk * kBK + (lane & 31);
-  if (blk >= nblk || j >= topk) return -1;
-  const int v = idx_row[j];
-  return (v >= 0 && v < n_kv) ? v : -1;
+  if (lane == 0) red[wave] = last;
+  wait_vmcnt0();
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) last = max(last, red[w]);
+  return __builtin_amdgcn_readfirstlane((last + kBK) / kBK);
 }
 
 }  // namespace
@@ -82,17 +80,25 @@ DSA_DEV int load_idx(const int32_t* idx_row, int blk, int nblk, int topk, int n_
 // ------------------------------------------------------------------------------------------
 // B1: recompute P and dS; stage them.  One workgroup per query, wave = 32 heads.
 // ------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 1) void bwd_sp_kernel(SparseBwdParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kBufBytes];
+struct SpSmem {
+  char tile[kStages][kTileBytes];
+  int32_t idx[kMaxTopkBwd];
+  int red[4];
+};
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
+  constexpr int G = tile_copies_per_wave<NW>();
+  constexpr int S = 8;  // staging stores per wave per block (4 x P, 4 x dS)
+  __shared__ __attribute__((aligned(16))) SpSmem sm;
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5, hl = lane & 31;
   const int head = blockIdx.y * 128 + wave * 32 + hl;
   const bool head_ok = head < p.n_heads;
+  const bool wave_stores = blockIdx.y * 128 + wave * 32 < p.n_heads;  // wave-uniform
   const int hsafe = head_ok ? head : 0;
-  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
-  const int nblk = count_blocks(idx_row, p.topk, p.n_kv, p.causal, t, lane);
 
   // Q (576) and dO (512) fragments, d-contiguous: lane holds [16*ks + 8*hb, +8).
   u32x4 qf[kDqk / 16], df[kDv / 16];
@@ -118,37 +124,59 @@ __global__ __launch_bounds__(256, 1) void bwd_sp_kernel(SparseBwdParams p) {
   const float lse = head_ok ? p.lse[(int64_t)t * p.lse_stride_t + head] : -INFINITY;
   const float lse2 = lse * kLog2e;
   const bool row_live = lse != -INFINITY;
+  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
+                                       p.causal, t);
 
-  const int64_t stage_off = ((int64_t)t * p.n_heads + hsafe) * p.topk_pad;
+  // staged rows: element (t, head, j) at ((t * H + head) * topk_pad + j); lane writes keys
+  // 8*q4 + 4*hb .. +3 of each block
+  const int64_t stage_off = ((int64_t)t * p.n_heads + hsafe) * p.topk_pad + hb * 4;
   bf16_t* ps_row = p.p_stage + stage_off;
   bf16_t* ds_row = p.ds_stage + stage_off;
+  const uint32_t qk_v = hl * 1024u + 16u * (hb ^ kv_swz(hl));
+  const uint32_t qk_r = kTileVBytes + hl * 128u + 16u * (hb ^ ((hl >> 1) & 7u));
 
-  int idx_cur = load_idx(idx_row, 0, nblk, p.topk, p.n_kv, lane);
-  int idx_nxt = load_idx(idx_row, 1, nblk, p.topk, p.n_kv, lane);
-  if (nblk > 0) gather_block(smem, p.kv, p.kv_stride, idx_cur, wave, nwaves, lane);
-
+  if (nblk > 0) gather_tile<NW>(sm.tile[0], sm.idx[lane & 31], p.kv, wave, lane);
+  if (nblk > 1) gather_tile<NW>(sm.tile[1], sm.idx[kBK + (lane & 31)], p.kv, wave, lane);
+  u32x2 pw[4], dw[4];   // previous block's values, stored right after the next block's barrier
   for (int blk = 0; blk < nblk; ++blk) {
-    wait_vmcnt0();
+    // issue order per block: [wait][barrier][stores(blk-1)][copies(blk+2)][compute] -> after
+    // block blk's copies come stores(blk-1) and copies(blk+1)
+    if (blk + 1 >= nblk) wait_vmcnt<0>();
+    else if (blk == 0 || !wave_stores) wait_vmcnt<G>();
+    else wait_vmcnt<G + S>();
     __syncthreads();
-    if (blk + 1 < nblk)
-      gather_block(smem + ((blk + 1) & 1) * kBufBytes, p.kv, p.kv_stride, idx_nxt, wave, nwaves, lane);
-    const int idx_nn = load_idx(idx_row, blk + 2, nblk, p.topk, p.n_kv, lane);
-    const char* buf = smem + (blk & 1) * kBufBytes;
-    const bool kvalid = idx_cur >= 0 && (!p.causal || idx_cur <= t);
-    const uint32_t vmask = (uint32_t)__ballot(kvalid);
+    if (blk > 0 && head_ok) {  // wave_stores => at least one lane active => the wave issues S stores
+      const int j = (blk - 1) * kBK;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        *reinterpret_cast<u32x2*>(ps_row + j + 8 * q4) = pw[q4];
+        *reinterpret_cast<u32x2*>(ds_row + j + 8 * q4) = dw[q4];
+      }
+    }
+    if (blk + 2 < nblk)
+      gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
+    const char* buf = sm.tile[blk % kStages];
+    uint32_t qv = qk_v, qr = qk_r;
+    asm volatile("" : "+v"(qv), "+v"(qr));
+    const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
     // S^T = K . Q^T and dP^T = V . dO^T share the A operand (V = K[:, :512]).
     f32x16 s = f32x16{}, dp = f32x16{};
-    const char* a0 = buf + (hl * kPitch + hb) * 16;
+    {
+      auto addr = [&](int ks) { return buf + (ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
+      u32x4 a[kPre];
 #pragma unroll
-    for (int ks = 0; ks < kDqk / 16; ++ks) {
-      const bf16x8 a = as_bf16x8(lds_load16(a0 + ks * 32));
-      s = mfma32x32x16(a, as_bf16x8(qf[ks]), s);
-      if (ks < kDv / 16) dp = mfma32x32x16(a, as_bf16x8(df[ks]), dp);
-      if ((ks & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < kPre; ++i) a[i] = lds_load16(addr(i));
+#pragma unroll
+      for (int ks = 0; ks < kDqk / 16; ++ks) {
+        const u32x4 cur = a[ks % kPre];
+        if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(addr(ks + kPre));
+        s = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), s);
+        if (ks < kDv / 16) dp = mfma32x32x16(as_bf16x8(cur), as_bf16x8(df[ks]), dp);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // P and scale * dS; key of element i = (i/4)*8 + 4*hb + i%4
-    u32x2 pw[4], dw[4];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       float pv[4], dv[4];
@@ -164,81 +192,128 @@ __global__ __launch_bounds__(256, 1) void bwd_sp_kernel(SparseBwdParams p) {
       pw[q4] = u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
       dw[q4] = u32x2{pack_bf16x2(dv[0], dv[1]), pack_bf16x2(dv[2], dv[3])};
     }
-    if (head_ok) {
+  }
+  if (nblk > 0 && head_ok) {
+    const int j = (nblk - 1) * kBK;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int j = blk * kBK + q4 * 8 + hb * 4;
-        *reinterpret_cast<u32x2*>(ps_row + j) = pw[q4];
-        *reinterpret_cast<u32x2*>(ds_row + j) = dw[q4];
-      }
+    for (int q4 = 0; q4 < 4; ++q4) {
+      *reinterpret_cast<u32x2*>(ps_row + j + 8 * q4) = pw[q4];
+      *reinterpret_cast<u32x2*>(ds_row + j + 8 * q4) = dw[q4];
     }
-    idx_cur = idx_nxt;
-    idx_nxt = idx_nn;
   }
 }
 
 // ------------------------------------------------------------------------------------------
 // B2: dQ^T[576 x 32 heads] = K^T . (scale*dS)^T per wave, over the query's gathered rows.
 // ------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 1) void bwd_dq_kernel(SparseBwdParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kBufBytes];
+constexpr int kDsTileBytes = 128 * 64;  // [128 heads][32 keys] bf16
+
+struct DqSmem {
+  char tile[kStages][kTileBytes];
+  char ds[kStages][kDsTileBytes];
+  int32_t idx[kMaxTopkBwd];
+  int red[4];
+};
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
+  constexpr int HR = 32 * NW;                                  // head rows copied per block
+  constexpr int G = tile_copies_per_wave<NW>() + HR / 16 / NW;
+  __shared__ __attribute__((aligned(16))) DqSmem sm;
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5, hl = lane & 31;
-  const int head = blockIdx.y * 128 + wave * 32 + hl;
+  const int h0 = blockIdx.y * 128;
+  const int head = h0 + wave * 32 + hl;
   const bool head_ok = head < p.n_heads;
-  const int hsafe = head_ok ? head : 0;
-  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
-  const int nblk = count_blocks(idx_row, p.topk, p.n_kv, p.causal, t, lane);
-  const bf16_t* ds_row = p.ds_stage + ((int64_t)t * p.n_heads + hsafe) * p.topk_pad + hb * 8;
+  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
+                                       p.causal, t);
+  // dS rows of this workgroup's heads; rows past n_heads re-read row 0 (never stored).  16-byte
+  // chunk q of head row h lands at position q ^ ((h >> 2) & 3): bank-conflict-free column reads.
+  const int hrows = min(HR, p.n_heads - h0);
+  const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + ((int64_t)t * p.n_heads + h0) * p.topk_pad);
+  const int64_t ds_stride = (int64_t)p.topk_pad * 2;
+  auto copy_ds = [&](char* dst, int blk) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int k = 0; k < HR / 16 / NW; ++k) {
+      const int i = w + k * NW;
+      const int h = 16 * i + (lane >> 2);
+      const int q = (lane & 3) ^ ((h >> 2) & 3);
+      const int hs = h < hrows ? h : 0;
+      async_copy16_unordered(ds_base + hs * ds_stride + blk * kBK * 2 + q * 16, base + i * 1024u);
+    }
+  };
 
-  const int g = lane >> 4, gi = lane & 15;
-  const int tr_key = 8 * (g >> 1) + (gi >> 2);     // natural key order: k-slot 8*hb + e
-  const int tr_col = 16 * (g & 1) + 4 * (gi & 3);
+  // A operand (K^T via ds_read_tr), natural key order: lane feeds key 16a + 8(g/2) + 4h + gi/4,
+  // latent column 32m + 16(g%2) + 4(gi%4).  Byte address: V part kt[a][h] ^ (64*m) (m < 16),
+  // rope part kr[a][h] ^ (64*(m-16)).
+  uint32_t kt[2][2], kr[2][2];
+  {
+    const int g = lane >> 4, gi = lane & 15;
+    const uint32_t cl = 2 * (g & 1) + ((gi & 3) >> 1);
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t key = 16 * a + 8 * (g >> 1) + 4 * h + (gi >> 2);
+        kt[a][h] = key * 1024u + 8u * (gi & 1) + 16u * (cl ^ kv_swz(key));
+        kr[a][h] = kTileVBytes + key * 128u + 8u * (gi & 1) + 16u * (cl ^ ((key >> 1) & 7u));
+      }
+  }
+  // B operand (dS^T): lane (head row wave*32 + hl, keys 16a + 8hb .. +7) = 16-byte chunk 2a + hb
+  const int hrow = wave * 32 + hl;
+  const uint32_t dsb = hrow * 64u;
+  const uint32_t dsq = (uint32_t)((hrow >> 2) & 3);
 
   f32x16 acc[kDqk / 32];
 #pragma unroll
   for (int m = 0; m < kDqk / 32; ++m) acc[m] = f32x16{};
 
-  int idx_cur = load_idx(idx_row, 0, nblk, p.topk, p.n_kv, lane);
-  int idx_nxt = load_idx(idx_row, 1, nblk, p.topk, p.n_kv, lane);
-  if (nblk > 0) gather_block(smem, p.kv, p.kv_stride, idx_cur, wave, nwaves, lane);
-  u32x4 dsv[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
   if (nblk > 0) {
-    dsv[0] = gload16(ds_row);
-    dsv[1] = gload16(ds_row + 16);
+    gather_tile<NW>(sm.tile[0], sm.idx[lane & 31], p.kv, wave, lane);
+    copy_ds(sm.ds[0], 0);
   }
-
+  if (nblk > 1) {
+    gather_tile<NW>(sm.tile[1], sm.idx[kBK + (lane & 31)], p.kv, wave, lane);
+    copy_ds(sm.ds[1], 1);
+  }
   for (int blk = 0; blk < nblk; ++blk) {
-    wait_vmcnt0();
+    if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
     __syncthreads();
-    if (blk + 1 < nblk)
-      gather_block(smem + ((blk + 1) & 1) * kBufBytes, p.kv, p.kv_stride, idx_nxt, wave, nwaves, lane);
-    const int idx_nn = load_idx(idx_row, blk + 2, nblk, p.topk, p.n_kv, lane);
-    u32x4 dsn[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
-    if (blk + 1 < nblk) {
-      dsn[0] = gload16(ds_row + (blk + 1) * kBK);
-      dsn[1] = gload16(ds_row + (blk + 1) * kBK + 16);
+    if (blk + 2 < nblk) {
+      gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
+      copy_ds(sm.ds[(blk + 2) % kStages], blk + 2);
     }
-    const char* buf = smem + (blk & 1) * kBufBytes;
+    const char* buf = sm.tile[blk % kStages];
+    const char* dsl = sm.ds[blk % kStages];
+    uint32_t k00 = kt[0][0], k01 = kt[0][1], k10 = kt[1][0], k11 = kt[1][1];
+    uint32_t r00 = kr[0][0], r01 = kr[0][1], r10 = kr[1][0], r11 = kr[1][1];
+    asm volatile("" : "+v"(k00), "+v"(k01), "+v"(k10), "+v"(k11), "+v"(r00), "+v"(r01), "+v"(r10), "+v"(r11));
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
-      const char* r0 = buf + ((16 * a + tr_key) * kPitch) * 16 + tr_col * 2;
-      const char* r1 = r0 + 4 * kPitch * 16;
-      const bf16x8 b = as_bf16x8(head_ok ? dsv[a] : u32x4{0, 0, 0, 0});
+      const bf16x8 b = as_bf16x8(lds_load16(dsl + dsb + 16u * ((2u * a + hb) ^ dsq)));
+      const uint32_t v0 = a ? k10 : k00, v1 = a ? k11 : k01;
+      const uint32_t q0 = a ? r10 : r00, q1 = a ? r11 : r01;
+      auto ld = [&](int m) {
+        const uint32_t x0 = m < 16 ? (v0 ^ (64u * m)) : (q0 ^ (64u * (m - 16)));
+        const uint32_t x1 = m < 16 ? (v1 ^ (64u * m)) : (q1 ^ (64u * (m - 16)));
+        const u32x2 lo = lds_read_tr16(buf + x0), hi = lds_read_tr16(buf + x1);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 v[kPre];
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) v[i] = ld(i);
 #pragma unroll
       for (int m = 0; m < kDqk / 32; ++m) {
-        const u32x2 lo = lds_read_tr16(r0 + m * 64);
-        const u32x2 hi = lds_read_tr16(r1 + m * 64);
-        acc[m] = mfma32x32x16(as_bf16x8(u32x4{lo[0], lo[1], hi[0], hi[1]}), b, acc[m]);
-        if ((m & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        const u32x4 cur = v[m % kPre];
+        if (m + kPre < kDqk / 32) v[m % kPre] = ld(m + kPre);
+        acc[m] = mfma32x32x16(as_bf16x8(cur), b, acc[m]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    dsv[0] = dsn[0];
-    dsv[1] = dsn[1];
-    idx_cur = idx_nxt;
-    idx_nxt = idx_nn;
   }
   if (!head_ok) return;
   bf16_t* dqrow = p.dq + (int64_t)t * p.dq_stride_t + (int64_t)head * kDqk;
@@ -255,101 +330,137 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(SparseBwdParams p) {
 
 // ------------------------------------------------------------------------------------------
 // B3: per-pair dKV partial rows G = (scale*dS)^T Q + P^T dO, contracted over all heads.
-// Wave w owns output row tiles (32 latent dims each): Q part tiles kQT[w], dO part tiles kVT[w].
+// Wave w owns output row tiles (32 latent dims each): Q part {4w..4w+3} (+16+w for w < 2),
+// dO part {4w..4w+3}.
 // ------------------------------------------------------------------------------------------
-namespace {
-constexpr int kHeads = 128;                         // B3 handles up to 128 heads (n_heads % 16 == 0)
-constexpr int kKs = kHeads / 16;                    // up to 8 head k-steps
-constexpr int kStagePitch = kBK * 2 + 16;           // bytes per head row of a staged 32-key tile (+pad)
-constexpr int kTileBytes = kHeads * kStagePitch;    // one staged [128 heads][32 keys] bf16 tile
+constexpr int kGHeads = 128;                        // B3 handles up to 128 heads (n_heads % 16 == 0)
+constexpr int kGKs = kGHeads / 16;                  // head k-steps
+constexpr int kStageTile = kGHeads * 64;            // one staged [128 heads][32 keys] bf16 tile
 constexpr int kRowPitch = kDqk * 2 + 16;            // bytes per staged head row of Q / dO
-}  // namespace
+constexpr int kSetupRows = 32;                      // head rows staged per setup round
+
+struct GSmem {
+  union {
+    char rows[kSetupRows * kRowPitch];              // setup: Q / dO rows for the transposed load
+    char st[kStages][2][kStageTile];                // loop: [dS | P] tiles
+  };
+  int32_t idx[kMaxTopkBwd];
+  int red[4];
+};
 
 __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
-  // LDS: staged Q / dO rows for the transposed register load (16 heads at a time), then the
-  // double-buffered [dS | P] tiles of each key block.
-  __shared__ __attribute__((aligned(16))) char smem[2 * kTileBytes + 16 * kRowPitch];
+  constexpr int NW = 4;
+  constexpr int G = 2 * kGHeads / 16 / NW;          // 4 copies per wave per block
+  __shared__ __attribute__((aligned(16))) GSmem sm;
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5;
   const int g = lane >> 4, gi = lane & 15;
-  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
-  const int nblk = count_blocks(idx_row, p.topk, p.n_kv, p.causal, t, lane);
+  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
+                                       p.causal, t);
   if (nblk == 0) return;
-
-  // tiles owned by this wave: Q part {4w..4w+3} (+16+w for w < 2), dO part {4w..4w+3}
+  const int nks = p.n_heads / 16;
   const int nq = wave < 2 ? 5 : 4;
   auto qtile = [&](int i) { return i < 4 ? 4 * wave + i : 16 + wave; };
 
-  // ---- load Q^T and dO^T fragments (A operand: lane row = latent dim, k = 8 heads) via LDS
-  u32x4 qa[5][kKs], va[4][kKs];
-  char* rows = smem + 2 * kTileBytes;
-  const int nks = p.n_heads / 16;
+  // ---- Q^T and dO^T fragments (A operand: row = latent dim, k = 8 heads) via LDS, 32 heads a round
+  u32x4 qa[5][kGKs], va[4][kGKs];
   const int tr_h = 8 * (g >> 1) + (gi >> 2);        // head row this lane feeds into ds_read_tr
   const int tr_c = 16 * (g & 1) + 4 * (gi & 3);     // latent column this lane feeds
-  for (int ks = 0; ks < kKs; ++ks) {
-    if (ks >= nks) {
 #pragma unroll
-      for (int i = 0; i < 5; ++i) qa[i][ks] = u32x4{0, 0, 0, 0};
+  for (int ks = 0; ks < kGKs; ++ks) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) va[i][ks] = u32x4{0, 0, 0, 0};
-      continue;
-    }
+    for (int i = 0; i < 5; ++i) qa[i][ks] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i][ks] = u32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int r0 = 0; r0 < kGHeads; r0 += kSetupRows) {
+    if (r0 >= p.n_heads) break;
+#pragma unroll
     for (int part = 0; part < 2; ++part) {
       const bf16_t* src = part == 0 ? p.q + (int64_t)t * p.q_stride_t : p.dout + (int64_t)t * p.dout_stride_t;
       const int width = part == 0 ? kDqk : kDv;
+      const int nrows = min(kSetupRows, p.n_heads - r0);
       __syncthreads();
-      for (int c = threadIdx.x; c < 16 * (width / 8); c += blockDim.x) {
+      for (int c = threadIdx.x; c < nrows * (width / 8); c += blockDim.x) {
         const int r = c / (width / 8), cc = c - r * (width / 8);
-        lds_store16(rows + r * kRowPitch + cc * 16, gload16(src + (int64_t)(16 * ks + r) * width + cc * 8));
+        lds_store16(sm.rows + r * kRowPitch + cc * 16, gload16(src + (int64_t)(r0 + r) * width + cc * 8));
       }
       __syncthreads();
-      if (part == 0) {
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-          if (i < nq) {
-            const char* r0 = rows + tr_h * kRowPitch + (32 * qtile(i) + tr_c) * 2;
-            const u32x2 lo = lds_read_tr16(r0), hi = lds_read_tr16(r0 + 4 * kRowPitch);
-            qa[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      for (int kk = 0; kk < kSetupRows / 16; ++kk) {
+        const int ks = r0 / 16 + kk;
+        if (ks >= nks) continue;
+        const char* rb = sm.rows + (16 * kk + tr_h) * kRowPitch + tr_c * 2;
+        if (part == 0) {
+#pragma unroll
+          for (int i = 0; i < 5; ++i) {
+            if (i < nq) {
+              const u32x2 lo = lds_read_tr16(rb + 64 * qtile(i)), hi = lds_read_tr16(rb + 4 * kRowPitch + 64 * qtile(i));
+              qa[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            }
           }
-        }
-      } else {
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const char* r0 = rows + tr_h * kRowPitch + (32 * (4 * wave + i) + tr_c) * 2;
-          const u32x2 lo = lds_read_tr16(r0), hi = lds_read_tr16(r0 + 4 * kRowPitch);
-          va[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          for (int i = 0; i < 4; ++i) {
+            const int mt = 4 * wave + i;
+            const u32x2 lo = lds_read_tr16(rb + 64 * mt), hi = lds_read_tr16(rb + 4 * kRowPitch + 64 * mt);
+            va[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          }
         }
       }
     }
   }
+  wait_vmcnt0();
+  __syncthreads();  // setup rows dead: the union now holds the [dS | P] ring
 
-  // ---- key blocks: stage [dS | P] tiles (rows = heads, 32 keys each) with LDS-direct copies
-  const int64_t st_base = (int64_t)t * p.n_heads * p.topk_pad;
-  auto stage = [&](int blk, char* dst) {
-    // 2 tiles x 128 rows x 64 B = 256 x 64 B pieces; lane c copies piece c (4 x 16 B each)
-    for (int c = threadIdx.x; c < 2 * p.n_heads * 4; c += blockDim.x) {
-      const int tile = c / (p.n_heads * 4), r = (c / 4) % p.n_heads, q = c & 3;
-      const bf16_t* src = (tile == 0 ? p.ds_stage : p.p_stage) + st_base + (int64_t)r * p.topk_pad + blk * kBK + q * 8;
-      lds_store16(dst + tile * kTileBytes + r * kStagePitch + q * 16, gload16(src));
+  // ---- key blocks: [dS | P] tiles (rows = heads, 32 keys each) through a 3-stage copy ring
+  const char* dsb = reinterpret_cast<const char*>(p.ds_stage + (int64_t)t * p.n_heads * p.topk_pad);
+  const char* psb = reinterpret_cast<const char*>(p.p_stage + (int64_t)t * p.n_heads * p.topk_pad);
+  const int64_t rstride = (int64_t)p.topk_pad * 2;
+  auto stage = [&](int s, int blk) {
+    // head rows past n_heads re-read row 0 (valid memory; their k-steps are skipped)
+    const uint32_t b0 = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][0]));
+    const uint32_t b1 = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][1]));
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int k = 0; k < kGHeads / 16 / NW; ++k) {
+      const int i = w + k * NW;
+      const int h = 16 * i + (lane >> 2);
+      const int hs = h < p.n_heads ? h : 0;
+      const int64_t off = hs * rstride + blk * kBK * 2 + (lane & 3) * 16;
+      async_copy16_unordered(dsb + off, b0 + i * 1024u);
+      async_copy16_unordered(psb + off, b1 + i * 1024u);
     }
   };
+  // G rows: every lane stores its fragments each block (keys that are not selected write the
+  // sink row past the last real one), so the per-wave store count is fixed: 4 per owned tile.
   const int64_t* pos_row = p.pair_pos + (int64_t)t * p.topk;
+  stage(0, 0);
+  if (nblk > 1) stage(1, 1);
   for (int blk = 0; blk < nblk; ++blk) {
+    // issue order per block: [wait][barrier][copies(blk+2)][compute][stores(blk)] -> after
+    // block blk's copies come stores(blk-1), copies(blk+1)
+    if (blk + 1 >= nblk) wait_vmcnt<0>();
+    else if (blk == 0) wait_vmcnt<G>();
+    else if (nq == 5) wait_vmcnt<G + 20>();
+    else wait_vmcnt<G + 16>();
     __syncthreads();
-    stage(blk, smem);
-    __syncthreads();
+    if (blk + 2 < nblk) stage((blk + 2) % kStages, blk + 2);
+    const char* sd = sm.st[blk % kStages][0];
+    const char* sp = sm.st[blk % kStages][1];
     f32x16 acc[5];
 #pragma unroll
     for (int i = 0; i < 5; ++i) acc[i] = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < kKs; ++ks) {
+    for (int ks = 0; ks < kGKs; ++ks) {
       if (ks >= nks) break;
       // B operands: dS / P [k = 8 heads][n = key]; lane key = lane % 32
-      const char* b0 = smem + (16 * ks + tr_h) * kStagePitch + tr_c * 2;
-      const u32x2 s_lo = lds_read_tr16(b0), s_hi = lds_read_tr16(b0 + 4 * kStagePitch);
-      const u32x2 p_lo = lds_read_tr16(b0 + kTileBytes), p_hi = lds_read_tr16(b0 + kTileBytes + 4 * kStagePitch);
+      const uint32_t o0 = (16 * ks + tr_h) * 64 + tr_c * 2;
+      const u32x2 s_lo = lds_read_tr16(sd + o0), s_hi = lds_read_tr16(sd + o0 + 4 * 64);
+      const u32x2 p_lo = lds_read_tr16(sp + o0), p_hi = lds_read_tr16(sp + o0 + 4 * 64);
       const bf16x8 bs = as_bf16x8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
       const bf16x8 bp = as_bf16x8(u32x4{p_lo[0], p_lo[1], p_hi[0], p_hi[1]});
 #pragma unroll
@@ -358,21 +469,20 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         if (i < 4) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), bp, acc[i]);
       }
     }
-    // write G rows (bf16) for the valid keys of this block; lane key = lane % 32
+    // write G rows (bf16); lane key = lane % 32
     const int j = blk * kBK + (lane & 31);
-    const int64_t pos = j < p.topk ? pos_row[j] : -1;
-    if (pos >= 0) {
-      bf16_t* grow = p.g_stage + pos * kDqk;
+    int64_t pos = j < p.topk ? pos_row[j] : -1;
+    if (pos < 0) pos = p.g_sink_row;
+    bf16_t* grow = p.g_stage + pos * kDqk;
 #pragma unroll
-      for (int i = 0; i < 5; ++i) {
-        if (i < nq) {
-          const int d0 = 32 * qtile(i);
+    for (int i = 0; i < 5; ++i) {
+      if (i < nq) {
+        const int d0 = 32 * qtile(i);
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const int d = d0 + 8 * q4 + 4 * hb;
-            *reinterpret_cast<u32x2*>(grow + d) =
-                u32x2{pack_bf16x2(acc[i][4 * q4], acc[i][4 * q4 + 1]), pack_bf16x2(acc[i][4 * q4 + 2], acc[i][4 * q4 + 3])};
-          }
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = d0 + 8 * q4 + 4 * hb;
+          *reinterpret_cast<u32x2*>(grow + d) =
+              u32x2{pack_bf16x2(acc[i][4 * q4], acc[i][4 * q4 + 1]), pack_bf16x2(acc[i][4 * q4 + 2], acc[i][4 * q4 + 3])};
         }
       }
     }
@@ -398,8 +508,9 @@ __global__ void csr_count_kernel(const int32_t* idx, int64_t idx_stride, int tot
   }
 }
 
-// Single-workgroup exclusive scan of counts[n] -> offsets[n+1] (int64), cursor[] zeroed.
-__global__ __launch_bounds__(1024) void csr_scan_kernel(const int32_t* counts, int n, int64_t* offsets, int32_t* cursor) {
+// Single-workgroup exclusive scan of counts[n] -> offsets[n+1] (int64); counts is then reset to
+// zero so it can serve as the per-key slot cursor of csr_fill_kernel.
+__global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* counts, int n, int64_t* offsets) {
   __shared__ int64_t part[1024];
   const int tid = threadIdx.x;
   const int per = (n + 1023) / 1024;
@@ -418,7 +529,7 @@ __global__ __launch_bounds__(1024) void csr_scan_kernel(const int32_t* counts, i
   for (int i = a; i < b; ++i) {
     offsets[i] = run;
     run += counts[i];
-    cursor[i] = 0;
+    counts[i] = 0;
   }
   if (tid == 1023) offsets[n] = part[1023];
 }
@@ -447,6 +558,7 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   __shared__ float red[3][kDqk];
   const int s = blockIdx.x;
   if (s >= n_kv) return;
+  constexpr int kChunks = kDqk / 8;
   const int c = threadIdx.x % kChunks, r = threadIdx.x / kChunks;
   const int64_t a = offsets[s], b = offsets[s + 1];
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -471,7 +583,8 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
 }
 
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
-  const int nwaves = p.n_heads >= 128 ? 4 : (p.n_heads + 31) / 32;
+  if (p.topk > kMaxTopkBwd) return -2;
+  const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
   hipLaunchKernelGGL(zero_i32_kernel, dim3((p.n_kv + 255) / 256), dim3(256), 0, stream, p.csr_counts, p.n_kv);
@@ -479,11 +592,19 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
   const int nb = (int)std::min<int64_t>((pairs + 255) / 256, 65536);
   hipLaunchKernelGGL(csr_count_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
                      p.n_kv, p.causal, p.csr_counts);
-  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, p.csr_counts, p.n_kv, p.csr_offsets, p.csr_counts);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, p.csr_counts, p.n_kv, p.csr_offsets);
   hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
                      p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
-  hipLaunchKernelGGL(bwd_sp_kernel, grid, dim3(64 * nwaves), 0, stream, p);
-  hipLaunchKernelGGL(bwd_dq_kernel, grid, dim3(64 * nwaves), 0, stream, p);
+  if (nw == 4) {
+    hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dq_kernel<4>, grid, dim3(256), 0, stream, p);
+  } else if (nw == 2) {
+    hipLaunchKernelGGL(bwd_sp_kernel<2>, grid, dim3(128), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dq_kernel<2>, grid, dim3(128), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(bwd_sp_kernel<1>, grid, dim3(64), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dq_kernel<1>, grid, dim3(64), 0, stream, p);
+  }
   hipLaunchKernelGGL(bwd_g_kernel, dim3(((p.total_q + 7) / 8) * 8), dim3(256), 0, stream, p);
   hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets, p.n_kv,
                      p.dkv, p.dkv_stride);
