@@ -116,6 +116,11 @@ DSA_DEV void async_copy16(const void* gsrc, void* lds_wave_base) {
                                    (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
 }
 
+// Generic pointer to the LDS byte address `a` (inverse of lds_addr).
+DSA_DEV const char* lds_ptr(uint32_t a) {
+  return (const char*)(const __attribute__((address_space(3))) char*)(uintptr_t)a;
+}
+
 // LDS byte address of a pointer into __shared__ memory.
 DSA_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;

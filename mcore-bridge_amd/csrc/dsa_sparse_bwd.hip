@@ -155,15 +155,15 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     }
     if (blk + 2 < nblk)
       gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
-    const char* buf = sm.tile[blk % kStages];
-    uint32_t qv = qk_v, qr = qk_r;
+    const uint32_t tb = lds_addr(sm.tile[blk % kStages]);   // 1 KB aligned: XORs stay in-tile
+    uint32_t qv = tb + qk_v, qr = tb + qk_r;
     asm volatile("" : "+v"(qv), "+v"(qr));
     const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
     // S^T = K . Q^T and dP^T = V . dO^T share the A operand (V = K[:, :512]).
     f32x16 s = f32x16{}, dp = f32x16{};
     {
-      auto addr = [&](int ks) { return buf + (ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
+      auto addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
       u32x4 a[kPre];
 #pragma unroll
       for (int i = 0; i < kPre; ++i) a[i] = lds_load16(addr(i));
@@ -287,10 +287,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
       gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
       copy_ds(sm.ds[(blk + 2) % kStages], blk + 2);
     }
-    const char* buf = sm.tile[blk % kStages];
+    const uint32_t tb = lds_addr(sm.tile[blk % kStages]);   // 1 KB aligned: XORs stay in-tile
     const char* dsl = sm.ds[blk % kStages];
-    uint32_t k00 = kt[0][0], k01 = kt[0][1], k10 = kt[1][0], k11 = kt[1][1];
-    uint32_t r00 = kr[0][0], r01 = kr[0][1], r10 = kr[1][0], r11 = kr[1][1];
+    uint32_t k00 = tb + kt[0][0], k01 = tb + kt[0][1], k10 = tb + kt[1][0], k11 = tb + kt[1][1];
+    uint32_t r00 = tb + kr[0][0], r01 = tb + kr[0][1], r10 = tb + kr[1][0], r11 = tb + kr[1][1];
     asm volatile("" : "+v"(k00), "+v"(k01), "+v"(k10), "+v"(k11), "+v"(r00), "+v"(r01), "+v"(r10), "+v"(r11));
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
       auto ld = [&](int m) {
         const uint32_t x0 = m < 16 ? (v0 ^ (64u * m)) : (q0 ^ (64u * (m - 16)));
         const uint32_t x1 = m < 16 ? (v1 ^ (64u * m)) : (q1 ^ (64u * (m - 16)));
-        const u32x2 lo = lds_read_tr16(buf + x0), hi = lds_read_tr16(buf + x1);
+        const u32x2 lo = lds_read_tr16(lds_ptr(x0)), hi = lds_read_tr16(lds_ptr(x1));
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4 v[kPre];
@@ -463,11 +463,13 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       const u32x2 p_lo = lds_read_tr16(sp + o0), p_hi = lds_read_tr16(sp + o0 + 4 * 64);
       const bf16x8 bs = as_bf16x8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
       const bf16x8 bp = as_bf16x8(u32x4{p_lo[0], p_lo[1], p_hi[0], p_hi[1]});
+      // Q-part products of all tiles first, then the dO-part ones: dependent MFMAs on one
+      // accumulator are 4-5 instructions apart instead of back to back
 #pragma unroll
-      for (int i = 0; i < 5; ++i) {
+      for (int i = 0; i < 5; ++i)
         if (i < nq) acc[i] = mfma32x32x16(as_bf16x8(qa[i][ks]), bs, acc[i]);
-        if (i < 4) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), bp, acc[i]);
-      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), bp, acc[i]);
     }
     // write G rows (bf16); lane key = lane % 32
     const int j = blk * kBK + (lane & 31);

@@ -133,30 +133,30 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       if (blk + 2 < nblk)
         gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
       const char* buf = sm.tile[blk % kStages];
-      uint32_t qv = qk_v, qr = qk_r;
-      uint32_t pv00 = pv[0][0], pv01 = pv[0][1], pv10 = pv[1][0], pv11 = pv[1][1];
-      // opaque per iteration: the swizzled operand addresses are recomputed (one v_xor each)
-      // right before use instead of being hoisted into ~100 loop-invariant VGPRs
+      // per-block absolute operand addresses (tile bases are 1 KB aligned and every XOR below
+      // only touches the low 10 bits); opaque so they are not hoisted into loop-invariant VGPRs
+      const uint32_t tb = lds_addr(buf);
+      uint32_t qv = tb + qk_v, qr = tb + qk_r;
+      uint32_t pv00 = tb + pv[0][0], pv01 = tb + pv[0][1], pv10 = tb + pv[1][0], pv11 = tb + pv[1][1];
       asm volatile("" : "+v"(qv), "+v"(qr), "+v"(pv00), "+v"(pv01), "+v"(pv10), "+v"(pv11));
       const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
-      // ---- S^T[32 keys x 32 heads] = K . Q^T  (two accumulator chains, A prefetched)
+      // ---- S^T[32 keys x 32 heads] = K . Q^T  (A operands prefetched)
       f32x16 s;
       {
-        auto qk_addr = [&](int ks) { return buf + (ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
+        auto qk_addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
         u32x4 a[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; ++i) a[i] = lds_load16(qk_addr(i));
-        f32x16 sa = f32x16{}, sb = f32x16{};
+        f32x16 sa = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < kDqk / 16; ++ks) {
           const u32x4 cur = a[ks % kPre];
           if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
-          if (ks & 1) sb = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sb);
-          else sa = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sa);
+          sa = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sa);
           __builtin_amdgcn_sched_barrier(0);
         }
-        s = sa + sb;
+        s = sa;
       }
 
       // ---- softmax numerator; key of s[i] = (i/4)*8 + 4*hb + i%4
@@ -198,15 +198,15 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
         u32x4 v[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; ++i) {
-          const u32x2 lo = lds_read_tr16(buf + (r0 ^ (64u * i))), hi = lds_read_tr16(buf + (r1 ^ (64u * i)));
+          const u32x2 lo = lds_read_tr16(lds_ptr(r0 ^ (64u * i))), hi = lds_read_tr16(lds_ptr(r1 ^ (64u * i)));
           v[i] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
 #pragma unroll
         for (int m = 0; m < kDv / 32; ++m) {
           const u32x4 cur = v[m % kPre];
           if (m + kPre < kDv / 32) {
-            const u32x2 lo = lds_read_tr16(buf + (r0 ^ (64u * (m + kPre))));
-            const u32x2 hi = lds_read_tr16(buf + (r1 ^ (64u * (m + kPre))));
+            const u32x2 lo = lds_read_tr16(lds_ptr(r0 ^ (64u * (m + kPre))));
+            const u32x2 hi = lds_read_tr16(lds_ptr(r1 ^ (64u * (m + kPre))));
             v[m % kPre] = u32x4{lo[0], lo[1], hi[0], hi[1]};
           }
           o[m] = mfma32x32x16(as_bf16x8(cur), b, o[m]);
