@@ -9,6 +9,8 @@ over T = 16384 packed tokens in 4 causal documents (cu_seqlens 0/10363/15340/155
 value = algorithmic FLOPs of the step / step time:
   sparse fwd 2176*H*N_sel + sparse bwd 5504*H*N_sel + indexer 2*Di*Hi*N_pairs
 (N_sel = sum_q min(K, visible keys) = 27,602,695; N_pairs = causally visible pairs).
+The line also carries a "decode" object for configs[4] (cfg5), whose bound is HBM: gather
+bytes of the selected cache rows / decode attention time.
 """
 from __future__ import annotations
 
@@ -86,12 +88,74 @@ def cpu_baseline(torch):
     }
 
 
+def decode_leg(torch, dev, reps: int = 50):
+    """cfg5 decode through the C ABI with preallocated buffers:
+    64 sequences, one new token each at position L_b - 1, cache lengths of the committed
+    fixture (sum 2,724,446 rows of 576 bf16), indexer 64 x 128 bf16, top-k 2048, 128 heads.
+    The attention is HBM-bound: gather bytes = sum_b min(K, L_b)*576*2 + q + O + idx."""
+    from mcore_bridge_amd import _lib, ops, workloads as W
+    cfg = W.CONFIGS["cfg5"]
+    lens = cfg.decode_lens
+    B, H, K = len(lens), cfg.H, cfg.K
+    N = sum(lens)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = (torch.randn(B, H, 576, generator=g, device=dev) * 0.1).bfloat16()
+    kv = torch.empty(N, 576, dtype=torch.bfloat16, device=dev)
+    for a in range(0, N, 1 << 20):   # fill in slices (bounded fp32 temporaries)
+        n = min(N - a, 1 << 20)
+        kv[a:a + n] = (torch.randn(n, 576, generator=g, device=dev) * 0.1).bfloat16()
+    qi = (torch.randn(B, cfg.Hi, cfg.Di, generator=g, device=dev) * 0.1).bfloat16()
+    ki = (torch.randn(N, cfg.Di, generator=g, device=dev) * 0.1).bfloat16()
+    w = torch.randn(B, cfg.Hi, generator=g, device=dev) / 8
+    cu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(B)], dtype=torch.int32, device=dev)
+    Lmax = max(lens)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3   # us per call
+
+    idx = ops.decode_indexer_topk(qi, ki, w, K, cu, Lmax)
+    t_sel = timed(lambda: ops.decode_indexer_topk(qi, ki, w, K, cu, Lmax))
+    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    ws_bytes = ops.decode_workspace_bytes(B, H, K)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lib = _lib.load()
+    args = (q.data_ptr(), kv.data_ptr(), idx.data_ptr(), B, N, H, 576, 512, K, W.SM_SCALE, out.data_ptr(),
+            lse.data_ptr(), ws.data_ptr(), ws_bytes, stream)
+    _lib.check("dsa_sparse_mla_decode", lib.dsa_sparse_mla_decode(*args))
+    t_attn = timed(lambda: lib.dsa_sparse_mla_decode(*args))
+    gather = sum(min(K, L) for L in lens) * 576 * 2 + q.numel() * 2 + out.numel() * 2 + idx.numel() * 4
+    scan = N * cfg.Di * 2
+    gbs = gather / (t_attn * 1e-6) / 1e9
+    return {
+        "workload": "cfg5: decode, 64 sequences x 1 token, cache lengths fixture (sum 2,724,446 rows), H=128, "
+                    "d_qk=576, d_v=512, indexer 64x128 bf16, top-k 2048",
+        "attention_us": round(t_attn, 2), "gather_bytes": gather, "gather_GBs": round(gbs, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4)},
+        "attention_tflops": round(2176 * H * sum(min(K, L) for L in lens) / (t_attn * 1e-6) / 1e12, 1),
+        "indexer_topk_us": round(t_sel, 2), "indexer_scan_bytes": scan,
+        "indexer_scan_GBs": round(scan / (t_sel * 1e-6) / 1e9, 1),
+        "n_split": ws_bytes // (B * H * (512 * 2 + 4)) if ws_bytes else 1,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the cfg5 decode leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build runs the DSA path on a single MI355X); "
@@ -187,6 +251,9 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": None},
     }
+    if not args.no_decode:
+        res["decode"] = decode_leg(torch, dev)
+        print(f"[bench] decode leg done: {res['decode']['attention_us']} us", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(res), flush=True)

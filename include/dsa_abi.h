@@ -90,6 +90,25 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
                        int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
                        void* out, float* lse, void* stream);
 
+/* Decode rows for the indexer and top-k: sequence b's new token (position L_b - 1) sees its
+ * whole cache, rows [cu_cache[b], cu_cache[b+1]) of the packed cache: row_base[b] = cu_cache[b],
+ * row_len[b] = L_b.  cu_cache [batch + 1] int32 on the device.  No reference counterpart: the
+ * reference's DSA has no KV cache (patcher.py:256 asserts no packing, deepseek_v4.py:94-95 no
+ * inference); this is the decode restriction of the causal rows of dsa_build_rows. */
+int dsa_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,
+                          void* stream);
+/* Workspace bytes for dsa_sparse_mla_decode (0 when the batch alone fills the device). */
+size_t dsa_sparse_mla_decode_workspace_size(int batch, int n_heads, int topk);
+/* Sparse MLA decode: one new query per sequence, q [batch, H, 576] bf16, over its selected rows
+ * of the latent cache kv_cache [n_kv, 576] (idx [batch, topk] global cache row ids, -1 pad).
+ * out [batch, H, 512] bf16, lse [batch, H] fp32.  Same arithmetic as dsa_sparse_mla_fwd with
+ * causal = 0 (the new token sees every cached row); the selected rows are split across
+ * workgroups and merged by their LSE, so a small batch still fills the device.  No reference
+ * counterpart (decode is not implemented by the reference, see dsa_build_decode_rows); the
+ * attention it computes is that of multi_latent_attention.py:262-270 for the last row. */
+int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
+                          int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
+                          void* workspace, size_t workspace_bytes, void* stream);
 /* Workspace bytes for dsa_sparse_mla_bwd. */
 size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk);
 

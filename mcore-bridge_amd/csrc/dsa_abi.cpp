@@ -2,6 +2,7 @@
 // Declarations and the reference interfaces they replace: include/dsa_abi.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
@@ -38,11 +39,34 @@ BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
   return L;
 }
 
+// Decode key splits: enough (sequence, split) work items to give every CU one workgroup
+// (the forward kernel holds one workgroup per CU), at least 4 key blocks of 32 per split.
+struct DecodeSplit {
+  int n_split, split_keys;
+};
+
+DecodeSplit decode_split(int batch, int n_heads, int topk) {
+  constexpr int kCUs = 256;
+  const int items = batch * ((n_heads + 127) / 128);
+  const int blocks = (topk + 31) / 32;
+  int n = (kCUs + items - 1) / items;
+  n = std::max(1, std::min(n, blocks / 4));
+  const int per = (blocks + n - 1) / n;                 // blocks per split
+  return DecodeSplit{(blocks + per - 1) / per, per * 32};
+}
+
+size_t decode_workspace(int batch, int n_heads, int topk) {
+  const DecodeSplit d = decode_split(batch, n_heads, topk);
+  if (d.n_split == 1) return 0;
+  const size_t rows = (size_t)batch * d.n_split * n_heads;
+  return align_up(rows * kDv * sizeof(uint16_t)) + align_up(rows * sizeof(float));
+}
+
 }  // namespace
 
 extern "C" {
 
-int dsa_abi_version(void) { return 100; }
+int dsa_abi_version(void) { return 101; }
 
 const char* dsa_strerror(int status) {
   switch (status) {
@@ -108,10 +132,60 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
   p.out = static_cast<dsa::bf16_t*>(out);
   p.lse = lse;
   p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.causal = causal ? 1 : 0;
+  p.n_split = 1; p.split_keys = topk;
   p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
   p.out_stride_t = (int64_t)n_heads * kDv; p.lse_stride_t = n_heads;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   return dsa::launch_sparse_mla_fwd(p, as_stream(stream));
+}
+
+int dsa_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len, void* stream) {
+  if (batch < 0) return DSA_ERR_INVALID_ARG;
+  if (batch == 0) return DSA_OK;
+  if (!cu_cache || !row_base || !row_len) return DSA_ERR_INVALID_ARG;
+  return dsa::launch_build_decode_rows(cu_cache, batch, row_base, row_len, as_stream(stream));
+}
+
+size_t dsa_sparse_mla_decode_workspace_size(int batch, int n_heads, int topk) {
+  if (batch < 0 || n_heads < 1 || topk < 1) return 0;
+  return decode_workspace(batch, n_heads, topk);
+}
+
+int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
+                          int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
+  if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
+  if (batch == 0) return DSA_OK;
+  if (!q || !kv_cache || !idx || !out || !lse || n_kv < 1) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(kv_cache) || !aligned16(out)) return DSA_ERR_INVALID_ARG;
+  const DecodeSplit d = decode_split(batch, n_heads, topk);
+  const size_t need = decode_workspace(batch, n_heads, topk);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace))) return DSA_ERR_WORKSPACE;
+  dsa::SparseFwdParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.kv = static_cast<const dsa::bf16_t*>(kv_cache);
+  p.idx = idx;
+  p.total_q = batch; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.causal = 0;
+  p.n_split = d.n_split; p.split_keys = d.n_split == 1 ? topk : d.split_keys;
+  p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
+  p.out_stride_t = (int64_t)n_heads * kDv; p.lse_stride_t = n_heads;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  if (d.n_split == 1) {
+    p.out = static_cast<dsa::bf16_t*>(out);
+    p.lse = lse;
+    return dsa::launch_sparse_mla_fwd(p, as_stream(stream));
+  }
+  char* ws = static_cast<char*>(workspace);
+  const size_t rows = (size_t)batch * d.n_split * n_heads;
+  dsa::bf16_t* part_o = reinterpret_cast<dsa::bf16_t*>(ws);
+  float* part_lse = reinterpret_cast<float*>(ws + align_up(rows * kDv * sizeof(uint16_t)));
+  p.out = part_o;
+  p.lse = part_lse;
+  int rc = dsa::launch_sparse_mla_fwd(p, as_stream(stream));
+  if (rc != 0) return rc;
+  return dsa::launch_decode_combine(part_o, part_lse, batch, n_heads, d.n_split, static_cast<dsa::bf16_t*>(out),
+                                    lse, as_stream(stream));
 }
 
 size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk) {

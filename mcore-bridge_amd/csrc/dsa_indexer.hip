@@ -10,7 +10,8 @@
 // row-major with column j <-> key row_base + j, which is also the layout of the reference's
 // returned index_scores when there is one document.
 //
-// K1: one wave = one (query, 2048-key chunk).  Q[64 heads x 128] stays in registers as the A
+// K1: one wave = one (query, key chunk of 256..2048 keys; shorter chunks when there are few
+// queries, e.g. decode, so that enough waves stream keys at once).  Q[64 heads x 128] stays in registers as the A
 // operand (row = head), key rows are the B operand loaded straight from global memory (256 B
 // per key, shared by the 4 waves of a workgroup through L1/L2); C[heads x 32 keys] is reduced
 // over heads in registers: each lane holds 16 heads of one key, so ReLU * w and the head sum
@@ -28,8 +29,10 @@
 namespace dsa {
 
 namespace {
-constexpr int kIdxChunk = 2048;   // keys per wave work item
-constexpr int kMaxHi = 64;        // indexer heads handled by the register tiling
+constexpr int kIdxChunkMax = 2048;  // keys per wave work item (prefill)
+constexpr int kIdxChunkMin = 256;
+constexpr int kIdxWaveTarget = 8192;  // shrink the chunk until this many work items exist
+constexpr int kMaxHi = 64;          // indexer heads handled by the register tiling
 }  // namespace
 
 template <bool FP8>
@@ -38,9 +41,9 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
   const int t = blockIdx.x * 4 + wave;
   if (t >= p.total_q) return;
   const int len = p.row_len[t];
-  const int c0 = blockIdx.y * kIdxChunk;
+  const int c0 = blockIdx.y * p.chunk;
   if (c0 >= len) return;
-  const int c1 = min(len, c0 + kIdxChunk);
+  const int c1 = min(len, c0 + p.chunk);
   const int base = p.row_base[t];
   const int hb = lane >> 5, hl = lane & 31;
   const int Di = p.head_dim;        // 64 or 128
@@ -69,13 +72,20 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
       for (int ks = 0; ks < 8; ++ks)
         qa[mt][ks] = (h < p.n_heads && ks < nks) ? gload16(q + (int64_t)h * Di + 16 * ks + 8 * hb) : u32x4{0, 0, 0, 0};
     }
+    // key block k0: lane reads key min(k0 + hl, c1 - 1) (the tail lanes re-read a valid row)
+    auto load_keys = [&](int k0, u32x4 (&dst)[8]) {
+      const bf16_t* krow = k + (int64_t)(base + min(k0 + hl, c1 - 1)) * Di + 8 * hb;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) dst[ks] = ks < nks ? gload16(krow + 16 * ks) : u32x4{0, 0, 0, 0};
+    };
+    u32x4 kn[8];
+    load_keys(c0, kn);
     for (int k0 = c0; k0 < c1; k0 += 32) {
       const int j = k0 + hl;
-      const int key = base + (j < c1 ? j : c0);
-      const bf16_t* krow = k + (int64_t)key * Di + 8 * hb;
       u32x4 kb[8];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) kb[ks] = ks < nks ? gload16(krow + 16 * ks) : u32x4{0, 0, 0, 0};
+      for (int ks = 0; ks < 8; ++ks) kb[ks] = kn[ks];
+      if (k0 + 32 < c1) load_keys(k0 + 32, kn);   // next block streams in under this one's MFMAs
       f32x16 c0a = f32x16{}, c1a = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
@@ -99,13 +109,20 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
       for (int ks = 0; ks < 8; ++ks)
         qa[mt][ks] = (h < p.n_heads && ks < nks) ? *reinterpret_cast<const long*>(q + (int64_t)h * Di + 16 * ks + 8 * hb) : 0l;
     }
+    auto load_keys = [&](int k0, long (&dst)[8]) {
+      const uint8_t* krow = k + (int64_t)(base + min(k0 + hl, c1 - 1)) * Di + 8 * hb;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) dst[ks] = ks < nks ? *reinterpret_cast<const long*>(krow + 16 * ks) : 0l;
+    };
+    long kn[8];
+    load_keys(c0, kn);
     for (int k0 = c0; k0 < c1; k0 += 32) {
       const int j = k0 + hl;
-      const int key = base + (j < c1 ? j : c0);
-      const uint8_t* krow = k + (int64_t)key * Di + 8 * hb;
+      const int key = base + min(j, c1 - 1);
       long kb[8];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) kb[ks] = ks < nks ? *reinterpret_cast<const long*>(krow + 16 * ks) : 0l;
+      for (int ks = 0; ks < 8; ++ks) kb[ks] = kn[ks];
+      if (k0 + 32 < c1) load_keys(k0 + 32, kn);
       f32x16 c0a = f32x16{}, c1a = f32x16{};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
@@ -129,10 +146,17 @@ __global__ void scores_fill_masked_kernel(float* scores, int64_t pitch, const in
   for (int64_t j = row_len[t] + threadIdx.x; j < pitch; j += blockDim.x) scores[(int64_t)t * pitch + j] = -INFINITY;
 }
 
-int launch_indexer_scores(const IndexerParams& p, hipStream_t stream) {
+int launch_indexer_scores(const IndexerParams& p_in, hipStream_t stream) {
+  IndexerParams p = p_in;
   if (p.n_heads > kMaxHi || (p.head_dim != 128 && p.head_dim != 64)) return -2;
-  int max_len = p.max_row_len;
-  const dim3 grid((p.total_q + 3) / 4, (max_len + kIdxChunk - 1) / kIdxChunk);
+  const int64_t max_len = p.max_row_len;
+  if (p.chunk == 0) {
+    p.chunk = kIdxChunkMax;
+    while (p.chunk > kIdxChunkMin && (int64_t)p.total_q * ((max_len + p.chunk - 1) / p.chunk) < kIdxWaveTarget)
+      p.chunk >>= 1;
+  }
+  if (p.chunk < 32 || p.chunk % 32 != 0) return -1;
+  const dim3 grid((p.total_q + 3) / 4, (unsigned)((max_len + p.chunk - 1) / p.chunk));
   if (grid.y == 0) return 0;
   if (p.fp8)
     hipLaunchKernelGGL(indexer_scores_kernel<true>, grid, dim3(256), 0, stream, p);
@@ -303,6 +327,23 @@ __global__ void build_rows_kernel(const int32_t* cu_seqlens, int n_seq, int tota
   const int start = cu_seqlens[lo], end = cu_seqlens[lo + 1];
   row_base[t] = start;
   row_len[t] = causal ? t - start + 1 : end - start;
+}
+
+// Decode rows: sequence b's one new token sits at position L_b - 1 and sees its whole cache
+// rows [cu_cache[b], cu_cache[b+1]).
+__global__ void build_decode_rows_kernel(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  row_base[b] = cu_cache[b];
+  row_len[b] = cu_cache[b + 1] - cu_cache[b];
+}
+
+int launch_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,
+                             hipStream_t stream) {
+  if (batch == 0) return 0;
+  hipLaunchKernelGGL(build_decode_rows_kernel, dim3((batch + 255) / 256), dim3(256), 0, stream, cu_cache, batch,
+                     row_base, row_len);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int launch_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,

@@ -16,6 +16,9 @@ struct SparseFwdParams {
   bf16_t* out;          // [total_q, n_heads, 512], token stride out_stride_t
   float* lse;           // [total_q, n_heads] natural-log LSE, token stride lse_stride_t
   int total_q, n_heads, n_kv, topk, causal;
+  int n_split;          // key splits per query (1 = whole row; > 1: out/lse are [total_q*n_split]
+                        // rows of normalised partials for launch_decode_combine)
+  int split_keys;       // index slots per split (multiple of 32 when n_split > 1; = topk otherwise)
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, lse_stride_t;
   float scale_log2;     // softmax scale * log2(e)
 };
@@ -54,6 +57,7 @@ struct IndexerParams {
   int total_q, n_heads, head_dim, fp8, max_row_len;
   int64_t pitch;
   int fill_masked;      // also write -inf into columns [row_len, pitch)
+  int chunk;            // keys per wave work item (power of two in [256, 2048]); 0 = launcher picks
 };
 
 struct TopkParams {
@@ -70,6 +74,10 @@ int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream);
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
+int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
+                          bf16_t* out, float* lse, hipStream_t stream);
+int launch_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,
+                             hipStream_t stream);
 int launch_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,
                       int32_t* row_len, hipStream_t stream);
 

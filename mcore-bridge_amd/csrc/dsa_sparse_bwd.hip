@@ -28,6 +28,7 @@
 // vmcnt counts every vector-memory instruction of the wave in issue order, so each wave issues
 // a fixed number of copies and stores per block and the waits count them exactly.
 #include <algorithm>
+#include <type_traits>
 
 #include "dsa_common.h"
 #include "dsa_kernels.h"
@@ -331,23 +332,34 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
 // ------------------------------------------------------------------------------------------
 // B3: per-pair dKV partial rows G = (scale*dS)^T Q + P^T dO, contracted over all heads.
 // Wave w owns output row tiles (32 latent dims each): Q part {4w..4w+3} (+16+w for w < 2),
-// dO part {4w..4w+3}.
+// dO part {4w..4w+3}.  Each block's G tile [32 keys x 576] goes through LDS so that every row
+// is written to its key-major position with contiguous 16-byte lane stores (a wave store
+// covers ~1 KB of one or two rows; written straight from the MFMA layout, every store
+// instruction would touch 32 rows 16 bytes each).
 // ------------------------------------------------------------------------------------------
 constexpr int kGHeads = 128;                        // B3 handles up to 128 heads (n_heads % 16 == 0)
 constexpr int kGKs = kGHeads / 16;                  // head k-steps
 constexpr int kStageTile = kGHeads * 64;            // one staged [128 heads][32 keys] bf16 tile
 constexpr int kRowPitch = kDqk * 2 + 16;            // bytes per staged head row of Q / dO
 constexpr int kSetupRows = 32;                      // head rows staged per setup round
+constexpr int kGRowBytes = kDqk * 2;                // one bf16 G row
+constexpr int kGChunks = kGRowBytes / 16;           // 72 16-byte chunks per row
+constexpr int kGStores = kBK * kGChunks / 256;      // 9 row-chunk stores per thread per block
 
 struct GSmem {
   union {
     char rows[kSetupRows * kRowPitch];              // setup: Q / dO rows for the transposed load
-    char st[kStages][2][kStageTile];                // loop: [dS | P] tiles
-  };
+    char st[kStages][2][kStageTile];                // loop: [dS | P] tiles; 16-byte chunk c of head
+  };                                                //   row h at chunk c ^ (2 * ((h >> 1) & 1))
+  char gtile[kBK * kGRowBytes];                     // block's G rows; chunk c of row r at c ^ (r & 7)
+  int64_t pos[kMaxTopkBwd];                         // G row of every index slot (sink if unselected)
   int32_t idx[kMaxTopkBwd];
   int red[4];
 };
 
+// KS = head k-steps run per block (a power of two >= n_heads / 16; steps past n_heads multiply
+// zero Q^T / dO^T fragments).
+template <int KS>
 __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   constexpr int NW = 4;
   constexpr int G = 2 * kGHeads / 16 / NW;          // 4 copies per wave per block
@@ -360,23 +372,30 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
                                        p.causal, t);
   if (nblk == 0) return;
+  {  // G row of every slot; the loads retire before the setup's final wait
+    const int64_t* pos_row = p.pair_pos + (int64_t)t * p.topk;
+    for (int j = threadIdx.x; j < nblk * kBK; j += NW * 64) {
+      const int64_t v = j < p.topk ? pos_row[j] : -1;
+      sm.pos[j] = v < 0 ? p.g_sink_row : v;
+    }
+  }
   const int nks = p.n_heads / 16;
-  const int nq = wave < 2 ? 5 : 4;
   auto qtile = [&](int i) { return i < 4 ? 4 * wave + i : 16 + wave; };
 
   // ---- Q^T and dO^T fragments (A operand: row = latent dim, k = 8 heads) via LDS, 32 heads a round
-  u32x4 qa[5][kGKs], va[4][kGKs];
+  u32x4 qa[5][KS], va[4][KS];
   const int tr_h = 8 * (g >> 1) + (gi >> 2);        // head row this lane feeds into ds_read_tr
   const int tr_c = 16 * (g & 1) + 4 * (gi & 3);     // latent column this lane feeds
 #pragma unroll
-  for (int ks = 0; ks < kGKs; ++ks) {
+  for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
     for (int i = 0; i < 5; ++i) qa[i][ks] = u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) va[i][ks] = u32x4{0, 0, 0, 0};
   }
+  const int nq = wave < 2 ? 5 : 4;
 #pragma unroll
-  for (int r0 = 0; r0 < kGHeads; r0 += kSetupRows) {
+  for (int r0 = 0; r0 < 16 * KS; r0 += kSetupRows) {
     if (r0 >= p.n_heads) break;
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
@@ -392,7 +411,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
 #pragma unroll
       for (int kk = 0; kk < kSetupRows / 16; ++kk) {
         const int ks = r0 / 16 + kk;
-        if (ks >= nks) continue;
+        if (ks >= nks || ks >= KS) continue;
         const char* rb = sm.rows + (16 * kk + tr_h) * kRowPitch + tr_c * 2;
         if (part == 0) {
 #pragma unroll
@@ -421,7 +440,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   const char* psb = reinterpret_cast<const char*>(p.p_stage + (int64_t)t * p.n_heads * p.topk_pad);
   const int64_t rstride = (int64_t)p.topk_pad * 2;
   auto stage = [&](int s, int blk) {
-    // head rows past n_heads re-read row 0 (valid memory; their k-steps are skipped)
+    // head rows past n_heads re-read row 0 (valid memory; their k-steps multiply zeros)
     const uint32_t b0 = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][0]));
     const uint32_t b1 = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][1]));
     const int w = __builtin_amdgcn_readfirstlane(wave);
@@ -430,65 +449,78 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       const int i = w + k * NW;
       const int h = 16 * i + (lane >> 2);
       const int hs = h < p.n_heads ? h : 0;
-      const int64_t off = hs * rstride + blk * kBK * 2 + (lane & 3) * 16;
+      const int chunk = (lane & 3) ^ (2 * ((h >> 1) & 1));   // LDS chunk lane&3 <- global chunk
+      const int64_t off = hs * rstride + blk * kBK * 2 + chunk * 16;
       async_copy16_unordered(dsb + off, b0 + i * 1024u);
       async_copy16_unordered(psb + off, b1 + i * 1024u);
     }
   };
-  // G rows: every lane stores its fragments each block (keys that are not selected write the
-  // sink row past the last real one), so the per-wave store count is fixed: 4 per owned tile.
-  const int64_t* pos_row = p.pair_pos + (int64_t)t * p.topk;
-  stage(0, 0);
-  if (nblk > 1) stage(1, 1);
-  for (int blk = 0; blk < nblk; ++blk) {
-    // issue order per block: [wait][barrier][copies(blk+2)][compute][stores(blk)] -> after
-    // block blk's copies come stores(blk-1), copies(blk+1)
-    if (blk + 1 >= nblk) wait_vmcnt<0>();
-    else if (blk == 0) wait_vmcnt<G>();
-    else if (nq == 5) wait_vmcnt<G + 20>();
-    else wait_vmcnt<G + 16>();
-    __syncthreads();
-    if (blk + 2 < nblk) stage((blk + 2) % kStages, blk + 2);
-    const char* sd = sm.st[blk % kStages][0];
-    const char* sp = sm.st[blk % kStages][1];
-    f32x16 acc[5];
+  // B operand address of this lane inside a tile: head row 16*ks + tr_h, bytes 2*tr_c .. +8
+  const uint32_t b_off = tr_h * 64 + 16 * (((2 * tr_c) >> 4) ^ (2 * ((tr_h >> 1) & 1))) + ((2 * tr_c) & 15);
+  // G tile LDS slots of this lane: key row lane % 32, chunk 4*qtile(i) + q4, half hb
+  const int gkey = lane & 31;
+
+  auto block_loop = [&](auto nq_c) {
+    constexpr int NQ = decltype(nq_c)::value;
+    stage(0, 0);
+    if (nblk > 1) stage(1, 1);
+    for (int blk = 0; blk < nblk; ++blk) {
+      // issue order per block: [wait][barrier][copies(blk+2)][compute][G -> LDS][barrier]
+      // [stores(blk)]: block blk waits for copies(blk) with copies(blk+1) and stores(blk-1)
+      // still allowed in flight.
+      if (blk + 1 >= nblk) wait_vmcnt<0>();
+      else if (blk == 0) wait_vmcnt<G>();
+      else wait_vmcnt<G + kGStores>();
+      __syncthreads();
+      if (blk + 2 < nblk) stage((blk + 2) % kStages, blk + 2);
+      const char* sd = sm.st[blk % kStages][0] + b_off;
+      const char* sp = sm.st[blk % kStages][1] + b_off;
+      f32x16 acc[NQ];
 #pragma unroll
-    for (int i = 0; i < 5; ++i) acc[i] = f32x16{};
+      for (int i = 0; i < NQ; ++i) acc[i] = f32x16{};
+      auto load_b = [&](int ks, u32x4& bs, u32x4& bp) {
+        const u32x2 s_lo = lds_read_tr16(sd + ks * 1024), s_hi = lds_read_tr16(sd + ks * 1024 + 4 * 64);
+        const u32x2 p_lo = lds_read_tr16(sp + ks * 1024), p_hi = lds_read_tr16(sp + ks * 1024 + 4 * 64);
+        bs = u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]};
+        bp = u32x4{p_lo[0], p_lo[1], p_hi[0], p_hi[1]};
+      };
+      u32x4 bs, bp;
+      load_b(0, bs, bp);
 #pragma unroll
-    for (int ks = 0; ks < kGKs; ++ks) {
-      if (ks >= nks) break;
-      // B operands: dS / P [k = 8 heads][n = key]; lane key = lane % 32
-      const uint32_t o0 = (16 * ks + tr_h) * 64 + tr_c * 2;
-      const u32x2 s_lo = lds_read_tr16(sd + o0), s_hi = lds_read_tr16(sd + o0 + 4 * 64);
-      const u32x2 p_lo = lds_read_tr16(sp + o0), p_hi = lds_read_tr16(sp + o0 + 4 * 64);
-      const bf16x8 bs = as_bf16x8(u32x4{s_lo[0], s_lo[1], s_hi[0], s_hi[1]});
-      const bf16x8 bp = as_bf16x8(u32x4{p_lo[0], p_lo[1], p_hi[0], p_hi[1]});
-      // Q-part products of all tiles first, then the dO-part ones: dependent MFMAs on one
-      // accumulator are 4-5 instructions apart instead of back to back
+      for (int ks = 0; ks < KS; ++ks) {
+        u32x4 bs_n, bp_n;
+        if (ks + 1 < KS) load_b(ks + 1, bs_n, bp_n);   // next k-step's operands under these MFMAs
+        // Q-part products of all tiles first, then the dO-part ones: dependent MFMAs on one
+        // accumulator are NQ instructions apart instead of back to back
 #pragma unroll
-      for (int i = 0; i < 5; ++i)
-        if (i < nq) acc[i] = mfma32x32x16(as_bf16x8(qa[i][ks]), bs, acc[i]);
+        for (int i = 0; i < NQ; ++i) acc[i] = mfma32x32x16(as_bf16x8(qa[i][ks]), as_bf16x8(bs), acc[i]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), bp, acc[i]);
-    }
-    // write G rows (bf16); lane key = lane % 32
-    const int j = blk * kBK + (lane & 31);
-    int64_t pos = j < p.topk ? pos_row[j] : -1;
-    if (pos < 0) pos = p.g_sink_row;
-    bf16_t* grow = p.g_stage + pos * kDqk;
+        for (int i = 0; i < 4; ++i) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), as_bf16x8(bp), acc[i]);
+        if (ks + 1 < KS) { bs = bs_n; bp = bp_n; }
+      }
+      // G tile -> LDS (bf16): lane holds key gkey, dims 32*qtile(i) + 8*q4 + 4*hb .. +3
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      if (i < nq) {
-        const int d0 = 32 * qtile(i);
+      for (int i = 0; i < NQ; ++i) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const int d = d0 + 8 * q4 + 4 * hb;
-          *reinterpret_cast<u32x2*>(grow + d) =
+          const int c = 4 * qtile(i) + q4;
+          *reinterpret_cast<u32x2*>(sm.gtile + gkey * kGRowBytes + 16 * (c ^ (gkey & 7)) + 8 * hb) =
               u32x2{pack_bf16x2(acc[i][4 * q4], acc[i][4 * q4 + 1]), pack_bf16x2(acc[i][4 * q4 + 2], acc[i][4 * q4 + 3])};
         }
       }
+      __syncthreads();
+      // rows -> their key-major G positions, 16 contiguous bytes per lane
+#pragma unroll
+      for (int i = 0; i < kGStores; ++i) {
+        const int cidx = threadIdx.x + 256 * i;
+        const int r = cidx / kGChunks, c = cidx - r * kGChunks;
+        const u32x4 v = lds_load16(sm.gtile + r * kGRowBytes + 16 * (c ^ (r & 7)));
+        *reinterpret_cast<u32x4*>(p.g_stage + sm.pos[blk * kBK + r] * kDqk + c * 8) = v;
+      }
     }
-  }
+  };
+  if (nq == 5) block_loop(std::integral_constant<int, 5>{});
+  else block_loop(std::integral_constant<int, 4>{});
 }
 
 // Zero fill (a kernel, not hipMemsetAsync, so the sequence stays safe under graph capture).
@@ -607,7 +639,16 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(bwd_sp_kernel<1>, grid, dim3(64), 0, stream, p);
     hipLaunchKernelGGL(bwd_dq_kernel<1>, grid, dim3(64), 0, stream, p);
   }
-  hipLaunchKernelGGL(bwd_g_kernel, dim3(((p.total_q + 7) / 8) * 8), dim3(256), 0, stream, p);
+  const int nks = p.n_heads / 16;
+  const dim3 ggrid(((p.total_q + 7) / 8) * 8);
+  if (nks > 4)
+    hipLaunchKernelGGL(bwd_g_kernel<8>, ggrid, dim3(256), 0, stream, p);
+  else if (nks > 2)
+    hipLaunchKernelGGL(bwd_g_kernel<4>, ggrid, dim3(256), 0, stream, p);
+  else if (nks > 1)
+    hipLaunchKernelGGL(bwd_g_kernel<2>, ggrid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(bwd_g_kernel<1>, ggrid, dim3(256), 0, stream, p);
   hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets, p.n_kv,
                      p.dkv, p.dkv_stride);
   return hipGetLastError() == hipSuccess ? 0 : -4;

@@ -60,8 +60,15 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   constexpr int G = tile_copies_per_wave<NW>();
   __shared__ __attribute__((aligned(16))) FwdSmem sm;
 
-  const int t = xcd_remap(blockIdx.x, p.total_q);
-  if (t >= p.total_q) return;
+  // work item = (query t, key split); n_split > 1 only for decode, where a few queries must
+  // still fill the chip: split s covers index slots [s*split_keys, (s+1)*split_keys) and writes
+  // its normalised partial output and LSE to row t*n_split + s (merged by the combine kernel)
+  const int n_items = p.total_q * p.n_split;
+  const int item = xcd_remap(blockIdx.x, n_items);
+  if (item >= n_items) return;
+  const int t = item / p.n_split;
+  const int split = item - t * p.n_split;
+  const int64_t orow = item;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int hb = lane >> 5;          // row half of the MFMA C layout
@@ -81,11 +88,13 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   }
 
   // ---- stage the index row (invalid -> -1) and find the last valid position
-  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
-  const int kpad = (p.topk + kBK - 1) / kBK * kBK;
+  const int k_first = split * p.split_keys;
+  const int n_slots = max(0, min(p.topk - k_first, p.split_keys));
+  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride + k_first;
+  const int kpad = (n_slots + kBK - 1) / kBK * kBK;
   int last = -1;
   for (int j = threadIdx.x; j < kpad; j += NW * 64) {
-    int v = j < p.topk ? idx_row[j] : -1;
+    int v = j < n_slots ? idx_row[j] : -1;
     if (v < 0 || v >= p.n_kv || (p.causal && v > t)) v = -1;
     sm.idx[j] = v;
     if (v >= 0) last = j;
@@ -227,7 +236,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   // ---- epilogue: normalise, store O (bf16) and LSE (natural log)
   if (!head_ok) return;
   const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
-  bf16_t* orow = p.out + (int64_t)t * p.out_stride_t + (int64_t)head * kDv;
+  bf16_t* optr = p.out + orow * p.out_stride_t + (int64_t)head * kDv;
 #pragma unroll
   for (int m = 0; m < kDv / 32; ++m) {
 #pragma unroll
@@ -236,18 +245,54 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       u32x2 v;
       v[0] = pack_bf16x2(o[m][4 * q4 + 0] * inv_l, o[m][4 * q4 + 1] * inv_l);
       v[1] = pack_bf16x2(o[m][4 * q4 + 2] * inv_l, o[m][4 * q4 + 3] * inv_l);
-      *reinterpret_cast<u32x2*>(orow + dv) = v;
+      *reinterpret_cast<u32x2*>(optr + dv) = v;
     }
   }
   if (hb == 0) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-    p.lse[(int64_t)t * p.lse_stride_t + head] = l_run > 0.f ? (m_use + __log2f(l_run)) * kLn2 : -INFINITY;
+    p.lse[orow * p.lse_stride_t + head] = l_run > 0.f ? (m_use + __log2f(l_run)) * kLn2 : -INFINITY;
   }
 }
 
+// Decode split merge: out[b,h] = sum_s e^{lse_s} O_s / sum_s e^{lse_s} over the n_split
+// normalised partials of (b, h); lse[b,h] = ln sum_s e^{lse_s}.  One wave per (b, h), 8 dv per lane.
+__global__ __launch_bounds__(256) void decode_combine_kernel(const bf16_t* part_o, const float* part_lse,
+                                                             int batch, int n_heads, int n_split,
+                                                             bf16_t* out, float* lse) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= batch * n_heads) return;
+  const int lane = threadIdx.x & 63;
+  const int b = r / n_heads, h = r - b * n_heads;
+  const int64_t prow0 = (int64_t)b * n_split * n_heads + h;   // partial row of split 0
+  float m = -INFINITY;
+  for (int s = 0; s < n_split; ++s) m = fmaxf(m, part_lse[prow0 + (int64_t)s * n_heads]);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  if (m != -INFINITY) {
+    for (int s = 0; s < n_split; ++s) {
+      const int64_t prow = prow0 + (int64_t)s * n_heads;
+      const float wgt = fast_exp2((part_lse[prow] - m) * kLog2e);
+      den += wgt;
+      const u32x4 v = gload16(part_o + prow * kDv + 8 * lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += wgt * bf16_lo(v[e]);
+        acc[2 * e + 1] += wgt * bf16_hi(v[e]);
+      }
+    }
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+  *reinterpret_cast<u32x4*>(out + (int64_t)r * kDv + 8 * lane) = o;
+  if (lane == 0) lse[r] = den > 0.f ? m + __log2f(den) * kLn2 : -INFINITY;
+}
+
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
-  if (p.topk > kMaxTopk) return -2;
-  const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
+  if (p.split_keys > kMaxTopk || p.n_split < 1 || (p.n_split > 1 && p.split_keys % kBK != 0)) return -2;
+  if ((int64_t)(p.n_split - 1) * p.split_keys >= p.topk) return -1;   // every split owns >= 1 slot
+  const dim3 grid(((p.total_q * p.n_split + 7) / 8) * 8, (p.n_heads + 127) / 128);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   if (nw == 4)
     hipLaunchKernelGGL(sparse_mla_fwd_kernel<4>, grid, dim3(256), 0, stream, p);
@@ -255,6 +300,15 @@ int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(sparse_mla_fwd_kernel<2>, grid, dim3(128), 0, stream, p);
   else
     hipLaunchKernelGGL(sparse_mla_fwd_kernel<1>, grid, dim3(64), 0, stream, p);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
+                          bf16_t* out, float* lse, hipStream_t stream) {
+  const int rows = batch * n_heads;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, part_o, part_lse, batch,
+                     n_heads, n_split, out, lse);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

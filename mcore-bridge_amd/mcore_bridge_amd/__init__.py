@@ -7,11 +7,12 @@ kernels of ``libdsa_amd.so`` (C ABI: include/dsa_abi.h); there is no CPU fallbac
 """
 from . import _lib
 from .dsa import fused_qk_topk_naive, sparse_mla_attention
-from .ops import (build_rows, bwd_workspace_bytes, indexer_scores, indexer_topk, sparse_mla, sparse_mla_bwd,
-                  sparse_mla_fwd, topk)
+from .ops import (build_decode_rows, build_rows, bwd_workspace_bytes, decode_indexer_topk, decode_workspace_bytes,
+                  indexer_scores, indexer_topk, sparse_mla, sparse_mla_bwd, sparse_mla_decode, sparse_mla_fwd, topk)
 
 __all__ = [
-    "build_rows", "bwd_workspace_bytes", "fused_qk_topk_naive", "indexer_scores", "indexer_topk",
-    "sparse_mla", "sparse_mla_attention", "sparse_mla_bwd", "sparse_mla_fwd", "topk",
+    "build_decode_rows", "build_rows", "bwd_workspace_bytes", "decode_indexer_topk", "decode_workspace_bytes",
+    "fused_qk_topk_naive", "indexer_scores", "indexer_topk", "sparse_mla", "sparse_mla_attention",
+    "sparse_mla_bwd", "sparse_mla_decode", "sparse_mla_fwd", "topk",
 ]
 __version__ = "0.1.0"

@@ -37,6 +37,10 @@ SIGNATURES = {
     "dsa_topk": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "dsa_sparse_mla_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                    c_float, c_int, c_void_p, c_void_p, c_void_p]),
+    "dsa_build_decode_rows": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "dsa_sparse_mla_decode_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "dsa_sparse_mla_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                      c_float, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsa_sparse_mla_bwd_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_void_p,

@@ -139,6 +139,41 @@ def indexer_topk(q: Tensor, k: Tensor, w: Tensor, index_topk: int, cu_seqlens: O
     return (idx, sc) if return_scores else idx
 
 
+@torch.library.custom_op("dsa_amd::build_decode_rows", mutates_args=())
+def build_decode_rows(cu_cache: Tensor) -> Tuple[Tensor, Tensor]:
+    """Per-sequence ``(row_base, row_len)`` int32 of one new token per sequence over its whole
+    cache: ``row_base[b] = cu_cache[b]``, ``row_len[b] = cu_cache[b+1] - cu_cache[b]``."""
+    _require_gpu(cu_cache)
+    cu = cu_cache.to(torch.int32).contiguous()
+    B = cu.numel() - 1
+    base = torch.empty(B, dtype=torch.int32, device=cu.device)
+    ln = torch.empty(B, dtype=torch.int32, device=cu.device)
+    with torch.cuda.device(cu.device):
+        _lib.call("dsa_build_decode_rows", _p(cu), B, _p(base), _p(ln), _stream(cu.device))
+    return base, ln
+
+
+@build_decode_rows.register_fake
+def _(cu_cache):
+    B = cu_cache.shape[0] - 1
+    return cu_cache.new_empty(B, dtype=torch.int32), cu_cache.new_empty(B, dtype=torch.int32)
+
+
+def decode_indexer_topk(q: Tensor, k_cache: Tensor, w: Tensor, index_topk: int, cu_cache: Tensor,
+                        max_cache_len: Optional[int] = None, q_scale: Optional[Tensor] = None,
+                        k_scale: Optional[Tensor] = None, return_scores: bool = False):
+    """K1 + K2 for decode: ``q [B, Hi, Di]`` (one new token per sequence), ``k_cache [sum L, Di]``
+    packed by ``cu_cache [B+1]``.  Returns ``idx [B, index_topk]`` int32 global cache rows
+    (ascending, ``-1`` pad) and, with ``return_scores``, the fp32 scores ``[B, max L]``."""
+    if max_cache_len is None:
+        max_cache_len = int((cu_cache[1:] - cu_cache[:-1]).max().item())
+    base, ln = build_decode_rows(cu_cache)
+    pitch = max(4, (max_cache_len + 3) // 4 * 4)
+    sc = indexer_scores(q, k_cache, w, base, ln, max_cache_len, pitch, q_scale, k_scale, return_scores)
+    idx = topk(sc, base, ln, index_topk)
+    return (idx, sc) if return_scores else idx
+
+
 # --------------------------------------------------------------------------------------
 # K3 / K4 sparse MLA
 # --------------------------------------------------------------------------------------
@@ -170,6 +205,36 @@ def sparse_mla_fwd(q: Tensor, kv: Tensor, idx: Tensor, sm_scale: float, causal: 
 def _(q, kv, idx, sm_scale, causal=False):
     T, H, _ = q.shape
     return q.new_empty(T, H, D_V), q.new_empty(T, H, dtype=torch.float32)
+
+
+def decode_workspace_bytes(batch: int, n_heads: int, topk_: int) -> int:
+    return int(_lib.load().dsa_sparse_mla_decode_workspace_size(batch, n_heads, topk_))
+
+
+@torch.library.custom_op("dsa_amd::sparse_mla_decode", mutates_args=())
+def sparse_mla_decode(q: Tensor, kv_cache: Tensor, idx: Tensor, sm_scale: float) -> Tuple[Tensor, Tensor]:
+    """Decode attention of one new token per sequence: ``q [B,H,576]`` over its selected rows
+    of ``kv_cache [N,576]`` (``idx [B,K]`` global rows).  ``(out [B,H,512] bf16, lse [B,H])``."""
+    _check_attn(q, kv_cache, idx)
+    q = q.contiguous()
+    kv_cache = kv_cache.contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    B, H, _ = q.shape
+    K = idx.shape[1]
+    out = torch.empty(B, H, D_V, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, H, dtype=torch.float32, device=q.device)
+    ws_bytes = decode_workspace_bytes(B, H, K)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_sparse_mla_decode", _p(q), _p(kv_cache), _p(idx), B, kv_cache.shape[0], H, D_QK, D_V, K,
+                  float(sm_scale), _p(out), _p(lse), _p(ws), ws_bytes, _stream(q.device))
+    return out, lse
+
+
+@sparse_mla_decode.register_fake
+def _(q, kv_cache, idx, sm_scale):
+    B, H, _ = q.shape
+    return q.new_empty(B, H, D_V), q.new_empty(B, H, dtype=torch.float32)
 
 
 def bwd_workspace_bytes(total_q: int, n_kv: int, n_heads: int, topk_: int) -> int:

@@ -79,6 +79,25 @@ def test_bwd_workspace_size_formula():
     assert lib.dsa_sparse_mla_bwd_workspace_size(-1, N, H, K) == 0
 
 
+def test_decode_entry_points_validate_and_size():
+    lib = _lib.load()
+    # batch 64 x 128 heads fills 64 of 256 CUs -> 4 key splits of 512 slots: bf16 partial rows + fp32 LSEs
+    rows = 64 * 4 * 128
+    assert lib.dsa_sparse_mla_decode_workspace_size(64, 128, 2048) == rows * 512 * 2 + rows * 4
+    assert lib.dsa_sparse_mla_decode_workspace_size(256, 128, 2048) == 0     # the batch alone fills the device
+    assert lib.dsa_sparse_mla_decode_workspace_size(64, 128, 64) == 0        # too few keys to split
+    assert lib.dsa_sparse_mla_decode_workspace_size(0, 0, 2048) == 0
+    dec = lambda q, dqk, ws, nbytes, batch=64: lib.dsa_sparse_mla_decode(q, P, P, batch, 100, 128, dqk, 512, 2048, 0.1,
+                                                                         P, P, ws, nbytes, N)
+    assert dec(P, 512, P, 1 << 30) == _lib.DSA_ERR_UNSUPPORTED
+    assert dec(N, 576, P, 1 << 30) == _lib.DSA_ERR_INVALID_ARG
+    assert dec(P, 576, N, 0) == _lib.DSA_ERR_WORKSPACE
+    assert dec(P, 576, P, 1024) == _lib.DSA_ERR_WORKSPACE
+    assert dec(N, 576, N, 0, batch=0) == _lib.DSA_OK
+    assert lib.dsa_build_decode_rows(N, 4, P, P, N) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_build_decode_rows(N, 0, N, N, N) == _lib.DSA_OK
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     from mcore_bridge_amd import ops

@@ -247,3 +247,116 @@ def test_sparse_mla_attention_sbhd_batch2():
     for b in range(B):
         ref = O.naive_unfused_sparse_attn_fp32(q[:, b:b + 1].float(), kv[:, b:b + 1].float(), ti[b:b + 1], W.SM_SCALE)
         _close(out[:, b], ref[:, 0], name=f"batch {b}")
+
+
+# ------------------------------------------------------------------ K5/K6 decode
+def _cu(lens):
+    cu = [0]
+    for L in lens:
+        cu.append(cu[-1] + L)
+    return torch.tensor(cu, dtype=torch.int32)
+
+
+def _decode_idx(lens, K, seed, device="cpu"):
+    """Per sequence a sorted random distinct subset of min(K, L) of its cache rows (global ids)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    cu = _cu(lens).tolist()
+    idx = torch.full((len(lens), K), -1, dtype=torch.int32, device=device)
+    for b, L in enumerate(lens):
+        m = min(K, L)
+        sel = torch.randperm(L, generator=g, device=device)[:m].sort().values
+        idx[b, :m] = (sel + cu[b]).to(torch.int32)
+    return idx
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_indexer_topk(fp8):
+    lens = [3000, 5000, 20000, 1500, 700, 2048]
+    print(f"[decode indexer+topk] fp8={fp8} lens={lens}", flush=True)
+    cfg = W.CONFIGS["cfg5"]
+    d = W.make_decode(cfg, lens=lens, H=16, seed=11)
+    cu = _cu(lens)
+    q, k, w = d["q_idx"], d["k_cache"], d["w"]
+    if fp8:
+        q8, qs = O.quantize_e4m3_rows(q * 10)
+        k8, ks = O.quantize_e4m3_rows(k * 10)
+        args = (q8.to(DEV), k8.to(DEV), w.to(DEV), cfg.K, cu.to(DEV), max(lens), qs.to(DEV), ks.to(DEV))
+        ref = O.decode_indexer_scores(q8.float(), k8.float(), w, cu[:-1], torch.tensor(lens), q_scale=qs, k_scale=ks)
+    else:
+        q, k = q.bfloat16(), k.bfloat16()
+        args = (q.to(DEV), k.to(DEV), w.to(DEV), cfg.K, cu.to(DEV), max(lens))
+        ref = O.decode_indexer_scores(q, k, w, cu[:-1], torch.tensor(lens))
+    idx, sc = ops.decode_indexer_topk(*args, return_scores=True)
+    idx, sc = idx.cpu().long(), sc.cpu().double()
+    tol = dict(rtol=2e-3, atol=2e-3) if fp8 else dict(rtol=1e-4, atol=1e-5)
+    for b, L in enumerate(lens):
+        torch.testing.assert_close(sc[b, :L], ref[b, :L], **tol)
+    # bit-exact selection from the kernel's own fp32 scores; >= 99.9 % overlap vs float64 scores
+    masked = sc.clone()
+    for b, L in enumerate(lens):
+        masked[b, L:] = float("-inf")
+    off = cu[:-1].long()[:, None]
+    want = O.topk_indices(masked, cfg.K)
+    assert torch.equal(idx, torch.where(want >= 0, want + off, want))
+    exact = O.topk_indices(ref, cfg.K)
+    inter = tot = 0
+    for b in range(len(lens)):
+        a = set(idx[b][idx[b] >= 0].tolist())
+        r = set((exact[b][exact[b] >= 0] + off[b]).tolist())
+        inter += len(a & r)
+        tot += len(r)
+    assert inter / tot >= 0.999, inter / tot
+    assert (idx[4, 700:] == -1).all() and (idx[4, :700] == torch.arange(700) + int(cu[4])).all()
+
+
+@pytest.mark.parametrize("lens,H,K", [([3000, 700, 5000, 1200, 64], 128, 2048), ([4096], 128, 2048),
+                                      ([900, 333, 2100], 16, 512), ([500, 600], 64, 100)])
+def test_sparse_decode(lens, H, K):
+    print(f"[decode attention] lens={lens} H={H} K={K}", flush=True)
+    d = W.make_decode(W.CONFIGS["cfg5"], lens=lens, H=H, seed=len(lens) + H)
+    q, kv = d["q"].bfloat16(), d["kv_cache"].bfloat16()
+    idx = _decode_idx(lens, K, seed=K)
+    out, lse = ops.sparse_mla_decode(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE)
+    o_ref, l_ref = O.sparse_mla_decode(q, kv, idx, W.SM_SCALE)
+    _close(out.cpu(), o_ref, name="out")
+    _close(lse.cpu(), l_ref, rel=1e-4, name="lse")
+
+
+def test_sparse_decode_empty_rows():
+    print("[decode attention empty rows]", flush=True)
+    lens = [300, 300, 300]
+    d = W.make_decode(W.CONFIGS["cfg5"], lens=lens, H=32, seed=5)
+    q, kv = d["q"].bfloat16(), d["kv_cache"].bfloat16()
+    idx = _decode_idx(lens, 2048, seed=1)
+    idx[1] = -1                                   # nothing selected -> out 0, lse -inf
+    idx[2, 5] = 10 ** 6                           # out of range -> ignored
+    out, lse = ops.sparse_mla_decode(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE)
+    ref_idx = idx.clone()
+    ref_idx[2, 5] = -1
+    o_ref, l_ref = O.sparse_mla_decode(q, kv, ref_idx, W.SM_SCALE)
+    assert (out[1] == 0).all() and torch.isinf(lse[1]).all() and (lse[1] < 0).all()
+    _close(out.cpu(), o_ref, name="out")
+    ok = torch.isfinite(l_ref)
+    _close(lse.cpu()[ok], l_ref[ok], rel=1e-4, name="lse")
+
+
+def test_sparse_decode_cfg5_full_size():
+    """cfg5 at full size: the split decode equals the unsplit non-causal forward kernel on the same
+    inputs (a size-independent property), and the oracle on two whole sequences."""
+    print("[decode attention cfg5 full size]", flush=True)
+    cfg = W.CONFIGS["cfg5"]
+    lens = cfg.decode_lens
+    g = torch.Generator(device=DEV).manual_seed(0)
+    q = (torch.randn(len(lens), cfg.H, 576, generator=g, device=DEV) * 0.1).bfloat16()
+    kv = (torch.randn(sum(lens), 576, generator=g, device=DEV) * 0.1).bfloat16()
+    idx = _decode_idx(lens, cfg.K, seed=3, device=DEV)
+    out, lse = ops.sparse_mla_decode(q, kv, idx, W.SM_SCALE)
+    ref_o, ref_l = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, False)
+    _close(out, ref_o, rel=5e-3, name="decode vs fwd out")
+    _close(lse, ref_l, rel=1e-5, name="decode vs fwd lse")
+    for b in (0, 31):
+        rows = idx[b][idx[b] >= 0].long()
+        o_ref, l_ref = O.sparse_mla_decode(q[b:b + 1].cpu(), kv[rows].cpu(),
+                                           torch.arange(rows.numel(), dtype=torch.int32)[None], W.SM_SCALE)
+        _close(out[b:b + 1].cpu(), o_ref, name=f"seq {b}")
+        _close(lse[b:b + 1].cpu(), l_ref, rel=1e-4, name=f"lse {b}")
