@@ -85,7 +85,8 @@ int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const 
  * absorbed MQA-latent form: out[t,h] = softmax_j(sm_scale * q[t,h] . kv[idx[t,j]]) kv[idx[t,j], :512],
  * lse[t,h] = ln sum_j exp(sm_scale * q[t,h] . kv[idx[t,j]]).  d_qk must be 576, d_v 512.
  * causal != 0 additionally ignores indices > t (the reference's triu mask).  A row without
- * a valid index yields out = 0, lse = -inf. */
+ * a valid index yields out = 0, lse = -inf.  sm_scale must be finite and > 0 (the reference's
+ * softmax scale 1/sqrt(d) * mscale^2 always is). */
 int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv,
                        int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
                        void* out, float* lse, void* stream);

@@ -120,7 +120,8 @@ int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const 
 int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv, int n_heads,
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* out, float* lse,
                        void* stream) {
-  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
+    return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (total_q == 0) return DSA_OK;
   if (!q || !kv || !idx || !out || !lse || n_kv < 1) return DSA_ERR_INVALID_ARG;
@@ -154,7 +155,8 @@ size_t dsa_sparse_mla_decode_workspace_size(int batch, int n_heads, int topk) {
 int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
                           int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
                           void* workspace, size_t workspace_bytes, void* stream) {
-  if (batch < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
+  if (batch < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
+    return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (batch == 0) return DSA_OK;
   if (!q || !kv_cache || !idx || !out || !lse || n_kv < 1) return DSA_ERR_INVALID_ARG;

@@ -1,7 +1,7 @@
 // Shared device helpers for the gfx950 DSA kernels (CDNA4, wave64).
 //
-// MFMA operand layouts used throughout (checked on the device by tests/test_gpu_kernels.py
-// through the parity tests, and by construction below):
+// MFMA operand layouts used throughout (checked on the device through the parity tests in
+// tests/test_gpu_parity.py, and by construction below):
 //   v_mfma_f32_32x32x16_bf16  C[32x32] += A[32x16] * B[16x32]
 //     A: lane l holds A[row = l%32][k = (l/32)*8 + 0..7]
 //     B: lane l holds B[k = (l/32)*8 + 0..7][col = l%32]
@@ -47,10 +47,11 @@ DSA_DEV u32x4 gload16(const void* p) { return *reinterpret_cast<const u32x4*>(p)
 DSA_DEV bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 DSA_DEV u32x4 as_u32x4(const bf16x8& v) { return __builtin_bit_cast(u32x4, v); }
 
-// Pack two floats into one dword of two bf16 (round to nearest even).
+// Pack two floats into one dword of two bf16 (round to nearest even): one v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 DSA_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  bf16_t a = (bf16_t)lo, b = (bf16_t)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
 DSA_DEV float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }

@@ -1,44 +1,42 @@
 // LDS tile of 32 gathered latent KV rows (576 bf16 each) and its gather, shared by the sparse
 // MLA forward and backward kernels (gfx950).
 //
-// Layout (36 KB per tile):
-//   V region    [32 rows][64 chunks of 16 B]  (latent dims 0..511), 1 KB per row.  Chunk c of
-//               row r sits at slot c ^ swz(r), swz(r) = (4r + r/4) & 63.
-//   rope region [32 rows][8 chunks of 16 B]   (dims 512..575).  Chunk c of row r sits at slot
-//               c ^ ((r >> 1) & 7).
-// The swizzles make both access patterns of the kernels bank-conflict free: 16 lanes reading
-// the same chunk of 16 consecutive rows (QK operand, ds_read_b128), and 32 lanes reading 4
-// rows x 4 neighbouring chunks in 8-byte halves (ds_read_b64_tr_b16 operands of PV / dQ).
+// Layout (37,376 B per tile; tiles are 128-byte aligned):
+//   V region    32 rows x 1040 B: latent dims 0..511 of one key in natural order + 16 B pad.
+//               Key k of the block lives in row key_row(k) = (k & ~7) | ((k & 3) << 1) | ((k >> 2) & 1).
+//   rope region [32 keys][8 chunks of 16 B] (dims 512..575); chunk c of key k sits at slot
+//               c ^ ((k >> 1) & 7).
+// LDS serves 8 lanes of a ds_read_b128 (16 lanes of a ds_read_b64_tr_b16) per clock from 32
+// four-byte banks (measured on MI355X).  The 1040-byte pitch puts 8 consecutive rows on 8
+// different 16-byte bank groups, so the QK operand read (8 consecutive lanes = 8 consecutive
+// keys, one 16-byte chunk each) is conflict free; key_row() places the 4 consecutive keys of
+// one 16-lane group of a transposing PV / dQ read on rows 2 apart (4 x 32 B, distinct banks).
+// Every V operand address is a per-lane base plus an immediate offset -- no per-access XOR.
 //
-// Gather: one wave instruction (global_load_lds_dwordx4, 64 lanes x 16 B) fills one V row --
-// the row id is wave-uniform (readlane), the address is SGPR base + per-lane offset and the
-// 64 lanes read one contiguous 1 KB row in swizzled order; 4 more instructions fill the rope
-// region (8 rows x 8 chunks each).  36 instructions per tile, split evenly over 1, 2 or 4
-// waves.  The copies are issued through inline asm (see async_copy16_unordered): the caller
-// completes them with s_waitcnt vmcnt + a barrier.
+// Gather: one wave instruction (global_load_lds_dwordx4, 64 lanes x 16 B) fills one V row:
+// the KV row address is wave-uniform (two readlanes into an SGPR pair) and lane i copies
+// chunk i to row base + 16*i.  4 more instructions fill the rope region (8 keys x 8 chunks
+// each).  36 instructions per tile, split evenly over 1, 2 or 4 waves.  The copies are issued
+// through inline asm: the caller completes them with s_waitcnt vmcnt + a barrier.
 #pragma once
 #include "dsa_common.h"
 
 namespace dsa {
 
 constexpr int kTileKeys = 32;
-constexpr int kTileVBytes = 32 * 1024;
+constexpr int kTileVPitch = 1040;
+constexpr int kTileVBytes = 32 * kTileVPitch;               // 33,280
 constexpr int kTileRopeBytes = 32 * 128;
-constexpr int kTileBytes = kTileVBytes + kTileRopeBytes;   // 36864
+constexpr int kTileBytes = kTileVBytes + kTileRopeBytes;    // 37,376 = 292 * 128
 constexpr int kTileInstr = 36;
 constexpr int kLatent = 576;
 
-DSA_DEV uint32_t kv_swz(uint32_t r) { return ((4u * r) + (r >> 2)) & 63u; }
+// V row of block key k (0..31).
+DSA_DEV constexpr uint32_t key_row(uint32_t k) { return (k & ~7u) | ((k & 3u) << 1) | ((k >> 2) & 1u); }
 
-// Byte offset of (row r, chunk c) inside a tile (c in 0..71).
-DSA_DEV uint32_t tile_off(uint32_t r, uint32_t c) {
-  return c < 64 ? r * 1024u + 16u * (c ^ kv_swz(r)) : kTileVBytes + r * 128u + 16u * ((c - 64) ^ ((r >> 1) & 7u));
-}
-
-// global_load_lds_dwordx4 with a scalar 64-bit base and a per-lane 32-bit byte offset.
-DSA_DEV void async_copy16_sv(const void* sbase, uint32_t voff, uint32_t lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(voff), "s"(sbase)
-               : "memory", "m0");
+// Byte offset of (key k, 16-byte chunk c) inside a tile (c in 0..71).
+DSA_DEV uint32_t tile_off(uint32_t k, uint32_t c) {
+  return c < 64 ? key_row(k) * kTileVPitch + 16u * c : kTileVBytes + k * 128u + 16u * ((c - 64) ^ ((k >> 1) & 7u));
 }
 
 // Copies issued per wave per tile.
@@ -48,31 +46,63 @@ constexpr int tile_copies_per_wave() {
   return kTileInstr / NW;
 }
 
-// Gather the 32 rows whose ids lane l%32 holds in `row_of_lane` (-1 = none: row 0 is loaded
-// and the caller masks it) into `tile`.
+// Per-lane gather sources of one wave for one block, from the block's 32 KV row ids in LDS
+// (idx_blk[k], -1 = no key: row 0 is loaded and the caller masks it).
+//   v     lane j < 32/NW: KV row address of key w + NW*j (its V copy is copy j)
+//   rope  [j]: this lane's 16 source bytes of rope group w + NW*j (keys 8*group + lane/8)
 template <int NW>
-DSA_DEV void gather_tile(char* tile, int row_of_lane, const bf16_t* kv, int wave, int lane) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(tile));
-  const int w = __builtin_amdgcn_readfirstlane(wave);
-  const char* kvb = reinterpret_cast<const char*>(kv);
+struct TileSrc {
+  const char* v;
+  const char* rope[4 / NW];
+};
+
+DSA_DEV const char* kv_row_addr(const bf16_t* kv, int row) {
+  return reinterpret_cast<const char*>(kv) + (int64_t)(row >= 0 ? row : 0) * (kLatent * 2);
+}
+
+template <int NW>
+DSA_DEV TileSrc<NW> tile_sources(const bf16_t* kv, const int32_t* idx_blk, int wave, int lane) {
+  TileSrc<NW> s;
+  s.v = kv_row_addr(kv, idx_blk[wave + NW * (lane % (32 / NW))]);
 #pragma unroll
-  for (int k = 0; k < 32 / NW; ++k) {
-    const int r = w + k * NW;
-    const int row = __builtin_amdgcn_readlane(row_of_lane, r);
-    const char* src = kvb + (int64_t)(row >= 0 ? row : 0) * (kLatent * 2);
-    async_copy16_sv(src, (uint32_t)(lane ^ kv_swz(r)) * 16u, base + r * 1024u);
+  for (int j = 0; j < 4 / NW; ++j) {
+    const int key = 8 * (wave + NW * j) + (lane >> 3);
+    const uint32_t c = (uint32_t)(lane & 7) ^ ((key >> 1) & 7u);
+    s.rope[j] = kv_row_addr(kv, idx_blk[key]) + (64 + c) * 16;
   }
+  return s;
+}
+
+// global_load_lds_dwordx4 with a scalar 64-bit row address and a per-lane byte offset.
+DSA_DEV void copy_row16(uint32_t lds_wave_base, const char* row, uint32_t lane_off) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(lane_off), "s"(row)
+               : "memory", "m0");
+}
+
+// Copy k (0 <= k < tile_copies_per_wave<NW>()) of this wave's share of a tile gather into the
+// tile at LDS byte address `tile`.  Copies 0 .. 32/NW-1 fill the V rows of keys w + NW*k
+// (row key_row(w + NW*k) = key_row(NW*k) + 2w), the rest fill rope groups.
+template <int NW>
+DSA_DEV void gather_part(uint32_t tile, const TileSrc<NW>& src, int wave, int lane, int k) {
+  const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+  if (k < 32 / NW) {
+    const uint64_t a = (uint64_t)src.v;
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)a, k);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(a >> 32), k);
+    const char* row = reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+    copy_row16(tile + (key_row(NW * k) + 2 * w) * kTileVPitch, row, (uint32_t)lane * 16u);
+  } else {
+    const int j = k - 32 / NW;
+    async_copy16_unordered(src.rope[j], tile + kTileVBytes + (w + NW * j) * 1024u);
+  }
+}
+
+// The whole gather of one tile (all of this wave's copies back to back).
+template <int NW>
+DSA_DEV void gather_tile(uint32_t tile, const bf16_t* kv, const int32_t* idx_blk, int wave, int lane) {
+  const TileSrc<NW> src = tile_sources<NW>(kv, idx_blk, wave, lane);
 #pragma unroll
-  for (int j = 0; j < 4; j += NW) {
-    const int jj = j + w;
-    if (NW == 4 || jj < 4) {
-      const int r = 8 * jj + (lane >> 3);
-      const int row = __shfl(row_of_lane, r, 64);
-      const uint32_t c = (uint32_t)(lane & 7) ^ ((r >> 1) & 7u);
-      const char* src = kvb + (int64_t)(row >= 0 ? row : 0) * (kLatent * 2) + (64 + c) * 16;
-      async_copy16_unordered(src, base + kTileVBytes + jj * 1024u);
-    }
-  }
+  for (int k = 0; k < tile_copies_per_wave<NW>(); ++k) gather_part<NW>(tile, src, wave, lane, k);
 }
 
 }  // namespace dsa

@@ -91,7 +91,9 @@ template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   constexpr int G = tile_copies_per_wave<NW>();
   constexpr int S = 8;  // staging stores per wave per block (4 x P, 4 x dS)
-  __shared__ __attribute__((aligned(16))) SpSmem sm;
+  constexpr int kCopyEvery = kDqk / 16 / G;   // S/dP steps per gather copy
+  static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the k-steps");
+  __shared__ __attribute__((aligned(128))) SpSmem sm;
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -133,11 +135,13 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   const int64_t stage_off = ((int64_t)t * p.n_heads + hsafe) * p.topk_pad + hb * 4;
   bf16_t* ps_row = p.p_stage + stage_off;
   bf16_t* ds_row = p.ds_stage + stage_off;
-  const uint32_t qk_v = hl * 1024u + 16u * (hb ^ kv_swz(hl));
+  const uint32_t qk_v = key_row(hl) * kTileVPitch + 16u * hb;
   const uint32_t qk_r = kTileVBytes + hl * 128u + 16u * (hb ^ ((hl >> 1) & 7u));
+  const uint32_t tile0 = lds_addr(sm.tile[0]);
 
-  if (nblk > 0) gather_tile<NW>(sm.tile[0], sm.idx[lane & 31], p.kv, wave, lane);
-  if (nblk > 1) gather_tile<NW>(sm.tile[1], sm.idx[kBK + (lane & 31)], p.kv, wave, lane);
+  if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
+  if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
+  uint32_t st_cur = 0, st_next = 2 * kTileBytes;   // ring byte offsets of blocks blk, blk+2
   u32x2 pw[4], dw[4];   // previous block's values, stored right after the next block's barrier
   for (int blk = 0; blk < nblk; ++blk) {
     // issue order per block: [wait][barrier][stores(blk-1)][copies(blk+2)][compute] -> after
@@ -154,9 +158,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         *reinterpret_cast<u32x2*>(ds_row + j + 8 * q4) = dw[q4];
       }
     }
-    if (blk + 2 < nblk)
-      gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
-    const uint32_t tb = lds_addr(sm.tile[blk % kStages]);   // 1 KB aligned: XORs stay in-tile
+    // block blk+2's gather: one copy per kCopyEvery S/dP steps below
+    const bool gather_next = blk + 2 < nblk;
+    TileSrc<NW> next_src;
+    if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+    const uint32_t next_tile = tile0 + st_next;
+    const uint32_t tb = tile0 + st_cur;   // 128-byte aligned: the rope XOR stays in its row
+    st_cur = st_cur == 2 * kTileBytes ? 0 : st_cur + kTileBytes;
+    st_next = st_next == 2 * kTileBytes ? 0 : st_next + kTileBytes;
     uint32_t qv = tb + qk_v, qr = tb + qk_r;
     asm volatile("" : "+v"(qv), "+v"(qr));
     const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     // S^T = K . Q^T and dP^T = V . dO^T share the A operand (V = K[:, :512]).
     f32x16 s = f32x16{}, dp = f32x16{};
     {
-      auto addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
+      auto addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv + 32u * ks) : (qr ^ (32u * (ks - 32)))); };
       u32x4 a[kPre];
 #pragma unroll
       for (int i = 0; i < kPre; ++i) a[i] = lds_load16(addr(i));
@@ -174,6 +183,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(addr(ks + kPre));
         s = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), s);
         if (ks < kDv / 16) dp = mfma32x32x16(as_bf16x8(cur), as_bf16x8(df[ks]), dp);
+        if (ks % kCopyEvery == 0 && gather_next)
+          gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -220,7 +231,9 @@ template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   constexpr int HR = 32 * NW;                                  // head rows copied per block
   constexpr int G = tile_copies_per_wave<NW>() + HR / 16 / NW;
-  __shared__ __attribute__((aligned(16))) DqSmem sm;
+  constexpr int kCopyEvery = kDqk / 16 / tile_copies_per_wave<NW>();   // MFMA steps per tile copy
+  static_assert(HR / 16 / NW == 2, "two dS copies per wave per block");
+  __shared__ __attribute__((aligned(128))) DqSmem sm;
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -235,21 +248,23 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   const int hrows = min(HR, p.n_heads - h0);
   const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + ((int64_t)t * p.n_heads + h0) * p.topk_pad);
   const int64_t ds_stride = (int64_t)p.topk_pad * 2;
-  auto copy_ds = [&](char* dst, int blk) {
+  // copy k (0 <= k < HR/16/NW = 2) of this wave's share of block blk's dS rows
+  auto copy_ds_part = [&](char* dst, int blk, int k) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
     const int w = __builtin_amdgcn_readfirstlane(wave);
+    const int i = w + k * NW;
+    const int h = 16 * i + (lane >> 2);
+    const int q = (lane & 3) ^ ((h >> 2) & 3);
+    const int hs = h < hrows ? h : 0;
+    async_copy16_unordered(ds_base + hs * ds_stride + blk * kBK * 2 + q * 16, base + i * 1024u);
+  };
+  auto copy_ds = [&](char* dst, int blk) {
 #pragma unroll
-    for (int k = 0; k < HR / 16 / NW; ++k) {
-      const int i = w + k * NW;
-      const int h = 16 * i + (lane >> 2);
-      const int q = (lane & 3) ^ ((h >> 2) & 3);
-      const int hs = h < hrows ? h : 0;
-      async_copy16_unordered(ds_base + hs * ds_stride + blk * kBK * 2 + q * 16, base + i * 1024u);
-    }
+    for (int k = 0; k < HR / 16 / NW; ++k) copy_ds_part(dst, blk, k);
   };
 
   // A operand (K^T via ds_read_tr), natural key order: lane feeds key 16a + 8(g/2) + 4h + gi/4,
-  // latent column 32m + 16(g%2) + 4(gi%4).  Byte address: V part kt[a][h] ^ (64*m) (m < 16),
+  // latent column 32m + 16(g%2) + 4(gi%4).  Byte address: V part kt[a][h] + 64*m (m < 16),
   // rope part kr[a][h] ^ (64*(m-16)).
   uint32_t kt[2][2], kr[2][2];
   {
@@ -260,10 +275,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint32_t key = 16 * a + 8 * (g >> 1) + 4 * h + (gi >> 2);
-        kt[a][h] = key * 1024u + 8u * (gi & 1) + 16u * (cl ^ kv_swz(key));
+        kt[a][h] = key_row(key) * kTileVPitch + 32u * (g & 1) + 8u * (gi & 3);
         kr[a][h] = kTileVBytes + key * 128u + 8u * (gi & 1) + 16u * (cl ^ ((key >> 1) & 7u));
       }
   }
+  const uint32_t tile0 = lds_addr(sm.tile[0]);
   // B operand (dS^T): lane (head row wave*32 + hl, keys 16a + 8hb .. +7) = 16-byte chunk 2a + hb
   const int hrow = wave * 32 + hl;
   const uint32_t dsb = hrow * 64u;
@@ -274,22 +290,28 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   for (int m = 0; m < kDqk / 32; ++m) acc[m] = f32x16{};
 
   if (nblk > 0) {
-    gather_tile<NW>(sm.tile[0], sm.idx[lane & 31], p.kv, wave, lane);
+    gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
     copy_ds(sm.ds[0], 0);
   }
   if (nblk > 1) {
-    gather_tile<NW>(sm.tile[1], sm.idx[kBK + (lane & 31)], p.kv, wave, lane);
+    gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
     copy_ds(sm.ds[1], 1);
   }
+  int st = 0;   // ring stage of block blk
   for (int blk = 0; blk < nblk; ++blk) {
     if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
     __syncthreads();
-    if (blk + 2 < nblk) {
-      gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
-      copy_ds(sm.ds[(blk + 2) % kStages], blk + 2);
-    }
-    const uint32_t tb = lds_addr(sm.tile[blk % kStages]);   // 1 KB aligned: XORs stay in-tile
-    const char* dsl = sm.ds[blk % kStages];
+    // block blk+2's copies, spread over the 36 MFMA steps below: tile copy k at step
+    // kCopyEvery*k, the dS copies at steps 1 and 3
+    const bool copy_next = blk + 2 < nblk;
+    const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
+    TileSrc<NW> next_src;
+    if (copy_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+    const uint32_t next_tile = tile0 + st_next * kTileBytes;
+    char* const next_ds = sm.ds[st_next];
+    const uint32_t tb = tile0 + st * kTileBytes;   // 128-byte aligned: the rope XOR stays in its row
+    const char* dsl = sm.ds[st];
+    st = st == 2 ? 0 : st + 1;
     uint32_t k00 = tb + kt[0][0], k01 = tb + kt[0][1], k10 = tb + kt[1][0], k11 = tb + kt[1][1];
     uint32_t r00 = tb + kr[0][0], r01 = tb + kr[0][1], r10 = tb + kr[1][0], r11 = tb + kr[1][1];
     asm volatile("" : "+v"(k00), "+v"(k01), "+v"(k10), "+v"(k11), "+v"(r00), "+v"(r01), "+v"(r10), "+v"(r11));
@@ -299,8 +321,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
       const uint32_t v0 = a ? k10 : k00, v1 = a ? k11 : k01;
       const uint32_t q0 = a ? r10 : r00, q1 = a ? r11 : r01;
       auto ld = [&](int m) {
-        const uint32_t x0 = m < 16 ? (v0 ^ (64u * m)) : (q0 ^ (64u * (m - 16)));
-        const uint32_t x1 = m < 16 ? (v1 ^ (64u * m)) : (q1 ^ (64u * (m - 16)));
+        const uint32_t x0 = m < 16 ? (v0 + 64u * m) : (q0 ^ (64u * (m - 16)));
+        const uint32_t x1 = m < 16 ? (v1 + 64u * m) : (q1 ^ (64u * (m - 16)));
         const u32x2 lo = lds_read_tr16(lds_ptr(x0)), hi = lds_read_tr16(lds_ptr(x1));
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
@@ -312,6 +334,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
         const u32x4 cur = v[m % kPre];
         if (m + kPre < kDqk / 32) v[m % kPre] = ld(m + kPre);
         acc[m] = mfma32x32x16(as_bf16x8(cur), b, acc[m]);
+        const int step = a * (kDqk / 32) + m;
+        if (copy_next) {
+          if (step % kCopyEvery == 0) gather_part<NW>(next_tile, next_src, wave, lane, step / kCopyEvery);
+          if (step == 1 || step == 3) copy_ds_part(next_ds, blk + 2, step >> 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -439,21 +466,22 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   const char* dsb = reinterpret_cast<const char*>(p.ds_stage + (int64_t)t * p.n_heads * p.topk_pad);
   const char* psb = reinterpret_cast<const char*>(p.p_stage + (int64_t)t * p.n_heads * p.topk_pad);
   const int64_t rstride = (int64_t)p.topk_pad * 2;
-  auto stage = [&](int s, int blk) {
-    // head rows past n_heads re-read row 0 (valid memory; their k-steps multiply zeros)
-    const uint32_t b0 = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][0]));
-    const uint32_t b1 = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][1]));
+  // copy c (0..3) of this wave's share of block blk's [dS | P] rows: rows 16*(w + (c/2)*NW) ..,
+  // dS for even c, P for odd c.  Head rows past n_heads re-read row 0 (valid memory; their
+  // k-steps multiply zeros).
+  auto stage_part = [&](int s, int blk, int c) {
+    const uint32_t b = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][c & 1]));
     const int w = __builtin_amdgcn_readfirstlane(wave);
+    const int i = w + (c >> 1) * NW;
+    const int h = 16 * i + (lane >> 2);
+    const int hs = h < p.n_heads ? h : 0;
+    const int chunk = (lane & 3) ^ (2 * ((h >> 1) & 1));   // LDS chunk lane&3 <- global chunk
+    const int64_t off = hs * rstride + blk * kBK * 2 + chunk * 16;
+    async_copy16_unordered(((c & 1) ? psb : dsb) + off, b + i * 1024u);
+  };
+  auto stage = [&](int s, int blk) {
 #pragma unroll
-    for (int k = 0; k < kGHeads / 16 / NW; ++k) {
-      const int i = w + k * NW;
-      const int h = 16 * i + (lane >> 2);
-      const int hs = h < p.n_heads ? h : 0;
-      const int chunk = (lane & 3) ^ (2 * ((h >> 1) & 1));   // LDS chunk lane&3 <- global chunk
-      const int64_t off = hs * rstride + blk * kBK * 2 + chunk * 16;
-      async_copy16_unordered(dsb + off, b0 + i * 1024u);
-      async_copy16_unordered(psb + off, b1 + i * 1024u);
-    }
+    for (int c = 0; c < G; ++c) stage_part(s, blk, c);
   };
   // B operand address of this lane inside a tile: head row 16*ks + tr_h, bytes 2*tr_c .. +8
   const uint32_t b_off = tr_h * 64 + 16 * (((2 * tr_c) >> 4) ^ (2 * ((tr_h >> 1) & 1))) + ((2 * tr_c) & 15);
@@ -472,7 +500,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       else if (blk == 0) wait_vmcnt<G>();
       else wait_vmcnt<G + kGStores>();
       __syncthreads();
-      if (blk + 2 < nblk) stage((blk + 2) % kStages, blk + 2);
+      const bool copy_next = blk + 2 < nblk;   // block blk+2's copies: copy c at k-step c*KS/G
       const char* sd = sm.st[blk % kStages][0] + b_off;
       const char* sp = sm.st[blk % kStages][1] + b_off;
       f32x16 acc[NQ];
@@ -490,6 +518,11 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       for (int ks = 0; ks < KS; ++ks) {
         u32x4 bs_n, bp_n;
         if (ks + 1 < KS) load_b(ks + 1, bs_n, bp_n);   // next k-step's operands under these MFMAs
+        if (copy_next) {
+#pragma unroll
+          for (int c = 0; c < G; ++c)
+            if (c * KS / G == ks) stage_part((blk + 2) % kStages, blk + 2, c);
+        }
         // Q-part products of all tiles first, then the dO-part ones: dependent MFMAs on one
         // accumulator are NQ instructions apart instead of back to back
 #pragma unroll

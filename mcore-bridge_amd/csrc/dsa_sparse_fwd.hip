@@ -12,8 +12,9 @@
 //   * the query's index row is staged once in LDS; selected KV rows are gathered 32 at a time
 //     straight into LDS with global_load_lds (16 B per lane, no VGPR staging, swizzled tile of
 //     dsa_kvtile.h) through a 3-stage ring, so block j+2 streams in while block j is
-//     multiplied.  The copies are issued through inline asm and completed with explicit
-//     s_waitcnt vmcnt(G) + barrier (every wave issues the same G copies per block).
+//     multiplied.  The copies are issued through inline asm, one every few QK MFMAs, and
+//     completed with explicit s_waitcnt vmcnt(G) + barrier (every wave issues the same G copies
+//     per block).
 //   * QK: 36 MFMA 32x32x16 per 32-key block, A operands prefetched 3 MFMAs ahead;
 //     PV: O^T += V^T . P^T, V^T from ds_read_b64_tr_b16 (hardware 16-bit transpose on the LDS
 //     read), P^T is the S^T accumulator converted to bf16 in place (the k order inside each
@@ -58,7 +59,9 @@ struct FwdSmem {
 template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdParams p) {
   constexpr int G = tile_copies_per_wave<NW>();
-  __shared__ __attribute__((aligned(16))) FwdSmem sm;
+  constexpr int kCopyEvery = kDqk / 16 / G;   // QK MFMAs per gather copy (36 MFMAs per block)
+  static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the QK MFMAs");
+  __shared__ __attribute__((aligned(128))) FwdSmem sm;
 
   // work item = (query t, key split); n_split > 1 only for decode, where a few queries must
   // still fill the chip: split s covers index slots [s*split_keys, (s+1)*split_keys) and writes
@@ -110,41 +113,46 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   f32x16 o[kDv / 32];
   float m_ref = -INFINITY, m_seen = -INFINITY, l_run = 0.f;
 
-  // QK operand addresses: lane reads row hl, chunk 2*ks + hb (see tile_off): V part at
-  // qk_v ^ (32*ks) for ks < 32, rope part at qk_r ^ (32*(ks-32)).
-  const uint32_t qk_v = hl * 1024u + 16u * (hb ^ kv_swz(hl));
+  // QK operand addresses: lane reads key hl, chunk 2*ks + hb (see tile_off): V part at
+  // qk_v + 32*ks for ks < 32, rope part at qk_r ^ (32*(ks-32)).
+  const uint32_t qk_v = key_row(hl) * kTileVPitch + 16u * hb;
   const uint32_t qk_r = kTileVBytes + hl * 128u + 16u * (hb ^ ((hl >> 1) & 7u));
   // PV operand addresses (ds_read_tr): lane feeds key 16a + 8h + 4(g/2) + gi/4 (the S^T C-layout
-  // key order) and dv 32m + 16(g%2) + 4(gi%4): byte pv[a][h] ^ (64*m).
+  // key order) and dv 32m + 16(g%2) + 4(gi%4): byte pv[a][h] + 64*m.
   uint32_t pv[2][2];
   {
     const int g = lane >> 4, gi = lane & 15;
-    const uint32_t cl = 2 * (g & 1) + ((gi & 3) >> 1);
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint32_t key = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
-        pv[a][h] = key * 1024u + 8u * (gi & 1) + 16u * (cl ^ kv_swz(key));
+        pv[a][h] = key_row(key) * kTileVPitch + 32u * (g & 1) + 8u * (gi & 3);
       }
   }
+  const uint32_t tile0 = lds_addr(sm.tile[0]);
 
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int m = 0; m < kDv / 32; ++m) o[m] = f32x16{};
     l_run = 0.f;
-    if (nblk > 0) gather_tile<NW>(sm.tile[0], sm.idx[lane & 31], p.kv, wave, lane);
-    if (nblk > 1) gather_tile<NW>(sm.tile[1], sm.idx[kBK + (lane & 31)], p.kv, wave, lane);
+    if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
+    if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
 
+    uint32_t st_cur = 0, st_next = 2 * kTileBytes;   // ring byte offsets of blocks blk, blk+2
     for (int blk = 0; blk < nblk; ++blk) {
       if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
       __syncthreads();
-      if (blk + 2 < nblk)
-        gather_tile<NW>(sm.tile[(blk + 2) % kStages], sm.idx[(blk + 2) * kBK + (lane & 31)], p.kv, wave, lane);
-      const char* buf = sm.tile[blk % kStages];
-      // per-block absolute operand addresses (tile bases are 1 KB aligned and every XOR below
-      // only touches the low 10 bits); opaque so they are not hoisted into loop-invariant VGPRs
-      const uint32_t tb = lds_addr(buf);
+      // block blk+2's gather is issued one copy per kCopyEvery QK MFMAs below
+      const bool gather_next = blk + 2 < nblk;
+      TileSrc<NW> next_src;
+      if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+      const uint32_t next_tile = tile0 + st_next;
+      // per-block absolute operand addresses (tiles are 128-byte aligned: the rope XOR below
+      // only touches bits 4..6); opaque so they are not hoisted into loop-invariant VGPRs
+      const uint32_t tb = tile0 + st_cur;
+      st_cur = st_cur == 2 * kTileBytes ? 0 : st_cur + kTileBytes;
+      st_next = st_next == 2 * kTileBytes ? 0 : st_next + kTileBytes;
       uint32_t qv = tb + qk_v, qr = tb + qk_r;
       uint32_t pv00 = tb + pv[0][0], pv01 = tb + pv[0][1], pv10 = tb + pv[1][0], pv11 = tb + pv[1][1];
       asm volatile("" : "+v"(qv), "+v"(qr), "+v"(pv00), "+v"(pv01), "+v"(pv10), "+v"(pv11));
@@ -153,7 +161,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       // ---- S^T[32 keys x 32 heads] = K . Q^T  (A operands prefetched)
       f32x16 s;
       {
-        auto qk_addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv ^ (32u * ks)) : (qr ^ (32u * (ks - 32)))); };
+        auto qk_addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv + 32u * ks) : (qr ^ (32u * (ks - 32)))); };
         u32x4 a[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; ++i) a[i] = lds_load16(qk_addr(i));
@@ -163,14 +171,15 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
           const u32x4 cur = a[ks % kPre];
           if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
           sa = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sa);
+          if (ks % kCopyEvery == 0 && gather_next)
+            gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
           __builtin_amdgcn_sched_barrier(0);
         }
         s = sa;
       }
 
-      // ---- softmax numerator; key of s[i] = (i/4)*8 + 4*hb + i%4
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] *= p.scale_log2;
+      // ---- softmax numerator in the exp2 domain, p = 2^(scale_log2 * s - m) (scale > 0);
+      // key of s[i] = (i/4)*8 + 4*hb + i%4
       if (vmask != 0xffffffffu) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -181,7 +190,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       float bmax = s[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) bmax = fmaxf(bmax, s[i]);
-      bmax = xor32_max(bmax);
+      bmax = xor32_max(bmax) * p.scale_log2;
       m_seen = fmaxf(m_seen, bmax);
       if (m_ref == -INFINITY) m_ref = bmax;          // O and l are still zero for this head
       const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
@@ -191,8 +200,10 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       for (int a = 0; a < 2; ++a) {
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          const float p0 = fast_exp2(fminf(s[a * 8 + e] - m_use, kHeadroom));
-          const float p1 = fast_exp2(fminf(s[a * 8 + e + 1] - m_use, kHeadroom));
+          // no clamp: an exponent above kHeadroom means m_seen > m_ref + kHeadroom, and the
+          // whole row is then recomputed against its true maximum (inf/NaN here is discarded)
+          const float p0 = fast_exp2(__builtin_fmaf(s[a * 8 + e], p.scale_log2, -m_use));
+          const float p1 = fast_exp2(__builtin_fmaf(s[a * 8 + e + 1], p.scale_log2, -m_use));
           rs += p0 + p1;
           pb[a][e >> 1] = pack_bf16x2(p0, p1);
         }
@@ -207,15 +218,15 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
         u32x4 v[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; ++i) {
-          const u32x2 lo = lds_read_tr16(lds_ptr(r0 ^ (64u * i))), hi = lds_read_tr16(lds_ptr(r1 ^ (64u * i)));
+          const u32x2 lo = lds_read_tr16(lds_ptr(r0 + 64u * i)), hi = lds_read_tr16(lds_ptr(r1 + 64u * i));
           v[i] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
 #pragma unroll
         for (int m = 0; m < kDv / 32; ++m) {
           const u32x4 cur = v[m % kPre];
           if (m + kPre < kDv / 32) {
-            const u32x2 lo = lds_read_tr16(lds_ptr(r0 ^ (64u * (m + kPre))));
-            const u32x2 hi = lds_read_tr16(lds_ptr(r1 ^ (64u * (m + kPre))));
+            const u32x2 lo = lds_read_tr16(lds_ptr(r0 + 64u * (m + kPre)));
+            const u32x2 hi = lds_read_tr16(lds_ptr(r1 + 64u * (m + kPre)));
             v[m % kPre] = u32x4{lo[0], lo[1], hi[0], hi[1]};
           }
           o[m] = mfma32x32x16(as_bf16x8(cur), b, o[m]);
