@@ -33,8 +33,8 @@ struct SparseBwdParams {
   bf16_t* dq;           // [total_q, n_heads, 576]
   float* dkv;           // [n_kv, 576] fp32 (fully written, no accumulation into old contents)
   // workspace (carved by the C-ABI from one caller buffer)
-  bf16_t* p_stage;      // [total_q, n_heads, topk_pad]  P
-  bf16_t* ds_stage;     // [total_q, n_heads, topk_pad]  scale * dS
+  bf16_t* p_stage;      // [total_q, topk_pad/32, n_heads, 32]  P (one contiguous tile per key block)
+  bf16_t* ds_stage;     // [total_q, topk_pad/32, n_heads, 32]  scale * dS
   bf16_t* g_stage;      // [total_q * topk + 1, 576] per-pair dKV partial rows, key-major order
   int64_t g_sink_row;   // last row of g_stage: write target of pairs that select nothing
   int64_t* pair_pos;    // [total_q, topk] row of G for each pair (-1 = not selected)

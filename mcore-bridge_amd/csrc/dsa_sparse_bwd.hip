@@ -130,9 +130,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
                                        p.causal, t);
 
-  // staged rows: element (t, head, j) at ((t * H + head) * topk_pad + j); lane writes keys
+  // staged tiles: element (t, head, slot 32*b + k) at ((t * NB + b) * H + head) * 32 + k
+  // (NB = topk_pad / 32): each block's [H heads x 32 keys] tile is contiguous; lane writes keys
   // 8*q4 + 4*hb .. +3 of each block
-  const int64_t stage_off = ((int64_t)t * p.n_heads + hsafe) * p.topk_pad + hb * 4;
+  const int64_t stage_off = ((int64_t)t * (p.topk_pad / kBK) * p.n_heads + hsafe) * kBK + hb * 4;
+  const int64_t stage_blk = (int64_t)p.n_heads * kBK;   // elements per staged block tile
   bf16_t* ps_row = p.p_stage + stage_off;
   bf16_t* ds_row = p.ds_stage + stage_off;
   const uint32_t qk_v = key_row(hl) * kTileVPitch + 16u * hb;
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     else wait_vmcnt<G + S>();
     __syncthreads();
     if (blk > 0 && head_ok) {  // wave_stores => at least one lane active => the wave issues S stores
-      const int j = (blk - 1) * kBK;
+      const int64_t j = (blk - 1) * stage_blk;
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         *reinterpret_cast<u32x2*>(ps_row + j + 8 * q4) = pw[q4];
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     }
   }
   if (nblk > 0 && head_ok) {
-    const int j = (nblk - 1) * kBK;
+    const int64_t j = (nblk - 1) * stage_blk;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       *reinterpret_cast<u32x2*>(ps_row + j + 8 * q4) = pw[q4];
@@ -246,8 +248,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   // dS rows of this workgroup's heads; rows past n_heads re-read row 0 (never stored).  16-byte
   // chunk q of head row h lands at position q ^ ((h >> 2) & 3): bank-conflict-free column reads.
   const int hrows = min(HR, p.n_heads - h0);
-  const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + ((int64_t)t * p.n_heads + h0) * p.topk_pad);
-  const int64_t ds_stride = (int64_t)p.topk_pad * 2;
+  // staged dS tile of block b: [H heads][32 keys] contiguous at ((t * NB + b) * H) * 32
+  const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + ((int64_t)t * (p.topk_pad / kBK) * p.n_heads + h0) * kBK);
+  const int64_t ds_blk = (int64_t)p.n_heads * kBK * 2;   // bytes per staged block tile
   // copy k (0 <= k < HR/16/NW = 2) of this wave's share of block blk's dS rows
   auto copy_ds_part = [&](char* dst, int blk, int k) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
     const int h = 16 * i + (lane >> 2);
     const int q = (lane & 3) ^ ((h >> 2) & 3);
     const int hs = h < hrows ? h : 0;
-    async_copy16_unordered(ds_base + hs * ds_stride + blk * kBK * 2 + q * 16, base + i * 1024u);
+    async_copy16_unordered(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
   };
   auto copy_ds = [&](char* dst, int blk) {
 #pragma unroll
@@ -359,10 +362,12 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
 // ------------------------------------------------------------------------------------------
 // B3: per-pair dKV partial rows G = (scale*dS)^T Q + P^T dO, contracted over all heads.
 // Wave w owns output row tiles (32 latent dims each): Q part {4w..4w+3} (+16+w for w < 2),
-// dO part {4w..4w+3}.  Each block's G tile [32 keys x 576] goes through LDS so that every row
-// is written to its key-major position with contiguous 16-byte lane stores (a wave store
-// covers ~1 KB of one or two rows; written straight from the MFMA layout, every store
-// instruction would touch 32 rows 16 bytes each).
+// dO part {4w..4w+3}.  Each block's G tile [32 keys x 576] goes through LDS (double buffered)
+// so that every row is written to its key-major position with contiguous 16-byte lane stores:
+// wave w stores the latent part of rows 8w..8w+7 (one 1 KB row per instruction) and the rope
+// part of the same rows (one instruction), 9 stores per wave, issued between the next block's
+// MFMAs.  Written straight from the MFMA layout, every store instruction would touch 32 rows
+// 16 bytes each.
 // ------------------------------------------------------------------------------------------
 constexpr int kGHeads = 128;                        // B3 handles up to 128 heads (n_heads % 16 == 0)
 constexpr int kGKs = kGHeads / 16;                  // head k-steps
@@ -370,16 +375,16 @@ constexpr int kStageTile = kGHeads * 64;            // one staged [128 heads][32
 constexpr int kRowPitch = kDqk * 2 + 16;            // bytes per staged head row of Q / dO
 constexpr int kSetupRows = 32;                      // head rows staged per setup round
 constexpr int kGRowBytes = kDqk * 2;                // one bf16 G row
-constexpr int kGChunks = kGRowBytes / 16;           // 72 16-byte chunks per row
-constexpr int kGStores = kBK * kGChunks / 256;      // 9 row-chunk stores per thread per block
+constexpr int kGTilePitch = kGRowBytes + 16;        // LDS pitch of a G tile row (bank spread)
+constexpr int kGStores = 9;                         // stores per wave per block: 8 rows + rope
 
 struct GSmem {
   union {
     char rows[kSetupRows * kRowPitch];              // setup: Q / dO rows for the transposed load
     char st[kStages][2][kStageTile];                // loop: [dS | P] tiles; 16-byte chunk c of head
   };                                                //   row h at chunk c ^ (2 * ((h >> 1) & 1))
-  char gtile[kBK * kGRowBytes];                     // block's G rows; chunk c of row r at c ^ (r & 7)
-  int64_t pos[kMaxTopkBwd];                         // G row of every index slot (sink if unselected)
+  char gtile[2][kBK * kGTilePitch];                 // G tiles of blocks blk (being written), blk-1
+  int32_t pos[kMaxTopkBwd];                         // G row of every index slot (sink if unselected)
   int32_t idx[kMaxTopkBwd];
   int red[4];
 };
@@ -403,7 +408,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     const int64_t* pos_row = p.pair_pos + (int64_t)t * p.topk;
     for (int j = threadIdx.x; j < nblk * kBK; j += NW * 64) {
       const int64_t v = j < p.topk ? pos_row[j] : -1;
-      sm.pos[j] = v < 0 ? p.g_sink_row : v;
+      sm.pos[j] = (int32_t)(v < 0 ? p.g_sink_row : v);   // < 2^31: checked by the launcher
     }
   }
   const int nks = p.n_heads / 16;
@@ -463,9 +468,10 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   __syncthreads();  // setup rows dead: the union now holds the [dS | P] ring
 
   // ---- key blocks: [dS | P] tiles (rows = heads, 32 keys each) through a 3-stage copy ring
+  // staged tiles of block b: [H heads][32 keys] bf16, contiguous (see B1)
   const char* dsb = reinterpret_cast<const char*>(p.ds_stage + (int64_t)t * p.n_heads * p.topk_pad);
   const char* psb = reinterpret_cast<const char*>(p.p_stage + (int64_t)t * p.n_heads * p.topk_pad);
-  const int64_t rstride = (int64_t)p.topk_pad * 2;
+  const int64_t st_blk = (int64_t)p.n_heads * kBK * 2;   // bytes per staged block tile
   // copy c (0..3) of this wave's share of block blk's [dS | P] rows: rows 16*(w + (c/2)*NW) ..,
   // dS for even c, P for odd c.  Head rows past n_heads re-read row 0 (valid memory; their
   // k-steps multiply zeros).
@@ -476,7 +482,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     const int h = 16 * i + (lane >> 2);
     const int hs = h < p.n_heads ? h : 0;
     const int chunk = (lane & 3) ^ (2 * ((h >> 1) & 1));   // LDS chunk lane&3 <- global chunk
-    const int64_t off = hs * rstride + blk * kBK * 2 + chunk * 16;
+    const int64_t off = blk * st_blk + hs * (kBK * 2) + chunk * 16;
     async_copy16_unordered(((c & 1) ? psb : dsb) + off, b + i * 1024u);
   };
   auto stage = [&](int s, int blk) {
@@ -485,22 +491,63 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   };
   // B operand address of this lane inside a tile: head row 16*ks + tr_h, bytes 2*tr_c .. +8
   const uint32_t b_off = tr_h * 64 + 16 * (((2 * tr_c) >> 4) ^ (2 * ((tr_h >> 1) & 1))) + ((2 * tr_c) & 15);
-  // G tile LDS slots of this lane: key row lane % 32, chunk 4*qtile(i) + q4, half hb
-  const int gkey = lane & 31;
+  // G tile write slot of this lane: key row lane % 32 (bytes 8*hb of each 16-byte chunk)
+  const uint32_t gt_w = (lane & 31) * kGTilePitch + 8 * hb;
+  const uint32_t gtile0 = lds_addr(sm.gtile[0]);
+  // stores of a finished G tile by this wave: latent chunks lane of rows 8w + i (i < 8), then
+  // the rope chunk lane % 8 of row 8w + lane / 8
+  const int rope_row = 8 * wave + (lane >> 3);
+  // store i of a finished tile: its 16 data bytes are read from LDS one k-step ahead
+  // (store_load), the global store is issued later (store_issue) -- no exposed LDS latency.
+  auto store_load = [&](uint32_t gt, int i) {
+    return i < 8 ? lds_load16(lds_ptr(gt + (8 * wave + i) * kGTilePitch + 16 * lane))
+                 : lds_load16(lds_ptr(gt + rope_row * kGTilePitch + 16 * (64 + (lane & 7))));
+  };
+  auto store_issue = [&](const int32_t (&rpos)[8], int32_t rope_pos, int i, const u32x4& v) {
+    if (i < 8)
+      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rpos[i] * kDqk + 8 * lane) = v;
+    else
+      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))) = v;
+  };
+  // k-step of copy c (c < G) and of store i (i < kGStores); stores follow copies in a step
+  constexpr auto copy_ks = [](int c) { return c * KS / G; };
+  constexpr auto store_ks = [](int i) { return i * KS / kGStores; };
+  constexpr int kStoresAfterLastCopy = [] {
+    int n = 0;
+    for (int i = 0; i < kGStores; ++i) n += (i * KS / kGStores) >= ((G - 1) * KS / G);
+    return n;
+  }();
 
   auto block_loop = [&](auto nq_c) {
     constexpr int NQ = decltype(nq_c)::value;
     stage(0, 0);
     if (nblk > 1) stage(1, 1);
     for (int blk = 0; blk < nblk; ++blk) {
-      // issue order per block: [wait][barrier][copies(blk+2)][compute][G -> LDS][barrier]
-      // [stores(blk)]: block blk waits for copies(blk) with copies(blk+1) and stores(blk-1)
-      // still allowed in flight.
+      // issue order of block blk: [wait][barrier] then, between its MFMAs, copies(blk+2) and
+      // stores(blk-1) (stores after copies within a k-step), then [G(blk) -> LDS].  Block blk
+      // needs copies(blk) done; issued after them: block 0 nothing of its own, block 1 the
+      // copies(3) + stores(0), block b >= 3 the trailing stores(b-3) of block b-2 plus block
+      // b-1's copies(b+1) + stores(b-2).
       if (blk + 1 >= nblk) wait_vmcnt<0>();
-      else if (blk == 0) wait_vmcnt<G>();
-      else wait_vmcnt<G + kGStores>();
+      else if (blk <= 1) wait_vmcnt<G>();
+      else if (blk == 2) wait_vmcnt<G + kGStores>();
+      else wait_vmcnt<G + kGStores + kStoresAfterLastCopy>();
       __syncthreads();
-      const bool copy_next = blk + 2 < nblk;   // block blk+2's copies: copy c at k-step c*KS/G
+      const bool copy_next = blk + 2 < nblk;
+      const bool store_prev = blk > 0;
+      const uint32_t gt_prev = gtile0 + ((blk - 1) & 1) * (kBK * kGTilePitch);
+      // G rows of the previous block's tile: this wave's 8 latent rows (wave-uniform) and the
+      // rope row of this lane
+      int32_t rpos[8], rope_pos = 0;
+      u32x4 sv[kGStores];
+      if (store_prev) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(blk - 1) * kBK + 8 * wave + i]);
+        rope_pos = sm.pos[(blk - 1) * kBK + rope_row];
+#pragma unroll
+        for (int i = 0; i < kGStores; ++i)
+          if (store_ks(i) == 0) sv[i] = store_load(gt_prev, i);
+      }
       const char* sd = sm.st[blk % kStages][0] + b_off;
       const char* sp = sm.st[blk % kStages][1] + b_off;
       f32x16 acc[NQ];
@@ -521,7 +568,14 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         if (copy_next) {
 #pragma unroll
           for (int c = 0; c < G; ++c)
-            if (c * KS / G == ks) stage_part((blk + 2) % kStages, blk + 2, c);
+            if (copy_ks(c) == ks) stage_part((blk + 2) % kStages, blk + 2, c);
+        }
+        if (store_prev) {
+#pragma unroll
+          for (int i = 0; i < kGStores; ++i) {
+            if (store_ks(i) == ks + 1) sv[i] = store_load(gt_prev, i);   // next step's data
+            if (store_ks(i) == ks) store_issue(rpos, rope_pos, i, sv[i]);
+          }
         }
         // Q-part products of all tiles first, then the dO-part ones: dependent MFMAs on one
         // accumulator are NQ instructions apart instead of back to back
@@ -531,25 +585,28 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         for (int i = 0; i < 4; ++i) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), as_bf16x8(bp), acc[i]);
         if (ks + 1 < KS) { bs = bs_n; bp = bp_n; }
       }
-      // G tile -> LDS (bf16): lane holds key gkey, dims 32*qtile(i) + 8*q4 + 4*hb .. +3
+      // G tile -> LDS (bf16): lane holds key lane % 32, dims 32*qtile(i) + 8*q4 + 4*hb .. +3
+      const uint32_t gt_cur = gtile0 + (blk & 1) * (kBK * kGTilePitch) + gt_w;
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const int c = 4 * qtile(i) + q4;
-          *reinterpret_cast<u32x2*>(sm.gtile + gkey * kGRowBytes + 16 * (c ^ (gkey & 7)) + 8 * hb) =
+          *reinterpret_cast<u32x2*>(const_cast<char*>(lds_ptr(gt_cur + 16 * c))) =
               u32x2{pack_bf16x2(acc[i][4 * q4], acc[i][4 * q4 + 1]), pack_bf16x2(acc[i][4 * q4 + 2], acc[i][4 * q4 + 3])};
         }
       }
-      __syncthreads();
-      // rows -> their key-major G positions, 16 contiguous bytes per lane
+    }
+    // the last block's G tile
+    __syncthreads();
+    {
+      const uint32_t gt = gtile0 + ((nblk - 1) & 1) * (kBK * kGTilePitch);
+      int32_t rpos[8];
 #pragma unroll
-      for (int i = 0; i < kGStores; ++i) {
-        const int cidx = threadIdx.x + 256 * i;
-        const int r = cidx / kGChunks, c = cidx - r * kGChunks;
-        const u32x4 v = lds_load16(sm.gtile + r * kGRowBytes + 16 * (c ^ (r & 7)));
-        *reinterpret_cast<u32x4*>(p.g_stage + sm.pos[blk * kBK + r] * kDqk + c * 8) = v;
-      }
+      for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(nblk - 1) * kBK + 8 * wave + i]);
+      const int32_t rope_pos = sm.pos[(nblk - 1) * kBK + rope_row];
+#pragma unroll
+      for (int i = 0; i < kGStores; ++i) store_issue(rpos, rope_pos, i, store_load(gt, i));
     }
   };
   if (nq == 5) block_loop(std::integral_constant<int, 5>{});
@@ -651,6 +708,7 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
 
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
   if (p.topk > kMaxTopkBwd) return -2;
+  if (p.g_sink_row >= INT32_MAX) return -2;   // B3 keeps G row numbers in 32 bits
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
