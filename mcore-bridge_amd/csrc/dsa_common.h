@@ -37,6 +37,25 @@ DSA_DEV f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// C += A * B with B and C in AccVGPRs.  gfx950 MFMAs read any operand from AccVGPRs, but the
+// compiler only ever feeds A/B from VGPRs (spilled fragments then cost 4 v_accvgpr_read per
+// MFMA); these forms let a kernel keep a loop-invariant B operand set in AccVGPRs.  Hazards the
+// compiler cannot see inside the asm are covered here and by the caller:
+//   - s_nop 1 before the MFMA: 2 wait states after a VALU write of A or an AccVGPR write of B/C;
+//   - the caller issues mfma_acc_drain() before any VALU reads C (8-pass XDL result: 11 wait
+//     states needed, 16 given).
+DSA_DEV void mfma32x32x16_acc_first(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=a"(c) : "v"(a), "a"(b));
+}
+DSA_DEV void mfma32x32x16_acc(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "a"(b));
+}
+DSA_DEV void mfma_acc_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 15");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 DSA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // 16-byte LDS / global access helpers.

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
       delta += bf16_lo(v[e]) * bf16_lo(o[e]) + bf16_hi(v[e]) * bf16_hi(o[e]);
   }
   delta = xor32_sum(delta);
+  const float delta_s = delta * p.scale;
   const float lse = head_ok ? p.lse[(int64_t)t * p.lse_stride_t + head] : -INFINITY;
   const float lse2 = lse * kLog2e;
   const bool row_live = lse != -INFINITY;
@@ -172,8 +173,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     asm volatile("" : "+v"(qv), "+v"(qr));
     const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
-    // S^T = K . Q^T and dP^T = V . dO^T share the A operand (V = K[:, :512]).
-    f32x16 s = f32x16{}, dp = f32x16{};
+    // S^T = K . Q^T and dP^T = V . dO^T share the A operand (V = K[:, :512]); the dO^T
+    // fragments and the dP accumulator stay in AccVGPRs (Q + dO = 272 registers per lane).
+    f32x16 s = f32x16{}, dp;
     {
       auto addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv + 32u * ks) : (qr ^ (32u * (ks - 32)))); };
       u32x4 a[kPre];
@@ -184,26 +186,34 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         const u32x4 cur = a[ks % kPre];
         if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(addr(ks + kPre));
         s = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), s);
-        if (ks < kDv / 16) dp = mfma32x32x16(as_bf16x8(cur), as_bf16x8(df[ks]), dp);
+        if (ks == 0) mfma32x32x16_acc_first(dp, cur, df[0]);
+        else if (ks < kDv / 16) mfma32x32x16_acc(dp, cur, df[ks]);
         if (ks % kCopyEvery == 0 && gather_next)
           gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // P and scale * dS; key of element i = (i/4)*8 + 4*hb + i%4
+    mfma_acc_drain();
+    // P = 2^(scale_log2 * s - lse2) and scale * dS = P * (scale * dP - scale * Delta); key of
+    // element i = (i/4)*8 + 4*hb + i%4.  Partial blocks / dead heads take the masked path.
+    float pv[16];
+    if (vmask == 0xffffffffu && __all(row_live)) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pv[i] = fast_exp2(__builtin_fmaf(s[i], p.scale_log2, -lse2));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = (i >> 2) * 8 + hb * 4 + (i & 3);
+        const bool ok = row_live && ((vmask >> key) & 1u);
+        pv[i] = ok ? fast_exp2(__builtin_fmaf(s[i], p.scale_log2, -lse2)) : 0.f;
+      }
+    }
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      float pv[4], dv[4];
+      float dv[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * q4 + e;
-        const int key = q4 * 8 + hb * 4 + e;
-        const bool ok = row_live && ((vmask >> key) & 1u);
-        const float pp = ok ? fast_exp2(s[i] * p.scale_log2 - lse2) : 0.f;
-        pv[e] = pp;
-        dv[e] = p.scale * pp * (dp[i] - delta);
-      }
-      pw[q4] = u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+      for (int e = 0; e < 4; ++e) dv[e] = pv[4 * q4 + e] * __builtin_fmaf(dp[4 * q4 + e], p.scale, -delta_s);
+      pw[q4] = u32x2{pack_bf16x2(pv[4 * q4], pv[4 * q4 + 1]), pack_bf16x2(pv[4 * q4 + 2], pv[4 * q4 + 3])};
       dw[q4] = u32x2{pack_bf16x2(dv[0], dv[1]), pack_bf16x2(dv[2], dv[3])};
     }
   }
