@@ -50,6 +50,18 @@ DSA_DEV void mfma32x32x16_acc_first(f32x16& c, const u32x4& a, const u32x4& b) {
 DSA_DEV void mfma32x32x16_acc(f32x16& c, const u32x4& a, const u32x4& b) {
   asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "a"(b));
 }
+// C += A * B with C pinned in AccVGPRs ("a") or VGPRs ("v") and A, B in VGPRs -- for kernels
+// whose accumulators exceed 256 registers, where the compiler would shuttle tiles between the
+// two files around every MFMA.  Same hazard contract as above.
+DSA_DEV void mfma32x32x16_cA(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+DSA_DEV void mfma32x32x16_cV(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+DSA_DEV void mfma32x32x16_cV_first(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(c) : "v"(a), "v"(b));
+}
 DSA_DEV void mfma_acc_drain() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_nop 15");

@@ -298,9 +298,12 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   const uint32_t dsb = hrow * 64u;
   const uint32_t dsq = (uint32_t)((hrow >> 2) & 3);
 
+  // dQ^T accumulators: 18 tiles = 288 registers per lane, more than either register file --
+  // tiles 0..15 are pinned in AccVGPRs and 16, 17 in VGPRs (AGPR/VGPR-constrained MFMAs)
   f32x16 acc[kDqk / 32];
 #pragma unroll
   for (int m = 0; m < kDqk / 32; ++m) acc[m] = f32x16{};
+  mfma_acc_drain();   // zero writes of the accumulators before their first MFMA read
 
   if (nblk > 0) {
     gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
@@ -346,7 +349,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
       for (int m = 0; m < kDqk / 32; ++m) {
         const u32x4 cur = v[m % kPre];
         if (m + kPre < kDqk / 32) v[m % kPre] = ld(m + kPre);
-        acc[m] = mfma32x32x16(as_bf16x8(cur), b, acc[m]);
+        if (m < 16) mfma32x32x16_cA(acc[m], cur, as_u32x4(b));
+        else mfma32x32x16_cV(acc[m], cur, as_u32x4(b));
         const int step = a * (kDqk / 32) + m;
         if (copy_next) {
           if (step % kCopyEvery == 0) gather_part<NW>(next_tile, next_src, wave, lane, step / kCopyEvery);
@@ -356,6 +360,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
       }
     }
   }
+  mfma_acc_drain();
   if (!head_ok) return;
   bf16_t* dqrow = p.dq + (int64_t)t * p.dq_stride_t + (int64_t)head * kDqk;
 #pragma unroll

@@ -132,9 +132,13 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   }
   const uint32_t tile0 = lds_addr(sm.tile[0]);
 
+  // Register files: O^T (256) is pinned in AccVGPRs and S^T in VGPRs through constrained MFMAs
+  // (left to itself the allocator parks S^T in AccVGPRs and moves an O tile out and back
+  // every block).
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int m = 0; m < kDv / 32; ++m) o[m] = f32x16{};
+    mfma_acc_drain();
     l_run = 0.f;
     if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
     if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
@@ -165,18 +169,20 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
         u32x4 a[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; ++i) a[i] = lds_load16(qk_addr(i));
-        f32x16 sa = f32x16{};
+        f32x16 sa;
 #pragma unroll
         for (int ks = 0; ks < kDqk / 16; ++ks) {
           const u32x4 cur = a[ks % kPre];
           if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
-          sa = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), sa);
+          if (ks == 0) mfma32x32x16_cV_first(sa, cur, qf[0]);
+          else mfma32x32x16_cV(sa, cur, qf[ks]);
           if (ks % kCopyEvery == 0 && gather_next)
             gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
           __builtin_amdgcn_sched_barrier(0);
         }
         s = sa;
       }
+      mfma_acc_drain();
 
       // ---- softmax numerator in the exp2 domain, p = 2^(scale_log2 * s - m) (scale > 0);
       // key of s[i] = (i/4)*8 + 4*hb + i%4
@@ -229,7 +235,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
             const u32x2 hi = lds_read_tr16(lds_ptr(r1 + 64u * (m + kPre)));
             v[m % kPre] = u32x4{lo[0], lo[1], hi[0], hi[1]};
           }
-          o[m] = mfma32x32x16(as_bf16x8(cur), b, o[m]);
+          mfma32x32x16_cA(o[m], cur, as_u32x4(b));
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -245,6 +251,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   }
 
   // ---- epilogue: normalise, store O (bf16) and LSE (natural log)
+  mfma_acc_drain();
   if (!head_ok) return;
   const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
   bf16_t* optr = p.out + orow * p.out_stride_t + (int64_t)head * kDv;
