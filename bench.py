@@ -15,6 +15,7 @@ bytes of the selected cache rows / decode attention time.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -43,6 +44,22 @@ def _cpu_model() -> str:
     except Exception:
         pass
     return platform.processor() or "unknown"
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "dsa_cfg3_hbm_traffic.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE, calibrated on a copy of known size; see that file), or None if absent."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 5 and cells[0] == kernel:
+                return int(cells[4].replace(",", ""))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(torch):
@@ -156,7 +173,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the cfg5 decode leg")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="only copy a 1 GiB tensor (known HBM bytes) to calibrate FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    if args.pmc_calibration:
+        import torch
+        x = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)              # 1 GiB read + 1 GiB written per copy
+        torch.cuda.synchronize()
+        print("pmc calibration copies done", flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build runs the DSA path on a single MI355X); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -179,24 +207,38 @@ def main():
     del x
     scale = W.SM_SCALE
 
-    ev = {k: [] for k in ("indexer_topk", "sparse_fwd", "sparse_bwd")}
+    # backward through the C ABI with preallocated outputs/workspace and per-stage events
+    from mcore_bridge_amd import _lib
+    lib = _lib.load()
+    N = kv.shape[0]
+    dq = torch.empty_like(q)
+    dkv = torch.empty(N, 576, dtype=torch.float32, device=dev)
+    ws_bytes = ops.bwd_workspace_bytes(T, N, H, K)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    STAGES = ("bwd_pairs", "bwd_sp", "bwd_dq", "bwd_g", "bwd_dkv_reduce")
+    ev = {k: [] for k in ("indexer_topk", "sparse_fwd") + STAGES}
+
+    def new_event():
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()          # materialise the handle; re-recorded by the library
+        return e
 
     def step(record: bool):
-        def mark():
-            e = torch.cuda.Event(enable_timing=True)
-            e.record()
-            return e
-        e0 = mark() if record else None
+        e0 = new_event() if record else None
         idx = ops.indexer_topk(qi, ki, w, K, cu_t, True, max_seqlen)
-        e1 = mark() if record else None
+        e1 = new_event() if record else None
         out, lse = ops.sparse_mla_fwd(q, kv, idx, scale, True)
-        e2 = mark() if record else None
-        dq, dkv = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, scale, True)
-        e3 = mark() if record else None
+        se = [new_event() for _ in range(6)] if record else None
+        arr = (ctypes.c_void_p * 6)(*[e.cuda_event for e in se]) if record else None
+        _lib.check("dsa_sparse_mla_bwd_timed", lib.dsa_sparse_mla_bwd_timed(
+            q.data_ptr(), kv.data_ptr(), idx.data_ptr(), out.data_ptr(), dout.data_ptr(), lse.data_ptr(), T, N, H,
+            576, 512, K, scale, 1, dq.data_ptr(), dkv.data_ptr(), ws.data_ptr(), ws_bytes, arr, stream))
         if record:
             ev["indexer_topk"].append((e0, e1))
-            ev["sparse_fwd"].append((e1, e2))
-            ev["sparse_bwd"].append((e2, e3))
+            ev["sparse_fwd"].append((e1, se[0]))
+            for i, name in enumerate(STAGES):
+                ev[name].append((se[i], se[i + 1]))
         return dq, dkv
 
     for i in range(args.warmup):
@@ -221,9 +263,27 @@ def main():
     fl_idx = 2 * cfg.Di * cfg.Hi * npairs
     total = fl_fwd + fl_bwd + fl_idx
     value = total / (ms_step * 1e-3) / 1e12
-    t_fwd, t_bwd, t_idx = avg_ms("sparse_fwd"), avg_ms("sparse_bwd"), avg_ms("indexer_topk")
-    # dominant single kernel measured live: the sparse MLA forward (one launch per step)
-    achieved = fl_fwd / (t_fwd * 1e-3) / 1e12
+    t = {k: avg_ms(k) for k in ev}
+    t_fwd, t_idx = t["sparse_fwd"], t["indexer_topk"]
+    t_bwd = sum(t[k] for k in STAGES)
+    # Algorithmic work of each hot kernel (one launch per step) and the roofline that bounds it.
+    #   fwd, B1 (S, dP), B2 (dQ): MFMA flops;  B3 (dKV partial rows), B5 (dKV reduce): HBM bytes
+    #   B3 bytes = G rows N_sel*1152 (write) + P, dS N_sel*H*4 + Q, dO T*H*2176 + idx, pair rows T*K*12
+    #   B5 bytes = G rows N_sel*1152 (read) + dKV N_kv*576*4 (write) + key offsets N_kv*8
+    work = {
+        "sparse_fwd": ("mfma", 2176 * H * nsel, "sparse_mla_fwd_kernel"),
+        "bwd_sp": ("mfma", 2176 * H * nsel, "bwd_sp_kernel"),
+        "bwd_dq": ("mfma", 1152 * H * nsel, "bwd_dq_kernel"),
+        "bwd_g": ("hbm", nsel * 1152 + nsel * H * 4 + T * H * 2176 + T * K * 12, "bwd_g_kernel"),
+        "bwd_dkv_reduce": ("hbm", nsel * 1152 + N * 576 * 4 + N * 8, "bwd_dkv_reduce_kernel"),
+    }
+    dom = max(work, key=lambda k: t[k])
+    bound, amount, kname = work[dom]
+    if bound == "mfma":
+        achieved, peak, unit = amount / (t[dom] * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = amount / (t[dom] * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    traffic = measured_traffic(kname)
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -242,14 +302,15 @@ def main():
                         "causal per document), H=128, d_qk=576, d_v=512, indexer 64x128, top-k 2048",
             "global_batch": 1, "seq_len": T, "parallelism": "single GPU",
         },
-        "breakdown_ms": {"indexer_topk": round(t_idx, 3), "sparse_fwd": round(t_fwd, 3),
-                         "sparse_bwd": round(t_bwd, 3)},
+        "breakdown_ms": {k: round(v, 3) for k, v in t.items()} | {"sparse_bwd": round(t_bwd, 3)},
         "breakdown_tflops": {"indexer": round(fl_idx / t_idx / 1e9, 2), "sparse_fwd": round(fl_fwd / t_fwd / 1e9, 2),
                              "sparse_bwd": round(fl_bwd / t_bwd / 1e9, 2),
-                             "sparse_fwd_bwd": round((fl_fwd + fl_bwd) / (t_fwd + t_bwd) / 1e9, 2)},
-        "roofline": {"bound": "mfma", "kernel": "sparse_mla_fwd_kernel", "achieved": round(achieved, 2),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                             "sparse_fwd_bwd": round((fl_fwd + fl_bwd) / (t_fwd + t_bwd) / 1e9, 2),
+                             "sparse_fwd_bwd_frac_bf16_peak": round((fl_fwd + fl_bwd) / (t_fwd + t_bwd) / 1e9
+                                                                    / PEAK_BF16_TFLOPS, 4)},
+        "roofline": {"bound": bound, "kernel": kname, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "algorithmic": amount, "ms": round(t[dom], 3)},
     }
     if not args.no_decode:
         res["decode"] = decode_leg(torch, dev)

@@ -122,6 +122,16 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* dsa_sparse_mla_bwd with per-stage timing, for profilers and benchmarks (no reference
+ * counterpart; the product path is dsa_sparse_mla_bwd).  stage_events: 6 hipEvent_t the caller
+ * created with timing enabled, recorded on `stream` before the pair ordering, then after it and
+ * after each of the score/probability, dQ, dKV-partial and dKV-reduce stages; NULL = untimed. */
+int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, const void* out,
+                             const void* dout, const float* lse, int total_q, int n_kv, int n_heads,
+                             int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq,
+                             float* dkv, void* workspace, size_t workspace_bytes,
+                             void* const* stage_events, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -199,6 +199,14 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
                        const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
                        float sm_scale, int causal, void* dq, float* dkv, void* workspace,
                        size_t workspace_bytes, void* stream) {
+  return dsa_sparse_mla_bwd_timed(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale,
+                                  causal, dq, dkv, workspace, workspace_bytes, nullptr, stream);
+}
+
+int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, const void* out,
+                             const void* dout, const float* lse, int total_q, int n_kv, int n_heads, int d_qk,
+                             int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
+                             void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream) {
   if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (n_heads > 128 || n_heads % 16 != 0) return DSA_ERR_UNSUPPORTED;
@@ -232,7 +240,10 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   if (total_q == 0) return DSA_OK;
-  return dsa::launch_sparse_mla_bwd(p, as_stream(stream));
+  if (stage_events)
+    for (int i = 0; i < 6; ++i)
+      if (!stage_events[i]) return DSA_ERR_INVALID_ARG;
+  return dsa::launch_sparse_mla_bwd(p, as_stream(stream), reinterpret_cast<hipEvent_t const*>(stage_events));
 }
 
 }  // extern "C"

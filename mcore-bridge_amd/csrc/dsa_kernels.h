@@ -71,7 +71,8 @@ struct TopkParams {
 };
 
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
-int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream);
+// ev (nullable): 6 events recorded around the stages B4 | B1 | B2 | B3 | B5.
+int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev);
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,

@@ -721,9 +721,11 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   }
 }
 
-int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
+int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev) {
   if (p.topk > kMaxTopkBwd) return -2;
   if (p.g_sink_row >= INT32_MAX) return -2;   // B3 keeps G row numbers in 32 bits
+  auto mark = [&](int i) { if (ev) hipEventRecord(ev[i], stream); };
+  mark(0);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
@@ -735,16 +737,21 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, p.csr_counts, p.n_kv, p.csr_offsets);
   hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
                      p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
+  mark(1);
   if (nw == 4) {
     hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);
+    mark(2);
     hipLaunchKernelGGL(bwd_dq_kernel<4>, grid, dim3(256), 0, stream, p);
   } else if (nw == 2) {
     hipLaunchKernelGGL(bwd_sp_kernel<2>, grid, dim3(128), 0, stream, p);
+    mark(2);
     hipLaunchKernelGGL(bwd_dq_kernel<2>, grid, dim3(128), 0, stream, p);
   } else {
     hipLaunchKernelGGL(bwd_sp_kernel<1>, grid, dim3(64), 0, stream, p);
+    mark(2);
     hipLaunchKernelGGL(bwd_dq_kernel<1>, grid, dim3(64), 0, stream, p);
   }
+  mark(3);
   const int nks = p.n_heads / 16;
   const dim3 ggrid(((p.total_q + 7) / 8) * 8);
   if (nks > 4)
@@ -755,8 +762,10 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(bwd_g_kernel<2>, ggrid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL(bwd_g_kernel<1>, ggrid, dim3(256), 0, stream, p);
+  mark(4);
   hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets, p.n_kv,
                      p.dkv, p.dkv_stride);
+  mark(5);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -45,6 +45,9 @@ SIGNATURES = {
     "dsa_sparse_mla_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                    c_size_t, c_void_p]),
+    "dsa_sparse_mla_bwd_timed": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                         c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p,
+                                         c_void_p, c_size_t, c_void_p, c_void_p]),
 }
 
 
