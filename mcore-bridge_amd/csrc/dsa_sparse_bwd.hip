@@ -147,20 +147,16 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   uint32_t st_cur = 0, st_next = 2 * kTileBytes;   // ring byte offsets of blocks blk, blk+2
   u32x2 pw[4], dw[4];   // previous block's values, stored right after the next block's barrier
   for (int blk = 0; blk < nblk; ++blk) {
-    // issue order per block: [wait][barrier][stores(blk-1)][copies(blk+2)][compute] -> after
-    // block blk's copies come stores(blk-1) and copies(blk+1)
+    // issue order per block: [wait][barrier], then between the S/dP MFMAs the copies of block
+    // blk+2 (k-steps 0, 4, .., 32) and the P/dS stores of block blk-1 (k-steps 1, 5, .., 29,
+    // all before the last copy): block blk needs copies(blk) done, with stores(blk-1) and
+    // copies(blk+1) of block blk-1 still allowed in flight.
     if (blk + 1 >= nblk) wait_vmcnt<0>();
     else if (blk == 0 || !wave_stores) wait_vmcnt<G>();
     else wait_vmcnt<G + S>();
     __syncthreads();
-    if (blk > 0 && head_ok) {  // wave_stores => at least one lane active => the wave issues S stores
-      const int64_t j = (blk - 1) * stage_blk;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        *reinterpret_cast<u32x2*>(ps_row + j + 8 * q4) = pw[q4];
-        *reinterpret_cast<u32x2*>(ds_row + j + 8 * q4) = dw[q4];
-      }
-    }
+    const bool store_prev = blk > 0 && head_ok;   // wave_stores => the wave issues all S stores
+    const int64_t store_j = (blk - 1) * stage_blk;
     // block blk+2's gather: one copy per kCopyEvery S/dP steps below
     const bool gather_next = blk + 2 < nblk;
     TileSrc<NW> next_src;
@@ -190,6 +186,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         else if (ks < kDv / 16) mfma32x32x16_acc(dp, cur, df[ks]);
         if (ks % kCopyEvery == 0 && gather_next)
           gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
+        if (ks % 4 == 1 && ks < 32 && store_prev) {
+          const int q = ks / 4;   // 0..7: P then dS of q4 = q / 2
+          if (q & 1) *reinterpret_cast<u32x2*>(ds_row + store_j + 8 * (q >> 1)) = dw[q >> 1];
+          else *reinterpret_cast<u32x2*>(ps_row + store_j + 8 * (q >> 1)) = pw[q >> 1];
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
