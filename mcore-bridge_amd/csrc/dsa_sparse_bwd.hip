@@ -149,10 +149,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   for (int blk = 0; blk < nblk; ++blk) {
     // issue order per block: [wait][barrier], then between the S/dP MFMAs the copies of block
     // blk+2 (k-steps 0, 4, .., 32) and the P/dS stores of block blk-1 (k-steps 1, 5, .., 29,
-    // all before the last copy): block blk needs copies(blk) done, with stores(blk-1) and
-    // copies(blk+1) of block blk-1 still allowed in flight.
+    // all before the last copy).  Block blk needs copies(blk) done; issued after them are
+    // block blk-1's copies(blk+1) and, from blk = 2 on (block 0 stores nothing), its stores of
+    // block blk-2.
     if (blk + 1 >= nblk) wait_vmcnt<0>();
-    else if (blk == 0 || !wave_stores) wait_vmcnt<G>();
+    else if (blk <= 1 || !wave_stores) wait_vmcnt<G>();
     else wait_vmcnt<G + S>();
     __syncthreads();
     const bool store_prev = blk > 0 && head_ok;   // wave_stores => the wave issues all S stores
