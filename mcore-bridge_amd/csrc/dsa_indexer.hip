@@ -31,7 +31,7 @@ namespace dsa {
 namespace {
 constexpr int kIdxChunkMax = 2048;  // keys per wave work item (prefill)
 constexpr int kIdxChunkMin = 256;
-constexpr int kIdxWaveTarget = 8192;  // shrink the chunk until this many work items exist
+constexpr int kIdxWaveTarget = 8192;   // shrink the chunk until this many work items exist
 constexpr int kMaxHi = 64;          // indexer heads handled by the register tiling
 }  // namespace
 
@@ -230,9 +230,36 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
     return;
   }
   const bool cached = n <= kCacheElems;
+  // long rows stay in global memory and are streamed as float4 when the row is 16-byte aligned
+  const bool vec = ((reinterpret_cast<uintptr_t>(sc) & 15) == 0);
+  const float4* sc4 = reinterpret_cast<const float4*>(sc);
   if (cached)
     for (int j = threadIdx.x; j < n; j += blockDim.x) cache[j] = order_key(sc[j]);
   auto key_at = [&](int j) -> uint32_t { return cached ? cache[j] : order_key(sc[j]); };
+  constexpr int T = kTopkThreads;
+  // f(j, key) over every element of the row, each thread a strided subset; loads unrolled
+  auto for_each_key = [&](auto&& f) {
+    if (cached || !vec) {
+      for (int j = threadIdx.x; j < n; j += T) f(key_at(j));
+      return;
+    }
+    const int n4 = n >> 2;
+    int g = threadIdx.x;
+    for (; g + 3 * T < n4; g += 4 * T) {
+      float4 x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = sc4[g + k * T];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        f(order_key(x[k].x)); f(order_key(x[k].y)); f(order_key(x[k].z)); f(order_key(x[k].w));
+      }
+    }
+    for (; g < n4; g += T) {
+      const float4 x = sc4[g];
+      f(order_key(x.x)); f(order_key(x.y)); f(order_key(x.z)); f(order_key(x.w));
+    }
+    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) f(order_key(sc[j]));
+  };
 
   // ---- radix select: find the K-th largest key (prefix over the top 32 bits)
   uint32_t prefix = 0, pmask = 0;
@@ -240,10 +267,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int b = threadIdx.x; b < 256; b += blockDim.x) hist[b] = 0;
     __syncthreads();
-    for (int j = threadIdx.x; j < n; j += blockDim.x) {
-      const uint32_t u = key_at(j);
+    for_each_key([&](uint32_t u) {
       if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
-    }
+    });
     __syncthreads();
     if (threadIdx.x < 64) {  // one wave: suffix scan of 256 bins, 4 per lane (lane 0 = top bins)
       const int l = threadIdx.x;
@@ -276,29 +302,48 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
   }
   const uint32_t thr = prefix;  // exact K-th largest key; take `need` of the keys equal to it
 
-  // ---- stable compaction in ascending index order
-  const int per = (n + kTopkThreads - 1) / kTopkThreads;
+  // ---- stable compaction in ascending index order (thread = contiguous chunk of 4k keys)
+  const int per = (n + 4 * kTopkThreads - 1) / (4 * kTopkThreads) * 4;
   const int a = min(n, (int)threadIdx.x * per), b = min(n, a + per);
+  // g(j, key) over the thread's chunk in index order
+  auto for_chunk = [&](auto&& g) {
+    int j = a;
+    if (!cached && vec) {
+      for (; j + 16 <= b; j += 16) {   // 4 loads in flight
+        float4 x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[k] = sc4[(j >> 2) + k];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          g(j + 4 * k, order_key(x[k].x)); g(j + 4 * k + 1, order_key(x[k].y));
+          g(j + 4 * k + 2, order_key(x[k].z)); g(j + 4 * k + 3, order_key(x[k].w));
+        }
+      }
+      for (; j + 4 <= b; j += 4) {
+        const float4 x = sc4[j >> 2];
+        g(j, order_key(x.x)); g(j + 1, order_key(x.y)); g(j + 2, order_key(x.z)); g(j + 3, order_key(x.w));
+      }
+    }
+    for (; j < b; ++j) g(j, key_at(j));
+  };
   int c_gt = 0, c_eq = 0;
-  for (int j = a; j < b; ++j) {
-    const uint32_t u = key_at(j);
+  for_chunk([&](int, uint32_t u) {
     c_gt += u > thr;
     c_eq += u == thr;
-  }
+  });
   int tot_gt, tot_eq;
   const int gt_before = block_exclusive_scan(c_gt, sh, &tot_gt);
   const int eq_before = block_exclusive_scan(c_eq, sh, &tot_eq);
   int pos = gt_before + min(eq_before, need);
   int eq_rank = eq_before;
-  for (int j = a; j < b; ++j) {
-    const uint32_t u = key_at(j);
+  for_chunk([&](int j, uint32_t u) {
     bool take = u > thr;
     if (u == thr) {
       take = eq_rank < need;
       ++eq_rank;
     }
     if (take) out[pos++] = base + j;
-  }
+  });
   if (p.out_count && threadIdx.x == 0) p.out_count[row] = K;
 }
 
