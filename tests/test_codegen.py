@@ -1,0 +1,105 @@
+"""Static check of the generated gfx950 code (CPU only: hipcc cross-compiles).
+
+Some MFMAs are issued through inline asm (the register-file-pinned forms in dsa_common.h); the
+compiler's hazard recognizer does not see inside asm, so those forms carry their own leading
+wait states.  This test compiles the attention kernels and checks every MFMA of the generated
+code: no VALU instruction may write one of its source registers in the 2 issue slots before it
+(the VALU-write -> MFMA-read hazard), so a compiler or code change that breaks the contract
+cannot slip through.
+"""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "mcore-bridge_amd", "csrc")
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "-w", "-S", "--cuda-device-only"]
+HAZARD_SLOTS = 2
+
+pytestmark = pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                                reason="hipcc not available")
+
+
+def _regs(tok):
+    """Register set of an operand token: ('v', i) / ('a', i) entries."""
+    m = re.fullmatch(r"([va])\[(\d+):(\d+)\]", tok)
+    if m:
+        return {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.fullmatch(r"([va])(\d+)", tok)
+    if m:
+        return {(m.group(1), int(m.group(2)))}
+    return set()
+
+
+def _operands(line):
+    body = line.split(";")[0].strip()
+    parts = body.split(None, 1)
+    if len(parts) < 2:
+        return parts[0] if parts else "", []
+    return parts[0], [t.strip() for t in parts[1].split(",")]
+
+
+def _violations(asm_text):
+    bad = []
+    window = []   # (slots, mnemonic, written regs) of the last instructions
+    func = "?"
+    for raw in asm_text.split("\n"):
+        line = raw.strip()
+        m = re.match(r"^(_Z\w+):", line)
+        if m:
+            func = m.group(1)
+        if not line or line.startswith((";", ".", "_")) or line.endswith(":"):
+            continue   # labels keep the window: the fall-through path is checked across them
+        mn, ops = _operands(line)
+        if not mn or not re.match(r"[vsdgb]", mn):
+            continue
+        if mn.startswith("v_mfma"):
+            srcs = set()
+            for t in ops[1:4]:
+                srcs |= _regs(t)
+            slots = 0
+            for s, pmn, wr in reversed(window):
+                if slots >= HAZARD_SLOTS:
+                    break
+                if wr & srcs and not pmn.startswith(("v_mfma", "ds_", "global_", "buffer_")):
+                    bad.append(f"{func}: {pmn} writes a source of `{line}`")
+                slots += s
+            window.append((1, mn, set()))
+        else:
+            slots = 1
+            if mn == "s_nop" and ops:
+                slots = int(ops[0], 0) + 1
+            written = _regs(ops[0]) if mn.startswith("v_") and ops else set()
+            window.append((slots, mn, written))
+        window = window[-8:]
+    return bad
+
+
+@pytest.mark.parametrize("src", ["dsa_sparse_fwd.hip", "dsa_sparse_bwd.hip"])
+def test_no_valu_write_right_before_mfma(src, tmp_path):
+    out = tmp_path / (src + ".s")
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    subprocess.run([hipcc, *FLAGS, "-o", str(out), os.path.join(CSRC, src)], check=True, cwd=CSRC,
+                   capture_output=True, timeout=600)
+    text = out.read_text()
+    assert "v_mfma" in text
+    bad = _violations(text)
+    assert not bad, "\n".join(bad[:20])
+
+
+def test_checker_flags_a_planted_hazard():
+    asm = "\n".join([
+        "\tv_mov_b32_e32 v4, v9",
+        "\tv_mfma_f32_32x32x16_bf16 v[0:15], v[4:7], v[8:11], v[0:15]",
+        "\tv_mov_b32_e32 v5, v9",
+        "\ts_nop 1",
+        "\tv_mfma_f32_32x32x16_bf16 v[0:15], v[4:7], v[8:11], v[0:15]",
+        "\tv_accvgpr_write_b32 a20, v1",
+        "\tv_mfma_f32_32x32x16_bf16 v[0:15], a[20:23], v[8:11], v[0:15]",
+    ])
+    bad = _violations(asm)
+    assert len(bad) == 2 and "v_mov_b32_e32" in bad[0] and "v_accvgpr_write_b32" in bad[1]
