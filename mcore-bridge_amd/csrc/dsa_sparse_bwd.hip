@@ -379,32 +379,48 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
 // ------------------------------------------------------------------------------------------
 // B3: per-pair dKV partial rows G = (scale*dS)^T Q + P^T dO, contracted over all heads.
 // Wave w owns output row tiles (32 latent dims each): Q part {4w..4w+3} (+16+w for w < 2),
-// dO part {4w..4w+3}.  Each block's G tile [32 keys x 576] goes through LDS (double buffered)
-// so that every row is written to its key-major position with contiguous 16-byte lane stores:
-// wave w stores the latent part of rows 8w..8w+7 (one 1 KB row per instruction) and the rope
-// part of the same rows (one instruction), 9 stores per wave, issued between the next block's
-// MFMAs.  Written straight from the MFMA layout, every store instruction would touch 32 rows
-// 16 bytes each.
+// dO part {4w..4w+3}.
+// Setup: Q[t] and dO[t] (contiguous [H x 576] / [H x 512] bf16) are copied straight into LDS
+// with asynchronous LDS-direct loads, 16 heads per round through a 3-round ring (two rounds in
+// flight while one is read), and the Q^T / dO^T operand fragments are taken from it with
+// transposing reads.  Chunk c of head row r sits at chunk c ^ (2 * (r & 3)), which puts the four
+// rows of every transposing read on distinct banks.
+// Each block's G tile [32 keys x 576] goes through LDS in fp32, written straight from the
+// accumulators, so that every row is written to its key-major position with contiguous 16-byte
+// lane stores: wave w stores the latent part of rows 8w..8w+7 (one 1 KB row per instruction) and
+// the rope part of the same rows (one instruction), 9 stores per wave, converted to bf16 and
+// issued between the next block's MFMAs.  Written straight from the MFMA layout, every store
+// instruction would touch 32 rows 16 bytes each.
 // ------------------------------------------------------------------------------------------
 constexpr int kGHeads = 128;                        // B3 handles up to 128 heads (n_heads % 16 == 0)
 constexpr int kGKs = kGHeads / 16;                  // head k-steps
 constexpr int kStageTile = kGHeads * 64;            // one staged [128 heads][32 keys] bf16 tile
-constexpr int kRowPitch = kDqk * 2 + 16;            // bytes per staged head row of Q / dO
-constexpr int kSetupRows = 32;                      // head rows staged per setup round
-constexpr int kGRowBytes = kDqk * 2;                // one bf16 G row
-constexpr int kGTilePitch = kGRowBytes + 16;        // LDS pitch of a G tile row (bank spread)
+constexpr int kQRound = 16 * kDqk * 2;              // Q bytes of one setup round (16 heads)
+constexpr int kORound = 16 * kDv * 2;               // dO bytes of one setup round
+constexpr int kRoundBytes = kQRound + kORound;
+constexpr int kRoundCopies = kRoundBytes / 1024;    // 1 KB LDS-direct copies per round (34)
+constexpr int kSetupStages = 3;
+constexpr int kGTilePitch = kDqk * 4 + 16;          // LDS pitch of an fp32 G tile row (bank spread)
 constexpr int kGStores = 9;                         // stores per wave per block: 8 rows + rope
 
 struct GSmem {
   union {
-    char rows[kSetupRows * kRowPitch];              // setup: Q / dO rows for the transposed load
-    char st[kStages][2][kStageTile];                // loop: [dS | P] tiles; 16-byte chunk c of head
-  };                                                //   row h at chunk c ^ (2 * ((h >> 1) & 1))
-  char gtile[2][kBK * kGTilePitch];                 // G tiles of blocks blk (being written), blk-1
+    char ring[kSetupStages][kRoundBytes];           // setup: Q / dO rows of 16 heads per round
+    struct {
+      char st[kStages][2][kStageTile];              // [dS | P] tiles; 16-byte chunk c of head row h
+                                                    //   at chunk c ^ (2 * ((h >> 1) & 1))
+      char gtile[kBK * kGTilePitch];                // fp32 G tile of the last finished block;
+    } loop;                                         //   16-byte chunk j of a row at j ^ ((j >> 3) & 1)
+  };
   int32_t pos[kMaxTopkBwd];                         // G row of every index slot (sink if unselected)
   int32_t idx[kMaxTopkBwd];
   int red[4];
 };
+static_assert(sizeof(GSmem) <= 160 * 1024, "B3 LDS budget");
+
+// Chunk slot of fp32 G-tile chunk j (4 dims): consecutive-lane reads of 32-byte pieces and
+// same-column writes of 32 rows are both conflict-free.
+DSA_DEV int gtile_slot(int j) { return j ^ ((j >> 3) & 1); }
 
 // KS = head k-steps run per block (a power of two >= n_heads / 16; steps past n_heads multiply
 // zero Q^T / dO^T fragments).
@@ -418,23 +434,81 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5;
   const int g = lane >> 4, gi = lane & 15;
-  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
-                                       p.causal, t);
-  if (nblk == 0) return;
-  {  // G row of every slot; the loads retire before the setup's final wait
-    const int64_t* pos_row = p.pair_pos + (int64_t)t * p.topk;
-    for (int j = threadIdx.x; j < nblk * kBK; j += NW * 64) {
-      const int64_t v = j < p.topk ? pos_row[j] : -1;
-      sm.pos[j] = (int32_t)(v < 0 ? p.g_sink_row : v);   // < 2^31: checked by the launcher
-    }
-  }
   const int nks = p.n_heads / 16;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+
+  // ---- setup copies: round r = heads 16r..16r+15 into ring[r % 3]; copy j (1 KB of LDS) is
+  // Q bytes 1024j of the round for j < 18, dO bytes 1024(j - 18) after; wave w issues copies
+  // w, w + 4, ... (9 for waves 0-1, 8 for waves 2-3)
+  const char* q_t = reinterpret_cast<const char*>(p.q + (int64_t)t * p.q_stride_t);
+  const char* o_t = reinterpret_cast<const char*>(p.dout + (int64_t)t * p.dout_stride_t);
+  const uint32_t ring0 = lds_addr(sm.ring[0]);
+  auto issue_round = [&](int r) {
+    const uint32_t dst = ring0 + (uint32_t)(r % kSetupStages) * kRoundBytes;
+#pragma unroll
+    for (int i = 0; i < (kRoundCopies + NW - 1) / NW; ++i) {
+      const int j = NW * i + wu;
+      if (j < kRoundCopies) {
+        const char* src;
+        if (j < kQRound / 1024) {   // 16-byte chunk c of the round's Q rows (72 per row)
+          const int c = j * 64 + lane, row = c / (kDqk / 8), slot = c - row * (kDqk / 8);
+          src = q_t + (int64_t)(16 * r + row) * (kDqk * 2) + 16 * (slot ^ (2 * (row & 3)));
+        } else {                    // chunk c of the round's dO rows (64 per row)
+          const int c = (j - kQRound / 1024) * 64 + lane, row = c >> 6, slot = c & 63;
+          src = o_t + (int64_t)(16 * r + row) * (kDv * 2) + 16 * (slot ^ (2 * (row & 3)));
+        }
+        async_copy16_unordered(src, __builtin_amdgcn_readfirstlane(dst + 1024u * j));
+      }
+    }
+  };
+  issue_round(0);
+  if (nks > 1) issue_round(1);
+
+  // ---- index row and G rows of every slot, all loads in flight together (and with the copies)
+  int nblk;
+  {
+    const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
+    const int64_t* pos_row = p.pair_pos + (int64_t)t * p.topk;
+    const int kpad = (p.topk + kBK - 1) / kBK * kBK;
+    constexpr int kPer = kMaxTopkBwd / (NW * 64);
+    int32_t iv[kPer];
+    int64_t pv[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int j = threadIdx.x + NW * 64 * i;
+      iv[i] = j < p.topk ? idx_row[j] : -1;
+      pv[i] = j < p.topk ? pos_row[j] : -1;
+    }
+    int last = -1;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int j = threadIdx.x + NW * 64 * i;
+      if (j < kpad) {
+        int v = iv[i];
+        if (v < 0 || v >= p.n_kv || (p.causal && v > t)) v = -1;
+        sm.idx[j] = v;
+        if (v >= 0) last = j;
+        sm.pos[j] = (int32_t)(pv[i] < 0 ? p.g_sink_row : pv[i]);   // < 2^31: checked by the launcher
+      }
+    }
+    last = wave_max_i(last);
+    if (lane == 0) sm.red[wave] = last;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; ++w) last = max(last, sm.red[w]);
+    nblk = __builtin_amdgcn_readfirstlane((last + kBK) / kBK);
+  }
+  if (nblk == 0) {
+    wait_vmcnt0();   // no copy outlives the workgroup
+    return;
+  }
   auto qtile = [&](int i) { return i < 4 ? 4 * wave + i : 16 + wave; };
 
-  // ---- Q^T and dO^T fragments (A operand: row = latent dim, k = 8 heads) via LDS, 32 heads a round
+  // ---- Q^T and dO^T fragments (A operand: row = latent dim, k = 8 heads)
   u32x4 qa[5][KS], va[4][KS];
   const int tr_h = 8 * (g >> 1) + (gi >> 2);        // head row this lane feeds into ds_read_tr
   const int tr_c = 16 * (g & 1) + 4 * (gi & 3);     // latent column this lane feeds
+  const int tr_sw = 2 * (gi >> 2);                  // chunk swizzle of rows tr_h and tr_h + 4
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
@@ -443,46 +517,40 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     for (int i = 0; i < 4; ++i) va[i][ks] = u32x4{0, 0, 0, 0};
   }
   const int nq = wave < 2 ? 5 : 4;
+  // byte address of (row tr_h + dr, latent column tr_c of tile mt) in a round part of row pitch rp
+  auto tr_at = [&](uint32_t part, int rp, int mt, int dr) {
+    const int cb = 64 * mt + 2 * tr_c;
+    return lds_ptr(part + (tr_h + dr) * rp + 16 * ((cb >> 4) ^ tr_sw) + (cb & 15));
+  };
+  // round ks: ready once this wave's copies of it are done (only round ks + 1 may still be in
+  // flight) and every wave has passed the barrier; the barrier also retires the reads of round
+  // ks - 1, whose buffer round ks + 2 then refills
 #pragma unroll
-  for (int r0 = 0; r0 < 16 * KS; r0 += kSetupRows) {
-    if (r0 >= p.n_heads) break;
+  for (int ks = 0; ks < KS; ++ks) {
+    if (ks >= nks) break;
+    if (ks + 1 < nks) {
+      if (wu < kRoundCopies % NW) wait_vmcnt<(kRoundCopies + NW - 1) / NW>();
+      else wait_vmcnt<kRoundCopies / NW>();
+    } else {
+      wait_vmcnt0();
+    }
+    __syncthreads();
+    if (ks + 2 < nks) issue_round(ks + 2);
+    const uint32_t qb = ring0 + (uint32_t)(ks % kSetupStages) * kRoundBytes, ob = qb + kQRound;
 #pragma unroll
-    for (int part = 0; part < 2; ++part) {
-      const bf16_t* src = part == 0 ? p.q + (int64_t)t * p.q_stride_t : p.dout + (int64_t)t * p.dout_stride_t;
-      const int width = part == 0 ? kDqk : kDv;
-      const int nrows = min(kSetupRows, p.n_heads - r0);
-      __syncthreads();
-      for (int c = threadIdx.x; c < nrows * (width / 8); c += blockDim.x) {
-        const int r = c / (width / 8), cc = c - r * (width / 8);
-        lds_store16(sm.rows + r * kRowPitch + cc * 16, gload16(src + (int64_t)(r0 + r) * width + cc * 8));
-      }
-      __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < kSetupRows / 16; ++kk) {
-        const int ks = r0 / 16 + kk;
-        if (ks >= nks || ks >= KS) continue;
-        const char* rb = sm.rows + (16 * kk + tr_h) * kRowPitch + tr_c * 2;
-        if (part == 0) {
-#pragma unroll
-          for (int i = 0; i < 5; ++i) {
-            if (i < nq) {
-              const u32x2 lo = lds_read_tr16(rb + 64 * qtile(i)), hi = lds_read_tr16(rb + 4 * kRowPitch + 64 * qtile(i));
-              qa[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-            }
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int mt = 4 * wave + i;
-            const u32x2 lo = lds_read_tr16(rb + 64 * mt), hi = lds_read_tr16(rb + 4 * kRowPitch + 64 * mt);
-            va[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-          }
-        }
+    for (int i = 0; i < 5; ++i) {
+      if (i < nq) {
+        const u32x2 lo = lds_read_tr16(tr_at(qb, kDqk * 2, qtile(i), 0)), hi = lds_read_tr16(tr_at(qb, kDqk * 2, qtile(i), 4));
+        qa[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x2 lo = lds_read_tr16(tr_at(ob, kDv * 2, 4 * wave + i, 0)), hi = lds_read_tr16(tr_at(ob, kDv * 2, 4 * wave + i, 4));
+      va[i][ks] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
   }
-  wait_vmcnt0();
-  __syncthreads();  // setup rows dead: the union now holds the [dS | P] ring
+  __syncthreads();  // ring dead (every copy waited for): the union now holds the [dS | P] ring
 
   // ---- key blocks: [dS | P] tiles (rows = heads, 32 keys each) through a 3-stage copy ring
   // staged tiles of block b: [H heads][32 keys] bf16, contiguous (see B1)
@@ -493,9 +561,8 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   // dS for even c, P for odd c.  Head rows past n_heads re-read row 0 (valid memory; their
   // k-steps multiply zeros).
   auto stage_part = [&](int s, int blk, int c) {
-    const uint32_t b = __builtin_amdgcn_readfirstlane(lds_addr(sm.st[s][c & 1]));
-    const int w = __builtin_amdgcn_readfirstlane(wave);
-    const int i = w + (c >> 1) * NW;
+    const uint32_t b = __builtin_amdgcn_readfirstlane(lds_addr(sm.loop.st[s][c & 1]));
+    const int i = wu + (c >> 1) * NW;
     const int h = 16 * i + (lane >> 2);
     const int hs = h < p.n_heads ? h : 0;
     const int chunk = (lane & 3) ^ (2 * ((h >> 1) & 1));   // LDS chunk lane&3 <- global chunk
@@ -508,23 +575,33 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   };
   // B operand address of this lane inside a tile: head row 16*ks + tr_h, bytes 2*tr_c .. +8
   const uint32_t b_off = tr_h * 64 + 16 * (((2 * tr_c) >> 4) ^ (2 * ((tr_h >> 1) & 1))) + ((2 * tr_c) & 15);
-  // G tile write slot of this lane: key row lane % 32 (bytes 8*hb of each 16-byte chunk)
-  const uint32_t gt_w = (lane & 31) * kGTilePitch + 8 * hb;
-  const uint32_t gtile0 = lds_addr(sm.gtile[0]);
-  // stores of a finished G tile by this wave: latent chunks lane of rows 8w + i (i < 8), then
-  // the rope chunk lane % 8 of row 8w + lane / 8
+  // G tile row of this lane's accumulators: key lane % 32.  Chunk 8*qtile + 2*q4 + hb of tile
+  // 4w + i sits at slot (8*(4w + i) + 2*q4) + (hb ^ (i & 1)), of the rope tile 16 + w at
+  // (8*(16 + w) + 2*q4) + (hb ^ (w & 1)): per-lane bases plus immediates.
+  const uint32_t gtile = lds_addr(sm.loop.gtile);
+  const uint32_t gt_w = gtile + (lane & 31) * kGTilePitch;
+  const uint32_t pk_even = gt_w + 512 * wave + 16 * hb, pk_odd = gt_w + 512 * wave + 16 * (hb ^ 1);
+  const uint32_t pk_rope = gt_w + 16 * (8 * (16 + wave)) + 16 * (hb ^ (wave & 1));
+  // stores of a finished G tile by this wave: latent dims 8*lane .. +7 of rows 8w + i (i < 8),
+  // then the rope dims 512 + 8 * (lane % 8) .. +7 of row 8w + lane / 8
   const int rope_row = 8 * wave + (lane >> 3);
-  // store i of a finished tile: its 16 data bytes are read from LDS one k-step ahead
-  // (store_load), the global store is issued later (store_issue) -- no exposed LDS latency.
-  auto store_load = [&](uint32_t gt, int i) {
-    return i < 8 ? lds_load16(lds_ptr(gt + (8 * wave + i) * kGTilePitch + 16 * lane))
-                 : lds_load16(lds_ptr(gt + rope_row * kGTilePitch + 16 * (64 + (lane & 7))));
+  // store i of a finished tile: its 8 fp32 values are read from LDS one k-step ahead
+  // (store_load), converted and stored later (store_issue) -- no exposed LDS latency.
+  struct StoreData { f32x4 a, b; };
+  auto store_load = [&](int i) {
+    const int row = i < 8 ? 8 * wave + i : rope_row;
+    const int j = i < 8 ? 2 * lane : 128 + 2 * (lane & 7);   // first of the two 4-dim chunks
+    const char* r = lds_ptr(gtile + row * kGTilePitch);
+    return StoreData{*reinterpret_cast<const f32x4*>(r + 16 * gtile_slot(j)),
+                     *reinterpret_cast<const f32x4*>(r + 16 * gtile_slot(j + 1))};
   };
-  auto store_issue = [&](const int32_t (&rpos)[8], int32_t rope_pos, int i, const u32x4& v) {
+  auto store_issue = [&](const int32_t (&rpos)[8], int32_t rope_pos, int i, const StoreData& v) {
+    const u32x4 o{pack_bf16x2(v.a[0], v.a[1]), pack_bf16x2(v.a[2], v.a[3]), pack_bf16x2(v.b[0], v.b[1]),
+                  pack_bf16x2(v.b[2], v.b[3])};
     if (i < 8)
-      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rpos[i] * kDqk + 8 * lane) = v;
+      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rpos[i] * kDqk + 8 * lane) = o;
     else
-      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))) = v;
+      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))) = o;
   };
   // k-step of copy c (c < G) and of store i (i < kGStores); stores follow copies in a step
   constexpr auto copy_ks = [](int c) { return c * KS / G; };
@@ -541,9 +618,9 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     if (nblk > 1) stage(1, 1);
     for (int blk = 0; blk < nblk; ++blk) {
       // issue order of block blk: [wait][barrier] then, between its MFMAs, copies(blk+2) and
-      // stores(blk-1) (stores after copies within a k-step), then [G(blk) -> LDS].  Block blk
-      // needs copies(blk) done; issued after them: block 0 nothing of its own, block 1 the
-      // copies(3) + stores(0), block b >= 3 the trailing stores(b-3) of block b-2 plus block
+      // stores(blk-1) (stores after copies within a k-step), then [barrier][G(blk) -> LDS].
+      // Block blk needs copies(blk) done; issued after them: block 0 nothing of its own, block 1
+      // the copies(3) + stores(0), block b >= 3 the trailing stores(b-3) of block b-2 plus block
       // b-1's copies(b+1) + stores(b-2).
       if (blk + 1 >= nblk) wait_vmcnt<0>();
       else if (blk <= 1) wait_vmcnt<G>();
@@ -552,21 +629,20 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       __syncthreads();
       const bool copy_next = blk + 2 < nblk;
       const bool store_prev = blk > 0;
-      const uint32_t gt_prev = gtile0 + ((blk - 1) & 1) * (kBK * kGTilePitch);
       // G rows of the previous block's tile: this wave's 8 latent rows (wave-uniform) and the
       // rope row of this lane
       int32_t rpos[8], rope_pos = 0;
-      u32x4 sv[kGStores];
+      StoreData sv[kGStores];
       if (store_prev) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(blk - 1) * kBK + 8 * wave + i]);
         rope_pos = sm.pos[(blk - 1) * kBK + rope_row];
 #pragma unroll
         for (int i = 0; i < kGStores; ++i)
-          if (store_ks(i) == 0) sv[i] = store_load(gt_prev, i);
+          if (store_ks(i) == 0) sv[i] = store_load(i);
       }
-      const char* sd = sm.st[blk % kStages][0] + b_off;
-      const char* sp = sm.st[blk % kStages][1] + b_off;
+      const char* sd = sm.loop.st[blk % kStages][0] + b_off;
+      const char* sp = sm.loop.st[blk % kStages][1] + b_off;
       f32x16 acc[NQ];
 #pragma unroll
       for (int i = 0; i < NQ; ++i) acc[i] = f32x16{};
@@ -590,7 +666,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         if (store_prev) {
 #pragma unroll
           for (int i = 0; i < kGStores; ++i) {
-            if (store_ks(i) == ks + 1) sv[i] = store_load(gt_prev, i);   // next step's data
+            if (store_ks(i) == ks + 1) sv[i] = store_load(i);   // next step's data
             if (store_ks(i) == ks) store_issue(rpos, rope_pos, i, sv[i]);
           }
         }
@@ -602,28 +678,27 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         for (int i = 0; i < 4; ++i) acc[i] = mfma32x32x16(as_bf16x8(va[i][ks]), as_bf16x8(bp), acc[i]);
         if (ks + 1 < KS) { bs = bs_n; bp = bp_n; }
       }
-      // G tile -> LDS (bf16): lane holds key lane % 32, dims 32*qtile(i) + 8*q4 + 4*hb .. +3
-      const uint32_t gt_cur = gtile0 + (blk & 1) * (kBK * kGTilePitch) + gt_w;
+      // G tile -> LDS (fp32, straight from the accumulators) once every wave has read the
+      // previous tile: lane holds key lane % 32, dims 32*qtile(i) + 8*q4 + 4*hb .. +3
+      __syncthreads();
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
+        const uint32_t base = i < 4 ? ((i & 1) ? pk_odd : pk_even) + 128 * i : pk_rope;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int c = 4 * qtile(i) + q4;
-          *reinterpret_cast<u32x2*>(const_cast<char*>(lds_ptr(gt_cur + 16 * c))) =
-              u32x2{pack_bf16x2(acc[i][4 * q4], acc[i][4 * q4 + 1]), pack_bf16x2(acc[i][4 * q4 + 2], acc[i][4 * q4 + 3])};
-        }
+        for (int q4 = 0; q4 < 4; ++q4)
+          *reinterpret_cast<f32x4*>(const_cast<char*>(lds_ptr(base + 32 * q4))) =
+              f32x4{acc[i][4 * q4], acc[i][4 * q4 + 1], acc[i][4 * q4 + 2], acc[i][4 * q4 + 3]};
       }
     }
     // the last block's G tile
     __syncthreads();
     {
-      const uint32_t gt = gtile0 + ((nblk - 1) & 1) * (kBK * kGTilePitch);
       int32_t rpos[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(nblk - 1) * kBK + 8 * wave + i]);
       const int32_t rope_pos = sm.pos[(nblk - 1) * kBK + rope_row];
 #pragma unroll
-      for (int i = 0; i < kGStores; ++i) store_issue(rpos, rope_pos, i, store_load(gt, i));
+      for (int i = 0; i < kGStores; ++i) store_issue(rpos, rope_pos, i, store_load(i));
     }
   };
   if (nq == 5) block_loop(std::integral_constant<int, 5>{});
