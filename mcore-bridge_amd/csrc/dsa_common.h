@@ -62,6 +62,13 @@ DSA_DEV void mfma32x32x16_cV(f32x16& c, const u32x4& a, const u32x4& b) {
 DSA_DEV void mfma32x32x16_cV_first(f32x16& c, const u32x4& a, const u32x4& b) {
   asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(c) : "v"(a), "v"(b));
 }
+// 16x16x32 forms (4-pass XDL; the same hazard contract).
+DSA_DEV void mfma16x16x32_cA(f32x4& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+DSA_DEV void mfma16x16x32_cV(f32x4& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
 DSA_DEV void mfma_acc_drain() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_nop 15");
@@ -161,9 +168,16 @@ DSA_DEV uint32_t lds_addr(const void* p) {
 // The same copy issued through inline asm (M0 = wave-uniform LDS base).  The compiler does not
 // model it, so it neither serialises later LDS reads against it nor waits for it: the caller
 // owns completion (s_waitcnt vmcnt(N) + barrier) -- that is what lets a multi-stage gather ring
-// overlap the MFMA work on earlier stages.
+// overlap the MFMA work on earlier stages.  M0 is written right before the LDS DMA, which reads
+// it one wait state later (s_nop 0).
 DSA_DEV void async_copy16_unordered(const void* gsrc, uint32_t lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(gsrc)
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(gsrc)
+               : "memory", "m0");
+}
+
+// 4-byte variant (global_load_lds_dword): lane i writes 4 bytes at lds_wave_base + 4*i.
+DSA_DEV void async_copy4_unordered(const void* gsrc, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_wave_base), "v"(gsrc)
                : "memory", "m0");
 }
 

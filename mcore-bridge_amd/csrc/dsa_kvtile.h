@@ -73,9 +73,12 @@ DSA_DEV TileSrc<NW> tile_sources(const bf16_t* kv, const int32_t* idx_blk, int w
   return s;
 }
 
-// global_load_lds_dwordx4 with a scalar 64-bit row address and a per-lane byte offset.
+// global_load_lds_dwordx4 with a scalar 64-bit row address and a per-lane byte offset.  The
+// row address comes from v_readlane (a VALU write of the SGPRs the load reads: 5 wait states)
+// and M0 is written right before the LDS DMA (1 wait state); the compiler cannot see either
+// inside the asm, so the nops are part of it.
 DSA_DEV void copy_row16(uint32_t lds_wave_base, const char* row, uint32_t lane_off) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(lane_off), "s"(row)
+  asm volatile("s_nop 4\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(lane_off), "s"(row)
                : "memory", "m0");
 }
 

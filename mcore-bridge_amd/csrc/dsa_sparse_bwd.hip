@@ -60,12 +60,25 @@ DSA_DEV int stage_index_row(int32_t* idx_s, int* red, const int32_t* idx_row, in
                             int t) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int kpad = (topk + kBK - 1) / kBK * kBK;
+  constexpr int kBatch = 8;   // loads in flight per thread (one memory round trip per batch)
   int last = -1;
-  for (int j = threadIdx.x; j < kpad; j += NW * 64) {
-    int v = j < topk ? idx_row[j] : -1;
-    if (v < 0 || v >= n_kv || (causal && v > t)) v = -1;
-    idx_s[j] = v;
-    if (v >= 0) last = j;
+  for (int j0 = threadIdx.x; j0 < kpad; j0 += kBatch * NW * 64) {
+    int v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int j = j0 + i * NW * 64;
+      v[i] = j < topk ? idx_row[j] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int j = j0 + i * NW * 64;
+      int x = v[i];
+      if (x < 0 || x >= n_kv || (causal && x > t)) x = -1;
+      if (j < kpad) {
+        idx_s[j] = x;
+        if (x >= 0) last = j;
+      }
+    }
   }
   last = wave_max_i(last);
   if (lane == 0) red[wave] = last;
@@ -82,8 +95,12 @@ DSA_DEV int stage_index_row(int32_t* idx_s, int* red, const int32_t* idx_row, in
 // B1: recompute P and dS; stage them.  One workgroup per query, wave = 32 heads.
 // ------------------------------------------------------------------------------------------
 struct SpSmem {
-  char tile[kStages][kTileBytes];
+  union {
+    char tile[kStages][kTileBytes];
+    char ostage[4][32][kDv * 2];   // setup: O rows of each wave's 32 heads (for Delta)
+  };
   int32_t idx[kMaxTopkBwd];
+  float lse[4][64];                // setup: LSE of each lane's head
   int red[4];
 };
 
@@ -103,33 +120,59 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   const bool wave_stores = blockIdx.y * 128 + wave * 32 < p.n_heads;  // wave-uniform
   const int hsafe = head_ok ? head : 0;
 
+  static_assert(NW <= 4, "O staging holds 4 waves");
+  // Setup, one memory round trip: the O rows of this wave's 32 heads stream into LDS
+  // (asynchronous, no registers; row i = head 32w + i, 16-byte chunk c at c ^ (i & 7)) while
+  // Q and dO load into their fragments and the index row into LDS.
+  {
+    const uint32_t ob = __builtin_amdgcn_readfirstlane(lds_addr(sm.ostage[wave]));
+    const char* o_t = reinterpret_cast<const char*>(p.out + (int64_t)t * p.out_stride_t);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int h = blockIdx.y * 128 + wave * 32 + i;
+      const int hs = h < p.n_heads ? h : 0;   // rows past n_heads re-read head 0 (unused)
+      async_copy16_unordered(o_t + (int64_t)hs * (kDv * 2) + 16 * (lane ^ (i & 7)), ob + 1024u * i);
+    }
+  }
   // Q (576) and dO (512) fragments, d-contiguous: lane holds [16*ks + 8*hb, +8).
   u32x4 qf[kDqk / 16], df[kDv / 16];
   const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)hsafe * kDqk + hb * 8;
   const bf16_t* drow = p.dout + (int64_t)t * p.dout_stride_t + (int64_t)hsafe * kDv + hb * 8;
-  const bf16_t* orow = p.out + (int64_t)t * p.out_stride_t + (int64_t)hsafe * kDv + hb * 8;
 #pragma unroll
   for (int ks = 0; ks < kDqk / 16; ++ks) {
     const u32x4 v = gload16(qrow + ks * 16);
     qf[ks] = head_ok ? v : u32x4{0, 0, 0, 0};
   }
-  float delta = 0.f;
 #pragma unroll
   for (int ks = 0; ks < kDv / 16; ++ks) {
     const u32x4 v = gload16(drow + ks * 16);
-    const u32x4 o = gload16(orow + ks * 16);
     df[ks] = head_ok ? v : u32x4{0, 0, 0, 0};
+  }
+  // LSE of this lane's head, also through LDS (a register load would be waited for at once)
+  async_copy4_unordered(p.lse + (int64_t)t * p.lse_stride_t + hsafe,
+                        __builtin_amdgcn_readfirstlane(lds_addr(sm.lse[wave])));
+  // (waits for every load above, the O copies included, then a barrier)
+  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
+                                       p.causal, t);
+  // Delta = rowsum(dO * O) of this lane's head: chunks 2*ks + hb of O row hl from LDS
+  float delta = 0.f;
+  {
+    const char* orow_s = sm.ostage[wave][hl];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      delta += bf16_lo(v[e]) * bf16_lo(o[e]) + bf16_hi(v[e]) * bf16_hi(o[e]);
+    for (int ks = 0; ks < kDv / 16; ++ks) {
+      const u32x4 o = lds_load16(orow_s + 16 * ((2 * ks + hb) ^ (hl & 7)));
+      const u32x4 v = df[ks];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        delta += bf16_lo(v[e]) * bf16_lo(o[e]) + bf16_hi(v[e]) * bf16_hi(o[e]);
+    }
   }
   delta = xor32_sum(delta);
   const float delta_s = delta * p.scale;
-  const float lse = head_ok ? p.lse[(int64_t)t * p.lse_stride_t + head] : -INFINITY;
+  const float lse = head_ok ? sm.lse[wave][lane] : -INFINITY;
   const float lse2 = lse * kLog2e;
   const bool row_live = lse != -INFINITY;
-  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
-                                       p.causal, t);
+  __syncthreads();   // O staging dead: the union now holds the KV tile ring
 
   // staged tiles: element (t, head, slot 32*b + k) at ((t * NB + b) * H + head) * 32 + k
   // (NB = topk_pad / 32): each block's [H heads x 32 keys] tile is contiguous; lane writes keys
@@ -230,46 +273,57 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
 }
 
 // ------------------------------------------------------------------------------------------
-// B2: dQ^T[576 x 32 heads] = K^T . (scale*dS)^T per wave, over the query's gathered rows.
+// B2: dQ^T[576 x 32*NW heads] = K^T . (scale*dS)^T over the query's gathered rows, with
+// 16x16x32 MFMAs.  Wave w owns 576/NW latent dims (DT tiles of 16) for every head of the
+// workgroup (HT tiles of 16): per 32-key block it reads DT K^T fragments (transposing reads of
+// the KV tile) and HT dS^T fragments, each K^T fragment feeding HT MFMAs and each dS^T fragment
+// DT.  (Split by heads instead, every wave would read the whole K^T tile for 36 MFMAs: four
+// times the LDS reads.)
 // ------------------------------------------------------------------------------------------
 constexpr int kDsTileBytes = 128 * 64;  // [128 heads][32 keys] bf16
+constexpr int kDqPitch = kDqk * 2 + 16;  // LDS pitch of a staged bf16 dQ row
 
 struct DqSmem {
-  char tile[kStages][kTileBytes];
-  char ds[kStages][kDsTileBytes];
+  union {
+    struct {
+      char tile[kStages][kTileBytes];
+      char ds[kStages][kDsTileBytes];   // 16-byte chunk q of head row h at q ^ ((h >> 1) & 3)
+    } ring;
+    char out[64][kDqPitch];             // epilogue: bf16 dQ rows of 64 heads
+  };
   int32_t idx[kMaxTopkBwd];
   int red[4];
 };
 
 template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
-  constexpr int HR = 32 * NW;                                  // head rows copied per block
-  constexpr int G = tile_copies_per_wave<NW>() + HR / 16 / NW;
-  constexpr int kCopyEvery = kDqk / 16 / tile_copies_per_wave<NW>();   // MFMA steps per tile copy
+  constexpr int HR = 32 * NW;                                  // head rows of the workgroup
+  constexpr int HT = HR / 16;                                  // head tiles
+  constexpr int DT = kDqk / 16 / NW;                           // dim tiles per wave
+  constexpr int TC = tile_copies_per_wave<NW>();
+  constexpr int G = TC + HR / 16 / NW;
   static_assert(HR / 16 / NW == 2, "two dS copies per wave per block");
+  static_assert(DT * NW * 16 == kDqk && DT >= TC, "dims split evenly; one tile copy per dim step");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
   const int t = xcd_remap(blockIdx.x, p.total_q);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int hb = lane >> 5, hl = lane & 31;
+  const int g = lane >> 4, gi = lane & 15;
   const int h0 = blockIdx.y * 128;
-  const int head = h0 + wave * 32 + hl;
-  const bool head_ok = head < p.n_heads;
   const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
                                        p.causal, t);
-  // dS rows of this workgroup's heads; rows past n_heads re-read row 0 (never stored).  16-byte
-  // chunk q of head row h lands at position q ^ ((h >> 2) & 3): bank-conflict-free column reads.
+  // dS rows of this workgroup's heads; rows past n_heads re-read row 0 (never stored).
   const int hrows = min(HR, p.n_heads - h0);
   // staged dS tile of block b: [H heads][32 keys] contiguous at ((t * NB + b) * H) * 32
   const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + ((int64_t)t * (p.topk_pad / kBK) * p.n_heads + h0) * kBK);
   const int64_t ds_blk = (int64_t)p.n_heads * kBK * 2;   // bytes per staged block tile
-  // copy k (0 <= k < HR/16/NW = 2) of this wave's share of block blk's dS rows
+  // copy k (0 <= k < 2) of this wave's share of block blk's dS rows
   auto copy_ds_part = [&](char* dst, int blk, int k) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
     const int w = __builtin_amdgcn_readfirstlane(wave);
     const int i = w + k * NW;
     const int h = 16 * i + (lane >> 2);
-    const int q = (lane & 3) ^ ((h >> 2) & 3);
+    const int q = (lane & 3) ^ ((h >> 1) & 3);
     const int hs = h < hrows ? h : 0;
     async_copy16_unordered(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
   };
@@ -278,100 +332,108 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
     for (int k = 0; k < HR / 16 / NW; ++k) copy_ds_part(dst, blk, k);
   };
 
-  // A operand (K^T via ds_read_tr), natural key order: lane feeds key 16a + 8(g/2) + 4h + gi/4,
-  // latent column 32m + 16(g%2) + 4(gi%4).  Byte address: V part kt[a][h] + 64*m (m < 16),
-  // rope part kr[a][h] ^ (64*(m-16)).
-  uint32_t kt[2][2], kr[2][2];
-  {
-    const int g = lane >> 4, gi = lane & 15;
-    const uint32_t cl = 2 * (g & 1) + ((gi & 3) >> 1);
+  // A operand (K^T, dims x keys) of dim tile D: lane (g, gi) gets dim 16D + gi, keys 8g .. 8g+7
+  // as two transposing reads of 4 keys (rows 8g + gi/4 and 8g + 4 + gi/4, 4 dims from
+  // 16D + 4(gi%4)).  V dims (D < 32): tile row key_row(key) (keys 8g + j sit 2 rows apart:
+  // conflict-free), byte kv[h] + 32D; rope dims: kr[h] ^ (32(D - 32)).
+  uint32_t kv[2], kr[2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t key = 16 * a + 8 * (g >> 1) + 4 * h + (gi >> 2);
-        kt[a][h] = key_row(key) * kTileVPitch + 32u * (g & 1) + 8u * (gi & 3);
-        kr[a][h] = kTileVBytes + key * 128u + 8u * (gi & 1) + 16u * (cl ^ ((key >> 1) & 7u));
-      }
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t key = 8 * g + 4 * h + (gi >> 2);
+    kv[h] = key_row(key) * kTileVPitch + 8u * (gi & 3);
+    kr[h] = kTileVBytes + key * 128u + 8u * (gi & 1) + 16u * (((gi & 3) >> 1) ^ ((key >> 1) & 7u));
   }
-  const uint32_t tile0 = lds_addr(sm.tile[0]);
-  // B operand (dS^T): lane (head row wave*32 + hl, keys 16a + 8hb .. +7) = 16-byte chunk 2a + hb
-  const int hrow = wave * 32 + hl;
-  const uint32_t dsb = hrow * 64u;
-  const uint32_t dsq = (uint32_t)((hrow >> 2) & 3);
+  // B operand (dS^T, keys x heads) of head tile j: head row 16j + gi, keys 8g .. 8g+7
+  const uint32_t ds_lane = gi * 64u + 16u * (g ^ ((gi >> 1) & 3));
+  const int d0 = __builtin_amdgcn_readfirstlane(wave) * DT;   // first dim tile of this wave
+  const uint32_t tile0 = lds_addr(sm.ring.tile[0]);
 
-  // dQ^T accumulators: 18 tiles = 288 registers per lane, more than either register file --
-  // tiles 0..15 are pinned in AccVGPRs and 16, 17 in VGPRs (AGPR/VGPR-constrained MFMAs)
-  f32x16 acc[kDqk / 32];
+  // dQ^T accumulators: DT x HT tiles of 16 x 16, 288 registers per lane -- more than either
+  // register file: tiles 0..63 (row-major) are pinned in AccVGPRs, the rest in VGPRs
+  // (AGPR/VGPR-constrained MFMAs; left to itself the compiler moves tiles between the files
+  // around the MFMAs).
+  constexpr int kTilesA = 64;
+  f32x4 acc[DT][HT];
 #pragma unroll
-  for (int m = 0; m < kDqk / 32; ++m) acc[m] = f32x16{};
+  for (int i = 0; i < DT; ++i)
+#pragma unroll
+    for (int j = 0; j < HT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   mfma_acc_drain();   // zero writes of the accumulators before their first MFMA read
 
   if (nblk > 0) {
     gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
-    copy_ds(sm.ds[0], 0);
+    copy_ds(sm.ring.ds[0], 0);
   }
   if (nblk > 1) {
     gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
-    copy_ds(sm.ds[1], 1);
+    copy_ds(sm.ring.ds[1], 1);
   }
   int st = 0;   // ring stage of block blk
   for (int blk = 0; blk < nblk; ++blk) {
     if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
     __syncthreads();
-    // block blk+2's copies, spread over the 36 MFMA steps below: tile copy k at step
-    // kCopyEvery*k, the dS copies at steps 1 and 3
+    // block blk+2's copies, one tile copy per dim step below, the dS copies at steps 1 and 3
     const bool copy_next = blk + 2 < nblk;
     const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
     TileSrc<NW> next_src;
     if (copy_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
     const uint32_t next_tile = tile0 + st_next * kTileBytes;
-    char* const next_ds = sm.ds[st_next];
+    char* const next_ds = sm.ring.ds[st_next];
     const uint32_t tb = tile0 + st * kTileBytes;   // 128-byte aligned: the rope XOR stays in its row
-    const char* dsl = sm.ds[st];
+    const char* dsl = sm.ring.ds[st] + ds_lane;
     st = st == 2 ? 0 : st + 1;
-    uint32_t k00 = tb + kt[0][0], k01 = tb + kt[0][1], k10 = tb + kt[1][0], k11 = tb + kt[1][1];
-    uint32_t r00 = tb + kr[0][0], r01 = tb + kr[0][1], r10 = tb + kr[1][0], r11 = tb + kr[1][1];
-    asm volatile("" : "+v"(k00), "+v"(k01), "+v"(k10), "+v"(k11), "+v"(r00), "+v"(r01), "+v"(r10), "+v"(r11));
+    uint32_t v0 = tb + kv[0], v1 = tb + kv[1], r0 = tb + kr[0], r1 = tb + kr[1];
+    asm volatile("" : "+v"(v0), "+v"(v1), "+v"(r0), "+v"(r1));
+    u32x4 b[HT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const bf16x8 b = as_bf16x8(lds_load16(dsl + dsb + 16u * ((2u * a + hb) ^ dsq)));
-      const uint32_t v0 = a ? k10 : k00, v1 = a ? k11 : k01;
-      const uint32_t q0 = a ? r10 : r00, q1 = a ? r11 : r01;
-      auto ld = [&](int m) {
-        const uint32_t x0 = m < 16 ? (v0 + 64u * m) : (q0 ^ (64u * (m - 16)));
-        const uint32_t x1 = m < 16 ? (v1 + 64u * m) : (q1 ^ (64u * (m - 16)));
-        const u32x2 lo = lds_read_tr16(lds_ptr(x0)), hi = lds_read_tr16(lds_ptr(x1));
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-      };
-      u32x4 v[kPre];
+    for (int j = 0; j < HT; ++j) b[j] = lds_load16(dsl + 1024 * j);
+    auto ld = [&](int i) {
+      const int D = d0 + i;   // wave-uniform
+      const uint32_t x0 = D < 32 ? v0 + 32u * D : r0 ^ (32u * (D - 32));
+      const uint32_t x1 = D < 32 ? v1 + 32u * D : r1 ^ (32u * (D - 32));
+      const u32x2 lo = lds_read_tr16(lds_ptr(x0)), hi = lds_read_tr16(lds_ptr(x1));
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    u32x4 a[kPre];
 #pragma unroll
-      for (int i = 0; i < kPre; ++i) v[i] = ld(i);
+    for (int i = 0; i < kPre; ++i) a[i] = ld(i);
 #pragma unroll
-      for (int m = 0; m < kDqk / 32; ++m) {
-        const u32x4 cur = v[m % kPre];
-        if (m + kPre < kDqk / 32) v[m % kPre] = ld(m + kPre);
-        if (m < 16) mfma32x32x16_cA(acc[m], cur, as_u32x4(b));
-        else mfma32x32x16_cV(acc[m], cur, as_u32x4(b));
-        const int step = a * (kDqk / 32) + m;
-        if (copy_next) {
-          if (step % kCopyEvery == 0) gather_part<NW>(next_tile, next_src, wave, lane, step / kCopyEvery);
-          if (step == 1 || step == 3) copy_ds_part(next_ds, blk + 2, step >> 1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < DT; ++i) {
+      const u32x4 cur = a[i % kPre];
+      if (i + kPre < DT) a[i % kPre] = ld(i + kPre);
+#pragma unroll
+      for (int j = 0; j < HT; ++j) {
+        if (i * HT + j < kTilesA) mfma16x16x32_cA(acc[i][j], cur, b[j]);
+        else mfma16x16x32_cV(acc[i][j], cur, b[j]);
       }
+      if (copy_next) {
+        if (i < TC) gather_part<NW>(next_tile, next_src, wave, lane, i);
+        if (i == 1 || i == 3) copy_ds_part(next_ds, blk + 2, i >> 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   mfma_acc_drain();
-  if (!head_ok) return;
-  bf16_t* dqrow = p.dq + (int64_t)t * p.dq_stride_t + (int64_t)head * kDqk;
+  // ---- epilogue: dQ rows through LDS (64 heads at a time), then coalesced 16-byte stores.
+  // Lane holds head 16j + gi, dims 16(d0 + i) + 4g .. +3 of tile (i, j).
+  bf16_t* dq_t = p.dq + (int64_t)t * p.dq_stride_t;
 #pragma unroll
-  for (int m = 0; m < kDqk / 32; ++m) {
+  for (int half = 0; half < (HT + 3) / 4; ++half) {
+    __syncthreads();   // ring (or the previous half) no longer read
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = 32 * m + 8 * q4 + 4 * hb;
-      *reinterpret_cast<u32x2*>(dqrow + d) =
-          u32x2{pack_bf16x2(acc[m][4 * q4], acc[m][4 * q4 + 1]), pack_bf16x2(acc[m][4 * q4 + 2], acc[m][4 * q4 + 3])};
+    for (int j = 4 * half; j < HT && j < 4 * half + 4; ++j) {
+      char* row = sm.out[16 * (j - 4 * half) + gi];
+#pragma unroll
+      for (int i = 0; i < DT; ++i)
+        *reinterpret_cast<u32x2*>(row + 2 * (16 * (d0 + i) + 4 * g)) =
+            u32x2{pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+    }
+    __syncthreads();
+    const int rows = min(64, hrows - 64 * half);
+    for (int c = threadIdx.x; c < rows * (kDqk / 8); c += NW * 64) {
+      const int r = c / (kDqk / 8), q = c - r * (kDqk / 8);
+      *reinterpret_cast<u32x4*>(dq_t + (int64_t)(h0 + 64 * half + r) * kDqk + 8 * q) =
+          lds_load16(sm.out[r] + 16 * q);
     }
   }
 }
@@ -801,7 +863,10 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev) {
   if (p.topk > kMaxTopkBwd) return -2;
   if (p.g_sink_row >= INT32_MAX) return -2;   // B3 keeps G row numbers in 32 bits
-  auto mark = [&](int i) { if (ev) hipEventRecord(ev[i], stream); };
+  bool marks_ok = true;   // a failed event record is reported like a failed launch
+  auto mark = [&](int i) {
+    if (ev && hipEventRecord(ev[i], stream) != hipSuccess) marks_ok = false;
+  };
   mark(0);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
@@ -843,7 +908,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets, p.n_kv,
                      p.dkv, p.dkv_stride);
   mark(5);
-  return hipGetLastError() == hipSuccess ? 0 : -4;
+  return hipGetLastError() == hipSuccess && marks_ok ? 0 : -4;
 }
 
 }  // namespace dsa

@@ -95,12 +95,25 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   const int n_slots = max(0, min(p.topk - k_first, p.split_keys));
   const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride + k_first;
   const int kpad = (n_slots + kBK - 1) / kBK * kBK;
+  constexpr int kBatch = 8;   // index loads in flight per thread (one round trip per batch)
   int last = -1;
-  for (int j = threadIdx.x; j < kpad; j += NW * 64) {
-    int v = j < n_slots ? idx_row[j] : -1;
-    if (v < 0 || v >= p.n_kv || (p.causal && v > t)) v = -1;
-    sm.idx[j] = v;
-    if (v >= 0) last = j;
+  for (int j0 = threadIdx.x; j0 < kpad; j0 += kBatch * NW * 64) {
+    int v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int j = j0 + i * NW * 64;
+      v[i] = j < n_slots ? idx_row[j] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int j = j0 + i * NW * 64;
+      int x = v[i];
+      if (x < 0 || x >= p.n_kv || (p.causal && x > t)) x = -1;
+      if (j < kpad) {
+        sm.idx[j] = x;
+        if (x >= 0) last = j;
+      }
+    }
   }
   last = wave_max_i(last);
   if (lane == 0) sm.red[wave] = last;

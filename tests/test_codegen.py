@@ -1,11 +1,15 @@
 """Static check of the generated gfx950 code (CPU only: hipcc cross-compiles).
 
-Some MFMAs are issued through inline asm (the register-file-pinned forms in dsa_common.h); the
-compiler's hazard recognizer does not see inside asm, so those forms carry their own leading
-wait states.  This test compiles the attention kernels and checks every MFMA of the generated
-code: no VALU instruction may write one of its source registers in the 2 issue slots before it
-(the VALU-write -> MFMA-read hazard), so a compiler or code change that breaks the contract
-cannot slip through.
+Some MFMAs and the LDS-direct gathers are issued through inline asm (dsa_common.h,
+dsa_kvtile.h); the compiler's hazard recognizer does not see inside asm, so those forms carry
+their own wait states.  This test compiles the kernels and checks the generated code for the
+hazards they must cover, so a compiler or code change that breaks the contract cannot slip
+through:
+  - no VALU instruction writes a source register of an MFMA in the 2 issue slots before it;
+  - an LDS DMA (global_load_lds_*) issues at least 1 wait state after the last M0 write;
+  - a vector memory instruction reading an SGPR base issues at least 5 wait states after a
+    VALU write (v_readlane / v_readfirstlane) of that SGPR.
+The last two distances are what the compiler itself inserts for the same sequences.
 """
 import os
 import re
@@ -41,6 +45,48 @@ def _operands(line):
     if len(parts) < 2:
         return parts[0] if parts else "", []
     return parts[0], [t.strip() for t in parts[1].split(",")]
+
+
+def _sregs(tok):
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return {i for i in range(int(m.group(1)), int(m.group(2)) + 1)}
+    m = re.fullmatch(r"s(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+def _mem_violations(asm_text):
+    """M0 -> LDS DMA (1 wait state) and VALU SGPR write -> VMEM SGPR read (5 wait states)."""
+    bad = []
+    since_m0 = 99            # wait states since the last M0 write
+    since_sgpr = {}          # SGPR -> wait states since a VALU wrote it
+    func = "?"
+    for raw in asm_text.split("\n"):
+        line = raw.strip()
+        m = re.match(r"^(_Z\w+):", line)
+        if m:
+            func, since_m0, since_sgpr = m.group(1), 99, {}
+        if not line or line.startswith((";", ".", "_")) or line.endswith(":"):
+            continue
+        mn, ops = _operands(line)
+        if not mn or not re.match(r"[vsdgb]", mn):
+            continue
+        if mn.startswith("global_load_lds") and since_m0 < 1:
+            bad.append(f"{func}: `{line}` issues {since_m0} wait states after an M0 write")
+        if mn.startswith(("global_", "buffer_", "scratch_")):
+            for r in set().union(*[_sregs(o) for o in ops]) if ops else set():
+                if since_sgpr.get(r, 99) < 5:
+                    bad.append(f"{func}: `{line}` reads s{r} {since_sgpr[r]} wait states after a VALU write")
+        n = int(ops[0], 0) + 1 if mn == "s_nop" and ops else 1
+        since_m0 += n
+        for r in since_sgpr:
+            since_sgpr[r] += n
+        if ops and ops[0] == "m0":
+            since_m0 = 0
+        if mn.startswith("v_readlane") or mn.startswith("v_readfirstlane"):
+            for r in _sregs(ops[0]):
+                since_sgpr[r] = 0
+    return bad
 
 
 def _violations(asm_text):
@@ -79,7 +125,7 @@ def _violations(asm_text):
     return bad
 
 
-@pytest.mark.parametrize("src", ["dsa_sparse_fwd.hip", "dsa_sparse_bwd.hip"])
+@pytest.mark.parametrize("src", ["dsa_sparse_fwd.hip", "dsa_sparse_bwd.hip", "dsa_indexer.hip"])
 def test_no_valu_write_right_before_mfma(src, tmp_path):
     out = tmp_path / (src + ".s")
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -87,7 +133,7 @@ def test_no_valu_write_right_before_mfma(src, tmp_path):
                    capture_output=True, timeout=600)
     text = out.read_text()
     assert "v_mfma" in text
-    bad = _violations(text)
+    bad = _violations(text) + _mem_violations(text)
     assert not bad, "\n".join(bad[:20])
 
 
@@ -103,3 +149,18 @@ def test_checker_flags_a_planted_hazard():
     ])
     bad = _violations(asm)
     assert len(bad) == 2 and "v_mov_b32_e32" in bad[0] and "v_accvgpr_write_b32" in bad[1]
+
+
+def test_checker_flags_planted_memory_hazards():
+    asm = "\n".join([
+        "\tv_readlane_b32 s0, v4, 3",
+        "\tv_readlane_b32 s1, v5, 3",
+        "\ts_mov_b32 m0, s4",
+        "\tglobal_load_lds_dwordx4 v254, s[0:1]",
+        "\ts_nop 4",
+        "\ts_mov_b32 m0, s5",
+        "\ts_nop 0",
+        "\tglobal_load_lds_dwordx4 v254, s[0:1]",
+    ])
+    bad = _mem_violations(asm)
+    assert len(bad) == 3, bad   # M0 distance 0, s0 distance 2, s1 distance 1; the second load is clean
