@@ -73,26 +73,36 @@ DSA_DEV TileSrc<NW> tile_sources(const bf16_t* kv, const int32_t* idx_blk, int w
   return s;
 }
 
-// global_load_lds_dwordx4 with a scalar 64-bit row address and a per-lane byte offset.  The
-// row address comes from v_readlane (a VALU write of the SGPRs the load reads: 5 wait states)
-// and M0 is written right before the LDS DMA (1 wait state); the compiler cannot see either
-// inside the asm, so the nops are part of it.
+// global_load_lds_dwordx4 with a scalar 64-bit row address and a per-lane byte offset.  M0 is
+// written right before the LDS DMA, which reads it one wait state later (s_nop 0).  The row
+// address comes from v_readlane, a VALU write of the SGPRs the DMA reads: that needs 5 wait
+// states, which the compiler cannot see inside the asm -- callers read a row (gather_row) at
+// least one copy slot before issuing it, in an earlier scheduling group (tests/test_codegen.py
+// checks the distance in the generated code).
 DSA_DEV void copy_row16(uint32_t lds_wave_base, const char* row, uint32_t lane_off) {
-  asm volatile("s_nop 4\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(lane_off), "s"(row)
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_wave_base), "v"(lane_off), "s"(row)
                : "memory", "m0");
 }
 
-// Copy k (0 <= k < tile_copies_per_wave<NW>()) of this wave's share of a tile gather into the
-// tile at LDS byte address `tile`.  Copies 0 .. 32/NW-1 fill the V rows of keys w + NW*k
-// (row key_row(w + NW*k) = key_row(NW*k) + 2w), the rest fill rope groups.
+// Scalar source row of copy k of this wave's share of a tile gather (V copies, k < 32/NW: two
+// readlanes; rope copies use per-lane addresses and need none).
 template <int NW>
-DSA_DEV void gather_part(uint32_t tile, const TileSrc<NW>& src, int wave, int lane, int k) {
+DSA_DEV const char* gather_row(const TileSrc<NW>& src, int k) {
+  if (k >= 32 / NW) return nullptr;
+  const uint64_t a = (uint64_t)src.v;
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)a, k);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(a >> 32), k);
+  return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
+// Copy k (0 <= k < tile_copies_per_wave<NW>()) of this wave's share of a tile gather into the
+// tile at LDS byte address `tile`; `row` = gather_row(src, k), read earlier.  Copies
+// 0 .. 32/NW-1 fill the V rows of keys w + NW*k (row key_row(w + NW*k) = key_row(NW*k) + 2w),
+// the rest fill rope groups.
+template <int NW>
+DSA_DEV void gather_issue(uint32_t tile, const TileSrc<NW>& src, const char* row, int wave, int lane, int k) {
   const uint32_t w = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   if (k < 32 / NW) {
-    const uint64_t a = (uint64_t)src.v;
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)a, k);
-    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(a >> 32), k);
-    const char* row = reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
     copy_row16(tile + (key_row(NW * k) + 2 * w) * kTileVPitch, row, (uint32_t)lane * 16u);
   } else {
     const int j = k - 32 / NW;
@@ -100,12 +110,21 @@ DSA_DEV void gather_part(uint32_t tile, const TileSrc<NW>& src, int wave, int la
   }
 }
 
-// The whole gather of one tile (all of this wave's copies back to back).
+// The whole gather of one tile (all of this wave's copies back to back; rows read two copies
+// ahead, the first two behind one explicit 5-wait-state pad).
 template <int NW>
 DSA_DEV void gather_tile(uint32_t tile, const bf16_t* kv, const int32_t* idx_blk, int wave, int lane) {
+  constexpr int n = tile_copies_per_wave<NW>();
   const TileSrc<NW> src = tile_sources<NW>(kv, idx_blk, wave, lane);
+  const char* row[2] = {gather_row<NW>(src, 0), gather_row<NW>(src, 1)};
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 4");
 #pragma unroll
-  for (int k = 0; k < tile_copies_per_wave<NW>(); ++k) gather_part<NW>(tile, src, wave, lane, k);
+  for (int k = 0; k < n; ++k) {
+    gather_issue<NW>(tile, src, row[k & 1], wave, lane, k);
+    if (k + 2 < n) row[k & 1] = gather_row<NW>(src, k + 2);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 }  // namespace dsa

@@ -205,6 +205,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     const bool gather_next = blk + 2 < nblk;
     TileSrc<NW> next_src;
     if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+    // source row of the next copy, read one copy slot ahead of its issue
+    const char* next_row = gather_next ? gather_row<NW>(next_src, 0) : nullptr;
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t next_tile = tile0 + st_next;
     const uint32_t tb = tile0 + st_cur;   // 128-byte aligned: the rope XOR stays in its row
     st_cur = st_cur == 2 * kTileBytes ? 0 : st_cur + kTileBytes;
@@ -228,8 +231,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         s = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), s);
         if (ks == 0) mfma32x32x16_acc_first(dp, cur, df[0]);
         else if (ks < kDv / 16) mfma32x32x16_acc(dp, cur, df[ks]);
-        if (ks % kCopyEvery == 0 && gather_next)
-          gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
+        if (ks % kCopyEvery == 0 && gather_next) {
+          gather_issue<NW>(next_tile, next_src, next_row, wave, lane, ks / kCopyEvery);
+          next_row = gather_row<NW>(next_src, ks / kCopyEvery + 1);
+        }
         if (ks % 4 == 1 && ks < 32 && store_prev) {
           const int q = ks / 4;   // 0..7: P then dS of q4 = q / 2
           if (q & 1) *reinterpret_cast<u32x2*>(ds_row + store_j + 8 * (q >> 1)) = dw[q >> 1];
@@ -377,6 +382,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
     const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
     TileSrc<NW> next_src;
     if (copy_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+    // source row of the next tile copy, read one copy slot ahead of its issue
+    const char* next_row = copy_next ? gather_row<NW>(next_src, 0) : nullptr;
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t next_tile = tile0 + st_next * kTileBytes;
     char* const next_ds = sm.ring.ds[st_next];
     const uint32_t tb = tile0 + st * kTileBytes;   // 128-byte aligned: the rope XOR stays in its row
@@ -407,7 +415,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
         else mfma16x16x32_cV(acc[i][j], cur, b[j]);
       }
       if (copy_next) {
-        if (i < TC) gather_part<NW>(next_tile, next_src, wave, lane, i);
+        if (i < TC) {
+          gather_issue<NW>(next_tile, next_src, next_row, wave, lane, i);
+          next_row = gather_row<NW>(next_src, i + 1);
+        }
         if (i == 1 || i == 3) copy_ds_part(next_ds, blk + 2, i >> 1);
       }
       __builtin_amdgcn_sched_barrier(0);

@@ -164,6 +164,9 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       const bool gather_next = blk + 2 < nblk;
       TileSrc<NW> next_src;
       if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+      // source row of the next copy, read one copy slot ahead of its issue
+      const char* next_row = gather_next ? gather_row<NW>(next_src, 0) : nullptr;
+      __builtin_amdgcn_sched_barrier(0);
       const uint32_t next_tile = tile0 + st_next;
       // per-block absolute operand addresses (tiles are 128-byte aligned: the rope XOR below
       // only touches bits 4..6); opaque so they are not hoisted into loop-invariant VGPRs
@@ -189,8 +192,10 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
           if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
           if (ks == 0) mfma32x32x16_cV_first(sa, cur, qf[0]);
           else mfma32x32x16_cV(sa, cur, qf[ks]);
-          if (ks % kCopyEvery == 0 && gather_next)
-            gather_part<NW>(next_tile, next_src, wave, lane, ks / kCopyEvery);
+          if (ks % kCopyEvery == 0 && gather_next) {
+            gather_issue<NW>(next_tile, next_src, next_row, wave, lane, ks / kCopyEvery);
+            next_row = gather_row<NW>(next_src, ks / kCopyEvery + 1);
+          }
           __builtin_amdgcn_sched_barrier(0);
         }
         s = sa;
