@@ -48,8 +48,13 @@ DSA_DEV u32x2 lds_read_tr16(const char* p) {
 }
 
 struct FwdSmem {
-  char tile[kStages][kTileBytes];
-  int32_t idx[kMaxTopk];
+  union {
+    struct {
+      char tile[kStages][kTileBytes];
+      int32_t idx[kMaxTopk];
+    };
+    char ostage[4][32][kDv * 2];   // epilogue: each wave's 32 bf16 output rows
+  };
   int red[4];
   int redo_flag;
 };
@@ -268,23 +273,34 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
     m_ref = m_seen;
   }
 
-  // ---- epilogue: normalise, store O (bf16) and LSE (natural log)
+  // ---- epilogue: normalise, store O (bf16) and LSE (natural log).  Each wave's 32 output rows
+  // go through its own LDS slab (the tile ring and index row are dead: every wave passed the
+  // barriers above), chunk c of row r at c ^ (r & 7), so that every global store writes one
+  // whole 1 KB row (16 B per lane).  Stored straight from the accumulator layout, each store
+  // instruction would write 32 rows 16 bytes apart: 8x the L2 requests.
   mfma_acc_drain();
-  if (!head_ok) return;
   const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
-  bf16_t* optr = p.out + orow * p.out_stride_t + (int64_t)head * kDv;
+  {
+    char* slab = sm.ostage[wave][0];
+    char* mine = slab + hl * (kDv * 2);
 #pragma unroll
-  for (int m = 0; m < kDv / 32; ++m) {
+    for (int m = 0; m < kDv / 32; ++m) {
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int dv = 32 * m + 8 * q4 + 4 * hb;
-      u32x2 v;
-      v[0] = pack_bf16x2(o[m][4 * q4 + 0] * inv_l, o[m][4 * q4 + 1] * inv_l);
-      v[1] = pack_bf16x2(o[m][4 * q4 + 2] * inv_l, o[m][4 * q4 + 3] * inv_l);
-      *reinterpret_cast<u32x2*>(optr + dv) = v;
+      for (int q4 = 0; q4 < 4; ++q4) {
+        u32x2 v;
+        v[0] = pack_bf16x2(o[m][4 * q4 + 0] * inv_l, o[m][4 * q4 + 1] * inv_l);
+        v[1] = pack_bf16x2(o[m][4 * q4 + 2] * inv_l, o[m][4 * q4 + 3] * inv_l);
+        *reinterpret_cast<u32x2*>(mine + 16 * ((4 * m + q4) ^ (hl & 7)) + 8 * hb) = v;
+      }
     }
+    const int h0w = blockIdx.y * 128 + wave * 32;
+    const int rows = min(32, p.n_heads - h0w);
+    bf16_t* obase = p.out + orow * p.out_stride_t + (int64_t)h0w * kDv;
+    for (int r = 0; r < rows; ++r)
+      *reinterpret_cast<u32x4*>(obase + (int64_t)r * kDv + 8 * lane) =
+          lds_load16(slab + r * (kDv * 2) + 16 * (lane ^ (r & 7)));
   }
-  if (hb == 0) {
+  if (head_ok && hb == 0) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     p.lse[orow * p.lse_stride_t + head] = l_run > 0.f ? (m_use + __log2f(l_run)) * kLn2 : -INFINITY;
   }
