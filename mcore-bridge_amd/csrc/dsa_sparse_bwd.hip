@@ -297,7 +297,7 @@ struct DqSmem {
     char out[64][kDqPitch];             // epilogue: bf16 dQ rows of 64 heads
   };
   int32_t idx[kMaxTopkBwd];
-  int red[4];
+  int red[8];
 };
 
 template <int NW>
@@ -445,6 +445,161 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
       const int r = c / (kDqk / 8), q = c - r * (kDqk / 8);
       *reinterpret_cast<u32x4*>(dq_t + (int64_t)(h0 + 64 * half + r) * kDqk + 8 * q) =
           lds_load16(sm.out[r] + 16 * q);
+    }
+  }
+}
+
+// B2 for 64 < n_heads <= 128: 8 waves, two per SIMD.  Waves 0-3 issue the block gathers (the
+// 4-wave copy split of the KV and dS tiles) and own 5 dim tiles each (dims 80w ..), waves 4-7
+// own 4 dim tiles each and only multiply, so a copy-issuing wave stalled on its copies leaves
+// its SIMD to its partner (with one wave per SIMD those stalls cost ~30% of the block).  Every
+// wave covers all 8 head tiles: K^T fragments are read once per workgroup.  Per SIMD: 72
+// MFMAs per block.  Accumulators: 5 x 8 tiles of 16 x 16; at two waves per SIMD each register
+// file holds 128 per wave, so dim tiles 0-3 are pinned in AccVGPRs and the 5th in VGPRs.
+__global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
+  constexpr int NW = 8, NWC = 4;                 // waves; copy-issuing waves
+  constexpr int HT = 8;                          // head tiles (128 heads)
+  constexpr int DTMAX = 5;                       // dim tiles per wave (5 for waves 0-3, 4 after)
+  constexpr int TC = tile_copies_per_wave<NWC>();
+  constexpr int G = TC + 2;                      // copies per copy-issuing wave per block
+  static_assert(TC <= 2 * HT - 6, "tile copies before the dS copy slots");
+  __shared__ __attribute__((aligned(128))) DqSmem sm;
+  const int t = xcd_remap(blockIdx.x, p.total_q);
+  if (t >= p.total_q) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const bool copier = wu < NWC;
+  const int g = lane >> 4, gi = lane & 15;
+  const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
+                                       p.causal, t);
+  const int hrows = min(128, p.n_heads);
+  const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + (int64_t)t * (p.topk_pad / kBK) * p.n_heads * kBK);
+  const int64_t ds_blk = (int64_t)p.n_heads * kBK * 2;   // bytes per staged block tile
+  // dS copy k (0, 1) of copy-issuing wave w: head rows 16 * (w + 4k) .. +15 (rows past n_heads
+  // re-read row 0; never stored)
+  auto copy_ds_part = [&](char* dst, int blk, int k) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst));
+    const int i = wu + k * NWC;
+    const int h = 16 * i + (lane >> 2);
+    const int q = (lane & 3) ^ ((h >> 1) & 3);
+    const int hs = h < hrows ? h : 0;
+    async_copy16_unordered(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
+  };
+  // operand addresses as in bwd_dq_kernel
+  uint32_t kv[2], kr[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t key = 8 * g + 4 * h + (gi >> 2);
+    kv[h] = key_row(key) * kTileVPitch + 8u * (gi & 3);
+    kr[h] = kTileVBytes + key * 128u + 8u * (gi & 1) + 16u * (((gi & 3) >> 1) ^ ((key >> 1) & 7u));
+  }
+  const uint32_t ds_lane = gi * 64u + 16u * (g ^ ((gi >> 1) & 3));
+  const int d0 = copier ? DTMAX * wu : DTMAX * NWC + (DTMAX - 1) * (wu - NWC);   // first dim tile
+  const int nd = copier ? DTMAX : DTMAX - 1;
+  const uint32_t tile0 = lds_addr(sm.ring.tile[0]);
+
+  f32x4 acc[DTMAX][HT];
+#pragma unroll
+  for (int i = 0; i < DTMAX; ++i)
+#pragma unroll
+    for (int j = 0; j < HT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  mfma_acc_drain();   // zero writes of the accumulators before their first MFMA read
+
+  if (copier) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (b < nblk) {
+        gather_tile<NWC>(tile0 + b * kTileBytes, p.kv, sm.idx + b * kBK, wu, lane);
+        copy_ds_part(sm.ring.ds[b], b, 0);
+        copy_ds_part(sm.ring.ds[b], b, 1);
+      }
+    }
+  }
+  // block loop, specialised for the two wave roles (dim tiles ND; copies or not)
+  auto block_loop = [&](auto nd_c, auto copier_c) {
+    constexpr int ND = decltype(nd_c)::value;
+    constexpr bool CP = decltype(copier_c)::value;
+    int st = 0;   // ring stage of block blk
+    for (int blk = 0; blk < nblk; ++blk) {
+      if (CP) {
+        if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
+      }
+      __syncthreads();
+      // block blk+2's copies (copy-issuing waves): tile copy k at half head step k, the dS
+      // copies at half steps 10 and 12; each copy's source row is read one half step ahead
+      const bool copy_next = CP && blk + 2 < nblk;
+      const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
+      TileSrc<NWC> next_src;
+      if (copy_next) next_src = tile_sources<NWC>(p.kv, sm.idx + (blk + 2) * kBK, wu, lane);
+      const char* next_row = copy_next ? gather_row<NWC>(next_src, 0) : nullptr;
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t next_tile = tile0 + st_next * kTileBytes;
+      char* const next_ds = sm.ring.ds[st_next];
+      const uint32_t tb = tile0 + st * kTileBytes;
+      const char* dsl = sm.ring.ds[st] + ds_lane;
+      st = st == 2 ? 0 : st + 1;
+      uint32_t v0 = tb + kv[0], v1 = tb + kv[1], r0 = tb + kr[0], r1 = tb + kr[1];
+      asm volatile("" : "+v"(v0), "+v"(v1), "+v"(r0), "+v"(r1));
+      auto ld = [&](int i) {
+        const int D = d0 + i;   // wave-uniform
+        const uint32_t x0 = D < 32 ? v0 + 32u * D : r0 ^ (32u * (D - 32));
+        const uint32_t x1 = D < 32 ? v1 + 32u * D : r1 ^ (32u * (D - 32));
+        const u32x2 lo = lds_read_tr16(lds_ptr(x0)), hi = lds_read_tr16(lds_ptr(x1));
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      auto copy_slot = [&](int h) {
+        if (!CP || !copy_next) return;
+        if (h < TC) {
+          gather_issue<NWC>(next_tile, next_src, next_row, wu, lane, h);
+          next_row = gather_row<NWC>(next_src, h + 1);
+        }
+        if (h == 10 || h == 12) copy_ds_part(next_ds, blk + 2, (h - 10) >> 1);
+      };
+      // the wave's K^T fragments stay in registers; dS^T fragments stream in two head tiles ahead
+      u32x4 a[ND];
+#pragma unroll
+      for (int i = 0; i < ND; ++i) a[i] = ld(i);
+      u32x4 bq[2] = {lds_load16(dsl), lds_load16(dsl + 1024)};
+#pragma unroll
+      for (int j = 0; j < HT; ++j) {
+        const u32x4 bj = bq[j & 1];
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+          if (i < 4) mfma16x16x32_cA(acc[i][j], a[i], bj);   // 128 registers in AccVGPRs
+          else mfma16x16x32_cV(acc[i][j], a[i], bj);          // the 5th dim tile in VGPRs
+          if (i == 1) {
+            copy_slot(2 * j);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        copy_slot(2 * j + 1);
+        if (j + 2 < HT) bq[j & 1] = lds_load16(dsl + 1024 * (j + 2));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  if (copier) block_loop(std::integral_constant<int, DTMAX>{}, std::true_type{});
+  else block_loop(std::integral_constant<int, DTMAX - 1>{}, std::false_type{});
+  mfma_acc_drain();
+  // ---- epilogue: dQ rows through LDS (64 heads at a time), then coalesced 16-byte stores.
+  bf16_t* dq_t = p.dq + (int64_t)t * p.dq_stride_t;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    __syncthreads();   // ring (or the previous half) no longer read
+#pragma unroll
+    for (int j = 4 * half; j < 4 * half + 4; ++j) {
+      char* row = sm.out[16 * (j - 4 * half) + gi];
+#pragma unroll
+      for (int i = 0; i < DTMAX; ++i)
+        if (i < nd)
+          *reinterpret_cast<u32x2*>(row + 2 * (16 * (d0 + i) + 4 * g)) =
+              u32x2{pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+    }
+    __syncthreads();
+    const int rows = min(64, hrows - 64 * half);
+    for (int c = threadIdx.x; c < rows * (kDqk / 8); c += NW * 64) {
+      const int r = c / (kDqk / 8), q = c - r * (kDqk / 8);
+      *reinterpret_cast<u32x4*>(dq_t + (int64_t)(64 * half + r) * kDqk + 8 * q) = lds_load16(sm.out[r] + 16 * q);
     }
   }
 }
@@ -894,7 +1049,8 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   if (nw == 4) {
     hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);
     mark(2);
-    hipLaunchKernelGGL(bwd_dq_kernel<4>, grid, dim3(256), 0, stream, p);
+    if (grid.y == 1) hipLaunchKernelGGL(bwd_dq8_kernel, grid, dim3(512), 0, stream, p);
+    else hipLaunchKernelGGL(bwd_dq_kernel<4>, grid, dim3(256), 0, stream, p);
   } else if (nw == 2) {
     hipLaunchKernelGGL(bwd_sp_kernel<2>, grid, dim3(128), 0, stream, p);
     mark(2);

@@ -8,8 +8,11 @@ through:
   - no VALU instruction writes a source register of an MFMA in the 2 issue slots before it;
   - an LDS DMA (global_load_lds_*) issues at least 1 wait state after the last M0 write;
   - a vector memory instruction reading an SGPR base issues at least 5 wait states after a
-    VALU write (v_readlane / v_readfirstlane) of that SGPR.
-The last two distances are what the compiler itself inserts for the same sequences.
+    VALU write (v_readlane / v_readfirstlane) of that SGPR;
+  - no instruction other than an MFMA accumulating into the same registers reads an MFMA
+    result within 8 (16x16x32) / 12 (32x32x16) wait states (VALU, v_accvgpr_read, store or LDS
+    write data).
+The distances are what the compiler itself inserts for the same sequences.
 """
 import os
 import re
@@ -89,6 +92,51 @@ def _mem_violations(asm_text):
     return bad
 
 
+def _mfma_result_wait(mn):
+    return 8 if "16x16" in mn else 12
+
+
+def _result_violations(asm_text):
+    """An MFMA result read by a non-MFMA instruction before the result latency has passed."""
+    bad = []
+    pending = []   # [wait states since issue, required, dst regs, mnemonic]
+    func = "?"
+    for raw in asm_text.split("\n"):
+        line = raw.strip()
+        m = re.match(r"^(_Z\w+):", line)
+        if m:
+            func, pending = m.group(1), []
+        if not line or line.startswith((";", ".", "_")) or line.endswith(":"):
+            continue
+        mn, ops = _operands(line)
+        if not mn or not re.match(r"[vsdgb]", mn):
+            continue
+        if mn.startswith("v_mfma"):
+            srcs = set()
+            for t in ops[1:3]:
+                srcs |= _regs(t)
+            for p in pending:   # A / B operands of a later MFMA are reads too
+                if p[0] < p[1] and p[2] & srcs:
+                    bad.append(f"{func}: `{line}` reads the result of `{p[3]}` {p[0]} wait states after it")
+        else:
+            if mn.startswith(("ds_write", "global_store", "buffer_store", "scratch_store", "flat_store")):
+                srcs = set().union(*[_regs(t) for t in ops]) if ops else set()
+            elif mn.startswith(("v_", "ds_", "global_", "buffer_", "scratch_", "flat_")):
+                srcs = set().union(*[_regs(t) for t in ops[1:]]) if len(ops) > 1 else set()
+            else:
+                srcs = set()
+            for p in pending:
+                if p[0] < p[1] and p[2] & srcs:
+                    bad.append(f"{func}: `{line}` reads the result of `{p[3]}` {p[0]} wait states after it")
+        n = int(ops[0], 0) + 1 if mn == "s_nop" and ops else 1
+        for p in pending:
+            p[0] += n
+        pending = [p for p in pending if p[0] < p[1]]
+        if mn.startswith("v_mfma"):
+            pending.append([0, _mfma_result_wait(mn), _regs(ops[0]), line])
+    return bad
+
+
 def _violations(asm_text):
     bad = []
     window = []   # (slots, mnemonic, written regs) of the last instructions
@@ -133,7 +181,7 @@ def test_no_valu_write_right_before_mfma(src, tmp_path):
                    capture_output=True, timeout=600)
     text = out.read_text()
     assert "v_mfma" in text
-    bad = _violations(text) + _mem_violations(text)
+    bad = _violations(text) + _mem_violations(text) + _result_violations(text)
     assert not bad, "\n".join(bad[:20])
 
 
@@ -164,3 +212,21 @@ def test_checker_flags_planted_memory_hazards():
     ])
     bad = _mem_violations(asm)
     assert len(bad) == 3, bad   # M0 distance 0, s0 distance 2, s1 distance 1; the second load is clean
+
+
+def test_checker_flags_a_planted_result_hazard():
+    asm = "\n".join([
+        "\tv_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[4:7], a[0:3]",
+        "\tv_mfma_f32_16x16x32_bf16 a[4:7], v[0:3], v[4:7], a[4:7]",
+        "\tv_accvgpr_read_b32 v9, a1",
+        "\ts_nop 7",
+        "\tv_accvgpr_read_b32 v10, a5",
+        "\tv_mfma_f32_32x32x16_bf16 v[16:31], v[0:3], v[4:7], v[16:31]",
+        "\tv_mfma_f32_32x32x16_bf16 v[16:31], v[0:3], v[4:7], v[16:31]",
+        "\ts_nop 10",
+        "\tglobal_store_dwordx4 v40, v[16:19], off",
+    ])
+    bad = _result_violations(asm)
+    # a1 one wait state after its MFMA; the accumulation into v[16:31] is allowed; the store
+    # comes 11 wait states after the second 32x32 MFMA (12 needed); a5 is clear
+    assert len(bad) == 2 and "a1" not in bad[1] and "global_store" in bad[1], bad
