@@ -35,19 +35,118 @@ constexpr int kIdxWaveTarget = 8192;   // shrink the chunk until this many work 
 constexpr int kMaxHi = 64;          // indexer heads handled by the register tiling
 }  // namespace
 
+// bf16 scores of a workgroup whose 4 queries share a document (the same key rows): each 32-key
+// block is copied into LDS once (LDS-direct, 3-stage ring) and all 4 waves take their B
+// operands from there -- loaded per wave, every key row went through the L1 4 times and the
+// key loads alone used the CU's whole 64 B/clk load path.  Row r of a block: 16-byte unit u at
+// slot u ^ (r & 7) (8 consecutive lanes read 8 rows at one unit: conflict-free).  The loop runs
+// to the longest of the 4 rows; a wave stores only its own columns.
+template <int DI>
+DSA_DEV void indexer_block_lds(const IndexerParams& p, int t, int c0, int c1_wg, int c1, int base, float (&wr)[2][16],
+                               const u32x4 (&qa)[2][8], char* ring) {
+  constexpr int RB = DI * 2;                 // bytes per key row
+  constexpr int U = RB / 16;                 // 16-byte units per row
+  constexpr int CPB = 32 * RB / 1024;        // 1 KB copies per block (8 or 4)
+  constexpr int CPW = CPB / 4;               // per wave
+  constexpr int BLK = 32 * RB;               // bytes per staged block
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hb = lane >> 5, hl = lane & 31;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const char* kbase = reinterpret_cast<const char*>(p.k);
+  const uint32_t ring0 = lds_addr(ring);
+  auto issue = [&](int blk, int k0) {        // this wave's copies of the block at key k0
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int ci = wu * CPW + c;           // copy index within the block
+      const int r = ci * (1024 / RB) + lane / U, u = lane % U;
+      const int key = base + min(k0 + r, c1_wg - 1);
+      async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ (r & 7)),
+                             __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)((blk % 3) * BLK + ci * 1024)));
+    }
+  };
+  const int nb = (c1_wg - c0 + 31) / 32;
+  issue(0, c0);
+  if (nb > 1) issue(1, c0 + 32);
+  for (int i = 0; i < nb; ++i) {
+    if (i + 1 < nb) wait_vmcnt<CPW>(); else wait_vmcnt<0>();
+    __syncthreads();
+    if (i + 2 < nb) issue(i + 2, c0 + 32 * (i + 2));
+    const char* row = ring + (i % 3) * BLK + hl * RB;
+    u32x4 kb[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      kb[ks] = ks < DI / 16 ? lds_load16(row + 16 * ((2 * ks + hb) ^ (hl & 7))) : u32x4{0, 0, 0, 0};
+    f32x16 c0a = f32x16{}, c1a = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < DI / 16; ++ks) {
+      c0a = mfma32x32x16(as_bf16x8(qa[0][ks]), as_bf16x8(kb[ks]), c0a);
+      c1a = mfma32x32x16(as_bf16x8(qa[1][ks]), as_bf16x8(kb[ks]), c1a);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc += wr[0][e] * fmaxf(c0a[e], 0.f) + wr[1][e] * fmaxf(c1a[e], 0.f);
+    acc = xor32_sum(acc);
+    const int j = c0 + 32 * i + hl;
+    if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc;
+  }
+}
+
 template <bool FP8>
 __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
+  const int c0 = blockIdx.y * p.chunk;
+  const int Di = p.head_dim;        // 64 or 128
+  const int nks = Di / 16;          // 4 or 8 k-steps of 16
+  const int hb = lane >> 5, hl = lane & 31;
+  if (!FP8) {
+    // shared-key path: the workgroup's queries (all valid) lie in one document and the chunk
+    // is not past the longest row (workgroup-uniform decisions, before any early return)
+    const int t0 = blockIdx.x * 4;
+    bool shared = t0 + 3 < p.total_q;
+    int c1_wg = 0;
+    if (shared) {
+      const int b0 = p.row_base[t0];
+      for (int i = 0; i < 4; ++i) {
+        shared = shared && p.row_base[t0 + i] == b0;
+        c1_wg = max(c1_wg, min(p.row_len[t0 + i], c0 + p.chunk));
+      }
+    }
+    if (shared) {
+      if (c0 >= c1_wg) return;
+      __shared__ __attribute__((aligned(16))) char ring[3 * 32 * 256];
+      const int len = p.row_len[t];
+      const int c1 = min(len, c0 + p.chunk);   // this wave stores columns < c1
+      const int base = p.row_base[t];
+      float wr[2][16];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int h = 32 * mt + (i >> 2) * 8 + 4 * hb + (i & 3);
+          wr[mt][i] = h < p.n_heads ? p.w[(int64_t)t * p.n_heads + h] : 0.f;
+        }
+      }
+      const bf16_t* q = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)t * p.n_heads * Di;
+      u32x4 qa[2][8];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int h = 32 * mt + hl;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+          qa[mt][ks] = (h < p.n_heads && ks < nks) ? gload16(q + (int64_t)h * Di + 16 * ks + 8 * hb) : u32x4{0, 0, 0, 0};
+      }
+      wait_vmcnt0();   // Q and w loaded: only the ring copies are counted below
+      if (Di == 128) indexer_block_lds<128>(p, t, c0, c1_wg, c1, base, wr, qa, ring);
+      else indexer_block_lds<64>(p, t, c0, c1_wg, c1, base, wr, qa, ring);
+      return;
+    }
+  }
   if (t >= p.total_q) return;
   const int len = p.row_len[t];
-  const int c0 = blockIdx.y * p.chunk;
   if (c0 >= len) return;
   const int c1 = min(len, c0 + p.chunk);
   const int base = p.row_base[t];
-  const int hb = lane >> 5, hl = lane & 31;
-  const int Di = p.head_dim;        // 64 or 128
-  const int nks = Di / 16;          // 4 or 8 k-steps of 16
 
   // per-lane weights for the 16 head rows of each of the 2 row tiles (heads >= n_heads -> 0)
   float wr[2][16];
