@@ -993,6 +993,60 @@ __global__ void csr_fill_kernel(const int32_t* idx, int64_t idx_stride, int tota
   }
 }
 
+// The same two steps with per-workgroup LDS histograms when the keys fit in LDS: a workgroup
+// takes a run of query rows, counts its pairs per key with LDS atomics and adds the non-zero
+// counts to the global ones (one global atomic per (workgroup, key) instead of per pair); the
+// fill reserves each key's slots for the whole workgroup with one global atomic and hands them
+// out with LDS atomics.
+constexpr int kCsrLdsKeys = 16384;
+constexpr int kCsrWgs = 256;
+DSA_DEV bool csr_pair_ok(int v, int t, int n_kv, int causal) { return v >= 0 && v < n_kv && (!causal || v <= t); }
+
+__global__ __launch_bounds__(1024) void csr_count_lds_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
+                                                             int topk, int n_kv, int causal, int32_t* counts) {
+  __shared__ int32_t hist[kCsrLdsKeys];
+  for (int k = threadIdx.x; k < n_kv; k += blockDim.x) hist[k] = 0;
+  __syncthreads();
+  const int per = (total_q + gridDim.x - 1) / gridDim.x;
+  const int t0 = blockIdx.x * per, t1 = min(total_q, t0 + per);
+  for (int t = t0; t < t1; ++t)
+    for (int j = threadIdx.x; j < topk; j += blockDim.x) {
+      const int v = idx[(int64_t)t * idx_stride + j];
+      if (csr_pair_ok(v, t, n_kv, causal)) atomicAdd(hist + v, 1);
+    }
+  __syncthreads();
+  for (int k = threadIdx.x; k < n_kv; k += blockDim.x)
+    if (hist[k]) atomicAdd(counts + k, hist[k]);
+}
+
+__global__ __launch_bounds__(1024) void csr_fill_lds_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
+                                                            int topk, int n_kv, int causal, const int64_t* offsets,
+                                                            int32_t* cursor, int64_t* pair_pos) {
+  __shared__ int32_t next[kCsrLdsKeys];   // counts, then the next free slot of each key
+  for (int k = threadIdx.x; k < n_kv; k += blockDim.x) next[k] = 0;
+  __syncthreads();
+  const int per = (total_q + gridDim.x - 1) / gridDim.x;
+  const int t0 = blockIdx.x * per, t1 = min(total_q, t0 + per);
+  for (int t = t0; t < t1; ++t)
+    for (int j = threadIdx.x; j < topk; j += blockDim.x) {
+      const int v = idx[(int64_t)t * idx_stride + j];
+      if (csr_pair_ok(v, t, n_kv, causal)) atomicAdd(next + v, 1);
+    }
+  __syncthreads();
+  for (int k = threadIdx.x; k < n_kv; k += blockDim.x) {
+    const int c = next[k];
+    if (c) next[k] = (int32_t)(offsets[k] + atomicAdd(cursor + k, c));   // < 2^31: checked by the launcher
+  }
+  __syncthreads();
+  for (int t = t0; t < t1; ++t)
+    for (int j = threadIdx.x; j < topk; j += blockDim.x) {
+      const int v = idx[(int64_t)t * idx_stride + j];
+      int64_t pos = -1;
+      if (csr_pair_ok(v, t, n_kv, causal)) pos = atomicAdd(next + v, 1);
+      pair_pos[(int64_t)t * topk + j] = pos;
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // B5: dKV[s] = sum of G rows in s's segment (fp32).  One workgroup (288 threads) per key:
 // 4 row lanes x 72 chunks of 8 dims.
@@ -1040,11 +1094,21 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   hipLaunchKernelGGL(zero_i32_kernel, dim3((p.n_kv + 255) / 256), dim3(256), 0, stream, p.csr_counts, p.n_kv);
   const int64_t pairs = (int64_t)p.total_q * p.topk;
   const int nb = (int)std::min<int64_t>((pairs + 255) / 256, 65536);
-  hipLaunchKernelGGL(csr_count_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
-                     p.n_kv, p.causal, p.csr_counts);
+  const bool lds_csr = p.n_kv <= kCsrLdsKeys;
+  const int nwg = std::max(1, std::min(kCsrWgs, p.total_q));
+  if (lds_csr)
+    hipLaunchKernelGGL(csr_count_lds_kernel, dim3(nwg), dim3(1024), 0, stream, p.idx, p.idx_stride, p.total_q,
+                       p.topk, p.n_kv, p.causal, p.csr_counts);
+  else
+    hipLaunchKernelGGL(csr_count_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
+                       p.n_kv, p.causal, p.csr_counts);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, p.csr_counts, p.n_kv, p.csr_offsets);
-  hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
-                     p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
+  if (lds_csr)
+    hipLaunchKernelGGL(csr_fill_lds_kernel, dim3(nwg), dim3(1024), 0, stream, p.idx, p.idx_stride, p.total_q,
+                       p.topk, p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
+  else
+    hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
+                       p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
   mark(1);
   if (nw == 4) {
     hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);
