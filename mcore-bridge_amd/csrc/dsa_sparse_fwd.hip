@@ -6,23 +6,29 @@
 //   lse[t,h] = ln sum_j exp(scale * q[t,h] . kv[idx[t,j]])
 //
 // Work decomposition (one workgroup = one query token, up to 128 heads):
-//   * wave w owns 32 heads.  Q[32 heads x 576] sits in registers for the whole key loop (the B
-//     operand of S^T = K . Q^T, 144 VGPRs), the output accumulator O^T[512 x 32 heads] in fp32
-//     (256 AGPRs).  Keeping O transposed puts all accumulators of one lane on a single head.
+//   * wave w owns 32 heads for the scores.  Q[32 heads x 576] sits in registers for the whole
+//     key loop (the B operand of S^T = K . Q^T, 144 VGPRs).
 //   * the query's index row is staged once in LDS; selected KV rows are gathered 32 at a time
 //     straight into LDS with global_load_lds (16 B per lane, no VGPR staging, swizzled tile of
-//     dsa_kvtile.h) through a 3-stage ring, so block j+2 streams in while block j is
-//     multiplied.  The copies are issued through inline asm, one every few QK MFMAs, and
-//     completed with explicit s_waitcnt vmcnt(G) + barrier (every wave issues the same G copies
-//     per block).
-//   * QK: 36 MFMA 32x32x16 per 32-key block, A operands prefetched 3 MFMAs ahead;
-//     PV: O^T += V^T . P^T, V^T from ds_read_b64_tr_b16 (hardware 16-bit transpose on the LDS
-//     read), P^T is the S^T accumulator converted to bf16 in place (the k order inside each
-//     MFMA is permuted to match the S^T C layout, so no shuffle is needed).
-//   * softmax in the exp2 domain against a per-head reference max fixed by the first valid
-//     block (2^64 headroom), so the O accumulators are never rescaled (a rescale would pull the
-//     256 AGPR accumulators through VGPRs).  A query whose scores overshoot the headroom is
-//     recomputed once with its exact row max.
+//     dsa_kvtile.h) through a 3-stage ring.  The copies are issued through inline asm, one
+//     every few QK MFMAs, and completed with an explicit s_waitcnt vmcnt(0) + barrier.
+//   * QK: 36 MFMA 32x32x16 per 32-key block, A operands prefetched 3 MFMAs ahead.
+//   * PV is split by latent dims: wave w accumulates O^T[128 dims x all 128 heads] in fp32
+//     (256 AGPRs), so each wave reads a quarter of the V^T tile (ds_read_b64_tr_b16, the
+//     hardware 16-bit transpose on the LDS read) instead of all of it.  Its B operand P^T comes
+//     from every wave through LDS: each wave writes its converted S^T accumulator (the k order
+//     inside each MFMA is permuted to match the S^T C layout, so no shuffle is needed), lane for
+//     lane in the MFMA B layout.
+//   * software pipeline: iteration j runs QK of block j, then PV of block j-1 with block j's
+//     softmax interleaved between the PV MFMAs (one exp per MFMA), so the softmax VALU work
+//     issues while the matrix pipe is busy.  Tiles j and j-1 are live, block j+1 is gathered
+//     into the third ring slot during QK(j).
+//   * softmax in the exp2 domain against a per-head reference max fixed by the first block
+//     holding a valid key (2^64 headroom), so the O accumulators are never rescaled (a rescale
+//     would pull the 256 AGPR accumulators through VGPRs).  A query whose scores overshoot the
+//     headroom is recomputed once with its exact row max.  Row sums and overshoot maxima stay
+//     per lane (one half of a head's keys) until the end of the pass: no cross-lane traffic
+//     per block.
 #include "dsa_common.h"
 #include "dsa_kernels.h"
 #include "dsa_kvtile.h"
@@ -51,12 +57,14 @@ struct FwdSmem {
   union {
     struct {
       char tile[kStages][kTileBytes];
+      u32x4 pbuf[2][8][64];   // P^T fragments of the last two blocks: [block & 1][2 * wave + a][lane]
       int32_t idx[kMaxTopk];
     };
-    char ostage[4][32][kDv * 2];   // epilogue: each wave's 32 bf16 output rows
+    char ostage[128][kDv * 2];   // epilogue: the workgroup's 128 bf16 output rows
   };
   int red[4];
   int redo_flag;
+  float inv_l[128];
 };
 
 }  // namespace
@@ -150,37 +158,90 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   }
   const uint32_t tile0 = lds_addr(sm.tile[0]);
 
-  // Register files: O^T (256) is pinned in AccVGPRs and S^T in VGPRs through constrained MFMAs
-  // (left to itself the allocator parks S^T in AccVGPRs and moves an O tile out and back
-  // every block).
+  // PV, split by latent dims: wave w accumulates O^T[dims DT*32*w .. +DT*32) x all NH*32 heads]
+  // (o[m' * NH + n] = dim tile m', head tile n) from its own quarter of the V^T tile and the
+  // P^T fragments of every wave, exchanged through LDS (lane-for-lane the MFMA B layout).  Each
+  // wave then reads 512/NW dims of V^T per block instead of all 512.
+  constexpr int DT = 16 / NW, NH = NW;
+  const uint32_t pbuf0 = lds_addr(&sm.pbuf[0][0][0]);
+  const uint32_t pv_dim0 = 64u * DT * wave;   // byte offset of this wave's first dim tile
+  auto pf_addr = [&](int parity, int n, int aa) {
+    return const_cast<char*>(lds_ptr(pbuf0 + (uint32_t)(((parity * 8 + 2 * n + aa) * 64 + lane) * 16)));
+  };
+  // O^T += V^T . P^T for one block of the tile at LDS address tp, P^T fragments of every wave in
+  // slot `parity`; the two 16-key halves run one after the other, each holding its NH P^T
+  // fragments while the V^T fragments stream (kPre ahead).  step(i) runs in the scheduling
+  // group of PV MFMA i, so independent VALU work issues while the matrix pipe is busy.
+  auto pv_block = [&](uint32_t tp, int parity, auto&& step) {
+    uint32_t r00 = tp + pv[0][0] + pv_dim0, r01 = tp + pv[0][1] + pv_dim0;
+    uint32_t r10 = tp + pv[1][0] + pv_dim0, r11 = tp + pv[1][1] + pv_dim0;
+    asm volatile("" : "+v"(r00), "+v"(r01), "+v"(r10), "+v"(r11));
+    auto vread = [&](int f) {   // V^T fragment f = DT * a + m'
+      const int aa = f / DT, mm = f % DT;
+      const uint32_t b0 = aa ? r10 : r00, b1 = aa ? r11 : r01;
+      const u32x2 lo = lds_read_tr16(lds_ptr(b0 + 64u * mm)), hi = lds_read_tr16(lds_ptr(b1 + 64u * mm));
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    constexpr int NF = 2 * DT;
+    u32x4 v[kPre];
+    u32x4 pfa[NH];
+#pragma unroll
+    for (int n = 0; n < NH; ++n) pfa[n] = lds_load16(pf_addr(parity, n, 0));
+#pragma unroll
+    for (int f = 0; f < kPre; ++f) v[f] = vread(f);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if (f == DT) {
+#pragma unroll
+        for (int n = 0; n < NH; ++n) pfa[n] = lds_load16(pf_addr(parity, n, 1));
+      }
+      const u32x4 cur = v[f % kPre];
+      if (f + kPre < NF) v[f % kPre] = vread(f + kPre);
+#pragma unroll
+      for (int n = 0; n < NH; ++n) {
+        mfma32x32x16_cA(o[(f % DT) * NH + n], cur, pfa[n]);
+        step(f * NH + n);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // Software pipeline: iteration blk multiplies S^T of block blk (QK), then runs the PV product
+  // of block blk-1 with block blk's softmax interleaved between its MFMAs.  Two tiles are live
+  // per iteration (blk, blk-1), so block blk+1 is gathered into the third ring slot during
+  // iteration blk's QK MFMAs.  Iteration 0 multiplies tile 0 by P = 0 in place of block -1.
+  // The reference max of every head is fixed by the first block holding a valid key (a
+  // wave-uniform event: validity is per key, shared by all heads); row sums and the overshoot
+  // maxima stay per lane (one half of a head's keys) until the end of the pass.
+  bool m_set = false;
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int m = 0; m < kDv / 32; ++m) o[m] = f32x16{};
     mfma_acc_drain();
     l_run = 0.f;
     if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
-    if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
-
-    uint32_t st_cur = 0, st_next = 2 * kTileBytes;   // ring byte offsets of blocks blk, blk+2
+    // block -1's P^T slot holds zeros (iteration 0 multiplies tile 0 by it)
+    lds_store16(pf_addr(1, wave, 0), u32x4{0, 0, 0, 0});
+    lds_store16(pf_addr(1, wave, 1), u32x4{0, 0, 0, 0});
+    uint32_t st_cur = 0, st_prev = 0;   // ring byte offsets of blocks blk and blk-1
     for (int blk = 0; blk < nblk; ++blk) {
-      if (blk + 1 < nblk) wait_vmcnt<G>(); else wait_vmcnt<0>();
+      wait_vmcnt<0>();
       __syncthreads();
-      // block blk+2's gather is issued one copy per kCopyEvery QK MFMAs below
-      const bool gather_next = blk + 2 < nblk;
+      const uint32_t st_next = st_cur == 2 * kTileBytes ? 0 : st_cur + kTileBytes;
+      // block blk+1's gather is issued one copy per kCopyEvery QK MFMAs below
+      const bool gather_next = blk + 1 < nblk;
       TileSrc<NW> next_src;
-      if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+      if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 1) * kBK, wave, lane);
       // source row of the next copy, read one copy slot ahead of its issue
       const char* next_row = gather_next ? gather_row<NW>(next_src, 0) : nullptr;
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t next_tile = tile0 + st_next;
       // per-block absolute operand addresses (tiles are 128-byte aligned: the rope XOR below
       // only touches bits 4..6); opaque so they are not hoisted into loop-invariant VGPRs
-      const uint32_t tb = tile0 + st_cur;
-      st_cur = st_cur == 2 * kTileBytes ? 0 : st_cur + kTileBytes;
-      st_next = st_next == 2 * kTileBytes ? 0 : st_next + kTileBytes;
+      const uint32_t tb = tile0 + st_cur, tp = tile0 + st_prev;
+      st_prev = st_cur;
+      st_cur = st_next;
       uint32_t qv = tb + qk_v, qr = tb + qk_r;
-      uint32_t pv00 = tb + pv[0][0], pv01 = tb + pv[0][1], pv10 = tb + pv[1][0], pv11 = tb + pv[1][1];
-      asm volatile("" : "+v"(qv), "+v"(qr), "+v"(pv00), "+v"(pv01), "+v"(pv10), "+v"(pv11));
+      asm volatile("" : "+v"(qv), "+v"(qr));
       const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
       // ---- S^T[32 keys x 32 heads] = K . Q^T  (A operands prefetched)
@@ -216,52 +277,42 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
           if (!((vmask >> key) & 1u)) s[i] = -INFINITY;
         }
       }
-      float bmax = s[0];
+      if (!m_set && vmask != 0u) {   // both row halves of a head take the same reference
+        float bm = s[0];
 #pragma unroll
-      for (int i = 1; i < 16; ++i) bmax = fmaxf(bmax, s[i]);
-      bmax = xor32_max(bmax) * p.scale_log2;
-      m_seen = fmaxf(m_seen, bmax);
-      if (m_ref == -INFINITY) m_ref = bmax;          // O and l are still zero for this head
-      const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-      float rs = 0.f;
-      u32x4 pb[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          // no clamp: an exponent above kHeadroom means m_seen > m_ref + kHeadroom, and the
-          // whole row is then recomputed against its true maximum (inf/NaN here is discarded)
-          const float p0 = fast_exp2(__builtin_fmaf(s[a * 8 + e], p.scale_log2, -m_use));
-          const float p1 = fast_exp2(__builtin_fmaf(s[a * 8 + e + 1], p.scale_log2, -m_use));
-          rs += p0 + p1;
-          pb[a][e >> 1] = pack_bf16x2(p0, p1);
-        }
+        for (int i = 1; i < 16; ++i) bm = fmaxf(bm, s[i]);
+        m_ref = xor32_max(bm) * p.scale_log2;
+        m_set = true;
       }
-      l_run += xor32_sum(rs);
-
-      // ---- O^T[512 x 32 heads] += V^T . P^T   (V^T via transposing LDS reads, prefetched)
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const uint32_t r0 = a ? pv10 : pv00, r1 = a ? pv11 : pv01;
-        const bf16x8 b = as_bf16x8(pb[a]);
-        u32x4 v[kPre];
-#pragma unroll
-        for (int i = 0; i < kPre; ++i) {
-          const u32x2 lo = lds_read_tr16(lds_ptr(r0 + 64u * i)), hi = lds_read_tr16(lds_ptr(r1 + 64u * i));
-          v[i] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      const float m_use = m_set ? m_ref : 0.f;
+      float bm0 = 0.f, bm1 = 0.f, rs = 0.f, p_even = 0.f;
+      u32x4 pb_new[2];
+      // no clamp: an exponent above kHeadroom means m_seen > m_ref + kHeadroom, and the whole
+      // row is then recomputed against its true maximum (inf/NaN here is discarded)
+      auto softmax_step = [&](int i) {
+        if (i == 0)
+          bm0 = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+        if (i == 1)
+          bm1 = fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])), fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15])));
+        if (i == 2) m_seen = fmaxf(m_seen, fmaxf(bm0, bm1) * p.scale_log2);
+        if (i >= 4 && i < 20) {   // one exp per PV MFMA
+          const int e = i - 4;
+          const float pe = fast_exp2(__builtin_fmaf(s[e], p.scale_log2, -m_use));
+          rs += pe;
+          if (e & 1) pb_new[e >> 3][(e & 7) >> 1] = pack_bf16x2(p_even, pe);
+          else p_even = pe;
         }
-#pragma unroll
-        for (int m = 0; m < kDv / 32; ++m) {
-          const u32x4 cur = v[m % kPre];
-          if (m + kPre < kDv / 32) {
-            const u32x2 lo = lds_read_tr16(lds_ptr(r0 + 64u * (m + kPre)));
-            const u32x2 hi = lds_read_tr16(lds_ptr(r1 + 64u * (m + kPre)));
-            v[m % kPre] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-          }
-          mfma32x32x16_cA(o[m], cur, as_u32x4(b));
-          __builtin_amdgcn_sched_barrier(0);
+        if (i == 21) {   // publish block blk's P^T fragments (read after the next barrier)
+          lds_store16(pf_addr(blk & 1, wave, 0), pb_new[0]);
+          lds_store16(pf_addr(blk & 1, wave, 1), pb_new[1]);
         }
-      }
+      };
+      pv_block(tp, (blk + 1) & 1, softmax_step);   // block blk-1's P^T slot
+      l_run += rs;
+    }
+    if (nblk > 0) {
+      __syncthreads();   // the last block's P^T fragments of every wave
+      pv_block(tile0 + st_prev, (nblk - 1) & 1, [](int) {});
     }
     // ---- did any head overshoot its reference?  (workgroup-uniform decision)
     const bool over = m_seen > m_ref + kHeadroom;
@@ -270,29 +321,39 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
     if (__any(over) && lane == 0) sm.redo_flag = 1;
     __syncthreads();
     if (!sm.redo_flag) break;
-    m_ref = m_seen;
+    m_ref = xor32_max(m_seen);
   }
+  l_run = xor32_sum(l_run);
 
-  // ---- epilogue: normalise, store O (bf16) and LSE (natural log).  Each wave's 32 output rows
-  // go through its own LDS slab (the tile ring and index row are dead: every wave passed the
-  // barriers above), chunk c of row r at c ^ (r & 7), so that every global store writes one
-  // whole 1 KB row (16 B per lane).  Stored straight from the accumulator layout, each store
-  // instruction would write 32 rows 16 bytes apart: 8x the L2 requests.
+  // ---- epilogue: normalise, store O (bf16) and LSE (natural log).  The output rows go
+  // through LDS (the tile ring, P^T slots and index row are dead: every wave passed the
+  // barriers above): wave w writes its dims of every head row, chunk c of row r at c ^ (r & 7),
+  // then stores its own 32 rows, one whole 1 KB row (16 B per lane) per store instruction.
+  // Stored straight from the accumulator layout, each store would write 32 rows 16 bytes
+  // apart: 8x the L2 requests.
   mfma_acc_drain();
-  const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
+  if (hb == 0) sm.inv_l[wave * 32 + hl] = l_run > 0.f ? 1.f / l_run : 0.f;
+  __syncthreads();
   {
-    char* slab = sm.ostage[wave][0];
-    char* mine = slab + hl * (kDv * 2);
 #pragma unroll
-    for (int m = 0; m < kDv / 32; ++m) {
+    for (int n = 0; n < NH; ++n) {
+      const float inv_l = sm.inv_l[32 * n + hl];
+      char* mine = sm.ostage[32 * n + hl];
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        u32x2 v;
-        v[0] = pack_bf16x2(o[m][4 * q4 + 0] * inv_l, o[m][4 * q4 + 1] * inv_l);
-        v[1] = pack_bf16x2(o[m][4 * q4 + 2] * inv_l, o[m][4 * q4 + 3] * inv_l);
-        *reinterpret_cast<u32x2*>(mine + 16 * ((4 * m + q4) ^ (hl & 7)) + 8 * hb) = v;
+      for (int mm = 0; mm < DT; ++mm) {
+        const f32x16& acc = o[mm * NH + n];
+        const int m = DT * wave + mm;   // dim tile: dims 32m .. 32m+31
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          u32x2 v;
+          v[0] = pack_bf16x2(acc[4 * q4 + 0] * inv_l, acc[4 * q4 + 1] * inv_l);
+          v[1] = pack_bf16x2(acc[4 * q4 + 2] * inv_l, acc[4 * q4 + 3] * inv_l);
+          *reinterpret_cast<u32x2*>(mine + 16 * ((4 * m + q4) ^ (hl & 7)) + 8 * hb) = v;
+        }
       }
     }
+    __syncthreads();
+    const char* slab = sm.ostage[wave * 32];
     const int h0w = blockIdx.y * 128 + wave * 32;
     const int rows = min(32, p.n_heads - h0w);
     bf16_t* obase = p.out + orow * p.out_stride_t + (int64_t)h0w * kDv;
