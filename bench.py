@@ -10,7 +10,8 @@ value = algorithmic FLOPs of the step / step time:
   sparse fwd 2176*H*N_sel + sparse bwd 5504*H*N_sel + indexer 2*Di*Hi*N_pairs
 (N_sel = sum_q min(K, visible keys) = 27,602,695; N_pairs = causally visible pairs).
 The line also carries a "decode" object for configs[4] (cfg5), whose bound is HBM: gather
-bytes of the selected cache rows / decode attention time.
+bytes of the selected cache rows / decode attention time, and an "indexer_prologue" object
+(the fused producer of the indexer's inputs at the cfg3 token count, HBM-bound).
 """
 from __future__ import annotations
 
@@ -166,6 +167,56 @@ def decode_leg(torch, dev, reps: int = 50):
     }
 
 
+def prologue_leg(torch, dev, reps: int = 50):
+    """Indexer prologue (the producer of the indexer's q, k, w; reference forward_before_topk,
+    patcher.py:268-300) at the cfg3 token count: T = 16384, Hi = 64, Di = 128, through the C ABI
+    with preallocated buffers, bf16 and fp8 outputs.  One pass over the projected rows, HBM-bound:
+    algorithmic bytes = q_lin + k_lin + w_lin + freqs read once + q, k (+ scales) + w written."""
+    from mcore_bridge_amd import _lib
+    T, Hi = 16384, 64
+    g = torch.Generator(device=dev).manual_seed(5)
+    q_lin = (torch.randn(T, Hi * 128, generator=g, device=dev) * 2).bfloat16()
+    k_lin = (torch.randn(T, 128, generator=g, device=dev) * 2).bfloat16()
+    w_lin = torch.randn(T, Hi, generator=g, device=dev).bfloat16()
+    lw = torch.ones(128, device=dev)
+    lb = torch.zeros(128, device=dev)
+    inv = 1.0 / (10000 ** (torch.arange(0, 64, 2, dtype=torch.float32, device=dev) / 64))
+    ang = torch.arange(T, dtype=torch.float32, device=dev)[:, None] * inv
+    fr = torch.cat([ang, ang], -1).contiguous()
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    res = {"workload": "indexer prologue at cfg3 size: T=16384 tokens, Hi=64, Di=128, rope 64 (LayerNorm + "
+                       "partial RoPE + 128-point Hadamard + head weights, one fused pass; projections excluded)"}
+    for fp8 in (False, True):
+        odt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+        q = torch.empty(T, Hi, 128, dtype=odt, device=dev)
+        k = torch.empty(T, 128, dtype=odt, device=dev)
+        w = torch.empty(T, Hi, dtype=torch.float32, device=dev)
+        qs = torch.empty(T, Hi, dtype=torch.float32, device=dev)
+        ks = torch.empty(T, dtype=torch.float32, device=dev)
+        args = (q_lin.data_ptr(), Hi * 128, k_lin.data_ptr(), 128, w_lin.data_ptr(), Hi, lw.data_ptr(), lb.data_ptr(),
+                fr.data_ptr(), 64, T, Hi, 128, 64, 1e-6, 1.0, Hi ** -0.5, 128 ** -0.5, 0, 0,
+                _lib.DSA_FP8_E4M3 if fp8 else _lib.DSA_BF16, q.data_ptr(), qs.data_ptr(), k.data_ptr(),
+                ks.data_ptr(), w.data_ptr(), stream)
+        for _ in range(3):
+            _lib.check("dsa_indexer_prologue", lib.dsa_indexer_prologue(*args))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            lib.dsa_indexer_prologue(*args)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        ob = 1 if fp8 else 2
+        nbytes = (T * Hi * 128 * 2 + T * 128 * 2 + T * Hi * 2 + T * 64 * 4
+                  + T * Hi * 128 * ob + T * 128 * ob + T * Hi * 4 + (T * Hi * 4 + T * 4 if fp8 else 0))
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res["fp8" if fp8 else "bf16"] = {"us": round(us, 2), "bytes": nbytes, "GBs": round(gbs, 1),
+                                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -315,6 +366,9 @@ def main():
     if not args.no_decode:
         res["decode"] = decode_leg(torch, dev)
         print(f"[bench] decode leg done: {res['decode']['attention_us']} us", file=sys.stderr, flush=True)
+    if not args.no_decode:
+        res["indexer_prologue"] = prologue_leg(torch, dev)
+        print(f"[bench] prologue leg done: {res['indexer_prologue']['bf16']['us']} us", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(res), flush=True)

@@ -63,6 +63,32 @@ const char* dsa_strerror(int status);
 int dsa_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal,
                    int32_t* row_base, int32_t* row_len, void* stream);
 
+/* Lightning-indexer prologue: the tail of DSAIndexer.forward_before_topk after its three
+ * projections (reference src/mcore_bridge/patcher.py:268-300, RoPE helper _apply_rope
+ * patcher.py:304-324 over the patched _apply_rotary_pos_emb_bshd,
+ * src/mcore_bridge/model/modules/transformer_layer.py:240-278), fused into one pass:
+ *   k = LayerNorm(k_lin; ln_weight, ln_bias, eps)                      (patcher.py:281-282)
+ *   RoPE on dims [0, 64) of every q and k row: optional de-interleave (rope_deinterleave =
+ *   dsa_indexer_rotary_interleaved), half-split or interleaved rotate_half (rotary_interleaved =
+ *   config.rotary_interleaved), cos/sin of freqs scaled by mscale; bf16 rounding as the
+ *   reference's bf16 ops (patcher.py:275,287)
+ *   q, k = normalised 128-point Walsh-Hadamard transform (rotate_activation, patcher.py:292-293)
+ *   w_out = w_lin * w_scale_heads * w_scale_softmax, rounded to bf16 after each product
+ *   (patcher.py:299-300: Hi^-0.5 and softmax_scale = Di^-0.5)
+ * q_lin [total_q, n_heads, 128] (token stride q_stride_t), k_lin [total_q, 128], w_lin [total_q,
+ * n_heads], bf16; ln_weight, ln_bias [128] fp32; freqs [total_q, 64] fp32 rotary angles.
+ * out_dtype DSA_BF16: q_out [total_q, n_heads, 128], k_out [total_q, 128] bf16.  DSA_FP8_E4M3:
+ * OCP e4m3fn with one absmax scale per row, q_scale [total_q, n_heads], k_scale [total_q]
+ * (x = x8 * scale, scale = absmax / 448), the fp8 input layout of dsa_indexer_scores.
+ * w_out [total_q, n_heads] fp32.  n_heads <= 64, head_dim = 128, rope_dim = 64 (the reference's
+ * x_pe split is its RoPE width only when head_dim = 2 * rope_dim). */
+int dsa_indexer_prologue(const void* q_lin, int64_t q_stride_t, const void* k_lin, int64_t k_stride_t,
+                         const void* w_lin, int64_t w_stride_t, const float* ln_weight, const float* ln_bias,
+                         const float* freqs, int64_t freqs_stride_t, int total_q, int n_heads, int head_dim,
+                         int rope_dim, float eps, float mscale, float w_scale_heads, float w_scale_softmax,
+                         int rope_deinterleave, int rotary_interleaved, int out_dtype, void* q_out,
+                         float* q_scale, void* k_out, float* k_scale, float* w_out, void* stream);
+
 /* Lightning-indexer scores (scoring half of fused_qk_topk_naive, patcher.py:358):
  *   scores[t, j] = sum_h w[t,h] * relu(q[t,h,:] . k[row_base[t] + j, :]),  j < row_len[t].
  * q [total_q, n_heads, head_dim], k [n_k, head_dim] in bf16 or OCP e4m3fn (then q_scale

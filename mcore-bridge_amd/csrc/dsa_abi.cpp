@@ -86,6 +86,42 @@ int dsa_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal
   return dsa::launch_build_rows(cu_seqlens, n_seq, total_q, causal, row_base, row_len, as_stream(stream));
 }
 
+int dsa_indexer_prologue(const void* q_lin, int64_t q_stride_t, const void* k_lin, int64_t k_stride_t,
+                         const void* w_lin, int64_t w_stride_t, const float* ln_weight, const float* ln_bias,
+                         const float* freqs, int64_t freqs_stride_t, int total_q, int n_heads, int head_dim,
+                         int rope_dim, float eps, float mscale, float w_scale_heads, float w_scale_softmax,
+                         int rope_deinterleave, int rotary_interleaved, int out_dtype, void* q_out,
+                         float* q_scale, void* k_out, float* k_scale, float* w_out, void* stream) {
+  if (total_q < 0 || n_heads < 1 || !(eps >= 0.f) || !std::isfinite(mscale) || !std::isfinite(w_scale_heads) ||
+      !std::isfinite(w_scale_softmax))
+    return DSA_ERR_INVALID_ARG;
+  if (n_heads > 64 || head_dim != 128 || rope_dim != 64) return DSA_ERR_UNSUPPORTED;
+  if (out_dtype != DSA_BF16 && out_dtype != DSA_FP8_E4M3) return DSA_ERR_UNSUPPORTED;
+  const bool fp8 = out_dtype == DSA_FP8_E4M3;
+  if (total_q == 0) return DSA_OK;
+  if (!q_lin || !k_lin || !w_lin || !ln_weight || !ln_bias || !freqs || !q_out || !k_out || !w_out)
+    return DSA_ERR_INVALID_ARG;
+  if (fp8 && (!q_scale || !k_scale)) return DSA_ERR_INVALID_ARG;
+  // rows are read and written as 2-element words
+  if (q_stride_t < (int64_t)n_heads * head_dim || k_stride_t < head_dim || w_stride_t < n_heads ||
+      freqs_stride_t < rope_dim || (q_stride_t & 1) || (k_stride_t & 1))
+    return DSA_ERR_INVALID_ARG;
+  auto al4 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 3u) == 0; };
+  if (!al4(q_lin) || !al4(k_lin) || !al4(q_out) || !al4(k_out)) return DSA_ERR_INVALID_ARG;
+  dsa::PrologueParams p{};
+  p.q_lin = static_cast<const dsa::bf16_t*>(q_lin);
+  p.k_lin = static_cast<const dsa::bf16_t*>(k_lin);
+  p.w_lin = static_cast<const dsa::bf16_t*>(w_lin);
+  p.ln_w = ln_weight; p.ln_b = ln_bias; p.freqs = freqs;
+  p.q_out = q_out; p.q_scale = q_scale; p.k_out = k_out; p.k_scale = k_scale; p.w_out = w_out;
+  p.total_q = total_q; p.n_heads = n_heads;
+  p.deinterleave = rope_deinterleave ? 1 : 0; p.rotary_interleaved = rotary_interleaved ? 1 : 0;
+  p.out_fp8 = fp8 ? 1 : 0;
+  p.eps = eps; p.mscale = mscale; p.w_scale_heads = w_scale_heads; p.w_scale_softmax = w_scale_softmax;
+  p.q_stride_t = q_stride_t; p.k_stride_t = k_stride_t; p.w_stride_t = w_stride_t; p.freqs_stride_t = freqs_stride_t;
+  return dsa::launch_indexer_prologue(p, as_stream(stream));
+}
+
 int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const void* k, int k_dtype,
                        const float* k_scale, const float* w, const int32_t* row_base, const int32_t* row_len,
                        int total_q, int n_k, int n_heads, int head_dim, int max_row_len, float* scores,

@@ -70,11 +70,29 @@ struct TopkParams {
   int64_t pitch;
 };
 
+struct PrologueParams {
+  const bf16_t* q_lin;  // [total_q, n_heads, 128] = wq_b(qr), token stride q_stride_t
+  const bf16_t* k_lin;  // [total_q, 128] = wk(x), token stride k_stride_t
+  const bf16_t* w_lin;  // [total_q, n_heads] = weights_proj(x), token stride w_stride_t
+  const float* ln_w;    // [128] k_norm weight
+  const float* ln_b;    // [128] k_norm bias
+  const float* freqs;   // [total_q, 64] rotary angles, token stride freqs_stride_t
+  void* q_out;          // [total_q, n_heads, 128] bf16 or e4m3fn
+  float* q_scale;       // [total_q, n_heads] (fp8 only)
+  void* k_out;          // [total_q, 128] bf16 or e4m3fn
+  float* k_scale;       // [total_q] (fp8 only)
+  float* w_out;         // [total_q, n_heads] fp32 (values exact in bf16)
+  int total_q, n_heads, deinterleave, rotary_interleaved, out_fp8;
+  float eps, mscale, w_scale_heads, w_scale_softmax;
+  int64_t q_stride_t, k_stride_t, w_stride_t, freqs_stride_t;
+};
+
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
 // ev (nullable): 6 events recorded around the stages B4 | B1 | B2 | B3 | B5.
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev);
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
+int launch_indexer_prologue(const PrologueParams& p, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
                           bf16_t* out, float* lse, hipStream_t stream);
 int launch_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,

@@ -11,8 +11,12 @@ that DSAttention runs on the indexer output (call site
 src/mcore_bridge/model/modules/multi_latent_attention.py:262-270): one shared 576-wide latent KV
 head, ``v = kv[..., :512]``, causal ``triu`` mask applied on top of the index mask.
 
-Both run entirely in the HIP kernels of libdsa_amd.so; torch ops here only reshape, cast and
-reorder indices.
+``indexer_forward_before_topk`` is the indexer's producer, reference
+``DSAIndexer.forward_before_topk`` (src/mcore_bridge/patcher.py:245-302): the three projections
+run as plain GEMMs (hipBLASLt through torch), everything after them in one fused HIP pass.
+
+All of them run in the HIP kernels of libdsa_amd.so; torch ops here only reshape, cast,
+reorder indices and (for the projections) multiply matrices.
 """
 from __future__ import annotations
 
@@ -103,3 +107,37 @@ def sparse_mla_attention(query: Tensor, kv: Tensor, topk_indices: Tensor, softma
     idx = torch.where(ti >= 0, ti + off, torch.full_like(ti, -1)).reshape(B * S, -1).to(torch.int32)
     out = ops.sparse_mla(q_thd, kv_thd, idx, softmax_scale, causal)     # [B*S, H, 512]
     return out.reshape(B, S, H * d_v).transpose(0, 1)
+
+
+def indexer_forward_before_topk(x: Tensor, qr: Tensor, wq_b: Tensor, wk: Tensor, k_norm_weight: Tensor,
+                                k_norm_bias: Tensor, weights_proj: Tensor, rotary_pos_emb: Tensor, *,
+                                index_n_heads: int, eps: float = 1e-6, mscale: float = 1.0,
+                                dsa_indexer_rotary_interleaved: bool = False, rotary_interleaved: bool = False,
+                                fp8: bool = False):
+    """``DSAIndexer.forward_before_topk(x, qr)`` (reference patcher.py:245-302), sequence-first.
+
+    ``x [S, B, hidden]``, ``qr [S, B, q_lora_rank]`` bf16; the weights of ``linear_wq_b``
+    (``[Hi * 128, q_lora_rank]``), ``linear_wk`` (``[128, hidden]``), ``k_norm`` (LayerNorm weight
+    and bias ``[128]``) and ``linear_weights_proj`` (``[Hi, hidden]``); ``rotary_pos_emb`` the
+    ``[S, 1, 1, 64]`` fp32 angles the caller passes in ``packed_seq_params`` (``:255``);
+    ``mscale`` = ``config.attention_scaling`` (``transformer_layer.py:249``).  Returns
+    ``(q [S, B, Hi, 128], k [S, B, 128], weights [S, B, Hi])`` like the reference (bf16 q/k, fp32
+    weights holding bf16 values) or, with ``fp8``, ``(q, q_scale [S, B, Hi], k, k_scale [S, B],
+    weights)`` in the fp8 input layout of ``fused_qk_topk_naive``."""
+    S, B, _ = x.shape
+    T = S * B
+    xb = x.reshape(T, -1)
+    qrb = qr.reshape(T, -1)
+    q_lin = torch.nn.functional.linear(qrb, wq_b)                       # :271
+    k_lin = torch.nn.functional.linear(xb, wk)                          # :281
+    w_lin = torch.nn.functional.linear(xb, weights_proj)                # :299
+    fr = rotary_pos_emb.reshape(S, -1).to(torch.float32)
+    fr = fr[:, None, :].expand(S, B, fr.shape[-1]).reshape(T, -1)       # token (s, b) -> angles of s
+    q, qs, k, ks, w = ops.indexer_prologue(q_lin, k_lin, w_lin, k_norm_weight, k_norm_bias, fr, eps, mscale,
+                                           dsa_indexer_rotary_interleaved, rotary_interleaved, fp8)
+    q = q.view(S, B, index_n_heads, 128)
+    k = k.view(S, B, 128)
+    w = w.view(S, B, index_n_heads)
+    if fp8:
+        return q, qs.view(S, B, index_n_heads), k, ks.view(S, B), w
+    return q, k, w

@@ -61,6 +61,65 @@ def _(cu_seqlens, total_q, causal):
 
 
 # --------------------------------------------------------------------------------------
+# K0 indexer prologue
+# --------------------------------------------------------------------------------------
+@torch.library.custom_op("dsa_amd::indexer_prologue", mutates_args=())
+def indexer_prologue(q_lin: Tensor, k_lin: Tensor, w_lin: Tensor, ln_weight: Tensor, ln_bias: Tensor,
+                     freqs: Tensor, eps: float, mscale: float, deinterleave: bool, rotary_interleaved: bool,
+                     fp8: bool = False) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The indexer's tail after its projections (reference ``forward_before_topk``,
+    patcher.py:268-300): ``k_norm`` LayerNorm of ``k``, partial RoPE of the first 64 dims of q
+    and k, the normalised 128-point Hadamard rotation, and the head weights
+    ``w * Hi**-0.5 * Di**-0.5`` -- one fused HIP pass.
+
+    ``q_lin [T, Hi, 128]`` (or ``[T, Hi * 128]``), ``k_lin [T, 128]``, ``w_lin [T, Hi]`` bf16;
+    ``ln_weight``, ``ln_bias [128]``; ``freqs [T, 64]`` fp32 rotary angles (Megatron's
+    ``rotary_pos_emb`` rows); ``deinterleave`` = ``dsa_indexer_rotary_interleaved``,
+    ``rotary_interleaved`` = ``config.rotary_interleaved``.  Returns ``(q, q_scale, k, k_scale, w)``:
+    bf16 ``q [T, Hi, 128]``, ``k [T, 128]`` (empty scales) or, with ``fp8``, float8_e4m3fn rows
+    and their absmax scales ``[T, Hi]``, ``[T]``; ``w [T, Hi]`` fp32."""
+    _require_gpu(q_lin, k_lin, w_lin, ln_weight, ln_bias, freqs)
+    T = q_lin.shape[0]
+    q3 = q_lin.reshape(T, -1, 128)
+    Hi = q3.shape[1]
+    _require(q_lin.dtype == torch.bfloat16 and k_lin.dtype == torch.bfloat16 and w_lin.dtype == torch.bfloat16,
+             "q_lin, k_lin, w_lin must be bf16")
+    _require(k_lin.shape == (T, 128) and w_lin.shape == (T, Hi), "k_lin [T, 128], w_lin [T, Hi]")
+    if not (q3.stride(2) == 1 and q3.stride(1) == 128):
+        q3 = q3.contiguous()
+    kl = k_lin if k_lin.stride(1) == 1 else k_lin.contiguous()
+    wl = w_lin if w_lin.stride(1) == 1 else w_lin.contiguous()
+    fr = freqs.reshape(T, -1).to(torch.float32)
+    _require(fr.shape[1] == 64, "freqs must hold 64 angles per token")
+    fr = fr if fr.stride(1) == 1 else fr.contiguous()
+    lw = ln_weight.to(torch.float32).contiguous()
+    lb = ln_bias.to(torch.float32).contiguous()
+    odt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    q = torch.empty(T, Hi, 128, dtype=odt, device=q_lin.device)
+    k = torch.empty(T, 128, dtype=odt, device=q_lin.device)
+    w = torch.empty(T, Hi, dtype=torch.float32, device=q_lin.device)
+    qs = torch.empty((T, Hi) if fp8 else (0,), dtype=torch.float32, device=q_lin.device)
+    ks = torch.empty((T,) if fp8 else (0,), dtype=torch.float32, device=q_lin.device)
+    with torch.cuda.device(q_lin.device):
+        _lib.call("dsa_indexer_prologue", _p(q3), q3.stride(0), _p(kl), kl.stride(0), _p(wl), wl.stride(0),
+                  _p(lw), _p(lb), _p(fr), fr.stride(0), T, Hi, 128, 64, float(eps), float(mscale),
+                  float(Hi ** -0.5), float(128 ** -0.5), int(deinterleave), int(rotary_interleaved),
+                  _lib.DSA_FP8_E4M3 if fp8 else _lib.DSA_BF16, _p(q), _p(qs if fp8 else None), _p(k),
+                  _p(ks if fp8 else None), _p(w), _stream(q_lin.device))
+    return q, qs, k, ks, w
+
+
+@indexer_prologue.register_fake
+def _(q_lin, k_lin, w_lin, ln_weight, ln_bias, freqs, eps, mscale, deinterleave, rotary_interleaved, fp8=False):
+    T = q_lin.shape[0]
+    Hi = q_lin.numel() // (T * 128) if T else 0
+    odt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    return (q_lin.new_empty(T, Hi, 128, dtype=odt), q_lin.new_empty((T, Hi) if fp8 else (0,), dtype=torch.float32),
+            q_lin.new_empty(T, 128, dtype=odt), q_lin.new_empty((T,) if fp8 else (0,), dtype=torch.float32),
+            q_lin.new_empty(T, Hi, dtype=torch.float32))
+
+
+# --------------------------------------------------------------------------------------
 # K1 indexer scores
 # --------------------------------------------------------------------------------------
 @torch.library.custom_op("dsa_amd::indexer_scores", mutates_args=())

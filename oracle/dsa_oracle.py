@@ -347,3 +347,85 @@ def quantize_e4m3_rows(x: torch.Tensor):
     scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
     xq = (x.to(torch.float32) / scale[..., None]).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
     return xq, scale
+
+
+# --------------------------------------------------------------------------------------
+# indexer prologue: everything between the indexer's projections and the scores
+# (reference DSAIndexer.forward_before_topk + _apply_rope, src/mcore_bridge/patcher.py:245-324,
+# with the patched RoPE of src/mcore_bridge/model/modules/transformer_layer.py:227-278)
+# --------------------------------------------------------------------------------------
+def hadamard_rows(x: torch.Tensor) -> torch.Tensor:
+    """Normalised Walsh-Hadamard transform over the last dim (natural / Sylvester order),
+    computed in float64: ``rotate_activation`` (upstream Megatron, applied at
+    ``patcher.py:292-293``) = ``fast_hadamard_transform.hadamard_transform(x, scale=n**-0.5)``
+    of the third-party ``fast_hadamard_transform`` package (absent here; its published
+    transform is this one).  Returns float64."""
+    n = x.shape[-1]
+    assert n & (n - 1) == 0, "power-of-two length"
+    y = x.to(torch.float64).clone()
+    h = 1
+    while h < n:
+        y = y.reshape(*y.shape[:-1], n // (2 * h), 2, h)
+        a, b = y[..., 0, :], y[..., 1, :]
+        y = torch.stack((a + b, a - b), dim=-2).reshape(*x.shape[:-1], n)
+        h *= 2
+    return y * n ** -0.5
+
+
+def rotate_half(x: torch.Tensor, rotary_interleaved: bool) -> torch.Tensor:
+    """Megatron-Core ``rope_utils._rotate_half`` (third-party megatron-core 0.17.1, absent here):
+    half-split ``cat(-x2, x1)`` or, interleaved, pairs ``(x[2i], x[2i+1]) -> (-x[2i+1], x[2i])``."""
+    if not rotary_interleaved:
+        x1, x2 = torch.chunk(x, 2, dim=-1)
+        return torch.cat((-x2, x1), dim=-1)
+    x1, x2 = x[..., 0::2], x[..., 1::2]
+    return torch.stack((-x2, x1), dim=-1).flatten(start_dim=-2)
+
+
+def indexer_rope(x: torch.Tensor, freqs: torch.Tensor, mscale: float, deinterleave: bool,
+                 rotary_interleaved: bool) -> torch.Tensor:
+    """Patched ``_apply_rotary_pos_emb_bshd`` (``transformer_layer.py:240-278``) on the RoPE part
+    of an indexer row, in the tensor's own dtype (bf16 rounds after every op like the reference;
+    float64 gives the exact rotation).  ``x [..., rot]``, ``freqs [..., rot]`` broadcastable fp32
+    angles; ``deinterleave`` = ``dsa_indexer_rotary_interleaved`` (``patcher.py:310-321`` swaps it
+    into ``multi_latent_attention``), ``rotary_interleaved`` = ``config.rotary_interleaved``."""
+    t = x
+    if deinterleave:                                                   # :261-264
+        t = torch.cat((t[..., 0::2], t[..., 1::2]), dim=-1)
+    cos_ = (torch.cos(freqs) * mscale).to(t.dtype)                     # :268-269
+    sin_ = (torch.sin(freqs) * mscale).to(t.dtype)
+    return (t * cos_) + (rotate_half(t, rotary_interleaved) * sin_)    # :273
+
+
+def indexer_prologue(q_lin: torch.Tensor, k_lin: torch.Tensor, w_lin: torch.Tensor, ln_weight: torch.Tensor,
+                     ln_bias: torch.Tensor, freqs: torch.Tensor, *, eps: float, mscale: float,
+                     deinterleave: bool, rotary_interleaved: bool, rope_dim: int = 64,
+                     dtype: torch.dtype = torch.bfloat16):
+    """``forward_before_topk`` after its three projections (``patcher.py:268-300``).
+
+    ``q_lin [T, Hi, Di]`` = ``linear_wq_b(qr)``, ``k_lin [T, Di]`` = ``linear_wk(x)``, ``w_lin [T, Hi]``
+    = ``linear_weights_proj(x)``, all bf16; ``ln_weight/ln_bias [Di]`` the ``k_norm`` LayerNorm
+    (it has a bias, ``gpt_bridge.py:1299-1300``); ``freqs [T, rope_dim]`` fp32 rotary angles of each
+    token.  The RoPE part is the first ``Di - rope_dim`` dims (``x_pe``, ``patcher.py:307-309``),
+    rotated over ``rope_dim`` angles, which is the whole of it only for ``Di = 2 * rope_dim``.
+    Returns ``(q [T, Hi, Di], k [T, Di], w [T, Hi])`` in ``dtype`` with
+    ``w = weights * Hi**-0.5 * Di**-0.5`` (``:299-300``; ``softmax_scale = Di**-0.5``).  ``dtype`` is
+    the rounding type of every step: bf16 like the reference, float64 for exact checks."""
+    T, Hi, Di = q_lin.shape
+    assert Di == 2 * rope_dim, "the reference's x_pe split matches its rotation only for Di = 2 * rope_dim"
+    bf = dtype
+    ln_t = torch.float32 if dtype == torch.bfloat16 else dtype          # LayerNorm math type
+    k = torch.nn.functional.layer_norm(k_lin.to(ln_t), (Di,), ln_weight.to(ln_t),
+                                       ln_bias.to(ln_t), eps).to(bf)                       # :281-282
+    f = freqs.to(torch.float32 if dtype == torch.bfloat16 else dtype)
+
+    def rope(x, fr):
+        pe, nope = x[..., :Di - rope_dim], x[..., Di - rope_dim:]
+        return torch.cat((indexer_rope(pe, fr, mscale, deinterleave, rotary_interleaved), nope), dim=-1)
+
+    q = rope(q_lin.to(bf), f[:, None, :])                                                  # :275
+    k = rope(k, f)                                                                         # :287
+    q = hadamard_rows(q).to(bf)                                                            # :292
+    k = hadamard_rows(k).to(bf)                                                            # :293
+    w = (w_lin.to(bf) * (Hi ** -0.5)) * (Di ** -0.5)                                       # :299-300
+    return q, k, w

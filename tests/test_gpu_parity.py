@@ -117,6 +117,114 @@ def test_indexer_topk_end_to_end(cfgname, S):
     assert inter / tot >= 0.999, inter / tot
 
 
+
+# ------------------------------------------------------------------ K0 indexer prologue
+def _prologue_case(T, Hi, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    q_lin = (torch.randn(T, Hi, 128, generator=g) * scale).bfloat16()
+    k_lin = (torch.randn(T, 128, generator=g) * scale + 0.5).bfloat16()
+    w_lin = torch.randn(T, Hi, generator=g).bfloat16()
+    lw = 1 + 0.2 * torch.randn(128, generator=g)
+    lb = 0.1 * torch.randn(128, generator=g)
+    fr = torch.rand(T, 64, generator=g) * 3000            # angles of positions up to ~16k
+    return q_lin, k_lin, w_lin, lw, lb, fr
+
+
+def _bf16_rows_close(got, ref, name):
+    # every step rounds to bf16 like the reference; the kernel's fp32 sums (LayerNorm, Hadamard)
+    # and cos/sin may sit on the other side of a rounding boundary, so: >= 99.9 % bit-equal,
+    # the rest within 2 bf16 ulp (relative) or 1e-3 of the row's magnitude
+    got, ref = got.float().cpu(), ref.float().cpu()
+    same = (got == ref).float().mean().item()
+    assert same >= 0.999, f"{name}: only {same:.5f} bit-equal"
+    d = (got - ref).abs()
+    lim = torch.maximum(ref.abs() * 2 ** -6, ref.abs().amax(-1, keepdim=True) * 1e-3)
+    assert (d <= lim).all(), f"{name}: max excess {(d - lim).max().item():.3e}"
+
+
+@pytest.mark.parametrize("dei,ri", [(False, False), (True, False), (False, True), (True, True)])
+def test_indexer_prologue_bf16(dei, ri):
+    print(f"[indexer prologue bf16] deinterleave={dei} rotary_interleaved={ri}", flush=True)
+    T, Hi = 333, 64
+    q_lin, k_lin, w_lin, lw, lb, fr = _prologue_case(T, Hi, 11 + 2 * dei + ri)
+    rq, rk, rw = O.indexer_prologue(q_lin, k_lin, w_lin, lw, lb, fr, eps=1e-6, mscale=1.07, deinterleave=dei,
+                                    rotary_interleaved=ri)
+    q, qs, k, ks, w = ops.indexer_prologue(q_lin.to(DEV), k_lin.to(DEV), w_lin.to(DEV), lw.to(DEV), lb.to(DEV),
+                                           fr.to(DEV), 1e-6, 1.07, dei, ri)
+    assert q.dtype == torch.bfloat16 and qs.numel() == 0 and ks.numel() == 0
+    assert torch.equal(w.cpu(), rw.float())                 # two bf16 roundings, bit for bit
+    _bf16_rows_close(q, rq, "q")
+    _bf16_rows_close(k, rk, "k")
+
+
+def test_indexer_prologue_fp8_and_strided_inputs():
+    print("[indexer prologue fp8]", flush=True)
+    T, Hi = 257, 16
+    q_lin, k_lin, w_lin, lw, lb, fr = _prologue_case(T, Hi, 21, scale=5.0)
+    q_lin[3] = 0                                            # all-zero rows -> scale 1
+    rq, rk, rw = O.indexer_prologue(q_lin, k_lin, w_lin, lw, lb, fr, eps=1e-6, mscale=1.0, deinterleave=True,
+                                    rotary_interleaved=False)
+    # q_lin as a column slice of a wider GEMM output, k_lin with a padded token stride
+    wide = torch.zeros(T, Hi * 128 + 64, dtype=torch.bfloat16)
+    wide[:, :Hi * 128] = q_lin.reshape(T, -1)
+    kpad = torch.zeros(T, 192, dtype=torch.bfloat16)
+    kpad[:, :128] = k_lin
+    args = (wide.to(DEV)[:, :Hi * 128], kpad.to(DEV)[:, :128], w_lin.to(DEV), lw.to(DEV), lb.to(DEV), fr.to(DEV),
+            1e-6, 1.0, True, False)
+    q8, qs, k8, ks, w = ops.indexer_prologue(*args, True)
+    qb, _, kb, _, wb = ops.indexer_prologue(*args, False)
+    assert q8.dtype == torch.float8_e4m3fn and qs.shape == (T, Hi) and ks.shape == (T,)
+    assert torch.equal(w.cpu(), rw.float()) and torch.equal(wb.cpu(), rw.float())
+    # the bf16 rows meet the bf16 bar; the fp8 rows are exactly the oracle's absmax e4m3fn
+    # quantisation (RNE, scale = absmax / 448) of those bf16 rows, codes and scales bit for bit
+    _bf16_rows_close(qb, rq, "q")
+    _bf16_rows_close(kb, rk, "k")
+    for got8, gs, own in ((q8, qs, qb), (k8, ks, kb)):
+        r8, rs = O.quantize_e4m3_rows(own.cpu())
+        assert torch.equal(gs.cpu(), rs)
+        assert torch.equal(got8.cpu().view(torch.uint8), r8.view(torch.uint8))
+    assert float(qs[3].max()) == 1.0 and (q8[3].cpu().float() == 0).all()
+
+
+def test_indexer_prologue_then_topk_end_to_end():
+    # Megatron layout, projections included: x, qr -> GEMMs -> fused prologue -> K1 + K2,
+    # against the oracle prologue and selection on the same projected rows
+    print("[indexer prologue + topk] S=1500", flush=True)
+    S, B, hidden, lora, Hi, K = 1500, 1, 256, 192, 64, 256
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(S, B, hidden, generator=g)).bfloat16()
+    qr = (torch.randn(S, B, lora, generator=g)).bfloat16()
+    wq_b = (torch.randn(Hi * 128, lora, generator=g) / lora ** 0.5).bfloat16()
+    wk = (torch.randn(128, hidden, generator=g) / hidden ** 0.5).bfloat16()
+    wproj = (torch.randn(Hi, hidden, generator=g) / hidden ** 0.5).bfloat16()
+    lw, lb = 1 + 0.1 * torch.randn(128, generator=g), 0.1 * torch.randn(128, generator=g)
+    inv = 1.0 / (10000 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+    ang = torch.arange(S, dtype=torch.float32)[:, None] * inv
+    rope = torch.cat([ang, ang], -1).view(S, 1, 1, 64)
+    from mcore_bridge_amd.dsa import indexer_forward_before_topk
+    q, k, w = indexer_forward_before_topk(x.to(DEV), qr.to(DEV), wq_b.to(DEV), wk.to(DEV), lw.to(DEV), lb.to(DEV),
+                                          wproj.to(DEV), rope.to(DEV), index_n_heads=Hi, eps=1e-6, mscale=1.0)
+    assert q.shape == (S, B, Hi, 128) and k.shape == (S, B, 128) and w.shape == (S, B, Hi)
+    # oracle from the same projected rows (the GEMMs are the library's; their rounding is not
+    # the prologue's)
+    q_lin = torch.nn.functional.linear(qr.to(DEV).reshape(S, -1), wq_b.to(DEV)).cpu().view(S, Hi, 128)
+    k_lin = torch.nn.functional.linear(x.to(DEV).reshape(S, -1), wk.to(DEV)).cpu()
+    w_lin = torch.nn.functional.linear(x.to(DEV).reshape(S, -1), wproj.to(DEV)).cpu()
+    rq, rk, rw = O.indexer_prologue(q_lin, k_lin, w_lin, lw, lb, rope.view(S, 64), eps=1e-6, mscale=1.0,
+                                    deinterleave=False, rotary_interleaved=False)
+    _bf16_rows_close(q[:, 0], rq, "q")
+    _bf16_rows_close(k[:, 0], rk, "k")
+    idx = ops.indexer_topk(q[:, 0].contiguous(), k[:, 0].contiguous(), w[:, 0].contiguous(), K).cpu()
+    ref = O.topk_indices(O.indexer_scores(rq, rk, rw.float()), K)
+    inter = tot = 0
+    for t in range(S):
+        a = set(idx[t][idx[t] >= 0].tolist())
+        b = set(ref[t][ref[t] >= 0].tolist())
+        inter += len(a & b)
+        tot += len(b)
+    assert inter / tot >= 0.999, inter / tot
+
+
 # ------------------------------------------------------------------ K3 forward
 def _attn_case(T, H, K, seed, cu=None, pad=0.1):
     g = torch.Generator().manual_seed(seed)

@@ -118,6 +118,118 @@ def test_indexer_matches_transformers_deepseek_v32():
         assert a == b, (t, a, b)
 
 
+
+# ------------------------------------------------------------------ indexer prologue
+def test_hadamard_rows_is_sylvester_and_orthonormal():
+    sl = pytest.importorskip("scipy.linalg")
+    for n in (8, 128):
+        H = O.hadamard_rows(torch.eye(n, dtype=torch.float64))      # row i = transform of e_i
+        ref = torch.tensor(sl.hadamard(n), dtype=torch.float64) / math.sqrt(n)
+        assert torch.allclose(H, ref, atol=1e-15)
+        assert torch.allclose(H @ H.T, torch.eye(n, dtype=torch.float64), atol=1e-12)
+    x = torch.randn(5, 128, dtype=torch.float64)
+    assert torch.allclose(O.hadamard_rows(O.hadamard_rows(x)), x, atol=1e-12)   # involution
+
+
+def test_indexer_rope_closed_forms():
+    # float64: every RoPE variant is a rotation of 2-vectors by theta_i, scaled by mscale; which
+    # input dims form a pair is what the two flags decide
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(6, 64, dtype=torch.float64, generator=g)
+    th = torch.rand(6, 32, dtype=torch.float64, generator=g) * 50
+    ms = 1.3
+    c, s = th.cos() * ms, th.sin() * ms
+    half, inter = torch.cat([th, th], -1), th.repeat_interleave(2, -1)
+    out = O.indexer_rope(x, half, ms, False, False)          # pairs (i, i + 32)
+    assert torch.allclose(out[:, :32], x[:, :32] * c - x[:, 32:] * s)
+    assert torch.allclose(out[:, 32:], x[:, 32:] * c + x[:, :32] * s)
+    out = O.indexer_rope(x, half, ms, True, False)           # input pairs (2i, 2i+1) -> (i, i + 32)
+    assert torch.allclose(out[:, :32], x[:, 0::2] * c - x[:, 1::2] * s)
+    assert torch.allclose(out[:, 32:], x[:, 1::2] * c + x[:, 0::2] * s)
+    out = O.indexer_rope(x, inter, ms, False, True)          # pairs (2i, 2i+1) in place
+    assert torch.allclose(out[:, 0::2], x[:, 0::2] * c - x[:, 1::2] * s)
+    assert torch.allclose(out[:, 1::2], x[:, 1::2] * c + x[:, 0::2] * s)
+    u = torch.cat([x[:, 0::2], x[:, 1::2]], -1)
+    out = O.indexer_rope(x, inter, ms, True, True)           # de-interleaved, then pairs in place
+    assert torch.allclose(out[:, 0::2], u[:, 0::2] * c - u[:, 1::2] * s)
+    assert torch.allclose(out[:, 1::2], u[:, 1::2] * c + u[:, 0::2] * s)
+
+
+def test_indexer_rope_bf16_matches_transformers():
+    # the third-party half-split RoPE (bf16 cos/sin scaled by attention_scaling, bf16 ops) is
+    # the reference's indexer RoPE with both interleave flags off, bit for bit
+    mod = pytest.importorskip("transformers.models.deepseek_v32.modeling_deepseek_v32")
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 10, 4, 64, generator=g).bfloat16()
+    th = torch.rand(2, 10, 32, generator=g) * 100
+    ms = 1.7
+    emb = torch.cat([th, th], -1)
+    cos, sin = (emb.cos() * ms).bfloat16(), (emb.sin() * ms).bfloat16()
+    hf, _ = mod.apply_rotary_pos_emb(x, x, cos, sin, unsqueeze_dim=2)
+    assert torch.equal(hf, O.indexer_rope(x, emb[:, :, None, :], ms, False, False))
+
+
+def test_indexer_prologue_matches_transformers_deepseek_v32():
+    # end to end against the third-party indexer, from its own projections: LayerNorm with
+    # bias, half-split RoPE on the first rope dims, head weights.  It leaves out the Hadamard
+    # rotation, which preserves every q.k, so in float64 the scores and the top-k agree.
+    mod = pytest.importorskip("transformers.models.deepseek_v32.modeling_deepseek_v32")
+    from transformers import DeepseekV32Config
+    cfg = DeepseekV32Config(hidden_size=64, q_lora_rank=32, index_n_heads=4, index_head_dim=32,
+                            qk_rope_head_dim=16, index_topk=8, num_attention_heads=4, kv_lora_rank=16,
+                            qk_nope_head_dim=16, v_head_dim=16)
+    torch.manual_seed(5)
+    ix = mod.DeepseekV32Indexer(cfg, 0).double().eval()
+    for p in ix.parameters():
+        torch.nn.init.normal_(p, std=0.3)
+    S = 24
+    x = torch.randn(1, S, 64, dtype=torch.float64)
+    qr = torch.randn(1, S, 32, dtype=torch.float64)
+    pos = torch.arange(S)[None]
+    inv = 1.0 / (10000 ** (torch.arange(0, 16, 2, dtype=torch.float64) / 16))
+    ang = pos[..., None].double() * inv
+    emb = torch.cat([ang, ang], -1)
+    hf_idx = ix(x, qr, (emb.cos(), emb.sin()), None, pos)[0]
+    with torch.no_grad():
+        q, k, w = O.indexer_prologue(ix.wq_b(qr)[0].view(S, 4, 32), ix.wk(x)[0], ix.weights_proj(x)[0],
+                                     ix.k_norm.weight, ix.k_norm.bias, emb[0], eps=1e-6, mscale=1.0,
+                                     deinterleave=False, rotary_interleaved=False, rope_dim=16,
+                                     dtype=torch.float64)
+        # the scores themselves: Hadamard-rotated rows give the unrotated dot products
+        qh, kh = O.hadamard_rows(q), O.hadamard_rows(k)             # H is an involution
+        sc = O.indexer_scores(q, k, w)
+        assert torch.allclose(sc, O.indexer_scores(qh, kh, w), atol=1e-9)
+    ours = O.topk_reference_order(sc, 8)
+    for t in range(S):
+        a = set(int(v) for v in ours[t] if v >= 0)
+        b = set(int(v) for v in hf_idx[t] if int(v) <= t)
+        # ReLU makes exact ties (several keys at 0); torch.topk breaks them arbitrarily, the
+        # oracle by lower index: only keys scoring exactly the k-th value may differ
+        kth = min(float(sc[t, j]) for j in a) if a else 0.0
+        assert len(a) == len(b) and all(float(sc[t, j]) == kth for j in a ^ b), (t, a, b)
+
+
+def test_indexer_prologue_bf16_rounding_steps():
+    # bf16 mode differs from the exact float64 prologue by rounding only (a planted wrong
+    # sign, pair or scale would not), and the head weights carry exactly two bf16 roundings
+    g = torch.Generator().manual_seed(9)
+    T, Hi = 7, 4
+    q_lin = torch.randn(T, Hi, 128, generator=g).bfloat16()
+    k_lin = torch.randn(T, 128, generator=g).bfloat16()
+    w_lin = torch.randn(T, Hi, generator=g).bfloat16()
+    lw, lb = torch.randn(128, generator=g), torch.randn(128, generator=g)
+    fr = torch.rand(T, 64, generator=g) * 30
+    for dei, ri in [(False, False), (True, False), (False, True), (True, True)]:
+        kw = dict(eps=1e-6, mscale=1.1, deinterleave=dei, rotary_interleaved=ri)
+        qb, kb, wb = O.indexer_prologue(q_lin, k_lin, w_lin, lw, lb, fr, **kw)
+        q6, k6, w6 = O.indexer_prologue(q_lin.double(), k_lin.double(), w_lin.double(), lw, lb, fr,
+                                        dtype=torch.float64, **kw)
+        for a, b in ((qb, q6), (kb, k6)):
+            assert (a.double() - b).abs().max() <= 0.03 * b.abs().max()
+        assert torch.equal(wb, ((w_lin * 0.5).bfloat16() * 128 ** -0.5).bfloat16())
+        assert torch.allclose(wb.double(), w6, rtol=2 ** -7)
+
+
 # ------------------------------------------------------------------ top-k
 def test_topk_bruteforce_ties_and_masks():
     g = torch.Generator().manual_seed(5)
