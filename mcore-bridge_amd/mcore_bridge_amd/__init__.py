@@ -1,18 +1,20 @@
 """mcore_bridge_amd -- MI355X-native (gfx950) DSA sparse-attention hot path.
 
 Kernel-native ops (packed THD layout) live in ``ops``; Megatron-compatible drop-ins
-(``fused_qk_topk_naive``, ``sparse_mla_attention``, ``indexer_forward_before_topk``) in ``dsa``; ``patch.install()`` swaps them
+(``fused_qk_topk_naive``, ``sparse_mla_attention``, ``absorbed_mla_sparse_attention``,
+``indexer_forward_before_topk``, the ``DSAIndexer`` module) in ``dsa``; ``patch.install()`` swaps them
 into Megatron-Core's DSA module when it is importable.  All arithmetic runs in the HIP
 kernels of ``libdsa_amd.so`` (C ABI: include/dsa_abi.h); there is no CPU fallback.
 """
 from . import _lib
-from .dsa import fused_qk_topk_naive, indexer_forward_before_topk, sparse_mla_attention
+from .dsa import (DSAIndexer, absorbed_mla_sparse_attention, fused_qk_topk_naive, indexer_forward_before_topk,
+                  sparse_mla_attention)
 from .ops import (build_decode_rows, build_rows, bwd_workspace_bytes, decode_indexer_topk, decode_workspace_bytes,
                   indexer_prologue, indexer_scores, indexer_topk, sparse_mla, sparse_mla_bwd, sparse_mla_decode,
                   sparse_mla_fwd, topk)
 
 __all__ = [
-    "build_decode_rows", "build_rows", "bwd_workspace_bytes", "decode_indexer_topk", "decode_workspace_bytes",
+    "DSAIndexer", "absorbed_mla_sparse_attention", "build_decode_rows", "build_rows", "bwd_workspace_bytes", "decode_indexer_topk", "decode_workspace_bytes",
     "fused_qk_topk_naive", "indexer_forward_before_topk", "indexer_prologue", "indexer_scores", "indexer_topk",
     "sparse_mla", "sparse_mla_attention", "sparse_mla_bwd", "sparse_mla_decode", "sparse_mla_fwd", "topk",
 ]

@@ -11,6 +11,11 @@ that DSAttention runs on the indexer output (call site
 src/mcore_bridge/model/modules/multi_latent_attention.py:262-270): one shared 576-wide latent KV
 head, ``v = kv[..., :512]``, causal ``triu`` mask applied on top of the index mask.
 
+``absorbed_mla_sparse_attention`` is the same attention for the caller's un-absorbed MLA tensors
+(multi_latent_attention.py:101-178 builds ``key_h = [kv_compressed W_UK_h^T, k_pos_emb]`` and
+``value_h = kv_compressed W_UV_h^T`` from ``linear_kv_up_proj``): the query is absorbed into the
+latent space, the kernel runs on ``[kv_compressed, k_pos_emb]``, ``W_UV`` is applied after.
+
 ``indexer_forward_before_topk`` is the indexer's producer, reference
 ``DSAIndexer.forward_before_topk`` (src/mcore_bridge/patcher.py:245-302): the three projections
 run as plain GEMMs (hipBLASLt through torch), everything after them in one fused HIP pass.
@@ -141,3 +146,105 @@ def indexer_forward_before_topk(x: Tensor, qr: Tensor, wq_b: Tensor, wk: Tensor,
     if fp8:
         return q, qs.view(S, B, index_n_heads), k, ks.view(S, B), w
     return q, k, w
+
+
+class _HeadwiseMatmul(torch.autograd.Function):
+    """``out[h] = a[h] @ b[h]`` for ``a [H, M, K]``, ``b [H, K, N]``, with every batched product in
+    forward and backward fed contiguous operands (no transposed views reach ``torch.bmm``)."""
+
+    @staticmethod
+    def forward(ctx, a: Tensor, b: Tensor) -> Tensor:
+        a, b = a.contiguous(), b.contiguous()
+        ctx.save_for_backward(a, b)
+        return torch.bmm(a, b)
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        a, b = ctx.saved_tensors
+        g = g.contiguous()
+        ga = torch.bmm(g, b.transpose(1, 2).contiguous()) if ctx.needs_input_grad[0] else None
+        gb = torch.bmm(a.transpose(1, 2).contiguous(), g) if ctx.needs_input_grad[1] else None
+        return ga, gb
+
+
+def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compressed: Tensor, k_pos_emb: Tensor,
+                                  kv_up_proj_weight: Tensor, topk_indices: Tensor, softmax_scale: float,
+                                  causal: bool = True) -> Tensor:
+    """Megatron's DSA core attention (called at reference multi_latent_attention.py:262-270) on
+    the MLA's un-absorbed inputs, computed in the absorbed latent space.
+
+    ``q_no_pe [S, B, H, dn]``, ``q_pos_emb [S, B, H, 64]`` (after RoPE), ``kv_compressed [S, B, 512]``
+    (after ``kv_layernorm``), ``k_pos_emb [S, B, 64]`` or ``[S, B, 1, 64]`` (after RoPE), bf16;
+    ``kv_up_proj_weight [H * (dn + dv), 512]`` the ``linear_kv_up_proj`` weight (per head ``dn`` rows
+    of ``W_UK`` then ``dv`` rows of ``W_UV``, ``:121-128``); ``topk_indices [B, S, K]``.  Returns
+    ``[S, B, H * dv]`` -- what the un-fused attention returns for ``query = [q_no_pe, q_pos_emb]``,
+    ``key_h = [kv_compressed W_UK_h^T, k_pos_emb]``, ``value_h = kv_compressed W_UV_h^T`` -- and is
+    differentiable w.r.t. every tensor input (the weight included)."""
+    S, B, H, dn = q_no_pe.shape
+    dc = kv_compressed.shape[-1]
+    assert dc + q_pos_emb.shape[-1] == ops.D_QK and dc == ops.D_V, "latent 512 + rope 64"
+    W = kv_up_proj_weight.view(H, -1, dc)
+    dv = W.shape[1] - dn
+    w_uk = W[:, :dn]                                                   # [H, dn, dc]
+    w_uv_t = W[:, dn:].transpose(1, 2)                                 # [H, dc, dv]
+    qn = q_no_pe.permute(2, 0, 1, 3).reshape(H, S * B, dn)
+    q_lat = _HeadwiseMatmul.apply(qn, w_uk)                            # [H, S*B, dc]
+    query = torch.cat([q_lat.view(H, S, B, dc).permute(1, 2, 0, 3), q_pos_emb], dim=-1)
+    kv = torch.cat([kv_compressed, k_pos_emb.reshape(S, B, -1)], dim=-1)
+    o_lat = sparse_mla_attention(query.contiguous(), kv.contiguous(), topk_indices, softmax_scale, ops.D_V, causal)
+    o = o_lat.reshape(S, B, H, dc).permute(2, 0, 1, 3).reshape(H, S * B, dc)
+    out = _HeadwiseMatmul.apply(o, w_uv_t)                             # [H, S*B, dv]
+    return out.view(H, S, B, dv).permute(1, 2, 0, 3).reshape(S, B, H * dv)
+
+
+class DSAIndexer(torch.nn.Module):
+    """Host mirror of the reference's patched ``DSAIndexer`` (src/mcore_bridge/patcher.py:243-380)
+    over the HIP kernels: same method names, arguments and returns, and Megatron's parameter names
+    (``linear_wq_b``, ``linear_wk``, ``k_norm``, ``linear_weights_proj``), so the indexer keys the
+    reference's bridge maps (``wq_b``, ``wk``, ``k_norm.{weight,bias}``, ``weights_proj``,
+    gpt_bridge.py:1292-1306) load one to one.
+
+    Forward only, like the reference without ``dsa_indexer_loss_coeff`` (the indexer KL loss and
+    its backward are not built): the outputs are computed under ``torch.no_grad``."""
+
+    def __init__(self, hidden_size: int, q_lora_rank: int, index_n_heads: int = 64, index_head_dim: int = 128,
+                 index_topk: int = 2048, qk_pos_emb_head_dim: int = 64, layernorm_epsilon: float = 1e-6,
+                 attention_scaling: float = 1.0, dsa_indexer_rotary_interleaved: bool = False,
+                 rotary_interleaved: bool = False, fp8: bool = False, device=None, dtype=torch.bfloat16):
+        super().__init__()
+        assert index_head_dim == 128 and qk_pos_emb_head_dim == 64, "index_head_dim 128, rope 64 (DSv3.2)"
+        kw = dict(device=device, dtype=dtype)
+        self.index_n_heads, self.index_head_dim, self.index_topk = index_n_heads, index_head_dim, index_topk
+        self.eps, self.mscale, self.fp8 = layernorm_epsilon, attention_scaling, fp8
+        self.dsa_indexer_rotary_interleaved, self.rotary_interleaved = dsa_indexer_rotary_interleaved, rotary_interleaved
+        self.linear_wq_b = torch.nn.Linear(q_lora_rank, index_n_heads * index_head_dim, bias=False, **kw)
+        self.linear_wk = torch.nn.Linear(hidden_size, index_head_dim, bias=False, **kw)
+        self.k_norm = torch.nn.LayerNorm(index_head_dim, eps=layernorm_epsilon, **kw)
+        self.linear_weights_proj = torch.nn.Linear(hidden_size, index_n_heads, bias=False, **kw)
+
+    @torch.no_grad()
+    def forward_before_topk(self, x: Tensor, qr: Tensor, packed_seq_params=None):
+        """``(q [S,B,Hi,Di], k [S,B,Di], weights [S,B,Hi])`` (with fp8: ``(q, q_scale, k, k_scale,
+        weights)``); ``packed_seq_params`` is the caller's ``(psp, rotary_pos_emb)`` tuple
+        (multi_latent_attention.py:260-261)."""
+        psp, rotary_pos_emb = packed_seq_params
+        assert psp is None, "Packed sequence is not supported for DSAttention"   # patcher.py:256
+        return indexer_forward_before_topk(
+            x, qr, self.linear_wq_b.weight, self.linear_wk.weight, self.k_norm.weight, self.k_norm.bias,
+            self.linear_weights_proj.weight, rotary_pos_emb, index_n_heads=self.index_n_heads, eps=self.eps,
+            mscale=self.mscale, dsa_indexer_rotary_interleaved=self.dsa_indexer_rotary_interleaved,
+            rotary_interleaved=self.rotary_interleaved, fp8=self.fp8)
+
+    @torch.no_grad()
+    def forward_with_scores(self, x: Tensor, qr: Tensor, mask: Optional[Tensor] = None, packed_seq_params=None):
+        """``(index_scores [B,S,S] fp32, topk_indices [B,S,index_topk] int64)`` (patcher.py:326-360)."""
+        out = self.forward_before_topk(x, qr, packed_seq_params)
+        if self.fp8:
+            q, qs, k, ks, w = out
+            return fused_qk_topk_naive(q, k, w, self.index_topk, mask, q_scale=qs, k_scale=ks)
+        q, k, w = out
+        return fused_qk_topk_naive(q, k, w, self.index_topk, mask)
+
+    def forward(self, x: Tensor, qr: Tensor, mask: Optional[Tensor] = None, packed_seq_params=None) -> Tensor:
+        """``topk_indices [B, S, index_topk]`` (patcher.py:362-378)."""
+        return self.forward_with_scores(x, qr, mask, packed_seq_params)[1]

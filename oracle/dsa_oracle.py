@@ -429,3 +429,27 @@ def indexer_prologue(q_lin: torch.Tensor, k_lin: torch.Tensor, w_lin: torch.Tens
     k = hadamard_rows(k).to(bf)                                                            # :293
     w = (w_lin.to(bf) * (Hi ** -0.5)) * (Di ** -0.5)                                       # :299-300
     return q, k, w
+
+
+
+# --------------------------------------------------------------------------------------
+# the reference's un-absorbed layout (what DSAttention receives)
+# --------------------------------------------------------------------------------------
+def unabsorbed_sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                topk_idx: torch.Tensor, sm_scale: float) -> torch.Tensor:
+    """Megatron's un-fused DSA attention on per-head tensors (``query``/``key [S, B, H, dq]``,
+    ``value [S, B, H, dv]``, built at ``multi_latent_attention.py:101-178``), float64: dense
+    scores, index mask (0 at ``topk_idx [B, S, K]``, negative = none), causal ``triu`` mask,
+    softmax, ``P V``.  Returns ``[S, B, H * dv]``."""
+    S, B, H, dq = query.shape
+    q = query.double().permute(1, 2, 0, 3)                           # [B, H, S, dq]
+    k = key.double().permute(1, 2, 0, 3)
+    v = value.double().permute(1, 2, 0, 3)
+    s = torch.matmul(q, k.transpose(-1, -2)) * sm_scale              # [B, H, S, S]
+    ti = topk_idx.to(torch.int64)
+    sel = torch.zeros(B, S, S + 1, dtype=torch.bool)                  # column S takes the padding
+    sel.scatter_(-1, torch.where(ti >= 0, ti, S), True)
+    m = torch.where(sel[..., :S], 0.0, NEG_INF) + torch.triu(torch.full((S, S), NEG_INF, dtype=torch.float64), diagonal=1)
+    p = torch.softmax(s + m[:, None], dim=-1).nan_to_num(0.0)
+    o = torch.matmul(p, v)                                           # [B, H, S, dv]
+    return o.permute(2, 0, 1, 3).reshape(S, B, -1)

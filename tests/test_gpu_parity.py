@@ -225,6 +225,86 @@ def test_indexer_prologue_then_topk_end_to_end():
     assert inter / tot >= 0.999, inter / tot
 
 
+
+
+def test_dsa_indexer_module_forward_with_scores():
+    # the DSAIndexer mirror end to end (its own parameters, (psp, rotary_pos_emb) tuple, causal
+    # mask): indices in torch.topk order over the oracle's prologue + scores of the same
+    # projected rows, >= 99.9 % overlap; the scores returned are the kernel's for those rows
+    print("[DSAIndexer module] S=700 B=2", flush=True)
+    from mcore_bridge_amd.dsa import DSAIndexer
+    S, B, hidden, lora, K = 700, 2, 256, 128, 128
+    torch.manual_seed(41)
+    ix = DSAIndexer(hidden, lora, index_n_heads=64, index_topk=K, attention_scaling=1.1,
+                    dsa_indexer_rotary_interleaved=True, device=DEV)
+    with torch.no_grad():
+        for p_ in ix.parameters():
+            p_.copy_(torch.randn_like(p_.float()).mul_(p_.shape[-1] ** -0.5 if p_.dim() == 2 else 0.1).add_(
+                1.0 if p_ is ix.k_norm.weight else 0.0))
+    x = torch.randn(S, B, hidden, device=DEV).bfloat16()
+    qr = torch.randn(S, B, lora, device=DEV).bfloat16()
+    inv = 1.0 / (10000 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+    ang = torch.arange(S, dtype=torch.float32)[:, None] * inv
+    rope = torch.stack([ang, ang], -1).reshape(S, 1, 1, 64).to(DEV)          # interleaved duplication
+    mask = torch.triu(torch.full((S, S), float("-inf"), device=DEV), diagonal=1).expand(B, S, S)
+    sc, idx = ix.forward_with_scores(x, qr, mask, (None, rope))
+    assert sc.shape == (B, S, S) and idx.shape == (B, S, K) and idx.dtype == torch.int64
+    for b in range(B):
+        q_lin = torch.nn.functional.linear(qr[:, b], ix.linear_wq_b.weight).cpu().view(S, 64, 128)
+        k_lin = torch.nn.functional.linear(x[:, b], ix.linear_wk.weight).cpu()
+        w_lin = torch.nn.functional.linear(x[:, b], ix.linear_weights_proj.weight).cpu()
+        rq, rk, rw = O.indexer_prologue(q_lin, k_lin, w_lin, ix.k_norm.weight.detach().cpu(),
+                                        ix.k_norm.bias.detach().cpu(), rope.view(S, 64).cpu(), eps=1e-6,
+                                        mscale=1.1, deinterleave=True, rotary_interleaved=False)
+        ref = O.topk_reference_order(O.indexer_scores(rq, rk, rw.float()), K)
+        got = idx[b].cpu()
+        inter = tot = 0
+        for t in range(S):
+            a = set(got[t][: min(K, t + 1)].tolist())
+            r = set(ref[t][ref[t] >= 0].tolist())
+            inter += len(a & r)
+            tot += len(r)
+        assert inter / tot >= 0.999, inter / tot
+        # the returned order is the score order of the returned scores (ties to the lower key)
+        vals = torch.gather(sc[b].cpu(), 1, got.clamp(min=0))
+        assert (vals[:, 1:] <= vals[:, :-1]).all()
+
+
+# ------------------------------------------------------------------ MLA absorption adapter
+@pytest.mark.parametrize("S,B,H,K", [(160, 2, 16, 48), (300, 1, 128, 128)])
+def test_absorbed_mla_adapter_matches_unabsorbed_reference(S, B, H, K):
+    # the caller's un-absorbed tensors (multi_latent_attention.py:101-178) -> absorbed kernels;
+    # reference: the un-fused attention on key_h = [c W_UK_h^T, k_pe], value_h = c W_UV_h^T in
+    # float64, output and the gradients of every input, weight included
+    print(f"[absorbed MLA adapter] S={S} B={B} H={H} K={K}", flush=True)
+    from mcore_bridge_amd.dsa import absorbed_mla_sparse_attention
+    g = torch.Generator().manual_seed(S + H)
+    dn, dr, dc, dv = 128, 64, 512, 128
+    qn = (torch.randn(S, B, H, dn, generator=g)).bfloat16()
+    qp = (torch.randn(S, B, H, dr, generator=g)).bfloat16()
+    c = (torch.randn(S, B, dc, generator=g)).bfloat16()
+    kp = (torch.randn(S, B, dr, generator=g)).bfloat16()
+    W = (torch.randn(H * (dn + dv), dc, generator=g) / dc ** 0.5).bfloat16()
+    idx = torch.stack([_attn_case(S, 1, K, S + b)[2] for b in range(B)]).long()   # [B, S, K] per batch
+    scale = (dn + dr) ** -0.5
+    dout = (torch.randn(S, B, H * dv, generator=g) * 0.1).bfloat16()
+    # reference, float64 on the CPU
+    ins = [x.double().requires_grad_() for x in (qn, qp, c, kp, W)]
+    rqn, rqp, rc, rkp, rW = ins
+    Wh = rW.view(H, dn + dv, dc)
+    key = torch.cat([torch.einsum("sbc,hnc->sbhn", rc, Wh[:, :dn]), rkp[:, :, None].expand(S, B, H, dr)], -1)
+    val = torch.einsum("sbc,hvc->sbhv", rc, Wh[:, dn:])
+    ref = O.unabsorbed_sparse_attention(torch.cat([rqn, rqp], -1), key, val, idx, scale)
+    ref.backward(dout.double())
+    # absorbed, on the GPU
+    gins = [x.to(DEV).requires_grad_() for x in (qn, qp, c, kp, W)]
+    out = absorbed_mla_sparse_attention(*gins, idx.to(DEV), scale)
+    out.backward(dout.to(DEV))
+    _close(out.detach(), ref.detach(), name="out")
+    for name, a, r in zip(("dq_no_pe", "dq_pos_emb", "dkv_compressed", "dk_pos_emb", "dW_kv_up"), gins, ins):
+        _close(a.grad, r.grad, name=name)
+
+
 # ------------------------------------------------------------------ K3 forward
 def _attn_case(T, H, K, seed, cu=None, pad=0.1):
     g = torch.Generator().manual_seed(seed)

@@ -57,3 +57,30 @@ def test_config_shapes():
     assert x["q"].shape == (64, 16, 576) and x["w"].min() >= 0      # cfg1 weights ~ U(0,1)
     y = W.make_prefill(W.CONFIGS["cfg1"], S=64)
     assert torch.equal(x["q"], y["q"])                                 # seeded, reproducible
+
+
+def test_dsa_indexer_parameters_are_the_bridge_keys():
+    # the reference's bridge maps exactly these Megatron indexer keys to the HF checkpoint
+    # (src/mcore_bridge/bridge/gpt_bridge.py:1292-1306); the mirror must expose the same names
+    # and Megatron's shapes so a converted state dict loads unchanged
+    ix = dsa.DSAIndexer(hidden_size=256, q_lora_rank=96, index_n_heads=8, index_topk=32, device="cpu")
+    shapes = {k: tuple(v.shape) for k, v in ix.state_dict().items()}
+    assert shapes == {"linear_wq_b.weight": (8 * 128, 96), "linear_wk.weight": (128, 256),
+                      "k_norm.weight": (128,), "k_norm.bias": (128,), "linear_weights_proj.weight": (8, 256)}
+    hf_names = {"wq_b.weight": "linear_wq_b.weight", "wk.weight": "linear_wk.weight",
+                "k_norm.weight": "k_norm.weight", "k_norm.bias": "k_norm.bias",
+                "weights_proj.weight": "linear_weights_proj.weight"}
+    sd = {hf_names[k]: torch.randn(shapes[hf_names[k]]).bfloat16() for k in hf_names}
+    ix.load_state_dict(sd)
+    assert torch.equal(ix.linear_wk.weight, sd["linear_wk.weight"])
+
+
+def test_dsa_indexer_rejects_packed_sequences_like_the_reference():
+    # patcher.py:255-256: packed_seq_params arrives as (psp, rotary_pos_emb) and psp must be None
+    ix = dsa.DSAIndexer(hidden_size=64, q_lora_rank=32, index_n_heads=4, index_topk=8, device="cpu")
+    try:
+        ix.forward_before_topk(torch.zeros(4, 1, 64), torch.zeros(4, 1, 32), (object(), torch.zeros(4, 1, 1, 64)))
+    except AssertionError as e:
+        assert "Packed sequence" in str(e)
+    else:
+        raise AssertionError("packed sequences must be rejected")

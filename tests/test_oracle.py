@@ -338,6 +338,36 @@ def test_absorbed_equals_unabsorbed_mha():
     torch.testing.assert_close(got, ref, rtol=1e-9, atol=1e-12)
 
 
+
+def test_unabsorbed_sparse_attention_pins():
+    # the reference's own un-absorbed layout: (a) selecting every visible key is causal SDPA,
+    # (b) with real selections it equals the absorbed form through the MLA identity
+    g = torch.Generator().manual_seed(12)
+    S, B, H, dn, dr, dc, dv = 18, 2, 3, 16, 64, 512, 24
+    q = torch.randn(S, B, H, dn + dr, generator=g, dtype=torch.float64)
+    k = torch.randn(S, B, H, dn + dr, generator=g, dtype=torch.float64)
+    v = torch.randn(S, B, H, dv, generator=g, dtype=torch.float64)
+    scale = (dn + dr) ** -0.5
+    full = torch.arange(S).expand(B, S, S)
+    got = O.unabsorbed_sparse_attention(q, k, v, full, scale)
+    sdpa = torch.nn.functional.scaled_dot_product_attention(q.permute(1, 2, 0, 3), k.permute(1, 2, 0, 3),
+                                                            v.permute(1, 2, 0, 3), is_causal=True, scale=scale)
+    torch.testing.assert_close(got, sdpa.permute(2, 0, 1, 3).reshape(S, B, H * dv), rtol=1e-10, atol=1e-12)
+    qn, qp = q[..., :dn], q[..., dn:]
+    c = torch.randn(S, B, dc, generator=g, dtype=torch.float64) * 0.2
+    kp = torch.randn(S, B, dr, generator=g, dtype=torch.float64)
+    Wuk = torch.randn(H, dn, dc, generator=g, dtype=torch.float64) * 0.05
+    Wuv = torch.randn(H, dv, dc, generator=g, dtype=torch.float64) * 0.05
+    idx = torch.stack([_rand_idx(S, 7, g) for _ in range(B)])              # [B, S, 7], -1 padded
+    key = torch.cat([torch.einsum("sbc,hnc->sbhn", c, Wuk), kp[:, :, None].expand(S, B, H, dr)], -1)
+    val = torch.einsum("sbc,hvc->sbhv", c, Wuv)
+    ref = O.unabsorbed_sparse_attention(torch.cat([qn, qp], -1), key, val, idx, scale)
+    for b in range(B):
+        q_abs = torch.cat([torch.einsum("shn,hnc->shc", qn[:, b], Wuk), qp[:, b]], -1)
+        o, _ = O.sparse_mla_fwd(q_abs, torch.cat([c[:, b], kp[:, b]], -1), idx[b], scale)
+        got_b = torch.einsum("shc,hvc->shv", o, Wuv).reshape(S, H * dv)
+        torch.testing.assert_close(got_b, ref[:, b], rtol=1e-9, atol=1e-12)
+
 def test_backward_closed_form_matches_autograd():
     g = torch.Generator().manual_seed(10)
     T, H, K = 24, 2, 7
