@@ -267,6 +267,31 @@ def sparse_mla_bwd(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, out: to
     return dq, dkv
 
 
+def sparse_mla_bwd_dkv_rows(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, out: torch.Tensor,
+                            dout: torch.Tensor, lse: torch.Tensor, sm_scale: float, keys, d_v: int = 512):
+    """``dKV`` rows of the listed keys only, by the closed form of ``sparse_mla_bwd`` restricted to
+    the (query, head) pairs that selected each key: ``P = exp(sm_scale*q.kv_s - lse)``,
+    ``dS = P*(dO.v_s - Delta)``, ``dKV[s] = sum sm_scale*dS*q + P*dO`` (first ``d_v`` columns).
+    Costs O(#selecting queries * H * D) per key, so it runs at full problem sizes."""
+    rows = []
+    kv64 = kv.to(torch.float64)
+    for s in keys:
+        hit = (idx.to(torch.int64) == int(s)).any(dim=1).nonzero().flatten().cpu()
+        acc = torch.zeros(kv.shape[1], dtype=torch.float64)
+        if hit.numel():
+            qq = q[hit].to(torch.float64)                              # [n, H, D]
+            oo, dd = out[hit].to(torch.float64), dout[hit].to(torch.float64)
+            l = lse[hit].to(torch.float64)                             # [n, H]
+            sc = torch.einsum("nhd,d->nh", qq, kv64[int(s)]) * sm_scale
+            p = torch.where(torch.isfinite(l), torch.exp(sc - l), torch.zeros_like(sc))
+            dp = torch.einsum("nhv,v->nh", dd, kv64[int(s), :d_v])
+            ds = p * (dp - (dd * oo).sum(-1))
+            acc = torch.einsum("nh,nhd->d", ds * sm_scale, qq)
+            acc[:d_v] += torch.einsum("nh,nhv->v", p, dd)
+        rows.append(acc)
+    return torch.stack(rows)
+
+
 # --------------------------------------------------------------------------------------
 # decode (no reference counterpart: the reference has no DSA cache, patcher.py:256)
 # --------------------------------------------------------------------------------------

@@ -384,6 +384,21 @@ def test_backward_closed_form_matches_autograd():
     torch.testing.assert_close(dkv, dkv_ref, rtol=1e-9, atol=1e-11)
 
 
+
+def test_dkv_rows_equal_full_backward():
+    # the per-key restriction used at full sizes equals the full closed-form backward
+    g = torch.Generator().manual_seed(13)
+    T, H, K = 40, 3, 9
+    q = torch.randn(T, H, 576, generator=g, dtype=torch.float64) * 0.3
+    kv = torch.randn(T, 576, generator=g, dtype=torch.float64) * 0.3
+    idx = _rand_idx(T, K, g)
+    out, lse = O.sparse_mla_fwd(q, kv, idx, 0.05)
+    dout = torch.randn(T, H, 512, generator=g, dtype=torch.float64)
+    _, dkv = O.sparse_mla_bwd(q, kv, idx, out, dout, lse, 0.05)
+    keys = [0, 5, 17, 39]
+    torch.testing.assert_close(O.sparse_mla_bwd_dkv_rows(q, kv, idx, out, dout, lse, 0.05, keys), dkv[keys],
+                               rtol=1e-10, atol=1e-12)
+
 def test_backward_gradcheck_tiny():
     g = torch.Generator().manual_seed(11)
     T, H = 6, 1
