@@ -111,7 +111,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   constexpr int kCopyEvery = kDqk / 16 / G;   // S/dP steps per gather copy
   static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the k-steps");
   __shared__ __attribute__((aligned(128))) SpSmem sm;
-  const int t = xcd_remap(blockIdx.x, p.total_q);
+  const int t = xcd_remap(blockIdx.x);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5, hl = lane & 31;
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   static_assert(HR / 16 / NW == 2, "two dS copies per wave per block");
   static_assert(DT * NW * 16 == kDqk && DT >= TC, "dims split evenly; one tile copy per dim step");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
-  const int t = xcd_remap(blockIdx.x, p.total_q);
+  const int t = xcd_remap(blockIdx.x);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, gi = lane & 15;
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
   constexpr int G = TC + 2;                      // copies per copy-issuing wave per block
   static_assert(TC <= 2 * HT - 6, "tile copies before the dS copy slots");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
-  const int t = xcd_remap(blockIdx.x, p.total_q);
+  const int t = xcd_remap(blockIdx.x);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(wave);
@@ -657,7 +657,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   constexpr int NW = 4;
   constexpr int G = 2 * kGHeads / 16 / NW;          // 4 copies per wave per block
   __shared__ __attribute__((aligned(16))) GSmem sm;
-  const int t = xcd_remap(blockIdx.x, p.total_q);
+  const int t = xcd_remap(blockIdx.x);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5;
@@ -1089,7 +1089,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   };
   mark(0);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
-  const dim3 grid(((p.total_q + 7) / 8) * 8, (p.n_heads + 127) / 128);
+  const dim3 grid(xcd_grid(p.total_q), (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
   hipLaunchKernelGGL(zero_i32_kernel, dim3((p.n_kv + 255) / 256), dim3(256), 0, stream, p.csr_counts, p.n_kv);
   const int64_t pairs = (int64_t)p.total_q * p.topk;
@@ -1126,7 +1126,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   }
   mark(3);
   const int nks = p.n_heads / 16;
-  const dim3 ggrid(((p.total_q + 7) / 8) * 8);
+  const dim3 ggrid(xcd_grid(p.total_q));
   if (nks > 4)
     hipLaunchKernelGGL(bwd_g_kernel<8>, ggrid, dim3(256), 0, stream, p);
   else if (nks > 2)
