@@ -478,3 +478,93 @@ def unabsorbed_sparse_attention(query: torch.Tensor, key: torch.Tensor, value: t
     p = torch.softmax(s + m[:, None], dim=-1).nan_to_num(0.0)
     o = torch.matmul(p, v)                                           # [B, H, S, dv]
     return o.permute(2, 0, 1, 3).reshape(S, B, -1)
+
+
+# --------------------------------------------------------------------------------------
+# indexer KL loss (model_config.py:204-205 dsa_indexer_loss_coeff / dsa_indexer_use_sparse_loss;
+# computed by megatron-core's compute_dsa_indexer_loss, third-party and absent here: restated
+# from its published algorithm, the DeepSeek-V3.2 report's indexer objective)
+# --------------------------------------------------------------------------------------
+KL_EPS = 1e-10
+
+
+def attention_head_probs(q: torch.Tensor, kv: torch.Tensor, idx: torch.Tensor, lse: torch.Tensor,
+                         sm_scale: float) -> torch.Tensor:
+    """Target of the sparse indexer loss: ``p[t, j] = (1/H) sum_h exp(sm_scale*q[t,h].kv[idx[t,j]] -
+    lse[t,h])`` for valid slots (0 elsewhere): the head-summed attention probabilities of the
+    selected keys, L1-normalised (each head's probabilities over the selected keys sum to 1)."""
+    T, H, D = q.shape
+    ii = idx.to(torch.int64)
+    valid = ii >= 0
+    g = kv.to(torch.float64)[ii.clamp(min=0)]                          # [T, K, D]
+    s = torch.einsum("thd,tkd->thk", q.to(torch.float64), g) * sm_scale
+    l = lse.to(torch.float64)[..., None]
+    p = torch.where(valid[:, None, :] & torch.isfinite(l), torch.exp(s - l), torch.zeros_like(s))
+    return p.sum(1) / H
+
+
+def indexer_kl_sparse(index_sel: torch.Tensor, target: torch.Tensor, valid: torch.Tensor):
+    """Per-row KL of the sparse indexer loss over the selected slots:
+    ``KL_t = sum_j p_tj (log(p_tj + eps) - log(softmax(I_t)_j + eps))`` with the index-score
+    softmax over valid slots only.  Returns ``(kl [T], d kl_t / d I_t [T, K])``; the gradient of
+    ``sum_j p log(pI + eps)`` is ``pI * sum_j(p pI/(pI+eps)) - p pI/(pI+eps)`` per slot."""
+    I = index_sel.to(torch.float64).masked_fill(~valid, NEG_INF)
+    lp = torch.log_softmax(I, dim=-1)
+    pI = torch.where(valid, lp.exp(), torch.zeros_like(lp))
+    p = target.to(torch.float64)
+    kl = (p * (torch.log(p + KL_EPS) - torch.log(pI + KL_EPS))).masked_fill(~valid, 0.0).sum(-1)
+    r = torch.where(valid, p * pI / (pI + KL_EPS), torch.zeros_like(pI))
+    grad = pI * r.sum(-1, keepdim=True) - r
+    return kl, torch.where(valid, grad, torch.zeros_like(grad))
+
+
+def indexer_scores_bwd(q_idx: torch.Tensor, k_idx: torch.Tensor, w: torch.Tensor, idx: torch.Tensor,
+                       d_scores: torch.Tensor, q_scale=None, k_scale=None):
+    """Gradients of ``I[t, j] = sum_h w[t,h] relu(q[t,h] . k[idx[t,j]])`` (the indexer scores of the
+    selected slots) given ``dI [T, K]``: ``dq[t,h] = w[t,h] sum_j dI[t,j] 1[z>0] k_j``,
+    ``dw[t,h] = sum_j dI[t,j] relu(z)``, ``dk[s] += sum_h dI[t,j] w[t,h] 1[z>0] q[t,h]``.  float64."""
+    qd = q_idx.to(torch.float64)
+    kd = k_idx.to(torch.float64)
+    if q_scale is not None:
+        qd = qd * q_scale.to(torch.float64)[..., None]
+        kd = kd * k_scale.to(torch.float64)[..., None]
+    ii = idx.to(torch.int64)
+    valid = ii >= 0
+    g = kd[ii.clamp(min=0)]                                            # [T, K, Di]
+    z = torch.einsum("thd,tkd->thk", qd, g)
+    dI = torch.where(valid, d_scores.to(torch.float64), torch.zeros_like(d_scores, dtype=torch.float64))
+    gm = dI[:, None, :] * (z > 0) * w.to(torch.float64)[..., None]     # [T, Hi, K]
+    dq = torch.einsum("thk,tkd->thd", gm, g)
+    dw = torch.einsum("tk,thk->th", dI, z.clamp(min=0))
+    dk = torch.zeros_like(kd)
+    contrib = torch.einsum("thk,thd->tkd", gm, qd)
+    dk.index_add_(0, ii.clamp(min=0).reshape(-1), (contrib * valid[..., None]).reshape(-1, kd.shape[1]))
+    return dq, dk, dw
+
+
+def compute_dsa_indexer_loss_dense(index_scores: torch.Tensor, topk_indices: torch.Tensor, query: torch.Tensor,
+                                   key: torch.Tensor, softmax_scale: float, loss_coeff: float,
+                                   sparse_loss: bool) -> torch.Tensor:
+    """Shape-for-shape restatement of megatron-core's ``compute_dsa_indexer_loss`` (dense form):
+    ``index_scores [B, S, S]`` (with the causal mask added, as ``fused_qk_topk_naive`` returns
+    them), ``topk_indices [B, S, K]``, per-head ``query``/``key [S, B, H, d]`` (detached in the
+    caller).  Target = head-summed fp32 softmax of the causal (+ index, if ``sparse_loss``)
+    masked attention scores, L1-normalised; KL(target || softmax(index_scores)) with 1e-10
+    inside the logs, summed over keys, averaged over (b, s), times ``loss_coeff``."""
+    S, B, H, d = query.shape
+    qf = query.double().permute(1, 2, 0, 3)
+    kf = key.double().permute(1, 2, 3, 0)
+    att = torch.matmul(qf, kf) * softmax_scale                         # [B, H, S, S]
+    causal = torch.triu(torch.full((S, S), NEG_INF, dtype=torch.float64), diagonal=1)
+    att = att + causal
+    isc = index_scores.double()
+    if sparse_loss:
+        imask = torch.full((B, S, S), NEG_INF, dtype=torch.float64).scatter_(-1, topk_indices.long(), 0.0)
+        att = att + imask[:, None]
+        isc = isc + imask
+    att = torch.softmax(att, dim=-1)
+    isc = torch.softmax(isc, dim=-1)
+    att = att.sum(1)
+    att = att / att.sum(-1, keepdim=True)
+    kl = att * (torch.log(att + KL_EPS) - torch.log(isc + KL_EPS))
+    return kl.sum(-1).mean() * loss_coeff

@@ -482,3 +482,92 @@ def test_algorithmic_work_constants():
     assert W.n_pairs([0, 4096]) == 8_390_656
     assert sum(W.CFG5_CACHE_LENS) == 2_724_446
     assert W.n_sel([0, 512], 128) == 57_408
+
+
+# ------------------------------------------------------------------ indexer KL loss
+def _kl_case(g, T=14, H=3, K=5, Hi=4, Di=32):
+    q = torch.randn(T, H, 576, generator=g, dtype=torch.float64) * 0.3
+    kv = torch.randn(T, 576, generator=g, dtype=torch.float64) * 0.3
+    qi = torch.randn(T, Hi, Di, generator=g, dtype=torch.float64)
+    ki = torch.randn(T, Di, generator=g, dtype=torch.float64)
+    w = torch.randn(T, Hi, generator=g, dtype=torch.float64)
+    idx = torch.full((T, K), -1, dtype=torch.int64)
+    for t in range(T):
+        c = torch.randperm(t + 1, generator=g)[:K]
+        idx[t, :len(c)] = c
+    return q, kv, qi, ki, w, idx
+
+
+def test_attention_head_probs_is_the_dense_head_sum():
+    g = torch.Generator().manual_seed(21)
+    q, kv, _, _, _, idx = _kl_case(g)
+    T, H = q.shape[:2]
+    sc = 0.07
+    _, lse = O.sparse_mla_fwd(q, kv, idx, sc)
+    p = O.attention_head_probs(q, kv, idx, lse, sc)
+    # dense per-head softmax under the index + causal mask, summed over heads, L1-normalised
+    sel = torch.zeros(T, T, dtype=torch.bool)
+    for t in range(T):
+        sel[t, idx[t][idx[t] >= 0]] = True
+    s = torch.einsum("thd,sd->hts", q, kv) * sc
+    dense = torch.softmax(s.masked_fill(~sel[None], float("-inf")), -1).sum(0)
+    dense = dense / dense.sum(-1, keepdim=True)
+    ref = torch.where(idx >= 0, torch.gather(dense, 1, idx.clamp(min=0)), torch.zeros_like(p))
+    torch.testing.assert_close(p, ref, rtol=1e-10, atol=1e-13)
+
+
+def test_indexer_kl_sparse_identities_and_gradient():
+    g = torch.Generator().manual_seed(22)
+    T, K = 9, 6
+    I = torch.randn(T, K, generator=g, dtype=torch.float64) * 3
+    valid = torch.rand(T, K, generator=g) > 0.2
+    valid[:, 0] = True
+    p = torch.rand(T, K, generator=g, dtype=torch.float64) * valid
+    p = p / p.sum(-1, keepdim=True)
+    kl, grad = O.indexer_kl_sparse(I, p, valid)
+    assert (kl >= -1e-9).all()
+    # zero when the index distribution is the target
+    pI = torch.softmax(I.masked_fill(~valid, float("-inf")), -1)
+    kl0, grad0 = O.indexer_kl_sparse(I, pI, valid)
+    assert kl0.abs().max() < 1e-8 and grad0.abs().max() < 1e-8
+    # closed-form gradient = autograd of the literal KL
+    Ia = I.clone().requires_grad_()
+    lp = torch.log_softmax(Ia.masked_fill(~valid, float("-inf")), -1)
+    pa = torch.where(valid, lp.exp(), torch.zeros_like(lp))
+    lit = (p * (torch.log(p + 1e-10) - torch.log(pa + 1e-10))).masked_fill(~valid, 0.0).sum()
+    lit.backward()
+    torch.testing.assert_close(grad, torch.where(valid, Ia.grad, torch.zeros_like(grad)), rtol=1e-9, atol=1e-12)
+    torch.testing.assert_close(kl.sum(), lit.detach(), rtol=1e-12, atol=1e-12)
+
+
+def test_indexer_scores_bwd_matches_autograd():
+    g = torch.Generator().manual_seed(23)
+    _, _, qi, ki, w, idx = _kl_case(g)
+    dI = torch.randn(idx.shape, generator=g, dtype=torch.float64)
+    qa, ka, wa = qi.clone().requires_grad_(), ki.clone().requires_grad_(), w.clone().requires_grad_()
+    z = torch.einsum("thd,tkd->thk", qa, ka[idx.clamp(min=0)])
+    I = torch.einsum("th,thk->tk", wa, z.clamp(min=0))
+    (I * torch.where(idx >= 0, dI, torch.zeros_like(dI))).sum().backward()
+    dq, dk, dw = O.indexer_scores_bwd(qi, ki, w, idx, dI)
+    for a, b in ((dq, qa.grad), (dk, ka.grad), (dw, wa.grad)):
+        torch.testing.assert_close(a, b, rtol=1e-10, atol=1e-12)
+
+
+def test_sparse_kl_decomposition_equals_dense_megatron_form():
+    # target x sparse KL over the selected slots == the literal dense restatement with
+    # sparse_loss (MQA form: every head's key is the shared latent row)
+    g = torch.Generator().manual_seed(24)
+    q, kv, qi, ki, w, idx = _kl_case(g, K=6)
+    T, H = q.shape[:2]
+    sc, coeff = 0.06, 0.3
+    full = torch.where(torch.arange(T)[None] <= torch.arange(T)[:, None], O.indexer_scores(qi, ki, w),
+                       torch.full((T, T), float("-inf"), dtype=torch.float64))
+    # the dense form needs topk_indices without padding: pad rows with already-selected keys
+    topk = torch.where(idx >= 0, idx, idx[:, :1])
+    ref = O.compute_dsa_indexer_loss_dense(full[None], topk[None], q[:, None], kv[:, None, None].expand(T, 1, H, 576),
+                                           sc, coeff, sparse_loss=True)
+    _, lse = O.sparse_mla_fwd(q, kv, idx, sc)
+    p = O.attention_head_probs(q, kv, idx, lse, sc)
+    valid = idx >= 0
+    kl, _ = O.indexer_kl_sparse(torch.gather(full, 1, idx.clamp(min=0)), p, valid)
+    torch.testing.assert_close(kl.mean() * coeff, ref, rtol=1e-9, atol=1e-12)
