@@ -158,6 +158,44 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
                              float* dkv, void* workspace, size_t workspace_bytes,
                              void* const* stage_events, void* stream);
 
+/* ---- Indexer KL loss (dsa_indexer_loss_coeff > 0 with dsa_indexer_use_sparse_loss,
+ * src/mcore_bridge/config/model_config.py:204-205; the loss itself is megatron-core's
+ * compute_dsa_indexer_loss, which the reference runs through torch autograd). ---- */
+
+/* Target of the sparse indexer loss: target[t, j] = (1/H) sum_h exp(sm_scale * q[t,h] .
+ * kv[idx[t,j]] - lse[t,h]) -- the head-summed attention probability of each selected key,
+ * L1-normalised -- recomputed from the sparse forward's lse.  target [total_q, topk] fp32, 0 at
+ * invalid slots.  q, kv, idx, lse as for dsa_sparse_mla_fwd; n_heads <= 128; topk <= 8192. */
+int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, const float* lse, int total_q,
+                          int n_kv, int n_heads, int d_qk, int topk, float sm_scale, int causal, float* target,
+                          void* stream);
+
+/* Per-query KL of the sparse indexer loss and its gradient: with pI = softmax of index_sel over
+ * the valid slots of row t, kl[t] = sum_j target (ln(target + 1e-10) - ln(pI + 1e-10)) and
+ * d_index[t, j] = grad_scale * d kl[t] / d index_sel[t, j] (0 at invalid slots).  The loss of the
+ * reference is coeff * mean_t kl[t]: pass grad_scale = coeff * dL / total_q. */
+int dsa_indexer_kl_loss(const float* index_sel, const float* target, const int32_t* idx, int total_q, int n_kv,
+                        int topk, int causal, float grad_scale, float* kl, float* d_index, void* stream);
+
+/* Indexer scores of the selected slots (the values fused_qk_topk_naive, patcher.py:338-376,
+ * scores at the keys its top-k keeps): scores[t, j] = sum_h w[t,h] relu(q[t,h] . k[idx[t,j]]),
+ * -inf at invalid slots.  q [total_q, n_heads, 128] bf16, k [n_k, 128] bf16, w [total_q,
+ * n_heads] fp32 (the prologue's w_out), idx [total_q, topk]; n_heads <= 64, topk <= 4096. */
+int dsa_indexer_selected_scores(const void* q, const void* k, const float* w, const int32_t* idx, int total_q,
+                                int n_k, int n_heads, int head_dim, int topk, int causal, float* scores,
+                                void* stream);
+
+/* Workspace bytes for dsa_indexer_scores_bwd. */
+size_t dsa_indexer_scores_bwd_workspace_size(int total_q, int n_k, int topk);
+
+/* Backward of dsa_indexer_selected_scores (replaces torch autograd through the indexer scores
+ * of patcher.py:338-376 for the selected slots) given d_index = dL/dscores [total_q, topk]:
+ * dq [total_q, n_heads, 128] fp32, dw [total_q, n_heads] fp32, dk [n_k, 128] fp32 (every row
+ * written; rows no query selected are zero).  Shapes and limits as for the forward. */
+int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const int32_t* idx, const float* d_index,
+                           int total_q, int n_k, int n_heads, int head_dim, int topk, int causal, float* dq,
+                           float* dw, float* dk, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

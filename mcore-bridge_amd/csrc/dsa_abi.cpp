@@ -39,6 +39,21 @@ BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
   return L;
 }
 
+struct IdxBwdLayout {
+  size_t g_stage, pair_pos, offsets, counts, total;
+};
+
+IdxBwdLayout idx_bwd_layout(int total_q, int n_k, int topk) {
+  IdxBwdLayout L{};
+  size_t off = 0;
+  L.g_stage = off; off += align_up(sizeof(uint16_t) * ((size_t)total_q * topk + 1) * 128);
+  L.pair_pos = off; off += align_up(sizeof(int64_t) * (size_t)total_q * topk);
+  L.offsets = off; off += align_up(sizeof(int64_t) * ((size_t)n_k + 1));
+  L.counts = off; off += align_up(sizeof(int32_t) * (size_t)n_k);
+  L.total = off;
+  return L;
+}
+
 // Decode key splits: enough (sequence, split) work items to give every CU one workgroup
 // (the forward kernel holds one workgroup per CU), at least 4 key blocks of 32 per split.
 struct DecodeSplit {
@@ -280,6 +295,85 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
     for (int i = 0; i < 6; ++i)
       if (!stage_events[i]) return DSA_ERR_INVALID_ARG;
   return dsa::launch_sparse_mla_bwd(p, as_stream(stream), reinterpret_cast<hipEvent_t const*>(stage_events));
+}
+
+int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, const float* lse, int total_q,
+                          int n_kv, int n_heads, int d_qk, int topk, float sm_scale, int causal, float* target,
+                          void* stream) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
+    return DSA_ERR_INVALID_ARG;
+  if (d_qk != kDqk) return DSA_ERR_UNSUPPORTED;
+  if (n_heads > 128) return DSA_ERR_UNSUPPORTED;
+  if (total_q == 0) return DSA_OK;
+  if (!q || !kv || !idx || !lse || !target || n_kv < 1) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(kv)) return DSA_ERR_INVALID_ARG;
+  dsa::KlTargetParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.kv = static_cast<const dsa::bf16_t*>(kv);
+  p.idx = idx; p.lse = lse; p.target = target;
+  p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.causal = causal ? 1 : 0;
+  p.q_stride_t = (int64_t)n_heads * kDqk; p.idx_stride = topk; p.lse_stride_t = n_heads; p.target_stride = topk;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  return dsa::launch_indexer_kl_target(p, as_stream(stream));
+}
+
+int dsa_indexer_kl_loss(const float* index_sel, const float* target, const int32_t* idx, int total_q, int n_kv,
+                        int topk, int causal, float grad_scale, float* kl, float* d_index, void* stream) {
+  if (total_q < 0 || n_kv < 0 || topk < 1 || !std::isfinite(grad_scale)) return DSA_ERR_INVALID_ARG;
+  if (total_q == 0) return DSA_OK;
+  if (!index_sel || !target || !idx || !kl || !d_index) return DSA_ERR_INVALID_ARG;
+  dsa::KlLossParams p{};
+  p.index_sel = index_sel; p.target = target; p.idx = idx; p.kl = kl; p.d_index = d_index;
+  p.total_q = total_q; p.topk = topk; p.n_kv = n_kv; p.causal = causal ? 1 : 0;
+  p.index_stride = topk; p.target_stride = topk; p.idx_stride = topk; p.d_stride = topk;
+  p.grad_scale = grad_scale;
+  return dsa::launch_indexer_kl(p, as_stream(stream));
+}
+
+int dsa_indexer_selected_scores(const void* q, const void* k, const float* w, const int32_t* idx, int total_q,
+                                int n_k, int n_heads, int head_dim, int topk, int causal, float* scores,
+                                void* stream) {
+  if (total_q < 0 || n_k < 0 || n_heads < 1 || topk < 1) return DSA_ERR_INVALID_ARG;
+  if (head_dim != 128 || n_heads > 64 || topk > 4096) return DSA_ERR_UNSUPPORTED;
+  if (total_q == 0) return DSA_OK;
+  if (!q || !k || !w || !idx || !scores || n_k < 1) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(k)) return DSA_ERR_INVALID_ARG;
+  dsa::IdxSelParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.k = static_cast<const dsa::bf16_t*>(k);
+  p.w = w; p.idx = idx; p.scores = scores;
+  p.total_q = total_q; p.n_heads = n_heads; p.n_k = n_k; p.topk = topk; p.causal = causal ? 1 : 0;
+  p.q_stride_t = (int64_t)n_heads * head_dim; p.idx_stride = topk; p.scores_stride = topk;
+  return dsa::launch_indexer_selected_scores(p, as_stream(stream));
+}
+
+size_t dsa_indexer_scores_bwd_workspace_size(int total_q, int n_k, int topk) {
+  if (total_q < 0 || n_k < 0 || topk < 1) return 0;
+  return idx_bwd_layout(total_q, n_k, topk).total;
+}
+
+int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const int32_t* idx, const float* d_index,
+                           int total_q, int n_k, int n_heads, int head_dim, int topk, int causal, float* dq,
+                           float* dw, float* dk, void* workspace, size_t workspace_bytes, void* stream) {
+  if (total_q < 0 || n_k < 1 || n_heads < 1 || topk < 1) return DSA_ERR_INVALID_ARG;
+  if (head_dim != 128 || n_heads > 64 || topk > 4096) return DSA_ERR_UNSUPPORTED;
+  if (!q || !k || !w || !idx || !d_index || !dq || !dw || !dk) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(dq)) return DSA_ERR_INVALID_ARG;
+  const IdxBwdLayout L = idx_bwd_layout(total_q, n_k, topk);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  dsa::IdxSelParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.k = static_cast<const dsa::bf16_t*>(k);
+  p.w = w; p.idx = idx; p.d_index = d_index; p.dq = dq; p.dw = dw; p.dk = dk;
+  p.g_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.g_stage);
+  p.g_sink_row = (int64_t)total_q * topk;
+  p.pair_pos = reinterpret_cast<int64_t*>(ws + L.pair_pos);
+  p.csr_offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
+  p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);
+  p.total_q = total_q; p.n_heads = n_heads; p.n_k = n_k; p.topk = topk; p.causal = causal ? 1 : 0;
+  p.q_stride_t = (int64_t)n_heads * head_dim; p.idx_stride = topk; p.d_stride = topk;
+  return dsa::launch_indexer_scores_bwd(p, as_stream(stream));
 }
 
 }  // extern "C"

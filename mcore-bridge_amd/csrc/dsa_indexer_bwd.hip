@@ -1,0 +1,406 @@
+// Lightning-indexer scores of the selected slots and their backward (gfx950).
+//
+//   I[t, j] = sum_h w[t,h] relu(q[t,h] . k[idx[t,j]])          (the reference's index scores,
+//             src/mcore_bridge/patcher.py:338-376 fused_qk_topk_naive, read at the top-k slots)
+//   dq[t,h] = w[t,h] sum_j dI[t,j] 1[z>0] k_j,   dw[t,h] = sum_j dI[t,j] relu(z),
+//   dk[s]   = sum over pairs (t, j) selecting s of sum_h dI[t,j] 1[z>0] w[t,h] q[t,h]
+// with z = q[t,h] . k[idx[t,j]] (bf16 operands, fp32 accumulation).  dI comes from the sparse
+// indexer KL loss (dsa_indexer_kl.hip); the reference trains the indexer with that loss
+// (dsa_indexer_loss_coeff, src/mcore_bridge/config/model_config.py:204-205) through torch
+// autograd, which this replaces.
+//
+// One workgroup (4 waves) per query; wave w takes the query's 32-key blocks w, w + 4, .., each
+// gathered into a wave-private double-buffered LDS tile by asynchronous global_load_lds copies
+// (so the loop has no workgroup barrier).  Per block, from the same K fragments:
+//   Z   = Q . K^T     (lane = key, 16 heads per lane)   -> scores, and G = dI_j 1[z>0]
+//   Z^T = K . Q^T     (lane = head, 16 keys per lane)   -> G^T and dw
+//   dq^T += K^T . G^T                  (K^T by transposing LDS reads; 128 AGPR accumulators)
+//   c^T  = (wQ)^T . G                  (the pair's dk row, w folded into a bf16 copy of Q in LDS)
+// c^T goes out through the block's own LDS tile (transposed to 256-byte rows) to the pair's
+// key-major row of a staging buffer; a second kernel sums every key's rows (no float atomics:
+// see the sparse MLA backward for the measured atomic rate).  The forward (scores only) runs the
+// Z product alone.
+//
+// LDS rows are 256 bytes (one key or one head, 128 bf16); 16-byte chunk c of row r sits at slot
+// c ^ swz(r), swz(r) = 2 (r & 3) + ((r >> 2) & 1): the Z operand read (8 consecutive keys, one
+// chunk) and the transposing read (4 consecutive keys x 2 chunks per 16 lanes) are then
+// conflict free.
+#include "dsa_common.h"
+#include "dsa_kernels.h"
+#include "dsa_kvtile.h"
+
+namespace dsa {
+
+namespace {
+
+constexpr int kDi = 128;
+constexpr int kHi = 64;
+constexpr int kRowB = kDi * 2;
+constexpr int kKTile = 32 * kRowB;
+constexpr int kMaxTopkIdx = 4096;
+constexpr int kPreI = 3;
+constexpr int kStoresPerBlock = 8;   // global stores of one block's dk rows (16 B per lane each)
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+DSA_DEV u32x2 lds_read_tr16(uint32_t a) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr(a)));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+DSA_DEV constexpr uint32_t swz(uint32_t r) { return ((r & 3u) << 1) | ((r >> 2) & 1u); }
+
+struct IdxSmem {
+  union {
+    struct {
+      char tile[4][2][kKTile];   // per-wave double-buffered K tiles
+      char qw[kHi * kRowB];      // backward: bf16(w_h q_h) rows
+    };
+    float part[4][kHi][68];      // backward epilogue: per-wave dq partials of 64 dims
+  };
+  int32_t idx[kMaxTopkIdx];
+  float row[kMaxTopkIdx];        // backward: dI (0 at invalid slots); forward: the scores
+  int32_t pos[kMaxTopkIdx];      // backward: staging row of each pair
+  float dwp[4][kHi];
+  int red[4];
+};
+static_assert(sizeof(IdxSmem) <= 160 * 1024, "indexer backward LDS budget");
+
+}  // namespace
+
+template <bool kBwd>
+__global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
+  __shared__ __attribute__((aligned(256))) IdxSmem sm;
+  const int t = xcd_remap(blockIdx.x);
+  if (t >= p.total_q) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hb = lane >> 5, hl = lane & 31;
+  const int nblk = stage_index_row<4>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_k, p.causal, t);
+  const int kpad = nblk * 32;
+
+  // Q fragments (A of Z, B of Z^T): head 32 mh + hl, dims 16 ks + 8 hb .. +7
+  const bf16_t* qt_row = p.q + (int64_t)t * p.q_stride_t;
+  u32x4 qf[2][8];
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh) {
+    const int head = 32 * mh + hl;
+    const bool ok = head < p.n_heads;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const u32x4 v = gload16(qt_row + (ok ? head : 0) * kDi + 16 * ks + 8 * hb);
+      qf[mh][ks] = ok ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+  const float* wrow = p.w + (int64_t)t * p.n_heads;
+  float wz[2][16];   // forward: weights of the Z rows (heads (i/4)*8 + 4 hb + i%4 of tile mh)
+  if (!kBwd) {
+#pragma unroll
+    for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int h = 32 * mh + (i >> 2) * 8 + 4 * hb + (i & 3);
+        wz[mh][i] = h < p.n_heads ? wrow[h] : 0.f;
+      }
+  } else {
+    // dI and the staging row of every slot; the w-scaled Q rows
+    const float* drow = p.d_index + (int64_t)t * p.d_stride;
+    const int64_t* prow = p.pair_pos + (int64_t)t * p.topk;
+    for (int j = threadIdx.x; j < kpad; j += 256) {
+      const bool ok = sm.idx[j] >= 0;
+      sm.row[j] = ok ? drow[j] : 0.f;
+      const int64_t ps = ok ? prow[j] : -1;
+      sm.pos[j] = (int32_t)(ps >= 0 ? ps : p.g_sink_row);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int cid = threadIdx.x + 256 * r;
+      const int h = cid >> 4, c = cid & 15;
+      const bool ok = h < p.n_heads;
+      const u32x4 v = gload16(qt_row + (ok ? h : 0) * kDi + 8 * c);
+      const float wh = ok ? wrow[h] : 0.f;
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(wh * bf16_lo(v[e]), wh * bf16_hi(v[e]));
+      lds_store16(const_cast<char*>(&sm.qw[h * kRowB + 16 * (c ^ swz(h))]), o);
+    }
+  }
+  wait_vmcnt0();   // every compiler-visible load retired before the asynchronous copies start
+  __syncthreads();
+
+  const uint32_t tiles = lds_addr(sm.tile[wave][0]);
+  const uint32_t qw0 = lds_addr(sm.qw);
+  // gather of block blk into the tile at LDS address buf: copy r moves keys 4r .. 4r+3, lane l
+  // filling slot l & 15 of key 4r + l / 16 from that key's chunk (l & 15) ^ swz(key)
+  auto gather = [&](uint32_t buf, int blk) {
+    const int kk0 = lane >> 4;
+    const uint32_t sl = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int kk = 4 * r + kk0;
+      const int row = sm.idx[blk * 32 + kk];
+      const char* src = reinterpret_cast<const char*>(p.k) + (int64_t)(row >= 0 ? row : 0) * kRowB +
+                        16u * (sl ^ swz(kk));
+      async_copy16_unordered(src, buf + 1024u * r);
+    }
+  };
+  // Z operand: key hl, chunk 2 ks + hb -> (tile + zoff) ^ 32 ks
+  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz(hl));
+  // transposing reads (A of dq^T / c^T): 16-lane group g, lane gi feeds row 16a + 8h + 4(g/2) +
+  // gi/4 (the C-layout row order of Z^T / Z) and dims 32m + 16(g%2) + 4(gi%4); m&1 selects the
+  // precomputed slot, m>>1 adds 128 bytes
+  uint32_t troff[2][2][2];
+  {
+    const int g = lane >> 4, gi = lane & 15;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int m1 = 0; m1 < 2; ++m1) {
+          const uint32_t key = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
+          const uint32_t cp = 2 * (g & 1) + ((gi >> 1) & 1);
+          troff[a][h][m1] = key * kRowB + 16u * ((4u * m1) ^ cp ^ swz(key)) + 8u * (gi & 1);
+        }
+  }
+
+  f32x16 dqa[4][2];
+  float dwacc[2] = {0.f, 0.f};
+  if (kBwd) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) dqa[m][n] = f32x16{};
+  }
+
+  if (wave < nblk) gather(tiles, wave);
+  int it = 0;
+  for (int blk = wave; blk < nblk; blk += 4, ++it) {
+    const uint32_t tb = tiles + (it & 1) * kKTile;
+    // block blk's copies were issued before the previous block's dk row stores
+    if (kBwd && it > 0) wait_vmcnt<kStoresPerBlock>();
+    else wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    if (blk + 4 < nblk) gather(tiles + ((it + 1) & 1) * kKTile, blk + 4);
+
+    // ---- Z (and Z^T): 8 k-steps of 16 dims, K fragments prefetched
+    f32x16 z[2], zt[2];
+    {
+      uint32_t zb = tb + zoff;
+      asm volatile("" : "+v"(zb));
+      u32x4 kf[kPreI];
+#pragma unroll
+      for (int i = 0; i < kPreI; ++i) kf[i] = lds_load16(lds_ptr(zb ^ (32u * i)));
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const u32x4 cur = kf[ks % kPreI];
+        if (ks + kPreI < 8) kf[ks % kPreI] = lds_load16(lds_ptr(zb ^ (32u * (ks + kPreI))));
+        if (ks == 0) {
+          mfma32x32x16_cV_first(z[0], qf[0][0], cur);
+          mfma32x32x16_cV_first(z[1], qf[1][0], cur);
+          if (kBwd) {
+            mfma32x32x16_cV_first(zt[0], cur, qf[0][0]);
+            mfma32x32x16_cV_first(zt[1], cur, qf[1][0]);
+          }
+        } else {
+          mfma32x32x16_cV(z[0], qf[0][ks], cur);
+          mfma32x32x16_cV(z[1], qf[1][ks], cur);
+          if (kBwd) {
+            mfma32x32x16_cV(zt[0], cur, qf[0][ks]);
+            mfma32x32x16_cV(zt[1], cur, qf[1][ks]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    mfma_acc_drain();
+
+    if (!kBwd) {
+      float sc = 0.f;
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc = __builtin_fmaf(wz[mh][i], fmaxf(z[mh][i], 0.f), sc);
+      sc += __shfl_xor(sc, 32, 64);
+      if (hb == 0) sm.row[blk * 32 + hl] = sm.idx[blk * 32 + hl] >= 0 ? sc : -INFINITY;
+      continue;
+    }
+
+    // ---- G^T (from Z^T: lane = head, rows = keys) and dw; G (from Z: lane = key, rows = heads)
+    const float d_own = sm.row[blk * 32 + hl];
+    float dr[16];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sm.row[blk * 32 + gq * 8 + 4 * hb]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dr[4 * gq + e] = v[e];
+    }
+    u32x4 gt[2][2], gz[2][2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      float dws = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float a0 = zt[n][i] > 0.f ? dr[i] : 0.f, a1 = zt[n][i + 1] > 0.f ? dr[i + 1] : 0.f;
+        gt[n][i >> 3][(i & 7) >> 1] = pack_bf16x2(a0, a1);
+        dws = __builtin_fmaf(dr[i], fmaxf(zt[n][i], 0.f), dws);
+        dws = __builtin_fmaf(dr[i + 1], fmaxf(zt[n][i + 1], 0.f), dws);
+        const float b0 = z[n][i] > 0.f ? d_own : 0.f, b1 = z[n][i + 1] > 0.f ? d_own : 0.f;
+        gz[n][i >> 3][(i & 7) >> 1] = pack_bf16x2(b0, b1);
+      }
+      dwacc[n] += dws;
+    }
+
+    // ---- dq^T[dims x heads] += K^T . G^T
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        const uint32_t o = 128u * (mm >> 1);
+        const u32x2 lo = lds_read_tr16(tb + troff[a][0][mm & 1] + o);
+        const u32x2 hi = lds_read_tr16(tb + troff[a][1][mm & 1] + o);
+        const u32x4 kt = u32x4{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int n = 0; n < 2; ++n) mfma32x32x16_cA(dqa[mm][n], kt, gt[n][a]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+
+    // ---- c^T[dims x keys] = (wQ)^T . G, staged as 256-byte key rows in this block's tile
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      f32x16 c;
+      const uint32_t o = 128u * (mt >> 1);
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const uint32_t base = qw0 + mh * kKTile + o;
+          const u32x2 lo = lds_read_tr16(base + troff[s][0][mt & 1]);
+          const u32x2 hi = lds_read_tr16(base + troff[s][1][mt & 1]);
+          const u32x4 qa = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          if (mh == 0 && s == 0) mfma32x32x16_cV_first(c, qa, gz[mh][s]);
+          else mfma32x32x16_cV(c, qa, gz[mh][s]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      mfma_acc_drain();
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const u32x2 v = u32x2{pack_bf16x2(c[4 * gq], c[4 * gq + 1]), pack_bf16x2(c[4 * gq + 2], c[4 * gq + 3])};
+        *reinterpret_cast<u32x2*>(const_cast<char*>(lds_ptr(tb + hl * kRowB + 16u * ((4u * mt + gq) ^ swz(hl)) + 8u * hb))) = v;
+      }
+    }
+    // ---- key rows out: copy s writes keys 4s .. 4s+3, 16 lanes per 256-byte row
+    {
+      const uint32_t sl = lane & 15;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int r = 4 * s + (lane >> 4);
+        const u32x4 v = lds_load16(lds_ptr(tb + r * kRowB + 16u * sl));
+        const int64_t grow = sm.pos[blk * 32 + r];
+        *reinterpret_cast<u32x4*>(p.g_stage + grow * kDi + 8 * (sl ^ swz(r))) = v;
+      }
+    }
+  }
+
+  if (!kBwd) {
+    __syncthreads();
+    float* out = p.scores + (int64_t)t * p.scores_stride;
+    for (int j = threadIdx.x; j < p.topk; j += 256) out[j] = j < kpad ? sm.row[j] : -INFINITY;
+    return;
+  }
+
+  // ---- epilogue: dw and dq summed over the four waves
+  mfma_acc_drain();
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const float v = xor32_sum(dwacc[n]);
+    if (hb == 0) sm.dwp[wave][32 * n + hl] = v;
+  }
+  __syncthreads();   // every wave is done with its tiles and the Q copy (the union is reused)
+  const int h_red = threadIdx.x >> 2;          // head of this thread's sums
+  const float w_red = h_red < p.n_heads ? wrow[h_red] : 0.f;
+  float* dq_row = p.dq + ((int64_t)t * p.n_heads + h_red) * kDi;
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph) {
+#pragma unroll
+    for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const f32x16& a = dqa[2 * ph + m2][n];
+          *reinterpret_cast<f32x4*>(&sm.part[wave][32 * n + hl][32 * m2 + 8 * gq + 4 * hb]) =
+              f32x4{a[4 * gq], a[4 * gq + 1], a[4 * gq + 2], a[4 * gq + 3]};
+        }
+    __syncthreads();
+    // thread -> (head threadIdx/4, 16 dims); 4 x 4 floats each
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = 16 * (threadIdx.x & 3) + 4 * q4;
+      f32x4 s = *reinterpret_cast<const f32x4*>(&sm.part[0][h_red][d]);
+#pragma unroll
+      for (int w = 1; w < 4; ++w) s += *reinterpret_cast<const f32x4*>(&sm.part[w][h_red][d]);
+      if (h_red < p.n_heads) *reinterpret_cast<f32x4*>(dq_row + 64 * ph + d) = s * w_red;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < p.n_heads) {
+    const int h = threadIdx.x;
+    p.dw[(int64_t)t * p.n_heads + h] = sm.dwp[0][h] + sm.dwp[1][h] + sm.dwp[2][h] + sm.dwp[3][h];
+  }
+}
+
+// dk[s] = sum of the 128-wide rows of key s's segment (fp32).  16 row lanes x 16 chunks.
+__global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stage, const int64_t* offsets, int n_k,
+                                                            float* dk) {
+  __shared__ float red[15][kDi];
+  const int s = blockIdx.x;
+  if (s >= n_k) return;
+  const int c = threadIdx.x & 15, r = threadIdx.x >> 4;
+  const int64_t a = offsets[s], b = offsets[s + 1];
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t i = a + r; i < b; i += 16) {
+    const u32x4 v = gload16(g_stage + i * kDi + c * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] += bf16_lo(v[e]);
+      acc[2 * e + 1] += bf16_hi(v[e]);
+    }
+  }
+  if (r > 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[r - 1][c * 8 + e] = acc[e];
+  }
+  __syncthreads();
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[e];
+#pragma unroll
+      for (int k = 0; k < 15; ++k) v += red[k][c * 8 + e];
+      dk[(int64_t)s * kDi + c * 8 + e] = v;
+    }
+  }
+}
+
+int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream) {
+  if (p.topk > kMaxTopkIdx || p.n_heads > kHi) return -2;
+  if (p.total_q == 0) return 0;
+  hipLaunchKernelGGL(indexer_sel_kernel<false>, dim3(xcd_grid(p.total_q)), dim3(256), 0, stream, p);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream) {
+  if (p.topk > kMaxTopkIdx || p.n_heads > kHi) return -2;
+  if (p.g_sink_row >= INT32_MAX) return -2;   // staging rows are kept in 32 bits
+  if (p.n_k > 0) launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_k, p.causal, p.csr_counts,
+                                 p.csr_offsets, p.pair_pos, stream);
+  if (p.total_q > 0)
+    hipLaunchKernelGGL(indexer_sel_kernel<true>, dim3(xcd_grid(p.total_q)), dim3(256), 0, stream, p);
+  if (p.n_k > 0)
+    hipLaunchKernelGGL(idx_dk_reduce_kernel, dim3(p.n_k), dim3(256), 0, stream, p.g_stage, p.csr_offsets, p.n_k, p.dk);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace dsa

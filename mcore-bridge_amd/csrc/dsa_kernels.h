@@ -87,12 +87,64 @@ struct PrologueParams {
   int64_t q_stride_t, k_stride_t, w_stride_t, freqs_stride_t;
 };
 
+struct KlTargetParams {
+  const bf16_t* q;      // [total_q, n_heads, 576], token stride q_stride_t
+  const bf16_t* kv;     // [n_kv, 576]
+  const int32_t* idx;   // [total_q, topk]
+  const float* lse;     // [total_q, n_heads] natural-log LSE of the sparse forward
+  float* target;        // [total_q, topk] head-averaged probabilities (0 at invalid slots)
+  int total_q, n_heads, n_kv, topk, causal;
+  int64_t q_stride_t, idx_stride, lse_stride_t, target_stride;
+  float scale_log2;     // softmax scale * log2(e)
+};
+
+struct KlLossParams {
+  const float* index_sel;  // [total_q, topk] index scores of the selected slots
+  const float* target;     // [total_q, topk]
+  const int32_t* idx;      // [total_q, topk]
+  float* kl;               // [total_q] per-query KL
+  float* d_index;          // [total_q, topk] grad_scale * d KL_t / d index_sel (0 at invalid slots)
+  int total_q, topk, n_kv, causal;
+  int64_t index_stride, target_stride, idx_stride, d_stride;
+  float grad_scale;
+};
+
+// Indexer scores of the selected slots, I[t, j] = sum_h w[t,h] relu(q[t,h] . k[idx[t,j]]), and
+// their backward (bf16 q / k, head_dim 128, n_heads <= 64).
+struct IdxSelParams {
+  const bf16_t* q;       // [total_q, n_heads, 128], token stride q_stride_t
+  const bf16_t* k;       // [n_k, 128]
+  const float* w;        // [total_q, n_heads]
+  const int32_t* idx;    // [total_q, topk]
+  float* scores;         // forward: [total_q, topk] (-inf at invalid slots)
+  const float* d_index;  // backward: [total_q, topk] dL/dI
+  float* dq;             // backward: [total_q, n_heads, 128] fp32
+  float* dw;             // backward: [total_q, n_heads] fp32
+  float* dk;             // backward: [n_k, 128] fp32 (every row written)
+  // backward workspace
+  bf16_t* g_stage;       // [total_q * topk + 1, 128] per-pair dk rows in key-major order
+  int64_t g_sink_row;    // last row of g_stage (pairs that select nothing)
+  int64_t* pair_pos;     // [total_q, topk]
+  int64_t* csr_offsets;  // [n_k + 1]
+  int32_t* csr_counts;   // [n_k]
+  int total_q, n_heads, n_k, topk, causal;
+  int64_t q_stride_t, idx_stride, scores_stride, d_stride;
+};
+
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
 // ev (nullable): 6 events recorded around the stages B4 | B1 | B2 | B3 | B5.
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev);
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
 int launch_indexer_prologue(const PrologueParams& p, hipStream_t stream);
+int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream);
+int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
+int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);
+int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream);
+// Key-major order of the selected (query, slot) pairs: csr_offsets [n_kv + 1] and the row of
+// every pair, pair_pos [total_q, topk] (-1 = not selected); csr_counts is scratch.
+void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
+                     int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
                           bf16_t* out, float* lse, hipStream_t stream);
 int launch_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,

@@ -127,4 +127,40 @@ DSA_DEV void gather_tile(uint32_t tile, const bf16_t* kv, const int32_t* idx_blk
   }
 }
 
+// Stage the query's index row in LDS (invalid -> -1); returns the number of 32-key blocks up
+// to the last valid entry (workgroup-uniform).  Also retires every outstanding load.
+template <int NW>
+DSA_DEV int stage_index_row(int32_t* idx_s, int* red, const int32_t* idx_row, int topk, int n_kv, int causal,
+                            int t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kpad = (topk + kTileKeys - 1) / kTileKeys * kTileKeys;
+  constexpr int kBatch = 8;   // loads in flight per thread (one memory round trip per batch)
+  int last = -1;
+  for (int j0 = threadIdx.x; j0 < kpad; j0 += kBatch * NW * 64) {
+    int v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int j = j0 + i * NW * 64;
+      v[i] = j < topk ? idx_row[j] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int j = j0 + i * NW * 64;
+      int x = v[i];
+      if (x < 0 || x >= n_kv || (causal && x > t)) x = -1;
+      if (j < kpad) {
+        idx_s[j] = x;
+        if (x >= 0) last = j;
+      }
+    }
+  }
+  last = wave_max_i(last);
+  if (lane == 0) red[wave] = last;
+  wait_vmcnt0();
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) last = max(last, red[w]);
+  return __builtin_amdgcn_readfirstlane((last + kTileKeys) / kTileKeys);
+}
+
 }  // namespace dsa

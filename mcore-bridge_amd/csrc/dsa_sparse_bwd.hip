@@ -53,42 +53,6 @@ DSA_DEV u32x2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-// Stage the query's index row in LDS (invalid -> -1); returns the number of 32-key blocks up
-// to the last valid entry (workgroup-uniform).  Also retires every outstanding load.
-template <int NW>
-DSA_DEV int stage_index_row(int32_t* idx_s, int* red, const int32_t* idx_row, int topk, int n_kv, int causal,
-                            int t) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kpad = (topk + kBK - 1) / kBK * kBK;
-  constexpr int kBatch = 8;   // loads in flight per thread (one memory round trip per batch)
-  int last = -1;
-  for (int j0 = threadIdx.x; j0 < kpad; j0 += kBatch * NW * 64) {
-    int v[kBatch];
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int j = j0 + i * NW * 64;
-      v[i] = j < topk ? idx_row[j] : -1;
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int j = j0 + i * NW * 64;
-      int x = v[i];
-      if (x < 0 || x >= n_kv || (causal && x > t)) x = -1;
-      if (j < kpad) {
-        idx_s[j] = x;
-        if (x >= 0) last = j;
-      }
-    }
-  }
-  last = wave_max_i(last);
-  if (lane == 0) red[wave] = last;
-  wait_vmcnt0();
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < NW; ++w) last = max(last, red[w]);
-  return __builtin_amdgcn_readfirstlane((last + kBK) / kBK);
-}
-
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
@@ -1080,6 +1044,28 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   }
 }
 
+void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
+                     int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_i32_kernel, dim3((n_kv + 255) / 256), dim3(256), 0, stream, csr_counts, n_kv);
+  const int64_t pairs = (int64_t)total_q * topk;
+  const int nb = (int)std::min<int64_t>((pairs + 255) / 256, 65536);
+  const bool lds_csr = n_kv <= kCsrLdsKeys;
+  const int nwg = std::max(1, std::min(kCsrWgs, total_q));
+  if (lds_csr)
+    hipLaunchKernelGGL(csr_count_lds_kernel, dim3(nwg), dim3(1024), 0, stream, idx, idx_stride, total_q,
+                       topk, n_kv, causal, csr_counts);
+  else
+    hipLaunchKernelGGL(csr_count_kernel, dim3(nb), dim3(256), 0, stream, idx, idx_stride, total_q, topk,
+                       n_kv, causal, csr_counts);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, csr_counts, n_kv, csr_offsets);
+  if (lds_csr)
+    hipLaunchKernelGGL(csr_fill_lds_kernel, dim3(nwg), dim3(1024), 0, stream, idx, idx_stride, total_q,
+                       topk, n_kv, causal, csr_offsets, csr_counts, pair_pos);
+  else
+    hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, idx, idx_stride, total_q, topk,
+                       n_kv, causal, csr_offsets, csr_counts, pair_pos);
+}
+
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev) {
   if (p.topk > kMaxTopkBwd) return -2;
   if (p.g_sink_row >= INT32_MAX) return -2;   // B3 keeps G row numbers in 32 bits
@@ -1091,24 +1077,8 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   const dim3 grid(xcd_grid(p.total_q), (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
-  hipLaunchKernelGGL(zero_i32_kernel, dim3((p.n_kv + 255) / 256), dim3(256), 0, stream, p.csr_counts, p.n_kv);
-  const int64_t pairs = (int64_t)p.total_q * p.topk;
-  const int nb = (int)std::min<int64_t>((pairs + 255) / 256, 65536);
-  const bool lds_csr = p.n_kv <= kCsrLdsKeys;
-  const int nwg = std::max(1, std::min(kCsrWgs, p.total_q));
-  if (lds_csr)
-    hipLaunchKernelGGL(csr_count_lds_kernel, dim3(nwg), dim3(1024), 0, stream, p.idx, p.idx_stride, p.total_q,
-                       p.topk, p.n_kv, p.causal, p.csr_counts);
-  else
-    hipLaunchKernelGGL(csr_count_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
-                       p.n_kv, p.causal, p.csr_counts);
-  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, p.csr_counts, p.n_kv, p.csr_offsets);
-  if (lds_csr)
-    hipLaunchKernelGGL(csr_fill_lds_kernel, dim3(nwg), dim3(1024), 0, stream, p.idx, p.idx_stride, p.total_q,
-                       p.topk, p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
-  else
-    hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, p.idx, p.idx_stride, p.total_q, p.topk,
-                       p.n_kv, p.causal, p.csr_offsets, p.csr_counts, p.pair_pos);
+  launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_kv, p.causal, p.csr_counts, p.csr_offsets,
+                  p.pair_pos, stream);
   mark(1);
   if (nw == 4) {
     hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);

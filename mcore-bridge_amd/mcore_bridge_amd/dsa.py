@@ -148,6 +148,42 @@ def indexer_forward_before_topk(x: Tensor, qr: Tensor, wq_b: Tensor, wk: Tensor,
     return q, k, w
 
 
+class _IndexerKL(torch.autograd.Function):
+    """``coeff * mean_t KL_t`` from per-row KLs and their gradients computed in one kernel pass."""
+
+    @staticmethod
+    def forward(ctx, index_sel: Tensor, target: Tensor, idx: Tensor, n_kv: int, causal: bool, coeff: float):
+        T = idx.shape[0]
+        kl, d = ops.indexer_kl_rows(index_sel, target, idx, n_kv, causal, coeff / max(T, 1))
+        ctx.save_for_backward(d)
+        return kl.sum() * (coeff / max(T, 1))
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        (d,) = ctx.saved_tensors
+        return d * g, None, None, None, None, None
+
+
+def indexer_kl_loss(q: Tensor, kv: Tensor, lse: Tensor, topk_indices: Tensor, q_idx: Tensor, k_idx: Tensor,
+                    w: Tensor, softmax_scale: float, loss_coeff: float, causal: bool = True) -> Tensor:
+    """Sparse DSA indexer loss in the packed THD layout (``dsa_indexer_loss_coeff`` with
+    ``dsa_indexer_use_sparse_loss``, reference src/mcore_bridge/config/model_config.py:204-205;
+    megatron-core's ``compute_dsa_indexer_loss`` restricted to the selected keys).
+
+    ``q [T, H, 576]``, ``kv [N, 576]``, ``lse [T, H]`` are the sparse attention's absorbed inputs
+    and forward LSE (``ops.sparse_mla_fwd``; detached, as the reference detaches query and key);
+    ``topk_indices [T, K]`` the indexer's selection; ``q_idx [T, Hi, 128]``, ``k_idx [N, 128]``
+    bf16 and ``w [T, Hi]`` fp32 the indexer's prologue outputs.  The target is the head-summed
+    attention probability of each selected key, L1-normalised; the loss is ``loss_coeff *
+    mean_t KL(target_t || softmax(I_t))`` over the selected keys with ``I`` the indexer scores at
+    those keys, differentiable in ``q_idx``, ``k_idx`` and ``w``."""
+    idx = topk_indices.to(torch.int32)
+    with torch.no_grad():
+        target = ops.indexer_kl_target(q.detach(), kv.detach(), idx, lse.detach(), softmax_scale, causal)
+    index_sel = ops.indexer_selected_scores(q_idx, k_idx, w, idx, causal)
+    return _IndexerKL.apply(index_sel, target, idx, k_idx.shape[0], causal, float(loss_coeff))
+
+
 class _HeadwiseMatmul(torch.autograd.Function):
     """``out[h] = a[h] @ b[h]`` for ``a [H, M, K]``, ``b [H, K, N]``, with every batched product in
     forward and backward fed contiguous operands (no transposed views reach ``torch.bmm``)."""

@@ -346,3 +346,129 @@ torch.library.register_autograd("dsa_amd::sparse_mla_fwd", _fwd_backward, setup_
 def sparse_mla(q: Tensor, kv: Tensor, idx: Tensor, sm_scale: float, causal: bool = False) -> Tensor:
     """Differentiable sparse MLA attention output ``[T, H, 512]``."""
     return sparse_mla_fwd(q, kv, idx, sm_scale, causal)[0]
+
+
+# --------------------------------------------------------------------------------------
+# indexer KL loss: target, per-row KL + gradient, selected-slot scores and their backward
+# --------------------------------------------------------------------------------------
+@torch.library.custom_op("dsa_amd::indexer_kl_target", mutates_args=())
+def indexer_kl_target(q: Tensor, kv: Tensor, idx: Tensor, lse: Tensor, sm_scale: float, causal: bool = True) -> Tensor:
+    """Head-averaged attention probability of every selected key, ``[T, K]`` fp32 (0 at invalid
+    slots), recomputed from the sparse forward's ``lse``: the target of the sparse indexer loss."""
+    _check_attn(q, kv, idx)
+    _require_gpu(lse)
+    q, kv, lse = q.contiguous(), kv.contiguous(), lse.float().contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, H, _ = q.shape
+    _require(lse.shape == (T, H), "lse must be [T, H]")
+    tgt = torch.empty(T, idx.shape[1], dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_indexer_kl_target", _p(q), _p(kv), _p(idx), _p(lse), T, kv.shape[0], H, D_QK, idx.shape[1],
+                  float(sm_scale), int(causal), _p(tgt), _stream(q.device))
+    return tgt
+
+
+@indexer_kl_target.register_fake
+def _(q, kv, idx, lse, sm_scale, causal=True):
+    return q.new_empty(q.shape[0], idx.shape[1], dtype=torch.float32)
+
+
+@torch.library.custom_op("dsa_amd::indexer_kl_rows", mutates_args=())
+def indexer_kl_rows(index_sel: Tensor, target: Tensor, idx: Tensor, n_kv: int, causal: bool,
+                    grad_scale: float) -> Tuple[Tensor, Tensor]:
+    """Per-query KL of the sparse indexer loss, ``kl [T]``, and ``grad_scale * d kl_t / d index_sel``
+    ``[T, K]`` (softmax of the index scores over the valid slots; 1e-10 inside both logs)."""
+    _require_gpu(index_sel, target, idx)
+    index_sel, target = index_sel.float().contiguous(), target.float().contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, K = idx.shape
+    _require(index_sel.shape == (T, K) and target.shape == (T, K), "index_sel and target must be [T, K]")
+    kl = torch.empty(T, dtype=torch.float32, device=idx.device)
+    d = torch.empty(T, K, dtype=torch.float32, device=idx.device)
+    with torch.cuda.device(idx.device):
+        _lib.call("dsa_indexer_kl_loss", _p(index_sel), _p(target), _p(idx), T, int(n_kv), K, int(causal),
+                  float(grad_scale), _p(kl), _p(d), _stream(idx.device))
+    return kl, d
+
+
+@indexer_kl_rows.register_fake
+def _(index_sel, target, idx, n_kv, causal, grad_scale):
+    T, K = idx.shape
+    return idx.new_empty(T, dtype=torch.float32), idx.new_empty(T, K, dtype=torch.float32)
+
+
+def _check_idx_sel(q: Tensor, k: Tensor, w: Tensor, idx: Tensor) -> None:
+    _require_gpu(q, k, w, idx)
+    _require(q.dim() == 3 and q.shape[-1] == 128 and q.dtype == torch.bfloat16, "q must be [T, Hi, 128] bf16")
+    _require(k.dim() == 2 and k.shape[-1] == 128 and k.dtype == torch.bfloat16, "k must be [N, 128] bf16")
+    _require(w.shape == q.shape[:2], "w must be [T, Hi]")
+    _require(idx.dim() == 2 and idx.shape[0] == q.shape[0], "idx must be [T, K]")
+
+
+@torch.library.custom_op("dsa_amd::indexer_selected_scores", mutates_args=())
+def indexer_selected_scores(q: Tensor, k: Tensor, w: Tensor, idx: Tensor, causal: bool = True) -> Tensor:
+    """Indexer scores of the selected slots, ``sum_h w[t,h] relu(q[t,h] . k[idx[t,j]])`` ``[T, K]``
+    fp32 (-inf at invalid slots); differentiable in q, k and w."""
+    _check_idx_sel(q, k, w, idx)
+    q, k, w = q.contiguous(), k.contiguous(), w.float().contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, Hi, _ = q.shape
+    sc = torch.empty(T, idx.shape[1], dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_indexer_selected_scores", _p(q), _p(k), _p(w), _p(idx), T, k.shape[0], Hi, 128,
+                  idx.shape[1], int(causal), _p(sc), _stream(q.device))
+    return sc
+
+
+@indexer_selected_scores.register_fake
+def _(q, k, w, idx, causal=True):
+    return q.new_empty(q.shape[0], idx.shape[1], dtype=torch.float32)
+
+
+def indexer_scores_bwd_workspace_bytes(total_q: int, n_k: int, topk_: int) -> int:
+    return int(_lib.load().dsa_indexer_scores_bwd_workspace_size(total_q, n_k, topk_))
+
+
+@torch.library.custom_op("dsa_amd::indexer_scores_bwd", mutates_args=())
+def indexer_scores_bwd(q: Tensor, k: Tensor, w: Tensor, idx: Tensor, d_scores: Tensor,
+                       causal: bool = True) -> Tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``indexer_selected_scores``: ``(dq [T,Hi,128], dw [T,Hi], dk [N,128])`` fp32."""
+    _check_idx_sel(q, k, w, idx)
+    _require_gpu(d_scores)
+    q, k, w = q.contiguous(), k.contiguous(), w.float().contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    d_scores = d_scores.float().contiguous()
+    T, Hi, _ = q.shape
+    N, K = k.shape[0], idx.shape[1]
+    _require(d_scores.shape == (T, K), "d_scores must be [T, K]")
+    dq = torch.empty(T, Hi, 128, dtype=torch.float32, device=q.device)
+    dw = torch.empty(T, Hi, dtype=torch.float32, device=q.device)
+    dk = torch.empty(N, 128, dtype=torch.float32, device=q.device)
+    ws_bytes = indexer_scores_bwd_workspace_bytes(T, N, K)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_indexer_scores_bwd", _p(q), _p(k), _p(w), _p(idx), _p(d_scores), T, N, Hi, 128, K,
+                  int(causal), _p(dq), _p(dw), _p(dk), _p(ws), ws_bytes, _stream(q.device))
+    return dq, dw, dk
+
+
+@indexer_scores_bwd.register_fake
+def _(q, k, w, idx, d_scores, causal=True):
+    T, Hi, _ = q.shape
+    return (q.new_empty(T, Hi, 128, dtype=torch.float32), q.new_empty(T, Hi, dtype=torch.float32),
+            k.new_empty(k.shape[0], 128, dtype=torch.float32))
+
+
+def _sel_setup(ctx, inputs, output):
+    q, k, w, idx, causal = inputs
+    ctx.save_for_backward(q, k, w, idx)
+    ctx.causal = causal
+
+
+def _sel_backward(ctx, d_scores):
+    q, k, w, idx = ctx.saved_tensors
+    dq, dw, dk = indexer_scores_bwd(q, k, w, idx, d_scores, ctx.causal)
+    return dq.to(q.dtype), dk.to(k.dtype), dw.to(w.dtype), None, None
+
+
+torch.library.register_autograd("dsa_amd::indexer_selected_scores", _sel_backward, setup_context=_sel_setup)

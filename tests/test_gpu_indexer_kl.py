@@ -1,0 +1,166 @@
+"""GPU parity of the sparse indexer KL loss path (target, per-row KL + gradient, selected-slot
+indexer scores and their backward) against the CPU oracle, through the C ABI.
+
+Bars as for the attention kernels: rtol / atol 2e-2 plus a normalised-error check against the
+float64 oracle on the same bf16 inputs; the end-to-end loss and its gradients are checked against
+torch autograd through the literal dense restatement of megatron-core's compute_dsa_indexer_loss.
+"""
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from mcore_bridge_amd import ops, workloads as W
+from mcore_bridge_amd.dsa import indexer_kl_loss
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL = ATOL = 2e-2
+
+
+def _close(got, ref, rel=1e-2, name="", atol=ATOL):
+    got = got.double().cpu()
+    ref = ref.double().cpu()
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=atol, msg=lambda m: f"{name}: {m}")
+    err = (got - ref).norm() / ref.norm().clamp_min(1e-30)
+    assert err < rel, f"{name}: normalised error {err:.3e} >= {rel}"
+
+
+def _idx_case(T, K, g, pad=0.1, cu=None):
+    vis = O.visibility_mask(T, None if cu is None else torch.tensor(cu, dtype=torch.int32), True)
+    idx = torch.full((T, K), -1, dtype=torch.int32)
+    for t in range(T):
+        cand = torch.nonzero(vis[t]).flatten()
+        cand = cand[torch.randperm(cand.numel(), generator=g)][:K]
+        m = cand.numel()
+        if t % 5 == 0:
+            m = max(1, int(m * (1 - pad)))
+        idx[t, :m] = torch.sort(cand[:m]).values.to(torch.int32)
+    return idx
+
+
+def _indexer_inputs(T, Hi, g, scale=0.3):
+    qi = (torch.randn(T, Hi, 128, generator=g) * scale).bfloat16()
+    ki = (torch.randn(T, 128, generator=g) * scale).bfloat16()
+    w = (torch.randn(T, Hi, generator=g) * 0.1).bfloat16().float()
+    return qi, ki, w
+
+
+@pytest.mark.parametrize("T,H,K", [(300, 128, 256), (200, 16, 128), (130, 64, 100), (520, 128, 512)])
+def test_indexer_kl_target(T, H, K):
+    print(f"[kl target] T={T} H={H} K={K}", flush=True)
+    g = torch.Generator().manual_seed(T + K)
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16()
+    idx = _idx_case(T, K, g, cu=[0, T // 3, T])
+    _, lse = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE, True)
+    tgt = ops.indexer_kl_target(q.to(DEV), kv.to(DEV), idx.to(DEV), lse, W.SM_SCALE, True).cpu()
+    ref = O.attention_head_probs(q, kv, idx, lse.cpu(), W.SM_SCALE)
+    _close(tgt, ref, rel=2e-3, name="target", atol=1e-4)
+    valid = idx >= 0
+    assert torch.all(tgt[~valid] == 0)
+    # every head's probabilities over the selected keys sum to one, so each target row does too
+    torch.testing.assert_close(tgt.double().sum(-1), torch.ones(T, dtype=torch.float64), rtol=0, atol=2e-3)
+
+
+def test_indexer_kl_target_noncausal_and_empty_rows():
+    print("[kl target] non-causal, empty rows", flush=True)
+    g = torch.Generator().manual_seed(5)
+    T, H, K = 96, 32, 64
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16()
+    idx = torch.stack([torch.randperm(T, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[3] = -1
+    idx[7, ::2] = -1
+    _, lse = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE, False)
+    tgt = ops.indexer_kl_target(q.to(DEV), kv.to(DEV), idx.to(DEV), lse, W.SM_SCALE, False).cpu()
+    ref = O.attention_head_probs(q, kv, idx, lse.cpu(), W.SM_SCALE)
+    _close(tgt, ref, rel=2e-3, name="target", atol=1e-4)
+    assert torch.all(tgt[3] == 0)
+
+
+@pytest.mark.parametrize("T,K", [(200, 128), (64, 2048), (300, 33)])
+def test_indexer_kl_rows(T, K):
+    print(f"[kl rows] T={T} K={K}", flush=True)
+    g = torch.Generator().manual_seed(11 + K)
+    idx = torch.stack([torch.randperm(max(T, K), generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[torch.rand(T, K, generator=g) < 0.1] = -1
+    idx[4] = -1
+    n_kv = max(T, K)
+    valid = idx >= 0
+    index_sel = torch.randn(T, K, generator=g) * 2
+    p = torch.rand(T, K, generator=g).double() * valid
+    p[2, :] = 0
+    p[2, 0] = 1.0 if valid[2, 0] else 0.0
+    p = p / p.sum(-1, keepdim=True).clamp_min(1e-30)
+    gs = 0.37
+    kl, d = ops.indexer_kl_rows(index_sel.to(DEV), p.float().to(DEV), idx.to(DEV), n_kv, False, gs)
+    rkl, rd = O.indexer_kl_sparse(index_sel.double(), p.float().double(), valid)
+    torch.testing.assert_close(kl.cpu().double(), rkl, rtol=1e-4, atol=1e-5)
+    _close(d.cpu(), rd * gs, rel=1e-4, name="d_index", atol=1e-6)
+    assert kl[4].item() == 0 and torch.all(d[4] == 0)
+
+
+@pytest.mark.parametrize("T,Hi,K,cu", [(300, 64, 256, [0, 300]), (200, 4, 128, [0, 90, 200]),
+                                       (260, 64, 2048, [0, 260]), (150, 33, 96, [0, 150])])
+def test_indexer_selected_scores(T, Hi, K, cu):
+    print(f"[selected scores] T={T} Hi={Hi} K={K}", flush=True)
+    g = torch.Generator().manual_seed(T + Hi)
+    qi, ki, w = _indexer_inputs(T, Hi, g)
+    idx = _idx_case(T, K, g, cu=cu)
+    got = ops.indexer_selected_scores(qi.to(DEV), ki.to(DEV), w.to(DEV), idx.to(DEV), True).cpu()
+    dense = O.indexer_scores(qi, ki, w, torch.tensor(cu, dtype=torch.int32), True)
+    valid = idx >= 0
+    ref = torch.gather(dense, 1, idx.clamp(min=0).long())
+    assert torch.all(torch.isneginf(got[~valid]))
+    _close(got[valid], ref[valid], rel=1e-4, name="scores", atol=1e-4)
+
+
+@pytest.mark.parametrize("T,Hi,K", [(300, 64, 256), (200, 4, 128), (160, 64, 2048), (130, 48, 100)])
+def test_indexer_scores_bwd(T, Hi, K):
+    print(f"[indexer scores bwd] T={T} Hi={Hi} K={K}", flush=True)
+    g = torch.Generator().manual_seed(3 * T + Hi)
+    qi, ki, w = _indexer_inputs(T, Hi, g)
+    idx = _idx_case(T, K, g, cu=[0, T // 2, T])
+    dI = torch.randn(T, K, generator=g) * 0.01
+    dq, dw, dk = ops.indexer_scores_bwd(qi.to(DEV), ki.to(DEV), w.to(DEV), idx.to(DEV), dI.to(DEV), True)
+    rq, rk, rw = O.indexer_scores_bwd(qi, ki, w, idx, dI)
+    _close(dq.cpu(), rq, name="dq")
+    _close(dw.cpu(), rw, name="dw")
+    _close(dk.cpu(), rk, name="dk")
+    never = torch.ones(T, dtype=torch.bool)
+    never[idx[idx >= 0].long()] = False
+    assert torch.all(dk.cpu()[never] == 0)
+
+
+def test_indexer_kl_loss_end_to_end_against_dense_megatron_form():
+    """Loss and gradients (q_idx, k_idx, w) of the sparse path against torch autograd through the
+    float64 dense restatement of compute_dsa_indexer_loss with sparse_loss (MQA form: every head's
+    key is the shared latent row)."""
+    print("[indexer kl loss e2e]", flush=True)
+    g = torch.Generator().manual_seed(17)
+    T, H, Hi, K = 256, 32, 64, 64
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16()
+    qi, ki, w = _indexer_inputs(T, Hi, g)
+    idx = _idx_case(T, K, g, pad=0.0)
+    sc, coeff = W.SM_SCALE, 0.25
+    _, lse = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), sc, True)
+    qg = qi.to(DEV).requires_grad_()
+    kg = ki.to(DEV).requires_grad_()
+    wg = w.to(DEV).requires_grad_()
+    loss = indexer_kl_loss(q.to(DEV), kv.to(DEV), lse, idx.to(DEV), qg, kg, wg, sc, coeff, True)
+    loss.backward()
+
+    qd = qi.double().requires_grad_()
+    kd = ki.double().requires_grad_()
+    wd = w.double().requires_grad_()
+    full = O.indexer_scores(qd, kd, wd)
+    topk = torch.where(idx >= 0, idx, idx[:, :1]).long()
+    ref = O.compute_dsa_indexer_loss_dense(full[None], topk[None], q.double()[:, None],
+                                           kv.double()[:, None, None].expand(T, 1, H, 576), sc, coeff,
+                                           sparse_loss=True)
+    ref.backward()
+    torch.testing.assert_close(loss.detach().cpu().double(), ref.detach(), rtol=2e-3, atol=1e-6)
+    for name, got, r in (("dq_idx", qg.grad, qd.grad), ("dk_idx", kg.grad, kd.grad), ("dw", wg.grad, wd.grad)):
+        scale = r.abs().max().clamp_min(1e-30)
+        _close(got.cpu() / scale, r / scale, rel=2e-2, name=name)
