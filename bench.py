@@ -10,8 +10,9 @@ value = algorithmic FLOPs of the step / step time:
   sparse fwd 2176*H*N_sel + sparse bwd 5504*H*N_sel + indexer 2*Di*Hi*N_pairs
 (N_sel = sum_q min(K, visible keys) = 27,602,695; N_pairs = causally visible pairs).
 The line also carries a "decode" object for configs[4] (cfg5), whose bound is HBM: gather
-bytes of the selected cache rows / decode attention time, and an "indexer_prologue" object
-(the fused producer of the indexer's inputs at the cfg3 token count, HBM-bound).
+bytes of the selected cache rows / decode attention time, an "indexer_prologue" object
+(the fused producer of the indexer's inputs at the cfg3 token count, HBM-bound) and an
+"indexer_kl" object (the sparse indexer KL loss and the indexer-score backward at cfg3).
 """
 from __future__ import annotations
 
@@ -217,6 +218,62 @@ def prologue_leg(torch, dev, reps: int = 50):
     return res
 
 
+def indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale: float, nsel: int, reps: int = 10):
+    """Sparse indexer KL loss at the cfg3 size (dsa_indexer_loss_coeff with the sparse loss,
+    model_config.py:204-205): the attention target from the forward LSE, the selected-slot indexer
+    scores, the per-row KL + gradient, and the indexer-score backward (pair order, per-query
+    dq / dw / dk rows, key reduction), each through the C ABI with preallocated buffers.
+    Algorithmic work per selected pair: target 2*576*H flops (S recompute); scores 2*128*Hi;
+    backward 4 x 2*128*Hi (Z, Z^T, dq, dk rows) + its 256-byte dk row written and read back."""
+    from mcore_bridge_amd import _lib
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    T, H, _ = q.shape
+    N, K = kv.shape[0], idx.shape[1]
+    Hi = qi.shape[1]
+    tgt = torch.empty(T, K, dtype=torch.float32, device=dev)
+    sel = torch.empty(T, K, dtype=torch.float32, device=dev)
+    kl = torch.empty(T, dtype=torch.float32, device=dev)
+    d = torch.empty(T, K, dtype=torch.float32, device=dev)
+    dq = torch.empty(T, Hi, 128, dtype=torch.float32, device=dev)
+    dw = torch.empty(T, Hi, dtype=torch.float32, device=dev)
+    dk = torch.empty(N, 128, dtype=torch.float32, device=dev)
+    ws_bytes = int(lib.dsa_indexer_scores_bwd_workspace_size(T, N, K))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    calls = {
+        "target": lambda: lib.dsa_indexer_kl_target(q.data_ptr(), kv.data_ptr(), idx.data_ptr(), lse.data_ptr(), T, N,
+                                                    H, 576, K, scale, 1, tgt.data_ptr(), stream),
+        "selected_scores": lambda: lib.dsa_indexer_selected_scores(qi.data_ptr(), ki.data_ptr(), w.data_ptr(),
+                                                                   idx.data_ptr(), T, N, Hi, 128, K, 1,
+                                                                   sel.data_ptr(), stream),
+        "kl_rows": lambda: lib.dsa_indexer_kl_loss(sel.data_ptr(), tgt.data_ptr(), idx.data_ptr(), T, N, K, 1,
+                                                   1.0 / T, kl.data_ptr(), d.data_ptr(), stream),
+        "scores_bwd": lambda: lib.dsa_indexer_scores_bwd(qi.data_ptr(), ki.data_ptr(), w.data_ptr(), idx.data_ptr(),
+                                                         d.data_ptr(), T, N, Hi, 128, K, 1, dq.data_ptr(),
+                                                         dw.data_ptr(), dk.data_ptr(), ws.data_ptr(), ws_bytes,
+                                                         stream),
+    }
+    res = {"workload": f"sparse indexer KL loss at cfg3 size: T={T}, H={H}, Hi={Hi}, top-k {K}, "
+                       f"{nsel} selected pairs"}
+    for name, fn in calls.items():
+        for _ in range(2):
+            _lib.check("dsa_" + name, fn())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name + "_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+    fl_t = 2 * 576 * H * nsel
+    fl_b = 4 * 2 * 128 * Hi * nsel
+    res["target_tflops"] = round(fl_t / (res["target_ms"] * 1e-3) / 1e12, 1)
+    res["scores_bwd_tflops"] = round(fl_b / (res["scores_bwd_ms"] * 1e-3) / 1e12, 1)
+    res["total_ms"] = round(sum(res[n + "_ms"] for n in calls), 3)
+    res["loss"] = round(float(kl.sum().item()) / T, 6)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -369,6 +426,12 @@ def main():
     if not args.no_decode:
         res["indexer_prologue"] = prologue_leg(torch, dev)
         print(f"[bench] prologue leg done: {res['indexer_prologue']['bf16']['us']} us", file=sys.stderr, flush=True)
+    if not args.no_decode:
+        idx = ops.indexer_topk(qi, ki, w, K, cu_t, True, max_seqlen)
+        _, lse = ops.sparse_mla_fwd(q, kv, idx, scale, True)
+        res["indexer_kl"] = indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale, nsel)
+        del idx, lse
+        print(f"[bench] indexer KL leg done: {res['indexer_kl']['total_ms']} ms", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(res), flush=True)

@@ -164,3 +164,60 @@ def test_indexer_kl_loss_end_to_end_against_dense_megatron_form():
     for name, got, r in (("dq_idx", qg.grad, qd.grad), ("dk_idx", kg.grad, kd.grad), ("dw", wg.grad, wd.grad)):
         scale = r.abs().max().clamp_min(1e-30)
         _close(got.cpu() / scale, r / scale, rel=2e-2, name=name)
+
+
+def test_indexer_kl_path_cfg3_full_size():
+    """The whole KL path at the bench's full size (T = 16384 in 4 documents, H = 128, Hi = 64,
+    K = 2048, indices from the indexer + top-k kernels): target and KL rows of sampled queries
+    against the oracle; the selected scores against the dense scores kernel at the same columns;
+    dq / dw of sampled queries and dk of sampled keys against the oracle over exactly the pairs
+    they depend on."""
+    print("[indexer kl cfg3 full size]", flush=True)
+    cfg = W.CONFIGS["cfg3"]
+    x = W.make_prefill(cfg, device=DEV, seed=3)
+    T, cu = cfg.S, x["cu_seqlens"]
+    qi, ki, w = x["q_idx"].bfloat16(), x["k_idx"].bfloat16(), x["w"].float()
+    idx, dense = ops.indexer_topk(qi, ki, w, cfg.K, cu, causal=True, return_scores=True)
+    q, kv = x["q"].bfloat16(), x["kv"].bfloat16()
+    del x
+    _, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
+    tgt = ops.indexer_kl_target(q, kv, idx, lse, W.SM_SCALE, True)
+    sel = ops.indexer_selected_scores(qi, ki, w, idx, True)
+    kl, d = ops.indexer_kl_rows(sel, tgt, idx, T, True, 1.0 / T)
+    dq, dw, dk = ops.indexer_scores_bwd(qi, ki, w, idx, d, True)
+    torch.cuda.synchronize()
+    # selected scores == the dense scores kernel at the selected columns (column j <-> key doc_start + j)
+    starts = torch.tensor(cfg.docs[:-1], device=DEV)
+    tok = torch.arange(T, device=DEV)
+    doc_start = starts[torch.searchsorted(starts, tok, right=True) - 1]
+    valid = idx >= 0
+    col = (idx.long() - doc_start[:, None]).clamp(min=0)
+    ref_sel = torch.gather(dense, 1, col)
+    del dense
+    torch.testing.assert_close(sel[valid], ref_sel[valid], rtol=1e-4, atol=1e-4)
+    assert torch.all(torch.isneginf(sel[~valid]))
+
+    sample = sorted({0, 1, 31, 2047, 2048, 5000, 10362, cfg.docs[1], cfg.docs[1] + 2100, cfg.docs[2] + 100,
+                     cfg.docs[3] + 5, T - 1})
+    si = torch.tensor(sample)
+    sd = si.to(DEV)
+    qc, kvc, idc = q[sd].cpu(), kv.cpu(), idx[sd].cpu()
+    rt = O.attention_head_probs(qc, kvc, idc, lse[sd].cpu(), W.SM_SCALE)
+    _close(tgt[sd].cpu(), rt, rel=2e-3, name="target", atol=1e-4)
+    rkl, rd = O.indexer_kl_sparse(sel[sd].cpu().double(), tgt[sd].cpu().double(), idc >= 0)
+    torch.testing.assert_close(kl[sd].cpu().double(), rkl, rtol=1e-4, atol=1e-5)
+    _close(d[sd].cpu(), rd / T, rel=1e-4, name="d_index", atol=1e-9)
+
+    qic, kic, wc, dc = qi.cpu(), ki.cpu(), w.cpu(), d.cpu()
+    rq, _, rw = O.indexer_scores_bwd(qic[si], kic, wc[si], idc, dc[si])
+    _close(dq[sd].cpu(), rq, name="dq", atol=1e-6)
+    _close(dw[sd].cpu(), rw, name="dw", atol=1e-6)
+    idx_c = idx.cpu()
+    for s in [0, 7, 1000, 10362, cfg.docs[1], cfg.docs[2] + 3, T - 2048, T - 1]:
+        rows = torch.nonzero((idx_c == s).any(1)).flatten()
+        if rows.numel() == 0:
+            assert torch.all(dk[s] == 0)
+            continue
+        only = torch.where(idx_c[rows] == s, idx_c[rows], torch.full_like(idx_c[rows], -1))
+        _, rk, _ = O.indexer_scores_bwd(qic[rows], kic, wc[rows], only, dc[rows])
+        _close(dk[s].cpu(), rk[s], name=f"dk[{s}]", atol=1e-6)
