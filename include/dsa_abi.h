@@ -89,6 +89,25 @@ int dsa_indexer_prologue(const void* q_lin, int64_t q_stride_t, const void* k_li
                          int rope_deinterleave, int rotary_interleaved, int out_dtype, void* q_out,
                          float* q_scale, void* k_out, float* k_scale, float* w_out, void* stream);
 
+/* Workspace bytes for dsa_indexer_prologue_bwd. */
+size_t dsa_indexer_prologue_bwd_workspace_size(int total_q);
+
+/* Backward of dsa_indexer_prologue with bf16 outputs (replaces torch autograd through the tail
+ * of DSAIndexer.forward_before_topk, patcher.py:268-300, and _apply_rope, patcher.py:304-324):
+ * given dq [total_q, n_heads, 128], dk [total_q, 128], dw [total_q, n_heads] fp32 (gradients of
+ * the prologue outputs, contiguous), writes the gradients of the projections' outputs dq_lin,
+ * dk_lin, dw_lin (bf16, token strides as given) and of k_norm's weight and bias (dln_weight,
+ * dln_bias [128] fp32, summed over tokens).  The forward's bf16 roundings pass the gradient
+ * through unchanged (the chain rule of the exact operations); the other arguments are those of
+ * the forward call. */
+int dsa_indexer_prologue_bwd(const float* dq, const float* dk, const float* dw, const void* k_lin,
+                             int64_t k_stride_t, const float* ln_weight, const float* freqs, int64_t freqs_stride_t,
+                             int total_q, int n_heads, int head_dim, int rope_dim, float eps, float mscale,
+                             float w_scale_heads, float w_scale_softmax, int rope_deinterleave,
+                             int rotary_interleaved, void* dq_lin, int64_t dq_lin_stride_t, void* dk_lin,
+                             int64_t dk_lin_stride_t, void* dw_lin, int64_t dw_lin_stride_t, float* dln_weight,
+                             float* dln_bias, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Lightning-indexer scores (scoring half of fused_qk_topk_naive, patcher.py:358):
  *   scores[t, j] = sum_h w[t,h] * relu(q[t,h,:] . k[row_base[t] + j, :]),  j < row_len[t].
  * q [total_q, n_heads, head_dim], k [n_k, head_dim] in bf16 or OCP e4m3fn (then q_scale

@@ -137,6 +137,51 @@ int dsa_indexer_prologue(const void* q_lin, int64_t q_stride_t, const void* k_li
   return dsa::launch_indexer_prologue(p, as_stream(stream));
 }
 
+size_t dsa_indexer_prologue_bwd_workspace_size(int total_q) {
+  if (total_q < 0) return 0;
+  return sizeof(float) * ((size_t)total_q + 64) * 256;
+}
+
+int dsa_indexer_prologue_bwd(const float* dq, const float* dk, const float* dw, const void* k_lin,
+                             int64_t k_stride_t, const float* ln_weight, const float* freqs, int64_t freqs_stride_t,
+                             int total_q, int n_heads, int head_dim, int rope_dim, float eps, float mscale,
+                             float w_scale_heads, float w_scale_softmax, int rope_deinterleave,
+                             int rotary_interleaved, void* dq_lin, int64_t dq_lin_stride_t, void* dk_lin,
+                             int64_t dk_lin_stride_t, void* dw_lin, int64_t dw_lin_stride_t, float* dln_weight,
+                             float* dln_bias, void* workspace, size_t workspace_bytes, void* stream) {
+  if (total_q < 0 || n_heads < 1 || !(eps >= 0.f) || !std::isfinite(mscale) || !std::isfinite(w_scale_heads) ||
+      !std::isfinite(w_scale_softmax))
+    return DSA_ERR_INVALID_ARG;
+  if (n_heads > 64 || head_dim != 128 || rope_dim != 64) return DSA_ERR_UNSUPPORTED;
+  if (!ln_weight || !dln_weight || !dln_bias) return DSA_ERR_INVALID_ARG;
+  if (total_q > 0 && (!dq || !dk || !dw || !k_lin || !freqs || !dq_lin || !dk_lin || !dw_lin))
+    return DSA_ERR_INVALID_ARG;
+  if (k_stride_t < head_dim || freqs_stride_t < rope_dim || dq_lin_stride_t < (int64_t)n_heads * head_dim ||
+      dk_lin_stride_t < head_dim || dw_lin_stride_t < n_heads || (k_stride_t & 1) || (dq_lin_stride_t & 1) ||
+      (dk_lin_stride_t & 1))
+    return DSA_ERR_INVALID_ARG;
+  auto al8 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 7u) == 0; };
+  auto al4 = [](const void* x) { return (reinterpret_cast<uintptr_t>(x) & 3u) == 0; };
+  if (!al8(dq) || !al8(dk) || !al4(k_lin) || !al4(dq_lin) || !al4(dk_lin)) return DSA_ERR_INVALID_ARG;
+  if (!workspace || workspace_bytes < dsa_indexer_prologue_bwd_workspace_size(total_q) || !al8(workspace))
+    return DSA_ERR_WORKSPACE;
+  dsa::PrologueBwdParams p{};
+  p.dq = dq; p.dk = dk; p.dw = dw;
+  p.k_lin = static_cast<const dsa::bf16_t*>(k_lin);
+  p.ln_w = ln_weight; p.freqs = freqs;
+  p.dq_lin = static_cast<dsa::bf16_t*>(dq_lin);
+  p.dk_lin = static_cast<dsa::bf16_t*>(dk_lin);
+  p.dw_lin = static_cast<dsa::bf16_t*>(dw_lin);
+  p.dln_w = dln_weight; p.dln_b = dln_bias;
+  p.dln_part = static_cast<float*>(workspace);
+  p.total_q = total_q; p.n_heads = n_heads;
+  p.deinterleave = rope_deinterleave ? 1 : 0; p.rotary_interleaved = rotary_interleaved ? 1 : 0;
+  p.eps = eps; p.mscale = mscale; p.w_scale_heads = w_scale_heads; p.w_scale_softmax = w_scale_softmax;
+  p.k_stride_t = k_stride_t; p.freqs_stride_t = freqs_stride_t; p.dq_lin_stride_t = dq_lin_stride_t;
+  p.dk_lin_stride_t = dk_lin_stride_t; p.dw_lin_stride_t = dw_lin_stride_t;
+  return dsa::launch_indexer_prologue_bwd(p, as_stream(stream));
+}
+
 int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const void* k, int k_dtype,
                        const float* k_scale, const float* w, const int32_t* row_base, const int32_t* row_len,
                        int total_q, int n_k, int n_heads, int head_dim, int max_row_len, float* scores,

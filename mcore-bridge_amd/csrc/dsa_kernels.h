@@ -109,6 +109,24 @@ struct KlLossParams {
   float grad_scale;
 };
 
+struct PrologueBwdParams {
+  const float* dq;      // [total_q, n_heads, 128] dL/dq (prologue output)
+  const float* dk;      // [total_q, 128] dL/dk
+  const float* dw;      // [total_q, n_heads] dL/dw
+  const bf16_t* k_lin;  // [total_q, 128], token stride k_stride_t (LayerNorm input)
+  const float* ln_w;    // [128]
+  const float* freqs;   // [total_q, 64], token stride freqs_stride_t
+  bf16_t* dq_lin;       // [total_q, n_heads * 128], token stride dq_lin_stride_t
+  bf16_t* dk_lin;       // [total_q, 128], token stride dk_lin_stride_t
+  bf16_t* dw_lin;       // [total_q, n_heads], token stride dw_lin_stride_t
+  float* dln_w;         // [128]
+  float* dln_b;         // [128]
+  float* dln_part;      // workspace: [total_q, 256] per-token rows + [64, 256] partial sums
+  int total_q, n_heads, deinterleave, rotary_interleaved;
+  float eps, mscale, w_scale_heads, w_scale_softmax;
+  int64_t k_stride_t, freqs_stride_t, dq_lin_stride_t, dk_lin_stride_t, dw_lin_stride_t;
+};
+
 // Indexer scores of the selected slots, I[t, j] = sum_h w[t,h] relu(q[t,h] . k[idx[t,j]]), and
 // their backward (bf16 q / k, head_dim 128, n_heads <= 64).
 struct IdxSelParams {
@@ -137,6 +155,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
 int launch_indexer_prologue(const PrologueParams& p, hipStream_t stream);
+int launch_indexer_prologue_bwd(const PrologueBwdParams& p, hipStream_t stream);
 int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream);
 int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);

@@ -152,6 +152,124 @@ __global__ __launch_bounds__(256) void indexer_prologue_kernel(PrologueParams p)
   }
 }
 
+// Backward of the prologue (the bf16 roundings of the forward pass the gradient through, as the
+// chain rule of the exact operations): per row, dy = H dz / sqrt(128) (the normalised Hadamard
+// matrix is symmetric and orthogonal), then the transpose of the RoPE rotation, du_j =
+// dy_j cs_j + sg_{jr(j)} dy_{jr(j)} sn_{jr(j)} (jr = the rotate_half partner, an involution), then
+// the transpose of the de-interleave; the k row continues through the LayerNorm backward
+// (per-token dgamma, dbeta rows, summed over tokens by a second kernel), and dw_lin =
+// dw * w_scale_heads * w_scale_softmax.
+DSA_DEV void rope_hadamard_bwd(float& x0, float& x1, const float* cs, const float* sn, int lane, int deinterleave,
+                               int rotary_interleaved) {
+  const float a = x0 + x1, b = x0 - x1;
+  x0 = a;
+  x1 = b;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float p0 = __shfl_xor(x0, m, 64), p1 = __shfl_xor(x1, m, 64);
+    const bool hi = lane & m;
+    x0 = hi ? p0 - x0 : x0 + p0;
+    x1 = hi ? p1 - x1 : x1 + p1;
+  }
+  constexpr float kNorm = 0.08838834764831845f;   // 128^-0.5
+  x0 *= kNorm;
+  x1 *= kNorm;
+  // du_j for j = 2l, 2l+1 (lanes 0..31 hold the RoPE dims)
+  float du[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int j = (2 * lane + e) & (kRot - 1);
+    const int jr = rotary_interleaved ? (j ^ 1) : ((j + kRot / 2) & (kRot - 1));
+    const float sgr = rotary_interleaved ? ((jr & 1) ? 1.f : -1.f) : (jr < kRot / 2 ? -1.f : 1.f);
+    du[e] = fetch(x0, x1, j) * cs[j] + sgr * fetch(x0, x1, jr) * sn[jr];
+  }
+  // dx[i] = du[src^-1(i)]: with de-interleave, dx[2l] = du[l] and dx[2l+1] = du[32 + l]
+  const float g0 = deinterleave ? fetch(du[0], du[1], lane & 31) : du[0];
+  const float g1 = deinterleave ? fetch(du[0], du[1], 32 + (lane & 31)) : du[1];
+  if (lane < kRot / 2) {
+    x0 = g0;
+    x1 = g1;
+  }
+}
+
+__global__ __launch_bounds__(256) void indexer_prologue_bwd_kernel(PrologueBwdParams p) {
+  __shared__ float cs[kRot], sn[kRot];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x;
+  if (wave == 0) {
+    const float f = p.freqs[(int64_t)t * p.freqs_stride_t + lane];
+    cs[lane] = round_bf16(cosf(f) * p.mscale);
+    sn[lane] = round_bf16(sinf(f) * p.mscale);
+  }
+  __syncthreads();
+  constexpr int kRowsPerWave = (64 + 1 + 3) / 4;
+  float2 g[kRowsPerWave];
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave; ++i) {
+    const int r = wave + 4 * i;
+    g[i] = float2{0.f, 0.f};
+    if (r <= p.n_heads) {
+      const float* src = r == p.n_heads ? p.dk + (int64_t)t * kDi : p.dq + ((int64_t)t * p.n_heads + r) * kDi;
+      g[i] = *reinterpret_cast<const float2*>(src + 2 * lane);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave; ++i) {
+    const int r = wave + 4 * i;
+    if (r > p.n_heads) break;
+    float x0 = g[i].x, x1 = g[i].y;
+    rope_hadamard_bwd(x0, x1, cs, sn, lane, p.deinterleave, p.rotary_interleaved);
+    if (r < p.n_heads) {
+      bf16_t* dst = p.dq_lin + (int64_t)t * p.dq_lin_stride_t + (int64_t)r * kDi;
+      *reinterpret_cast<uint32_t*>(dst + 2 * lane) = pack_bf16x2(x0, x1);
+      continue;
+    }
+    // k row: LayerNorm backward (statistics recomputed in fp32 as in the forward)
+    const uint32_t kv = *reinterpret_cast<const uint32_t*>(p.k_lin + (int64_t)t * p.k_stride_t + 2 * lane);
+    const float k0 = bf16_lo(kv), k1 = bf16_hi(kv);
+    const float mean = wave_sum(k0 + k1) * (1.f / kDi);
+    const float d0 = k0 - mean, d1 = k1 - mean;
+    const float rstd = 1.f / sqrtf(wave_sum(d0 * d0 + d1 * d1) * (1.f / kDi) + p.eps);
+    const float h0 = d0 * rstd, h1 = d1 * rstd;
+    float* part = p.dln_part + (int64_t)t * 2 * kDi;
+    *reinterpret_cast<float2*>(part + 2 * lane) = float2{x0 * h0, x1 * h1};
+    *reinterpret_cast<float2*>(part + kDi + 2 * lane) = float2{x0, x1};
+    const float e0 = x0 * p.ln_w[2 * lane], e1 = x1 * p.ln_w[2 * lane + 1];
+    const float me = wave_sum(e0 + e1) * (1.f / kDi);
+    const float mh = wave_sum(e0 * h0 + e1 * h1) * (1.f / kDi);
+    const float o0 = rstd * (e0 - me - h0 * mh), o1 = rstd * (e1 - me - h1 * mh);
+    *reinterpret_cast<uint32_t*>(p.dk_lin + (int64_t)t * p.dk_lin_stride_t + 2 * lane) = pack_bf16x2(o0, o1);
+    if (lane < p.n_heads) {
+      const float dwv = p.dw[(int64_t)t * p.n_heads + lane];
+      p.dw_lin[(int64_t)t * p.dw_lin_stride_t + lane] = (bf16_t)(dwv * p.w_scale_heads * p.w_scale_softmax);
+    }
+  }
+}
+
+// dgamma, dbeta = column sums of the per-token rows [T, 256]: kColParts workgroups sum strided
+// row sets, one workgroup adds their partials (fixed order: deterministic).
+constexpr int kColParts = 64;
+__global__ __launch_bounds__(256) void ln_col_partial_kernel(const float* part, int rows, float* out) {
+  float s = 0.f;
+  for (int r = blockIdx.x; r < rows; r += kColParts) s += part[(int64_t)r * 256 + threadIdx.x];
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+__global__ __launch_bounds__(256) void ln_col_final_kernel(const float* part2, float* dw, float* db) {
+  float s = 0.f;
+  for (int b = 0; b < kColParts; ++b) s += part2[b * 256 + threadIdx.x];
+  if (threadIdx.x < kDi) dw[threadIdx.x] = s;
+  else db[threadIdx.x - kDi] = s;
+}
+
+int launch_indexer_prologue_bwd(const PrologueBwdParams& p, hipStream_t stream) {
+  if (p.total_q > 0)
+    hipLaunchKernelGGL(indexer_prologue_bwd_kernel, dim3(p.total_q), dim3(256), 0, stream, p);
+  float* part2 = p.dln_part + (int64_t)p.total_q * 2 * kDi;
+  hipLaunchKernelGGL(ln_col_partial_kernel, dim3(kColParts), dim3(256), 0, stream, p.dln_part, p.total_q, part2);
+  hipLaunchKernelGGL(ln_col_final_kernel, dim3(1), dim3(256), 0, stream, part2, p.dln_w, p.dln_b);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int launch_indexer_prologue(const PrologueParams& p, hipStream_t stream) {
   if (p.total_q == 0) return 0;
   hipLaunchKernelGGL(indexer_prologue_kernel, dim3(p.total_q), dim3(256), 0, stream, p);

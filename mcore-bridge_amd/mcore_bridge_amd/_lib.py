@@ -39,6 +39,11 @@ SIGNATURES = {
                                      c_void_p, c_int64, c_int, c_int, c_int, c_int, c_float, c_float, c_float,
                                      c_float, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p]),
+    "dsa_indexer_prologue_bwd_workspace_size": (c_size_t, [c_int]),
+    "dsa_indexer_prologue_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p,
+                                         c_int64, c_int, c_int, c_int, c_int, c_float, c_float, c_float, c_float,
+                                         c_int, c_int, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                         c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsa_sparse_mla_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                    c_float, c_int, c_void_p, c_void_p, c_void_p]),
     "dsa_build_decode_rows": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),

@@ -240,8 +240,11 @@ class DSAIndexer(torch.nn.Module):
     reference's bridge maps (``wq_b``, ``wk``, ``k_norm.{weight,bias}``, ``weights_proj``,
     gpt_bridge.py:1292-1306) load one to one.
 
-    Forward only, like the reference without ``dsa_indexer_loss_coeff`` (the indexer KL loss and
-    its backward are not built): the outputs are computed under ``torch.no_grad``."""
+    ``forward_before_topk`` is differentiable in the bf16 layout (the prologue's backward kernel,
+    then the projections' GEMM backward), which is what training the indexer with the sparse KL
+    loss needs: pass its outputs to ``indexer_kl_loss``.  ``forward_with_scores`` and ``forward``
+    return scores and indices, which carry no gradient (the reference's dense, non-sparse loss
+    differentiates all index scores; that variant is not built)."""
 
     def __init__(self, hidden_size: int, q_lora_rank: int, index_n_heads: int = 64, index_head_dim: int = 128,
                  index_topk: int = 2048, qk_pos_emb_head_dim: int = 64, layernorm_epsilon: float = 1e-6,
@@ -258,13 +261,18 @@ class DSAIndexer(torch.nn.Module):
         self.k_norm = torch.nn.LayerNorm(index_head_dim, eps=layernorm_epsilon, **kw)
         self.linear_weights_proj = torch.nn.Linear(hidden_size, index_n_heads, bias=False, **kw)
 
-    @torch.no_grad()
     def forward_before_topk(self, x: Tensor, qr: Tensor, packed_seq_params=None):
         """``(q [S,B,Hi,Di], k [S,B,Di], weights [S,B,Hi])`` (with fp8: ``(q, q_scale, k, k_scale,
         weights)``); ``packed_seq_params`` is the caller's ``(psp, rotary_pos_emb)`` tuple
         (multi_latent_attention.py:260-261)."""
         psp, rotary_pos_emb = packed_seq_params
         assert psp is None, "Packed sequence is not supported for DSAttention"   # patcher.py:256
+        if self.fp8:
+            with torch.no_grad():
+                return self._before_topk(x, qr, rotary_pos_emb)
+        return self._before_topk(x, qr, rotary_pos_emb)
+
+    def _before_topk(self, x: Tensor, qr: Tensor, rotary_pos_emb: Tensor):
         return indexer_forward_before_topk(
             x, qr, self.linear_wq_b.weight, self.linear_wk.weight, self.k_norm.weight, self.k_norm.bias,
             self.linear_weights_proj.weight, rotary_pos_emb, index_n_heads=self.index_n_heads, eps=self.eps,

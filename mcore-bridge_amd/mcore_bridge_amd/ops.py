@@ -119,6 +119,72 @@ def _(q_lin, k_lin, w_lin, ln_weight, ln_bias, freqs, eps, mscale, deinterleave,
             q_lin.new_empty(T, Hi, dtype=torch.float32))
 
 
+@torch.library.custom_op("dsa_amd::indexer_prologue_bwd", mutates_args=())
+def indexer_prologue_bwd(dq: Tensor, dk: Tensor, dw: Tensor, k_lin: Tensor, ln_weight: Tensor, freqs: Tensor,
+                         eps: float, mscale: float, deinterleave: bool,
+                         rotary_interleaved: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward of the bf16 ``indexer_prologue``: ``(dq_lin [T, Hi, 128], dk_lin [T, 128], dw_lin
+    [T, Hi]`` bf16, ``dln_weight, dln_bias [128]`` fp32) from the gradients of its outputs."""
+    _require_gpu(dq, dk, dw, k_lin, ln_weight, freqs)
+    T, Hi = dw.shape
+    dq = dq.float().reshape(T, Hi, 128).contiguous()
+    dk = dk.float().contiguous()
+    dw = dw.float().contiguous()
+    kl = k_lin if k_lin.stride(1) == 1 else k_lin.contiguous()
+    fr = freqs.reshape(T, -1).to(torch.float32)
+    fr = fr if fr.stride(1) == 1 else fr.contiguous()
+    lw = ln_weight.to(torch.float32).contiguous()
+    dev = dq.device
+    dq_lin = torch.empty(T, Hi, 128, dtype=torch.bfloat16, device=dev)
+    dk_lin = torch.empty(T, 128, dtype=torch.bfloat16, device=dev)
+    dw_lin = torch.empty(T, Hi, dtype=torch.bfloat16, device=dev)
+    dlw = torch.empty(128, dtype=torch.float32, device=dev)
+    dlb = torch.empty(128, dtype=torch.float32, device=dev)
+    ws_bytes = int(_lib.load().dsa_indexer_prologue_bwd_workspace_size(T))
+    ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("dsa_indexer_prologue_bwd", _p(dq), _p(dk), _p(dw), _p(kl), kl.stride(0), _p(lw), _p(fr),
+                  fr.stride(0), T, Hi, 128, 64, float(eps), float(mscale), float(Hi ** -0.5), float(128 ** -0.5),
+                  int(deinterleave), int(rotary_interleaved), _p(dq_lin), Hi * 128, _p(dk_lin), 128, _p(dw_lin), Hi,
+                  _p(dlw), _p(dlb), _p(ws), ws_bytes, _stream(dev))
+    return dq_lin, dk_lin, dw_lin, dlw, dlb
+
+
+@indexer_prologue_bwd.register_fake
+def _(dq, dk, dw, k_lin, ln_weight, freqs, eps, mscale, deinterleave, rotary_interleaved):
+    T, Hi = dw.shape
+    return (dq.new_empty(T, Hi, 128, dtype=torch.bfloat16), dq.new_empty(T, 128, dtype=torch.bfloat16),
+            dq.new_empty(T, Hi, dtype=torch.bfloat16), dq.new_empty(128, dtype=torch.float32),
+            dq.new_empty(128, dtype=torch.float32))
+
+
+def _pro_setup(ctx, inputs, output):
+    q_lin, k_lin, w_lin, ln_weight, ln_bias, freqs, eps, mscale, deinterleave, rotary_interleaved, fp8 = inputs
+    ctx.save_for_backward(k_lin, ln_weight, freqs)
+    ctx.args = (eps, mscale, deinterleave, rotary_interleaved)
+    ctx.fp8 = fp8
+    ctx.shapes = (q_lin.shape, q_lin.dtype, w_lin.dtype, ln_weight.dtype, ln_bias.dtype)
+
+
+def _pro_backward(ctx, dq, dqs, dk, dks, dw):
+    if ctx.fp8:
+        raise RuntimeError("indexer_prologue: the fp8 outputs are not differentiable; use the bf16 prologue for "
+                           "training")
+    k_lin, ln_weight, freqs = ctx.saved_tensors
+    qshape, qdt, wdt, lwdt, lbdt = ctx.shapes
+    T = k_lin.shape[0]
+    Hi = qshape[1] if len(qshape) == 3 else qshape[1] // 128
+    dq = torch.zeros(T, Hi, 128, dtype=torch.float32, device=k_lin.device) if dq is None else dq
+    dk = torch.zeros(T, 128, dtype=torch.float32, device=k_lin.device) if dk is None else dk
+    dw = torch.zeros(T, Hi, dtype=torch.float32, device=k_lin.device) if dw is None else dw
+    dq_lin, dk_lin, dw_lin, dlw, dlb = indexer_prologue_bwd(dq, dk, dw, k_lin, ln_weight, freqs, *ctx.args)
+    return (dq_lin.reshape(qshape).to(qdt), dk_lin, dw_lin.to(wdt), dlw.to(lwdt), dlb.to(lbdt),
+            None, None, None, None, None, None)
+
+
+torch.library.register_autograd("dsa_amd::indexer_prologue", _pro_backward, setup_context=_pro_setup)
+
+
 # --------------------------------------------------------------------------------------
 # K1 indexer scores
 # --------------------------------------------------------------------------------------

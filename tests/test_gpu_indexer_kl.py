@@ -221,3 +221,97 @@ def test_indexer_kl_path_cfg3_full_size():
         only = torch.where(idx_c[rows] == s, idx_c[rows], torch.full_like(idx_c[rows], -1))
         _, rk, _ = O.indexer_scores_bwd(qic[rows], kic, wc[rows], only, dc[rows])
         _close(dk[s].cpu(), rk[s], name=f"dk[{s}]", atol=1e-6)
+
+
+def _pro_case(T, Hi, g):
+    q_lin = (torch.randn(T, Hi, 128, generator=g) * 2).bfloat16()
+    k_lin = (torch.randn(T, 128, generator=g) * 2 + 0.5).bfloat16()
+    w_lin = torch.randn(T, Hi, generator=g).bfloat16()
+    lw = 1 + 0.2 * torch.randn(128, generator=g)
+    lb = 0.1 * torch.randn(128, generator=g)
+    fr = torch.rand(T, 64, generator=g) * 3000
+    return q_lin, k_lin, w_lin, lw, lb, fr
+
+
+@pytest.mark.parametrize("dei,ri,Hi", [(False, False, 64), (True, False, 64), (False, True, 16), (True, True, 33)])
+def test_indexer_prologue_backward(dei, ri, Hi):
+    """Gradients of the bf16 prologue (HIP backward kernel through the op's autograd) against torch
+    autograd through the float64 oracle prologue."""
+    print(f"[prologue bwd] dei={dei} ri={ri} Hi={Hi}", flush=True)
+    g = torch.Generator().manual_seed(40 + Hi + 2 * dei + ri)
+    T, eps, ms = 150, 1e-6, 1.3
+    ins = _pro_case(T, Hi, g)
+    gq = torch.randn(T, Hi, 128, generator=g)
+    gk = torch.randn(T, 128, generator=g)
+    gw = torch.randn(T, Hi, generator=g)
+    dv = [x.to(DEV).requires_grad_() if i != 5 else x.to(DEV) for i, x in enumerate(ins)]
+    q, _, k, _, w = ops.indexer_prologue(*dv, eps, ms, dei, ri)
+    ((q.float() * gq.to(DEV)).sum() + (k.float() * gk.to(DEV)).sum() + (w * gw.to(DEV)).sum()).backward()
+    rf = [x.double().requires_grad_() if i != 5 else x for i, x in enumerate(ins)]
+    rq, rk, rw = O.indexer_prologue(*rf, eps=eps, mscale=ms, deinterleave=dei, rotary_interleaved=ri,
+                                    dtype=torch.float64)
+    # the kernel receives the upstream gradients of the bf16 outputs q, k rounded to bf16
+    gqb, gkb = gq.bfloat16().double(), gk.bfloat16().double()
+    ((rq * gqb).sum() + (rk * gkb).sum() + (rw * gw.double()).sum()).backward()
+    for name, a, b in zip(("dq_lin", "dk_lin", "dw_lin", "dln_weight", "dln_bias"), dv[:5], rf[:5]):
+        assert a.grad.dtype == a.dtype, name
+        # tolerances relative to the tensor's scale: dln_* are sums over all tokens
+        scale = b.grad.abs().max().clamp_min(1e-30)
+        _close(a.grad.cpu() / scale, b.grad / scale, name=name)
+
+
+def test_indexer_module_trains_with_the_sparse_kl_loss():
+    """The whole indexer training path: DSAIndexer.forward_before_topk (GEMMs + prologue), the
+    sparse KL loss against the attention's probabilities, and the backward into the indexer's
+    parameters.  Reference: float64 autograd of the dense restatement of compute_dsa_indexer_loss
+    at the same forward values (the kernels' bf16 q, k, w; the ReLU masks and softmaxes are then
+    those of the GPU pass), its gradients carried through the float64 oracle prologue and the
+    projections (same top-k indices on both sides)."""
+    print("[indexer training e2e]", flush=True)
+    from mcore_bridge_amd.dsa import DSAIndexer
+    g = torch.Generator().manual_seed(77)
+    S, hidden, qlr, Hi, H, K = 192, 256, 192, 64, 16, 48
+    mod = DSAIndexer(hidden, qlr, index_n_heads=Hi, index_topk=K, device=DEV)
+    with torch.no_grad():
+        for p_ in mod.parameters():
+            p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(p_.dtype))
+        mod.k_norm.weight.add_(1.0)
+    x = (torch.randn(S, 1, hidden, generator=g)).bfloat16()
+    qr = (torch.randn(S, 1, qlr, generator=g)).bfloat16()
+    fr = torch.rand(S, 1, 1, 64, generator=g) * 200
+    q, k, w = mod.forward_before_topk(x.to(DEV), qr.to(DEV), (None, fr.to(DEV)))
+    idx = ops.indexer_topk(q.detach().reshape(S, Hi, 128), k.detach().reshape(S, 128), w.detach().reshape(S, Hi), K)
+    qa = (torch.randn(S, H, 576, generator=g) * 0.1).bfloat16()
+    kva = (torch.randn(S, 576, generator=g) * 0.1).bfloat16()
+    _, lse = ops.sparse_mla_fwd(qa.to(DEV), kva.to(DEV), idx, W.SM_SCALE, True)
+    coeff = 0.5
+    loss = indexer_kl_loss(qa.to(DEV), kva.to(DEV), lse, idx, q.reshape(S, Hi, 128), k.reshape(S, 128),
+                           w.reshape(S, Hi), W.SM_SCALE, coeff, True)
+    loss.backward()
+
+    # dense loss at the GPU's forward values
+    qv = q.detach().cpu().double().reshape(S, Hi, 128).requires_grad_()
+    kvv = k.detach().cpu().double().reshape(S, 128).requires_grad_()
+    wv = w.detach().cpu().double().reshape(S, Hi).requires_grad_()
+    ic = idx.cpu().long()
+    topk = torch.where(ic >= 0, ic, ic[:, :1])
+    ref = O.compute_dsa_indexer_loss_dense(O.indexer_scores(qv, kvv, wv)[None], topk[None], qa.double()[:, None],
+                                           kva.double()[:, None, None].expand(S, 1, H, 576), W.SM_SCALE, coeff,
+                                           sparse_loss=True)
+    ref.backward()
+    torch.testing.assert_close(loss.detach().cpu().double(), ref.detach(), rtol=1e-3, atol=1e-6)
+    # ... carried through the float64 prologue and projections
+    P = {n: p_.detach().double().cpu().requires_grad_() for n, p_ in mod.named_parameters()}
+    xd, qrd = x.double()[:, 0], qr.double()[:, 0]
+    q_lin = (qrd @ P["linear_wq_b.weight"].T).reshape(S, Hi, 128)
+    k_lin = xd @ P["linear_wk.weight"].T
+    w_lin = xd @ P["linear_weights_proj.weight"].T
+    rq, rk, rw = O.indexer_prologue(q_lin, k_lin, w_lin, P["k_norm.weight"], P["k_norm.bias"], fr.reshape(S, 64),
+                                    eps=mod.eps, mscale=mod.mscale, deinterleave=False, rotary_interleaved=False,
+                                    dtype=torch.float64)
+    # the kernels receive the gradients of the bf16 outputs q, k rounded to bf16
+    torch.autograd.backward([rq, rk, rw], [qv.grad.bfloat16().double(), kvv.grad.bfloat16().double(), wv.grad])
+    for n, p_ in mod.named_parameters():
+        r = P[n].grad
+        scale = r.abs().max().clamp_min(1e-30)
+        _close(p_.grad.cpu() / scale, r / scale, rel=2e-2, name=n)
