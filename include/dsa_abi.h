@@ -14,6 +14,14 @@
  *   dsa_sparse_mla_bwd
  *       replaces torch autograd through that un-fused attention (the reference defines no
  *       custom backward; multi_latent_attention.py:262-270 is the forward call site).
+ *   dsa_indexer_prologue (+ _bwd)
+ *       replaces the tail of DSAIndexer.forward_before_topk after its projections,
+ *       patcher.py:268-300 (and torch autograd through it).
+ *   dsa_indexer_kl_target, dsa_indexer_kl_loss, dsa_indexer_selected_scores (+ _bwd)
+ *       replace megatron-core's compute_dsa_indexer_loss with the sparse loss (enabled by
+ *       dsa_indexer_loss_coeff / dsa_indexer_use_sparse_loss, src/mcore_bridge/config/
+ *       model_config.py:204-205) and torch autograd through the index scores of
+ *       fused_qk_topk_naive (patcher.py:338-376) at the selected slots.
  *
  * Conventions
  *   - All pointers are device pointers on the current HIP device, except where noted.
