@@ -106,3 +106,60 @@ def test_ops_refuse_cpu_tensors():
     idx = torch.zeros(4, 2, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="GPU"):
         ops.sparse_mla_fwd(q, kv, idx, 0.1, True)
+
+
+def test_indexer_loss_entry_points_validate_and_size():
+    lib = _lib.load()
+    # KL target: d_qk must be 576, at most 128 heads, finite positive scale; empty work is a no-op
+    tgt = lambda q, dqk, H, sc, T=4: lib.dsa_indexer_kl_target(q, P, P, P, T, 8, H, dqk, 16, sc, 1, P, N)
+    assert tgt(P, 512, 16, 0.1) == _lib.DSA_ERR_UNSUPPORTED
+    assert tgt(P, 576, 129, 0.1) == _lib.DSA_ERR_UNSUPPORTED
+    assert tgt(N, 576, 16, 0.1) == _lib.DSA_ERR_INVALID_ARG
+    assert tgt(P, 576, 16, float("nan")) == _lib.DSA_ERR_INVALID_ARG
+    assert tgt(ctypes.c_void_p(4100), 576, 16, 0.1) == _lib.DSA_ERR_INVALID_ARG
+    assert tgt(N, 576, 16, 0.1, T=0) == _lib.DSA_OK
+    # KL rows: finite gradient scale, non-null buffers
+    assert lib.dsa_indexer_kl_loss(P, P, P, 4, 8, 16, 1, float("inf"), P, P, N) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_indexer_kl_loss(P, P, P, 4, 8, 16, 1, 1.0, P, N, N) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_indexer_kl_loss(N, N, N, 0, 8, 16, 1, 1.0, N, N, N) == _lib.DSA_OK
+    # selected scores: head_dim 128, <= 64 heads, top-k <= 4096, aligned rows
+    sel = lambda q, H, D, K, T=4: lib.dsa_indexer_selected_scores(q, P, P, P, T, 8, H, D, K, 1, P, N)
+    assert sel(P, 64, 64, 16) == _lib.DSA_ERR_UNSUPPORTED
+    assert sel(P, 65, 128, 16) == _lib.DSA_ERR_UNSUPPORTED
+    assert sel(P, 64, 128, 4097) == _lib.DSA_ERR_UNSUPPORTED
+    assert sel(ctypes.c_void_p(4104), 64, 128, 16) == _lib.DSA_ERR_INVALID_ARG
+    assert sel(N, 64, 128, 16, T=0) == _lib.DSA_OK
+    # scores backward: workspace = dk rows (T*K + 1) x 256 B + pair rows T*K x 8 B + key offsets / counts
+    T, Nk, K = 16384, 16384, 2048
+    ws = lib.dsa_indexer_scores_bwd_workspace_size(T, Nk, K)
+    assert (T * K + 1) * 256 + T * K * 8 + (Nk + 1) * 8 + Nk * 4 <= ws < (T * K + 1) * 256 + T * K * 8 + 12 * Nk + 1024
+    assert lib.dsa_indexer_scores_bwd_workspace_size(-1, Nk, K) == 0
+    bwd = lambda dq, ws_, nbytes: lib.dsa_indexer_scores_bwd(P, P, P, P, P, 4, 8, 64, 128, 16, 1, dq, P, P, ws_, nbytes, N)
+    assert bwd(P, P, 16) == _lib.DSA_ERR_WORKSPACE
+    assert bwd(P, N, 1 << 30) == _lib.DSA_ERR_WORKSPACE
+    assert bwd(N, P, 1 << 30) == _lib.DSA_ERR_INVALID_ARG
+    # prologue backward: (T + 64) rows of 256 floats of workspace; limits as the forward
+    assert lib.dsa_indexer_prologue_bwd_workspace_size(1000) == (1000 + 64) * 256 * 4
+    pb = lambda dq, H, ws_, nbytes, stride=64 * 128: lib.dsa_indexer_prologue_bwd(
+        dq, P, P, P, 128, P, P, 64, 4, H, 128, 64, 1e-6, 1.0, 0.125, 0.088, 0, 0, P, stride, P, 128, P, 64, P, P,
+        ws_, nbytes, N)
+    assert pb(P, 65, P, 1 << 20) == _lib.DSA_ERR_UNSUPPORTED
+    assert pb(P, 64, P, 16) == _lib.DSA_ERR_WORKSPACE
+    assert pb(ctypes.c_void_p(4100), 64, P, 1 << 20) == _lib.DSA_ERR_INVALID_ARG
+    assert pb(P, 64, P, 1 << 20, stride=127) == _lib.DSA_ERR_INVALID_ARG
+
+
+def test_indexer_loss_ops_refuse_cpu_tensors():
+    import torch
+    from mcore_bridge_amd import ops
+    q = torch.zeros(4, 16, 576, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 576, dtype=torch.bfloat16)
+    idx = torch.zeros(4, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.indexer_kl_target(q, kv, idx, torch.zeros(4, 16), 0.1, True)
+    qi = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
+    ki = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.indexer_selected_scores(qi, ki, torch.zeros(4, 8), idx, True)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.indexer_kl_rows(torch.zeros(4, 2), torch.zeros(4, 2), idx, 4, True, 1.0)
