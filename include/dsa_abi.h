@@ -17,7 +17,7 @@
  *   dsa_indexer_prologue (+ _bwd)
  *       replaces the tail of DSAIndexer.forward_before_topk after its projections,
  *       patcher.py:268-300 (and torch autograd through it).
- *   dsa_indexer_kl_target, dsa_indexer_kl_loss, dsa_indexer_selected_scores (+ _bwd)
+ *   dsa_indexer_kl_target (+ _from_bwd), dsa_indexer_kl_loss, dsa_indexer_selected_scores (+ _bwd)
  *       replace megatron-core's compute_dsa_indexer_loss with the sparse loss (enabled by
  *       dsa_indexer_loss_coeff / dsa_indexer_use_sparse_loss, src/mcore_bridge/config/
  *       model_config.py:204-205) and torch autograd through the index scores of
@@ -196,6 +196,14 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
 int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, const float* lse, int total_q,
                           int n_kv, int n_heads, int d_qk, int topk, float sm_scale, int causal, float* target,
                           void* stream);
+
+/* The same target from the workspace of a dsa_sparse_mla_bwd call that just ran on the same q,
+ * kv, idx, lse (same total_q, n_kv, n_heads, topk, causal; no other call on that workspace in
+ * between): its first stage recomputes P for every head and stages it in bf16, so the target is
+ * the head mean of those tiles and no S product is recomputed.  Stream-ordered after that call. */
+int dsa_indexer_kl_target_from_bwd(const void* bwd_workspace, size_t bwd_workspace_bytes, const int32_t* idx,
+                                   int total_q, int n_kv, int n_heads, int topk, int causal, float* target,
+                                   void* stream);
 
 /* Per-query KL of the sparse indexer loss and its gradient: with pI = softmax of index_sel over
  * the valid slots of row t, kl[t] = sum_j target (ln(target + 1e-10) - ln(pI + 1e-10)) and

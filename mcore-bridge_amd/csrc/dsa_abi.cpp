@@ -362,6 +362,24 @@ int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, con
   return dsa::launch_indexer_kl_target(p, as_stream(stream));
 }
 
+int dsa_indexer_kl_target_from_bwd(const void* bwd_workspace, size_t bwd_workspace_bytes, const int32_t* idx,
+                                   int total_q, int n_kv, int n_heads, int topk, int causal, float* target,
+                                   void* stream) {
+  if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1) return DSA_ERR_INVALID_ARG;
+  if (n_heads > 128 || n_heads % 16 != 0) return DSA_ERR_UNSUPPORTED;
+  if (total_q == 0) return DSA_OK;
+  if (!idx || !target) return DSA_ERR_INVALID_ARG;
+  const BwdLayout L = bwd_layout(total_q, n_kv, n_heads, topk);
+  if (!bwd_workspace || bwd_workspace_bytes < L.total || !aligned16(bwd_workspace)) return DSA_ERR_WORKSPACE;
+  dsa::KlFromPParams p{};
+  p.p_stage = reinterpret_cast<const dsa::bf16_t*>(static_cast<const char*>(bwd_workspace) + L.p_stage);
+  p.idx = idx; p.target = target;
+  p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.topk_pad = topk_pad(topk);
+  p.causal = causal ? 1 : 0;
+  p.idx_stride = topk; p.target_stride = topk;
+  return dsa::launch_indexer_kl_target_from_p(p, as_stream(stream));
+}
+
 int dsa_indexer_kl_loss(const float* index_sel, const float* target, const int32_t* idx, int total_q, int n_kv,
                         int topk, int causal, float grad_scale, float* kl, float* d_index, void* stream) {
   if (total_q < 0 || n_kv < 0 || topk < 1 || !std::isfinite(grad_scale)) return DSA_ERR_INVALID_ARG;

@@ -12,6 +12,8 @@
 //       registers, S = Q . K^T per 32-key block (the forward's operands swapped, so each lane
 //       holds one key and 16 heads), P = 2^(scale_log2 * S - lse2), summed over heads in the
 //       lane, across its half-wave partner and across the waves through LDS.
+//   kl_target_from_p_kernel   the same target as the head mean of the P tiles the sparse MLA
+//       backward stages (for callers that apply the loss in the backward pass: no S recompute).
 //   indexer_kl_kernel         one workgroup per query: softmax of the index scores over the valid
 //       slots, the KL of the row and d(loss)/dI.
 #include "dsa_common.h"
@@ -194,6 +196,66 @@ __global__ __launch_bounds__(256) void indexer_kl_kernel(KlLossParams p) {
     }
     g[j] = v;
   }
+}
+
+// The same target from the P tiles the sparse MLA backward stages (B1 recomputes P = exp(scale *
+// S - lse) for every head and stores it in bf16, [t][block][head][32 keys]): target[t, j] = (1/H)
+// sum_h P[t, h, j], no S recompute.  One workgroup per query; thread (c, h0) reads 8 keys of
+// heads h0, h0 + 64 per block, summed over the wave's heads with lane shuffles and over the
+// waves through LDS.  Blocks past the query's last valid slot were not staged: their slots are 0.
+__global__ __launch_bounds__(256) void kl_target_from_p_kernel(KlFromPParams p) {
+  __shared__ float part[4][32];
+  __shared__ int red[4];
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int32_t* ix = p.idx + (int64_t)t * p.idx_stride;
+  int last = -1;
+  for (int j = threadIdx.x; j < p.topk; j += 256) {
+    const int x = ix[j];
+    if (x >= 0 && x < p.n_kv && (!p.causal || x <= t)) last = j;
+  }
+  last = wave_max_i(last);
+  if (lane == 0) red[wave] = last;
+  __syncthreads();
+  last = max(max(red[0], red[1]), max(red[2], red[3]));
+  const int nblk = (last + kBK) / kBK;
+  float* out = p.target + (int64_t)t * p.target_stride;
+  const float inv_h = 1.f / (float)p.n_heads;
+  const int c = threadIdx.x & 3, h0 = threadIdx.x >> 2;
+  const bf16_t* base = p.p_stage + (int64_t)t * (p.topk_pad / kBK) * p.n_heads * kBK;
+  for (int b = 0; b < nblk; ++b) {
+    const bf16_t* tile = base + (int64_t)b * p.n_heads * kBK;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int h = h0; h < p.n_heads; h += 64) {
+      const u32x4 v = gload16(tile + h * kBK + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += bf16_lo(v[e]);
+        acc[2 * e + 1] += bf16_hi(v[e]);
+      }
+    }
+#pragma unroll
+    for (int o = 4; o < 64; o <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+    if (lane < 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[wave][8 * lane + e] = acc[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < kBK && b * kBK + (int)threadIdx.x < p.topk) {
+      const int k = threadIdx.x;
+      out[b * kBK + k] = (part[0][k] + part[1][k] + part[2][k] + part[3][k]) * inv_h;
+    }
+    __syncthreads();
+  }
+  for (int j = nblk * kBK + threadIdx.x; j < p.topk; j += 256) out[j] = 0.f;
+}
+
+int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream) {
+  if (p.total_q == 0) return 0;
+  hipLaunchKernelGGL(kl_target_from_p_kernel, dim3(p.total_q), dim3(256), 0, stream, p);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream) {

@@ -98,6 +98,14 @@ struct KlTargetParams {
   float scale_log2;     // softmax scale * log2(e)
 };
 
+struct KlFromPParams {
+  const bf16_t* p_stage;  // the sparse backward's staged P tiles [total_q][topk_pad / 32][n_heads][32]
+  const int32_t* idx;     // [total_q, topk]
+  float* target;          // [total_q, topk]
+  int total_q, n_heads, n_kv, topk, topk_pad, causal;
+  int64_t idx_stride, target_stride;
+};
+
 struct KlLossParams {
   const float* index_sel;  // [total_q, topk] index scores of the selected slots
   const float* target;     // [total_q, topk]
@@ -158,6 +166,7 @@ int launch_indexer_prologue(const PrologueParams& p, hipStream_t stream);
 int launch_indexer_prologue_bwd(const PrologueBwdParams& p, hipStream_t stream);
 int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream);
 int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
+int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream);
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream);
 // Key-major order of the selected (query, slot) pairs: csr_offsets [n_kv + 1] and the row of

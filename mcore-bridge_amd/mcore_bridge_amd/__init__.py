@@ -8,7 +8,7 @@ kernels of ``libdsa_amd.so`` (C ABI: include/dsa_abi.h); there is no CPU fallbac
 """
 from . import _lib
 from .dsa import (DSAIndexer, absorbed_mla_sparse_attention, fused_qk_topk_naive, indexer_forward_before_topk,
-                  indexer_kl_loss, sparse_mla_attention)
+                  indexer_kl_loss, sparse_mla_attention, sparse_mla_with_indexer_loss)
 from .ops import (build_decode_rows, build_rows, bwd_workspace_bytes, decode_indexer_topk, decode_workspace_bytes,
                   indexer_kl_rows, indexer_kl_target, indexer_prologue, indexer_scores, indexer_scores_bwd,
                   indexer_selected_scores, indexer_topk, sparse_mla, sparse_mla_bwd, sparse_mla_decode,
@@ -18,6 +18,7 @@ __all__ = [
     "DSAIndexer", "absorbed_mla_sparse_attention", "build_decode_rows", "build_rows", "bwd_workspace_bytes", "decode_indexer_topk", "decode_workspace_bytes",
     "fused_qk_topk_naive", "indexer_forward_before_topk", "indexer_kl_loss", "indexer_kl_rows", "indexer_kl_target",
     "indexer_prologue", "indexer_scores", "indexer_scores_bwd", "indexer_selected_scores", "indexer_topk",
-    "sparse_mla", "sparse_mla_attention", "sparse_mla_bwd", "sparse_mla_decode", "sparse_mla_fwd", "topk",
+    "sparse_mla", "sparse_mla_attention", "sparse_mla_bwd", "sparse_mla_decode", "sparse_mla_fwd",
+    "sparse_mla_with_indexer_loss", "topk",
 ]
 __version__ = "0.1.0"

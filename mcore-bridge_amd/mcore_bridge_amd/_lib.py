@@ -59,6 +59,8 @@ SIGNATURES = {
                                          c_void_p, c_size_t, c_void_p, c_void_p]),
     "dsa_indexer_kl_target": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                       c_float, c_int, c_void_p, c_void_p]),
+    "dsa_indexer_kl_target_from_bwd": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                               c_void_p, c_void_p]),
     "dsa_indexer_kl_loss": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "dsa_indexer_selected_scores": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

@@ -184,6 +184,54 @@ def indexer_kl_loss(q: Tensor, kv: Tensor, lse: Tensor, topk_indices: Tensor, q_
     return _IndexerKL.apply(index_sel, target, idx, k_idx.shape[0], causal, float(loss_coeff))
 
 
+class _SparseMLAWithIndexerLoss(torch.autograd.Function):
+    """Sparse attention whose backward also applies the sparse indexer KL loss (see
+    ``sparse_mla_with_indexer_loss``)."""
+
+    @staticmethod
+    def forward(ctx, q, kv, q_idx, k_idx, w, idx, sm_scale, coeff, loss_scale, causal, loss_out):
+        out, lse = ops.sparse_mla_fwd(q, kv, idx, sm_scale, causal)
+        ctx.save_for_backward(q, kv, q_idx, k_idx, w, idx, out, lse)
+        ctx.args = (sm_scale, coeff, loss_scale, causal)
+        ctx.loss_out = loss_out
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, kv, q_idx, k_idx, w, idx, out, lse = ctx.saved_tensors
+        sm_scale, coeff, loss_scale, causal = ctx.args
+        dq, dkv, target = ops.sparse_mla_bwd_with_target(q, kv, idx, out, dout, lse, sm_scale, causal)
+        T = idx.shape[0]
+        sel = ops.indexer_selected_scores(q_idx.detach(), k_idx.detach(), w.detach(), idx, causal)
+        kl, d = ops.indexer_kl_rows(sel, target, idx, k_idx.shape[0], causal, coeff * loss_scale / max(T, 1))
+        ctx.loss_out.copy_(kl.sum() * (coeff / max(T, 1)))
+        dqi = dki = dwi = None
+        if any(ctx.needs_input_grad[2:5]):
+            dqi, dwi, dki = ops.indexer_scores_bwd(q_idx.detach(), k_idx.detach(), w.detach(), idx, d, causal)
+            dqi, dki, dwi = dqi.to(q_idx.dtype), dki.to(k_idx.dtype), dwi.to(w.dtype)
+        return dq, dkv.to(kv.dtype), dqi, dki, dwi, None, None, None, None, None, None
+
+
+def sparse_mla_with_indexer_loss(q: Tensor, kv: Tensor, topk_indices: Tensor, q_idx: Tensor, k_idx: Tensor,
+                                 w: Tensor, softmax_scale: float, loss_coeff: float, causal: bool = True,
+                                 loss_scale: float = 1.0):
+    """Sparse MLA attention (``ops.sparse_mla``, packed THD) whose backward also applies the sparse
+    indexer KL loss, the way Megatron's ``DSAIndexerLossAutoScaler`` attaches the indexer loss to
+    the attention output: the loss needs no separate backward call.  The target comes from the P
+    tiles the attention backward recomputes anyway, so no score product is repeated (the
+    forward-time ``indexer_kl_loss`` recomputes it).
+
+    Returns ``(out [T, H, 512], loss)``: ``loss`` is a 0-dim fp32 tensor that holds ``loss_coeff *
+    mean_t KL_t`` once the backward pass has run (for logging); the gradients reaching ``q_idx``,
+    ``k_idx`` and ``w`` are those of ``loss_scale * loss`` (``loss_scale`` plays the role of the
+    auto-scaler's loss scale)."""
+    loss = torch.zeros((), dtype=torch.float32, device=q.device)
+    idx = topk_indices.to(torch.int32)
+    out = _SparseMLAWithIndexerLoss.apply(q, kv, q_idx, k_idx, w, idx, float(softmax_scale), float(loss_coeff),
+                                          float(loss_scale), bool(causal), loss)
+    return out, loss
+
+
 class _HeadwiseMatmul(torch.autograd.Function):
     """``out[h] = a[h] @ b[h]`` for ``a [H, M, K]``, ``b [H, K, N]``, with every batched product in
     forward and backward fed contiguous operands (no transposed views reach ``torch.bmm``)."""

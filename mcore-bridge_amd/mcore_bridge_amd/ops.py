@@ -392,6 +392,37 @@ def _(q, kv, idx, out, dout, lse, sm_scale, causal=False):
     return torch.empty_like(q), kv.new_empty(kv.shape[0], D_QK, dtype=torch.float32)
 
 
+@torch.library.custom_op("dsa_amd::sparse_mla_bwd_with_target", mutates_args=())
+def sparse_mla_bwd_with_target(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor,
+                               sm_scale: float, causal: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
+    """``sparse_mla_bwd`` plus the sparse indexer loss target ``[T, K]`` fp32, read from the P tiles
+    the backward stages (head mean of P; no S recompute)."""
+    _check_attn(q, kv, idx)
+    _require_gpu(out, dout, lse)
+    q, kv, out, lse = q.contiguous(), kv.contiguous(), out.contiguous(), lse.contiguous()
+    dout = dout.to(torch.bfloat16).contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, H, _ = q.shape
+    N, K = kv.shape[0], idx.shape[1]
+    dq = torch.empty_like(q)
+    dkv = torch.empty(N, D_QK, dtype=torch.float32, device=q.device)
+    tgt = torch.empty(T, K, dtype=torch.float32, device=q.device)
+    ws_bytes = bwd_workspace_bytes(T, N, H, K)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_sparse_mla_bwd", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), T, N, H, D_QK, D_V, K,
+                  float(sm_scale), int(causal), _p(dq), _p(dkv), _p(ws), ws_bytes, _stream(q.device))
+        _lib.call("dsa_indexer_kl_target_from_bwd", _p(ws), ws_bytes, _p(idx), T, N, H, K, int(causal), _p(tgt),
+                  _stream(q.device))
+    return dq, dkv, tgt
+
+
+@sparse_mla_bwd_with_target.register_fake
+def _(q, kv, idx, out, dout, lse, sm_scale, causal=False):
+    return (torch.empty_like(q), kv.new_empty(kv.shape[0], D_QK, dtype=torch.float32),
+            q.new_empty(q.shape[0], idx.shape[1], dtype=torch.float32))
+
+
 def _fwd_setup(ctx, inputs, output):
     q, kv, idx, sm_scale, causal = inputs
     out, lse = output

@@ -118,6 +118,10 @@ def test_indexer_loss_entry_points_validate_and_size():
     assert tgt(P, 576, 16, float("nan")) == _lib.DSA_ERR_INVALID_ARG
     assert tgt(ctypes.c_void_p(4100), 576, 16, 0.1) == _lib.DSA_ERR_INVALID_ARG
     assert tgt(N, 576, 16, 0.1, T=0) == _lib.DSA_OK
+    # target from the attention backward's workspace: its head limits, and a workspace of its size
+    fb = lambda H, nbytes: lib.dsa_indexer_kl_target_from_bwd(P, nbytes, P, 4, 8, H, 16, 1, P, N)
+    assert fb(24, 1 << 30) == _lib.DSA_ERR_UNSUPPORTED
+    assert fb(32, lib.dsa_sparse_mla_bwd_workspace_size(4, 8, 32, 16) - 1) == _lib.DSA_ERR_WORKSPACE
     # KL rows: finite gradient scale, non-null buffers
     assert lib.dsa_indexer_kl_loss(P, P, P, 4, 8, 16, 1, float("inf"), P, P, N) == _lib.DSA_ERR_INVALID_ARG
     assert lib.dsa_indexer_kl_loss(P, P, P, 4, 8, 16, 1, 1.0, P, N, N) == _lib.DSA_ERR_INVALID_ARG

@@ -180,8 +180,16 @@ def test_indexer_kl_path_cfg3_full_size():
     idx, dense = ops.indexer_topk(qi, ki, w, cfg.K, cu, causal=True, return_scores=True)
     q, kv = x["q"].bfloat16(), x["kv"].bfloat16()
     del x
-    _, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
+    out, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
     tgt = ops.indexer_kl_target(q, kv, idx, lse, W.SM_SCALE, True)
+    # the same target from the P tiles of the attention backward (bf16 P, head mean)
+    dout = (torch.randn(out.shape, device=DEV, generator=torch.Generator(device=DEV).manual_seed(9)) * 0.01).bfloat16()
+    _, _, tgt_b = ops.sparse_mla_bwd_with_target(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    del out, dout
+    assert torch.all(tgt_b[idx < 0] == 0)
+    err = ((tgt_b - tgt).norm() / tgt.norm()).item()
+    assert err < 2e-3, f"target from the backward's P tiles: normalised error {err:.2e}"
+    del tgt_b
     sel = ops.indexer_selected_scores(qi, ki, w, idx, True)
     kl, d = ops.indexer_kl_rows(sel, tgt, idx, T, True, 1.0 / T)
     dq, dw, dk = ops.indexer_scores_bwd(qi, ki, w, idx, d, True)
@@ -315,3 +323,34 @@ def test_indexer_module_trains_with_the_sparse_kl_loss():
         r = P[n].grad
         scale = r.abs().max().clamp_min(1e-30)
         _close(p_.grad.cpu() / scale, r / scale, rel=2e-2, name=n)
+
+
+def test_fused_attention_with_indexer_loss_matches_the_separate_path():
+    """sparse_mla_with_indexer_loss (loss applied in the attention's backward, target from its P
+    tiles) against sparse_mla + indexer_kl_loss: identical attention gradients, the same loss and
+    indexer gradients up to the bf16 rounding of the staged P."""
+    print("[fused attention + indexer loss]", flush=True)
+    from mcore_bridge_amd.dsa import sparse_mla_with_indexer_loss
+    g = torch.Generator().manual_seed(31)
+    T, H, Hi, K = 300, 64, 64, 128
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    qi, ki, w = (x.to(DEV) for x in _indexer_inputs(T, Hi, g))
+    idx = _idx_case(T, K, g, cu=[0, 120, T]).to(DEV)
+    dout = (torch.randn(T, H, 512, generator=g) * 0.01).bfloat16().to(DEV)
+    sc, coeff = W.SM_SCALE, 0.3
+    leaves = lambda: [x.clone().requires_grad_() for x in (q, kv, qi, ki, w)]
+    qa, kva, qia, kia, wa = leaves()
+    out_a, lse_a = ops.sparse_mla_fwd(qa, kva, idx, sc, True)
+    loss_a = indexer_kl_loss(qa, kva, lse_a, idx, qia, kia, wa, sc, coeff, True)
+    (out_a.float() * dout.float()).sum().add(loss_a).backward()
+    qb, kvb, qib, kib, wb = leaves()
+    out_b, loss_b = sparse_mla_with_indexer_loss(qb, kvb, idx, qib, kib, wb, sc, coeff, True)
+    assert loss_b.item() == 0.0                      # filled by the backward pass
+    (out_b.float() * dout.float()).sum().backward()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(qa.grad, qb.grad) and torch.equal(kva.grad, kvb.grad)
+    torch.testing.assert_close(loss_b, loss_a.detach(), rtol=2e-3, atol=1e-7)
+    for name, a, b in (("q_idx", qia.grad, qib.grad), ("k_idx", kia.grad, kib.grad), ("w", wa.grad, wb.grad)):
+        err = ((b.double() - a.double()).norm() / a.double().norm()).item()
+        assert err < 1e-2, f"{name}: normalised difference {err:.2e}"
