@@ -15,11 +15,14 @@
 //   Z   = Q . K^T     (lane = key, 16 heads per lane)   -> scores, and G = dI_j 1[z>0]
 //   Z^T = K . Q^T     (lane = head, 16 keys per lane)   -> G^T and dw
 //   dq^T += K^T . G^T                  (K^T by transposing LDS reads; 128 AGPR accumulators)
-//   c^T  = (wQ)^T . G                  (the pair's dk row, w folded into a bf16 copy of Q in LDS)
-// c^T goes out through the block's own LDS tile (transposed to 256-byte rows) to the pair's
-// key-major row of a staging buffer; a second kernel sums every key's rows (no float atomics:
-// see the sparse MLA backward for the measured atomic rate).  The forward (scores only) runs the
-// Z product alone.
+//   c^T  = (wQ)^T . G                  (the pair's dk row; w folded into a bf16 copy of Q, whose
+//                                       transposed fragments are read once per query into 64
+//                                       AccVGPRs; the four 32-dim tiles as independent chains)
+// The setup issues every load (Q rows, index row, dI, pair rows, head weights) before using any:
+// one memory round trip per query.  c^T goes out through the block's own LDS tile (transposed to
+// 256-byte rows) to the pair's key-major row of a staging buffer; a second kernel sums every
+// key's rows (no float atomics: see the sparse MLA backward for the measured atomic rate).  The
+// forward (scores only) runs the Z product alone.
 //
 // LDS rows are 256 bytes (one key or one head, 128 bf16); 16-byte chunk c of row r sits at slot
 // c ^ swz(r), swz(r) = 2 (r & 3) + ((r >> 2) & 1): the Z operand read (8 consecutive keys, one
@@ -51,6 +54,15 @@ DSA_DEV u32x2 lds_read_tr16(uint32_t a) {
 
 DSA_DEV constexpr uint32_t swz(uint32_t r) { return ((r & 3u) << 1) | ((r >> 2) & 1u); }
 
+// C += A * B with A in AccVGPRs (loop-invariant operand), B and C in VGPRs; hazards as the other
+// asm forms (dsa_common.h).
+DSA_DEV void mfma32x32x16_aA_cV(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "a"(a), "v"(b));
+}
+DSA_DEV void mfma32x32x16_aA_cV_first(f32x16& c, const u32x4& a, const u32x4& b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=v"(c) : "a"(a), "v"(b));
+}
+
 struct IdxSmem {
   union {
     struct {
@@ -77,9 +89,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hb = lane >> 5, hl = lane & 31;
-  const int nblk = stage_index_row<4>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_k, p.causal, t);
-  const int kpad = nblk * 32;
-
+  // ---- setup: every load issued before any is used (one memory round trip)
   // Q fragments (A of Z, B of Z^T): head 32 mh + hl, dims 16 ks + 8 hb .. +7
   const bf16_t* qt_row = p.q + (int64_t)t * p.q_stride_t;
   u32x4 qf[2][8];
@@ -103,31 +113,70 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
         const int h = 32 * mh + (i >> 2) * 8 + 4 * hb + (i & 3);
         wz[mh][i] = h < p.n_heads ? wrow[h] : 0.f;
       }
-  } else {
-    // dI and the staging row of every slot; the w-scaled Q rows
-    const float* drow = p.d_index + (int64_t)t * p.d_stride;
-    const int64_t* prow = p.pair_pos + (int64_t)t * p.topk;
-    for (int j = threadIdx.x; j < kpad; j += 256) {
-      const bool ok = sm.idx[j] >= 0;
-      sm.row[j] = ok ? drow[j] : 0.f;
-      const int64_t ps = ok ? prow[j] : -1;
-      sm.pos[j] = (int32_t)(ps >= 0 ? ps : p.g_sink_row);
-    }
+  }
+  // index row and, backward, dI and the staging row of every slot
+  constexpr int kPer = kMaxTopkIdx / 256;
+  const int32_t* idx_row = p.idx + (int64_t)t * p.idx_stride;
+  const float* drow = kBwd ? p.d_index + (int64_t)t * p.d_stride : nullptr;
+  const int64_t* prow = kBwd ? p.pair_pos + (int64_t)t * p.topk : nullptr;
+  int32_t iv[kPer];
+  float dv[kPer];
+  int64_t pv[kPer];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int cid = threadIdx.x + 256 * r;
-      const int h = cid >> 4, c = cid & 15;
-      const bool ok = h < p.n_heads;
-      const u32x4 v = gload16(qt_row + (ok ? h : 0) * kDi + 8 * c);
-      const float wh = ok ? wrow[h] : 0.f;
-      u32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(wh * bf16_lo(v[e]), wh * bf16_hi(v[e]));
-      lds_store16(const_cast<char*>(&sm.qw[h * kRowB + 16 * (c ^ swz(h))]), o);
+  for (int i = 0; i < kPer; ++i) {
+    const int j = threadIdx.x + 256 * i;
+    const bool in = j < p.topk;
+    iv[i] = in ? idx_row[j] : -1;
+    if (kBwd) {
+      dv[i] = in ? drow[j] : 0.f;
+      pv[i] = in ? prow[j] : -1;
     }
   }
+  // backward: rows of Q and the head weights for the w-scaled copy
+  u32x4 qv4[4];
+  float wh4[4];
+  if (kBwd) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = (threadIdx.x + 256 * r) >> 4, c = (threadIdx.x + 256 * r) & 15;
+      const bool ok = h < p.n_heads;
+      qv4[r] = gload16(qt_row + (ok ? h : 0) * kDi + 8 * c);
+      wh4[r] = ok ? wrow[h] : 0.f;
+    }
+  }
+  const int kpad_t = (p.topk + 31) / 32 * 32;
+  int last = -1;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = threadIdx.x + 256 * i;
+    if (j < kpad_t) {
+      int x = iv[i];
+      if (x < 0 || x >= p.n_k || (p.causal && x > t)) x = -1;
+      sm.idx[j] = x;
+      if (x >= 0) last = j;
+      if (kBwd) {
+        sm.row[j] = x >= 0 ? dv[i] : 0.f;
+        sm.pos[j] = (int32_t)(x >= 0 && pv[i] >= 0 ? pv[i] : p.g_sink_row);
+      }
+    }
+  }
+  if (kBwd) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int h = (threadIdx.x + 256 * r) >> 4, c = (threadIdx.x + 256 * r) & 15;
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(wh4[r] * bf16_lo(qv4[r][e]), wh4[r] * bf16_hi(qv4[r][e]));
+      lds_store16(&sm.qw[h * kRowB + 16 * (c ^ swz(h))], o);
+    }
+  }
+  last = wave_max_i(last);
+  if (lane == 0) sm.red[wave] = last;
   wait_vmcnt0();   // every compiler-visible load retired before the asynchronous copies start
   __syncthreads();
+  last = max(max(sm.red[0], sm.red[1]), max(sm.red[2], sm.red[3]));
+  const int nblk = __builtin_amdgcn_readfirstlane((last + 32) / 32);
+  const int kpad = nblk * 32;
 
   const uint32_t tiles = lds_addr(sm.tile[wave][0]);
   const uint32_t qw0 = lds_addr(sm.qw);
@@ -165,6 +214,21 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
         }
   }
 
+  // (wQ)^T fragments for the dk-row product, read once per query: [mt][mh][s]
+  u32x4 qt[4][2][2];
+  if (kBwd) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const uint32_t base = qw0 + mh * kKTile + 128u * (mt >> 1);
+          const u32x2 lo = lds_read_tr16(base + troff[s2][0][mt & 1]);
+          const u32x2 hi = lds_read_tr16(base + troff[s2][1][mt & 1]);
+          qt[mt][mh][s2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+  }
   f32x16 dqa[4][2];
   float dwacc[2] = {0.f, 0.f};
   if (kBwd) {
@@ -266,29 +330,30 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
         __builtin_amdgcn_sched_barrier(0);
       }
 
-    // ---- c^T[dims x keys] = (wQ)^T . G, staged as 256-byte key rows in this block's tile
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      f32x16 c;
-      const uint32_t o = 128u * (mt >> 1);
+    // ---- c^T[dims x keys] = (wQ)^T . G: four independent dim-tile chains, then staged as 256-byte
+    // key rows in this block's tile
+    {
+      f32x16 c[4];
 #pragma unroll
       for (int mh = 0; mh < 2; ++mh)
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const uint32_t base = qw0 + mh * kKTile + o;
-          const u32x2 lo = lds_read_tr16(base + troff[s][0][mt & 1]);
-          const u32x2 hi = lds_read_tr16(base + troff[s][1][mt & 1]);
-          const u32x4 qa = u32x4{lo[0], lo[1], hi[0], hi[1]};
-          if (mh == 0 && s == 0) mfma32x32x16_cV_first(c, qa, gz[mh][s]);
-          else mfma32x32x16_cV(c, qa, gz[mh][s]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            if (mh == 0 && s == 0) mfma32x32x16_aA_cV_first(c[mt], qt[mt][mh][s], gz[mh][s]);
+            else mfma32x32x16_aA_cV(c[mt], qt[mt][mh][s], gz[mh][s]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
       mfma_acc_drain();
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const u32x2 v = u32x2{pack_bf16x2(c[4 * gq], c[4 * gq + 1]), pack_bf16x2(c[4 * gq + 2], c[4 * gq + 3])};
-        *reinterpret_cast<u32x2*>(const_cast<char*>(lds_ptr(tb + hl * kRowB + 16u * ((4u * mt + gq) ^ swz(hl)) + 8u * hb))) = v;
-      }
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const u32x2 v = u32x2{pack_bf16x2(c[mt][4 * gq], c[mt][4 * gq + 1]),
+                                pack_bf16x2(c[mt][4 * gq + 2], c[mt][4 * gq + 3])};
+          *reinterpret_cast<u32x2*>(const_cast<char*>(
+              lds_ptr(tb + hl * kRowB + 16u * ((4u * mt + gq) ^ swz(hl)) + 8u * hb))) = v;
+        }
     }
     // ---- key rows out: copy s writes keys 4s .. 4s+3, 16 lanes per 256-byte row
     {
