@@ -354,3 +354,22 @@ def test_fused_attention_with_indexer_loss_matches_the_separate_path():
     for name, a, b in (("q_idx", qia.grad, qib.grad), ("k_idx", kia.grad, kib.grad), ("w", wa.grad, wb.grad)):
         err = ((b.double() - a.double()).norm() / a.double().norm()).item()
         assert err < 1e-2, f"{name}: normalised difference {err:.2e}"
+
+
+def test_indexer_scores_bwd_more_keys_than_the_lds_pair_order_holds():
+    """n_k = 20000 > 16384: the pair order takes its global-atomic path."""
+    print("[indexer scores bwd] n_k=20000", flush=True)
+    g = torch.Generator().manual_seed(20001)
+    T, Hi, K, N = 64, 64, 256, 20000
+    qi = (torch.randn(T, Hi, 128, generator=g) * 0.3).bfloat16()
+    ki = (torch.randn(N, 128, generator=g) * 0.3).bfloat16()
+    w = (torch.randn(T, Hi, generator=g) * 0.1).bfloat16().float()
+    idx = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[:, :8] = torch.arange(8, dtype=torch.int32)
+    idx[3, 50:] = -1
+    dI = torch.randn(T, K, generator=g) * 0.01
+    dq, dw, dk = ops.indexer_scores_bwd(qi.to(DEV), ki.to(DEV), w.to(DEV), idx.to(DEV), dI.to(DEV), False)
+    rq, rk, rw = O.indexer_scores_bwd(qi, ki, w, idx, dI)
+    _close(dq.cpu(), rq, name="dq")
+    _close(dw.cpu(), rw, name="dw")
+    _close(dk.cpu(), rk, name="dk")

@@ -582,3 +582,21 @@ def test_sparse_decode_cfg5_full_size():
                                            torch.arange(rows.numel(), dtype=torch.int32)[None], W.SM_SCALE)
         _close(out[b:b + 1].cpu(), o_ref, name=f"seq {b}")
         _close(lse[b:b + 1].cpu(), l_ref, rel=1e-4, name=f"lse {b}")
+
+
+def test_sparse_bwd_more_keys_than_the_lds_pair_order_holds():
+    """n_kv = 20000 > 16384: the pair order takes its global-atomic path (no LDS histograms)."""
+    print("[sparse bwd] n_kv=20000", flush=True)
+    g = torch.Generator().manual_seed(20000)
+    T, H, K, N = 64, 16, 256, 20000
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(N, 576, generator=g) * 0.1).bfloat16()
+    idx = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[:, :8] = torch.arange(8, dtype=torch.int32)          # shared keys: several pairs per key
+    idx[5, 100:] = -1
+    dout = (torch.randn(T, H, 512, generator=g) * 0.01).bfloat16()
+    out, lse = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE, False)
+    dq, dkv = ops.sparse_mla_bwd(q.to(DEV), kv.to(DEV), idx.to(DEV), out, dout.to(DEV), lse, W.SM_SCALE, False)
+    rdq, rdkv = O.sparse_mla_bwd(q, kv, idx.long(), out.cpu(), dout, lse.cpu(), W.SM_SCALE)
+    _close(dq.cpu(), rdq, name="dq")
+    _close(dkv.cpu(), rdkv, name="dkv")
