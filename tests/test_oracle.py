@@ -475,7 +475,7 @@ def test_naive_fp32_compositions_match_oracle():
 
 
 def test_algorithmic_work_constants():
-    # BASELINE.md's N_sel and FLOP figures
+    # selected-pair counts of the benchmark configurations: sum over queries of min(K, visible keys)
     assert W.n_sel([0, 4096], 2048) == 6_292_480
     assert W.n_sel(W.CFG3_CU_SEQLENS, 2048) == 27_602_695
     assert W.n_sel([0, 32768], 2048) == 65_012_736
