@@ -23,6 +23,9 @@
 //                      key-major position.
 //   B4 csr_*           key-major order of the selected pairs: count, scan, position.
 //   B5 bwd_dkv_reduce  per key: fp32 sum of its contiguous G rows -> dKV.
+// The G rows (1152 B per selected pair, far more than the caches hold) are written and read with
+// non-temporal stores and loads, so they stream through L2 without displacing the operands B3
+// and B5 re-read.
 // B1-B3 stream their per-block operands into LDS through 3-stage rings of asynchronous
 // global_load_lds copies (see dsa_kvtile.h) completed by explicit s_waitcnt vmcnt + barrier.
 // vmcnt counts every vector-memory instruction of the wave in issue order, so each wave issues
@@ -791,9 +794,9 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     const u32x4 o{pack_bf16x2(v.a[0], v.a[1]), pack_bf16x2(v.a[2], v.a[3]), pack_bf16x2(v.b[0], v.b[1]),
                   pack_bf16x2(v.b[2], v.b[3])};
     if (i < 8)
-      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rpos[i] * kDqk + 8 * lane) = o;
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rpos[i] * kDqk + 8 * lane));
     else
-      *reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))) = o;
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))));
   };
   // k-step of copy c (c < G) and of store i (i < kGStores); stores follow copies in a step
   constexpr auto copy_ks = [](int c) { return c * KS / G; };
@@ -1025,7 +1028,7 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   const int64_t a = offsets[s], b = offsets[s + 1];
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int64_t i = a + r; i < b; i += 4) {
-    const u32x4 v = gload16(g_stage + i * kDqk + c * 8);
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g_stage + i * kDqk + c * 8));
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       acc[2 * e] += bf16_lo(v[e]);
