@@ -2,12 +2,12 @@
 
 Kernel-native ops (packed THD layout) live in ``ops``; Megatron-compatible drop-ins
 (``fused_qk_topk_naive``, ``sparse_mla_attention``, ``absorbed_mla_sparse_attention``,
-``indexer_forward_before_topk``, ``indexer_kl_loss``, the ``DSAIndexer`` module) in ``dsa``; ``patch.install()`` swaps them
+``indexer_forward_before_topk``, ``indexer_kl_loss``, the ``DSAIndexer`` and ``DSAttention`` modules) in ``dsa``; ``patch.install()`` swaps them
 into Megatron-Core's DSA module when it is importable.  All arithmetic runs in the HIP
 kernels of ``libdsa_amd.so`` (C ABI: include/dsa_abi.h); there is no CPU fallback.
 """
 from . import _lib
-from .dsa import (DSAIndexer, absorbed_mla_sparse_attention, fused_qk_topk_naive, indexer_forward_before_topk,
+from .dsa import (DSAIndexer, DSAttention, absorbed_mla_sparse_attention, fused_qk_topk_naive, indexer_forward_before_topk,
                   indexer_kl_loss, sparse_mla_attention, sparse_mla_with_indexer_loss)
 from .ops import (build_decode_rows, build_rows, bwd_workspace_bytes, decode_indexer_topk, decode_workspace_bytes,
                   indexer_kl_rows, indexer_kl_target, indexer_prologue, indexer_scores, indexer_scores_bwd,
@@ -15,7 +15,7 @@ from .ops import (build_decode_rows, build_rows, bwd_workspace_bytes, decode_ind
                   sparse_mla_fwd, topk)
 
 __all__ = [
-    "DSAIndexer", "absorbed_mla_sparse_attention", "build_decode_rows", "build_rows", "bwd_workspace_bytes", "decode_indexer_topk", "decode_workspace_bytes",
+    "DSAIndexer", "DSAttention", "absorbed_mla_sparse_attention", "build_decode_rows", "build_rows", "bwd_workspace_bytes", "decode_indexer_topk", "decode_workspace_bytes",
     "fused_qk_topk_naive", "indexer_forward_before_topk", "indexer_kl_loss", "indexer_kl_rows", "indexer_kl_target",
     "indexer_prologue", "indexer_scores", "indexer_scores_bwd", "indexer_selected_scores", "indexer_topk",
     "sparse_mla", "sparse_mla_attention", "sparse_mla_bwd", "sparse_mla_decode", "sparse_mla_fwd",

@@ -77,15 +77,17 @@ def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
         if general_mask:
             sc = sc + mask[b].to(torch.float32)
         idx = ops.topk(sc, base, ln, kk).to(torch.int64)            # ascending key ids, -1 pad
+        pad = idx < 0
         if causal:
             # masked (-inf) keys of row t are t+1, t+2, ...: a stable top-k takes them in order,
             # so the padding slot j holds key j.
             slot = torch.arange(kk, device=q.device).expand_as(idx)
-            idx = torch.where(idx < 0, slot, idx)
+            idx = torch.where(pad, slot, idx)
         # reference order: score descending, ties to the lower index (stable sort of an
-        # ascending-index list)
+        # ascending-index list); padded slots score -inf (the masked tail of `sc` is only
+        # written when the scores are returned)
         vals = torch.gather(sc, 1, idx.clamp(min=0))
-        vals = torch.where(idx < 0, torch.full_like(vals, float("-inf")), vals)
+        vals = torch.where(pad, torch.full_like(vals, float("-inf")), vals)
         order = torch.sort(vals, dim=1, descending=True, stable=True).indices
         idx_out[b] = torch.gather(idx, 1, order)
         if scores_out is not None:
@@ -340,3 +342,65 @@ class DSAIndexer(torch.nn.Module):
     def forward(self, x: Tensor, qr: Tensor, mask: Optional[Tensor] = None, packed_seq_params=None) -> Tensor:
         """``topk_indices [B, S, index_topk]`` (patcher.py:362-378)."""
         return self.forward_with_scores(x, qr, mask, packed_seq_params)[1]
+
+
+class DSAttention(torch.nn.Module):
+    """Host mirror of Megatron's ``DSAttention``, the core attention that mcore-bridge's MLA calls
+    as ``self.core_attention(query, key, value, attention_mask, packed_seq_params=(psp,
+    rotary_pos_emb), attn_mask_type=..., x=..., qr=...)`` (reference
+    src/mcore_bridge/model/modules/multi_latent_attention.py:262-270), over the HIP kernels.
+
+    Same forward signature, with the tensors in the kernels' absorbed MQA-latent layout:
+    ``query [S, B, H, 576]`` (q_nope absorbed through ``W_UK``, then q_pe) and ``key [S, B, 576]``
+    = ``[kv_compressed, k_pos_emb]``, the one latent row every head shares; ``value`` is None
+    (V = ``key[..., :512]``).  ``absorbed_mla_sparse_attention`` shows the absorption from the
+    caller's un-absorbed tensors.  The composition is Megatron's:
+    - the indexer's ``forward_before_topk``;
+    - the top-k under the causal mask;
+    - sparse attention over the selected keys, with the causal mask on top;
+    - in training with ``loss_coeff > 0``, the sparse indexer KL loss, applied in the attention's
+      backward. Its value is in ``last_indexer_loss`` after the backward pass.
+    Returns ``[S, B, H * 512]``.  The dense (non-sparse) indexer loss is not built."""
+
+    def __init__(self, indexer: DSAIndexer, softmax_scale: float, loss_coeff: float = 0.0,
+                 use_sparse_loss: bool = True):
+        super().__init__()
+        self.indexer = indexer
+        self.softmax_scale = float(softmax_scale)
+        self.loss_coeff = float(loss_coeff)
+        self.use_sparse_loss = use_sparse_loss
+        self.last_indexer_loss: Optional[Tensor] = None
+
+    def forward(self, query: Tensor, key: Tensor, value: Optional[Tensor], attention_mask: Optional[Tensor],
+                x: Tensor, qr: Tensor, attn_mask_type=None, attention_bias=None, packed_seq_params=None) -> Tensor:
+        assert value is None, "absorbed layout: V is key[..., :512]"
+        assert attention_bias is None, "DSA takes no attention bias"
+        assert attention_mask is None or _is_causal_mask(attention_mask), "DSA attention is causal"
+        S, B, H, D = query.shape
+        train_loss = self.training and self.loss_coeff > 0 and torch.is_grad_enabled()
+        if train_loss and (not self.use_sparse_loss or self.indexer.fp8):
+            raise NotImplementedError("only the sparse indexer loss with the bf16 indexer is built")
+        with torch.set_grad_enabled(train_loss):
+            out = self.indexer.forward_before_topk(x, qr, packed_seq_params)
+        if self.indexer.fp8:
+            q_i, qs, k_i, ks, w = out
+            _, topk = fused_qk_topk_naive(q_i, k_i, w, self.indexer.index_topk, causal=True, return_scores=False,
+                                          q_scale=qs, k_scale=ks)
+        else:
+            q_i, k_i, w = out
+            _, topk = fused_qk_topk_naive(q_i.detach(), k_i.detach(), w.detach(), self.indexer.index_topk,
+                                          causal=True, return_scores=False)
+        if not train_loss:
+            return sparse_mla_attention(query, key, topk, self.softmax_scale, causal=True)
+        # packed THD with global key ids (batch b's keys are rows b*S ..)
+        q_thd = query.transpose(0, 1).reshape(B * S, H, D)
+        kv_thd = key.transpose(0, 1).reshape(B * S, D)
+        off = (torch.arange(B, device=query.device, dtype=torch.int64) * S).view(B, 1, 1)
+        idx = torch.where(topk >= 0, topk + off, torch.full_like(topk, -1)).reshape(B * S, -1).to(torch.int32)
+        Hi = q_i.shape[2]
+        o, loss = sparse_mla_with_indexer_loss(q_thd, kv_thd, idx, q_i.transpose(0, 1).reshape(B * S, Hi, -1),
+                                               k_i.transpose(0, 1).reshape(B * S, -1),
+                                               w.transpose(0, 1).reshape(B * S, Hi), self.softmax_scale,
+                                               self.loss_coeff, True)
+        self.last_indexer_loss = loss
+        return o.reshape(B, S, H * ops.D_V).transpose(0, 1)

@@ -373,3 +373,58 @@ def test_indexer_scores_bwd_more_keys_than_the_lds_pair_order_holds():
     _close(dq.cpu(), rq, name="dq")
     _close(dw.cpu(), rw, name="dw")
     _close(dk.cpu(), rk, name="dk")
+
+
+def test_dsattention_module_composes_indexer_attention_and_loss():
+    """DSAttention (Megatron's core-attention signature, absorbed layout, batch 2): in eval it
+    equals fused_qk_topk_naive on the indexer's outputs + sparse_mla_attention; in training its
+    output and attention gradients are the same, the indexer's parameters receive the sparse KL
+    loss's gradients and last_indexer_loss holds that loss."""
+    print("[DSAttention module]", flush=True)
+    from mcore_bridge_amd.dsa import DSAIndexer, DSAttention, fused_qk_topk_naive, sparse_mla_attention
+    g = torch.Generator().manual_seed(55)
+    S, B, H, hidden, qlr, Hi, K = 160, 2, 16, 256, 192, 64, 48
+    indexer = DSAIndexer(hidden, qlr, index_n_heads=Hi, index_topk=K, device=DEV)
+    with torch.no_grad():
+        for p_ in indexer.parameters():
+            p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(p_.dtype))
+        indexer.k_norm.weight.add_(1.0)
+    coeff, sc = 0.5, W.SM_SCALE
+    attn = DSAttention(indexer, sc, loss_coeff=coeff)
+    query = (torch.randn(S, B, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    key = (torch.randn(S, B, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    x = torch.randn(S, B, hidden, generator=g).bfloat16().to(DEV)
+    qr = torch.randn(S, B, qlr, generator=g).bfloat16().to(DEV)
+    fr = (torch.rand(S, 1, 1, 64, generator=g) * 200).to(DEV)
+    mask = torch.triu(torch.full((S, S), float("-inf"), device=DEV), 1).expand(B, S, S)
+    psp = (None, fr)
+
+    attn.eval()
+    with torch.no_grad():
+        out_e = attn(query, key, None, mask, x, qr, packed_seq_params=psp)
+        q_i, k_i, w = indexer.forward_before_topk(x, qr, psp)
+        _, topk = fused_qk_topk_naive(q_i, k_i, w, K, causal=True, return_scores=False)
+        ref = sparse_mla_attention(query, key, topk, sc, causal=True)
+    assert torch.equal(out_e, ref)
+
+    attn.train()
+    dout = (torch.randn(S, B, H * 512, generator=g) * 0.01).to(DEV)
+    qa, ka = query.clone().requires_grad_(), key.clone().requires_grad_()
+    out_t = attn(qa, ka, None, mask, x, qr, packed_seq_params=psp)
+    assert torch.equal(out_t.detach(), ref)
+    (out_t.float() * dout).sum().backward()
+    qb, kb = query.clone().requires_grad_(), key.clone().requires_grad_()
+    (sparse_mla_attention(qb, kb, topk, sc, causal=True).float() * dout).sum().backward()
+    assert torch.equal(qa.grad, qb.grad) and torch.equal(ka.grad, kb.grad)
+    for n, p_ in indexer.named_parameters():
+        assert p_.grad is not None and bool(torch.isfinite(p_.grad).all()) and p_.grad.abs().sum() > 0, n
+    # the loss it applied: indexer_kl_loss on the same packed inputs
+    off = (torch.arange(B, device=DEV) * S).view(B, 1, 1)
+    idx = torch.where(topk >= 0, topk + off, torch.full_like(topk, -1)).reshape(B * S, -1).to(torch.int32)
+    q_thd, kv_thd = query.transpose(0, 1).reshape(B * S, H, 576), key.transpose(0, 1).reshape(B * S, 576)
+    _, lse = ops.sparse_mla_fwd(q_thd, kv_thd, idx, sc, True)
+    with torch.no_grad():
+        ref_loss = indexer_kl_loss(q_thd, kv_thd, lse, idx, q_i.transpose(0, 1).reshape(B * S, Hi, 128),
+                                   k_i.transpose(0, 1).reshape(B * S, 128), w.transpose(0, 1).reshape(B * S, Hi),
+                                   sc, coeff, True)
+    torch.testing.assert_close(attn.last_indexer_loss, ref_loss, rtol=2e-3, atol=1e-7)

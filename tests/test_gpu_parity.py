@@ -419,6 +419,12 @@ def test_fused_qk_topk_naive_dropin():
     # exactly a stable torch.topk of the returned scores (score desc, ties -> lower index)
     ref_ti = O.topk_reference_order(sc[0].cpu().double().nan_to_num(neginf=-1e300), cfg.K)
     assert torch.equal(ti[0].cpu(), ref_ti)
+    # without the scores (the masked tail of the score rows is then never written): the same
+    # indices in the same order, padded rows included (rows t < K - 1 hold masked keys)
+    for causal in (None, True):
+        none, ti2 = fused_qk_topk_naive(q.to(DEV), k.to(DEV), w.to(DEV), cfg.K, mask.to(DEV), causal=causal,
+                                        return_scores=False)
+        assert none is None and torch.equal(ti2, ti)
 
 
 def test_sparse_mla_attention_sbhd_batch2():
