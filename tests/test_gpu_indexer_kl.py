@@ -428,3 +428,35 @@ def test_dsattention_module_composes_indexer_attention_and_loss():
                                    k_i.transpose(0, 1).reshape(B * S, 128), w.transpose(0, 1).reshape(B * S, Hi),
                                    sc, coeff, True)
     torch.testing.assert_close(attn.last_indexer_loss, ref_loss, rtol=2e-3, atol=1e-7)
+
+
+@pytest.mark.parametrize("T,K", [(1, 1), (37, 5), (40, 1)])
+def test_kl_path_tiny_shapes(T, K):
+    """Partial 32-key blocks and single queries through every kernel of the KL path."""
+    print(f"[kl path tiny] T={T} K={K}", flush=True)
+    g = torch.Generator().manual_seed(100 + T + K)
+    H, Hi = 16, 64
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16()
+    qi, ki, w = _indexer_inputs(T, Hi, g)
+    idx = _idx_case(T, K, g, pad=0.5)
+    if T > 2:
+        idx[2] = -1                                      # a row with no valid key
+    _, lse = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), W.SM_SCALE, True)
+    tgt = ops.indexer_kl_target(q.to(DEV), kv.to(DEV), idx.to(DEV), lse, W.SM_SCALE, True).cpu()
+    _close(tgt, O.attention_head_probs(q, kv, idx, lse.cpu(), W.SM_SCALE), rel=2e-3, name="target", atol=1e-4)
+    sel = ops.indexer_selected_scores(qi.to(DEV), ki.to(DEV), w.to(DEV), idx.to(DEV), True).cpu()
+    valid = idx >= 0
+    ref_sel = torch.gather(O.indexer_scores(qi, ki, w), 1, idx.clamp(min=0).long())
+    assert torch.all(torch.isneginf(sel[~valid]))
+    if valid.any():
+        _close(sel[valid], ref_sel[valid], rel=1e-4, name="scores", atol=1e-4)
+    kl, d = ops.indexer_kl_rows(sel.to(DEV), tgt.to(DEV), idx.to(DEV), T, True, 1.0 / T)
+    rkl, rd = O.indexer_kl_sparse(sel.double(), tgt.double(), valid)
+    torch.testing.assert_close(kl.cpu().double(), rkl, rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(d.cpu().double(), rd / T, rtol=1e-3, atol=1e-7)
+    dI = torch.randn(T, K, generator=g) * 0.01
+    dq, dw, dk = ops.indexer_scores_bwd(qi.to(DEV), ki.to(DEV), w.to(DEV), idx.to(DEV), dI.to(DEV), True)
+    rq, rk, rw = O.indexer_scores_bwd(qi, ki, w, idx, dI)
+    for name, a, b in (("dq", dq, rq), ("dw", dw, rw), ("dk", dk, rk)):
+        torch.testing.assert_close(a.cpu().double(), b, rtol=2e-2, atol=2e-3, msg=lambda m: f"{name}: {m}")
