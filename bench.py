@@ -152,6 +152,21 @@ def decode_leg(torch, dev, reps: int = 50):
             lse.data_ptr(), ws.data_ptr(), ws_bytes, stream)
     _lib.check("dsa_sparse_mla_decode", lib.dsa_sparse_mla_decode(*args))
     t_attn = timed(lambda: lib.dsa_sparse_mla_decode(*args))
+    # the whole decode step (rows, indexer scores, top-k, split attention, merge) replayed from a
+    # HIP graph: the serving path, launch gaps removed
+    def decode_step():
+        ix = ops.decode_indexer_topk(qi, ki, w, K, cu, Lmax)
+        return ops.sparse_mla_decode(q, kv, ix, W.SM_SCALE)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        decode_step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        decode_step()
+    t_step_graph = timed(graph.replay)
+    del graph
     gather = sum(min(K, L) for L in lens) * 576 * 2 + q.numel() * 2 + out.numel() * 2 + idx.numel() * 4
     scan = N * cfg.Di * 2
     gbs = gather / (t_attn * 1e-6) / 1e9
@@ -165,6 +180,7 @@ def decode_leg(torch, dev, reps: int = 50):
         "indexer_topk_us": round(t_sel, 2), "indexer_scan_bytes": scan,
         "indexer_scan_GBs": round(scan / (t_sel * 1e-6) / 1e9, 1),
         "n_split": ws_bytes // (B * H * (512 * 2 + 4)) if ws_bytes else 1,
+        "decode_step_us_hip_graph": round(t_step_graph, 2),
     }
 
 
