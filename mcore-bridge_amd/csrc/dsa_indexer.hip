@@ -16,6 +16,8 @@
 // per key, shared by the 4 waves of a workgroup through L1/L2); C[heads x 32 keys] is reduced
 // over heads in registers: each lane holds 16 heads of one key, so ReLU * w and the head sum
 // are lane-local plus one exchange with the lane 32 apart.
+// At most 512 bf16 queries of 128-dim rows (decode) K1 runs as indexer_scores_rows_kernel instead:
+// one query per workgroup, key rows staged in LDS by contiguous LDS-direct copies.
 // fp8 (OCP e4m3fn, gfx950 MFMA native): I = k_scale[s] * sum_h (w * q_scale)[t,h] *
 // relu(q8 . k8) -- valid because ReLU is positive-homogeneous and both scales are > 0.
 //
@@ -32,6 +34,7 @@ namespace {
 constexpr int kIdxChunkMax = 2048;  // keys per wave work item (prefill)
 constexpr int kIdxChunkMin = 256;
 constexpr int kIdxWaveTarget = 8192;   // shrink the chunk until this many work items exist
+constexpr int kRowsMode = 512;      // at most this many queries (bf16, 128-dim): indexer_scores_rows_kernel
 constexpr int kMaxHi = 64;          // indexer heads handled by the register tiling
 }  // namespace
 
@@ -237,6 +240,89 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
   }
 }
 
+// Few long rows (decode; bf16, 128-dim rows): one query per workgroup, its 4 waves on 4 consecutive
+// key chunks. The query's Q rows are staged once in LDS (chunk u of head row h at u ^ (h & 7): the
+// A-operand reads of 8 consecutive heads are conflict-free) and its head weights sit in registers.
+// Key rows reach LDS through contiguous LDS-direct copies, 1 KB (4 whole rows) per instruction,
+// into a 2-stage ring per wave. The per-lane row loads of indexer_scores_kernel touch 32 rows of
+// 32 B per instruction; at decode's few, very long rows that access pattern, not latency or
+// occupancy, was what held the scan back (cfg5: ~200 us there, ~163 us here, same scores bit for
+// bit). Deeper rings (3-4 stages) cost a workgroup per CU of LDS and ran slower.
+__global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams p) {
+  // Q rows (chunk u of head row h at u ^ (h & 7)), head weights, and per wave a 2-stage ring of
+  // 32-key blocks (chunk c of key r at c ^ (r & 7)) filled by contiguous LDS-direct copies
+  __shared__ __attribute__((aligned(256))) char qs[kMaxHi * 256];
+  __shared__ __attribute__((aligned(256))) char ring[4][2][32 * 256];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.x;
+  const int hb = lane >> 5, hl = lane & 31;
+  constexpr int Di = 128, nks = Di / 16, RB = Di * 2;   // the launcher routes only 128-dim rows here
+  const bf16_t* q = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)t * p.n_heads * Di;
+  for (int c = threadIdx.x; c < kMaxHi * 16; c += 256) {
+    const int h = c >> 4, u = c & 15;
+    const u32x4 v = h < p.n_heads ? gload16(q + (int64_t)h * Di + 8 * u) : u32x4{0, 0, 0, 0};
+    lds_store16(qs + h * 256 + 16 * (u ^ (h & 7)), v);
+  }
+  float wr[2][16];   // weights of the accumulator rows: heads 32 mt + (i/4)*8 + 4 hb + i%4
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int h = 32 * mt + (i >> 2) * 8 + 4 * hb + (i & 3);
+      wr[mt][i] = h < p.n_heads ? p.w[(int64_t)t * p.n_heads + h] : 0.f;
+    }
+  const int c0 = ((int)blockIdx.y * 4 + wave) * p.chunk;
+  const int len = p.row_len[t];
+  const int base = p.row_base[t];
+  wait_vmcnt0();   // compiler-visible loads retired before the copies start
+  __syncthreads();
+  if (c0 >= len) return;
+  const int c1 = min(len, c0 + p.chunk);
+  const char* kbase = reinterpret_cast<const char*>(p.k);
+  const uint32_t ring0 = lds_addr(ring[wave][0]);
+  // copy r of a block moves keys 4r .. 4r+3 -- 1 KB contiguous in memory: lane l fills
+  // slot l & 15 of key 4r + l / 16 with that key's chunk (l & 15) ^ (key & 7)
+  auto gather = [&](uint32_t dst, int k0) {
+    const int kk0 = lane >> 4;
+    const uint32_t sl = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int kk = 4 * r + kk0;
+      const int row = base + min(k0 + kk, c1 - 1);
+      const char* src = kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7));
+      async_copy16_unordered(src, dst + 1024u * r);
+    }
+  };
+  const uint32_t qa0 = lds_addr(qs) + hl * 256, qa1 = lds_addr(qs) + (32 + hl) * 256;
+  gather(ring0, c0);
+  int it = 0;
+  for (int k0 = c0; k0 < c1; k0 += 32, ++it) {
+    const int j = k0 + hl;
+    const uint32_t tb = ring0 + (it & 1) * (32 * 256);
+    if (it == 0) wait_vmcnt<0>();
+    else wait_vmcnt<1>();   // issued after this block's copies: the previous block's score store
+    asm volatile("" ::: "memory");
+    if (k0 + 32 < c1) gather(ring0 + ((it + 1) & 1) * (32 * 256), k0 + 32);
+    uint32_t a0b = qa0, a1b = qa1, kb = tb + hl * 256;
+    asm volatile("" : "+v"(a0b), "+v"(a1b), "+v"(kb));
+    f32x16 c0a = f32x16{}, c1a = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < nks; ++ks) {
+      const uint32_t u = 16u * ((2 * ks + hb) ^ (hl & 7));
+      const u32x4 a0 = lds_load16(lds_ptr(a0b + u)), a1 = lds_load16(lds_ptr(a1b + u));
+      const u32x4 b = lds_load16(lds_ptr(kb + u));
+      c0a = mfma32x32x16(as_bf16x8(a0), as_bf16x8(b), c0a);
+      c1a = mfma32x32x16(as_bf16x8(a1), as_bf16x8(b), c1a);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += wr[0][i] * fmaxf(c0a[i], 0.f) + wr[1][i] * fmaxf(c1a[i], 0.f);
+    acc = xor32_sum(acc);
+    if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc;
+  }
+}
+
 // Fill the masked tail [row_len, pitch) of each score row with -inf (only when the caller
 // wants the reference's dense [S, S] index_scores).
 __global__ void scores_fill_masked_kernel(float* scores, int64_t pitch, const int32_t* row_len, int rows) {
@@ -257,7 +343,10 @@ int launch_indexer_scores(const IndexerParams& p_in, hipStream_t stream) {
   if (p.chunk < 32 || p.chunk % 32 != 0) return -1;
   const dim3 grid((p.total_q + 3) / 4, (unsigned)((max_len + p.chunk - 1) / p.chunk));
   if (grid.y == 0) return 0;
-  if (p.fp8)
+  if (!p.fp8 && p.head_dim == 128 && p.total_q <= kRowsMode) {
+    const dim3 rgrid(p.total_q, (grid.y + 3) / 4);
+    hipLaunchKernelGGL(indexer_scores_rows_kernel, rgrid, dim3(256), 0, stream, p);
+  } else if (p.fp8)
     hipLaunchKernelGGL(indexer_scores_kernel<true>, grid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL(indexer_scores_kernel<false>, grid, dim3(256), 0, stream, p);

@@ -57,7 +57,10 @@ def test_topk_bit_exact_from_fp32_scores(n, k):
 
 
 # ------------------------------------------------------------------ K1 indexer
-@pytest.mark.parametrize("Hi,Di,cu", [(64, 128, [0, 700]), (4, 64, [0, 300, 512]), (64, 128, [0, 100, 2500, 2600])])
+# (at most 512 queries of 128-dim rows take the one-query-per-workgroup form of the scan: the
+#  20-head case has heads that do not fill the 32-head MFMA tiles and rows of 1 and 34 keys)
+@pytest.mark.parametrize("Hi,Di,cu", [(64, 128, [0, 700]), (4, 64, [0, 300, 512]), (64, 128, [0, 100, 2500, 2600]),
+                                      (20, 128, [0, 1, 35, 300]), (64, 128, [0, 512])])
 def test_indexer_scores_bf16(Hi, Di, cu):
     print(f"[indexer bf16] Hi={Hi} Di={Di} cu={cu}", flush=True)
     T = cu[-1]
