@@ -130,9 +130,14 @@ int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const v
 
 /* Top-k selection half of fused_qk_topk_naive (patcher.py:358): for each row the min(topk,
  * row_len) largest scores (ties -> lower key), emitted as key ids row_base + j in ascending
- * order, padded with -1.  out_idx [rows, topk] int32; out_count [rows] (nullable). */
+ * order, padded with -1.  out_idx [rows, topk] int32; out_count [rows] (nullable); every
+ * row_len <= pitch.  workspace (nullable, 16-byte aligned, at least dsa_topk_workspace_size
+ * bytes) lets fewer than 256 rows longer than 8192 keys (decode) split each row over several
+ * workgroups -- the same indices bit for bit; null keeps one workgroup per row. */
+size_t dsa_topk_workspace_size(int rows, int64_t pitch, int topk);
 int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const int32_t* row_len,
-             int rows, int topk, int32_t* out_idx, int32_t* out_count, void* stream);
+             int rows, int topk, int32_t* out_idx, int32_t* out_count, void* workspace,
+             size_t workspace_bytes, void* stream);
 
 /* Sparse MLA forward (DSAttention's un-fused sparse attention, multi_latent_attention.py:262-270),
  * absorbed MQA-latent form: out[t,h] = softmax_j(sm_scale * q[t,h] . kv[idx[t,j]]) kv[idx[t,j], :512],

@@ -202,14 +202,26 @@ int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const v
   return dsa::launch_indexer_scores(p, as_stream(stream));
 }
 
+size_t dsa_topk_workspace_size(int rows, int64_t pitch, int topk) {
+  return dsa::topk_workspace_size(rows, pitch, topk);
+}
+
 int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const int32_t* row_len, int rows,
-             int topk, int32_t* out_idx, int32_t* out_count, void* stream) {
+             int topk, int32_t* out_idx, int32_t* out_count, void* workspace, size_t workspace_bytes,
+             void* stream) {
   if (rows < 0 || topk < 1 || pitch < 0) return DSA_ERR_INVALID_ARG;
   if (rows == 0) return DSA_OK;
   if (!scores || !row_base || !row_len || !out_idx) return DSA_ERR_INVALID_ARG;
   dsa::TopkParams p{};
   p.scores = scores; p.row_base = row_base; p.row_len = row_len; p.out_idx = out_idx; p.out_count = out_count;
   p.rows = rows; p.topk = topk; p.pitch = pitch;
+  const size_t ws = dsa::topk_workspace_size(rows, pitch, topk);
+  if (workspace && ws > 0) {
+    if (workspace_bytes < ws || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+    const size_t n = ws / (sizeof(uint32_t) + sizeof(int32_t));
+    p.cand_key = static_cast<uint32_t*>(workspace);
+    p.cand_idx = reinterpret_cast<int32_t*>(p.cand_key + n);
+  }
   return dsa::launch_topk(p, as_stream(stream));
 }
 

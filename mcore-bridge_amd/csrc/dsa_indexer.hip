@@ -23,8 +23,9 @@
 //
 // K2: one workgroup per row.  4 passes of 8-bit MSB-first radix select over order-preserving
 // uint32 keys (LDS histograms) find the exact K-th largest value; one stable compaction pass
-// (block-wide prefix sums) then emits every larger key plus the lowest-index ties, in ascending
-// key order, -1 padded.
+// (each wave ranks 64 consecutive keys per step with ballots) then emits every larger key plus
+// the lowest-index ties, in ascending key order, -1 padded.  Fewer than 256 rows longer than a slice (decode) are split: a workgroup
+// per (row, 8192-key slice) keeps the slice's top-K, one per row then selects from those.
 #include "dsa_common.h"
 #include "dsa_kernels.h"
 
@@ -362,6 +363,9 @@ int launch_indexer_scores(const IndexerParams& p_in, hipStream_t stream) {
 namespace {
 constexpr int kTopkThreads = 512;
 constexpr int kCacheElems = 16384;  // rows up to this length are cached in LDS (64 KB)
+// histogram copies, interleaved by lane & 7 (bin b, copy c at 8 b + c): the atomics of one
+// instruction that hit one bin land on 8 addresses in 8 banks instead of one
+constexpr int kHistCopies = 8;
 
 DSA_DEV uint32_t order_key(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -369,100 +373,100 @@ DSA_DEV uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Block-wide exclusive scan of one int per thread (kTopkThreads threads); returns the prefix
-// and writes the total to *total.
-DSA_DEV int block_exclusive_scan(int v, int* sh, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int incl = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int n = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += n;
-  }
-  if (lane == 63) sh[wave] = incl;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int w = 0; w < kTopkThreads / 64; ++w) {
-      const int x = sh[w];
-      sh[w] = run;
-      run += x;
-    }
-    sh[kTopkThreads / 64] = run;
-  }
-  __syncthreads();
-  const int res = sh[wave] + incl - v;
-  *total = sh[kTopkThreads / 64];
-  __syncthreads();
-  return res;
-}
 }  // namespace
 
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
-  __shared__ uint32_t cache[kCacheElems];
-  __shared__ int hist[256];
-  __shared__ int sh[kTopkThreads / 64 + 1];
-  __shared__ uint32_t sel_prefix;
-  __shared__ int sel_need;
-  const int row = blockIdx.x;
-  if (row >= p.rows) return;
-  const int n = p.row_len[row];
-  const int base = p.row_base[row];
-  const int K = p.topk;
-  int32_t* out = p.out_idx + (int64_t)row * K;
-  const float* sc = p.scores + (int64_t)row * p.pitch;
-
-  if (n <= K) {  // everything visible is selected
-    for (int j = threadIdx.x; j < K; j += blockDim.x) out[j] = j < n ? base + j : -1;
-    if (p.out_count && threadIdx.x == 0) p.out_count[row] = n;
-    return;
-  }
+// Exact top-k of one list of n > K entries in one workgroup: the K largest under (key desc,
+// position asc), emitted as emit(rank, position, key) with rank ascending in position. Entries are
+// fp32 scores mapped through order_key, or (kKeys) order keys already.
+template <bool kKeys, class Emit>
+DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, int* hist, int* sh,
+                               uint32_t* sel_prefix, int* sel_need, Emit&& emit) {
+  const uint32_t* bits = static_cast<const uint32_t*>(src);
+  auto conv = [](uint32_t x) -> uint32_t { return kKeys ? x : order_key(__builtin_bit_cast(float, x)); };
   const bool cached = n <= kCacheElems;
-  // long rows stay in global memory and are streamed as float4 when the row is 16-byte aligned
-  const bool vec = ((reinterpret_cast<uintptr_t>(sc) & 15) == 0);
-  const float4* sc4 = reinterpret_cast<const float4*>(sc);
-  if (cached)
-    for (int j = threadIdx.x; j < n; j += blockDim.x) cache[j] = order_key(sc[j]);
-  auto key_at = [&](int j) -> uint32_t { return cached ? cache[j] : order_key(sc[j]); };
+  // long lists stay in global memory and are streamed as 16-byte vectors when aligned
+  const bool vec = ((reinterpret_cast<uintptr_t>(bits) & 15) == 0);
+  const uint4* sc4 = reinterpret_cast<const uint4*>(bits);
   constexpr int T = kTopkThreads;
-  // f(j, key) over every element of the row, each thread a strided subset; loads unrolled
+  if (cached) {  // 16-byte loads, 4 in flight per thread: one memory round trip per 8192 entries
+    int j0 = 0;
+    if (vec) {
+      const int n4 = n >> 2;
+      uint4* c4 = reinterpret_cast<uint4*>(cache);
+      int g = threadIdx.x;
+      for (; g + 3 * T < n4; g += 4 * T) {
+        uint4 x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[k] = sc4[g + k * T];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c4[g + k * T] = uint4{conv(x[k].x), conv(x[k].y), conv(x[k].z), conv(x[k].w)};
+      }
+      for (; g < n4; g += T) {
+        const uint4 x = sc4[g];
+        c4[g] = uint4{conv(x.x), conv(x.y), conv(x.z), conv(x.w)};
+      }
+      j0 = 4 * n4;
+    }
+    for (int j = j0 + threadIdx.x; j < n; j += T) cache[j] = conv(bits[j]);
+  }
+  // (the cached and the global paths stay separate loops: a load through a pointer selected
+  // between the two would be a flat load, one round trip per entry)
+  // f(key) over every entry, each thread a strided subset; loads unrolled
   auto for_each_key = [&](auto&& f) {
-    if (cached || !vec) {
-      for (int j = threadIdx.x; j < n; j += T) f(key_at(j));
+    if (cached) {
+      int j = threadIdx.x;
+      for (; j + 3 * T < n; j += 4 * T) {
+        uint32_t x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[k] = cache[j + k * T];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f(x[k]);
+      }
+      for (; j < n; j += T) f(cache[j]);
+      return;
+    }
+    if (!vec) {
+      for (int j = threadIdx.x; j < n; j += T) f(conv(bits[j]));
       return;
     }
     const int n4 = n >> 2;
     int g = threadIdx.x;
     for (; g + 3 * T < n4; g += 4 * T) {
-      float4 x[4];
+      uint4 x[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) x[k] = sc4[g + k * T];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        f(order_key(x[k].x)); f(order_key(x[k].y)); f(order_key(x[k].z)); f(order_key(x[k].w));
+        f(conv(x[k].x)); f(conv(x[k].y)); f(conv(x[k].z)); f(conv(x[k].w));
       }
     }
     for (; g < n4; g += T) {
-      const float4 x = sc4[g];
-      f(order_key(x.x)); f(order_key(x.y)); f(order_key(x.z)); f(order_key(x.w));
+      const uint4 x = sc4[g];
+      f(conv(x.x)); f(conv(x.y)); f(conv(x.z)); f(conv(x.w));
     }
-    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) f(order_key(sc[j]));
+    for (int j = 4 * n4 + threadIdx.x; j < n; j += T) f(conv(bits[j]));
   };
 
   // ---- radix select: find the K-th largest key (prefix over the top 32 bits)
   uint32_t prefix = 0, pmask = 0;
   int need = K;  // still to take from the keys matching the current prefix
+  int* hcopy = hist + (threadIdx.x & (kHistCopies - 1));
+  auto bin_count = [&](int b) {
+    const int4 x = *reinterpret_cast<const int4*>(hist + kHistCopies * b);
+    const int4 y = *reinterpret_cast<const int4*>(hist + kHistCopies * b + 4);
+    return x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
+  };
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += blockDim.x) hist[b] = 0;
+    for (int b = threadIdx.x; b < 256 * kHistCopies; b += blockDim.x) hist[b] = 0;
     __syncthreads();
     for_each_key([&](uint32_t u) {
-      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255], 1);
+      if ((u & pmask) == prefix) atomicAdd(&hcopy[kHistCopies * ((u >> shift) & 255)], 1);
     });
     __syncthreads();
     if (threadIdx.x < 64) {  // one wave: suffix scan of 256 bins, 4 per lane (lane 0 = top bins)
       const int l = threadIdx.x;
       const int b0 = 255 - 4 * l;
-      const int c0 = hist[b0], c1 = hist[b0 - 1], c2 = hist[b0 - 2], c3 = hist[b0 - 3];
+      const int c0 = bin_count(b0), c1 = bin_count(b0 - 1), c2 = bin_count(b0 - 2), c3 = bin_count(b0 - 3);
       const int tot = c0 + c1 + c2 + c3;
       int incl = tot;
 #pragma unroll
@@ -478,66 +482,181 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
           if (above + cs[q] >= need) { bin = b0 - q; break; }
           above += cs[q];
         }
-        sel_prefix = prefix | ((uint32_t)bin << shift);
-        sel_need = need - above;
+        *sel_prefix = prefix | ((uint32_t)bin << shift);
+        *sel_need = need - above;
       }
     }
     __syncthreads();
-    prefix = sel_prefix;
-    need = sel_need;
+    prefix = *sel_prefix;
+    need = *sel_need;
     pmask |= 255u << shift;
     __syncthreads();
   }
   const uint32_t thr = prefix;  // exact K-th largest key; take `need` of the keys equal to it
 
-  // ---- stable compaction in ascending index order (thread = contiguous chunk of 4k keys)
-  const int per = (n + 4 * kTopkThreads - 1) / (4 * kTopkThreads) * 4;
-  const int a = min(n, (int)threadIdx.x * per), b = min(n, a + per);
-  // g(j, key) over the thread's chunk in index order
-  auto for_chunk = [&](auto&& g) {
-    int j = a;
-    if (!cached && vec) {
-      for (; j + 16 <= b; j += 16) {   // 4 loads in flight
-        float4 x[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) x[k] = sc4[(j >> 2) + k];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          g(j + 4 * k, order_key(x[k].x)); g(j + 4 * k + 1, order_key(x[k].y));
-          g(j + 4 * k + 2, order_key(x[k].z)); g(j + 4 * k + 3, order_key(x[k].w));
-        }
+  // ---- stable compaction in ascending position order: wave w takes a contiguous range, 64
+  // consecutive entries per step (conflict-free LDS reads, coalesced global ones), and ranks them
+  // with ballots; the waves' offsets come from one scan of their counts
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int NW = kTopkThreads / 64;
+  const int per_w = (n + 64 * NW - 1) / (64 * NW) * 64;
+  const int wa = min(n, wave * per_w), wb = min(n, wa + per_w);
+  const uint64_t lt_mask = (1ull << lane) - 1;
+  // f(j, key, valid) over the wave's range, 64 consecutive entries per call; global loads 4 steps
+  // ahead
+  auto for_wave_range = [&](auto&& f) {
+    if (cached) {
+      for (int j0 = wa; j0 < wb; j0 += 64) {
+        const int j = j0 + lane;
+        f(j, j < wb ? cache[j] : 0u, j < wb);
       }
-      for (; j + 4 <= b; j += 4) {
-        const float4 x = sc4[j >> 2];
-        g(j, order_key(x.x)); g(j + 1, order_key(x.y)); g(j + 2, order_key(x.z)); g(j + 3, order_key(x.w));
-      }
+      return;
     }
-    for (; j < b; ++j) g(j, key_at(j));
+    int j0 = wa;
+    for (; j0 + 4 * 64 <= wb; j0 += 4 * 64) {
+      uint32_t x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = bits[j0 + 64 * k + lane];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) f(j0 + 64 * k + lane, conv(x[k]), true);
+    }
+    for (; j0 < wb; j0 += 64) {
+      const int j = j0 + lane;
+      f(j, j < wb ? conv(bits[j]) : 0u, j < wb);
+    }
   };
-  int c_gt = 0, c_eq = 0;
-  for_chunk([&](int, uint32_t u) {
-    c_gt += u > thr;
-    c_eq += u == thr;
+  int w_gt = 0, w_eq = 0;
+  for_wave_range([&](int, uint32_t u, bool v) {
+    w_gt += __popcll(__ballot(v && u > thr));
+    w_eq += __popcll(__ballot(v && u == thr));
   });
-  int tot_gt, tot_eq;
-  const int gt_before = block_exclusive_scan(c_gt, sh, &tot_gt);
-  const int eq_before = block_exclusive_scan(c_eq, sh, &tot_eq);
+  if (lane == 0) { sh[wave] = w_gt; sh[NW + wave] = w_eq; }
+  __syncthreads();
+  int gt_before = 0, eq_before = 0;
+  for (int w = 0; w < wave; ++w) { gt_before += sh[w]; eq_before += sh[NW + w]; }
   int pos = gt_before + min(eq_before, need);
-  int eq_rank = eq_before;
-  for_chunk([&](int j, uint32_t u) {
-    bool take = u > thr;
-    if (u == thr) {
-      take = eq_rank < need;
-      ++eq_rank;
-    }
-    if (take) out[pos++] = base + j;
+  int eq_run = eq_before;
+  for_wave_range([&](int j, uint32_t u, bool v) {
+    const bool gt = v && u > thr, eq = v && u == thr;
+    const uint64_t eqm = __ballot(eq);
+    const bool take = gt || (eq && eq_run + __popcll(eqm & lt_mask) < need);
+    const uint64_t tm = __ballot(take);
+    if (take) emit(pos + __popcll(tm & lt_mask), j, u);
+    pos += __popcll(tm);
+    eq_run += __popcll(eqm);
   });
-  if (p.out_count && threadIdx.x == 0) p.out_count[row] = K;
 }
 
-int launch_topk(const TopkParams& p, hipStream_t stream) {
-  if (p.rows == 0) return 0;
-  hipLaunchKernelGGL(topk_kernel, dim3(p.rows), dim3(kTopkThreads), 0, stream, p);
+#define DSA_TOPK_SHARED                               \
+  __shared__ __attribute__((aligned(16))) uint32_t cache[kCacheElems]; \
+  __shared__ __attribute__((aligned(16))) int hist[256 * kHistCopies]; \
+  __shared__ int sh[2 * (kTopkThreads / 64)];         \
+  __shared__ uint32_t sel_prefix;                     \
+  __shared__ int sel_need
+
+// One row in one workgroup: rows of at most K visible keys take them all, -1 padded.
+DSA_DEV void topk_row(const TopkParams& p, int row, int n, uint32_t* cache, int* hist, int* sh,
+                      uint32_t* sel_prefix, int* sel_need) {
+  const int base = p.row_base[row];
+  const int K = p.topk;
+  int32_t* out = p.out_idx + (int64_t)row * K;
+  if (n <= K) {  // everything visible is selected
+    for (int j = threadIdx.x; j < K; j += blockDim.x) out[j] = j < n ? base + j : -1;
+  } else {
+    block_select_topk<false>(p.scores + (int64_t)row * p.pitch, n, K, cache, hist, sh, sel_prefix, sel_need,
+                             [&](int r, int j, uint32_t) { out[r] = base + j; });
+  }
+  if (p.out_count && threadIdx.x == 0) p.out_count[row] = min(n, K);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(TopkParams p) {
+  DSA_TOPK_SHARED;
+  const int row = blockIdx.x;
+  if (row >= p.rows) return;
+  topk_row(p, row, p.row_len[row], cache, hist, sh, &sel_prefix, &sel_need);
+}
+
+// Few long rows (decode): a row longer than one slice is split over blockIdx.y. Slice g keeps its
+// own top-K (or all of it, when shorter -- only a row's last slice can be) as order keys and key
+// ids at candidates [g K, (g+1) K) of the row; topk_merge_kernel then selects from the candidates.
+// Every key of the row's top-K is in its slice's top-K (fewer than K keys of the row, hence of the
+// slice, come before it), and candidate positions ascend with the key ids, so the merge's
+// (key desc, position asc) order is the row's (score desc, key asc) order: the result is the
+// one-workgroup selection's, bit for bit.
+__global__ __launch_bounds__(kTopkThreads) void topk_slice_kernel(TopkParams p) {
+  DSA_TOPK_SHARED;
+  const int row = blockIdx.x, g = blockIdx.y;
+  if (row >= p.rows) return;
+  const int n = (int)min((int64_t)p.row_len[row], p.pitch);
+  if (n <= p.slice) {  // the whole row in slice 0's workgroup
+    if (g == 0) topk_row(p, row, n, cache, hist, sh, &sel_prefix, &sel_need);
+    return;
+  }
+  const int j0 = g * p.slice;
+  if (j0 >= n) return;
+  const int m = min(p.slice, n - j0);
+  const int K = p.topk;
+  const int key0 = p.row_base[row] + j0;
+  const int64_t c0 = ((int64_t)row * p.n_slices + g) * K;
+  uint32_t* ck = p.cand_key + c0;
+  int32_t* ci = p.cand_idx + c0;
+  const float* sc = p.scores + (int64_t)row * p.pitch + j0;
+  if (m <= K) {
+    for (int j = threadIdx.x; j < m; j += blockDim.x) {
+      ck[j] = order_key(sc[j]);
+      ci[j] = key0 + j;
+    }
+    return;
+  }
+  block_select_topk<false>(sc, m, K, cache, hist, sh, &sel_prefix, &sel_need, [&](int r, int j, uint32_t u) {
+    ck[r] = u;
+    ci[r] = key0 + j;
+  });
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(TopkParams p) {
+  DSA_TOPK_SHARED;
+  const int row = blockIdx.x;
+  if (row >= p.rows) return;
+  const int n = (int)min((int64_t)p.row_len[row], p.pitch);
+  if (n <= p.slice) return;  // done by topk_slice_kernel
+  const int K = p.topk;
+  const int full = (n - 1) / p.slice;  // slices before the last: K candidates each
+  const int nc = full * K + min(K, n - full * p.slice);
+  const int64_t c0 = (int64_t)row * p.n_slices * K;
+  const int32_t* ci = p.cand_idx + c0;
+  int32_t* out = p.out_idx + (int64_t)row * K;
+  block_select_topk<true>(p.cand_key + c0, nc, K, cache, hist, sh, &sel_prefix, &sel_need,
+                          [&](int r, int j, uint32_t) { out[r] = ci[j]; });
+  if (p.out_count && threadIdx.x == 0) p.out_count[row] = K;
+}
+#undef DSA_TOPK_SHARED
+
+// Split selection: fewer rows than this leave CUs idle in one-workgroup-per-row selection.
+constexpr int kTopkSplitRows = 256;
+constexpr int kTopkSliceMin = 8192;
+
+int topk_slice_len(int topk) { return max(kTopkSliceMin, (topk + 3) / 4 * 16); }
+
+size_t topk_workspace_size(int rows, int64_t pitch, int topk) {
+  if (rows <= 0 || rows >= kTopkSplitRows || topk < 1) return 0;
+  const int64_t slice = topk_slice_len(topk);
+  if (pitch <= slice) return 0;
+  const int64_t n_slices = (pitch + slice - 1) / slice;
+  return (size_t)rows * n_slices * topk * (sizeof(uint32_t) + sizeof(int32_t));
+}
+
+int launch_topk(const TopkParams& p_in, hipStream_t stream) {
+  if (p_in.rows == 0) return 0;
+  TopkParams p = p_in;
+  if (p.cand_key && topk_workspace_size(p.rows, p.pitch, p.topk) > 0) {
+    p.slice = topk_slice_len(p.topk);
+    p.n_slices = (int)((p.pitch + p.slice - 1) / p.slice);
+    hipLaunchKernelGGL(topk_slice_kernel, dim3(p.rows, p.n_slices), dim3(kTopkThreads), 0, stream, p);
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(p.rows), dim3(kTopkThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(topk_kernel, dim3(p.rows), dim3(kTopkThreads), 0, stream, p);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -68,6 +68,10 @@ struct TopkParams {
   int32_t* out_count;        // [rows] number selected, or null
   int rows, topk;
   int64_t pitch;
+  // split selection of few long rows (null: one workgroup per row); set by launch_topk
+  uint32_t* cand_key;        // [rows, n_slices, topk] order keys of the slices' candidates
+  int32_t* cand_idx;         // [rows, n_slices, topk] their key ids
+  int slice, n_slices;
 };
 
 struct PrologueParams {
@@ -162,6 +166,8 @@ int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev);
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
+// Workspace bytes of launch_topk's split selection (cand_key + cand_idx); 0 when it is not used.
+size_t topk_workspace_size(int rows, int64_t pitch, int topk);
 int launch_indexer_prologue(const PrologueParams& p, hipStream_t stream);
 int launch_indexer_prologue_bwd(const PrologueBwdParams& p, hipStream_t stream);
 int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream);

@@ -34,7 +34,9 @@ SIGNATURES = {
     "dsa_indexer_scores": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_int,
                                    c_void_p]),
-    "dsa_topk": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "dsa_topk_workspace_size": (c_size_t, [c_int, c_int64, c_int]),
+    "dsa_topk": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                         c_size_t, c_void_p]),
     "dsa_indexer_prologue": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
                                      c_void_p, c_int64, c_int, c_int, c_int, c_int, c_float, c_float, c_float,
                                      c_float, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,

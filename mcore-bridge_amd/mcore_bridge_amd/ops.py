@@ -234,9 +234,12 @@ def topk(scores: Tensor, row_base: Tensor, row_len: Tensor, k: int) -> Tensor:
     s = scores if scores.stride(1) == 1 else scores.contiguous()
     rows = s.shape[0]
     out = torch.empty(rows, k, dtype=torch.int32, device=s.device)
+    # few long rows (decode) split each row over several workgroups through this workspace
+    nws = int(_lib.load().dsa_topk_workspace_size(rows, s.stride(0), k))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=s.device)
     with torch.cuda.device(s.device):
         _lib.call("dsa_topk", _p(s), s.stride(0), _p(row_base.contiguous()), _p(row_len.contiguous()), rows, k,
-                  _p(out), ctypes.c_void_p(0), _stream(s.device))
+                  _p(out), ctypes.c_void_p(0), _p(ws) if nws else ctypes.c_void_p(0), nws, _stream(s.device))
     return out
 
 

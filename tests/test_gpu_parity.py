@@ -35,7 +35,10 @@ def _rows(cu, T, causal=True):
 
 
 # ------------------------------------------------------------------ K2 top-k
-@pytest.mark.parametrize("n,k", [(300, 64), (2048, 2048), (5000, 2048), (20000, 2048), (700, 129), (64, 1)])
+# (24 rows longer than 8192 keys take the split selection: n = 8292 leaves a last slice shorter than
+#  k, 65268 is cfg5's longest cache with 8 slices, 140000 gives more candidates than LDS caches)
+@pytest.mark.parametrize("n,k", [(300, 64), (2048, 2048), (5000, 2048), (20000, 2048), (700, 129), (64, 1),
+                                 (8292, 2048), (65268, 2048), (140000, 2048), (40000, 4096)])
 def test_topk_bit_exact_from_fp32_scores(n, k):
     print(f"[topk] n={n} k={k}", flush=True)
     g = torch.Generator().manual_seed(n + k)
@@ -43,6 +46,7 @@ def test_topk_bit_exact_from_fp32_scores(n, k):
     sc = torch.randn(rows, n, generator=g)
     sc[: rows // 2] = torch.round(sc[: rows // 2] * 3) / 3          # many exact ties
     sc[2, :] = 0.0                                                   # all ties
+    sc[3, :] = torch.where(torch.rand(n, generator=g) < 0.5, -0.0, 0.0)  # signed zeros tie too
     ln = torch.randint(1, n + 1, (rows,), generator=g).to(torch.int32)
     ln[0] = n
     ln[1] = min(n, k)
