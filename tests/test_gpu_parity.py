@@ -60,6 +60,49 @@ def test_topk_bit_exact_from_fp32_scores(n, k):
         assert torch.equal(got[r], ref[:k] if ref.numel() >= k else torch.cat([ref, ref.new_full((k - ref.numel(),), -1)])), r
 
 
+def test_topk_split_equals_one_workgroup_cfg5_full_size():
+    """cfg5's 64 cache lengths (up to 65,265 keys): the split selection (slices + merge, through
+    the workspace) returns the one-workgroup-per-row selection's indices bit for bit, on scores
+    with many exact ties and on the real indexer scores of the decode leg."""
+    import ctypes
+    from mcore_bridge_amd import _lib
+    print("[topk split vs one workgroup, cfg5 full size]", flush=True)
+    cfg = W.CONFIGS["cfg5"]
+    lens = torch.tensor(cfg.decode_lens, dtype=torch.int32)
+    B, L, K = lens.numel(), int(lens.max()), cfg.K
+    pitch = (L + 3) // 4 * 4
+    g = torch.Generator(device=DEV).manual_seed(5)
+    base = (torch.cumsum(lens, 0) - lens).to(torch.int32).to(DEV)
+    ln = lens.to(DEV)
+    lib = _lib.load()
+    nws = int(lib.dsa_topk_workspace_size(B, pitch, K))
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sc_ties = torch.round(torch.randn(B, pitch, generator=g, device=DEV) * 4) / 4
+    qi = (torch.randn(B, cfg.Hi, cfg.Di, generator=g, device=DEV) * 0.1).bfloat16()
+    ki = (torch.randn(int(lens.sum()), cfg.Di, generator=g, device=DEV) * 0.1).bfloat16()
+    w = torch.randn(B, cfg.Hi, generator=g, device=DEV) / 8
+    sc_real = ops.indexer_scores(qi, ki, w, base, ln, L, pitch)
+    res = {}
+    for name, sc in (("ties", sc_ties), ("indexer", sc_real)):
+        got = res[name] = torch.empty(B, K, dtype=torch.int32, device=DEV)
+        ref = torch.empty(B, K, dtype=torch.int32, device=DEV)
+        cnt = torch.empty(B, dtype=torch.int32, device=DEV)
+        assert lib.dsa_topk(P(sc), pitch, P(base), P(ln), B, K, P(got), P(cnt), P(ws), nws, st) == 0
+        assert lib.dsa_topk(P(sc), pitch, P(base), P(ln), B, K, P(ref), None, None, 0, st) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), name
+        assert (cnt == K).all(), name
+        assert torch.equal(ops.topk(sc, base, ln, K), ref), name     # the op takes the split path
+    # one row against the float64 oracle (the longest)
+    r = int(lens.argmax())
+    row = sc_ties[r, :L].double().cpu()
+    want = O.topk_indices(row[None], K)[0] + int(base[r])
+    assert torch.equal(res["ties"][r].cpu().long(), want)
+
+
 # ------------------------------------------------------------------ K1 indexer
 # (at most 512 queries of 128-dim rows take the one-query-per-workgroup form of the scan: the
 #  20-head case has heads that do not fill the 32-head MFMA tiles and rows of 1 and 34 keys)
