@@ -132,7 +132,7 @@ int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const v
  * row_len) largest scores (ties -> lower key), emitted as key ids row_base + j in ascending
  * order, padded with -1.  out_idx [rows, topk] int32; out_count [rows] (nullable); every
  * row_len <= pitch.  workspace (nullable, 16-byte aligned, at least dsa_topk_workspace_size
- * bytes) lets fewer than 256 rows longer than 8192 keys (decode) split each row over several
+ * bytes) lets fewer than 256 rows longer than 16384 keys (decode) split each row over several
  * workgroups -- the same indices bit for bit; null keeps one workgroup per row. */
 size_t dsa_topk_workspace_size(int rows, int64_t pitch, int topk);
 int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const int32_t* row_len,

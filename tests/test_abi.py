@@ -64,9 +64,9 @@ def test_invalid_arguments_rejected_before_launch():
     assert lib.dsa_topk(P, 8, P, P, 4, 2, N, N, N, 0, N) == _lib.DSA_ERR_INVALID_ARG
     # top-k split workspace: few rows longer than a slice only; too small a workspace is refused
     ws = lib.dsa_topk_workspace_size(64, 65268, 2048)
-    assert ws == 64 * 8 * 2048 * 8                               # 8 slices of 8192 keys
+    assert ws == 64 * 4 * 2048 * 8                               # 4 slices of 16384 keys
     assert lib.dsa_topk_workspace_size(256, 65268, 2048) == 0    # the rows alone fill the device
-    assert lib.dsa_topk_workspace_size(64, 8192, 2048) == 0      # one slice per row
+    assert lib.dsa_topk_workspace_size(64, 16384, 2048) == 0     # one slice per row
     assert lib.dsa_topk_workspace_size(0, 65268, 2048) == 0
     assert lib.dsa_topk(P, 65268, P, P, 64, 2048, P, N, P, ws - 1, N) == _lib.DSA_ERR_WORKSPACE
     # backward: heads not a multiple of 16, workspace too small

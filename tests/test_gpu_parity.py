@@ -35,10 +35,10 @@ def _rows(cu, T, causal=True):
 
 
 # ------------------------------------------------------------------ K2 top-k
-# (24 rows longer than 8192 keys take the split selection: n = 8292 leaves a last slice shorter than
-#  k, 65268 is cfg5's longest cache with 8 slices, 140000 gives more candidates than LDS caches)
+# (24 rows longer than 16384 keys take the split selection: n = 16484 leaves a last slice shorter than
+#  k, 65268 is cfg5's longest cache with 4 slices, 140000 gives more candidates than LDS caches)
 @pytest.mark.parametrize("n,k", [(300, 64), (2048, 2048), (5000, 2048), (20000, 2048), (700, 129), (64, 1),
-                                 (8292, 2048), (65268, 2048), (140000, 2048), (40000, 4096)])
+                                 (16484, 2048), (65268, 2048), (140000, 2048), (40000, 4096)])
 def test_topk_bit_exact_from_fp32_scores(n, k):
     print(f"[topk] n={n} k={k}", flush=True)
     g = torch.Generator().manual_seed(n + k)
