@@ -362,7 +362,9 @@ int launch_indexer_scores(const IndexerParams& p_in, hipStream_t stream) {
 // ------------------------------------------------------------------------------------------
 namespace {
 constexpr int kTopkThreads = 512;
-constexpr int kCacheElems = 16384;  // rows up to this length are cached in LDS (64 KB)
+// rows up to this length are cached in LDS (64 KB); a launch sizes its cache to what its rows
+// can need (the pitch, the slice or the candidates), so short rows leave LDS for more workgroups
+constexpr int kCacheElems = 16384;
 // histogram copies, interleaved by lane & 7 (bin b, copy c at 8 b + c): the atomics of one
 // instruction that hit one bin land on 8 addresses in 8 banks instead of one
 constexpr int kHistCopies = 8;
@@ -379,11 +381,11 @@ DSA_DEV uint32_t order_key(float f) {
 // position asc), emitted as emit(rank, position, key) with rank ascending in position. Entries are
 // fp32 scores mapped through order_key, or (kKeys) order keys already.
 template <bool kKeys, class Emit>
-DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, int* hist, int* sh,
+DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, int cache_cap, int* hist, int* sh,
                                uint32_t* sel_prefix, int* sel_need, Emit&& emit) {
   const uint32_t* bits = static_cast<const uint32_t*>(src);
   auto conv = [](uint32_t x) -> uint32_t { return kKeys ? x : order_key(__builtin_bit_cast(float, x)); };
-  const bool cached = n <= kCacheElems;
+  const bool cached = n <= cache_cap;
   // long lists stay in global memory and are streamed as 16-byte vectors when aligned
   const bool vec = ((reinterpret_cast<uintptr_t>(bits) & 15) == 0);
   const uint4* sc4 = reinterpret_cast<const uint4*>(bits);
@@ -548,7 +550,7 @@ DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, i
 }
 
 #define DSA_TOPK_SHARED                               \
-  __shared__ __attribute__((aligned(16))) uint32_t cache[kCacheElems]; \
+  extern __shared__ __attribute__((aligned(16))) uint32_t cache[]; /* p.cache_elems */ \
   __shared__ __attribute__((aligned(16))) int hist[256 * kHistCopies]; \
   __shared__ int sh[2 * (kTopkThreads / 64)];         \
   __shared__ uint32_t sel_prefix;                     \
@@ -563,7 +565,8 @@ DSA_DEV void topk_row(const TopkParams& p, int row, int n, uint32_t* cache, int*
   if (n <= K) {  // everything visible is selected
     for (int j = threadIdx.x; j < K; j += blockDim.x) out[j] = j < n ? base + j : -1;
   } else {
-    block_select_topk<false>(p.scores + (int64_t)row * p.pitch, n, K, cache, hist, sh, sel_prefix, sel_need,
+    block_select_topk<false>(p.scores + (int64_t)row * p.pitch, n, K, cache, p.cache_elems, hist, sh, sel_prefix,
+                             sel_need,
                              [&](int r, int j, uint32_t) { out[r] = base + j; });
   }
   if (p.out_count && threadIdx.x == 0) p.out_count[row] = min(n, K);
@@ -608,7 +611,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_slice_kernel(TopkParams p) 
     }
     return;
   }
-  block_select_topk<false>(sc, m, K, cache, hist, sh, &sel_prefix, &sel_need, [&](int r, int j, uint32_t u) {
+  block_select_topk<false>(sc, m, K, cache, p.cache_elems, hist, sh, &sel_prefix, &sel_need,
+                           [&](int r, int j, uint32_t u) {
     ck[r] = u;
     ci[r] = key0 + j;
   });
@@ -626,7 +630,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(TopkParams p) 
   const int64_t c0 = (int64_t)row * p.n_slices * K;
   const int32_t* ci = p.cand_idx + c0;
   int32_t* out = p.out_idx + (int64_t)row * K;
-  block_select_topk<true>(p.cand_key + c0, nc, K, cache, hist, sh, &sel_prefix, &sel_need,
+  block_select_topk<true>(p.cand_key + c0, nc, K, cache, p.cache_elems, hist, sh, &sel_prefix, &sel_need,
                           [&](int r, int j, uint32_t) { out[r] = ci[j]; });
   if (p.out_count && threadIdx.x == 0) p.out_count[row] = K;
 }
@@ -651,13 +655,18 @@ size_t topk_workspace_size(int rows, int64_t pitch, int topk) {
 int launch_topk(const TopkParams& p_in, hipStream_t stream) {
   if (p_in.rows == 0) return 0;
   TopkParams p = p_in;
+  auto cache_for = [](int64_t n) { return (int)std::min<int64_t>(kCacheElems, (n + 3) / 4 * 4); };
   if (p.cand_key && topk_workspace_size(p.rows, p.pitch, p.topk) > 0) {
     p.slice = topk_slice_len(p.topk);
     p.n_slices = (int)((p.pitch + p.slice - 1) / p.slice);
-    hipLaunchKernelGGL(topk_slice_kernel, dim3(p.rows, p.n_slices), dim3(kTopkThreads), 0, stream, p);
-    hipLaunchKernelGGL(topk_merge_kernel, dim3(p.rows), dim3(kTopkThreads), 0, stream, p);
+    // rows up to one slice run whole in the slice kernel: its cache covers min(pitch, slice)
+    p.cache_elems = cache_for(std::min<int64_t>(p.pitch, p.slice));
+    hipLaunchKernelGGL(topk_slice_kernel, dim3(p.rows, p.n_slices), dim3(kTopkThreads), p.cache_elems * 4, stream, p);
+    p.cache_elems = cache_for((int64_t)p.n_slices * p.topk);
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(p.rows), dim3(kTopkThreads), p.cache_elems * 4, stream, p);
   } else {
-    hipLaunchKernelGGL(topk_kernel, dim3(p.rows), dim3(kTopkThreads), 0, stream, p);
+    p.cache_elems = cache_for(p.pitch);
+    hipLaunchKernelGGL(topk_kernel, dim3(p.rows), dim3(kTopkThreads), p.cache_elems * 4, stream, p);
   }
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }

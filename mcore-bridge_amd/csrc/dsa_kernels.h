@@ -72,6 +72,7 @@ struct TopkParams {
   uint32_t* cand_key;        // [rows, n_slices, topk] order keys of the slices' candidates
   int32_t* cand_idx;         // [rows, n_slices, topk] their key ids
   int slice, n_slices;
+  int cache_elems;           // LDS cache entries of the launch (set by launch_topk)
 };
 
 struct PrologueParams {
