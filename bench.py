@@ -64,46 +64,123 @@ def measured_traffic(kernel: str):
     return None
 
 
-def cpu_baseline(torch):
-    """Reference algorithm class on the host (oracle/dsa_oracle.py naive fp32 compositions):
-    dense indexer scores + full-row top-k, dense index-masked attention forward, autograd
-    backward; bounded sample of the same workload, algorithmic FLOPs / wall time."""
-    from oracle import dsa_oracle as O
-    from mcore_bridge_amd import workloads as W
-    S, H, Hi, Di, K = 2048, 16, 64, 128, 512
+def _median_time(fn, runs: int = 3):
+    """1 warm-up call, then the median wall time of `runs` calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _cpu_rows_case(torch, O, W, name, cfg, L, rows, backward, fp8=False, runs=3):
+    """Time the reference's dense naive path (fused_qk_topk_naive + un-fused masked attention, fp32,
+    autograd backward when `backward`) for the `rows` last query rows of one causal document of L
+    tokens, all heads.  The naive path computes every key of a row (masked, not skipped), so its
+    work is linear in (rows x document length); returns seconds and the extrapolation unit."""
+    H, Hi, Di, K = cfg.H, cfg.Hi, cfg.Di, cfg.K
     g = torch.Generator().manual_seed(0)
-    q = torch.randn(S, 1, H, 576, generator=g) * 0.1
-    kv = torch.randn(S, 1, 576, generator=g) * 0.1
-    qi = torch.randn(S, 1, Hi, Di, generator=g) * 0.1
-    ki = torch.randn(S, 1, Di, generator=g) * 0.1
-    w = torch.randn(S, 1, Hi, generator=g) / 8
-    dout = torch.randn(S, 1, H * 512, generator=g) * 0.01
-    mask = torch.triu(torch.full((S, S), float("-inf")), 1)[None]
+    a = L - rows
+    q = torch.randn(rows, 1, H, 576, generator=g) * 0.1
+    kv = torch.randn(L, 1, 576, generator=g) * 0.1
+    sd = 1.0 if fp8 else 0.1
+    qi = torch.randn(rows, 1, Hi, Di, generator=g) * sd
+    ki = torch.randn(L, 1, Di, generator=g) * sd
+    if fp8:   # cfg4 stores the indexer inputs as e4m3fn + scales; the naive path dequantises them
+        q8, qs = W.quantize_e4m3_rows(qi)
+        k8, ks = W.quantize_e4m3_rows(ki)
+        qi, ki = (q8, qs), (k8, ks)
+    w = torch.randn(rows, 1, Hi, generator=g) / 8
+    dout = torch.randn(rows, 1, H * 512, generator=g) * 0.01
+    mask = torch.triu(torch.full((rows, L), float("-inf")), diagonal=1 + a)[None]
 
     def run():
-        _, ti = O.naive_fused_qk_topk_fp32(qi, ki, w, K, mask)
-        qq = q.clone().requires_grad_()
-        kk = kv.clone().requires_grad_()
-        o = O.naive_unfused_sparse_attn_fp32(qq, kk, ti, W.SM_SCALE)
-        o.backward(dout)
+        qq, kk = qi, ki
+        if fp8:
+            qq = qi[0].float() * qi[1][..., None]
+            kk = ki[0].float() * ki[1][..., None]
+        _, ti = O.naive_fused_qk_topk_fp32(qq, kk, w, K, mask)
+        qg = q.clone().requires_grad_(backward)
+        kg = kv.clone().requires_grad_(backward)
+        with torch.set_grad_enabled(backward):
+            o = O.naive_unfused_sparse_attn_fp32(qg, kg, ti, W.SM_SCALE, q_offset=a)
+            if backward:
+                o.backward(dout)
         return o
 
-    run()
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    nsel = W.n_sel([0, S], K)
-    flops = 7680 * H * nsel + 2 * Di * Hi * W.n_pairs([0, S])
+    return _median_time(run, runs), rows * L
+
+
+def cpu_baseline(torch, dev):
+    """The reference's algorithm class on the host cores, per configuration (the oracle's fp32
+    restatements of fused_qk_topk_naive and the un-fused masked attention; autograd backward):
+      cfg1: the whole fwd+bwd (S=512);
+      cfg2 / cfg3 / cfg4: a block of the last query rows of the longest document, all heads,
+        timed and extrapolated linearly in (query rows x document length) -- the naive path
+        computes every key of every row, masked or not -- to the config's documents;
+      cfg5: every sequence's dense index scan + top-k + attention over the selected rows.
+    1 warm-up, median of 3.  value = the config's algorithmic FLOPs (the same counts as the GPU
+    numbers) / measured or extrapolated time.  The headline object is cfg3's."""
+    from oracle import dsa_oracle as O
+    from mcore_bridge_amd import workloads as W
+    threads = torch.get_num_threads()
+    per = {}
+
+    def flops(cu, K, H, Hi, Di, backward):
+        return ((7680 if backward else 2176) * H * W.n_sel(cu, K) + 2 * Di * Hi * W.n_pairs(cu))
+
+    # cfg1: whole problem
+    c1 = W.CONFIGS["cfg1"]
+    t, _ = _cpu_rows_case(torch, O, W, "cfg1", c1, c1.S, c1.S, True)
+    f = flops([0, c1.S], c1.K, c1.H, c1.Hi, c1.Di, True)
+    per["cfg1"] = {"value": round(f / t / 1e12, 6), "unit": "TFLOP/s", "ms": round(t * 1e3, 2),
+                   "sample": "whole fwd+bwd, S=512, H=16, Hi=4, Di=64, top-k 128"}
+    for name, rows, backward, fp8 in (("cfg2", 64, False, False), ("cfg3", 32, True, False), ("cfg4", 16, False, True)):
+        c = W.CONFIGS[name]
+        cu = c.docs
+        lens = [b - a for a, b in zip(cu[:-1], cu[1:])]
+        L = max(lens)
+        t, unit = _cpu_rows_case(torch, O, W, name, c, L, rows, backward, fp8)
+        full_units = sum(x * x for x in lens)
+        t_full = t * full_units / unit
+        f = flops(cu, c.K, c.H, c.Hi, c.Di, backward)
+        per[name] = {"value": round(f / t_full / 1e12, 6), "unit": "TFLOP/s",
+                     "ms_extrapolated": round(t_full * 1e3, 1), "ms_sample": round(t * 1e3, 1),
+                     "sample": (f"last {rows} query rows of a causal document of {L} tokens, H={c.H}, Hi={c.Hi}, "
+                                f"top-k {c.K}, {'fwd+bwd' if backward else 'fwd'}"
+                                f"{', indexer inputs e4m3fn dequantised' if fp8 else ''}; extrapolated x"
+                                f"{full_units / unit:.1f} (sum of document length^2 / (rows x {L}))")}
+    # cfg5: all 64 sequences (bf16 inputs drawn on the device, copied to the host, converted to
+    # fp32 per sequence inside the timed region)
+    c5 = W.CONFIGS["cfg5"]
+    lens = c5.decode_lens
+    g = torch.Generator(device=dev).manual_seed(0)
+    N = sum(lens)
+    kv = torch.empty(N, 576, dtype=torch.bfloat16)
+    for a0 in range(0, N, 1 << 20):
+        n = min(N - a0, 1 << 20)
+        kv[a0:a0 + n] = (torch.randn(n, 576, generator=g, device=dev) * 0.1).bfloat16().cpu()
+    kc = (torch.randn(N, c5.Di, generator=g, device=dev) * 0.1).bfloat16().cpu()
+    q = (torch.randn(len(lens), c5.H, 576, generator=g, device=dev) * 0.1).bfloat16().cpu()
+    qi = (torch.randn(len(lens), c5.Hi, c5.Di, generator=g, device=dev) * 0.1).bfloat16().cpu()
+    w = (torch.randn(len(lens), c5.Hi, generator=g, device=dev) / 8).cpu()
+    t = _median_time(lambda: O.naive_decode_fp32(q, kv, qi, kc, w, lens, c5.K, W.SM_SCALE))
+    sel = sum(min(c5.K, L) for L in lens)
+    f = 2176 * c5.H * sel + 2 * c5.Di * c5.Hi * N
+    gather = sel * 576 * 2 + q.numel() * 2 + len(lens) * c5.H * 512 * 2 + len(lens) * c5.K * 4
+    per["cfg5"] = {"value": round(f / t / 1e12, 6), "unit": "TFLOP/s", "ms": round(t * 1e3, 2),
+                   "gather_GBs": round(gather / t / 1e9, 2),
+                   "sample": "all 64 sequences: dense index scan of the whole cache, top-k 2048, attention over "
+                             "the selected rows (128 heads)"}
+    del kv, kc
+    c3 = per["cfg3"]
     return {
-        "value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": (f"one causal document S={S}, H={H} of 128 heads, Hi={Hi}, Di={Di}, top-k={K}: dense fp32 "
-                   f"indexer + full-row top-k, dense index-masked attention fwd + autograd bwd "
-                   f"(reference algorithm class), median of 3 = {t * 1e3:.0f} ms; cpu {_cpu_model()}, "
-                   f"os.cpu_count()={os.cpu_count()}"),
+        "value": c3["value"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": (f"cfg3 ({c3['sample']}); fp32 oracle restatements of the reference's naive path; "
+                   f"cpu {_cpu_model()}, os.cpu_count()={os.cpu_count()}, torch threads {threads}"),
+        "per_config": per,
     }
 
 
@@ -297,6 +374,73 @@ def indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale: float, nsel: i
     return res
 
 
+def _time_ms(torch, fn, reps: int, warm: int = 2):
+    """Average ms of fn() over `reps` calls, HIP events on torch's current stream (every op here
+    launches on it)."""
+    for _ in range(warm):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+PEAK_FP8_TFLOPS = 5000.0
+
+
+def prefill_fwd_leg(torch, dev, name: str, reps: int = 10):
+    """cfg2 (bf16 indexer) or cfg4 (fp8 e4m3fn indexer with absmax row scales, S = 32768): one
+    causal document, indexer scores, top-k 2048 and the bf16 sparse MLA forward (H = 128), each
+    timed on its own with preallocated inputs.  Indexer: 2*Di*Hi flops per visible pair on bf16 /
+    fp8 MFMA; top-k: the fp32 score rows it reads (N_pairs * 4 bytes); forward: 2176*H flops per
+    selected pair on bf16 MFMA."""
+    from mcore_bridge_amd import ops, workloads as W
+    cfg = W.CONFIGS[name]
+    S, H, K = cfg.S, cfg.H, cfg.K
+    x = W.make_prefill(cfg, device=dev, seed=0)
+    q, kv, w = x["q"].bfloat16(), x["kv"].bfloat16(), x["w"]
+    if cfg.fp8_indexer:
+        qi, qs = W.quantize_e4m3_rows(x.pop("q_idx"))
+        ki, ks = W.quantize_e4m3_rows(x.pop("k_idx"))
+    else:
+        qi, ki = x.pop("q_idx").bfloat16(), x.pop("k_idx").bfloat16()
+        qs = ks = None
+    del x
+    cu = torch.tensor([0, S], dtype=torch.int32, device=dev)
+    base, ln = ops.build_rows(cu, S, True)
+    sc = ops.indexer_scores(qi, ki, w, base, ln, S, S, qs, ks, False)
+    idx = ops.topk(sc, base, ln, K)
+    t_sc = _time_ms(torch, lambda: ops.indexer_scores(qi, ki, w, base, ln, S, S, qs, ks, False), reps)
+    t_tk = _time_ms(torch, lambda: ops.topk(sc, base, ln, K), reps)
+    t_fw = _time_ms(torch, lambda: ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True), reps)
+    npairs, nsel = W.n_pairs([0, S]), W.n_sel([0, S], K)
+    fl_i = 2 * cfg.Di * cfg.Hi * npairs
+    fl_f = 2176 * H * nsel
+    peak_i = PEAK_FP8_TFLOPS if cfg.fp8_indexer else PEAK_BF16_TFLOPS
+    ti = fl_i / (t_sc * 1e-3) / 1e12
+    tf = fl_f / (t_fw * 1e-3) / 1e12
+    res = {
+        "workload": (f"{name}: one causal document S={S}, H={H}, d_qk=576, d_v=512, indexer {cfg.Hi}x{cfg.Di} "
+                     f"{'fp8 e4m3fn (absmax row scales)' if cfg.fp8_indexer else 'bf16'}, top-k {K}"),
+        "indexer_ms": round(t_sc, 4), "indexer_tflops": round(ti, 1),
+        "indexer_roofline": {"bound": "mfma", "dtype": "fp8" if cfg.fp8_indexer else "bf16", "achieved": round(ti, 1),
+                             "peak": peak_i, "unit": "TFLOP/s", "frac": round(ti / peak_i, 4),
+                             "algorithmic": fl_i},
+        "topk_ms": round(t_tk, 4), "topk_score_bytes": npairs * 4,
+        "topk_GBs": round(npairs * 4 / (t_tk * 1e-3) / 1e9, 1),
+        "sparse_fwd_ms": round(t_fw, 4), "sparse_fwd_tflops": round(tf, 1),
+        "sparse_fwd_roofline": {"bound": "mfma", "dtype": "bf16", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "algorithmic": fl_f},
+        "chain_ms": round(t_sc + t_tk + t_fw, 4),
+    }
+    del q, kv, qi, ki, sc, idx
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -401,20 +545,38 @@ def main():
     #   fwd, B1 (S, dP), B2 (dQ): MFMA flops;  B3 (dKV partial rows), B5 (dKV reduce): HBM bytes
     #   B3 bytes = G rows N_sel*1152 (write) + P, dS N_sel*H*4 + Q, dO T*H*2176 + idx, pair rows T*K*12
     #   B5 bytes = G rows N_sel*1152 (read) + dKV N_kv*576*4 (write) + key offsets N_kv*8
+    # Algorithmic work of each hot kernel (one launch per step) and the roofline that bounds it:
+    # the attention products are bf16 MFMA flops (fwd 2176*H, B1 S+dP 2176*H, B2 dQ 1152*H, B3 dKV
+    # rows 2176*H per selected pair); B5 streams the per-pair dKV rows, so HBM bytes.  The
+    # algorithmic bytes of each kernel are the operands it must read and the results it must write
+    # (q, O, dO, dq: T*H*(576|512)*2; kv rows N*1152; idx T*K*4; lse T*H*4; dKV N*576*4) -- the
+    # staged P / dS tiles and dKV rows are this design's intermediates and are not counted.
+    qb, ob, kvb, ib, lb = T * H * 576 * 2, T * H * 512 * 2, N * 1152, T * K * 4, T * H * 4
     work = {
-        "sparse_fwd": ("mfma", 2176 * H * nsel, "sparse_mla_fwd_kernel"),
-        "bwd_sp": ("mfma", 2176 * H * nsel, "bwd_sp_kernel"),
-        "bwd_dq": ("mfma", 1152 * H * nsel, "bwd_dq_kernel"),
-        "bwd_g": ("hbm", nsel * 1152 + nsel * H * 4 + T * H * 2176 + T * K * 12, "bwd_g_kernel"),
-        "bwd_dkv_reduce": ("hbm", nsel * 1152 + N * 576 * 4 + N * 8, "bwd_dkv_reduce_kernel"),
+        "sparse_fwd": ("mfma", 2176 * H * nsel, "sparse_mla_fwd_kernel", qb + kvb + ib + ob + lb),
+        "bwd_sp": ("mfma", 2176 * H * nsel, "bwd_sp_kernel", qb + kvb + ib + 2 * ob + lb),
+        "bwd_dq": ("mfma", 1152 * H * nsel, "bwd_dq8_kernel" if H == 128 else "bwd_dq_kernel", kvb + ib + qb),
+        "bwd_g": ("mfma", 2176 * H * nsel, "bwd_g_kernel", qb + ob + kvb + ib),
+        "bwd_dkv_reduce": ("hbm", nsel * 1152 + N * 576 * 4 + N * 8, "bwd_dkv_reduce_kernel", N * 576 * 4),
     }
     dom = max(work, key=lambda k: t[k])
-    bound, amount, kname = work[dom]
+    bound, amount, kname, alg_bytes = work[dom]
     if bound == "mfma":
         achieved, peak, unit = amount / (t[dom] * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
     else:
         achieved, peak, unit = amount / (t[dom] * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
     traffic = measured_traffic(kname)
+    bwd_kernels = [work[k][2] for k in STAGES if k in work] + ["csr_count_lds_kernel", "csr_fill_lds_kernel"]
+    bwd_counter = [measured_traffic(k) for k in bwd_kernels]
+    bwd_alg = qb + kvb + ib + 2 * ob + lb + qb + N * 576 * 4
+    bwd_traffic = {
+        "algorithmic_bytes": bwd_alg,
+        "counter_bytes": sum(bwd_counter) if all(b is not None for b in bwd_counter) else None,
+        "per_kernel_counter_bytes": dict(zip(bwd_kernels, bwd_counter)),
+        "source": "profiles/dsa_cfg3_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; calibrated)",
+    }
+    if bwd_traffic["counter_bytes"]:
+        bwd_traffic["ratio"] = round(bwd_traffic["counter_bytes"] / bwd_alg, 2)
     res = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -441,7 +603,11 @@ def main():
                                                                     / PEAK_BF16_TFLOPS, 4)},
         "roofline": {"bound": bound, "kernel": kname, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": traffic,
-                     "algorithmic": amount, "ms": round(t[dom], 3)},
+                     "traffic_source": "profiles/dsa_cfg3_hbm_traffic.md (committed rocprofv3 PMC summary)",
+                     "algorithmic": amount, "algorithmic_bytes": alg_bytes,
+                     "traffic_over_algorithmic_bytes": round(traffic / alg_bytes, 2) if traffic else None,
+                     "ms": round(t[dom], 3)},
+        "backward_traffic": bwd_traffic,
     }
     if not args.no_decode:
         res["decode"] = decode_leg(torch, dev)
@@ -455,8 +621,13 @@ def main():
         res["indexer_kl"] = indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale, nsel, ws)
         del idx, lse
         print(f"[bench] indexer KL leg done: {res['indexer_kl']['total_ms']} ms", file=sys.stderr, flush=True)
+    if not args.no_decode:
+        for name in ("cfg2", "cfg4"):
+            res[name] = prefill_fwd_leg(torch, dev, name)
+            print(f"[bench] {name} leg done: chain {res[name]['chain_ms']} ms", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(torch)
+        res["cpu_baseline"] = cpu_baseline(torch, dev)
+        print("[bench] cpu baseline done", file=sys.stderr, flush=True)
     print(json.dumps(res), flush=True)
 
 

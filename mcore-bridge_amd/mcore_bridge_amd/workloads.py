@@ -99,6 +99,26 @@ def make_prefill(cfg: Config, device="cpu", seed: int = 0, S: Optional[int] = No
     return out
 
 
+E4M3_MAX = 448.0
+
+
+def quantize_e4m3_rows(x: torch.Tensor, rows_per_chunk: int = 4096):
+    """cfg4's storage format of the indexer inputs: OCP e4m3fn with one fp32 absmax scale per row
+    of the last dim (``scale = absmax / 448``, 1 for an all-zero row), ``x ~= x8 * scale``.
+    Runs on ``x``'s device in chunks of rows (bounded temporaries).  Returns ``(x8, scale)``."""
+    lead = x.shape[:-1]
+    flat = x.reshape(-1, x.shape[-1])
+    x8 = torch.empty(flat.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    sc = torch.empty(flat.shape[0], dtype=torch.float32, device=x.device)
+    for a in range(0, flat.shape[0], rows_per_chunk):
+        c = flat[a:a + rows_per_chunk].to(torch.float32)
+        amax = c.abs().amax(dim=-1)
+        s = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+        x8[a:a + rows_per_chunk] = (c / s[:, None]).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+        sc[a:a + rows_per_chunk] = s
+    return x8.view(*lead, x.shape[-1]), sc.view(lead)
+
+
 def make_decode(cfg: Config, device="cpu", seed: int = 0, lens: Optional[List[int]] = None,
                 H: Optional[int] = None) -> Dict[str, torch.Tensor]:
     """Decode inputs: one query per sequence at position L_b - 1 over a packed latent cache."""

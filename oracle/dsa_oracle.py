@@ -107,6 +107,33 @@ def indexer_scores(q_idx: torch.Tensor, k_idx: torch.Tensor, w: torch.Tensor,
     return scores
 
 
+def indexer_scores_rows(q_idx: torch.Tensor, k_idx: torch.Tensor, w: torch.Tensor, rows,
+                        cu_seqlens: Optional[torch.Tensor] = None, causal: bool = True,
+                        q_scale: Optional[torch.Tensor] = None,
+                        k_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rows ``rows`` of ``indexer_scores`` (``[len(rows), T]`` float64) without forming the
+    ``[T, T]`` matrix: the same sum ``sum_h w[t,h] relu(q[t,h] . k[s])`` for each listed query
+    over every key, ``-inf`` where the key is not visible.  For full-size checks of sampled
+    queries (costs ``len(rows) * Hi * T * Di``)."""
+    T = k_idx.shape[0]
+    start, end = doc_bounds(T, cu_seqlens)
+    kd = k_idx.to(torch.float64)
+    if k_scale is not None:
+        kd = kd * k_scale.to(torch.float64)[:, None]
+    out = torch.full((len(rows), T), NEG_INF, dtype=torch.float64)
+    s = torch.arange(T)
+    for i, t in enumerate(int(r) for r in rows):
+        qd = q_idx[t].to(torch.float64)
+        if q_scale is not None:
+            qd = qd * q_scale[t].to(torch.float64)[:, None]
+        row = (torch.relu(qd @ kd.T) * w[t].to(torch.float64)[:, None]).sum(0)   # [T]
+        vis = (s >= start[t]) & (s < end[t])
+        if causal:
+            vis &= s <= t
+        out[i] = row.masked_fill(~vis, NEG_INF)
+    return out
+
+
 def indexer_scores_bruteforce(q_idx, k_idx, w, cu_seqlens=None, causal=True):
     """Triple loop restatement of ``indexer_scores`` for tiny shapes (pins the einsum)."""
     T, Hi, Di = q_idx.shape
@@ -343,20 +370,43 @@ def naive_fused_qk_topk_fp32(q_sbhd: torch.Tensor, k_sbd: torch.Tensor, w_sbh: t
 
 
 def naive_unfused_sparse_attn_fp32(q_sbhd: torch.Tensor, kv_sbd: torch.Tensor, topk_idx: torch.Tensor,
-                                   sm_scale: float, d_v: int = 512) -> torch.Tensor:
+                                   sm_scale: float, d_v: int = 512, q_offset: int = 0) -> torch.Tensor:
     """Shape-for-shape fp32 restatement of Megatron's un-fused sparse attention in the absorbed
     layout: dense ``[B*H, S, S]`` scores, index mask scattered to 0 at ``topk_idx``, causal
-    ``triu`` mask, float softmax, ``P V``.  ``q [S,B,H,576]``, ``kv [S,B,576]`` -> ``[S,B,H*d_v]``."""
-    S, B, H, D = q_sbhd.shape
-    qf = q_sbhd.float().permute(1, 2, 0, 3)                          # [B, H, S, D]
+    ``triu`` mask, float softmax, ``P V``.  ``q [S,B,H,576]``, ``kv [S,B,576]`` -> ``[S,B,H*d_v]``.
+    ``q`` may hold a block of ``R`` consecutive query rows at positions ``q_offset ..`` of the
+    ``S`` keys (``topk_idx [B,R,K]``): the same dense rows for a row subset of the problem."""
+    R, B, H, D = q_sbhd.shape
+    S = kv_sbd.shape[0]
+    qf = q_sbhd.float().permute(1, 2, 0, 3)                          # [B, H, R, D]
     kf = kv_sbd.float().permute(1, 0, 2)                             # [B, S, D]
-    s = torch.matmul(qf, kf.transpose(1, 2).unsqueeze(1)) * sm_scale  # [B, H, S, S]
-    imask = torch.full((B, S, S), NEG_INF)
+    s = torch.matmul(qf, kf.transpose(1, 2).unsqueeze(1)) * sm_scale  # [B, H, R, S]
+    imask = torch.full((B, R, S), NEG_INF)
     imask.scatter_(-1, topk_idx, 0.0)
-    imask = imask + torch.triu(torch.full((S, S), NEG_INF), diagonal=1)[None]
+    imask = imask + torch.triu(torch.full((R, S), NEG_INF), diagonal=1 + q_offset)[None]
     p = torch.softmax(s + imask[:, None], dim=-1)
-    o = torch.matmul(p, kf[:, None, :, :d_v])                        # [B, H, S, d_v]
-    return o.permute(2, 0, 1, 3).reshape(S, B, H * d_v)
+    o = torch.matmul(p, kf[:, None, :, :d_v])                        # [B, H, R, d_v]
+    return o.permute(2, 0, 1, 3).reshape(R, B, H * d_v)
+
+
+def naive_decode_fp32(q: torch.Tensor, kv_cache: torch.Tensor, q_idx: torch.Tensor, k_cache: torch.Tensor,
+                      w: torch.Tensor, cache_lens, index_topk: int, sm_scale: float, d_v: int = 512):
+    """Per-sequence fp32 composition of the same two stages for decode (one new query per
+    sequence over its cache rows, packed by ``cache_lens``): dense index scores over the whole
+    cache, ``topk``, then dense attention restricted to the selected rows.  No reference
+    counterpart (the reference has no DSA cache); this is the CPU timing of the decode config.
+    Returns ``out [B, H, d_v]`` fp32."""
+    outs = []
+    off = 0
+    for b, L in enumerate(int(x) for x in cache_lens):
+        kc = k_cache[off:off + L].float()
+        sc = (torch.relu(q_idx[b].float() @ kc.T) * w[b].float()[:, None]).sum(0)        # [L]
+        sel = sc.topk(min(index_topk, L)).indices
+        g = kv_cache[off:off + L].float()[sel]                                          # [k, 576]
+        p = torch.softmax((q[b].float() @ g.T) * sm_scale, dim=-1)                      # [H, k]
+        outs.append(p @ g[:, :d_v])
+        off += L
+    return torch.stack(outs)
 
 
 # --------------------------------------------------------------------------------------

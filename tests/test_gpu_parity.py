@@ -601,7 +601,14 @@ def test_sparse_fwd_bwd_cfg3_full_size():
     del x
     out, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
     dq, dkv = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    # out / lse of EVERY query against an fp32 reference: the per-key dKV oracle below takes the
+    # kernel's out and lse of every selecting query, so those must be verified rows, not assumed
+    from gpu_reference import close_on_device, sparse_mla_fwd_fp32
+    ref_o, ref_l = sparse_mla_fwd_fp32(q, kv, idx, W.SM_SCALE, True)
     torch.cuda.synchronize()
+    close_on_device(out, ref_o, name="out (all rows, fp32 reference)")
+    torch.testing.assert_close(lse, ref_l, rtol=1e-4, atol=1e-4)
+    del ref_o, ref_l
     starts = cfg.docs[:-1]
     sample = sorted({0, 1, 31, 2047, 2048, 5000, 10362, starts[1], starts[1] + 2100, starts[2] + 100,
                      starts[3] + 5, T - 1})

@@ -39,6 +39,51 @@ def test_indexer_scores_bruteforce_with_documents():
         torch.testing.assert_close(a[fin], b[fin], rtol=1e-12, atol=1e-12)
 
 
+def test_indexer_scores_rows_equal_full_matrix_rows():
+    # the sampled-row form used by the full-size GPU checks equals the rows of the dense form
+    # (documents, causal and not, fp8 scales), and the brute-force loop
+    g = torch.Generator().manual_seed(11)
+    T, Hi, Di = 23, 3, 8
+    q = torch.randn(T, Hi, Di, generator=g, dtype=torch.float64)
+    k = torch.randn(T, Di, generator=g, dtype=torch.float64)
+    w = torch.randn(T, Hi, generator=g, dtype=torch.float64)
+    qs = torch.rand(T, Hi, generator=g, dtype=torch.float64) + 0.5
+    ks = torch.rand(T, generator=g, dtype=torch.float64) + 0.5
+    cu = torch.tensor([0, 7, 20, 23], dtype=torch.int32)
+    rows = [0, 6, 7, 15, 22]
+    for causal in (True, False):
+        full = O.indexer_scores(q, k, w, cu, causal, q_scale=qs, k_scale=ks)
+        part = O.indexer_scores_rows(q, k, w, rows, cu, causal, q_scale=qs, k_scale=ks)
+        assert torch.equal(torch.isinf(full[rows]), torch.isinf(part))
+        fin = torch.isfinite(part)
+        torch.testing.assert_close(part[fin], full[rows][fin], rtol=1e-12, atol=1e-12)
+    bf = O.indexer_scores_bruteforce(q, k, w, cu, True)[rows]
+    part = O.indexer_scores_rows(q, k, w, rows, cu, True)
+    fin = torch.isfinite(bf)
+    assert torch.equal(fin, torch.isfinite(part))
+    torch.testing.assert_close(part[fin], bf[fin], rtol=1e-12, atol=1e-12)
+
+
+def test_e4m3_row_quantisation():
+    # absmax per row maps to +-448 exactly (the largest finite e4m3fn value), zero rows get
+    # scale 1, and the workload generator's quantiser (bench/test inputs of cfg4) is the oracle's
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(40, 6, 128, generator=g) * 3
+    x[3, 2] = 0.0
+    x8, s = O.quantize_e4m3_rows(x)
+    assert s[3, 2] == 1.0 and (x8[3, 2].float() == 0).all()
+    amax = x.abs().amax(-1)
+    torch.testing.assert_close(s[amax > 0], amax[amax > 0] / 448.0, rtol=0, atol=0)
+    top = x8.float().abs().amax(-1)
+    assert (top[amax > 0] == 448.0).all()
+    # round to nearest: every dequantised value within half an e4m3 ulp (2^-4 relative, 2^-9 near 0)
+    deq = x8.float() * s[..., None]
+    ulp = torch.maximum(x.abs() * 2 ** -3, s[..., None] * 2 ** -9)
+    assert ((deq - x).abs() <= ulp / 2 + 1e-7).all()
+    w8, ws = W.quantize_e4m3_rows(x)
+    assert torch.equal(w8.view(torch.uint8), x8.view(torch.uint8)) and torch.equal(ws, s)
+
+
 def _hadamard(n):
     h = torch.ones(1, 1, dtype=torch.float64)
     while h.shape[0] < n:
@@ -472,6 +517,27 @@ def test_naive_fp32_compositions_match_oracle():
     idx = O.topk_indices(ref, cfg.K)
     o_ref, _ = O.sparse_mla_fwd(x["q"], x["kv"], idx, W.SM_SCALE)
     torch.testing.assert_close(o[:, 0].double().view(S, cfg.H, 512), o_ref, rtol=1e-4, atol=1e-5)
+    # a row block (the bench's CPU timing of the large configs) equals those rows of the whole
+    a, b = 40, 70
+    sc_r, ti_r = O.naive_fused_qk_topk_fp32(x["q_idx"][a:b, None], x["k_idx"][:, None], x["w"][a:b, None], cfg.K,
+                                            mask[:, a:b])
+    torch.testing.assert_close(sc_r[0][fin[a:b]].double(), ref[a:b][fin[a:b]], rtol=1e-5, atol=1e-5)
+    o_r = O.naive_unfused_sparse_attn_fp32(x["q"][a:b, None], x["kv"][:, None], ti_r, W.SM_SCALE, q_offset=a)
+    torch.testing.assert_close(o_r[:, 0].double().view(b - a, cfg.H, 512), o_ref[a:b], rtol=1e-4, atol=1e-5)
+
+
+def test_naive_decode_fp32_matches_oracle():
+    # the decode CPU timing composition equals the oracle's decode scores, selection and attention
+    lens = [50, 130, 7]
+    d = W.make_decode(W.CONFIGS["cfg5"], lens=lens, H=8, seed=3)
+    K = 32
+    o = O.naive_decode_fp32(d["q"], d["kv_cache"], d["q_idx"], d["k_cache"], d["w"], lens, K, W.SM_SCALE)
+    sc = O.decode_indexer_scores(d["q_idx"], d["k_cache"], d["w"], d["cache_offsets"], d["cache_lens"])
+    sel = O.topk_indices(sc, K)
+    offs = d["cache_offsets"].long()[:, None]
+    gidx = torch.where(sel >= 0, sel + offs, sel)
+    o_ref, _ = O.sparse_mla_decode(d["q"], d["kv_cache"], gidx, W.SM_SCALE)
+    torch.testing.assert_close(o.double(), o_ref, rtol=1e-4, atol=1e-5)
 
 
 def test_algorithmic_work_constants():
@@ -571,3 +637,23 @@ def test_sparse_kl_decomposition_equals_dense_megatron_form():
     valid = idx >= 0
     kl, _ = O.indexer_kl_sparse(torch.gather(full, 1, idx.clamp(min=0)), p, valid)
     torch.testing.assert_close(kl.mean() * coeff, ref, rtol=1e-9, atol=1e-12)
+
+
+def test_fp32_torch_reference_matches_oracle():
+    # the fp32 PyTorch reference that the full-size GPU tests run over every row equals the float64
+    # oracle (causal flag, padding, rows without keys), here on the CPU
+    from gpu_reference import sparse_mla_fwd_fp32
+    g = torch.Generator().manual_seed(13)
+    T, H, K = 40, 4, 16
+    q = torch.randn(T, H, 576, generator=g) * 0.1
+    kv = torch.randn(T, 576, generator=g) * 0.1
+    idx = torch.randint(0, T, (T, K), generator=g)
+    idx[3] = -1
+    idx[5, :4] = -1
+    o, l = sparse_mla_fwd_fp32(q, kv, idx, W.SM_SCALE, causal=True, chunk=7)
+    ii = torch.where(idx <= torch.arange(T)[:, None], idx, torch.full_like(idx, -1))
+    ro, rl = O.sparse_mla_fwd(q, kv, ii, W.SM_SCALE)
+    torch.testing.assert_close(o.double(), ro, rtol=1e-5, atol=1e-6)
+    fin = torch.isfinite(rl)
+    assert torch.equal(fin, torch.isfinite(l))
+    torch.testing.assert_close(l.double()[fin], rl[fin], rtol=1e-5, atol=1e-5)
