@@ -33,14 +33,30 @@ from torch import Tensor
 from . import ops
 
 
-def _is_causal_mask(mask: Tensor) -> bool:
-    """True if ``mask`` [B, S, S] is the float causal mask DSAttention builds (0 on/below the
-    diagonal, -inf above)."""
-    S = mask.shape[-1]
-    if mask.shape[-2] != S:
-        return False
-    ref = torch.triu(torch.full((S, S), float("-inf"), device=mask.device, dtype=mask.dtype), diagonal=1)
-    return bool(torch.equal(mask, ref.expand_as(mask)))
+def _split_packed(packed_seq_params):
+    """The caller's ``(psp, rotary_pos_emb)`` tuple (multi_latent_attention.py:260-261)."""
+    if isinstance(packed_seq_params, tuple):
+        return packed_seq_params
+    return packed_seq_params, None
+
+
+def _thd_docs(psp):
+    """``(cu_seqlens_q int32, max_seqlen_q or None)`` of a packed THD ``PackedSeqParams``, else None."""
+    if psp is None or getattr(psp, "qkv_format", "thd") != "thd":
+        return None
+    cu = psp.cu_seqlens_q
+    assert cu is not None, "THD packing needs cu_seqlens_q"
+    cu = cu.to(torch.int32)
+    ms = getattr(psp, "max_seqlen_q", None)
+    return cu, (int(ms) if ms is not None else None)
+
+
+def _mask_type_is_causal(attn_mask_type) -> bool:
+    """DSA attention is causal (DSAttention applies the triu mask on top of the index mask); an
+    explicit ``attn_mask_type`` (Megatron's AttnMaskType) must be a causal kind."""
+    if attn_mask_type is None:
+        return True
+    return "causal" in getattr(attn_mask_type, "name", str(attn_mask_type)).lower()
 
 
 def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
@@ -55,14 +71,24 @@ def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
     and the indices ordered like ``torch.topk`` (score descending) with the tie rule made
     explicit: equal scores -- including the ``-inf`` of masked keys -- go to the lower index.
 
-    Keyword extensions: ``causal`` skips the mask inspection (True = the triu mask);
-    ``return_scores=False`` skips materialising the ``[B, S, S]`` scores (first output None);
-    ``q_scale [S, B, Hi]`` / ``k_scale [S, B]`` with float8_e4m3fn ``q`` / ``k``.
+    A ``mask`` is applied as given: the scores of every key are computed and the mask added, which
+    is exact for any additive mask, the causal ``triu`` one included, and never inspects the mask
+    on the host.  ``causal=True`` declares the mask to be the causal ``triu`` mask (it is then not
+    read) and scores only the visible keys, half the work; ``causal=False`` with no mask scores
+    every key.
+
+    Keyword extensions: ``causal``; ``return_scores=False`` skips materialising the ``[B, S, S]``
+    scores (first output None); ``q_scale [S, B, Hi]`` / ``k_scale [S, B]`` with float8_e4m3fn
+    ``q`` / ``k``.  The scores carry no gradient (see ``DSAIndexer``).
     """
+    if return_scores and torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, weights)):
+        raise NotImplementedError(
+            "fused_qk_topk_naive: the index_scores of this build carry no gradient; differentiate the indexer "
+            "through indexer_kl_loss (sparse loss) or call this under torch.no_grad()")
     S, B, Hi, Di = q.shape
     kk = min(index_topk, S)
     if causal is None:
-        causal = mask is not None and _is_causal_mask(mask)
+        causal = False
     general_mask = mask is not None and not causal
     scores_out = torch.empty(B, S, S, dtype=torch.float32, device=q.device) if (return_scores or general_mask) else None
     idx_out = torch.empty(B, S, kk, dtype=torch.int64, device=q.device)
@@ -120,8 +146,13 @@ def indexer_forward_before_topk(x: Tensor, qr: Tensor, wq_b: Tensor, wk: Tensor,
                                 k_norm_bias: Tensor, weights_proj: Tensor, rotary_pos_emb: Tensor, *,
                                 index_n_heads: int, eps: float = 1e-6, mscale: float = 1.0,
                                 dsa_indexer_rotary_interleaved: bool = False, rotary_interleaved: bool = False,
-                                fp8: bool = False):
+                                fp8: bool = False, positions: Optional[Tensor] = None):
     """``DSAIndexer.forward_before_topk(x, qr)`` (reference patcher.py:245-302), sequence-first.
+
+    ``positions`` (optional, ``[S * B]`` int64 on the device) gives each token's row of
+    ``rotary_pos_emb`` -- for packed THD input (``[T, 1, ...]``), the token's position inside its
+    document, where Megatron's THD RoPE restarts the angles; by default token ``(s, b)`` takes row
+    ``s``.
 
     ``x [S, B, hidden]``, ``qr [S, B, q_lora_rank]`` bf16; the weights of ``linear_wq_b``
     (``[Hi * 128, q_lora_rank]``), ``linear_wk`` (``[128, hidden]``), ``k_norm`` (LayerNorm weight
@@ -138,8 +169,11 @@ def indexer_forward_before_topk(x: Tensor, qr: Tensor, wq_b: Tensor, wk: Tensor,
     q_lin = torch.nn.functional.linear(qrb, wq_b)                       # :271
     k_lin = torch.nn.functional.linear(xb, wk)                          # :281
     w_lin = torch.nn.functional.linear(xb, weights_proj)                # :299
-    fr = rotary_pos_emb.reshape(S, -1).to(torch.float32)
-    fr = fr[:, None, :].expand(S, B, fr.shape[-1]).reshape(T, -1)       # token (s, b) -> angles of s
+    fr = rotary_pos_emb.reshape(-1, rotary_pos_emb.shape[-1]).to(torch.float32)
+    if positions is not None:
+        fr = fr[positions]                                              # token -> angles of its position
+    else:
+        fr = fr[:S, None, :].expand(S, B, fr.shape[-1]).reshape(T, -1)  # token (s, b) -> angles of s
     q, qs, k, ks, w = ops.indexer_prologue(q_lin, k_lin, w_lin, k_norm_weight, k_norm_bias, fr, eps, mscale,
                                            dsa_indexer_rotary_interleaved, rotary_interleaved, fp8)
     q = q.view(S, B, index_n_heads, 128)
@@ -290,6 +324,14 @@ class DSAIndexer(torch.nn.Module):
     reference's bridge maps (``wq_b``, ``wk``, ``k_norm.{weight,bias}``, ``weights_proj``,
     gpt_bridge.py:1292-1306) load one to one.
 
+    Packing: the reference asserts that no ``PackedSeqParams`` is given (patcher.py:256).  This
+    mirror also accepts packed THD input (``psp.qkv_format == 'thd'`` with ``cu_seqlens_q``, as the
+    MLA caller packs it, multi_latent_attention.py:90-96): ``x [T, 1, hidden]``, ``qr [T, q_lora_rank]``
+    (or ``[T, 1, ...]``), RoPE angles restarting at each document, indices restricted to the query's
+    own document.  THD outputs are token-major: ``q [T, Hi, 128]``, ``k [T, 128]``, ``w [T, Hi]``,
+    ``topk_indices [T, K]`` global token ids (ascending, ``-1`` pad) and ``index_scores [T, max_seqlen]``
+    (column j = key ``doc_start + j``, ``-inf`` past the causal row).
+
     ``forward_before_topk`` is differentiable in the bf16 layout (the prologue's backward kernel,
     then the projections' GEMM backward), which is what training the indexer with the sparse KL
     loss needs: pass its outputs to ``indexer_kl_loss``.  ``forward_with_scores`` and ``forward``
@@ -314,34 +356,61 @@ class DSAIndexer(torch.nn.Module):
     def forward_before_topk(self, x: Tensor, qr: Tensor, packed_seq_params=None):
         """``(q [S,B,Hi,Di], k [S,B,Di], weights [S,B,Hi])`` (with fp8: ``(q, q_scale, k, k_scale,
         weights)``); ``packed_seq_params`` is the caller's ``(psp, rotary_pos_emb)`` tuple
-        (multi_latent_attention.py:260-261)."""
-        psp, rotary_pos_emb = packed_seq_params
-        assert psp is None, "Packed sequence is not supported for DSAttention"   # patcher.py:256
-        if self.fp8:
-            with torch.no_grad():
+        (multi_latent_attention.py:260-261).  Packed THD input gives the token-major layout."""
+        psp, rotary_pos_emb = _split_packed(packed_seq_params)
+        docs = _thd_docs(psp)
+        assert psp is None or docs is not None, "only THD packing is supported"
+        with torch.set_grad_enabled(torch.is_grad_enabled() and not self.fp8):
+            if docs is None:
                 return self._before_topk(x, qr, rotary_pos_emb)
-        return self._before_topk(x, qr, rotary_pos_emb)
+            cu, _ = docs
+            T = x.shape[0]
+            _, row_len = ops.build_rows(cu, T, True)      # causal row length = position in document + 1
+            out = self._before_topk(x.reshape(T, 1, -1), qr.reshape(T, 1, -1), rotary_pos_emb,
+                                    positions=row_len.to(torch.int64) - 1)
+            return tuple(o.reshape(T, *o.shape[2:]) for o in out)
 
-    def _before_topk(self, x: Tensor, qr: Tensor, rotary_pos_emb: Tensor):
+    def _before_topk(self, x: Tensor, qr: Tensor, rotary_pos_emb: Tensor, positions: Optional[Tensor] = None):
         return indexer_forward_before_topk(
             x, qr, self.linear_wq_b.weight, self.linear_wk.weight, self.k_norm.weight, self.k_norm.bias,
             self.linear_weights_proj.weight, rotary_pos_emb, index_n_heads=self.index_n_heads, eps=self.eps,
             mscale=self.mscale, dsa_indexer_rotary_interleaved=self.dsa_indexer_rotary_interleaved,
-            rotary_interleaved=self.rotary_interleaved, fp8=self.fp8)
+            rotary_interleaved=self.rotary_interleaved, fp8=self.fp8, positions=positions)
+
+    def topk_from_outputs(self, out, mask: Optional[Tensor] = None, docs=None, causal: Optional[bool] = None,
+                          return_scores: bool = True):
+        """Scores and top-k from ``forward_before_topk``'s outputs (sbhd, or THD when ``docs`` =
+        ``(cu_seqlens, max_seqlen)``)."""
+        if self.fp8:
+            q, qs, k, ks, w = out
+        else:
+            (q, k, w), qs, ks = out, None, None
+        if docs is None:
+            return fused_qk_topk_naive(q.detach(), k.detach(), w.detach(), self.index_topk, mask, causal=causal,
+                                       return_scores=return_scores, q_scale=qs, k_scale=ks)
+        cu, max_s = docs
+        res = ops.indexer_topk(q.detach(), k.detach(), w.detach(), self.index_topk, cu, True, max_s, qs, ks,
+                               return_scores=return_scores)
+        idx, sc = res if return_scores else (res, None)
+        return sc, idx.to(torch.int64)
 
     @torch.no_grad()
     def forward_with_scores(self, x: Tensor, qr: Tensor, mask: Optional[Tensor] = None, packed_seq_params=None):
-        """``(index_scores [B,S,S] fp32, topk_indices [B,S,index_topk] int64)`` (patcher.py:326-360)."""
+        """``(index_scores [B,S,S] fp32, topk_indices [B,S,index_topk] int64)`` (patcher.py:326-360);
+        THD input: ``(index_scores [T, max_seqlen], topk_indices [T, index_topk])`` (the mask is the
+        causal one of each document)."""
+        psp, _ = _split_packed(packed_seq_params)
+        docs = _thd_docs(psp)
         out = self.forward_before_topk(x, qr, packed_seq_params)
-        if self.fp8:
-            q, qs, k, ks, w = out
-            return fused_qk_topk_naive(q, k, w, self.index_topk, mask, q_scale=qs, k_scale=ks)
-        q, k, w = out
-        return fused_qk_topk_naive(q, k, w, self.index_topk, mask)
+        return self.topk_from_outputs(out, mask, docs)
 
     def forward(self, x: Tensor, qr: Tensor, mask: Optional[Tensor] = None, packed_seq_params=None) -> Tensor:
-        """``topk_indices [B, S, index_topk]`` (patcher.py:362-378)."""
-        return self.forward_with_scores(x, qr, mask, packed_seq_params)[1]
+        """``topk_indices [B, S, index_topk]`` (patcher.py:362-378), ``[T, index_topk]`` for THD."""
+        psp, _ = _split_packed(packed_seq_params)
+        docs = _thd_docs(psp)
+        with torch.no_grad():
+            out = self.forward_before_topk(x, qr, packed_seq_params)
+            return self.topk_from_outputs(out, mask, docs, return_scores=False)[1]
 
 
 class DSAttention(torch.nn.Module):
@@ -360,7 +429,13 @@ class DSAttention(torch.nn.Module):
     - sparse attention over the selected keys, with the causal mask on top;
     - in training with ``loss_coeff > 0``, the sparse indexer KL loss, applied in the attention's
       backward. Its value is in ``last_indexer_loss`` after the backward pass.
-    Returns ``[S, B, H * 512]``.  The dense (non-sparse) indexer loss is not built."""
+    Returns ``[S, B, H * 512]``.  Packed THD input (``psp.qkv_format == 'thd'``: ``query [T, H, 576]``,
+    ``key [T, 576]``, ``x [T, 1, hidden]``, ``qr [T, q_lora_rank]``) attends within each document
+    and returns ``[T, H * 512]``, the un-packed caller's THD output (multi_latent_attention.py:272-281).
+
+    The attention is causal by construction, as DSA's is: ``attention_mask`` is not read (so it
+    is never inspected on the host), and ``attn_mask_type``, when given, must be a causal kind.
+    The dense (non-sparse) indexer loss is not built."""
 
     def __init__(self, indexer: DSAIndexer, softmax_scale: float, loss_coeff: float = 0.0,
                  use_sparse_loss: bool = True):
@@ -375,32 +450,39 @@ class DSAttention(torch.nn.Module):
                 x: Tensor, qr: Tensor, attn_mask_type=None, attention_bias=None, packed_seq_params=None) -> Tensor:
         assert value is None, "absorbed layout: V is key[..., :512]"
         assert attention_bias is None, "DSA takes no attention bias"
-        assert attention_mask is None or _is_causal_mask(attention_mask), "DSA attention is causal"
-        S, B, H, D = query.shape
+        assert _mask_type_is_causal(attn_mask_type), "DSA attention is causal"
+        psp, _ = _split_packed(packed_seq_params)
+        docs = _thd_docs(psp)
         train_loss = self.training and self.loss_coeff > 0 and torch.is_grad_enabled()
         if train_loss and (not self.use_sparse_loss or self.indexer.fp8):
             raise NotImplementedError("only the sparse indexer loss with the bf16 indexer is built")
         with torch.set_grad_enabled(train_loss):
             out = self.indexer.forward_before_topk(x, qr, packed_seq_params)
-        if self.indexer.fp8:
-            q_i, qs, k_i, ks, w = out
-            _, topk = fused_qk_topk_naive(q_i, k_i, w, self.indexer.index_topk, causal=True, return_scores=False,
-                                          q_scale=qs, k_scale=ks)
+        _, topk = self.indexer.topk_from_outputs(out, None, docs, causal=True, return_scores=False)
+        if docs is not None:
+            # packed THD: global token ids already, one query row per token
+            T, H, D = query.shape
+            q_thd, kv_thd = query, key.reshape(T, D)
+            idx = topk.to(torch.int32)
         else:
-            q_i, k_i, w = out
-            _, topk = fused_qk_topk_naive(q_i.detach(), k_i.detach(), w.detach(), self.indexer.index_topk,
-                                          causal=True, return_scores=False)
+            S, B, H, D = query.shape
+            if not train_loss:
+                return sparse_mla_attention(query, key, topk, self.softmax_scale, causal=True)
+            # packed THD with global key ids (batch b's keys are rows b*S ..)
+            q_thd = query.transpose(0, 1).reshape(B * S, H, D)
+            kv_thd = key.transpose(0, 1).reshape(B * S, D)
+            off = (torch.arange(B, device=query.device, dtype=torch.int64) * S).view(B, 1, 1)
+            idx = torch.where(topk >= 0, topk + off, torch.full_like(topk, -1)).reshape(B * S, -1).to(torch.int32)
         if not train_loss:
-            return sparse_mla_attention(query, key, topk, self.softmax_scale, causal=True)
-        # packed THD with global key ids (batch b's keys are rows b*S ..)
-        q_thd = query.transpose(0, 1).reshape(B * S, H, D)
-        kv_thd = key.transpose(0, 1).reshape(B * S, D)
-        off = (torch.arange(B, device=query.device, dtype=torch.int64) * S).view(B, 1, 1)
-        idx = torch.where(topk >= 0, topk + off, torch.full_like(topk, -1)).reshape(B * S, -1).to(torch.int32)
-        Hi = q_i.shape[2]
-        o, loss = sparse_mla_with_indexer_loss(q_thd, kv_thd, idx, q_i.transpose(0, 1).reshape(B * S, Hi, -1),
-                                               k_i.transpose(0, 1).reshape(B * S, -1),
-                                               w.transpose(0, 1).reshape(B * S, Hi), self.softmax_scale,
-                                               self.loss_coeff, True)
+            return ops.sparse_mla(q_thd.contiguous(), kv_thd.contiguous(), idx, self.softmax_scale, True).reshape(T, -1)
+        q_i, k_i, w = out
+        Hi = q_i.shape[-2]
+        if docs is None:
+            q_i, k_i, w = (q_i.transpose(0, 1).reshape(B * S, Hi, -1), k_i.transpose(0, 1).reshape(B * S, -1),
+                           w.transpose(0, 1).reshape(B * S, Hi))
+        o, loss = sparse_mla_with_indexer_loss(q_thd.contiguous(), kv_thd.contiguous(), idx, q_i, k_i, w,
+                                               self.softmax_scale, self.loss_coeff, True)
         self.last_indexer_loss = loss
+        if docs is not None:
+            return o.reshape(T, H * ops.D_V)
         return o.reshape(B, S, H * ops.D_V).transpose(0, 1)

@@ -460,3 +460,91 @@ def test_kl_path_tiny_shapes(T, K):
     rq, rk, rw = O.indexer_scores_bwd(qi, ki, w, idx, dI)
     for name, a, b in (("dq", dq, rq), ("dw", dw, rw), ("dk", dk, rk)):
         torch.testing.assert_close(a.cpu().double(), b, rtol=2e-2, atol=2e-3, msg=lambda m: f"{name}: {m}")
+
+
+def test_dsattention_thd_packed_equals_per_document():
+    """Packed THD through the module mirrors (PackedSeqParams with cu_seqlens_q, as the MLA caller
+    packs it, multi_latent_attention.py:90-96): the indexer's outputs, the top-k, the attention
+    output and its gradients equal the per-document unpacked calls, and in training the indexer's
+    parameter gradients are the token-weighted sum of the per-document ones (the loss is a mean
+    over all packed tokens)."""
+    import types
+    from mcore_bridge_amd.dsa import DSAIndexer, DSAttention
+    print("[DSAttention THD packed vs per document]", flush=True)
+    g = torch.Generator().manual_seed(77)
+    lens = [50, 130, 77]
+    cu_l = [0] + [sum(lens[:i + 1]) for i in range(len(lens))]
+    T, H, hidden, qlr, Hi, K = cu_l[-1], 16, 256, 192, 64, 40
+    indexer = DSAIndexer(hidden, qlr, index_n_heads=Hi, index_topk=K, device=DEV)
+    with torch.no_grad():
+        for p_ in indexer.parameters():
+            p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(p_.dtype))
+        indexer.k_norm.weight.add_(1.0)
+    coeff, sc = 0.5, W.SM_SCALE
+    attn = DSAttention(indexer, sc, loss_coeff=coeff)
+    query = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    key = (torch.randn(T, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    x = torch.randn(T, 1, hidden, generator=g).bfloat16().to(DEV)
+    qr = torch.randn(T, qlr, generator=g).bfloat16().to(DEV)
+    rope = (torch.rand(max(lens), 1, 1, 64, generator=g) * 200).to(DEV)
+    psp = types.SimpleNamespace(qkv_format="thd", cu_seqlens_q=torch.tensor(cu_l, dtype=torch.int32, device=DEV),
+                                max_seqlen_q=max(lens))
+    dout = (torch.randn(T, H * 512, generator=g) * 0.01).to(DEV)
+
+    def per_doc(train):
+        outs, qg, kg, grads = [], [], [], {n: 0 for n, _ in indexer.named_parameters()}
+        for d, (a, b) in enumerate(zip(cu_l[:-1], cu_l[1:])):
+            S = b - a
+            qd = query[a:b].unsqueeze(1).clone().requires_grad_(train)
+            kd = key[a:b].unsqueeze(1).clone().requires_grad_(train)
+            indexer.zero_grad(set_to_none=True)
+            with torch.set_grad_enabled(train):
+                o = attn(qd, kd, None, None, x[a:b], qr[a:b].unsqueeze(1), packed_seq_params=(None, rope[:S]))
+            outs.append(o.detach()[:, 0])
+            if train:
+                (o[:, 0].float() * dout[a:b]).sum().backward()
+                qg.append(qd.grad[:, 0])
+                kg.append(kd.grad[:, 0])
+                for n, p_ in indexer.named_parameters():
+                    grads[n] = grads[n] + p_.grad.float() * (S / T)
+        return torch.cat(outs), (torch.cat(qg) if train else None), (torch.cat(kg) if train else None), grads
+
+    # indexer outputs and top-k (the projections are library GEMMs over T vs per-document rows, so
+    # they may round differently: outputs within bf16 rounding, selections >= 99 % equal)
+    with torch.no_grad():
+        q_p, k_p, w_p = indexer.forward_before_topk(x, qr, (psp, rope))
+        idx_p = indexer(x, qr, None, (psp, rope))
+        inter = tot = 0
+        for a, b in zip(cu_l[:-1], cu_l[1:]):
+            q_d, k_d, w_d = indexer.forward_before_topk(x[a:b], qr[a:b].unsqueeze(1), (None, rope[:b - a]))
+            _close(q_p[a:b].cpu(), q_d[:, 0].cpu(), rel=1e-2, name="q_idx")
+            _close(k_p[a:b].cpu(), k_d[:, 0].cpu(), rel=1e-2, name="k_idx")
+            _close(w_p[a:b].cpu(), w_d[:, 0].cpu(), rel=1e-2, name="w")
+            i_d = indexer(x[a:b], qr[a:b].unsqueeze(1), None, (None, rope[:b - a]))[0]   # [S, K] local, score order
+            for t in range(b - a):
+                want = set((i_d[t][i_d[t] <= t] + a).tolist())
+                got = set(idx_p[a + t][idx_p[a + t] >= 0].tolist())
+                assert all(a <= j <= a + t for j in got), (a, t)        # own document, causal
+                inter += len(want & got)
+                tot += len(want)
+        assert inter / tot >= 0.99, inter / tot
+    # eval
+    attn.eval()
+    with torch.no_grad():
+        out_p = attn(query, key, None, None, x, qr, packed_seq_params=(psp, rope))
+    out_d, _, _, _ = per_doc(False)
+    assert out_p.shape == (T, H * 512)
+    _close(out_p.cpu(), out_d.cpu(), rel=1e-2, name="out packed vs per document")
+    # training with the sparse indexer loss applied in the backward
+    attn.train()
+    qa, ka = query.clone().requires_grad_(), key.clone().requires_grad_()
+    indexer.zero_grad(set_to_none=True)
+    out_t = attn(qa, ka, None, None, x, qr, packed_seq_params=(psp, rope))
+    (out_t.float() * dout).sum().backward()
+    grads_p = {n: p_.grad.float().clone() for n, p_ in indexer.named_parameters()}
+    out_dt, qg, kg, grads_d = per_doc(True)
+    _close(out_t.detach().cpu(), out_dt.cpu(), rel=1e-2, name="train out")
+    _close(qa.grad.cpu(), qg.cpu(), rel=1e-2, name="dq packed vs per document")
+    _close(ka.grad.cpu(), kg.cpu(), rel=1e-2, name="dkv packed vs per document")
+    for n in grads_p:
+        _close(grads_p[n].cpu(), grads_d[n].cpu(), rel=2e-2, name=f"indexer {n}")

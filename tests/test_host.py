@@ -1,5 +1,5 @@
 """CPU tests of the host-side logic: the Megatron plug-in point, workload constants, and the
-causal-mask detection used by the fused_qk_topk_naive drop-in."""
+mask-type / packing helpers of the Megatron-shaped drop-ins."""
 import sys
 import types
 
@@ -38,14 +38,22 @@ def test_patch_install_without_megatron_is_a_no_op():
         assert patch.install() is False
 
 
-def test_causal_mask_detection():
-    S = 9
-    m = torch.triu(torch.full((S, S), float("-inf")), 1)[None].expand(2, S, S)
-    assert dsa._is_causal_mask(m)
-    m2 = m.clone()
-    m2[1, 3, 5] = 0.0
-    assert not dsa._is_causal_mask(m2)
-    assert not dsa._is_causal_mask(torch.zeros(1, S, S))
+def test_mask_type_and_packing_helpers():
+    # DSA attention is causal by construction: no mask is inspected on the host, an explicit
+    # Megatron AttnMaskType must be a causal kind; THD PackedSeqParams give (cu_seqlens, max_seqlen)
+    class MaskType:
+        def __init__(self, name):
+            self.name = name
+    assert dsa._mask_type_is_causal(None)
+    assert dsa._mask_type_is_causal(MaskType("causal")) and dsa._mask_type_is_causal(MaskType("padding_causal"))
+    assert not dsa._mask_type_is_causal(MaskType("no_mask"))
+    psp = types.SimpleNamespace(qkv_format="thd", cu_seqlens_q=torch.tensor([0, 3, 7]), max_seqlen_q=4)
+    cu, ms = dsa._thd_docs(psp)
+    assert cu.dtype == torch.int32 and cu.tolist() == [0, 3, 7] and ms == 4
+    assert dsa._thd_docs(None) is None
+    assert dsa._thd_docs(types.SimpleNamespace(qkv_format="sbhd", cu_seqlens_q=None)) is None
+    assert dsa._split_packed((psp, "rope")) == (psp, "rope")
+    assert dsa._split_packed(None) == (None, None)
 
 
 def test_config_shapes():
@@ -75,12 +83,14 @@ def test_dsa_indexer_parameters_are_the_bridge_keys():
     assert torch.equal(ix.linear_wk.weight, sd["linear_wk.weight"])
 
 
-def test_dsa_indexer_rejects_packed_sequences_like_the_reference():
-    # patcher.py:255-256: packed_seq_params arrives as (psp, rotary_pos_emb) and psp must be None
+def test_dsa_indexer_rejects_non_thd_packing():
+    # the reference rejects every PackedSeqParams (patcher.py:256); the mirror accepts THD packing
+    # (tested on the GPU) and rejects any other packed format before touching a kernel
     ix = dsa.DSAIndexer(hidden_size=64, q_lora_rank=32, index_n_heads=4, index_topk=8, device="cpu")
+    psp = types.SimpleNamespace(qkv_format="sbhd", cu_seqlens_q=None)
     try:
-        ix.forward_before_topk(torch.zeros(4, 1, 64), torch.zeros(4, 1, 32), (object(), torch.zeros(4, 1, 1, 64)))
+        ix.forward_before_topk(torch.zeros(4, 1, 64), torch.zeros(4, 1, 32), (psp, torch.zeros(4, 1, 1, 64)))
     except AssertionError as e:
-        assert "Packed sequence" in str(e)
+        assert "THD" in str(e)
     else:
-        raise AssertionError("packed sequences must be rejected")
+        raise AssertionError("non-THD packing must be rejected")
