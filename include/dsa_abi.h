@@ -54,7 +54,8 @@ typedef enum {
   DSA_ERR_UNSUPPORTED = -2,   /* valid request this build does not implement (e.g. d_qk != 576) */
   DSA_ERR_WORKSPACE = -3,     /* workspace missing or smaller than *_workspace_size() */
   DSA_ERR_LAUNCH = -4,        /* a kernel launch failed (HIP error) */
-  DSA_ERR_DEVICE = -5         /* no usable gfx950 device */
+  DSA_ERR_DEVICE = -5,        /* no usable gfx950 device */
+  DSA_ERR_SCRATCH = -6        /* request exceeds the static scratch of an allocation-free entry point */
 } dsa_status;
 
 typedef enum { DSA_BF16 = 0, DSA_FP8_E4M3 = 1 } dsa_dtype;
@@ -168,6 +169,21 @@ size_t dsa_sparse_mla_decode_workspace_size(int batch, int n_heads, int topk);
 int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
                           int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
                           void* workspace, size_t workspace_bytes, void* stream);
+/* Allocation-free form of dsa_sparse_mla_decode.  No counterpart in the reference: it exists for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments minus the workspace, same kernels, split and
+ * results; the split partials live in a static device array of the library,
+ * dsa_sparse_mla_decode_scratch_bytes() = 64 MiB per GPU the library runs on, held until the
+ * process ends.  Requests whose partials exceed it (dsa_sparse_mla_decode_workspace_size() > 64 MiB)
+ * return DSA_ERR_SCRATCH; under this build's split rule the partials never exceed 65,280 rows
+ * (67,107,840 bytes), so every request fits.  Calls neither allocate
+ * nor free memory.  All calls on one GPU share its scratch: calls that overlap in time on one GPU
+ * (different streams, or host threads without ordering) race on it. */
+size_t dsa_sparse_mla_decode_scratch_bytes(void);
+int dsa_sparse_mla_decode_noalloc(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
+                                  int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
+                                  void* stream);
+
 /* Workspace bytes for dsa_sparse_mla_bwd. */
 size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk);
 

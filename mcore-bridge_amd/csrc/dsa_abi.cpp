@@ -91,6 +91,9 @@ const char* dsa_strerror(int status) {
     case DSA_ERR_WORKSPACE: return "workspace missing or too small";
     case DSA_ERR_LAUNCH: return "kernel launch failed";
     case DSA_ERR_DEVICE: return "no usable gfx950 device";
+    case DSA_ERR_SCRATCH:
+      return "request needs more than the static scratch of the allocation-free entry point "
+             "(dsa_sparse_mla_decode_scratch_bytes); use the workspace form";
     default: return "unknown dsa status";
   }
 }
@@ -296,6 +299,28 @@ int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* id
   if (rc != 0) return rc;
   return dsa::launch_decode_combine(part_o, part_lse, batch, n_heads, d.n_split, static_cast<dsa::bf16_t*>(out),
                                     lse, as_stream(stream));
+}
+
+size_t dsa_sparse_mla_decode_scratch_bytes(void) { return dsa::kDecodeScratchBytes; }
+
+int dsa_sparse_mla_decode_noalloc(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
+                                  int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
+                                  void* stream) {
+  if (batch < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
+    return DSA_ERR_INVALID_ARG;
+  if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
+  if (batch == 0) return DSA_OK;
+  const size_t need = decode_workspace(batch, n_heads, topk);
+  if (need > dsa::kDecodeScratchBytes) return DSA_ERR_SCRATCH;
+  void* scratch = nullptr;
+  if (need > 0) {
+    const int rc = dsa::decode_scratch_address(&scratch);
+    if (rc != 0) return rc == -5 ? DSA_ERR_DEVICE : DSA_ERR_LAUNCH;
+  }
+  // the same kernels and split as dsa_sparse_mla_decode, with the partials in the static scratch
+  // (every split writes all of its rows, so nothing needs clearing between calls)
+  return dsa_sparse_mla_decode(q, kv_cache, idx, batch, n_kv, n_heads, d_qk, d_v, topk, sm_scale, out, lse,
+                               scratch, need > 0 ? dsa::kDecodeScratchBytes : 0, stream);
 }
 
 size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk) {

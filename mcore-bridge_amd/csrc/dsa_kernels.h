@@ -182,6 +182,11 @@ void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int to
                      int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
                           bf16_t* out, float* lse, hipStream_t stream);
+// Static per-device scratch of the allocation-free decode entry point (64 MiB): device address of
+// the current device's copy, looked up with hipGetSymbolAddress on the first call per device.
+// 0 on success, -5 no usable device, -4 lookup failed.
+constexpr size_t kDecodeScratchBytes = size_t(64) << 20;
+int decode_scratch_address(void** out);
 int launch_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,
                              hipStream_t stream);
 int launch_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,

@@ -29,6 +29,8 @@
 //     headroom is recomputed once with its exact row max.  Row sums and overshoot maxima stay
 //     per lane (one half of a head's keys) until the end of the pass: no cross-lane traffic
 //     per block.
+#include <mutex>
+
 #include "dsa_common.h"
 #include "dsa_kernels.h"
 #include "dsa_kvtile.h"
@@ -414,6 +416,30 @@ int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
   else
     hipLaunchKernelGGL(sparse_mla_fwd_kernel<1>, grid, dim3(64), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// Static device scratch of the allocation-free decode entry point: the split partials live here
+// instead of in a caller workspace.  Every GPU the library runs on holds its own copy until the
+// process ends; in host code `decode_scratch` names a host-side stand-in, so kernels get the
+// device address that hipGetSymbolAddress returns, looked up once per device.
+namespace {
+__device__ __align__(256) char decode_scratch[kDecodeScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int decode_scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -5;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(decode_scratch)) != hipSuccess || !ptr) return -4;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
 }
 
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,

@@ -22,6 +22,7 @@ DSA_ERR_UNSUPPORTED = -2
 DSA_ERR_WORKSPACE = -3
 DSA_ERR_LAUNCH = -4
 DSA_ERR_DEVICE = -5
+DSA_ERR_SCRATCH = -6
 
 DSA_BF16 = 0
 DSA_FP8_E4M3 = 1
@@ -52,6 +53,9 @@ SIGNATURES = {
     "dsa_sparse_mla_decode_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "dsa_sparse_mla_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                       c_float, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "dsa_sparse_mla_decode_scratch_bytes": (c_size_t, []),
+    "dsa_sparse_mla_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                              c_int, c_float, c_void_p, c_void_p, c_void_p]),
     "dsa_sparse_mla_bwd_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_void_p,
