@@ -289,7 +289,7 @@ class _HeadwiseMatmul(torch.autograd.Function):
 
 def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compressed: Tensor, k_pos_emb: Tensor,
                                   kv_up_proj_weight: Tensor, topk_indices: Tensor, softmax_scale: float,
-                                  causal: bool = True) -> Tensor:
+                                  causal: bool = True, indexer_loss=None):
     """Megatron's DSA core attention (called at reference multi_latent_attention.py:262-270) on
     the MLA's un-absorbed inputs, computed in the absorbed latent space.
 
@@ -299,7 +299,11 @@ def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compres
     of ``W_UK`` then ``dv`` rows of ``W_UV``, ``:121-128``); ``topk_indices [B, S, K]``.  Returns
     ``[S, B, H * dv]`` -- what the un-fused attention returns for ``query = [q_no_pe, q_pos_emb]``,
     ``key_h = [kv_compressed W_UK_h^T, k_pos_emb]``, ``value_h = kv_compressed W_UV_h^T`` -- and is
-    differentiable w.r.t. every tensor input (the weight included)."""
+    differentiable w.r.t. every tensor input (the weight included).
+
+    ``indexer_loss = (q_idx, k_idx, w, loss_coeff, loss_scale)`` (the indexer's bf16 outputs,
+    ``[S, B, Hi, 128]``, ``[S, B, 128]``, ``[S, B, Hi]``) also applies the sparse indexer KL loss in
+    the attention's backward (``sparse_mla_with_indexer_loss``); the call then returns ``(out, loss)``."""
     S, B, H, dn = q_no_pe.shape
     dc = kv_compressed.shape[-1]
     assert dc + q_pos_emb.shape[-1] == ops.D_QK and dc == ops.D_V, "latent 512 + rope 64"
@@ -311,47 +315,33 @@ def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compres
     q_lat = _HeadwiseMatmul.apply(qn, w_uk)                            # [H, S*B, dc]
     query = torch.cat([q_lat.view(H, S, B, dc).permute(1, 2, 0, 3), q_pos_emb], dim=-1)
     kv = torch.cat([kv_compressed, k_pos_emb.reshape(S, B, -1)], dim=-1)
-    o_lat = sparse_mla_attention(query.contiguous(), kv.contiguous(), topk_indices, softmax_scale, ops.D_V, causal)
+    loss = None
+    if indexer_loss is None:
+        o_lat = sparse_mla_attention(query.contiguous(), kv.contiguous(), topk_indices, softmax_scale, ops.D_V,
+                                     causal)
+    else:
+        q_i, k_i, w_i, coeff, loss_scale = indexer_loss
+        Hi = q_i.shape[-2]
+        off = (torch.arange(B, device=query.device, dtype=torch.int64) * S).view(B, 1, 1)
+        ti = topk_indices.to(torch.int64)
+        idx = torch.where(ti >= 0, ti + off, torch.full_like(ti, -1)).reshape(B * S, -1).to(torch.int32)
+        o_thd, loss = sparse_mla_with_indexer_loss(
+            query.transpose(0, 1).reshape(B * S, H, ops.D_QK).contiguous(),
+            kv.transpose(0, 1).reshape(B * S, ops.D_QK).contiguous(), idx,
+            q_i.transpose(0, 1).reshape(B * S, Hi, -1), k_i.transpose(0, 1).reshape(B * S, -1),
+            w_i.transpose(0, 1).reshape(B * S, Hi), softmax_scale, coeff, causal, loss_scale)
+        o_lat = o_thd.reshape(B, S, H * ops.D_V).transpose(0, 1)
     o = o_lat.reshape(S, B, H, dc).permute(2, 0, 1, 3).reshape(H, S * B, dc)
     out = _HeadwiseMatmul.apply(o, w_uv_t)                             # [H, S*B, dv]
-    return out.view(H, S, B, dv).permute(1, 2, 0, 3).reshape(S, B, H * dv)
+    out = out.view(H, S, B, dv).permute(1, 2, 0, 3).reshape(S, B, H * dv)
+    return out if indexer_loss is None else (out, loss)
 
 
-class DSAIndexer(torch.nn.Module):
-    """Host mirror of the reference's patched ``DSAIndexer`` (src/mcore_bridge/patcher.py:243-380)
-    over the HIP kernels: same method names, arguments and returns, and Megatron's parameter names
-    (``linear_wq_b``, ``linear_wk``, ``k_norm``, ``linear_weights_proj``), so the indexer keys the
-    reference's bridge maps (``wq_b``, ``wk``, ``k_norm.{weight,bias}``, ``weights_proj``,
-    gpt_bridge.py:1292-1306) load one to one.
-
-    Packing: the reference asserts that no ``PackedSeqParams`` is given (patcher.py:256).  This
-    mirror also accepts packed THD input (``psp.qkv_format == 'thd'`` with ``cu_seqlens_q``, as the
-    MLA caller packs it, multi_latent_attention.py:90-96): ``x [T, 1, hidden]``, ``qr [T, q_lora_rank]``
-    (or ``[T, 1, ...]``), RoPE angles restarting at each document, indices restricted to the query's
-    own document.  THD outputs are token-major: ``q [T, Hi, 128]``, ``k [T, 128]``, ``w [T, Hi]``,
-    ``topk_indices [T, K]`` global token ids (ascending, ``-1`` pad) and ``index_scores [T, max_seqlen]``
-    (column j = key ``doc_start + j``, ``-inf`` past the causal row).
-
-    ``forward_before_topk`` is differentiable in the bf16 layout (the prologue's backward kernel,
-    then the projections' GEMM backward), which is what training the indexer with the sparse KL
-    loss needs: pass its outputs to ``indexer_kl_loss``.  ``forward_with_scores`` and ``forward``
-    return scores and indices, which carry no gradient (the reference's dense, non-sparse loss
-    differentiates all index scores; that variant is not built)."""
-
-    def __init__(self, hidden_size: int, q_lora_rank: int, index_n_heads: int = 64, index_head_dim: int = 128,
-                 index_topk: int = 2048, qk_pos_emb_head_dim: int = 64, layernorm_epsilon: float = 1e-6,
-                 attention_scaling: float = 1.0, dsa_indexer_rotary_interleaved: bool = False,
-                 rotary_interleaved: bool = False, fp8: bool = False, device=None, dtype=torch.bfloat16):
-        super().__init__()
-        assert index_head_dim == 128 and qk_pos_emb_head_dim == 64, "index_head_dim 128, rope 64 (DSv3.2)"
-        kw = dict(device=device, dtype=dtype)
-        self.index_n_heads, self.index_head_dim, self.index_topk = index_n_heads, index_head_dim, index_topk
-        self.eps, self.mscale, self.fp8 = layernorm_epsilon, attention_scaling, fp8
-        self.dsa_indexer_rotary_interleaved, self.rotary_interleaved = dsa_indexer_rotary_interleaved, rotary_interleaved
-        self.linear_wq_b = torch.nn.Linear(q_lora_rank, index_n_heads * index_head_dim, bias=False, **kw)
-        self.linear_wk = torch.nn.Linear(hidden_size, index_head_dim, bias=False, **kw)
-        self.k_norm = torch.nn.LayerNorm(index_head_dim, eps=layernorm_epsilon, **kw)
-        self.linear_weights_proj = torch.nn.Linear(hidden_size, index_n_heads, bias=False, **kw)
+class _IndexerComputation:
+    """The indexer's kernel path over parameters named like Megatron's DSAIndexer: ``linear_wq_b``,
+    ``linear_wk``, ``k_norm`` (LayerNorm with bias), ``linear_weights_proj`` (modules with a
+    ``.weight``), plus ``index_n_heads``, ``index_topk``, ``eps``, ``mscale``, the two RoPE flags and
+    ``fp8``.  Shared by the ``DSAIndexer`` mirror and ``IndexerView`` (an installed Megatron indexer)."""
 
     def forward_before_topk(self, x: Tensor, qr: Tensor, packed_seq_params=None):
         """``(q [S,B,Hi,Di], k [S,B,Di], weights [S,B,Hi])`` (with fp8: ``(q, q_scale, k, k_scale,
@@ -393,6 +383,70 @@ class DSAIndexer(torch.nn.Module):
                                return_scores=return_scores)
         idx, sc = res if return_scores else (res, None)
         return sc, idx.to(torch.int64)
+
+
+
+class IndexerView(_IndexerComputation):
+    """The kernel path over the parameters of an existing indexer module (Megatron's DSAIndexer, or
+    any module with its parameter names): shares the module's parameters, copies nothing.  The
+    hyper-parameters come from the module where it holds them and from the transformer config
+    otherwise (``dsa_indexer_topk``, ``layernorm_epsilon``, ``attention_scaling``,
+    ``dsa_indexer_rotary_interleaved``, ``rotary_interleaved``; reference model_config.py:199-206)."""
+
+    def __init__(self, module, config=None, fp8: bool = False):
+        def pick(name, cfg_name, default):
+            v = getattr(module, name, None)
+            if v is None and config is not None:
+                v = getattr(config, cfg_name, None)
+            return default if v is None else v
+        self.linear_wq_b, self.linear_wk = module.linear_wq_b, module.linear_wk
+        self.k_norm, self.linear_weights_proj = module.k_norm, module.linear_weights_proj
+        self.index_n_heads = pick("index_n_heads", "dsa_indexer_n_heads", None)
+        self.index_topk = pick("index_topk", "dsa_indexer_topk", None)
+        assert self.index_n_heads is not None and self.index_topk is not None, "indexer heads / top-k unknown"
+        self.eps = getattr(module.k_norm, "eps", None) or pick("eps", "layernorm_epsilon", 1e-6)
+        self.mscale = pick("mscale", "attention_scaling", 1.0)
+        self.dsa_indexer_rotary_interleaved = bool(pick("dsa_indexer_rotary_interleaved",
+                                                        "dsa_indexer_rotary_interleaved", False))
+        self.rotary_interleaved = bool(pick("rotary_interleaved", "rotary_interleaved", False))
+        self.fp8 = fp8
+
+
+class DSAIndexer(_IndexerComputation, torch.nn.Module):
+    """Host mirror of the reference's patched ``DSAIndexer`` (src/mcore_bridge/patcher.py:243-380)
+    over the HIP kernels: same method names, arguments and returns, and Megatron's parameter names
+    (``linear_wq_b``, ``linear_wk``, ``k_norm``, ``linear_weights_proj``), so the indexer keys the
+    reference's bridge maps (``wq_b``, ``wk``, ``k_norm.{weight,bias}``, ``weights_proj``,
+    gpt_bridge.py:1292-1306) load one to one.
+
+    Packing: the reference asserts that no ``PackedSeqParams`` is given (patcher.py:256).  This
+    mirror also accepts packed THD input (``psp.qkv_format == 'thd'`` with ``cu_seqlens_q``, as the
+    MLA caller packs it, multi_latent_attention.py:90-96): ``x [T, 1, hidden]``, ``qr [T, q_lora_rank]``
+    (or ``[T, 1, ...]``), RoPE angles restarting at each document, indices restricted to the query's
+    own document.  THD outputs are token-major: ``q [T, Hi, 128]``, ``k [T, 128]``, ``w [T, Hi]``,
+    ``topk_indices [T, K]`` global token ids (ascending, ``-1`` pad) and ``index_scores [T, max_seqlen]``
+    (column j = key ``doc_start + j``, ``-inf`` past the causal row).
+
+    ``forward_before_topk`` is differentiable in the bf16 layout (the prologue's backward kernel,
+    then the projections' GEMM backward), which is what training the indexer with the sparse KL
+    loss needs: pass its outputs to ``indexer_kl_loss``.  ``forward_with_scores`` and ``forward``
+    return scores and indices, which carry no gradient (the reference's dense, non-sparse loss
+    differentiates all index scores; that variant is not built)."""
+
+    def __init__(self, hidden_size: int, q_lora_rank: int, index_n_heads: int = 64, index_head_dim: int = 128,
+                 index_topk: int = 2048, qk_pos_emb_head_dim: int = 64, layernorm_epsilon: float = 1e-6,
+                 attention_scaling: float = 1.0, dsa_indexer_rotary_interleaved: bool = False,
+                 rotary_interleaved: bool = False, fp8: bool = False, device=None, dtype=torch.bfloat16):
+        super().__init__()
+        assert index_head_dim == 128 and qk_pos_emb_head_dim == 64, "index_head_dim 128, rope 64 (DSv3.2)"
+        kw = dict(device=device, dtype=dtype)
+        self.index_n_heads, self.index_head_dim, self.index_topk = index_n_heads, index_head_dim, index_topk
+        self.eps, self.mscale, self.fp8 = layernorm_epsilon, attention_scaling, fp8
+        self.dsa_indexer_rotary_interleaved, self.rotary_interleaved = dsa_indexer_rotary_interleaved, rotary_interleaved
+        self.linear_wq_b = torch.nn.Linear(q_lora_rank, index_n_heads * index_head_dim, bias=False, **kw)
+        self.linear_wk = torch.nn.Linear(hidden_size, index_head_dim, bias=False, **kw)
+        self.k_norm = torch.nn.LayerNorm(index_head_dim, eps=layernorm_epsilon, **kw)
+        self.linear_weights_proj = torch.nn.Linear(hidden_size, index_n_heads, bias=False, **kw)
 
     @torch.no_grad()
     def forward_with_scores(self, x: Tensor, qr: Tensor, mask: Optional[Tensor] = None, packed_seq_params=None):

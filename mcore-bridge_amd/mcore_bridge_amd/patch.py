@@ -11,6 +11,10 @@ from __future__ import annotations
 import importlib
 
 from .dsa import fused_qk_topk_naive
+# The whole DSA attention (indexer, top-k, absorbed sparse attention, indexer loss) goes in at the
+# layer spec instead: install_attention(spec) swaps an absorbed MLASelfAttention subclass into every
+# MLA layer spec, the mechanism of reference src/mcore_bridge/model/register.py:158-162.
+from .mla import install_attention, uninstall_attention  # noqa: F401
 
 DSA_MODULE = "megatron.core.transformer.experimental_attention_variant.dsa"
 

@@ -94,3 +94,22 @@ def test_dsa_indexer_rejects_non_thd_packing():
         assert "THD" in str(e)
     else:
         raise AssertionError("non-THD packing must be rejected")
+
+
+def test_install_attention_swaps_mla_in_layer_specs():
+    # the absorbed DSA MLA goes into every layer spec whose self-attention module is an
+    # MLASelfAttention, as reference register.py:158-162 swaps its own; other modules are left alone
+    import megatron_standin as M
+    from mcore_bridge_amd import mla
+    spec = M.spec_with(M.MLASelfAttention, n_layers=3)
+    other = type("SelfAttention", (torch.nn.Module,), {})
+    spec.layer_specs[1].submodules.self_attention.module = other
+    assert mla.install_attention(spec) == 2
+    a0 = spec.layer_specs[0].submodules.self_attention.module
+    assert issubclass(a0, M.MLASelfAttention) and a0 is not M.MLASelfAttention
+    assert a0 is spec.layer_specs[2].submodules.self_attention.module          # one class per base
+    assert spec.layer_specs[1].submodules.self_attention.module is other
+    assert mla.install_attention(spec) == 0                                     # idempotent
+    assert mla._rope_fn(a0) is M.apply_rotary_pos_emb                           # the caller's own RoPE
+    assert mla.uninstall_attention(spec) == 2
+    assert spec.layer_specs[0].submodules.self_attention.module is M.MLASelfAttention
