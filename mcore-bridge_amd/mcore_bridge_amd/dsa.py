@@ -79,18 +79,21 @@ def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
 
     Keyword extensions: ``causal``; ``return_scores=False`` skips materialising the ``[B, S, S]``
     scores (first output None); ``q_scale [S, B, Hi]`` / ``k_scale [S, B]`` with float8_e4m3fn
-    ``q`` / ``k``.  The scores carry no gradient (see ``DSAIndexer``).
+    ``q`` / ``k``.  The bf16 index scores are differentiable in ``q``, ``k`` and ``weights`` (head
+    dim 128): autograd through them runs the dense score backward, which is what the reference's
+    dense indexer loss (compute_dsa_indexer_loss with the default sparse_loss=False) backpropagates
+    through; the indices carry none.
     """
-    if return_scores and torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, weights)):
-        raise NotImplementedError(
-            "fused_qk_topk_naive: the index_scores of this build carry no gradient; differentiate the indexer "
-            "through indexer_kl_loss (sparse loss) or call this under torch.no_grad()")
+    if (return_scores and q_scale is not None and torch.is_grad_enabled()
+            and any(t.requires_grad for t in (q, k, weights))):
+        raise NotImplementedError("fused_qk_topk_naive: the fp8 index scores carry no gradient")
     S, B, Hi, Di = q.shape
     kk = min(index_topk, S)
     if causal is None:
         causal = False
     general_mask = mask is not None and not causal
-    scores_out = torch.empty(B, S, S, dtype=torch.float32, device=q.device) if (return_scores or general_mask) else None
+    need_scores = return_scores or general_mask
+    scores_out = []
     idx_out = torch.empty(B, S, kk, dtype=torch.int64, device=q.device)
     cu = torch.tensor([0, S], dtype=torch.int32, device=q.device)
     for b in range(B):
@@ -98,11 +101,10 @@ def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
         qs = q_scale[:, b].contiguous() if q_scale is not None else None
         ks = k_scale[:, b].contiguous() if k_scale is not None else None
         base, ln = ops.build_rows(cu, S, bool(causal))
-        need_scores = scores_out is not None
         sc = ops.indexer_scores(qb, kb, wb, base, ln, S, S, qs, ks, need_scores)
         if general_mask:
             sc = sc + mask[b].to(torch.float32)
-        idx = ops.topk(sc, base, ln, kk).to(torch.int64)            # ascending key ids, -1 pad
+        idx = ops.topk(sc.detach(), base, ln, kk).to(torch.int64)   # ascending key ids, -1 pad
         pad = idx < 0
         if causal:
             # masked (-inf) keys of row t are t+1, t+2, ...: a stable top-k takes them in order,
@@ -112,13 +114,14 @@ def fused_qk_topk_naive(q: Tensor, k: Tensor, weights: Tensor, index_topk: int,
         # reference order: score descending, ties to the lower index (stable sort of an
         # ascending-index list); padded slots score -inf (the masked tail of `sc` is only
         # written when the scores are returned)
-        vals = torch.gather(sc, 1, idx.clamp(min=0))
-        vals = torch.where(pad, torch.full_like(vals, float("-inf")), vals)
-        order = torch.sort(vals, dim=1, descending=True, stable=True).indices
-        idx_out[b] = torch.gather(idx, 1, order)
-        if scores_out is not None:
-            scores_out[b] = sc
-    return (scores_out if return_scores else None), idx_out
+        with torch.no_grad():
+            vals = torch.gather(sc, 1, idx.clamp(min=0))
+            vals = torch.where(pad, torch.full_like(vals, float("-inf")), vals)
+            order = torch.sort(vals, dim=1, descending=True, stable=True).indices
+            idx_out[b] = torch.gather(idx, 1, order)
+        if return_scores:
+            scores_out.append(sc)
+    return (torch.stack(scores_out) if return_scores else None), idx_out
 
 
 def sparse_mla_attention(query: Tensor, kv: Tensor, topk_indices: Tensor, softmax_scale: float,
@@ -220,6 +223,59 @@ def indexer_kl_loss(q: Tensor, kv: Tensor, lse: Tensor, topk_indices: Tensor, q_
     return _IndexerKL.apply(index_sel, target, idx, k_idx.shape[0], causal, float(loss_coeff))
 
 
+def indexer_kl_loss_dense(q: Tensor, kv: Tensor, q_idx: Tensor, k_idx: Tensor, w: Tensor, softmax_scale: float,
+                          loss_coeff: float, cu_seqlens: Optional[Tensor] = None,
+                          max_seqlen: Optional[int] = None) -> Tensor:
+    """Dense DSA indexer loss in the packed THD layout: the reference's default
+    (``dsa_indexer_loss_coeff > 0`` with ``dsa_indexer_use_sparse_loss = False``, reference
+    src/mcore_bridge/config/model_config.py:204-205; megatron-core's ``compute_dsa_indexer_loss``
+    with ``sparse_loss=False``).
+
+    The target of query t is the head-mean of its dense causal attention probabilities over EVERY
+    visible key of its document (``q [T, H, 576]``, ``kv [N, 576]`` absorbed, detached as the
+    reference detaches query and key), and the loss is ``loss_coeff * mean_t KL(target_t ||
+    softmax(I_t))`` with ``I`` the index scores of all visible keys -- differentiable in ``q_idx [T,
+    Hi, 128]``, ``k_idx [N, 128]`` (bf16) and ``w [T, Hi]`` through the dense score backward.
+    ``cu_seqlens`` (int32, device) gives the documents (one document of T tokens by default)."""
+    T = q.shape[0]
+    if cu_seqlens is None:
+        cu_seqlens = torch.tensor([0, T], dtype=torch.int32, device=q.device)
+        max_seqlen = T
+    if max_seqlen is None:
+        max_seqlen = int((cu_seqlens[1:] - cu_seqlens[:-1]).max().item())
+    base, ln = ops.build_rows(cu_seqlens.to(torch.int32), T, True)
+    pitch = max(4, (max_seqlen + 3) // 4 * 4)
+    with torch.no_grad():
+        qd, kvd = q.detach(), kv.detach()
+        lse = ops.dense_attention_lse(qd, kvd, base, ln, max_seqlen, softmax_scale)
+        target = ops.dense_attention_target(qd, kvd, lse, base, ln, max_seqlen, pitch, softmax_scale)
+        idx = ops.dense_row_indices(base, ln, 0, pitch)
+    scores = ops.indexer_scores(q_idx, k_idx, w, base, ln, max_seqlen, pitch, None, None, True)
+    return _IndexerKL.apply(scores, target, idx, k_idx.shape[0], False, float(loss_coeff))
+
+
+class _AttachIndexerLoss(torch.autograd.Function):
+    """``out`` unchanged in the forward; the backward also sends ``loss_scale`` into ``loss`` -- the
+    way Megatron's DSAIndexerLossAutoScaler attaches the indexer loss to the attention output, so
+    the loss needs no separate backward call."""
+
+    @staticmethod
+    def forward(ctx, out: Tensor, loss: Tensor, loss_scale: float):
+        ctx.loss_scale = loss_scale
+        ctx.loss_meta = (loss.shape, loss.dtype, loss.device)
+        return out.view_as(out)
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        shape, dtype, dev = ctx.loss_meta
+        return g, torch.full(shape, ctx.loss_scale, dtype=dtype, device=dev), None
+
+
+def attach_indexer_loss(out: Tensor, loss: Tensor, loss_scale: float = 1.0) -> Tensor:
+    """``out`` with ``loss_scale * loss`` applied in its backward (see ``_AttachIndexerLoss``)."""
+    return _AttachIndexerLoss.apply(out, loss, float(loss_scale))
+
+
 class _SparseMLAWithIndexerLoss(torch.autograd.Function):
     """Sparse attention whose backward also applies the sparse indexer KL loss (see
     ``sparse_mla_with_indexer_loss``)."""
@@ -301,9 +357,12 @@ def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compres
     ``key_h = [kv_compressed W_UK_h^T, k_pos_emb]``, ``value_h = kv_compressed W_UV_h^T`` -- and is
     differentiable w.r.t. every tensor input (the weight included).
 
-    ``indexer_loss = (q_idx, k_idx, w, loss_coeff, loss_scale)`` (the indexer's bf16 outputs,
-    ``[S, B, Hi, 128]``, ``[S, B, 128]``, ``[S, B, Hi]``) also applies the sparse indexer KL loss in
-    the attention's backward (``sparse_mla_with_indexer_loss``); the call then returns ``(out, loss)``."""
+    ``indexer_loss = (q_idx, k_idx, w, loss_coeff, loss_scale[, sparse[, docs]])`` (the indexer's
+    bf16 outputs, ``[S, B, Hi, 128]``, ``[S, B, 128]``, ``[S, B, Hi]``) also applies the indexer KL
+    loss in the attention's backward -- the sparse loss (``sparse_mla_with_indexer_loss``, default)
+    or, with ``sparse=False``, the dense one (``indexer_kl_loss_dense``; its documents are each
+    batch row, or ``docs = (cu_seqlens, max_seqlen)`` for packed THD rows in a batch of one); the
+    call then returns ``(out, loss)``."""
     S, B, H, dn = q_no_pe.shape
     dc = kv_compressed.shape[-1]
     assert dc + q_pos_emb.shape[-1] == ops.D_QK and dc == ops.D_V, "latent 512 + rope 64"
@@ -320,16 +379,27 @@ def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compres
         o_lat = sparse_mla_attention(query.contiguous(), kv.contiguous(), topk_indices, softmax_scale, ops.D_V,
                                      causal)
     else:
-        q_i, k_i, w_i, coeff, loss_scale = indexer_loss
+        q_i, k_i, w_i, coeff, loss_scale = indexer_loss[:5]
+        sparse = indexer_loss[5] if len(indexer_loss) > 5 else True
+        docs = indexer_loss[6] if len(indexer_loss) > 6 else None
         Hi = q_i.shape[-2]
         off = (torch.arange(B, device=query.device, dtype=torch.int64) * S).view(B, 1, 1)
         ti = topk_indices.to(torch.int64)
         idx = torch.where(ti >= 0, ti + off, torch.full_like(ti, -1)).reshape(B * S, -1).to(torch.int32)
-        o_thd, loss = sparse_mla_with_indexer_loss(
-            query.transpose(0, 1).reshape(B * S, H, ops.D_QK).contiguous(),
-            kv.transpose(0, 1).reshape(B * S, ops.D_QK).contiguous(), idx,
-            q_i.transpose(0, 1).reshape(B * S, Hi, -1), k_i.transpose(0, 1).reshape(B * S, -1),
-            w_i.transpose(0, 1).reshape(B * S, Hi), softmax_scale, coeff, causal, loss_scale)
+        q_thd = query.transpose(0, 1).reshape(B * S, H, ops.D_QK).contiguous()
+        kv_thd = kv.transpose(0, 1).reshape(B * S, ops.D_QK).contiguous()
+        qi_thd = q_i.transpose(0, 1).reshape(B * S, Hi, -1)
+        ki_thd, wi_thd = k_i.transpose(0, 1).reshape(B * S, -1), w_i.transpose(0, 1).reshape(B * S, Hi)
+        if sparse:
+            o_thd, loss = sparse_mla_with_indexer_loss(q_thd, kv_thd, idx, qi_thd, ki_thd, wi_thd, softmax_scale,
+                                                       coeff, causal, loss_scale)
+        else:
+            o_thd = ops.sparse_mla(q_thd, kv_thd, idx, softmax_scale, causal)
+            if docs is None:
+                docs = (torch.arange(0, (B + 1) * S, S, device=query.device, dtype=torch.int32), S)
+            loss = indexer_kl_loss_dense(q_thd, kv_thd, qi_thd, ki_thd, wi_thd, softmax_scale, coeff, *docs)
+            o_thd = attach_indexer_loss(o_thd, loss, loss_scale)
+            loss = loss.detach()
         o_lat = o_thd.reshape(B, S, H * ops.D_V).transpose(0, 1)
     o = o_lat.reshape(S, B, H, dc).permute(2, 0, 1, 3).reshape(H, S * B, dc)
     out = _HeadwiseMatmul.apply(o, w_uv_t)                             # [H, S*B, dv]
@@ -429,9 +499,9 @@ class DSAIndexer(_IndexerComputation, torch.nn.Module):
 
     ``forward_before_topk`` is differentiable in the bf16 layout (the prologue's backward kernel,
     then the projections' GEMM backward), which is what training the indexer with the sparse KL
-    loss needs: pass its outputs to ``indexer_kl_loss``.  ``forward_with_scores`` and ``forward``
-    return scores and indices, which carry no gradient (the reference's dense, non-sparse loss
-    differentiates all index scores; that variant is not built)."""
+    loss needs: pass its outputs to ``indexer_kl_loss`` (sparse) or ``indexer_kl_loss_dense``.
+    ``forward_with_scores`` and ``forward`` run under no_grad, as the reference's indices need no
+    gradient; the scores of ``fused_qk_topk_naive`` called with grad enabled are differentiable."""
 
     def __init__(self, hidden_size: int, q_lora_rank: int, index_n_heads: int = 64, index_head_dim: int = 128,
                  index_topk: int = 2048, qk_pos_emb_head_dim: int = 64, layernorm_epsilon: float = 1e-6,
@@ -489,7 +559,8 @@ class DSAttention(torch.nn.Module):
 
     The attention is causal by construction, as DSA's is: ``attention_mask`` is not read (so it
     is never inspected on the host), and ``attn_mask_type``, when given, must be a causal kind.
-    The dense (non-sparse) indexer loss is not built."""
+    ``use_sparse_loss=False`` (the reference default) trains the indexer with the dense loss
+    (``indexer_kl_loss_dense``), computed in the forward and applied in the output's backward."""
 
     def __init__(self, indexer: DSAIndexer, softmax_scale: float, loss_coeff: float = 0.0,
                  use_sparse_loss: bool = True):
@@ -508,8 +579,8 @@ class DSAttention(torch.nn.Module):
         psp, _ = _split_packed(packed_seq_params)
         docs = _thd_docs(psp)
         train_loss = self.training and self.loss_coeff > 0 and torch.is_grad_enabled()
-        if train_loss and (not self.use_sparse_loss or self.indexer.fp8):
-            raise NotImplementedError("only the sparse indexer loss with the bf16 indexer is built")
+        if train_loss and self.indexer.fp8:
+            raise NotImplementedError("the indexer loss needs the bf16 indexer (the fp8 scores carry no gradient)")
         with torch.set_grad_enabled(train_loss):
             out = self.indexer.forward_before_topk(x, qr, packed_seq_params)
         _, topk = self.indexer.topk_from_outputs(out, None, docs, causal=True, return_scores=False)
@@ -534,8 +605,20 @@ class DSAttention(torch.nn.Module):
         if docs is None:
             q_i, k_i, w = (q_i.transpose(0, 1).reshape(B * S, Hi, -1), k_i.transpose(0, 1).reshape(B * S, -1),
                            w.transpose(0, 1).reshape(B * S, Hi))
-        o, loss = sparse_mla_with_indexer_loss(q_thd.contiguous(), kv_thd.contiguous(), idx, q_i, k_i, w,
-                                               self.softmax_scale, self.loss_coeff, True)
+        if self.use_sparse_loss:
+            o, loss = sparse_mla_with_indexer_loss(q_thd.contiguous(), kv_thd.contiguous(), idx, q_i, k_i, w,
+                                                   self.softmax_scale, self.loss_coeff, True)
+        else:
+            # dense loss (the reference default): over every visible key, computed here and applied in
+            # the backward of the output
+            if docs is not None:
+                cu, max_s = docs
+            else:
+                cu, max_s = torch.arange(0, (B + 1) * S, S, device=query.device, dtype=torch.int32), S
+            o = ops.sparse_mla(q_thd.contiguous(), kv_thd.contiguous(), idx, self.softmax_scale, True)
+            loss = indexer_kl_loss_dense(q_thd, kv_thd, q_i, k_i, w, self.softmax_scale, self.loss_coeff, cu, max_s)
+            o = attach_indexer_loss(o, loss)
+            loss = loss.detach()
         self.last_indexer_loss = loss
         if docs is not None:
             return o.reshape(T, H * ops.D_V)

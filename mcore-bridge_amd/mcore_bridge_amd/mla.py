@@ -13,8 +13,9 @@ RoPE function of the base class's own module), then the DSA path of this package
 latent layout -- the indexer's kernel path over the core attention's indexer parameters
 (``IndexerView``), the causal top-k, and ``absorbed_mla_sparse_attention`` (``W_UK`` folded into
 the query, the shared ``[kv_compressed, k_pos_emb]`` latent row, ``W_UV`` after the kernel) --
-with the sparse indexer KL loss applied in the attention's backward when training with
-``dsa_indexer_loss_coeff > 0`` (``dsa_indexer_use_sparse_loss``, model_config.py:204-205).
+with the indexer KL loss applied in the attention's backward when training with
+``dsa_indexer_loss_coeff > 0`` -- the dense loss by default, the sparse one with
+``dsa_indexer_use_sparse_loss`` (model_config.py:204-205).
 ``install_attention(spec)`` makes the swap in a layer spec, the way register.py:158-162 does.
 
 Scope: one tensor-parallel rank holding every head (the kernels' single-GPU share), no
@@ -109,8 +110,6 @@ class _AbsorbedDSAForward:
         ix = self._dsa_indexer()
         coeff = float(getattr(cfg, "dsa_indexer_loss_coeff", 0.0) or 0.0)
         train_loss = self.training and coeff > 0 and torch.is_grad_enabled()
-        if train_loss and not getattr(cfg, "dsa_indexer_use_sparse_loss", False):
-            raise NotImplementedError("the dense indexer loss (dsa_indexer_use_sparse_loss=False) is not built")
         if train_loss and ix.fp8:
             raise NotImplementedError("the indexer loss needs the bf16 indexer")
         with torch.set_grad_enabled(train_loss):
@@ -124,8 +123,10 @@ class _AbsorbedDSAForward:
         w_kv = self.linear_kv_up_proj.weight
         scale = self._dsa_softmax_scale()
         if train_loss:
+            sparse = bool(getattr(cfg, "dsa_indexer_use_sparse_loss", False))
             out, loss = absorbed_mla_sparse_attention(q_nope, q_pe, kv_c, k_pe, w_kv, topk, scale, True,
-                                                      indexer_loss=(*ix_out, coeff, self.indexer_loss_scale))
+                                                      indexer_loss=(*ix_out, coeff, self.indexer_loss_scale, sparse,
+                                                                    docs))
             self.last_indexer_loss = loss
         else:
             out = absorbed_mla_sparse_attention(q_nope, q_pe, kv_c, k_pe, w_kv, topk, scale, True)

@@ -572,3 +572,79 @@ def _sel_backward(ctx, d_scores):
 
 
 torch.library.register_autograd("dsa_amd::indexer_selected_scores", _sel_backward, setup_context=_sel_setup)
+
+
+# --------------------------------------------------------------------------------------
+# dense rows: every visible key of each query (the reference's [B, S, S] index scores and its
+# dense indexer loss), through the kernels above in blocks of key columns
+# --------------------------------------------------------------------------------------
+SCORES_BWD_COLS = 4096   # key columns per call of the selected-slot score backward
+ATTN_COLS = 8192         # key columns per call of the sparse forward / KL target
+
+
+def dense_row_indices(row_base: Tensor, row_len: Tensor, start: int, width: int) -> Tensor:
+    """``[T, width]`` int32: key id ``row_base[t] + start + j`` where ``start + j < row_len[t]``, else -1
+    (column block ``[start, start + width)`` of the dense rows)."""
+    j = torch.arange(start, start + width, device=row_base.device, dtype=torch.int32)
+    ids = row_base.to(torch.int32)[:, None] + j[None]
+    return torch.where(j[None] < row_len.to(torch.int32)[:, None], ids, torch.full_like(ids, -1))
+
+
+def indexer_scores_dense_bwd(q: Tensor, k: Tensor, w: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
+                             d_scores: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``indexer_scores`` (bf16, head_dim 128) from ``d_scores [T, pitch]``: only columns
+    ``j < row_len[t]`` carry gradient (the rest are constants).  Runs the selected-slot score
+    backward on blocks of ``SCORES_BWD_COLS`` columns and sums them.  ``(dq, dw, dk)`` fp32."""
+    dq = dw = dk = None
+    for c0 in range(0, max(max_row_len, 1), SCORES_BWD_COLS):
+        width = min(SCORES_BWD_COLS, max_row_len - c0)
+        idx = dense_row_indices(row_base, row_len, c0, width)
+        d = d_scores[:, c0:c0 + width].float()
+        d = torch.where(idx >= 0, d, torch.zeros_like(d)).contiguous()
+        a, b, c = indexer_scores_bwd(q, k, w, idx, d, False)
+        dq, dw, dk = (a, b, c) if dq is None else (dq + a, dw + b, dk + c)
+    return dq, dw, dk
+
+
+def _isc_setup(ctx, inputs, output):
+    q, k, w, row_base, row_len, max_row_len, pitch, q_scale, k_scale, fill_masked = inputs
+    ctx.save_for_backward(q, k, w, row_base, row_len)
+    ctx.max_row_len = max_row_len
+    ctx.fp8 = q_scale is not None
+
+
+def _isc_backward(ctx, d_scores):
+    q, k, w, row_base, row_len = ctx.saved_tensors
+    if ctx.fp8 or q.shape[-1] != 128:
+        raise NotImplementedError("indexer_scores backward: bf16 inputs with head_dim 128 only")
+    dq, dw, dk = indexer_scores_dense_bwd(q, k, w, row_base, row_len, ctx.max_row_len, d_scores)
+    return dq.to(q.dtype), dk.to(k.dtype), dw.to(w.dtype), None, None, None, None, None, None, None
+
+
+torch.library.register_autograd("dsa_amd::indexer_scores", _isc_backward, setup_context=_isc_setup)
+
+
+def dense_attention_lse(q: Tensor, kv: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
+                        sm_scale: float) -> Tensor:
+    """``[T, H]`` natural-log LSE of every query's dense attention over all of its visible keys
+    (the sparse forward over blocks of ``ATTN_COLS`` dense key columns, combined by logaddexp)."""
+    lse = None
+    for c0 in range(0, max(max_row_len, 1), ATTN_COLS):
+        idx = dense_row_indices(row_base, row_len, c0, min(ATTN_COLS, max_row_len - c0))
+        _, l = sparse_mla_fwd(q, kv, idx, sm_scale, False)
+        lse = l if lse is None else torch.logaddexp(lse, l)
+    return lse
+
+
+def dense_attention_target(q: Tensor, kv: Tensor, lse: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
+                           pitch: int, sm_scale: float) -> Tensor:
+    """Target of the dense indexer loss, ``[T, pitch]`` fp32: column j = key ``row_base[t] + j`` holds
+    ``(1/H) sum_h exp(sm_scale * q[t,h] . kv[key] - lse[t,h])`` (0 past the row), the head-mean of the
+    dense attention probabilities (``lse`` from ``dense_attention_lse``)."""
+    T = q.shape[0]
+    tgt = torch.zeros(T, pitch, dtype=torch.float32, device=q.device)
+    for c0 in range(0, max(max_row_len, 1), ATTN_COLS):
+        width = min(ATTN_COLS, max_row_len - c0)
+        idx = dense_row_indices(row_base, row_len, c0, width)
+        tgt[:, c0:c0 + width] = indexer_kl_target(q, kv, idx, lse, sm_scale, False)
+    return tgt

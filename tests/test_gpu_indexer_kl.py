@@ -10,7 +10,7 @@ import torch
 
 from oracle import dsa_oracle as O
 from mcore_bridge_amd import ops, workloads as W
-from mcore_bridge_amd.dsa import indexer_kl_loss
+from mcore_bridge_amd.dsa import fused_qk_topk_naive, indexer_kl_loss
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -548,3 +548,103 @@ def test_dsattention_thd_packed_equals_per_document():
     _close(ka.grad.cpu(), kg.cpu(), rel=1e-2, name="dkv packed vs per document")
     for n in grads_p:
         _close(grads_p[n].cpu(), grads_d[n].cpu(), rel=2e-2, name=f"indexer {n}")
+
+
+@pytest.mark.parametrize("cols", [None, 96])
+def test_fused_qk_topk_naive_scores_are_differentiable(cols, monkeypatch):
+    """The [B, S, S] index scores of the drop-in carry the dense score backward (what the reference's
+    dense indexer loss backpropagates through): gradients of q, k, weights against float64 autograd
+    of the oracle's scores, with the causal triu mask and without; ``cols`` shrinks the column
+    blocks of the dense backward so that several blocks run."""
+    print(f"[index scores autograd] cols={cols}", flush=True)
+    if cols:
+        monkeypatch.setattr(ops, "SCORES_BWD_COLS", cols)
+    g = torch.Generator().manual_seed(31)
+    S, B, Hi = 200, 2, 64
+    q = (torch.randn(S, B, Hi, 128, generator=g) * 0.1).bfloat16()
+    k = (torch.randn(S, B, 128, generator=g) * 0.1).bfloat16()
+    w = torch.randn(S, B, Hi, generator=g) / 8
+    R = torch.randn(B, S, S, generator=g)
+    mask = torch.triu(torch.full((S, S), float("-inf")), 1)[None].expand(B, S, S)
+    for m, causal in ((mask, None), (None, True), (None, False)):
+        qd, kd, wd = (x.to(DEV).requires_grad_() for x in (q, k, w))
+        sc, _ = fused_qk_topk_naive(qd, kd, wd, 32, m.to(DEV) if m is not None else None, causal=causal)
+        (torch.where(torch.isfinite(sc), sc, torch.zeros_like(sc)) * R.to(DEV)).sum().backward()
+        qr, kr, wr = (x.double().requires_grad_() for x in (q, k, w))
+        ref = torch.stack([O.indexer_scores(qr[:, b], kr[:, b], wr[:, b], causal=causal is not False) for b in range(B)])
+        (torch.where(torch.isfinite(ref), ref, torch.zeros_like(ref)) * R.double()).sum().backward()
+        for name, a, r in (("dq", qd.grad, qr.grad), ("dk", kd.grad, kr.grad), ("dw", wd.grad, wr.grad)):
+            _close(a.cpu(), r, name=f"{name} (mask={m is not None}, causal={causal})")
+
+
+@pytest.mark.parametrize("cols", [None, 64])
+def test_dense_indexer_loss_matches_float64_autograd(cols, monkeypatch):
+    """The dense indexer loss (the reference default, dsa_indexer_use_sparse_loss=False) over packed
+    documents: loss and gradients of q_idx, k_idx, w against float64 autograd through the oracle's
+    dense scores and compute_dsa_indexer_loss(sparse_loss=False), document by document (the
+    reference's mean over tokens); ``cols`` shrinks every column block of the dense path."""
+    print(f"[dense indexer loss] cols={cols}", flush=True)
+    from mcore_bridge_amd.dsa import indexer_kl_loss_dense
+    if cols:
+        monkeypatch.setattr(ops, "SCORES_BWD_COLS", cols)
+        monkeypatch.setattr(ops, "ATTN_COLS", cols)
+    g = torch.Generator().manual_seed(41)
+    cu = [0, 130, 300, 301, 420]
+    T, H, Hi, coeff = cu[-1], 16, 64, 0.4
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16()
+    qi, ki, w = _indexer_inputs(T, Hi, g)
+    qd, kd, wd = (x.to(DEV).requires_grad_() for x in (qi, ki, w))
+    loss = indexer_kl_loss_dense(q.to(DEV), kv.to(DEV), qd, kd, wd, W.SM_SCALE, coeff,
+                                 torch.tensor(cu, dtype=torch.int32, device=DEV), max(b - a for a, b in zip(cu[:-1], cu[1:])))
+    loss.backward()
+    qr, kr, wr = (x.double().requires_grad_() for x in (qi, ki, w))
+    ref = 0.0
+    for a, b in zip(cu[:-1], cu[1:]):
+        S = b - a
+        I = O.indexer_scores(qr[a:b], kr[a:b], wr[a:b])
+        key = kv[a:b].double()[:, None, None, :].expand(S, 1, H, 576)
+        topk = torch.zeros(1, S, 1, dtype=torch.long)
+        ref = ref + O.compute_dsa_indexer_loss_dense(I[None], topk, q[a:b].double()[:, None], key, W.SM_SCALE,
+                                                     coeff, False) * (S / T)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 2e-3 * abs(ref.item()) + 1e-7, (loss.item(), ref.item())
+    for name, a, r in (("dq_idx", qd.grad, qr.grad), ("dk_idx", kd.grad, kr.grad), ("dw", wd.grad, wr.grad)):
+        _close(a.cpu(), r, name=name)
+
+
+def test_dsattention_dense_loss_matches_the_separate_op():
+    """DSAttention with use_sparse_loss=False (the reference default): the training output equals the
+    eval output, last_indexer_loss equals indexer_kl_loss_dense on the indexer's outputs (batch rows
+    as documents), and the indexer parameters receive gradients through the dense score backward."""
+    from mcore_bridge_amd.dsa import DSAIndexer, DSAttention, indexer_kl_loss_dense
+    print("[DSAttention dense loss]", flush=True)
+    g = torch.Generator().manual_seed(57)
+    S, B, H, hidden, qlr, Hi, K = 120, 2, 16, 256, 192, 64, 40
+    indexer = DSAIndexer(hidden, qlr, index_n_heads=Hi, index_topk=K, device=DEV)
+    with torch.no_grad():
+        for p_ in indexer.parameters():
+            p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(p_.dtype))
+        indexer.k_norm.weight.add_(1.0)
+    attn = DSAttention(indexer, W.SM_SCALE, loss_coeff=0.25, use_sparse_loss=False)
+    query = (torch.randn(S, B, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    key = (torch.randn(S, B, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    x = torch.randn(S, B, hidden, generator=g).bfloat16().to(DEV)
+    qr = torch.randn(S, B, qlr, generator=g).bfloat16().to(DEV)
+    psp = (None, (torch.rand(S, 1, 1, 64, generator=g) * 200).to(DEV))
+    attn.eval()
+    with torch.no_grad():
+        out_e = attn(query, key, None, None, x, qr, packed_seq_params=psp)
+    attn.train()
+    out_t = attn(query, key, None, None, x, qr, packed_seq_params=psp)
+    assert torch.equal(out_t.detach(), out_e)
+    (out_t.float() * 0.01).sum().backward()
+    for n, p_ in indexer.named_parameters():
+        assert p_.grad is not None and bool(torch.isfinite(p_.grad).all()) and p_.grad.abs().sum() > 0, n
+    with torch.no_grad():
+        q_i, k_i, w = indexer.forward_before_topk(x, qr, psp)
+        cu = torch.arange(0, (B + 1) * S, S, device=DEV, dtype=torch.int32)
+        ref = indexer_kl_loss_dense(query.transpose(0, 1).reshape(B * S, H, 576), key.transpose(0, 1).reshape(B * S, 576),
+                                    q_i.transpose(0, 1).reshape(B * S, Hi, 128), k_i.transpose(0, 1).reshape(B * S, 128),
+                                    w.transpose(0, 1).reshape(B * S, Hi), W.SM_SCALE, 0.25, cu, S)
+    torch.testing.assert_close(attn.last_indexer_loss, ref, rtol=1e-5, atol=1e-8)

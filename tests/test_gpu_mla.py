@@ -1,8 +1,8 @@
 """The absorbed DSA MLA swapped into a layer spec (mcore_bridge_amd.mla), on the GPU, against the
 reference MLA's un-absorbed forward (multi_latent_attention.py:43-178, 262-290) in float64 built
 from the same module's weights: output and the gradients of the input and of every weight, sbhd
-with batch 2, THD packing against per-document calls, and the training path with the sparse indexer
-loss.  The Megatron modules are stand-ins (tests/megatron_standin.py) with the reference's names."""
+with batch 2, THD packing against per-document calls, and the training path with the sparse and
+the dense indexer loss.  The Megatron modules are stand-ins (tests/megatron_standin.py) with the reference's names."""
 import types
 
 import pytest
@@ -106,7 +106,13 @@ def test_absorbed_mla_swap_trains_the_indexer_with_the_sparse_loss():
     assert loss is not None and bool(torch.isfinite(loss)) and float(loss) > 0
     for n, p in indexer.named_parameters():
         assert p.grad is not None and bool(torch.isfinite(p.grad).all()) and float(p.grad.abs().sum()) > 0, n
-    # the dense loss is the reference default and is refused with a clear error, not silently skipped
+    # the dense loss (the reference default): same forward, the loss over every visible key
     mod.config.dsa_indexer_use_sparse_loss = False
-    with pytest.raises(NotImplementedError):
-        mod(x, None, rotary_pos_emb=rope)
+    indexer.zero_grad(set_to_none=True)
+    out_d, _ = mod(x, None, rotary_pos_emb=rope)
+    _close(out_d.detach(), out_e, rel=1e-3, name="dense-loss training forward = eval forward")
+    (out_d.float() * 0.01).sum().backward()
+    loss_d = mod.last_indexer_loss
+    assert bool(torch.isfinite(loss_d)) and float(loss_d) > 0
+    for n, p in indexer.named_parameters():
+        assert p.grad is not None and bool(torch.isfinite(p.grad).all()) and float(p.grad.abs().sum()) > 0, n

@@ -657,3 +657,55 @@ def test_fp32_torch_reference_matches_oracle():
     fin = torch.isfinite(rl)
     assert torch.equal(fin, torch.isfinite(l))
     torch.testing.assert_close(l.double()[fin], rl[fin], rtol=1e-5, atol=1e-5)
+
+
+def _dense_loss_bruteforce(I, query, key, scale, coeff):
+    # scalar loops over (t, s, h): the dense indexer loss of compute_dsa_indexer_loss with
+    # sparse_loss=False, for one sequence (I [S, S] index scores, query / key [S, H, d])
+    S, H, _ = query.shape
+    tot = 0.0
+    for t in range(S):
+        att = [0.0] * (t + 1)
+        for h in range(H):
+            a = [float(query[t, h] @ key[s, h]) * scale for s in range(t + 1)]
+            m = max(a)
+            z = sum(math.exp(x - m) for x in a)
+            for s in range(t + 1):
+                att[s] += math.exp(a[s] - m) / z
+        z = sum(att)
+        att = [x / z for x in att]
+        iv = [float(I[t, s]) for s in range(t + 1)]
+        m = max(iv)
+        zi = sum(math.exp(x - m) for x in iv)
+        pI = [math.exp(x - m) / zi for x in iv]
+        tot += sum(p * (math.log(p + O.KL_EPS) - math.log(q + O.KL_EPS)) for p, q in zip(att, pI))
+    return tot / S * coeff
+
+
+def test_dense_indexer_loss_pins():
+    # compute_dsa_indexer_loss with sparse_loss=False: (1) scalar brute force; (2) the decomposition
+    # into per-row KL (indexer_kl_sparse with every visible key valid) against the head-mean dense
+    # attention target (attention_head_probs with the dense LSE); (3) its autograd gradient with
+    # respect to the index scores equals that closed form
+    g = torch.Generator().manual_seed(21)
+    S, H, d = 9, 3, 576
+    q = torch.randn(S, H, d, generator=g, dtype=torch.float64) * 0.05
+    kv = torch.randn(S, d, generator=g, dtype=torch.float64) * 0.05
+    I = torch.randn(S, S, generator=g, dtype=torch.float64)
+    causal = torch.triu(torch.full((S, S), float("-inf"), dtype=torch.float64), diagonal=1)
+    Ic = (I + causal).requires_grad_()
+    key = kv[:, None, :].expand(S, H, d)
+    topk = torch.zeros(1, S, 2, dtype=torch.long)            # unused with sparse_loss=False
+    coeff, scale = 0.7, 0.3
+    loss = O.compute_dsa_indexer_loss_dense(Ic[None], topk, q[:, None], key[:, None], scale, coeff, False)
+    assert abs(loss.item() - _dense_loss_bruteforce(I, q, key, scale, coeff)) < 1e-10
+    idx = torch.where(torch.arange(S)[None] <= torch.arange(S)[:, None], torch.arange(S)[None], -1)
+    _, lse = O.sparse_mla_fwd(q, kv, idx, scale)
+    tgt = O.attention_head_probs(q, kv, idx, lse, scale)
+    sel = torch.gather(I, 1, idx.clamp(min=0))
+    kl, dkl = O.indexer_kl_sparse(sel, tgt, idx >= 0)
+    assert abs(loss.item() - coeff * kl.mean().item()) < 1e-10
+    loss.backward()
+    dense_grad = torch.zeros(S, S, dtype=torch.float64).scatter_add_(1, idx.clamp(min=0), dkl * (idx >= 0))
+    torch.testing.assert_close(Ic.grad, dense_grad * coeff / S,
+                               rtol=1e-9, atol=1e-12)
