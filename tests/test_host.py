@@ -113,3 +113,43 @@ def test_install_attention_swaps_mla_in_layer_specs():
     assert mla._rope_fn(a0) is M.apply_rotary_pos_emb                           # the caller's own RoPE
     assert mla.uninstall_attention(spec) == 2
     assert spec.layer_specs[0].submodules.self_attention.module is M.MLASelfAttention
+
+
+def test_v4_hybrid_index_rows():
+    # window slots stay inside the document and at or before t; HCA slots are exactly the visible
+    # compressed entries of t's own document; CSA selections are offset past the raw rows
+    from mcore_bridge_amd import v4
+    cu, W, rate = [0, 9, 20], 4, 3
+    T = cu[-1]
+    idx = v4.hybrid_indices(cu, W, rate)
+    off = v4.compressed_layout(cu, rate)
+    assert off == [0, 3, 6]
+    for d, (a, b) in enumerate(zip(cu[:-1], cu[1:])):
+        for t in range(a, b):
+            row = [int(x) for x in idx[t] if x >= 0]
+            want = list(range(max(a, t - W + 1), t + 1)) + [T + off[d] + w for w in range((t - a + 1) // rate)]
+            assert row == want, (t, row, want)
+    sel = torch.tensor([[1, -1]] * T)
+    csa = v4.hybrid_indices(cu, W, 0, sel)
+    assert csa.shape == (T, W + 2) and (csa[:, W] == T + 1).all() and (csa[:, W + 1] == -1).all()
+
+
+def test_v4_mirror_parameters_are_the_bridge_keys():
+    # the reference's bridge maps these Megatron keys of DSv4HybridSelfAttention to the HF checkpoint
+    # (src/mcore_bridge/model/gpts/deepseek_v4.py:432-464)
+    from mcore_bridge_amd import v4
+    m = v4.DSv4HybridAttention("compressed_sparse_attention", 64, 16, 32, o_groups=4, o_lora_rank=16,
+                               index_n_heads=4, index_head_dim=128, device="cpu")
+    keys = set(m.state_dict())
+    for k in ("linear_proj.weight", "linear_o_group_proj", "linear_q_down_proj.weight", "linear_q_up_proj.weight",
+              "linear_kv_proj.weight", "core_attention.attn_sink", "q_layernorm.weight", "kv_layernorm.weight",
+              "core_attention.compressor.ape", "core_attention.compressor.linear_wkv.weight",
+              "core_attention.compressor.linear_wgate.weight", "core_attention.compressor.norm.weight",
+              "core_attention.indexer.linear_wq_b.weight", "core_attention.indexer.linear_weights_proj.weight",
+              "core_attention.indexer.compressor.ape", "core_attention.indexer.compressor.linear_wkv.weight",
+              "core_attention.indexer.compressor.linear_wgate.weight",
+              "core_attention.indexer.compressor.norm.weight"):
+        assert k in keys, k
+    hca = v4.DSv4HybridAttention("heavily_compressed_attention", 64, 16, 32, o_groups=4, o_lora_rank=16, device="cpu")
+    assert "core_attention.indexer.linear_wq_b.weight" not in hca.state_dict()
+    assert hca.state_dict()["core_attention.compressor.ape"].shape == (128, 512)
