@@ -18,8 +18,10 @@
 // are lane-local plus one exchange with the lane 32 apart.
 // At most 512 bf16 queries of 128-dim rows (decode) K1 runs as indexer_scores_rows_kernel instead:
 // one query per workgroup, key rows staged in LDS by contiguous LDS-direct copies.
-// fp8 (OCP e4m3fn, gfx950 MFMA native): I = k_scale[s] * sum_h (w * q_scale)[t,h] *
-// relu(q8 . k8) -- valid because ReLU is positive-homogeneous and both scales are > 0.
+// fp8 (OCP e4m3fn): gfx950's 32x32x64 fp8 MFMA (twice the bf16 rate per instruction), through
+// the same LDS ring as bf16 when a workgroup's queries share a document;
+// I = k_scale[s] * sum_h (w * q_scale)[t,h] * relu(q8 . k8) -- valid because ReLU is
+// positive-homogeneous and both scales are > 0.
 //
 // K2: one workgroup per row.  4 passes of 8-bit MSB-first radix select over order-preserving
 // uint32 keys (LDS histograms) find the exact K-th largest value; one stable compaction pass
@@ -95,6 +97,70 @@ DSA_DEV void indexer_block_lds(const IndexerParams& p, int t, int c0, int c1_wg,
   }
 }
 
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// gfx950's fp8 MFMA: C[32x32] += A[32x64] * B[64x32] on OCP e4m3fn (format code 0 for A and B), no
+// block scales.  Lane l holds 32 consecutive k of row / column l % 32; the k order inside one
+// MFMA only has to agree between A and B, so both take k = 32 * (l / 32) + 0..31 of a 64-wide step.
+DSA_DEV f32x16 mfma32x32x64_fp8(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+DSA_DEV i32x8 cat16(const u32x4& lo, const u32x4& hi) {
+  return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+// fp8 (e4m3fn, 128-dim rows) scores of a workgroup whose 4 queries share a document: the LDS ring
+// of the bf16 path with 128-byte key rows (4 KB per 32-key block, one 1 KB LDS-direct copy per
+// wave), two 32x32x64 fp8 MFMAs per row tile and block, and the chunk's k_scale values staged in
+// LDS once (I = k_scale[s] * sum_h (w q_scale)[t,h] relu(q8 . k8)).  Row r of a block: 16-byte unit
+// u at slot u ^ (r & 7) (the operand reads of 8 consecutive keys are conflict-free).
+DSA_DEV void indexer_block_lds_fp8(const IndexerParams& p, int t, int c0, int c1_wg, int c1, int base,
+                                   float (&wr)[2][16], const i32x8 (&qa)[2][2], char* ring, float* ks_s) {
+  constexpr int RB = 128, BLK = 32 * RB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hb = lane >> 5, hl = lane & 31;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const char* kbase = reinterpret_cast<const char*>(p.k);
+  const uint32_t ring0 = lds_addr(ring);
+  // the chunk's key scales, through compiler-visible loads retired before the first copy
+  for (int j = threadIdx.x; j < c1_wg - c0; j += 256) ks_s[j] = p.k_scale[base + c0 + j];
+  wait_vmcnt0();
+  auto issue = [&](int blk, int k0) {        // copy wu of the block at key k0: rows 8 wu .. 8 wu + 7
+    const int r = wu * 8 + (lane >> 3), u = lane & 7;
+    const int key = base + min(k0 + r, c1_wg - 1);
+    async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ (r & 7)),
+                           __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)((blk % 3) * BLK + wu * 1024)));
+  };
+  const int nb = (c1_wg - c0 + 31) / 32;
+  issue(0, c0);
+  if (nb > 1) issue(1, c0 + 32);
+  for (int i = 0; i < nb; ++i) {
+    if (i + 1 < nb) wait_vmcnt<1>(); else wait_vmcnt<0>();
+    __syncthreads();
+    if (i + 2 < nb) issue(i + 2, c0 + 32 * (i + 2));
+    const char* row = ring + (i % 3) * BLK + hl * RB;
+    i32x8 kb[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int u0 = 4 * st + 2 * hb;
+      kb[st] = cat16(lds_load16(row + 16 * (u0 ^ (hl & 7))), lds_load16(row + 16 * ((u0 + 1) ^ (hl & 7))));
+    }
+    f32x16 c0a = f32x16{}, c1a = f32x16{};
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      c0a = mfma32x32x64_fp8(qa[0][st], kb[st], c0a);
+      c1a = mfma32x32x64_fp8(qa[1][st], kb[st], c1a);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc += wr[0][e] * fmaxf(c0a[e], 0.f) + wr[1][e] * fmaxf(c1a[e], 0.f);
+    acc = xor32_sum(acc);
+    const int j = c0 + 32 * i + hl;
+    if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc * ks_s[j - c0];
+  }
+}
+
 template <bool FP8>
 __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -103,7 +169,7 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
   const int Di = p.head_dim;        // 64 or 128
   const int nks = Di / 16;          // 4 or 8 k-steps of 16
   const int hb = lane >> 5, hl = lane & 31;
-  if (!FP8) {
+  if (!FP8 || Di == 128) {
     // shared-key path: the workgroup's queries (all valid) lie in one document and the chunk
     // is not past the longest row (workgroup-uniform decisions, before any early return)
     const int t0 = blockIdx.x * 4;
@@ -128,8 +194,28 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int h = 32 * mt + (i >> 2) * 8 + 4 * hb + (i & 3);
-          wr[mt][i] = h < p.n_heads ? p.w[(int64_t)t * p.n_heads + h] : 0.f;
+          float w = h < p.n_heads ? p.w[(int64_t)t * p.n_heads + h] : 0.f;
+          if (FP8 && h < p.n_heads) w *= p.q_scale[(int64_t)t * p.n_heads + h];
+          wr[mt][i] = w;
         }
+      }
+      if constexpr (FP8) {
+        __shared__ float ks_s[kIdxChunkMax];
+        const uint8_t* q8 = reinterpret_cast<const uint8_t*>(p.q) + (int64_t)t * p.n_heads * 128;
+        i32x8 qa8[2][2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int h = 32 * mt + hl;
+#pragma unroll
+          for (int st = 0; st < 2; ++st) {
+            const uint8_t* src = q8 + (int64_t)(h < p.n_heads ? h : 0) * 128 + 64 * st + 32 * hb;
+            const u32x4 lo = gload16(src), hi = gload16(src + 16);
+            qa8[mt][st] = h < p.n_heads ? cat16(lo, hi) : i32x8{};
+          }
+        }
+        wait_vmcnt0();
+        indexer_block_lds_fp8(p, t, c0, c1_wg, c1, base, wr, qa8, ring, ks_s);
+        return;
       }
       const bf16_t* q = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)t * p.n_heads * Di;
       u32x4 qa[2][8];
@@ -202,35 +288,40 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
       if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc;
     }
   } else {
+    // gfx950's 32x32x64 fp8 MFMA: Di / 64 steps, lane holds 32 consecutive bytes of a row
     const uint8_t* q = reinterpret_cast<const uint8_t*>(p.q) + (int64_t)t * p.n_heads * Di;
     const uint8_t* k = reinterpret_cast<const uint8_t*>(p.k);
-    long qa[2][8];
+    const int nst = Di / 64;
+    i32x8 qa[2][2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int h = 32 * mt + hl;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        qa[mt][ks] = (h < p.n_heads && ks < nks) ? *reinterpret_cast<const long*>(q + (int64_t)h * Di + 16 * ks + 8 * hb) : 0l;
+      for (int st = 0; st < 2; ++st) {
+        const uint8_t* src = q + (int64_t)(h < p.n_heads ? h : 0) * Di + 64 * st + 32 * hb;
+        qa[mt][st] = (h < p.n_heads && st < nst) ? cat16(gload16(src), gload16(src + 16)) : i32x8{};
+      }
     }
-    auto load_keys = [&](int k0, long (&dst)[8]) {
-      const uint8_t* krow = k + (int64_t)(base + min(k0 + hl, c1 - 1)) * Di + 8 * hb;
+    auto load_keys = [&](int k0, i32x8 (&dst)[2]) {
+      const uint8_t* krow = k + (int64_t)(base + min(k0 + hl, c1 - 1)) * Di + 32 * hb;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) dst[ks] = ks < nks ? *reinterpret_cast<const long*>(krow + 16 * ks) : 0l;
+      for (int st = 0; st < 2; ++st)
+        dst[st] = st < nst ? cat16(gload16(krow + 64 * st), gload16(krow + 64 * st + 16)) : i32x8{};
     };
-    long kn[8];
+    i32x8 kn[2];
     load_keys(c0, kn);
     for (int k0 = c0; k0 < c1; k0 += 32) {
       const int j = k0 + hl;
       const int key = base + min(j, c1 - 1);
-      long kb[8];
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) kb[ks] = kn[ks];
+      i32x8 kb[2] = {kn[0], kn[1]};
       if (k0 + 32 < c1) load_keys(k0 + 32, kn);
       f32x16 c0a = f32x16{}, c1a = f32x16{};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        c0a = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qa[0][ks], kb[ks], c0a, 0, 0, 0);
-        c1a = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(qa[1][ks], kb[ks], c1a, 0, 0, 0);
+      for (int st = 0; st < 2; ++st) {
+        if (st < nst) {
+          c0a = mfma32x32x64_fp8(qa[0][st], kb[st], c0a);
+          c1a = mfma32x32x64_fp8(qa[1][st], kb[st], c1a);
+        }
       }
       float acc = 0.f;
 #pragma unroll
