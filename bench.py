@@ -566,7 +566,7 @@ def main():
     else:
         achieved, peak, unit = amount / (t[dom] * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
     traffic = measured_traffic(kname)
-    bwd_kernels = [work[k][2] for k in STAGES if k in work] + ["csr_count_lds_kernel", "csr_fill_lds_kernel"]
+    bwd_kernels = [work[k][2] for k in STAGES if k in work] + ["csr_hist_kernel", "csr_colscan_kernel", "csr_fill_kernel"]
     bwd_counter = [measured_traffic(k) for k in bwd_kernels]
     bwd_alg = qb + kvb + ib + 2 * ob + lb + qb + N * 576 * 4
     bwd_traffic = {

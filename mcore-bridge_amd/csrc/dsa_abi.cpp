@@ -34,7 +34,7 @@ BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
   L.g_stage = off; off += align_up(sizeof(uint16_t) * ((size_t)total_q * topk + 1) * kDqk);
   L.pair_pos = off; off += align_up(sizeof(int64_t) * (size_t)total_q * topk);
   L.offsets = off; off += align_up(sizeof(int64_t) * ((size_t)n_kv + 1));
-  L.counts = off; off += align_up(sizeof(int32_t) * (size_t)n_kv);
+  L.counts = off; off += align_up(sizeof(int32_t) * dsa::csr_count_entries(total_q, n_kv));
   L.total = off;
   return L;
 }
@@ -49,7 +49,7 @@ IdxBwdLayout idx_bwd_layout(int total_q, int n_k, int topk) {
   L.g_stage = off; off += align_up(sizeof(uint16_t) * ((size_t)total_q * topk + 1) * 128);
   L.pair_pos = off; off += align_up(sizeof(int64_t) * (size_t)total_q * topk);
   L.offsets = off; off += align_up(sizeof(int64_t) * ((size_t)n_k + 1));
-  L.counts = off; off += align_up(sizeof(int32_t) * (size_t)n_k);
+  L.counts = off; off += align_up(sizeof(int32_t) * dsa::csr_count_entries(total_q, n_k));
   L.total = off;
   return L;
 }

@@ -39,7 +39,7 @@ struct SparseBwdParams {
   int64_t g_sink_row;   // last row of g_stage: write target of pairs that select nothing
   int64_t* pair_pos;    // [total_q, topk] row of G for each pair (-1 = not selected)
   int64_t* csr_offsets; // [n_kv + 1]
-  int32_t* csr_counts;  // [n_kv] counts, then per-key cursor
+  int32_t* csr_counts;  // [csr_count_entries(total_q, n_kv)] scratch of the pair ordering
   int total_q, n_heads, n_kv, topk, topk_pad, causal;
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, dout_stride_t, lse_stride_t, dq_stride_t, dkv_stride;
   float scale, scale_log2;
@@ -157,7 +157,7 @@ struct IdxSelParams {
   int64_t g_sink_row;    // last row of g_stage (pairs that select nothing)
   int64_t* pair_pos;     // [total_q, topk]
   int64_t* csr_offsets;  // [n_k + 1]
-  int32_t* csr_counts;   // [n_k]
+  int32_t* csr_counts;   // [csr_count_entries(total_q, n_k)]
   int total_q, n_heads, n_k, topk, causal;
   int64_t q_stride_t, idx_stride, scores_stride, d_stride;
 };
@@ -176,8 +176,19 @@ int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
 int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream);
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream);
-// Key-major order of the selected (query, slot) pairs: csr_offsets [n_kv + 1] and the row of
-// every pair, pair_pos [total_q, topk] (-1 = not selected); csr_counts is scratch.
+// Key-major order of the selected (query, slot) pairs, ascending in query inside each key:
+// csr_offsets [n_kv + 1] and the row of every pair, pair_pos [total_q, topk] (-1 = not
+// selected); csr_counts is scratch of csr_count_entries() int32.  topk <= 4096.
+// The query rows are cut into csr_groups() runs (at most 256, at most 2^24 run x key counters).
+inline int csr_groups(int total_q, int n_kv) {
+  const int64_t cap = (int64_t(1) << 24) / (n_kv > 0 ? n_kv : 1);
+  int64_t g = total_q < 256 ? total_q : 256;
+  if (g > cap) g = cap;
+  return g > 0 ? (int)g : 1;
+}
+inline size_t csr_count_entries(int total_q, int n_kv) {
+  return (size_t)(csr_groups(total_q, n_kv) + 1) * (size_t)(n_kv > 0 ? n_kv : 0);
+}
 void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
                      int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,

@@ -900,34 +900,84 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   else block_loop(std::integral_constant<int, 4>{});
 }
 
-// Zero fill (a kernel, not hipMemsetAsync, so the sequence stays safe under graph capture).
-__global__ void zero_i32_kernel(int32_t* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
+// ------------------------------------------------------------------------------------------
+// B4: key-major order of the selected (query, slot) pairs, ascending in query inside every
+// key's segment, so that B5 adds each key's G rows in one fixed order and dKV is the same bit
+// for bit from run to run.  The query rows are cut into csr_groups() contiguous runs, run b
+// taken by workgroup b, and the keys into LDS tiles of kCsrLdsKeys:
+//   csr_hist_kernel     cnt[b][k] = pairs of run b that select key k
+//   csr_colscan_kernel  per key: cnt[b][k] <- pairs of the runs before b; cnt[nb][k] = total
+//   csr_scan_kernel     offsets = exclusive scan of the totals
+//   csr_fill_kernel     run b hands out key k's slots from offsets[k] + cnt[b][k] on, one row
+//                       at a time in row order (a barrier between rows)
+// Integer counts make every step exact.  A top-k row holds a key at most once; a row that
+// repeats one gives it consecutive slots in either order, and those G rows are equal (same
+// logits, same P and dS), so the sum is still the same.
+// ------------------------------------------------------------------------------------------
+constexpr int kCsrLdsKeys = 16384;
+constexpr int kCsrThreads = 1024;
+constexpr int kCsrPer = kMaxTopkBwd / kCsrThreads;   // index slots per thread and row
+DSA_DEV bool csr_pair_ok(int v, int t, int n_kv, int causal) { return v >= 0 && v < n_kv && (!causal || v <= t); }
+
+// rows [t0, t1) of this workgroup's run
+DSA_DEV void csr_run(int total_q, int& t0, int& t1) {
+  const int per = (total_q + gridDim.x - 1) / gridDim.x;
+  t0 = min(total_q, (int)blockIdx.x * per);
+  t1 = min(total_q, t0 + per);
 }
 
-// ------------------------------------------------------------------------------------------
-// B4: key-major order of the selected (query, slot) pairs.
-// ------------------------------------------------------------------------------------------
-__global__ void csr_count_kernel(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv,
-                                 int causal, int32_t* counts) {
-  const int64_t n = (int64_t)total_q * topk;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-    const int t = (int)(e / topk), j = (int)(e - (int64_t)t * topk);
-    const int v = idx[(int64_t)t * idx_stride + j];
-    if (v >= 0 && v < n_kv && (!causal || v <= t)) atomicAdd(counts + v, 1);
+__global__ __launch_bounds__(kCsrThreads) void csr_hist_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
+                                                              int topk, int n_kv, int causal, int32_t* cnt) {
+  __shared__ int32_t hist[kCsrLdsKeys];
+  int t0, t1;
+  csr_run(total_q, t0, t1);
+  for (int k0 = 0; k0 < n_kv; k0 += kCsrLdsKeys) {
+    const int nk = min(kCsrLdsKeys, n_kv - k0);
+    for (int k = threadIdx.x; k < nk; k += kCsrThreads) hist[k] = 0;
+    __syncthreads();
+    for (int t = t0; t < t1; ++t)
+      for (int j = threadIdx.x; j < topk; j += kCsrThreads) {
+        const int v = idx[(int64_t)t * idx_stride + j];
+        if (csr_pair_ok(v, t, n_kv, causal) && v >= k0 && v - k0 < nk) atomicAdd(hist + (v - k0), 1);
+      }
+    __syncthreads();
+    for (int k = threadIdx.x; k < nk; k += kCsrThreads) cnt[(int64_t)blockIdx.x * n_kv + k0 + k] = hist[k];
+    __syncthreads();   // the next tile clears hist
   }
 }
 
-// Single-workgroup exclusive scan of counts[n] -> offsets[n+1] (int64); counts is then reset to
-// zero so it can serve as the per-key slot cursor of csr_fill_kernel.
-__global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* counts, int n, int64_t* offsets) {
+// One thread per key walks the runs in order (8 loads in flight per step).
+__global__ __launch_bounds__(256) void csr_colscan_kernel(int32_t* cnt, int n_runs, int n_kv) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n_kv) return;
+  int32_t run = 0;
+  int b = 0;
+  for (; b + 8 <= n_runs; b += 8) {
+    int32_t c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c[u] = cnt[(int64_t)(b + u) * n_kv + k];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      cnt[(int64_t)(b + u) * n_kv + k] = run;
+      run += c[u];
+    }
+  }
+  for (; b < n_runs; ++b) {
+    const int32_t c = cnt[(int64_t)b * n_kv + k];
+    cnt[(int64_t)b * n_kv + k] = run;
+    run += c;
+  }
+  cnt[(int64_t)n_runs * n_kv + k] = run;
+}
+
+// Single-workgroup exclusive scan of totals[n] -> offsets[n + 1] (int64).
+__global__ __launch_bounds__(1024) void csr_scan_kernel(const int32_t* totals, int n, int64_t* offsets) {
   __shared__ int64_t part[1024];
   const int tid = threadIdx.x;
   const int per = (n + 1023) / 1024;
   const int a = min(n, tid * per), b = min(n, a + per);
   int64_t s = 0;
-  for (int i = a; i < b; ++i) s += counts[i];
+  for (int i = a; i < b; ++i) s += totals[i];
   part[tid] = s;
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
@@ -939,79 +989,51 @@ __global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* counts, int n, 
   int64_t run = tid > 0 ? part[tid - 1] : 0;
   for (int i = a; i < b; ++i) {
     offsets[i] = run;
-    run += counts[i];
-    counts[i] = 0;
+    run += totals[i];
   }
   if (tid == 1023) offsets[n] = part[1023];
 }
 
-// Position of every pair inside its key's segment (one integer atomic per pair claims a slot).
-// Slot order inside a segment follows scheduling, and B5 sums a segment in slot order, so dKV
-// can differ in the last fp32 bits between runs (bounded by a test).
-__global__ void csr_fill_kernel(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv,
-                                int causal, const int64_t* offsets, int32_t* cursor, int64_t* pair_pos) {
-  const int64_t n = (int64_t)total_q * topk;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-    const int t = (int)(e / topk), j = (int)(e - (int64_t)t * topk);
-    const int v = idx[(int64_t)t * idx_stride + j];
-    int64_t pos = -1;
-    if (v >= 0 && v < n_kv && (!causal || v <= t)) pos = offsets[v] + atomicAdd(cursor + v, 1);
-    pair_pos[e] = pos;
+__global__ __launch_bounds__(kCsrThreads) void csr_fill_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
+                                                              int topk, int n_kv, int causal, const int64_t* offsets,
+                                                              const int32_t* cnt, int64_t* pair_pos) {
+  __shared__ int32_t next[kCsrLdsKeys];   // next free slot of each key of the tile
+  int t0, t1;
+  csr_run(total_q, t0, t1);
+  auto load_row = [&](int t, int32_t (&v)[kCsrPer]) {
+#pragma unroll
+    for (int i = 0; i < kCsrPer; ++i) {
+      const int j = (int)threadIdx.x + kCsrThreads * i;
+      v[i] = t < t1 && j < topk ? idx[(int64_t)t * idx_stride + j] : -1;
+    }
+  };
+  for (int k0 = 0; k0 < n_kv; k0 += kCsrLdsKeys) {
+    const int nk = min(kCsrLdsKeys, n_kv - k0);
+    for (int k = threadIdx.x; k < nk; k += kCsrThreads)   // < 2^31: checked by the launchers
+      next[k] = (int32_t)(offsets[k0 + k] + cnt[(int64_t)blockIdx.x * n_kv + k0 + k]);
+    __syncthreads();
+    int32_t cur[kCsrPer], nxt[kCsrPer];
+    load_row(t0, cur);
+    for (int t = t0; t < t1; ++t) {
+      load_row(t + 1, nxt);   // the next row's indices under this row's slot claims
+#pragma unroll
+      for (int i = 0; i < kCsrPer; ++i) {
+        const int j = (int)threadIdx.x + kCsrThreads * i;
+        if (j < topk) {
+          const int v = cur[i];
+          int64_t* dst = pair_pos + (int64_t)t * topk + j;
+          if (!csr_pair_ok(v, t, n_kv, causal)) {
+            if (k0 == 0) *dst = -1;
+          } else if (v >= k0 && v - k0 < nk) {
+            *dst = atomicAdd(next + (v - k0), 1);
+          }
+        }
+      }
+      __syncthreads();   // every slot of row t before any of row t + 1
+#pragma unroll
+      for (int i = 0; i < kCsrPer; ++i) cur[i] = nxt[i];
+    }
   }
-}
-
-// The same two steps with per-workgroup LDS histograms when the keys fit in LDS: a workgroup
-// takes a run of query rows, counts its pairs per key with LDS atomics and adds the non-zero
-// counts to the global ones (one global atomic per (workgroup, key) instead of per pair); the
-// fill reserves each key's slots for the whole workgroup with one global atomic and hands them
-// out with LDS atomics.
-constexpr int kCsrLdsKeys = 16384;
-constexpr int kCsrWgs = 256;
-DSA_DEV bool csr_pair_ok(int v, int t, int n_kv, int causal) { return v >= 0 && v < n_kv && (!causal || v <= t); }
-
-__global__ __launch_bounds__(1024) void csr_count_lds_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
-                                                             int topk, int n_kv, int causal, int32_t* counts) {
-  __shared__ int32_t hist[kCsrLdsKeys];
-  for (int k = threadIdx.x; k < n_kv; k += blockDim.x) hist[k] = 0;
-  __syncthreads();
-  const int per = (total_q + gridDim.x - 1) / gridDim.x;
-  const int t0 = blockIdx.x * per, t1 = min(total_q, t0 + per);
-  for (int t = t0; t < t1; ++t)
-    for (int j = threadIdx.x; j < topk; j += blockDim.x) {
-      const int v = idx[(int64_t)t * idx_stride + j];
-      if (csr_pair_ok(v, t, n_kv, causal)) atomicAdd(hist + v, 1);
-    }
-  __syncthreads();
-  for (int k = threadIdx.x; k < n_kv; k += blockDim.x)
-    if (hist[k]) atomicAdd(counts + k, hist[k]);
-}
-
-__global__ __launch_bounds__(1024) void csr_fill_lds_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
-                                                            int topk, int n_kv, int causal, const int64_t* offsets,
-                                                            int32_t* cursor, int64_t* pair_pos) {
-  __shared__ int32_t next[kCsrLdsKeys];   // counts, then the next free slot of each key
-  for (int k = threadIdx.x; k < n_kv; k += blockDim.x) next[k] = 0;
-  __syncthreads();
-  const int per = (total_q + gridDim.x - 1) / gridDim.x;
-  const int t0 = blockIdx.x * per, t1 = min(total_q, t0 + per);
-  for (int t = t0; t < t1; ++t)
-    for (int j = threadIdx.x; j < topk; j += blockDim.x) {
-      const int v = idx[(int64_t)t * idx_stride + j];
-      if (csr_pair_ok(v, t, n_kv, causal)) atomicAdd(next + v, 1);
-    }
-  __syncthreads();
-  for (int k = threadIdx.x; k < n_kv; k += blockDim.x) {
-    const int c = next[k];
-    if (c) next[k] = (int32_t)(offsets[k] + atomicAdd(cursor + k, c));   // < 2^31: checked by the launcher
-  }
-  __syncthreads();
-  for (int t = t0; t < t1; ++t)
-    for (int j = threadIdx.x; j < topk; j += blockDim.x) {
-      const int v = idx[(int64_t)t * idx_stride + j];
-      int64_t pos = -1;
-      if (csr_pair_ok(v, t, n_kv, causal)) pos = atomicAdd(next + v, 1);
-      pair_pos[(int64_t)t * topk + j] = pos;
-    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1049,24 +1071,14 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
 
 void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
                      int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream) {
-  hipLaunchKernelGGL(zero_i32_kernel, dim3((n_kv + 255) / 256), dim3(256), 0, stream, csr_counts, n_kv);
-  const int64_t pairs = (int64_t)total_q * topk;
-  const int nb = (int)std::min<int64_t>((pairs + 255) / 256, 65536);
-  const bool lds_csr = n_kv <= kCsrLdsKeys;
-  const int nwg = std::max(1, std::min(kCsrWgs, total_q));
-  if (lds_csr)
-    hipLaunchKernelGGL(csr_count_lds_kernel, dim3(nwg), dim3(1024), 0, stream, idx, idx_stride, total_q,
-                       topk, n_kv, causal, csr_counts);
-  else
-    hipLaunchKernelGGL(csr_count_kernel, dim3(nb), dim3(256), 0, stream, idx, idx_stride, total_q, topk,
-                       n_kv, causal, csr_counts);
-  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, csr_counts, n_kv, csr_offsets);
-  if (lds_csr)
-    hipLaunchKernelGGL(csr_fill_lds_kernel, dim3(nwg), dim3(1024), 0, stream, idx, idx_stride, total_q,
-                       topk, n_kv, causal, csr_offsets, csr_counts, pair_pos);
-  else
-    hipLaunchKernelGGL(csr_fill_kernel, dim3(nb), dim3(256), 0, stream, idx, idx_stride, total_q, topk,
-                       n_kv, causal, csr_offsets, csr_counts, pair_pos);
+  const int nr = csr_groups(total_q, n_kv);
+  hipLaunchKernelGGL(csr_hist_kernel, dim3(nr), dim3(kCsrThreads), 0, stream, idx, idx_stride, total_q, topk, n_kv,
+                     causal, csr_counts);
+  hipLaunchKernelGGL(csr_colscan_kernel, dim3((n_kv + 255) / 256), dim3(256), 0, stream, csr_counts, nr, n_kv);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, csr_counts + (int64_t)nr * n_kv, n_kv,
+                     csr_offsets);
+  hipLaunchKernelGGL(csr_fill_kernel, dim3(nr), dim3(kCsrThreads), 0, stream, idx, idx_stride, total_q, topk, n_kv,
+                     causal, csr_offsets, csr_counts, pair_pos);
 }
 
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev) {

@@ -81,8 +81,10 @@ def test_bwd_workspace_size_formula():
     T, N, H, K = 16384, 16384, 128, 2048
     ws = lib.dsa_sparse_mla_bwd_workspace_size(T, N, H, K)
     stage = T * H * K * 2
-    assert ws >= 2 * stage + T * K * 576 * 2 + T * K * 8
-    assert ws < 2 * stage + T * K * 576 * 2 + T * K * 8 + 64 * N + 4096
+    # P and dS tiles, G rows, pair rows, key offsets, and the pair ordering's integer counters:
+    # 257 rows (256 query runs + totals) of N
+    fixed = 2 * stage + T * K * 576 * 2 + T * K * 8 + (N + 1) * 8 + 257 * N * 4
+    assert fixed <= ws < fixed + 4096
     assert lib.dsa_sparse_mla_bwd_workspace_size(-1, N, H, K) == 0
 
 
@@ -140,10 +142,12 @@ def test_indexer_loss_entry_points_validate_and_size():
     assert sel(P, 64, 128, 4097) == _lib.DSA_ERR_UNSUPPORTED
     assert sel(ctypes.c_void_p(4104), 64, 128, 16) == _lib.DSA_ERR_INVALID_ARG
     assert sel(N, 64, 128, 16, T=0) == _lib.DSA_OK
-    # scores backward: workspace = dk rows (T*K + 1) x 256 B + pair rows T*K x 8 B + key offsets / counts
+    # scores backward: workspace = dk rows (T*K + 1) x 256 B + pair rows T*K x 8 B + key offsets
+    # + the pair ordering's counters (256 query runs + totals) x Nk
     T, Nk, K = 16384, 16384, 2048
     ws = lib.dsa_indexer_scores_bwd_workspace_size(T, Nk, K)
-    assert (T * K + 1) * 256 + T * K * 8 + (Nk + 1) * 8 + Nk * 4 <= ws < (T * K + 1) * 256 + T * K * 8 + 12 * Nk + 1024
+    fixed = (T * K + 1) * 256 + T * K * 8 + (Nk + 1) * 8 + 257 * Nk * 4
+    assert fixed <= ws < fixed + 1024
     assert lib.dsa_indexer_scores_bwd_workspace_size(-1, Nk, K) == 0
     bwd = lambda dq, ws_, nbytes: lib.dsa_indexer_scores_bwd(P, P, P, P, P, 4, 8, 64, 128, 16, 1, dq, P, P, ws_, nbytes, N)
     assert bwd(P, P, 16) == _lib.DSA_ERR_WORKSPACE

@@ -648,7 +648,7 @@ def test_sparse_decode_cfg5_full_size():
 
 
 def test_sparse_bwd_more_keys_than_the_lds_pair_order_holds():
-    """n_kv = 20000 > 16384: the pair order takes its global-atomic path (no LDS histograms)."""
+    """n_kv = 20000 > 16384: the pair order runs over two LDS key tiles."""
     print("[sparse bwd] n_kv=20000", flush=True)
     g = torch.Generator().manual_seed(20000)
     T, H, K, N = 64, 16, 256, 20000
