@@ -9,10 +9,19 @@ over T = 16384 packed tokens in 4 causal documents (cu_seqlens 0/10363/15340/155
 value = algorithmic FLOPs of the step / step time:
   sparse fwd 2176*H*N_sel + sparse bwd 5504*H*N_sel + indexer 2*Di*Hi*N_pairs
 (N_sel = sum_q min(K, visible keys) = 27,602,695; N_pairs = causally visible pairs).
-The line also carries a "decode" object for configs[4] (cfg5), whose bound is HBM: gather
-bytes of the selected cache rows / decode attention time, an "indexer_prologue" object
-(the fused producer of the indexer's inputs at the cfg3 token count, HBM-bound) and an
-"indexer_kl" object (the sparse indexer KL loss and the indexer-score backward at cfg3).
+The line also carries:
+  "roofline"          the dominant kernel by time against the roofline of its algorithmic work
+                      (MFMA flops, or HBM bytes for B5), with its counter traffic from the
+                      committed rocprofv3 summary; "backward_traffic" the whole backward's;
+  "cfg2" / "cfg4"     the prefill chain (indexer -> top-k -> forward) at configs[1] (S = 4096,
+                      bf16) and configs[3] (S = 32768, fp8 indexer against the fp8 peak);
+  "decode"            configs[4] (cfg5), HBM-bound: gathered bytes of the selected cache rows /
+                      decode attention time, plus the decode indexer and the graph-replayed step;
+  "indexer_prologue"  the fused producer of the indexer's inputs at the cfg3 token count (HBM);
+  "indexer_kl"        the sparse indexer KL loss and the indexer-score backward at cfg3;
+  "cpu_baseline"      the oracle's reference-shaped fp32 compositions timed on the host per config
+                      (cfg1 whole; cfg2/cfg3/cfg4 a few query rows, extrapolated by visible keys;
+                      cfg5 every sequence) -- a reported baseline, not the target.
 """
 from __future__ import annotations
 
