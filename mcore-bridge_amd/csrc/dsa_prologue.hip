@@ -15,10 +15,10 @@
 // fp8 input layout of the indexer scores kernel).  The three projections are plain GEMMs and
 // stay with hipBLASLt.
 //
-// One workgroup per token, one wave per 128-dim row (the token's q rows and its k row); lane l
-// holds dims 2l, 2l+1.  The token's cos/sin are computed once into LDS; each row is read once,
-// transformed in registers (RoPE operands and Hadamard butterflies move between lanes) and
-// written once: the kernel is bound by HBM (2 bytes in, 2 or 1 out per dim).
+// One workgroup per token; 16 lanes per 128-dim row (the token's q rows and its k row), 4 rows
+// per wave.  The token's cos/sin are computed once into LDS; each row is read once, transformed
+// in registers (Hadamard butterflies and RoPE partners move between lanes by DPP) and written
+// once: the kernel is bound by HBM (2 bytes in, 2 or 1 out per dim).
 #include "dsa_common.h"
 #include "dsa_kernels.h"
 
@@ -44,111 +44,266 @@ DSA_DEV uint32_t pack_e4m3x2(float a, float b) {
 
 }  // namespace
 
-// Transform of one 128-dim row held as (x0, x1) = dims (2l, 2l+1) of lane l: RoPE on dims
-// [0, 64) with the token's bf16 cos/sin from LDS, then the Hadamard rotation; returns the
-// bf16-rounded result in (x0, x1).
-DSA_DEV void rope_hadamard(float& x0, float& x1, const float* cs, const float* sn, int lane, int deinterleave,
-                           int rotary_interleaved) {
-  // output j takes u(j) and the rotate_half partner sign * u(jr), u = x or its de-interleave
-  // (u(j) = x[2j], u(32 + j) = x[2j + 1]); every lane runs the shuffles, lanes 0..31 own
-  // outputs 2l, 2l+1
-  float y[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int j = (2 * lane + e) & (kRot - 1);
-    const int jr = rotary_interleaved ? (j ^ 1) : ((j + kRot / 2) & (kRot - 1));
-    const float sg = rotary_interleaved ? ((j & 1) ? 1.f : -1.f) : (j < kRot / 2 ? -1.f : 1.f);
-    const int sj = deinterleave ? (j < kRot / 2 ? 2 * j : 2 * (j - kRot / 2) + 1) : j;
-    const int sr = deinterleave ? (jr < kRot / 2 ? 2 * jr : 2 * (jr - kRot / 2) + 1) : jr;
-    const float u = fetch(x0, x1, sj), ur = sg * fetch(x0, x1, sr);
-    y[e] = round_bf16(round_bf16(u * cs[j]) + round_bf16(ur * sn[j]));
-  }
-  if (lane < kRot / 2) {
-    x0 = y[0];
-    x1 = y[1];
-  }
-  // normalised Walsh-Hadamard transform, natural order: stride 1 inside the lane, strides
-  // 2..64 between lanes l and l ^ (stride / 2)
-  const float a = x0 + x1, b = x0 - x1;
-  x0 = a;
-  x1 = b;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float p0 = __shfl_xor(x0, m, 64), p1 = __shfl_xor(x1, m, 64);
-    const bool hi = lane & m;
-    x0 = hi ? p0 - x0 : x0 + p0;
-    x1 = hi ? p1 - x1 : x1 + p1;
-  }
-  constexpr float kNorm = 0.08838834764831845f;   // 128^-0.5
-  x0 = round_bf16(x0 * kNorm);
-  x1 = round_bf16(x1 * kNorm);
+// ---- forward: 16-lane row groups.  Lane L = lane & 15 of group g = lane >> 4 holds dims
+// 4L..4L+3 (h = 0: the RoPE dims) and 64 + 4L..+3 (h = 1) of one 128-dim row, so a wave
+// transforms 4 rows at once.  Dim index bits 0-1 and 6 are in-lane, bits 2-5 are the lane bits:
+// the Hadamard's four cross-lane butterfly stages and the half-split RoPE partner (lane ^ 8)
+// are DPP moves inside 16-lane rows, at VALU rate and with no trip through the LDS crossbar
+// (the previous one-row-per-wave layout needed 16 dependent ds_bpermute per row).
+// (all rows and banks enabled and every source lane inside the row: no lane keeps an old value)
+template <int CTRL>
+DSA_DEV float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppXor3 = 0x1B;         // quad_perm [3, 2, 1, 0]
+constexpr int kDppRowMirror = 0x140;   // lane i <- 15 - i in its row of 16
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i in its half row of 8
+
+// value of lane L ^ (1 << B) of the same 16-lane group
+template <int B>
+DSA_DEV float lane_xor(float v) {
+  if constexpr (B == 0) return dpp_mov<kDppXor1>(v);
+  else if constexpr (B == 1) return dpp_mov<kDppXor2>(v);
+  else if constexpr (B == 2) return dpp_mov<kDppXor3>(dpp_mov<kDppHalfMirror>(v));   // (i ^ 7) ^ 3
+  else return dpp_mov<kDppHalfMirror>(dpp_mov<kDppRowMirror>(v));                    // (i ^ 15) ^ 7
+}
+DSA_DEV float group_sum(float v) {
+  v += lane_xor<0>(v);
+  v += lane_xor<1>(v);
+  v += lane_xor<2>(v);
+  return v + lane_xor<3>(v);
+}
+DSA_DEV float group_max(float v) {
+  v = fmaxf(v, lane_xor<0>(v));
+  v = fmaxf(v, lane_xor<1>(v));
+  v = fmaxf(v, lane_xor<2>(v));
+  return fmaxf(v, lane_xor<3>(v));
 }
 
-// bf16 pair, or e4m3fn pair + the row's absmax scale (scale = amax / 448, 1 for a zero row;
-// x / scale clamped to +-448, RNE)
-DSA_DEV void store_row(float x0, float x1, void* out, float* scale_out, int64_t row, int lane, int fp8) {
-  if (!fp8) {
-    bf16_t* dst = reinterpret_cast<bf16_t*>(out) + row * kDi;
-    *reinterpret_cast<uint32_t*>(dst + 2 * lane) = pack_bf16x2(x0, x1);
+// Cross-lane butterfly stage on lane bit B (dim bit B + 2): x[i] + x[i + s] on the low lane,
+// x[i] - x[i + s] on the high one.
+// As p + sx * x with sx = -1 on the high lane: one fma (exact sign, one rounding) after the move.
+template <int B>
+DSA_DEV void butterfly_lanes(float (&v)[2][4], int L) {
+  const float sx = ((L >> B) & 1) ? -1.f : 1.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[h][e] = fmaf(sx, v[h][e], lane_xor<B>(v[h][e]));
+}
+
+// RoPE on the h = 0 values (bf16-exact inputs; u = the row or its de-interleave), then the
+// normalised natural-order Walsh-Hadamard transform over all 128 dims (fp32; the caller rounds
+// to bf16).
+// cs, sn: the token's bf16 cos / sin * mscale of this lane's RoPE dims 4L..4L+3.
+DSA_DEV void rope_hadamard_group(float (&v)[2][4], const float (&cs)[4], const float (&sn)[4], int lane,
+                                 int deinterleave, int rotary_interleaved) {
+  const int L = lane & 15;
+  float u[4];
+  if (deinterleave) {
+    // u(j) = x[2j] (j < 32), x[2(j - 32) + 1] (j >= 32): the 4 values of lane L come from the
+    // even (L < 8) or odd (L >= 8) halves of the two words of lanes 2 (L & 7) and 2 (L & 7) + 1
+    const int w0 = (int)pack_bf16x2(v[0][0], v[0][1]), w1 = (int)pack_bf16x2(v[0][2], v[0][3]);
+    const int src = 4 * ((lane & 48) + 2 * (L & 7));
+    const uint32_t a0 = __builtin_amdgcn_ds_bpermute(src, w0), a1 = __builtin_amdgcn_ds_bpermute(src, w1);
+    const uint32_t b0 = __builtin_amdgcn_ds_bpermute(src + 4, w0), b1 = __builtin_amdgcn_ds_bpermute(src + 4, w1);
+    const bool odd = L >= 8;
+    u[0] = odd ? bf16_hi(a0) : bf16_lo(a0);
+    u[1] = odd ? bf16_hi(a1) : bf16_lo(a1);
+    u[2] = odd ? bf16_hi(b0) : bf16_lo(b0);
+    u[3] = odd ? bf16_hi(b1) : bf16_lo(b1);
   } else {
-    const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-    const float scale = amax > 0.f ? amax / 448.f : 1.f;
-    const float q0 = fminf(fmaxf(x0 / scale, -448.f), 448.f), q1 = fminf(fmaxf(x1 / scale, -448.f), 448.f);
-    uint8_t* dst = reinterpret_cast<uint8_t*>(out) + row * kDi;
-    *reinterpret_cast<uint16_t*>(dst + 2 * lane) = (uint16_t)pack_e4m3x2(q0, q1);
-    if (lane == 0) scale_out[row] = scale;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) u[e] = v[0][e];
   }
+  // rotate_half partner u(jr) and the sign of dim j = 4L + e
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float ur, sg;
+    if (rotary_interleaved) {
+      ur = u[e ^ 1];
+      sg = (e & 1) ? 1.f : -1.f;
+    } else {
+      ur = lane_xor<3>(u[e]);
+      sg = L < 8 ? -1.f : 1.f;
+    }
+    v[0][e] = round_bf16(round_bf16(u[e] * cs[e]) + round_bf16(sg * ur * sn[e]));
+  }
+  // Hadamard: in-lane bits 0, 1 and 6, then lane bits 0-3
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float a = v[h][0] + v[h][1], b = v[h][0] - v[h][1];
+    const float c = v[h][2] + v[h][3], d = v[h][2] - v[h][3];
+    v[h][0] = a + c;
+    v[h][1] = b + d;
+    v[h][2] = a - c;
+    v[h][3] = b - d;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = v[0][e] + v[1][e], b = v[0][e] - v[1][e];
+    v[0][e] = a;
+    v[1][e] = b;
+  }
+  butterfly_lanes<0>(v, L);
+  butterfly_lanes<1>(v, L);
+  butterfly_lanes<2>(v, L);
+  butterfly_lanes<3>(v, L);
+  constexpr float kNorm = 0.08838834764831845f;   // 128^-0.5
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[h][e] *= kNorm;
 }
 
-// One workgroup per token: its 64 cos/sin values are computed once (wave 0) into LDS, then the
-// four waves share the token's n_heads q rows and its k row (LayerNorm first; that wave also
-// scales the head weights).
-__global__ __launch_bounds__(256) void indexer_prologue_kernel(PrologueParams p) {
-  __shared__ float cs[kRot], sn[kRot];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x;
-  if (wave == 0) {
-    const float f = p.freqs[(int64_t)t * p.freqs_stride_t + lane];
-    cs[lane] = round_bf16(cosf(f) * p.mscale);
-    sn[lane] = round_bf16(sinf(f) * p.mscale);
-  }
-  __syncthreads();
-  // rows r = 0 .. n_heads: q head r, or (r = n_heads) the k row; wave w takes r = w, w + 4, ..
-  // (at most kRowsPerWave), all of its loads issued before the first row is transformed
-  constexpr int kRowsPerWave = (64 + 1 + 3) / 4;
-  uint32_t pr[kRowsPerWave];
+// One row of a group (fp32 values, rounded to bf16 here): bf16, or e4m3fn of the bf16 values
+// + the row's absmax scale (scale = amax / 448, 1 for a
+// zero row; x / scale clamped to +-448, RNE).  Every lane of the wave takes part (group
+// reductions); only lanes of a valid row store.
+DSA_DEV void store_group_row(float (&v)[2][4], void* out, float* scale_out, int64_t row, bool valid, int L,
+                             int fp8) {
+  if (!fp8) {   // the packing conversion is the bf16 rounding (RNE)
+    if (!valid) return;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<bf16_t*>(out) + row * kDi);
 #pragma unroll
-  for (int i = 0; i < kRowsPerWave; ++i) {
-    const int r = wave + 4 * i;
-    pr[i] = 0;
-    if (r <= p.n_heads) {
+    for (int h = 0; h < 2; ++h) {
+      dst[32 * h + 2 * L] = pack_bf16x2(v[h][0], v[h][1]);
+      dst[32 * h + 2 * L + 1] = pack_bf16x2(v[h][2], v[h][3]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      const uint32_t w = pack_bf16x2(v[h][e], v[h][e + 1]);
+      v[h][e] = bf16_lo(w);
+      v[h][e + 1] = bf16_hi(w);
+    }
+  float m = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[h][e]));
+  const float amax = group_max(m);
+  if (!valid) return;
+  const float scale = amax > 0.f ? amax / 448.f : 1.f;
+  // x / scale correctly rounded from the correctly rounded reciprocal plus one exact-remainder
+  // correction (Markstein): the remainder x - q0 * scale is exact in an fma, and
+  // q0 + rem * (1 / scale) rounds to the nearest quotient.  Quotients in the fp32 subnormal
+  // range may differ by an ulp; they are far below e4m3's smallest subnormal (2^-9) and encode 0.
+  const float rcp = 1.f / scale;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out) + row * kDi);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float q0 = v[h][e] * rcp;
+      const float qc = fmaf(fmaf(-q0, scale, v[h][e]), rcp, q0);
+      q[e] = fminf(fmaxf(qc, -448.f), 448.f);
+    }
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    dst[16 * h + L] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)lo, true);
+  }
+  if (L == 0) scale_out[row] = scale;
+}
+
+// One workgroup per token: every wave issues the loads of its rows, then wave 0 computes the
+// token's 64 cos/sin values into LDS and scales the head weights; the token's n_heads q rows
+// and its k row (row n_heads, LayerNorm first) are taken 4 at a time, wave w taking row quads
+// w, w + 4, ..
+__global__ __launch_bounds__(256) void indexer_prologue_kernel(PrologueParams p) {
+  __shared__ __attribute__((aligned(16))) float cs_s[kRot], sn_s[kRot];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, L = lane & 15;
+  const int t = blockIdx.x;
+  // all loads of this wave's rows first: 4 words per lane and row (dims 4L.., 64 + 4L..)
+  constexpr int kMaxQuads = (64 + 1 + 15) / 16;   // row quads per wave
+  const int n_rows = p.n_heads + 1, n_quads = (n_rows + 3) / 4;
+  uint32_t w[kMaxQuads][4];
+#pragma unroll
+  for (int i = 0; i < kMaxQuads; ++i) {
+    const int quad = wave + 4 * i, r = 4 * quad + g;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[i][k] = 0;
+    if (quad < n_quads && r < n_rows) {
       const bf16_t* src = r == p.n_heads ? p.k_lin + (int64_t)t * p.k_stride_t
                                          : p.q_lin + (int64_t)t * p.q_stride_t + (int64_t)r * kDi;
-      pr[i] = *reinterpret_cast<const uint32_t*>(src + 2 * lane);
+      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        w[i][2 * h] = s32[32 * h + 2 * L];
+        w[i][2 * h + 1] = s32[32 * h + 2 * L + 1];
+      }
+    }
+  }
+  if (wave == 0) {   // under the row loads: the token's cos / sin and head weights
+    const float f = p.freqs[(int64_t)t * p.freqs_stride_t + lane];
+    cs_s[lane] = round_bf16(cosf(f) * p.mscale);
+    sn_s[lane] = round_bf16(sinf(f) * p.mscale);
+    if (lane < p.n_heads) {   // head weights: w * Hi^-0.5, then * Di^-0.5, each rounded to bf16
+      const float w = (float)p.w_lin[(int64_t)t * p.w_stride_t + lane];
+      p.w_out[(int64_t)t * p.n_heads + lane] = round_bf16(round_bf16(w * p.w_scale_heads) * p.w_scale_softmax);
+    }
+  }
+  __syncthreads();
+  float cs[4], sn[4];
+  {
+    const f32x4 c4 = *reinterpret_cast<const f32x4*>(cs_s + 4 * L), s4 = *reinterpret_cast<const f32x4*>(sn_s + 4 * L);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cs[e] = c4[e];
+      sn[e] = s4[e];
     }
   }
 #pragma unroll
-  for (int i = 0; i < kRowsPerWave; ++i) {
-    const int r = wave + 4 * i;
-    if (r > p.n_heads) break;
-    const bool is_k = r == p.n_heads;
-    float x0 = bf16_lo(pr[i]), x1 = bf16_hi(pr[i]);
-    if (is_k) {
-      // k_norm: fp32 LayerNorm over the row, output rounded to bf16
-      const float mean = wave_sum(x0 + x1) * (1.f / kDi);
-      const float d0 = x0 - mean, d1 = x1 - mean;
-      const float rstd = 1.f / sqrtf(wave_sum(d0 * d0 + d1 * d1) * (1.f / kDi) + p.eps);
-      x0 = round_bf16(d0 * rstd * p.ln_w[2 * lane] + p.ln_b[2 * lane]);
-      x1 = round_bf16(d1 * rstd * p.ln_w[2 * lane + 1] + p.ln_b[2 * lane + 1]);
-      // head weights: w * Hi^-0.5, then * Di^-0.5, each rounded to bf16
-      if (lane < p.n_heads) {
-        const float w = (float)p.w_lin[(int64_t)t * p.w_stride_t + lane];
-        p.w_out[(int64_t)t * p.n_heads + lane] = round_bf16(round_bf16(w * p.w_scale_heads) * p.w_scale_softmax);
+  for (int i = 0; i < kMaxQuads; ++i) {
+    const int quad = wave + 4 * i;
+    if (quad >= n_quads) break;
+    const int r = 4 * quad + g;
+    const bool valid = r < n_rows, is_k = r == p.n_heads;
+    float v[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v[h][0] = bf16_lo(w[i][2 * h]);
+      v[h][1] = bf16_hi(w[i][2 * h]);
+      v[h][2] = bf16_lo(w[i][2 * h + 1]);
+      v[h][3] = bf16_hi(w[i][2 * h + 1]);
+    }
+    if (quad == p.n_heads / 4) {
+      // the quad with the k row: k_norm (fp32 LayerNorm over the row, output rounded to bf16),
+      // computed by every group, kept by the k row's
+      float s = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s += v[h][e];
+      const float mean = group_sum(s) * (1.f / kDi);
+      float d[2][4], s2 = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          d[h][e] = v[h][e] - mean;
+          s2 += d[h][e] * d[h][e];
+        }
+      const float rstd = 1.f / sqrtf(group_sum(s2) * (1.f / kDi) + p.eps);
+      if (is_k) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int dim = 64 * h + 4 * L + e;
+            v[h][e] = round_bf16(d[h][e] * rstd * p.ln_w[dim] + p.ln_b[dim]);
+          }
       }
     }
-    rope_hadamard(x0, x1, cs, sn, lane, p.deinterleave, p.rotary_interleaved);
-    if (is_k) store_row(x0, x1, p.k_out, p.k_scale, t, lane, p.out_fp8);
-    else store_row(x0, x1, p.q_out, p.q_scale, (int64_t)t * p.n_heads + r, lane, p.out_fp8);
+    rope_hadamard_group(v, cs, sn, lane, p.deinterleave, p.rotary_interleaved);
+    if (is_k) store_group_row(v, p.k_out, p.k_scale, t, valid, L, p.out_fp8);
+    else store_group_row(v, p.q_out, p.q_scale, (int64_t)t * p.n_heads + r, valid, L, p.out_fp8);
   }
 }
 
