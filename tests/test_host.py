@@ -153,3 +153,30 @@ def test_v4_mirror_parameters_are_the_bridge_keys():
     hca = v4.DSv4HybridAttention("heavily_compressed_attention", 64, 16, 32, o_groups=4, o_lora_rank=16, device="cpu")
     assert "core_attention.indexer.linear_wq_b.weight" not in hca.state_dict()
     assert hca.state_dict()["core_attention.compressor.ape"].shape == (128, 512)
+
+
+def test_e4m3_quotient_from_corrected_reciprocal():
+    """The fp8 prologue quantises x / scale as fma(fma(-q0, scale, x), r, q0) with r = RN(1 / scale)
+    and q0 = RN(x * r) (one exact-remainder correction).  Over every finite bf16 x with
+    |x| <= amax and a spread of row maxima amax (scale = RN(amax / 448)), the result equals the
+    correctly rounded quotient wherever |x| >= 2^-100 (or x = 0) and the quotient is a normal fp32
+    number.  Below that the remainder (~ x * 2^-24) underflows fp32's subnormal range; values
+    that small are far outside any activation range.  float64 emulates the fp32 fmas: the product q0 * scale is
+    exact, the remainder is exact by Sterbenz."""
+    import numpy as np
+    rng = np.random.default_rng(1)
+    xs = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    xs = xs[np.isfinite(xs)]
+    tiny = np.float32(2.0 ** -126)
+    for amax in np.abs(xs[rng.integers(len(xs), size=60)]):
+        if not (1e-30 < amax < 1e30):
+            continue
+        s = np.float32(np.float64(amax) / 448.0)
+        x = xs[np.abs(xs) <= amax].astype(np.float64)
+        exact = (x / np.float64(s)).astype(np.float32)
+        r = np.float32(1.0 / np.float64(s))
+        q0 = (x * np.float64(r)).astype(np.float32)
+        rem = (x - q0.astype(np.float64) * np.float64(s)).astype(np.float32)
+        q = (rem.astype(np.float64) * np.float64(r) + q0.astype(np.float64)).astype(np.float32)
+        normal = (np.abs(exact) >= tiny) & ((x == 0) | (np.abs(x) >= 2.0 ** -100))
+        assert np.array_equal(q[normal], exact[normal]), float(amax)
