@@ -192,8 +192,8 @@ DSA_DEV void store_group_row(float (&v)[2][4], void* out, float* scale_out, int6
   const float scale = amax > 0.f ? amax / 448.f : 1.f;
   // x / scale correctly rounded from the correctly rounded reciprocal plus one exact-remainder
   // correction (Markstein): the remainder x - q0 * scale is exact in an fma, and
-  // q0 + rem * (1 / scale) rounds to the nearest quotient.  Quotients in the fp32 subnormal
-  // range may differ by an ulp; they are far below e4m3's smallest subnormal (2^-9) and encode 0.
+  // q0 + rem * (1 / scale) rounds to the nearest quotient -- for |x| >= 2^-100 and normal
+  // quotients; below that the remainder underflows and the result may be an ulp off.
   const float rcp = 1.f / scale;
   uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out) + row * kDi);
 #pragma unroll
