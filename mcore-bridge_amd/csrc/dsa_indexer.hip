@@ -16,8 +16,9 @@
 // per key, shared by the 4 waves of a workgroup through L1/L2); C[heads x 32 keys] is reduced
 // over heads in registers: each lane holds 16 heads of one key, so ReLU * w and the head sum
 // are lane-local plus one exchange with the lane 32 apart.
-// At most 512 bf16 queries of 128-dim rows (decode) K1 runs as indexer_scores_rows_kernel instead:
-// one query per workgroup, key rows staged in LDS by contiguous LDS-direct copies.
+// At most 512 queries of 128-dim rows (decode) K1 runs as indexer_scores_rows_kernel (bf16) or
+// indexer_scores_rows_fp8_kernel instead: one query per workgroup, key rows staged in LDS by
+// contiguous LDS-direct copies.
 // fp8 (OCP e4m3fn): gfx950's 32x32x64 fp8 MFMA (twice the bf16 rate per instruction), through
 // the same LDS ring as bf16 when a workgroup's queries share a document;
 // I = k_scale[s] * sum_h (w * q_scale)[t,h] * relu(q8 . k8) -- valid because ReLU is
@@ -37,7 +38,7 @@ namespace {
 constexpr int kIdxChunkMax = 2048;  // keys per wave work item (prefill)
 constexpr int kIdxChunkMin = 256;
 constexpr int kIdxWaveTarget = 8192;   // shrink the chunk until this many work items exist
-constexpr int kRowsMode = 512;      // at most this many queries (bf16, 128-dim): indexer_scores_rows_kernel
+constexpr int kRowsMode = 512;      // at most this many queries (128-dim rows): the rows kernels
 constexpr int kMaxHi = 64;          // indexer heads handled by the register tiling
 }  // namespace
 
@@ -415,6 +416,122 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
   }
 }
 
+// Few long rows, fp8 (decode; e4m3fn, 128-dim rows): one query per workgroup as in
+// indexer_scores_rows_kernel, with 128-byte key rows.  A 32-key block is 4 KB of rows (4
+// contiguous 1 KB LDS-direct copies of 8 rows per wave, row r's 16-byte unit u at slot u ^ (r & 7))
+// plus its 32 key scales (one 4-byte LDS-direct copy per lane: 256 B, lanes >= 32 repeat the
+// last key), through a per-wave ring of kRowsFp8Stages blocks (kRowsFp8Stages - 1 in flight while
+// one is computed; 2, 3, 4 and 6 stages and 512- or 1024-key chunks all measured within 10 % at
+// cfg5: ~110 us for the 360 MB of fp8 keys and scales, 3.3 TB/s, with the L1's pending-miss
+// stalls at ~40 % of the cycles).  The query's fp8 A fragments sit in registers
+// (32 VGPRs); two 32x32x64 fp8 MFMAs per row tile and block;
+// I = k_scale[s] * sum_h (w q_scale)[t,h] relu(q8 . k8).
+constexpr int kRowsFp8Stages = 3;
+constexpr int kRowsFp8Block = 32 * 128 + 256;   // rows + scales of one 32-key block
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31]
+DSA_DEV void wait_vmcnt_upto31(int n) {
+  switch (n) {
+#define DSA_WAIT_CASE(i) case i: wait_vmcnt<i>(); break;
+    DSA_WAIT_CASE(0) DSA_WAIT_CASE(1) DSA_WAIT_CASE(2) DSA_WAIT_CASE(3) DSA_WAIT_CASE(4) DSA_WAIT_CASE(5)
+    DSA_WAIT_CASE(6) DSA_WAIT_CASE(7) DSA_WAIT_CASE(8) DSA_WAIT_CASE(9) DSA_WAIT_CASE(10) DSA_WAIT_CASE(11)
+    DSA_WAIT_CASE(12) DSA_WAIT_CASE(13) DSA_WAIT_CASE(14) DSA_WAIT_CASE(15) DSA_WAIT_CASE(16)
+    DSA_WAIT_CASE(17) DSA_WAIT_CASE(18) DSA_WAIT_CASE(19) DSA_WAIT_CASE(20) DSA_WAIT_CASE(21)
+    DSA_WAIT_CASE(22) DSA_WAIT_CASE(23) DSA_WAIT_CASE(24) DSA_WAIT_CASE(25) DSA_WAIT_CASE(26)
+    DSA_WAIT_CASE(27) DSA_WAIT_CASE(28) DSA_WAIT_CASE(29) DSA_WAIT_CASE(30) DSA_WAIT_CASE(31)
+#undef DSA_WAIT_CASE
+    default: wait_vmcnt0(); break;
+  }
+}
+
+__global__ __launch_bounds__(256) void indexer_scores_rows_fp8_kernel(IndexerParams p) {
+  constexpr int RB = 128, NS = kRowsFp8Stages, CPB = 5;   // copies per block: 4 row copies + scales
+  __shared__ __attribute__((aligned(256))) char ring[4][NS][kRowsFp8Block];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.x;
+  const int hb = lane >> 5, hl = lane & 31;
+  const int c0 = ((int)blockIdx.y * 4 + wave) * p.chunk;
+  const int len = p.row_len[t];
+  if (c0 >= len) return;   // nothing below is shared between waves: no barrier
+  const int c1 = min(len, c0 + p.chunk);
+  const int base = p.row_base[t];
+  const char* kbase = reinterpret_cast<const char*>(p.k);
+  const uint32_t ring0 = lds_addr(ring[wave][0]);
+  // copy r < 4 of a block moves keys 8r .. 8r+7 -- 1 KB contiguous in memory: lane l fills slot
+  // l & 7 of key 8r + l / 8 with that key's unit (l & 7) ^ (key & 7); copy 4 the key scales
+  auto gather = [&](int blk) {
+    const int k0 = c0 + 32 * blk;
+    const uint32_t dst = ring0 + (uint32_t)(blk % NS) * kRowsFp8Block;
+    const int kk0 = lane >> 3;
+    const uint32_t sl = lane & 7;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kk = 8 * r + kk0;
+      const int row = base + min(k0 + kk, c1 - 1);
+      async_copy16_unordered(kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7)), dst + 1024u * r);
+    }
+    async_copy4_unordered(p.k_scale + base + min(k0 + hl, c1 - 1), dst + 4096u);
+  };
+  // the first blocks' copies go out before the query's loads, so the two latencies overlap
+  const int nb = (c1 - c0 + 31) / 32;
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < nb) gather(i);
+  const uint8_t* q8 = reinterpret_cast<const uint8_t*>(p.q) + (int64_t)t * p.n_heads * RB;
+  i32x8 qa[2][2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int h = 32 * mt + hl;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const uint8_t* src = q8 + (int64_t)(h < p.n_heads ? h : 0) * RB + 64 * st + 32 * hb;
+      const u32x4 lo = gload16(src), hi = gload16(src + 16);
+      qa[mt][st] = h < p.n_heads ? cat16(lo, hi) : i32x8{};
+    }
+  }
+  float wr[2][16];   // (w * q_scale) of the accumulator rows: heads 32 mt + (i/4)*8 + 4 hb + i%4
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int h = 32 * mt + (i >> 2) * 8 + 4 * hb + (i & 3);
+      wr[mt][i] = h < p.n_heads ? p.w[(int64_t)t * p.n_heads + h] * p.q_scale[(int64_t)t * p.n_heads + h] : 0.f;
+    }
+  // every load so far retired (the compiler's and the first copies): the waits below count
+  // only the ring's copies and the score stores
+  wait_vmcnt0();
+  for (int it = 0; it < nb; ++it) {
+    const int k0 = c0 + 32 * it;
+    const int j = k0 + hl;
+    // issued after block it's copies: the copies of min(NS - 2, nb - 1 - it) later blocks and
+    // the score stores of the min(it, NS - 1) blocks before it
+    wait_vmcnt_upto31(CPB * min(NS - 2, nb - 1 - it) + min(it, NS - 1));
+    asm volatile("" ::: "memory");
+    if (it + NS - 1 < nb) gather(it + NS - 1);
+    const uint32_t tb = ring0 + (uint32_t)(it % NS) * kRowsFp8Block;
+    const char* row = lds_ptr(tb + hl * RB);
+    i32x8 kb[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int u0 = 4 * st + 2 * hb;
+      kb[st] = cat16(lds_load16(row + 16 * (u0 ^ (hl & 7))), lds_load16(row + 16 * ((u0 + 1) ^ (hl & 7))));
+    }
+    const float ksc = *reinterpret_cast<const float*>(lds_ptr(tb + 4096u + 4u * hl));
+    f32x16 c0a = f32x16{}, c1a = f32x16{};
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      c0a = mfma32x32x64_fp8(qa[0][st], kb[st], c0a);
+      c1a = mfma32x32x64_fp8(qa[1][st], kb[st], c1a);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += wr[0][i] * fmaxf(c0a[i], 0.f) + wr[1][i] * fmaxf(c1a[i], 0.f);
+    acc = xor32_sum(acc);
+    if (hb == 0 && j < c1) p.scores[(int64_t)t * p.pitch + j] = acc * ksc;
+  }
+}
+
 // Fill the masked tail [row_len, pitch) of each score row with -inf (only when the caller
 // wants the reference's dense [S, S] index_scores).
 __global__ void scores_fill_masked_kernel(float* scores, int64_t pitch, const int32_t* row_len, int rows) {
@@ -432,12 +549,14 @@ int launch_indexer_scores(const IndexerParams& p_in, hipStream_t stream) {
     while (p.chunk > kIdxChunkMin && (int64_t)p.total_q * ((max_len + p.chunk - 1) / p.chunk) < kIdxWaveTarget)
       p.chunk >>= 1;
   }
+  const bool rows_mode = p.head_dim == 128 && p.total_q <= kRowsMode;
   if (p.chunk < 32 || p.chunk % 32 != 0) return -1;
   const dim3 grid((p.total_q + 3) / 4, (unsigned)((max_len + p.chunk - 1) / p.chunk));
   if (grid.y == 0) return 0;
-  if (!p.fp8 && p.head_dim == 128 && p.total_q <= kRowsMode) {
+  if (rows_mode) {
     const dim3 rgrid(p.total_q, (grid.y + 3) / 4);
-    hipLaunchKernelGGL(indexer_scores_rows_kernel, rgrid, dim3(256), 0, stream, p);
+    if (p.fp8) hipLaunchKernelGGL(indexer_scores_rows_fp8_kernel, rgrid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(indexer_scores_rows_kernel, rgrid, dim3(256), 0, stream, p);
   } else if (p.fp8)
     hipLaunchKernelGGL(indexer_scores_kernel<true>, grid, dim3(256), 0, stream, p);
   else

@@ -553,6 +553,31 @@ def test_decode_indexer_topk(fp8):
     assert (idx[4, 700:] == -1).all() and (idx[4, :700] == torch.arange(700) + int(cu[4])).all()
 
 
+def test_decode_fp8_rows_kernel_partial_heads_and_chunks():
+    """fp8 decode rows kernel with 20 indexer heads (zero-padded A rows), rows shorter than one
+    32-key block and a row spanning several wave chunks, against the float64 oracle."""
+    lens = [5, 777, 4100, 31, 9000]
+    print(f"[decode fp8 rows] Hi=20 lens={lens}", flush=True)
+    g = torch.Generator().manual_seed(77)
+    Hi, N = 20, sum(lens)
+    q8, qs = O.quantize_e4m3_rows(torch.randn(len(lens), Hi, 128, generator=g))
+    k8, ks = O.quantize_e4m3_rows(torch.randn(N, 128, generator=g))
+    w = torch.randn(len(lens), Hi, generator=g)
+    cu = _cu(lens)
+    idx, sc = ops.decode_indexer_topk(q8.to(DEV), k8.to(DEV), w.to(DEV), 64, cu.to(DEV), max(lens), qs.to(DEV),
+                                      ks.to(DEV), return_scores=True)
+    ref = O.decode_indexer_scores(q8.float(), k8.float(), w, cu[:-1], torch.tensor(lens), q_scale=qs, k_scale=ks)
+    sc = sc.cpu().double()
+    for b, L in enumerate(lens):
+        torch.testing.assert_close(sc[b, :L], ref[b, :L], rtol=2e-3, atol=2e-3)
+    masked = sc.clone()
+    for b, L in enumerate(lens):
+        masked[b, L:] = float("-inf")
+    off = cu[:-1].long()[:, None]
+    want = O.topk_indices(masked, 64)
+    assert torch.equal(idx.cpu().long(), torch.where(want >= 0, want + off, want))
+
+
 @pytest.mark.parametrize("lens,H,K", [([3000, 700, 5000, 1200, 64], 128, 2048), ([4096], 128, 2048),
                                       ([900, 333, 2100], 16, 512), ([500, 600], 64, 100)])
 def test_sparse_decode(lens, H, K):
