@@ -184,13 +184,24 @@ int dsa_sparse_mla_decode_noalloc(const void* q, const void* kv_cache, const int
                                   int n_heads, int d_qk, int d_v, int topk, float sm_scale, void* out, float* lse,
                                   void* stream);
 
-/* Workspace bytes for dsa_sparse_mla_bwd. */
+/* Workspace bytes for dsa_sparse_mla_bwd in one pass over all total_q query rows (the staged P
+ * and dS tiles, ~4.5 KB per selected (query, key) pair of G rows and pair rows, key counters). */
 size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int topk);
+
+/* Workspace bytes for dsa_sparse_mla_bwd run in passes of chunk_q query rows (rounded up to a
+ * multiple of 256): a bounded workspace for long sequences.  No reference counterpart (torch
+ * autograd has no workspace); for callers that must cap the backward's scratch memory. */
+size_t dsa_sparse_mla_bwd_workspace_size_chunked(int total_q, int n_kv, int n_heads, int topk, int chunk_q);
 
 /* Sparse MLA backward (autograd of dsa_sparse_mla_fwd; replaces torch autograd through the
  * un-fused attention called at multi_latent_attention.py:262-270).  Writes dq [T, H, 576] bf16
  * and dkv [n_kv, 576] fp32 (every row written; rows no query selected are zero).
- * n_heads <= 128 and a multiple of 16. */
+ * n_heads <= 128 and a multiple of 16.  With a workspace of at least
+ * dsa_sparse_mla_bwd_workspace_size() it runs in one pass; with a smaller one (at least the
+ * chunked size of 256 rows) it runs in passes of the most multiples of 256 query rows that fit,
+ * in query order, adding each pass's dkv into the previous ones.  dkv is the same bit for bit
+ * from run to run for a given workspace size (the per-key sums run in ascending query order);
+ * different pass sizes may differ in the last fp32 bits. */
 int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const void* out,
                        const void* dout, const float* lse, int total_q, int n_kv, int n_heads,
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
@@ -221,7 +232,9 @@ int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, con
 /* The same target from the workspace of a dsa_sparse_mla_bwd call that just ran on the same q,
  * kv, idx, lse (same total_q, n_kv, n_heads, topk, causal; no other call on that workspace in
  * between): its first stage recomputes P for every head and stages it in bf16, so the target is
- * the head mean of those tiles and no S product is recomputed.  Stream-ordered after that call. */
+ * the head mean of those tiles and no S product is recomputed.  Stream-ordered after that call.
+ * Needs that call's one-pass workspace (dsa_sparse_mla_bwd_workspace_size() bytes): a chunked
+ * backward keeps only its last pass's tiles (DSA_ERR_WORKSPACE). */
 int dsa_indexer_kl_target_from_bwd(const void* bwd_workspace, size_t bwd_workspace_bytes, const int32_t* idx,
                                    int total_q, int n_kv, int n_heads, int topk, int causal, float* target,
                                    void* stream);

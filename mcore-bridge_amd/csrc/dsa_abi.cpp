@@ -39,6 +39,20 @@ BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
   return L;
 }
 
+// Query rows per pass of the sparse backward for a workspace of `bytes`: total_q when the whole
+// layout fits, else the most whole units of kBwdChunkUnit rows whose layout fits (0: none).
+constexpr int kBwdChunkUnit = 256;
+int bwd_chunk_rows(int total_q, int n_kv, int n_heads, int topk, size_t bytes) {
+  if (bwd_layout(total_q, n_kv, n_heads, topk).total <= bytes) return total_q;
+  int lo = 0, hi = total_q / kBwdChunkUnit;   // units; layouts grow with the rows
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (bwd_layout(mid * kBwdChunkUnit, n_kv, n_heads, topk).total <= bytes) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo * kBwdChunkUnit;
+}
+
 struct IdxBwdLayout {
   size_t g_stage, pair_pos, offsets, counts, total;
 };
@@ -328,6 +342,12 @@ size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int
   return bwd_layout(total_q, n_kv, n_heads, topk).total;
 }
 
+size_t dsa_sparse_mla_bwd_workspace_size_chunked(int total_q, int n_kv, int n_heads, int topk, int chunk_q) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || chunk_q < 1) return 0;
+  const int rows = std::min(total_q, (chunk_q + kBwdChunkUnit - 1) / kBwdChunkUnit * kBwdChunkUnit);
+  return bwd_layout(rows, n_kv, n_heads, topk).total;
+}
+
 int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
                        const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
                        float sm_scale, int causal, void* dq, float* dkv, void* workspace,
@@ -346,26 +366,23 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
   if (!q || !kv || !idx || !out || !dout || !lse || !dq || !dkv) return DSA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(dout) || !aligned16(dq) || !aligned16(dkv))
     return DSA_ERR_INVALID_ARG;
-  const BwdLayout L = bwd_layout(total_q, n_kv, n_heads, topk);
-  if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  // query rows per pass: all of them when the whole layout fits the workspace, else the most
+  // whole units of kBwdChunkUnit rows whose layout fits (the timed variant needs one pass)
+  const int chunk = bwd_chunk_rows(total_q, n_kv, n_heads, topk, workspace_bytes);
+  if (!workspace || chunk == 0 || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  if (stage_events && chunk < total_q) return DSA_ERR_WORKSPACE;
+  const BwdLayout L = bwd_layout(chunk, n_kv, n_heads, topk);
   char* ws = static_cast<char*>(workspace);
   dsa::SparseBwdParams p{};
-  p.q = static_cast<const dsa::bf16_t*>(q);
   p.kv = static_cast<const dsa::bf16_t*>(kv);
-  p.idx = idx;
-  p.out = static_cast<const dsa::bf16_t*>(out);
-  p.dout = static_cast<const dsa::bf16_t*>(dout);
-  p.lse = lse;
-  p.dq = static_cast<dsa::bf16_t*>(dq);
   p.dkv = dkv;
   p.p_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.p_stage);
   p.ds_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.ds_stage);
   p.g_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.g_stage);
-  p.g_sink_row = (int64_t)total_q * topk;
   p.pair_pos = reinterpret_cast<int64_t*>(ws + L.pair_pos);
   p.csr_offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
   p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);
-  p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.topk_pad = topk_pad(topk);
+  p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.topk_pad = topk_pad(topk);
   p.causal = causal ? 1 : 0;
   p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
   p.out_stride_t = (int64_t)n_heads * kDv; p.dout_stride_t = (int64_t)n_heads * kDv;
@@ -376,7 +393,24 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
   if (stage_events)
     for (int i = 0; i < 6; ++i)
       if (!stage_events[i]) return DSA_ERR_INVALID_ARG;
-  return dsa::launch_sparse_mla_bwd(p, as_stream(stream), reinterpret_cast<hipEvent_t const*>(stage_events));
+  // passes in query order: the first writes dkv, the later ones add to it (a fixed order, so the
+  // result is the same from run to run for a given workspace size)
+  for (int c0 = 0; c0 < total_q; c0 += chunk) {
+    const int rows = std::min(chunk, total_q - c0);
+    p.q = static_cast<const dsa::bf16_t*>(q) + (int64_t)c0 * p.q_stride_t;
+    p.idx = idx + (int64_t)c0 * topk;
+    p.out = static_cast<const dsa::bf16_t*>(out) + (int64_t)c0 * p.out_stride_t;
+    p.dout = static_cast<const dsa::bf16_t*>(dout) + (int64_t)c0 * p.dout_stride_t;
+    p.lse = lse + (int64_t)c0 * n_heads;
+    p.dq = static_cast<dsa::bf16_t*>(dq) + (int64_t)c0 * p.dq_stride_t;
+    p.total_q = rows;
+    p.q_offset = c0;
+    p.dkv_accumulate = c0 > 0 ? 1 : 0;
+    p.g_sink_row = (int64_t)rows * topk;
+    const int rc = dsa::launch_sparse_mla_bwd(p, as_stream(stream), reinterpret_cast<hipEvent_t const*>(stage_events));
+    if (rc != 0) return rc;
+  }
+  return DSA_OK;
 }
 
 int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, const float* lse, int total_q,

@@ -459,7 +459,7 @@ int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream) {
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream) {
   if (p.topk > kMaxTopkIdx || p.n_heads > kHi) return -2;
   if (p.g_sink_row >= INT32_MAX) return -2;   // staging rows are kept in 32 bits
-  if (p.n_k > 0) launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_k, p.causal, p.csr_counts,
+  if (p.n_k > 0) launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_k, p.causal, 0, p.csr_counts,
                                  p.csr_offsets, p.pair_pos, stream);
   if (p.total_q > 0)
     hipLaunchKernelGGL(indexer_sel_kernel<true>, dim3(xcd_grid(p.total_q)), dim3(256), 0, stream, p);

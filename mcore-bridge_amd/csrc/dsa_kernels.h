@@ -41,6 +41,8 @@ struct SparseBwdParams {
   int64_t* csr_offsets; // [n_kv + 1]
   int32_t* csr_counts;  // [csr_count_entries(total_q, n_kv)] scratch of the pair ordering
   int total_q, n_heads, n_kv, topk, topk_pad, causal;
+  int q_offset;         // position of row 0 (the causal test is key <= q_offset + row): a query chunk
+  int dkv_accumulate;   // 1: B5 adds into dkv (the later chunks of a chunked backward)
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, dout_stride_t, lse_stride_t, dq_stride_t, dkv_stride;
   float scale, scale_log2;
 };
@@ -176,8 +178,9 @@ int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
 int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream);
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream);
-// Key-major order of the selected (query, slot) pairs, ascending in query inside each key:
-// csr_offsets [n_kv + 1] and the row of every pair, pair_pos [total_q, topk] (-1 = not
+// Key-major order of the selected (query, slot) pairs, ascending in query inside each key
+// (row t is at position t_offset + t for the causal test): csr_offsets [n_kv + 1] and the row of
+// every pair, pair_pos [total_q, topk] (-1 = not
 // selected); csr_counts is scratch of csr_count_entries() int32.  topk <= 4096.
 // The query rows are cut into csr_groups() runs (at most 256, at most 2^24 run x key counters).
 inline int csr_groups(int total_q, int n_kv) {
@@ -190,7 +193,7 @@ inline size_t csr_count_entries(int total_q, int n_kv) {
   return (size_t)(csr_groups(total_q, n_kv) + 1) * (size_t)(n_kv > 0 ? n_kv : 0);
 }
 void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
-                     int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream);
+                     int t_offset, int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
                           bf16_t* out, float* lse, hipStream_t stream);
 // Static per-device scratch of the allocation-free decode entry point (64 MiB): device address of

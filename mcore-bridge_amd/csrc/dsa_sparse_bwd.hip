@@ -120,7 +120,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
                         __builtin_amdgcn_readfirstlane(lds_addr(sm.lse[wave])));
   // (waits for every load above, the O copies included, then a barrier)
   const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
-                                       p.causal, t);
+                                       p.causal, t + p.q_offset);
   // Delta = rowsum(dO * O) of this lane's head: chunks 2*ks + hb of O row hl from LDS
   float delta = 0.f;
   {
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   const int g = lane >> 4, gi = lane & 15;
   const int h0 = blockIdx.y * 128;
   const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
-                                       p.causal, t);
+                                       p.causal, t + p.q_offset);
   // dS rows of this workgroup's heads; rows past n_heads re-read row 0 (never stored).
   const int hrows = min(HR, p.n_heads - h0);
   // staged dS tile of block b: [H heads][32 keys] contiguous at ((t * NB + b) * H) * 32
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
   const bool copier = wu < NWC;
   const int g = lane >> 4, gi = lane & 15;
   const int nblk = stage_index_row<NW>(sm.idx, sm.red, p.idx + (int64_t)t * p.idx_stride, p.topk, p.n_kv,
-                                       p.causal, t);
+                                       p.causal, t + p.q_offset);
   const int hrows = min(128, p.n_heads);
   const char* ds_base = reinterpret_cast<const char*>(p.ds_stage + (int64_t)t * (p.topk_pad / kBK) * p.n_heads * kBK);
   const int64_t ds_blk = (int64_t)p.n_heads * kBK * 2;   // bytes per staged block tile
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       const int j = threadIdx.x + NW * 64 * i;
       if (j < kpad) {
         int v = iv[i];
-        if (v < 0 || v >= p.n_kv || (p.causal && v > t)) v = -1;
+        if (v < 0 || v >= p.n_kv || (p.causal && v > t + p.q_offset)) v = -1;
         sm.idx[j] = v;
         if (v >= 0) last = j;
         sm.pos[j] = (int32_t)(pv[i] < 0 ? p.g_sink_row : pv[i]);   // < 2^31: checked by the launcher
@@ -927,7 +927,7 @@ DSA_DEV void csr_run(int total_q, int& t0, int& t1) {
 }
 
 __global__ __launch_bounds__(kCsrThreads) void csr_hist_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
-                                                              int topk, int n_kv, int causal, int32_t* cnt) {
+                                                              int topk, int n_kv, int causal, int t_offset, int32_t* cnt) {
   __shared__ int32_t hist[kCsrLdsKeys];
   int t0, t1;
   csr_run(total_q, t0, t1);
@@ -938,7 +938,7 @@ __global__ __launch_bounds__(kCsrThreads) void csr_hist_kernel(const int32_t* id
     for (int t = t0; t < t1; ++t)
       for (int j = threadIdx.x; j < topk; j += kCsrThreads) {
         const int v = idx[(int64_t)t * idx_stride + j];
-        if (csr_pair_ok(v, t, n_kv, causal) && v >= k0 && v - k0 < nk) atomicAdd(hist + (v - k0), 1);
+        if (csr_pair_ok(v, t + t_offset, n_kv, causal) && v >= k0 && v - k0 < nk) atomicAdd(hist + (v - k0), 1);
       }
     __syncthreads();
     for (int k = threadIdx.x; k < nk; k += kCsrThreads) cnt[(int64_t)blockIdx.x * n_kv + k0 + k] = hist[k];
@@ -995,7 +995,8 @@ __global__ __launch_bounds__(1024) void csr_scan_kernel(const int32_t* totals, i
 }
 
 __global__ __launch_bounds__(kCsrThreads) void csr_fill_kernel(const int32_t* idx, int64_t idx_stride, int total_q,
-                                                              int topk, int n_kv, int causal, const int64_t* offsets,
+                                                              int topk, int n_kv, int causal, int t_offset,
+                                                              const int64_t* offsets,
                                                               const int32_t* cnt, int64_t* pair_pos) {
   __shared__ int32_t next[kCsrLdsKeys];   // next free slot of each key of the tile
   int t0, t1;
@@ -1022,7 +1023,7 @@ __global__ __launch_bounds__(kCsrThreads) void csr_fill_kernel(const int32_t* id
         if (j < topk) {
           const int v = cur[i];
           int64_t* dst = pair_pos + (int64_t)t * topk + j;
-          if (!csr_pair_ok(v, t, n_kv, causal)) {
+          if (!csr_pair_ok(v, t + t_offset, n_kv, causal)) {
             if (k0 == 0) *dst = -1;
           } else if (v >= k0 && v - k0 < nk) {
             *dst = atomicAdd(next + (v - k0), 1);
@@ -1037,11 +1038,12 @@ __global__ __launch_bounds__(kCsrThreads) void csr_fill_kernel(const int32_t* id
 }
 
 // ------------------------------------------------------------------------------------------
-// B5: dKV[s] = sum of G rows in s's segment (fp32).  One workgroup (288 threads) per key:
+// B5: dKV[s] = sum of G rows in s's segment (fp32), or dKV[s] += that sum for the later query
+// chunks of a chunked backward.  One workgroup (288 threads) per key:
 // 4 row lanes x 72 chunks of 8 dims.
 // ------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_stage, const int64_t* offsets,
-                                                             int n_kv, float* dkv, int64_t dkv_stride) {
+                                                             int n_kv, float* dkv, int64_t dkv_stride, int accumulate) {
   __shared__ float red[3][kDqk];
   const int s = blockIdx.x;
   if (s >= n_kv) return;
@@ -1065,20 +1067,23 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   if (r == 0) {
     float* out = dkv + (int64_t)s * dkv_stride + c * 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = acc[e] + red[0][c * 8 + e] + red[1][c * 8 + e] + red[2][c * 8 + e];
+    for (int e = 0; e < 8; ++e) {
+      const float v = acc[e] + red[0][c * 8 + e] + red[1][c * 8 + e] + red[2][c * 8 + e];
+      out[e] = accumulate ? out[e] + v : v;
+    }
   }
 }
 
 void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
-                     int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream) {
+                     int t_offset, int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream) {
   const int nr = csr_groups(total_q, n_kv);
   hipLaunchKernelGGL(csr_hist_kernel, dim3(nr), dim3(kCsrThreads), 0, stream, idx, idx_stride, total_q, topk, n_kv,
-                     causal, csr_counts);
+                     causal, t_offset, csr_counts);
   hipLaunchKernelGGL(csr_colscan_kernel, dim3((n_kv + 255) / 256), dim3(256), 0, stream, csr_counts, nr, n_kv);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, stream, csr_counts + (int64_t)nr * n_kv, n_kv,
                      csr_offsets);
   hipLaunchKernelGGL(csr_fill_kernel, dim3(nr), dim3(kCsrThreads), 0, stream, idx, idx_stride, total_q, topk, n_kv,
-                     causal, csr_offsets, csr_counts, pair_pos);
+                     causal, t_offset, csr_offsets, csr_counts, pair_pos);
 }
 
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev) {
@@ -1092,8 +1097,8 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   const dim3 grid(xcd_grid(p.total_q), (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
-  launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_kv, p.causal, p.csr_counts, p.csr_offsets,
-                  p.pair_pos, stream);
+  launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_kv, p.causal, p.q_offset, p.csr_counts,
+                  p.csr_offsets, p.pair_pos, stream);
   mark(1);
   if (nw == 4) {
     hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);
@@ -1122,7 +1127,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
     hipLaunchKernelGGL(bwd_g_kernel<1>, ggrid, dim3(256), 0, stream, p);
   mark(4);
   hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets, p.n_kv,
-                     p.dkv, p.dkv_stride);
+                     p.dkv, p.dkv_stride, p.dkv_accumulate);
   mark(5);
   return hipGetLastError() == hipSuccess && marks_ok ? 0 : -4;
 }

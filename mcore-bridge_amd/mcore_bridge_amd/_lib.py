@@ -57,6 +57,7 @@ SIGNATURES = {
     "dsa_sparse_mla_decode_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                               c_int, c_float, c_void_p, c_void_p, c_void_p]),
     "dsa_sparse_mla_bwd_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "dsa_sparse_mla_bwd_workspace_size_chunked": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                    c_size_t, c_void_p]),

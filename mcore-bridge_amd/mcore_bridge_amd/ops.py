@@ -369,10 +369,16 @@ def bwd_workspace_bytes(total_q: int, n_kv: int, n_heads: int, topk_: int) -> in
     return int(_lib.load().dsa_sparse_mla_bwd_workspace_size(total_q, n_kv, n_heads, topk_))
 
 
+def bwd_workspace_bytes_chunked(total_q: int, n_kv: int, n_heads: int, topk_: int, chunk_q: int) -> int:
+    return int(_lib.load().dsa_sparse_mla_bwd_workspace_size_chunked(total_q, n_kv, n_heads, topk_, chunk_q))
+
+
 @torch.library.custom_op("dsa_amd::sparse_mla_bwd", mutates_args=())
 def sparse_mla_bwd(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sm_scale: float,
-                   causal: bool = False) -> Tuple[Tensor, Tensor]:
-    """Gradients of ``sparse_mla_fwd``: ``(dq [T,H,576] bf16, dkv [N,576] fp32)``."""
+                   causal: bool = False, max_workspace_bytes: int = 0) -> Tuple[Tensor, Tensor]:
+    """Gradients of ``sparse_mla_fwd``: ``(dq [T,H,576] bf16, dkv [N,576] fp32)``.
+    ``max_workspace_bytes`` > 0 caps the scratch memory: the backward then runs in passes of as
+    many query rows as fit (at least 256), adding each pass's dkv into the previous ones."""
     _check_attn(q, kv, idx)
     _require_gpu(out, dout, lse)
     q, kv, out, lse = q.contiguous(), kv.contiguous(), out.contiguous(), lse.contiguous()
@@ -383,6 +389,8 @@ def sparse_mla_bwd(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor
     dq = torch.empty_like(q)
     dkv = torch.empty(N, D_QK, dtype=torch.float32, device=q.device)
     ws_bytes = bwd_workspace_bytes(T, N, H, K)
+    if 0 < max_workspace_bytes < ws_bytes:
+        ws_bytes = max(int(max_workspace_bytes), bwd_workspace_bytes_chunked(T, N, H, K, 256))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         _lib.call("dsa_sparse_mla_bwd", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), T, N, H, D_QK, D_V, K,
@@ -391,7 +399,7 @@ def sparse_mla_bwd(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor
 
 
 @sparse_mla_bwd.register_fake
-def _(q, kv, idx, out, dout, lse, sm_scale, causal=False):
+def _(q, kv, idx, out, dout, lse, sm_scale, causal=False, max_workspace_bytes=0):
     return torch.empty_like(q), kv.new_empty(kv.shape[0], D_QK, dtype=torch.float32)
 
 
@@ -434,9 +442,18 @@ def _fwd_setup(ctx, inputs, output):
     ctx.causal = causal
 
 
+_BWD_WORKSPACE_LIMIT = [0]
+
+
+def set_backward_workspace_limit(nbytes: int) -> None:
+    """Cap the scratch memory of the autograd backward of ``sparse_mla_fwd`` (0 = one pass over all
+    query rows, the fastest; otherwise passes of as many rows as fit, at least 256)."""
+    _BWD_WORKSPACE_LIMIT[0] = max(0, int(nbytes))
+
+
 def _fwd_backward(ctx, dout, dlse):
     q, kv, idx, out, lse = ctx.saved_tensors
-    dq, dkv = sparse_mla_bwd(q, kv, idx, out, dout, lse, ctx.sm_scale, ctx.causal)
+    dq, dkv = sparse_mla_bwd(q, kv, idx, out, dout, lse, ctx.sm_scale, ctx.causal, _BWD_WORKSPACE_LIMIT[0])
     return dq, dkv.to(kv.dtype), None, None, None
 
 

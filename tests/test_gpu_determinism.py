@@ -61,3 +61,32 @@ def test_indexer_score_bwd_is_bitwise_repeatable():
     for r in runs[1:]:
         for a, b, name in zip(r, runs[0], ("dq", "dw", "dk")):
             assert torch.equal(a, b), f"{name} differs between runs"
+
+
+@pytest.mark.parametrize("T,N,H,K", [(3000, 3000, 64, 512), (1100, 20000, 16, 256)])
+def test_chunked_sparse_bwd_matches_one_pass(T, N, H, K):
+    """A workspace below the one-pass size runs the backward in passes of whole 256-row units
+    (the causal test then takes each pass's query offset, and later passes add into dkv).  The
+    index rows also hold future keys (causal: to be dropped) and keys past n_kv.  dq equals the
+    one-pass dq bit for bit (no cross-query sum); dkv agrees to fp32 reordering and repeats bit
+    for bit."""
+    print(f"[chunked sparse bwd] T={T} N={N} H={H} K={K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(T * 7 + K)
+    q = (torch.randn(T, H, 576, generator=g, device=DEV) * 0.1).bfloat16()
+    kv = (torch.randn(N, 576, generator=g, device=DEV) * 0.1).bfloat16()
+    idx = torch.argsort(torch.rand(T, N, generator=g, device=DEV), dim=1)[:, :K].to(torch.int32)
+    idx[:, :32] = torch.arange(32, dtype=torch.int32, device=DEV)     # shared keys, all passes
+    idx[::7, -1] = N + 5                                               # out of range: ignored
+    idx = idx.contiguous()
+    dout = (torch.randn(T, H, 512, generator=g, device=DEV) * 0.01).bfloat16()
+    out, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
+    dq1, dkv1 = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    cap = ops.bwd_workspace_bytes_chunked(T, N, H, K, 512)               # passes of 512 rows
+    assert cap < ops.bwd_workspace_bytes(T, N, H, K)
+    dq2, dkv2 = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True, cap)
+    dq3, dkv3 = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True, cap)
+    assert torch.equal(dq2, dq1)
+    assert torch.equal(dq3, dq2) and torch.equal(dkv3, dkv2)
+    torch.testing.assert_close(dkv2, dkv1, rtol=1e-5, atol=1e-7)
+    err = (dkv2 - dkv1).norm() / dkv1.norm()
+    assert err < 1e-6, float(err)
