@@ -587,6 +587,261 @@ DSA_DEV uint32_t order_key(float f) {
 
 }  // namespace
 
+// Long rows (more entries than the LDS cache holds), fp32 scores in global memory: three passes
+// over the row instead of the general path's six.
+//   A  histogram of the top 12 bits of every order key (4096 bins, in the unused cache): the bin
+//      b* that holds the K-th largest key, and how many keys lie above it;
+//   B  the keys of bin b* with their positions into an LDS candidate list, and per compaction
+//      wave the number of keys above b*;
+//   then the remaining 20 bits are radix-selected over the candidates alone, the compaction's
+//   per-wave counts come from pass B and the candidates, and
+//   C  is the compaction's emitting pass (as in block_select_topk).
+// Returns false, having emitted nothing, when bin b* holds more keys than the candidate list;
+// the caller then runs the general path (its own state is rebuilt from scratch).
+constexpr int kLongBins = 4096;
+
+template <class Emit>
+DSA_DEV bool block_select_topk_long(const float* src, int n, int K, uint32_t* cache, int cache_cap, int* hist,
+                                    int* sh, uint32_t* sel_prefix, int* sel_need, Emit&& emit) {
+  constexpr int T = kTopkThreads, NW = T / 64;
+  const int cap = (cache_cap - kLongBins) / 2;   // candidate slots
+  if (cap < 1024 || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return false;
+  const uint32_t* bits = reinterpret_cast<const uint32_t*>(src);
+  const uint4* b4 = reinterpret_cast<const uint4*>(src);
+  int* h12 = reinterpret_cast<int*>(cache);
+  uint32_t* ckey = cache + kLongBins;
+  int* cpos = reinterpret_cast<int*>(cache + kLongBins + cap);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int per_w = (n + 64 * NW - 1) / (64 * NW) * 64;
+  const int wa = min(n, wave * per_w), wb = min(n, wa + per_w);
+  // f(j, u[4], v[4]) over this wave's range, 256 consecutive entries per call: lane l holds
+  // entries j .. j+3, j = j0 + 4 l (16-byte loads, 4 calls' loads in flight); a ragged tail in
+  // 4-byte loads
+  auto for_wave_range = [&](auto&& f) {
+    const int wb4 = wa + (wb - wa) / 256 * 256;
+    int j0 = wa;
+    for (; j0 + 4 * 256 <= wb4; j0 += 4 * 256) {
+      uint4 x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[k] = b4[(j0 + 256 * k) / 4 + lane];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t u[4] = {order_key(__builtin_bit_cast(float, x[k].x)), order_key(__builtin_bit_cast(float, x[k].y)),
+                               order_key(__builtin_bit_cast(float, x[k].z)), order_key(__builtin_bit_cast(float, x[k].w))};
+        const bool v[4] = {true, true, true, true};
+        f(j0 + 256 * k + 4 * lane, u, v);
+      }
+    }
+    for (; j0 < wb; j0 += 256) {
+      uint32_t u[4];
+      bool v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = j0 + 4 * lane + e;
+        v[e] = j < wb;
+        u[e] = v[e] ? order_key(__builtin_bit_cast(float, bits[j])) : 0u;
+      }
+      f(j0 + 4 * lane, u, v);
+    }
+  };
+
+  // ---- A: 12-bit histogram
+  for (int b = threadIdx.x; b < kLongBins; b += T) h12[b] = 0;
+  __syncthreads();
+  for_wave_range([&](int, const uint32_t (&u)[4], const bool (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (v[e]) atomicAdd(&h12[u[e] >> 20], 1);
+  });
+  __syncthreads();
+  {  // bins in descending order, 8 per thread; block scan of the per-thread totals
+    const int b_hi = kLongBins - 1 - 8 * (int)threadIdx.x;
+    int c[8], tot = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      c[i] = h12[b_hi - i];
+      tot += c[i];
+    }
+    int incl = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    if (lane == 63) sh[wave] = incl;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      if (w < wave) incl += sh[w];
+    const int excl = incl - tot;
+    if (excl < K && K <= incl) {
+      int above = excl, bin = b_hi;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (above + c[i] >= K) {
+          bin = b_hi - i;
+          break;
+        }
+        above += c[i];
+      }
+      *sel_prefix = (uint32_t)bin;
+      *sel_need = K - above;
+    }
+    __syncthreads();
+  }
+  const uint32_t bstar = *sel_prefix;
+  int need = *sel_need;
+  // ---- B: candidates of bin b*, counts above it per wave (hist[0] counts the candidates)
+  if (threadIdx.x == 0) hist[0] = 0;
+  __syncthreads();
+  int w_above = 0;
+  for_wave_range([&](int j, const uint32_t (&u)[4], const bool (&v)[4]) {
+    int above = 0, nin = 0;
+    bool in[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t top = u[e] >> 20;
+      above += (v[e] && top > bstar) ? 1 : 0;
+      in[e] = v[e] && top == bstar;
+      nin += in[e] ? 1 : 0;
+    }
+    w_above += above;
+    const uint64_t m = __ballot(nin > 0);
+    if (m) {   // the lanes' candidates in lane order: an exclusive scan of nin over the wave
+      int incl = nin;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+      }
+      int slot0 = 0;
+      if (lane == 63) slot0 = atomicAdd(&hist[0], incl);
+      slot0 = __shfl(slot0, 63, 64);
+      int slot = slot0 + incl - nin;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (in[e]) {
+          if (slot < cap) {
+            ckey[slot] = u[e];
+            cpos[slot] = j + e;
+          }
+          ++slot;
+        }
+    }
+  });
+  w_above = wave_sum_i(w_above);
+  if (lane == 0) sh[wave] = w_above;
+  __syncthreads();
+  const int nc = hist[0];
+  __syncthreads();   // every thread has read the count before hist is reused (or the fallback)
+  if (nc > cap) return false;
+
+  // ---- radix select of bits 19..0 over the candidates: digits at bits 19..12, 11..4, 7..0
+  uint32_t prefix = bstar << 20, pmask = 0xFFF00000u;
+  int* hcopy = hist + (threadIdx.x & (kHistCopies - 1));
+  auto bin_count = [&](int b) {
+    const int4 x = *reinterpret_cast<const int4*>(hist + kHistCopies * b);
+    const int4 y = *reinterpret_cast<const int4*>(hist + kHistCopies * b + 4);
+    return x.x + x.y + x.z + x.w + y.x + y.y + y.z + y.w;
+  };
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 12 : (pass == 1 ? 4 : 0);
+    for (int b = threadIdx.x; b < 256 * kHistCopies; b += T) hist[b] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nc; i += T) {
+      const uint32_t u = ckey[i];
+      if ((u & pmask) == prefix) atomicAdd(&hcopy[kHistCopies * ((u >> shift) & 255)], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {  // one wave: suffix scan of 256 bins, 4 per lane (lane 0 = top bins)
+      const int l = threadIdx.x;
+      const int b0 = 255 - 4 * l;
+      const int c0 = bin_count(b0), c1 = bin_count(b0 - 1), c2 = bin_count(b0 - 2), c3 = bin_count(b0 - 3);
+      const int tot = c0 + c1 + c2 + c3;
+      int incl = tot;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if (l >= o) incl += v;
+      }
+      const int excl = incl - tot;
+      if (excl < need && need <= incl) {
+        int above = excl, bin = b0;
+        const int cs[4] = {c0, c1, c2, c3};
+        for (int q = 0; q < 4; ++q) {
+          if (above + cs[q] >= need) { bin = b0 - q; break; }
+          above += cs[q];
+        }
+        *sel_prefix = prefix | ((uint32_t)bin << shift);
+        *sel_need = need - above;
+      }
+    }
+    __syncthreads();
+    prefix = *sel_prefix;
+    need = *sel_need;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  const uint32_t thr = prefix;  // exact K-th largest key; `need` of the keys equal to it are taken
+
+  // ---- per-wave counts: above b* (pass B) + candidates above thr / equal to it, by wave range
+  if (threadIdx.x < 2 * NW) hist[threadIdx.x] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < nc; i += T) {
+    const uint32_t u = ckey[i];
+    const int w = cpos[i] / per_w;
+    if (u > thr) atomicAdd(&hist[w], 1);
+    else if (u == thr) atomicAdd(&hist[NW + w], 1);
+  }
+  __syncthreads();
+  int gt_before = 0, eq_before = 0;
+  for (int w = 0; w < wave; ++w) {
+    gt_before += sh[w] + hist[w];
+    eq_before += hist[NW + w];
+  }
+  // ---- C: emit, ascending position (lane-major, then the lane's 4 consecutive entries)
+  int pos = gt_before + min(eq_before, need);
+  int eq_run = eq_before;
+  for_wave_range([&](int j, const uint32_t (&u)[4], const bool (&v)[4]) {
+    bool gt[4], eq[4];
+    int n_eq = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gt[e] = v[e] && u[e] > thr;
+      eq[e] = v[e] && u[e] == thr;
+      n_eq += eq[e] ? 1 : 0;
+    }
+    int eq_incl = n_eq;   // wave scan of the per-lane tie counts
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(eq_incl, o, 64);
+      if (lane >= o) eq_incl += t;
+    }
+    int eq_seen = eq_run + eq_incl - n_eq;   // ties before this lane's first entry
+    bool take[4];
+    int n_take = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      take[e] = gt[e] || (eq[e] && eq_seen < need);
+      eq_seen += eq[e] ? 1 : 0;
+      n_take += take[e] ? 1 : 0;
+    }
+    int tk_incl = n_take;   // wave scan of the per-lane take counts
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(tk_incl, o, 64);
+      if (lane >= o) tk_incl += t;
+    }
+    int r = pos + tk_incl - n_take;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (take[e]) emit(r++, j + e, u[e]);
+    pos += __shfl(tk_incl, 63, 64);
+    eq_run += __shfl(eq_incl, 63, 64);
+  });
+  return true;
+}
+
 // Exact top-k of one list of n > K entries in one workgroup: the K largest under (key desc,
 // position asc), emitted as emit(rank, position, key) with rank ascending in position. Entries are
 // fp32 scores mapped through order_key, or (kKeys) order keys already.
@@ -596,6 +851,11 @@ DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, i
   const uint32_t* bits = static_cast<const uint32_t*>(src);
   auto conv = [](uint32_t x) -> uint32_t { return kKeys ? x : order_key(__builtin_bit_cast(float, x)); };
   const bool cached = n <= cache_cap;
+  if constexpr (!kKeys) {
+    if (!cached && block_select_topk_long(static_cast<const float*>(src), n, K, cache, cache_cap, hist, sh,
+                                          sel_prefix, sel_need, emit))
+      return;
+  }
   // long lists stay in global memory and are streamed as 16-byte vectors when aligned
   const bool vec = ((reinterpret_cast<uintptr_t>(bits) & 15) == 0);
   const uint4* sc4 = reinterpret_cast<const uint4*>(bits);

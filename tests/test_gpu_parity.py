@@ -60,6 +60,38 @@ def test_topk_bit_exact_from_fp32_scores(n, k):
         assert torch.equal(got[r], ref[:k] if ref.numel() >= k else torch.cat([ref, ref.new_full((k - ref.numel(),), -1)])), r
 
 
+@pytest.mark.parametrize("n,k", [(16484, 2048), (32768, 2048), (40000, 4096), (140000, 2048), (20000, 64)])
+def test_topk_one_workgroup_long_rows_bit_exact(n, k):
+    """Rows longer than the 16384-entry LDS cache in one workgroup per row (no split workspace):
+    the three-pass candidate path, and its fallback when the threshold's 12-bit bin holds more
+    keys than the candidate list (rows of all-equal or few distinct values)."""
+    import ctypes
+    from mcore_bridge_amd import _lib
+    print(f"[topk one workgroup, long rows] n={n} k={k}", flush=True)
+    g = torch.Generator().manual_seed(n + 3 * k)
+    rows = 12
+    sc = torch.randn(rows, n, generator=g) * torch.rand(rows, 1, generator=g) * 4
+    sc[0] = 0.0                                                      # all ties: fallback
+    sc[1] = torch.round(sc[1] * 2) / 2                               # few distinct values
+    sc[2] = torch.where(torch.rand(n, generator=g) < 0.5, -0.0, 0.0)  # signed zeros tie
+    sc[3, : n // 2] = 1.0                                            # a wide tie at the threshold
+    sc[4] = torch.relu(sc[4])                                        # many exact zeros below
+    ln = torch.randint(k + 1, n + 1, (rows,), generator=g).to(torch.int32)
+    ln[:6] = n
+    base = torch.randint(0, 1000, (rows,), generator=g).to(torch.int32)
+    scd, bd, ld = sc.to(DEV), base.to(DEV), ln.to(DEV)
+    out = torch.empty(rows, k, dtype=torch.int32, device=DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert _lib.load().dsa_topk(P(scd), n, P(bd), P(ld), rows, k, P(out), None, None, 0, st) == 0
+    got = out.cpu().long()
+    for r in range(rows):
+        row = sc[r].double().clone()
+        row[int(ln[r]):] = float("-inf")
+        ref = O.topk_indices(row[None], k)[0] + int(base[r])
+        assert torch.equal(got[r], ref), r
+
+
 def test_topk_split_equals_one_workgroup_cfg5_full_size():
     """cfg5's 64 cache lengths (up to 65,265 keys): the split selection (slices + merge, through
     the workspace) returns the one-workgroup-per-row selection's indices bit for bit, on scores
