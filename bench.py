@@ -16,7 +16,8 @@ The line also carries:
   "cfg2" / "cfg4"     the prefill chain (indexer -> top-k -> forward) at configs[1] (S = 4096,
                       bf16) and configs[3] (S = 32768, fp8 indexer against the fp8 peak);
   "decode"            configs[4] (cfg5), HBM-bound: gathered bytes of the selected cache rows /
-                      decode attention time, plus the decode indexer and the graph-replayed step;
+                      decode attention time, plus the decode indexer over a bf16 and over an
+                      e4m3 key cache, and the graph-replayed step;
   "indexer_prologue"  the fused producer of the indexer's inputs at the cfg3 token count (HBM);
   "indexer_kl"        the sparse indexer KL loss and the indexer-score backward at cfg3;
   "cpu_baseline"      the oracle's reference-shaped fp32 compositions timed on the host per config
