@@ -175,6 +175,12 @@ DSA_DEV void async_copy16_unordered(const void* gsrc, uint32_t lds_wave_base) {
                : "memory", "m0");
 }
 
+// The same copy with the non-temporal cache policy (nt): streamed data that is read once.
+DSA_DEV void async_copy16_nt(const void* gsrc, uint32_t lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds_wave_base), "v"(gsrc)
+               : "memory", "m0");
+}
+
 // 4-byte variant (global_load_lds_dword): lane i writes 4 bytes at lds_wave_base + 4*i.
 DSA_DEV void async_copy4_unordered(const void* gsrc, uint32_t lds_wave_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_wave_base), "v"(gsrc)

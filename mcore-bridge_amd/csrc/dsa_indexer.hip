@@ -340,7 +340,9 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
 // into a 2-stage ring per wave. The per-lane row loads of indexer_scores_kernel touch 32 rows of
 // 32 B per instruction; at decode's few, very long rows that access pattern, not latency or
 // occupancy, was what held the scan back (cfg5: ~200 us there, ~163 us here, same scores bit for
-// bit). Deeper rings (3-4 stages) cost a workgroup per CU of LDS and ran slower.
+// bit). Deeper rings (3-4 stages) cost a workgroup per CU of LDS and ran slower.  The copies
+// carry the non-temporal hint: each key row is read once, and keeping the stream out of the
+// caches' normal replacement took the cfg5 scan from ~171 to ~151 us.
 __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams p) {
   // Q rows (chunk u of head row h at u ^ (h & 7)), head weights, and per wave a 2-stage ring of
   // 32-key blocks (chunk c of key r at c ^ (r & 7)) filled by contiguous LDS-direct copies
@@ -384,7 +386,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
       const int kk = 4 * r + kk0;
       const int row = base + min(k0 + kk, c1 - 1);
       const char* src = kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7));
-      async_copy16_unordered(src, dst + 1024u * r);
+      async_copy16_nt(src, dst + 1024u * r);   // each key row is read once: non-temporal
     }
   };
   const uint32_t qa0 = lds_addr(qs) + hl * 256, qa1 = lds_addr(qs) + (32 + hl) * 256;
@@ -423,7 +425,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
 // last key), through a per-wave ring of kRowsFp8Stages blocks (kRowsFp8Stages - 1 in flight while
 // one is computed; 2, 3, 4 and 6 stages and 512- or 1024-key chunks all measured within 10 % at
 // cfg5: ~110 us for the 360 MB of fp8 keys and scales, 3.3 TB/s, with the L1's pending-miss
-// stalls at ~40 % of the cycles).  The query's fp8 A fragments sit in registers
+// stalls at ~40 % of the cycles; non-temporal row copies then took it to ~92 us).  The query's fp8 A fragments sit in registers
 // (32 VGPRs); two 32x32x64 fp8 MFMAs per row tile and block;
 // I = k_scale[s] * sum_h (w q_scale)[t,h] relu(q8 . k8).
 constexpr int kRowsFp8Stages = 3;
@@ -469,7 +471,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_fp8_kernel(IndexerPar
     for (int r = 0; r < 4; ++r) {
       const int kk = 8 * r + kk0;
       const int row = base + min(k0 + kk, c1 - 1);
-      async_copy16_unordered(kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7)), dst + 1024u * r);
+      async_copy16_nt(kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7)), dst + 1024u * r);   // read once
     }
     async_copy4_unordered(p.k_scale + base + min(k0 + hl, c1 - 1), dst + 4096u);
   };
