@@ -25,7 +25,9 @@
 //   B5 bwd_dkv_reduce  per key: fp32 sum of its contiguous G rows -> dKV.
 // The G rows (1152 B per selected pair, far more than the caches hold) are written and read with
 // non-temporal stores and loads, so they stream through L2 without displacing the operands B3
-// and B5 re-read.
+// and B5 re-read; B2 and B3 read the staged P / dS tiles (read once each) with non-temporal
+// LDS-direct copies.  B1 writes those tiles with ordinary 16-byte stores: non-temporal stores
+// that cover a fraction of a cache line each ran B1 ~3x slower.
 // B1-B3 stream their per-block operands into LDS through 3-stage rings of asynchronous
 // global_load_lds copies (see dsa_kvtile.h) completed by explicit s_waitcnt vmcnt + barrier.
 // vmcnt counts every vector-memory instruction of the wave in issue order, so each wave issues
@@ -56,6 +58,23 @@ DSA_DEV u32x2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// lo = keys k .. k+3 and hi = keys k+8 .. k+11 in the lower half-wave (lane l < 32), keys
+// k+4 .. k+7 and k+12 .. k+15 in the upper half (lane l + 32, same head).  One
+// v_permlane32_swap per dword trades the lower half's hi for the upper half's lo, after which
+// the lower lane holds keys k .. k+7 and the upper lane k+8 .. k+15: one 16-byte store each.
+DSA_DEV u32x4 swap_key_halves(u32x2 lo, u32x2 hi) {
+  u32x4 r;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(lo[c], hi[c], false, false);
+    // sw[0] = lo with lanes 32..63 taken from hi's lanes 0..31; sw[1] = hi with lanes 0..31
+    // taken from lo's lanes 32..63
+    r[c] = sw[0];
+    r[2 + c] = sw[1];
+  }
+  return r;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
@@ -74,7 +93,7 @@ struct SpSmem {
 template <int NW>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   constexpr int G = tile_copies_per_wave<NW>();
-  constexpr int S = 8;  // staging stores per wave per block (4 x P, 4 x dS)
+  constexpr int S = 4;  // staging stores per wave per block (2 x P, 2 x dS)
   constexpr int kCopyEvery = kDqk / 16 / G;   // S/dP steps per gather copy
   static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the k-steps");
   __shared__ __attribute__((aligned(128))) SpSmem sm;
@@ -142,9 +161,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   __syncthreads();   // O staging dead: the union now holds the KV tile ring
 
   // staged tiles: element (t, head, slot 32*b + k) at ((t * NB + b) * H + head) * 32 + k
-  // (NB = topk_pad / 32): each block's [H heads x 32 keys] tile is contiguous; lane writes keys
-  // 8*q4 + 4*hb .. +3 of each block
-  const int64_t stage_off = ((int64_t)t * (p.topk_pad / kBK) * p.n_heads + hsafe) * kBK + hb * 4;
+  // (NB = topk_pad / 32): each block's [H heads x 32 keys] tile is contiguous; after the half
+  // swap (swap_key_halves) lane writes keys 16*pr + 8*hb .. +7 of each block, pr = 0, 1
+  const int64_t stage_off = ((int64_t)t * (p.topk_pad / kBK) * p.n_heads + hsafe) * kBK + hb * 8;
   const int64_t stage_blk = (int64_t)p.n_heads * kBK;   // elements per staged block tile
   bf16_t* ps_row = p.p_stage + stage_off;
   bf16_t* ds_row = p.ds_stage + stage_off;
@@ -155,10 +174,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
   if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
   uint32_t st_cur = 0, st_next = 2 * kTileBytes;   // ring byte offsets of blocks blk, blk+2
-  u32x2 pw[4], dw[4];   // previous block's values, stored right after the next block's barrier
+  u32x4 pw[2], dw[2];   // previous block's values, stored right after the next block's barrier
   for (int blk = 0; blk < nblk; ++blk) {
     // issue order per block: [wait][barrier], then between the S/dP MFMAs the copies of block
-    // blk+2 (k-steps 0, 4, .., 32) and the P/dS stores of block blk-1 (k-steps 1, 5, .., 29,
+    // blk+2 (k-steps 0, 4, .., 32) and the P/dS stores of block blk-1 (k-steps 1, 9, 17, 25,
     // all before the last copy).  Block blk needs copies(blk) done; issued after them are
     // block blk-1's copies(blk+1) and, from blk = 2 on (block 0 stores nothing), its stores of
     // block blk-2.
@@ -202,10 +221,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
           gather_issue<NW>(next_tile, next_src, next_row, wave, lane, ks / kCopyEvery);
           next_row = gather_row<NW>(next_src, ks / kCopyEvery + 1);
         }
-        if (ks % 4 == 1 && ks < 32 && store_prev) {
-          const int q = ks / 4;   // 0..7: P then dS of q4 = q / 2
-          if (q & 1) *reinterpret_cast<u32x2*>(ds_row + store_j + 8 * (q >> 1)) = dw[q >> 1];
-          else *reinterpret_cast<u32x2*>(ps_row + store_j + 8 * (q >> 1)) = pw[q >> 1];
+        if (ks % 8 == 1 && ks < 32 && store_prev) {
+          const int q = ks / 8;   // 0..3: P then dS of key half pr = q / 2
+          if (q & 1) *reinterpret_cast<u32x4*>(ds_row + store_j + 16 * (q >> 1)) = dw[q >> 1];
+          else *reinterpret_cast<u32x4*>(ps_row + store_j + 16 * (q >> 1)) = pw[q >> 1];
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -225,21 +244,27 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         pv[i] = ok ? fast_exp2(__builtin_fmaf(s[i], p.scale_log2, -lse2)) : 0.f;
       }
     }
+    u32x2 pk[4], dk[4];   // keys 8*q4 + 4*hb .. +3
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       float dv[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) dv[e] = pv[4 * q4 + e] * __builtin_fmaf(dp[4 * q4 + e], p.scale, -delta_s);
-      pw[q4] = u32x2{pack_bf16x2(pv[4 * q4], pv[4 * q4 + 1]), pack_bf16x2(pv[4 * q4 + 2], pv[4 * q4 + 3])};
-      dw[q4] = u32x2{pack_bf16x2(dv[0], dv[1]), pack_bf16x2(dv[2], dv[3])};
+      pk[q4] = u32x2{pack_bf16x2(pv[4 * q4], pv[4 * q4 + 1]), pack_bf16x2(pv[4 * q4 + 2], pv[4 * q4 + 3])};
+      dk[q4] = u32x2{pack_bf16x2(dv[0], dv[1]), pack_bf16x2(dv[2], dv[3])};
+    }
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      pw[pr] = swap_key_halves(pk[2 * pr], pk[2 * pr + 1]);
+      dw[pr] = swap_key_halves(dk[2 * pr], dk[2 * pr + 1]);
     }
   }
   if (nblk > 0 && head_ok) {
     const int64_t j = (nblk - 1) * stage_blk;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      *reinterpret_cast<u32x2*>(ps_row + j + 8 * q4) = pw[q4];
-      *reinterpret_cast<u32x2*>(ds_row + j + 8 * q4) = dw[q4];
+    for (int pr = 0; pr < 2; ++pr) {
+      *reinterpret_cast<u32x4*>(ps_row + j + 16 * pr) = pw[pr];
+      *reinterpret_cast<u32x4*>(ds_row + j + 16 * pr) = dw[pr];
     }
   }
 }
@@ -297,7 +322,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
     const int h = 16 * i + (lane >> 2);
     const int q = (lane & 3) ^ ((h >> 1) & 3);
     const int hs = h < hrows ? h : 0;
-    async_copy16_unordered(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
+    async_copy16_nt(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
   };
   auto copy_ds = [&](char* dst, int blk) {
 #pragma unroll
@@ -450,7 +475,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
     const int h = 16 * i + (lane >> 2);
     const int q = (lane & 3) ^ ((h >> 1) & 3);
     const int hs = h < hrows ? h : 0;
-    async_copy16_unordered(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
+    async_copy16_nt(ds_base + blk * ds_blk + hs * (kBK * 2) + q * 16, base + i * 1024u);
   };
   // operand addresses as in bwd_dq_kernel
   uint32_t kv[2], kr[2];
@@ -762,7 +787,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     const int hs = h < p.n_heads ? h : 0;
     const int chunk = (lane & 3) ^ (2 * ((h >> 1) & 1));   // LDS chunk lane&3 <- global chunk
     const int64_t off = blk * st_blk + hs * (kBK * 2) + chunk * 16;
-    async_copy16_unordered(((c & 1) ? psb : dsb) + off, b + i * 1024u);
+    async_copy16_nt(((c & 1) ? psb : dsb) + off, b + i * 1024u);
   };
   auto stage = [&](int s, int blk) {
 #pragma unroll
