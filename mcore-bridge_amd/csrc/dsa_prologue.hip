@@ -48,55 +48,80 @@ DSA_DEV uint32_t pack_e4m3x2(float a, float b) {
 // 4L..4L+3 (h = 0: the RoPE dims) and 64 + 4L..+3 (h = 1) of one 128-dim row, so a wave
 // transforms 4 rows at once.  Dim index bits 0-1 and 6 are in-lane, bits 2-5 are the lane bits:
 // the Hadamard's four cross-lane butterfly stages and the half-split RoPE partner (lane ^ 8)
-// are DPP moves inside 16-lane rows, at VALU rate and with no trip through the LDS crossbar
-// (the previous one-row-per-wave layout needed 16 dependent ds_bpermute per row).
+// are DPP operations inside 16-lane rows, at VALU rate and with no trip through the LDS crossbar
+// (the previous one-row-per-wave layout needed 16 dependent ds_bpermute per row).  After the
+// transform lane L holds chunk hadamard_chunk(L) of the output row (dims 4C.., 64 + 4C..).
 // (all rows and banks enabled and every source lane inside the row: no lane keeps an old value)
 template <int CTRL>
 DSA_DEV float dpp_mov(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
-constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
-constexpr int kDppXor3 = 0x1B;         // quad_perm [3, 2, 1, 0]
-constexpr int kDppRowMirror = 0x140;   // lane i <- 15 - i in its row of 16
-constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i in its half row of 8
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]: lane i <- i ^ 1
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]: lane i <- i ^ 2
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i <- 7 - i in its half row of 8 (i ^ 7)
+constexpr int kDppRor8 = 0x128;        // row_ror:8: lane i <- (i + 8) mod 16 in its row (i ^ 8)
 
-// value of lane L ^ (1 << B) of the same 16-lane group
-template <int B>
-DSA_DEV float lane_xor(float v) {
-  if constexpr (B == 0) return dpp_mov<kDppXor1>(v);
-  else if constexpr (B == 1) return dpp_mov<kDppXor2>(v);
-  else if constexpr (B == 2) return dpp_mov<kDppXor3>(dpp_mov<kDppHalfMirror>(v));   // (i ^ 7) ^ 3
-  else return dpp_mov<kDppHalfMirror>(dpp_mov<kDppRowMirror>(v));                    // (i ^ 15) ^ 7
-}
+// Sum / max over the 16 lanes of a group: butterflies on lane masks 7, 1, 2, 8 (together they
+// span the 4 lane bits; each is one DPP move, which the compiler folds into the add / max).  A
+// pair of lanes computes a + b and b + a, so every lane ends with the same value.
 DSA_DEV float group_sum(float v) {
-  v += lane_xor<0>(v);
-  v += lane_xor<1>(v);
-  v += lane_xor<2>(v);
-  return v + lane_xor<3>(v);
+  v += dpp_mov<kDppHalfMirror>(v);
+  v += dpp_mov<kDppXor1>(v);
+  v += dpp_mov<kDppXor2>(v);
+  return v + dpp_mov<kDppRor8>(v);
 }
 DSA_DEV float group_max(float v) {
-  v = fmaxf(v, lane_xor<0>(v));
-  v = fmaxf(v, lane_xor<1>(v));
-  v = fmaxf(v, lane_xor<2>(v));
-  return fmaxf(v, lane_xor<3>(v));
+  v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_mov<kDppXor1>(v));
+  v = fmaxf(v, dpp_mov<kDppXor2>(v));
+  return fmaxf(v, dpp_mov<kDppRor8>(v));
 }
 
-// Cross-lane butterfly stage on lane bit B (dim bit B + 2): x[i] + x[i + s] on the low lane,
-// x[i] - x[i + s] on the high one.
-// As p + sx * x with sx = -1 on the high lane: one fma (exact sign, one rounding) after the move.
-template <int B>
-DSA_DEV void butterfly_lanes(float (&v)[2][4], int L) {
-  const float sx = ((L >> B) & 1) ? -1.f : 1.f;
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[h][e] = fmaf(sx, v[h][e], lane_xor<B>(v[h][e]));
+// The Hadamard's 16-point transform over the lane bits as four butterfly stages on lane masks
+// 7, 1, 2, 8 (pivot bits 2, 0, 1, 3), each one v_fmac_f32 per value with the partner's value
+// as a DPP source: x <- x + c * x[partner], c = -1 on the lane whose pivot bit is set.  That
+// lane holds the negated butterfly difference (x[partner] - x rounds to the exact negation), so
+// lane L ends with sigma(L) * (H16 y)[hadamard_chunk(L)] where sigma = hadamard_sign(L): the
+// caller scales by sigma and stores lane L's values at chunk hadamard_chunk(L).  (Masks 4 and
+// 8 as XORs would need two DPP moves each; 7 and 8 need one.)  The leading s_nop covers the
+// DPP-read hazards of the asm block (VALU write -> DPP read of the same VGPR: 2 wait states;
+// EXEC write -> DPP: 5); inside the block each value is re-read 8 instructions after its
+// write.  Every lane of the wave executes it (no divergence at the call sites).
+DSA_DEV void hadamard_lanes(float (&v)[2][4], int L) {
+  const float c0 = (L & 4) ? -1.f : 1.f, c1 = (L & 1) ? -1.f : 1.f;
+  const float c2 = (L & 2) ? -1.f : 1.f, c3 = (L & 8) ? -1.f : 1.f;
+#define DSA_FMAC_DPP(ctrl, c)                                                     \
+  "v_fmac_f32_dpp %0, %0, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %1, %1, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %2, %2, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %3, %3, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %4, %4, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %5, %5, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %6, %6, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t" \
+  "v_fmac_f32_dpp %7, %7, " c " " ctrl " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+  asm("s_nop 4\n\t"
+      DSA_FMAC_DPP("row_half_mirror", "%8")
+      DSA_FMAC_DPP("quad_perm:[1,0,3,2]", "%9")
+      DSA_FMAC_DPP("quad_perm:[2,3,0,1]", "%10")
+      DSA_FMAC_DPP("row_ror:8", "%11")
+      : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]),
+        "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[1][2]), "+v"(v[1][3])
+      : "v"(c0), "v"(c1), "v"(c2), "v"(c3));
+#undef DSA_FMAC_DPP
+}
+// chunk of the natural-order transform that lane L holds after hadamard_lanes: L with bit 2
+// flipped where bits 0 and 1 differ
+DSA_DEV int hadamard_chunk(int L) { return L ^ (((L ^ (L >> 1)) & 1) << 2); }
+// its sign: the signed permutation of the mask-7 stage (-1 on lanes 5, 6, 13, 14) times the
+// parity of L (one negation per pivot bit set)
+DSA_DEV float hadamard_sign(int L) {
+  const int neg = (((L ^ (L >> 1)) & (L >> 2)) ^ __builtin_popcount(L)) & 1;
+  return neg ? -1.f : 1.f;
 }
 
 // RoPE on the h = 0 values (bf16-exact inputs; u = the row or its de-interleave), then the
 // normalised natural-order Walsh-Hadamard transform over all 128 dims (fp32; the caller rounds
-// to bf16).
+// to bf16); lane L ends with output dims 4C..4C+3 and 64 + 4C..+3, C = hadamard_chunk(L).
 // cs, sn: the token's bf16 cos / sin * mscale of this lane's RoPE dims 4L..4L+3.
 DSA_DEV void rope_hadamard_group(float (&v)[2][4], const float (&cs)[4], const float (&sn)[4], int lane,
                                  int deinterleave, int rotary_interleaved) {
@@ -126,7 +151,7 @@ DSA_DEV void rope_hadamard_group(float (&v)[2][4], const float (&cs)[4], const f
       ur = u[e ^ 1];
       sg = (e & 1) ? 1.f : -1.f;
     } else {
-      ur = lane_xor<3>(u[e]);
+      ur = dpp_mov<kDppRor8>(u[e]);   // lane L ^ 8: dim j + 32 or j - 32
       sg = L < 8 ? -1.f : 1.f;
     }
     v[0][e] = round_bf16(round_bf16(u[e] * cs[e]) + round_bf16(sg * ur * sn[e]));
@@ -147,30 +172,30 @@ DSA_DEV void rope_hadamard_group(float (&v)[2][4], const float (&cs)[4], const f
     v[0][e] = a;
     v[1][e] = b;
   }
-  butterfly_lanes<0>(v, L);
-  butterfly_lanes<1>(v, L);
-  butterfly_lanes<2>(v, L);
-  butterfly_lanes<3>(v, L);
-  constexpr float kNorm = 0.08838834764831845f;   // 128^-0.5
+  hadamard_lanes(v, L);
+  const float norm = hadamard_sign(L) * 0.08838834764831845f;   // +-128^-0.5
+  // v * norm + 0: an exact zero (a zero row, a cancelled sum) leaves as +0 on the lanes with
+  // norm < 0 too, as in the natural-order transform
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[h][e] *= kNorm;
+    for (int e = 0; e < 4; ++e) v[h][e] = fmaf(v[h][e], norm, 0.f);
 }
 
 // One row of a group (fp32 values, rounded to bf16 here): bf16, or e4m3fn of the bf16 values
 // + the row's absmax scale (scale = amax / 448, 1 for a
 // zero row; x / scale clamped to +-448, RNE).  Every lane of the wave takes part (group
-// reductions); only lanes of a valid row store.
+// reductions); only lanes of a valid row store.  The lane's values are output chunk C (dims
+// 4C..4C+3 and 64 + 4C..+3).
 DSA_DEV void store_group_row(float (&v)[2][4], void* out, float* scale_out, int64_t row, bool valid, int L,
-                             int fp8) {
+                             int C, int fp8) {
   if (!fp8) {   // the packing conversion is the bf16 rounding (RNE)
     if (!valid) return;
     uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<bf16_t*>(out) + row * kDi);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      dst[32 * h + 2 * L] = pack_bf16x2(v[h][0], v[h][1]);
-      dst[32 * h + 2 * L + 1] = pack_bf16x2(v[h][2], v[h][3]);
+      dst[32 * h + 2 * C] = pack_bf16x2(v[h][0], v[h][1]);
+      dst[32 * h + 2 * C + 1] = pack_bf16x2(v[h][2], v[h][3]);
     }
     return;
   }
@@ -206,7 +231,7 @@ DSA_DEV void store_group_row(float (&v)[2][4], void* out, float* scale_out, int6
       q[e] = fminf(fmaxf(qc, -448.f), 448.f);
     }
     const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-    dst[16 * h + L] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)lo, true);
+    dst[16 * h + C] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)lo, true);
   }
   if (L == 0) scale_out[row] = scale;
 }
@@ -302,8 +327,9 @@ __global__ __launch_bounds__(256) void indexer_prologue_kernel(PrologueParams p)
       }
     }
     rope_hadamard_group(v, cs, sn, lane, p.deinterleave, p.rotary_interleaved);
-    if (is_k) store_group_row(v, p.k_out, p.k_scale, t, valid, L, p.out_fp8);
-    else store_group_row(v, p.q_out, p.q_scale, (int64_t)t * p.n_heads + r, valid, L, p.out_fp8);
+    const int C = hadamard_chunk(L);
+    if (is_k) store_group_row(v, p.k_out, p.k_scale, t, valid, L, C, p.out_fp8);
+    else store_group_row(v, p.q_out, p.q_scale, (int64_t)t * p.n_heads + r, valid, L, C, p.out_fp8);
   }
 }
 

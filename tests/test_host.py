@@ -180,3 +180,36 @@ def test_e4m3_quotient_from_corrected_reciprocal():
         q = (rem.astype(np.float64) * np.float64(r) + q0.astype(np.float64)).astype(np.float32)
         normal = (np.abs(exact) >= tiny) & ((x == 0) | (np.abs(x) >= 2.0 ** -100))
         assert np.array_equal(q[normal], exact[normal]), float(amax)
+
+
+def test_prologue_hadamard_lane_stages():
+    """The prologue's 128-point Hadamard: in-lane butterflies on dim bits 0, 1, 6, then four
+    cross-lane stages on lane masks 7, 1, 2, 8 (DPP row_half_mirror, quad_perm xor 1 / xor 2,
+    row_ror:8) with pivot bits 2, 0, 1, 3, each x <- x + c * x[partner] (c = -1 where the pivot bit
+    is set).  Lane L must then hold sign(L) * (H y)[dims 4C.., 64 + 4C..] with
+    C = L ^ (((L ^ (L >> 1)) & 1) << 2) and sign(L) = -1 iff (bit 2 and bit 0 != bit 1) xor
+    parity(L) -- the chunk and sign the kernel stores with.  Checked against scipy's Sylvester
+    matrix (natural order) on random rows, in float64 (the float32 kernel rounds the same sums)."""
+    import numpy as np
+    from scipy.linalg import hadamard
+    H = hadamard(128).astype(np.float64)
+    rng = np.random.default_rng(7)
+    partner = [lambda L: (L & 8) | (7 - (L & 7)), lambda L: L ^ 1, lambda L: L ^ 2, lambda L: (L + 8) % 16]
+    pivots = [2, 0, 1, 3]
+    for _ in range(4):
+        x = rng.standard_normal(128)
+        v = np.array([[[x[64 * h + 4 * L + e] for e in range(4)] for h in range(2)] for L in range(16)])
+        for L in range(16):
+            for h in range(2):
+                a, b = v[L, h, 0] + v[L, h, 1], v[L, h, 0] - v[L, h, 1]
+                c, d = v[L, h, 2] + v[L, h, 3], v[L, h, 2] - v[L, h, 3]
+                v[L, h] = [a + c, b + d, a - c, b - d]
+            v[L] = [v[L, 0] + v[L, 1], v[L, 0] - v[L, 1]]
+        for part, piv in zip(partner, pivots):
+            v = np.array([v[L] + (-1.0 if (L >> piv) & 1 else 1.0) * v[part(L)] for L in range(16)])
+        ref = H @ x
+        for L in range(16):
+            C = L ^ (((L ^ (L >> 1)) & 1) << 2)
+            neg = (((L ^ (L >> 1)) & (L >> 2)) ^ bin(L).count("1")) & 1
+            want = np.array([[ref[64 * h + 4 * C + e] for e in range(4)] for h in range(2)])
+            np.testing.assert_allclose(v[L] * (-1.0 if neg else 1.0), want, rtol=0, atol=1e-9)
