@@ -86,7 +86,8 @@ DSA_DEV float group_max(float v) {
 // 8 as XORs would need two DPP moves each; 7 and 8 need one.)  The leading s_nop covers the
 // DPP-read hazards of the asm block (VALU write -> DPP read of the same VGPR: 2 wait states;
 // EXEC write -> DPP: 5); inside the block each value is re-read 8 instructions after its
-// write.  Every lane of the wave executes it (no divergence at the call sites).
+// write, and the trailing s_nop gives a DPP read of the block's results after it its 2 wait
+// states.  Every lane of the wave executes it (no divergence at the call sites).
 DSA_DEV void hadamard_lanes(float (&v)[2][4], int L) {
   const float c0 = (L & 4) ? -1.f : 1.f, c1 = (L & 1) ? -1.f : 1.f;
   const float c2 = (L & 2) ? -1.f : 1.f, c3 = (L & 8) ? -1.f : 1.f;
@@ -104,6 +105,7 @@ DSA_DEV void hadamard_lanes(float (&v)[2][4], int L) {
       DSA_FMAC_DPP("quad_perm:[1,0,3,2]", "%9")
       DSA_FMAC_DPP("quad_perm:[2,3,0,1]", "%10")
       DSA_FMAC_DPP("row_ror:8", "%11")
+      "s_nop 1"
       : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]),
         "+v"(v[1][0]), "+v"(v[1][1]), "+v"(v[1][2]), "+v"(v[1][3])
       : "v"(c0), "v"(c1), "v"(c2), "v"(c3));
