@@ -425,14 +425,26 @@ __global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stag
   const int c = threadIdx.x & 15, r = threadIdx.x >> 4;
   const int64_t a = offsets[s], b = offsets[s + 1];
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t i = a + r; i < b; i += 16) {
-    const u32x4 v = gload16(g_stage + i * kDi + c * 8);
+  auto add_row = [&](const u32x4& v) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       acc[2 * e] += bf16_lo(v[e]);
       acc[2 * e + 1] += bf16_hi(v[e]);
     }
+  };
+  auto load_row = [&](int64_t i) {   // each row is read once: non-temporal
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g_stage + i * kDi + c * 8));
+  };
+  // rows a + r, a + r + 16, ..: four loads in flight per thread, summed in row order
+  int64_t i = a + r;
+  for (; i + 48 < b; i += 64) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = load_row(i + 16 * u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add_row(v[u]);
   }
+  for (; i < b; i += 16) add_row(load_row(i));
   if (r > 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[r - 1][c * 8 + e] = acc[e];

@@ -1076,14 +1076,27 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   const int c = threadIdx.x % kChunks, r = threadIdx.x / kChunks;
   const int64_t a = offsets[s], b = offsets[s + 1];
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int64_t i = a + r; i < b; i += 4) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g_stage + i * kDqk + c * 8));
+  auto add_row = [&](const u32x4& v) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       acc[2 * e] += bf16_lo(v[e]);
       acc[2 * e + 1] += bf16_hi(v[e]);
     }
+  };
+  auto load_row = [&](int64_t i) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g_stage + i * kDqk + c * 8));
+  };
+  // rows a + r, a + r + 4, ..: four loads in flight per thread, summed in row order (a loop of
+  // one load and its adds kept a single 16-byte load per thread in flight)
+  int64_t i = a + r;
+  for (; i + 12 < b; i += 16) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = load_row(i + 4 * u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add_row(v[u]);
   }
+  for (; i < b; i += 4) add_row(load_row(i));
   if (r > 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[r - 1][c * 8 + e] = acc[e];
