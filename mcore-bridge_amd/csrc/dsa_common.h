@@ -94,6 +94,10 @@ DSA_DEV uint32_t pack_bf16x2(float lo, float hi) {
 
 DSA_DEV float bf16_lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
 DSA_DEV float bf16_hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xffff0000u); }
+// max(x, 0) as an integer max of the bit pattern: one v_max_i32 (negative values and -0 give +0;
+// a NaN with the sign bit clear passes through).  fmaxf(x, 0) costs two v_max_f32 in IEEE mode
+// (a NaN-quieting max of x with itself first).
+DSA_DEV float relu_bits(float x) { return __builtin_bit_cast(float, max(__builtin_bit_cast(int, x), 0)); }
 
 // 8x8 transpose of 16-bit elements held as 8 rows x 4 dwords (row r = 8 consecutive
 // elements of one source row).  Output operand t (t = 0..7) gathers element t of each row:

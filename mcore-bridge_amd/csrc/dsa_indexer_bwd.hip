@@ -285,7 +285,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
 #pragma unroll
       for (int mh = 0; mh < 2; ++mh)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sc = __builtin_fmaf(wz[mh][i], fmaxf(z[mh][i], 0.f), sc);
+        for (int i = 0; i < 16; ++i) sc = __builtin_fmaf(wz[mh][i], relu_bits(z[mh][i]), sc);
       sc += __shfl_xor(sc, 32, 64);
       if (hb == 0) sm.row[blk * 32 + hl] = sm.idx[blk * 32 + hl] >= 0 ? sc : -INFINITY;
       continue;
@@ -308,8 +308,8 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
       for (int i = 0; i < 16; i += 2) {
         const float a0 = zt[n][i] > 0.f ? dr[i] : 0.f, a1 = zt[n][i + 1] > 0.f ? dr[i + 1] : 0.f;
         gt[n][i >> 3][(i & 7) >> 1] = pack_bf16x2(a0, a1);
-        dws = __builtin_fmaf(dr[i], fmaxf(zt[n][i], 0.f), dws);
-        dws = __builtin_fmaf(dr[i + 1], fmaxf(zt[n][i + 1], 0.f), dws);
+        dws = __builtin_fmaf(dr[i], relu_bits(zt[n][i]), dws);
+        dws = __builtin_fmaf(dr[i + 1], relu_bits(zt[n][i + 1]), dws);
         const float b0 = z[n][i] > 0.f ? d_own : 0.f, b1 = z[n][i + 1] > 0.f ? d_own : 0.f;
         gz[n][i >> 3][(i & 7) >> 1] = pack_bf16x2(b0, b1);
       }
