@@ -42,6 +42,18 @@ constexpr int kRowsMode = 512;      // at most this many queries (128-dim rows):
 constexpr int kMaxHi = 64;          // indexer heads handled by the register tiling
 }  // namespace
 
+// Slot of 16-byte chunk c of LDS row r is c ^ row_swz<RB>(r).  ds_read_b128 serves 16 lanes per
+// cycle from gfx950's 64 banks (a 256-byte window), and the operand reads here take one chunk of
+// 16 consecutive rows at a time: rows of 256 bytes all start in bank 0, so the 16 rows need 16
+// distinct slots (c ^ (r & 15)); rows of 128 bytes pair up in a window, so rows r and r ^ 1 may
+// share a slot but r and r + 2k may not (c ^ ((r >> 1) & 7)).  (An XOR with r & 7 leaves rows r
+// and r + 8 on the same banks: 2-way conflicts, ~45 % of the LDS cycles in the counters.)
+template <int RB>
+DSA_DEV int row_swz(int r) {
+  static_assert(RB == 256 || RB == 128, "LDS rows of 256 or 128 bytes");
+  return RB == 256 ? (r & 15) : ((r >> 1) & 7);
+}
+
 // sum_e w[0][e] relu(c0[e]) + sum_e w[1][e] relu(c1[e]) for the lane's 16 + 16 accumulator rows
 // (heads): one fma chain, tile 0 then tile 1 (the order of indexer_sel_kernel), ReLU by
 // relu_bits: 2 VALU instructions per head (v_max_i32, v_fmac_f32) instead of ~3.5 (two v_max_f32
@@ -59,7 +71,7 @@ DSA_DEV float weighted_relu_sum(const float (&w)[2][16], const f32x16& c0, const
 // block is copied into LDS once (LDS-direct, 3-stage ring) and all 4 waves take their B
 // operands from there -- loaded per wave, every key row went through the L1 4 times and the
 // key loads alone used the CU's whole 64 B/clk load path.  Row r of a block: 16-byte unit u at
-// slot u ^ (r & 7) (8 consecutive lanes read 8 rows at one unit: conflict-free).  The loop runs
+// slot u ^ row_swz<RB>(r) (16 consecutive lanes read 16 rows at one unit: conflict-free).  The loop runs
 // to the longest of the 4 rows; a wave stores only its own columns.
 template <int DI>
 DSA_DEV void indexer_block_lds(const IndexerParams& p, int t, int c0, int c1_wg, int c1, int base, float (&wr)[2][16],
@@ -80,7 +92,7 @@ DSA_DEV void indexer_block_lds(const IndexerParams& p, int t, int c0, int c1_wg,
       const int ci = wu * CPW + c;           // copy index within the block
       const int r = ci * (1024 / RB) + lane / U, u = lane % U;
       const int key = base + min(k0 + r, c1_wg - 1);
-      async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ (r & 7)),
+      async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ row_swz<RB>(r)),
                              __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)((blk % 3) * BLK + ci * 1024)));
     }
   };
@@ -95,7 +107,7 @@ DSA_DEV void indexer_block_lds(const IndexerParams& p, int t, int c0, int c1_wg,
     u32x4 kb[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      kb[ks] = ks < DI / 16 ? lds_load16(row + 16 * ((2 * ks + hb) ^ (hl & 7))) : u32x4{0, 0, 0, 0};
+      kb[ks] = ks < DI / 16 ? lds_load16(row + 16 * ((2 * ks + hb) ^ row_swz<RB>(hl))) : u32x4{0, 0, 0, 0};
     f32x16 c0a = f32x16{}, c1a = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < DI / 16; ++ks) {
@@ -126,7 +138,7 @@ DSA_DEV i32x8 cat16(const u32x4& lo, const u32x4& hi) {
 // of the bf16 path with 128-byte key rows (4 KB per 32-key block, one 1 KB LDS-direct copy per
 // wave), two 32x32x64 fp8 MFMAs per row tile and block, and the chunk's k_scale values staged in
 // LDS once (I = k_scale[s] * sum_h (w q_scale)[t,h] relu(q8 . k8)).  Row r of a block: 16-byte unit
-// u at slot u ^ (r & 7) (the operand reads of 8 consecutive keys are conflict-free).
+// u at slot u ^ row_swz<128>(r) (the operand reads of 16 consecutive keys are conflict-free).
 DSA_DEV void indexer_block_lds_fp8(const IndexerParams& p, int t, int c0, int c1_wg, int c1, int base,
                                    float (&wr)[2][16], const i32x8 (&qa)[2][2], char* ring, float* ks_s) {
   constexpr int RB = 128, BLK = 32 * RB;
@@ -141,7 +153,7 @@ DSA_DEV void indexer_block_lds_fp8(const IndexerParams& p, int t, int c0, int c1
   auto issue = [&](int blk, int k0) {        // copy wu of the block at key k0: rows 8 wu .. 8 wu + 7
     const int r = wu * 8 + (lane >> 3), u = lane & 7;
     const int key = base + min(k0 + r, c1_wg - 1);
-    async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ (r & 7)),
+    async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ row_swz<RB>(r)),
                            __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)((blk % 3) * BLK + wu * 1024)));
   };
   const int nb = (c1_wg - c0 + 31) / 32;
@@ -156,7 +168,7 @@ DSA_DEV void indexer_block_lds_fp8(const IndexerParams& p, int t, int c0, int c1
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int u0 = 4 * st + 2 * hb;
-      kb[st] = cat16(lds_load16(row + 16 * (u0 ^ (hl & 7))), lds_load16(row + 16 * ((u0 + 1) ^ (hl & 7))));
+      kb[st] = cat16(lds_load16(row + 16 * (u0 ^ row_swz<128>(hl))), lds_load16(row + 16 * ((u0 + 1) ^ row_swz<128>(hl))));
     }
     f32x16 c0a = f32x16{}, c1a = f32x16{};
 #pragma unroll
@@ -339,7 +351,7 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
 }
 
 // Few long rows (decode; bf16, 128-dim rows): one query per workgroup, its 4 waves on 4 consecutive
-// key chunks. The query's Q rows are staged once in LDS (chunk u of head row h at u ^ (h & 7): the
+// key chunks. The query's Q rows are staged once in LDS (chunk u of head row h at u ^ row_swz<256>(h): the
 // A-operand reads of 8 consecutive heads are conflict-free) and its head weights sit in registers.
 // Key rows reach LDS through contiguous LDS-direct copies, 1 KB (4 whole rows) per instruction,
 // into a 2-stage ring per wave. The per-lane row loads of indexer_scores_kernel touch 32 rows of
@@ -349,8 +361,8 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
 // carry the non-temporal hint: each key row is read once, and keeping the stream out of the
 // caches' normal replacement took the cfg5 scan from ~171 to ~151 us.
 __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams p) {
-  // Q rows (chunk u of head row h at u ^ (h & 7)), head weights, and per wave a 2-stage ring of
-  // 32-key blocks (chunk c of key r at c ^ (r & 7)) filled by contiguous LDS-direct copies
+  // Q rows (chunk u of head row h at u ^ row_swz<256>(h)), head weights, and per wave a 2-stage ring of
+  // 32-key blocks (chunk c of key r at c ^ row_swz<256>(r)) filled by contiguous LDS-direct copies
   __shared__ __attribute__((aligned(256))) char qs[kMaxHi * 256];
   __shared__ __attribute__((aligned(256))) char ring[4][2][32 * 256];
   const int lane = threadIdx.x & 63;
@@ -362,7 +374,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
   for (int c = threadIdx.x; c < kMaxHi * 16; c += 256) {
     const int h = c >> 4, u = c & 15;
     const u32x4 v = h < p.n_heads ? gload16(q + (int64_t)h * Di + 8 * u) : u32x4{0, 0, 0, 0};
-    lds_store16(qs + h * 256 + 16 * (u ^ (h & 7)), v);
+    lds_store16(qs + h * 256 + 16 * (u ^ row_swz<256>(h)), v);
   }
   float wr[2][16];   // weights of the accumulator rows: heads 32 mt + (i/4)*8 + 4 hb + i%4
 #pragma unroll
@@ -382,7 +394,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
   const char* kbase = reinterpret_cast<const char*>(p.k);
   const uint32_t ring0 = lds_addr(ring[wave][0]);
   // copy r of a block moves keys 4r .. 4r+3 -- 1 KB contiguous in memory: lane l fills
-  // slot l & 15 of key 4r + l / 16 with that key's chunk (l & 15) ^ (key & 7)
+  // slot l & 15 of key 4r + l / 16 with that key's chunk (l & 15) ^ row_swz<256>(key)
   auto gather = [&](uint32_t dst, int k0) {
     const int kk0 = lane >> 4;
     const uint32_t sl = lane & 15;
@@ -390,7 +402,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
     for (int r = 0; r < 8; ++r) {
       const int kk = 4 * r + kk0;
       const int row = base + min(k0 + kk, c1 - 1);
-      const char* src = kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7));
+      const char* src = kbase + (int64_t)row * RB + 16u * (sl ^ row_swz<256>(kk));
       async_copy16_nt(src, dst + 1024u * r);   // each key row is read once: non-temporal
     }
   };
@@ -409,7 +421,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
     f32x16 c0a = f32x16{}, c1a = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < nks; ++ks) {
-      const uint32_t u = 16u * ((2 * ks + hb) ^ (hl & 7));
+      const uint32_t u = 16u * ((2 * ks + hb) ^ row_swz<256>(hl));
       const u32x4 a0 = lds_load16(lds_ptr(a0b + u)), a1 = lds_load16(lds_ptr(a1b + u));
       const u32x4 b = lds_load16(lds_ptr(kb + u));
       c0a = mfma32x32x16(as_bf16x8(a0), as_bf16x8(b), c0a);
@@ -423,7 +435,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_kernel(IndexerParams 
 
 // Few long rows, fp8 (decode; e4m3fn, 128-dim rows): one query per workgroup as in
 // indexer_scores_rows_kernel, with 128-byte key rows.  A 32-key block is 4 KB of rows (4
-// contiguous 1 KB LDS-direct copies of 8 rows per wave, row r's 16-byte unit u at slot u ^ (r & 7))
+// contiguous 1 KB LDS-direct copies of 8 rows per wave, row r's 16-byte unit u at slot u ^ row_swz<128>(r))
 // plus its 32 key scales (one 4-byte LDS-direct copy per lane: 256 B, lanes >= 32 repeat the
 // last key), through a per-wave ring of kRowsFp8Stages blocks (kRowsFp8Stages - 1 in flight while
 // one is computed; 2, 3, 4 and 6 stages and 512- or 1024-key chunks all measured within 10 % at
@@ -464,7 +476,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_fp8_kernel(IndexerPar
   const char* kbase = reinterpret_cast<const char*>(p.k);
   const uint32_t ring0 = lds_addr(ring[wave][0]);
   // copy r < 4 of a block moves keys 8r .. 8r+7 -- 1 KB contiguous in memory: lane l fills slot
-  // l & 7 of key 8r + l / 8 with that key's unit (l & 7) ^ (key & 7); copy 4 the key scales
+  // l & 7 of key 8r + l / 8 with that key's unit (l & 7) ^ row_swz<128>(key); copy 4 the key scales
   auto gather = [&](int blk) {
     const int k0 = c0 + 32 * blk;
     const uint32_t dst = ring0 + (uint32_t)(blk % NS) * kRowsFp8Block;
@@ -474,7 +486,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_fp8_kernel(IndexerPar
     for (int r = 0; r < 4; ++r) {
       const int kk = 8 * r + kk0;
       const int row = base + min(k0 + kk, c1 - 1);
-      async_copy16_nt(kbase + (int64_t)row * RB + 16u * (sl ^ (kk & 7)), dst + 1024u * r);   // read once
+      async_copy16_nt(kbase + (int64_t)row * RB + 16u * (sl ^ row_swz<128>(kk)), dst + 1024u * r);   // read once
     }
     async_copy4_unordered(p.k_scale + base + min(k0 + hl, c1 - 1), dst + 4096u);
   };
@@ -520,7 +532,7 @@ __global__ __launch_bounds__(256) void indexer_scores_rows_fp8_kernel(IndexerPar
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int u0 = 4 * st + 2 * hb;
-      kb[st] = cat16(lds_load16(row + 16 * (u0 ^ (hl & 7))), lds_load16(row + 16 * ((u0 + 1) ^ (hl & 7))));
+      kb[st] = cat16(lds_load16(row + 16 * (u0 ^ row_swz<128>(hl))), lds_load16(row + 16 * ((u0 + 1) ^ row_swz<128>(hl))));
     }
     const float ksc = *reinterpret_cast<const float*>(lds_ptr(tb + 4096u + 4u * hl));
     f32x16 c0a = f32x16{}, c1a = f32x16{};
