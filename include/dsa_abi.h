@@ -201,7 +201,8 @@ size_t dsa_sparse_mla_bwd_workspace_size_chunked(int total_q, int n_kv, int n_he
  * chunked size of 256 rows) it runs in passes of the most multiples of 256 query rows that fit,
  * in query order, adding each pass's dkv into the previous ones.  dkv is the same bit for bit
  * from run to run for a given workspace size (the per-key sums run in ascending query order);
- * different pass sizes may differ in the last fp32 bits. */
+ * different pass sizes may differ in the last fp32 bits.  total_q == 0 writes dkv = 0 and
+ * touches nothing else (the per-query pointers and the workspace may then be NULL). */
 int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const void* out,
                        const void* dout, const float* lse, int total_q, int n_kv, int n_heads,
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,

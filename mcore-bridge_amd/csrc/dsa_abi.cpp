@@ -363,8 +363,15 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
   if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (n_heads > 128 || n_heads % 16 != 0) return DSA_ERR_UNSUPPORTED;
-  if (!q || !kv || !idx || !out || !dout || !lse || !dq || !dkv) return DSA_ERR_INVALID_ARG;
-  if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(dout) || !aligned16(dq) || !aligned16(dkv))
+  if (!dkv || !aligned16(dkv)) return DSA_ERR_INVALID_ARG;
+  // no query rows: every key's gradient is an empty sum (the per-query buffers and the
+  // workspace are not touched and may be null; the timed variant has no stages to record)
+  if (total_q == 0) {
+    if (stage_events) return DSA_ERR_INVALID_ARG;
+    return dsa::launch_zero_dkv(dkv, n_kv, kDqk, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+  }
+  if (!q || !kv || !idx || !out || !dout || !lse || !dq) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(dout) || !aligned16(dq))
     return DSA_ERR_INVALID_ARG;
   // query rows per pass: all of them when the whole layout fits the workspace, else the most
   // whole units of kBwdChunkUnit rows whose layout fits (the timed variant needs one pass)
@@ -389,7 +396,6 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
   p.lse_stride_t = n_heads; p.dq_stride_t = (int64_t)n_heads * kDqk; p.dkv_stride = kDqk;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  if (total_q == 0) return DSA_OK;
   if (stage_events)
     for (int i = 0; i < 6; ++i)
       if (!stage_events[i]) return DSA_ERR_INVALID_ARG;

@@ -1112,6 +1112,20 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   }
 }
 
+// dKV of a backward with no query rows: every key's sum is empty.  A fill kernel rather than a
+// memset, so a captured graph holds no memset node.
+__global__ __launch_bounds__(256) void zero_rows_kernel(float* rows, int n_rows, int64_t stride, int width) {
+  const int r = blockIdx.x;
+  if (r >= n_rows) return;
+  for (int c = threadIdx.x; c < width; c += 256) rows[(int64_t)r * stride + c] = 0.f;
+}
+
+int launch_zero_dkv(float* dkv, int n_kv, int64_t stride, hipStream_t stream) {
+  if (n_kv <= 0) return 0;
+  hipLaunchKernelGGL(zero_rows_kernel, dim3(n_kv), dim3(256), 0, stream, dkv, n_kv, stride, kDqk);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
                      int t_offset, int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream) {
   const int nr = csr_groups(total_q, n_kv);

@@ -72,6 +72,11 @@ def test_invalid_arguments_rejected_before_launch():
     # backward: heads not a multiple of 16, workspace too small
     assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 24, 576, 512, 8, 0.1, 1, P, P, P, 1 << 30, N) == _lib.DSA_ERR_UNSUPPORTED
     assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 32, 576, 512, 8, 0.1, 1, P, P, P, 16, N) == _lib.DSA_ERR_WORKSPACE
+    # no query rows: dkv is still written (must be given), nothing else is needed; no stages to time
+    assert lib.dsa_sparse_mla_bwd(N, N, N, N, N, N, 0, 4, 32, 576, 512, 8, 0.1, 1, N, N, N, 0, N) == _lib.DSA_ERR_INVALID_ARG
+    ev = (ctypes.c_void_p * 6)(*([P] * 6))
+    assert lib.dsa_sparse_mla_bwd_timed(N, N, N, N, N, N, 0, 4, 32, 576, 512, 8, 0.1, 1, N, P, N, 0, ev, N) == \
+        _lib.DSA_ERR_INVALID_ARG
     # rows: bad n_seq
     assert lib.dsa_build_rows(P, 0, 4, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
 

@@ -641,6 +641,26 @@ def test_sparse_decode_empty_rows():
     _close(lse.cpu()[ok], l_ref[ok], rel=1e-4, name="lse")
 
 
+def test_sparse_fwd_bwd_no_query_rows():
+    """No query rows (an empty batch): the forward returns empty out / lse, the backward an empty
+    dq and dkv = 0 for every key -- written, not left as the allocator's contents (the output
+    buffer is first filled with NaN through a same-size allocation freed just before)."""
+    print("[sparse fwd/bwd no query rows] N=300 H=32 K=64", flush=True)
+    g = torch.Generator().manual_seed(3)
+    kv = (torch.randn(300, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    q = torch.empty(0, 32, 576, dtype=torch.bfloat16, device=DEV)
+    idx = torch.empty(0, 64, dtype=torch.int32, device=DEV)
+    out, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
+    assert out.shape == (0, 32, 512) and lse.shape == (0, 32)
+    junk = torch.full((300, 576), float("nan"), device=DEV)
+    del junk
+    dq, dkv = ops.sparse_mla_bwd(q, kv, idx, out, torch.empty(0, 32, 512, dtype=torch.bfloat16, device=DEV), lse,
+                                 W.SM_SCALE, True)
+    torch.cuda.synchronize()
+    assert dq.shape == (0, 32, 576) and dkv.shape == (300, 576)
+    assert torch.equal(dkv.cpu(), torch.zeros(300, 576))
+
+
 
 def test_sparse_fwd_bwd_cfg3_full_size():
     """cfg3 at the bench's full size (T = 16384 in 4 documents, H = 128, K = 2048, indices from the
