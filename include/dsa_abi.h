@@ -261,7 +261,9 @@ size_t dsa_indexer_scores_bwd_workspace_size(int total_q, int n_k, int topk);
 /* Backward of dsa_indexer_selected_scores (replaces torch autograd through the indexer scores
  * of patcher.py:338-376 for the selected slots) given d_index = dL/dscores [total_q, topk]:
  * dq [total_q, n_heads, 128] fp32, dw [total_q, n_heads] fp32, dk [n_k, 128] fp32 (every row
- * written; rows no query selected are zero).  Shapes and limits as for the forward. */
+ * written; rows no query selected are zero).  Shapes and limits as for the forward.
+ * total_q == 0 writes dk = 0 and touches nothing else (the other pointers and the workspace
+ * may then be NULL). */
 int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const int32_t* idx, const float* d_index,
                            int total_q, int n_k, int n_heads, int head_dim, int topk, int causal, float* dq,
                            float* dw, float* dk, void* workspace, size_t workspace_bytes, void* stream);

@@ -368,7 +368,7 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
   // workspace are not touched and may be null; the timed variant has no stages to record)
   if (total_q == 0) {
     if (stage_events) return DSA_ERR_INVALID_ARG;
-    return dsa::launch_zero_dkv(dkv, n_kv, kDqk, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+    return dsa::launch_zero_rows(dkv, n_kv, kDqk, kDqk, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
   }
   if (!q || !kv || !idx || !out || !dout || !lse || !dq) return DSA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(dout) || !aligned16(dq))
@@ -497,7 +497,10 @@ int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const i
                            float* dw, float* dk, void* workspace, size_t workspace_bytes, void* stream) {
   if (total_q < 0 || n_k < 1 || n_heads < 1 || topk < 1) return DSA_ERR_INVALID_ARG;
   if (head_dim != 128 || n_heads > 64 || topk > 4096) return DSA_ERR_UNSUPPORTED;
-  if (!q || !k || !w || !idx || !d_index || !dq || !dw || !dk) return DSA_ERR_INVALID_ARG;
+  if (!dk) return DSA_ERR_INVALID_ARG;
+  // no query rows: dk = 0 (empty sums); dq and dw are empty, the workspace is not needed
+  if (total_q == 0) return dsa::launch_zero_rows(dk, n_k, head_dim, head_dim, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+  if (!q || !k || !w || !idx || !d_index || !dq || !dw) return DSA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(k) || !aligned16(dq)) return DSA_ERR_INVALID_ARG;
   const IdxBwdLayout L = idx_bwd_layout(total_q, n_k, topk);
   if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) return DSA_ERR_WORKSPACE;

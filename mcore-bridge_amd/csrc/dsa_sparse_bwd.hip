@@ -1112,17 +1112,17 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   }
 }
 
-// dKV of a backward with no query rows: every key's sum is empty.  A fill kernel rather than a
-// memset, so a captured graph holds no memset node.
+// Key gradients of a backward with no query rows: every key's sum is empty.  A fill kernel
+// rather than a memset, so a captured graph holds no memset node.
 __global__ __launch_bounds__(256) void zero_rows_kernel(float* rows, int n_rows, int64_t stride, int width) {
   const int r = blockIdx.x;
   if (r >= n_rows) return;
   for (int c = threadIdx.x; c < width; c += 256) rows[(int64_t)r * stride + c] = 0.f;
 }
 
-int launch_zero_dkv(float* dkv, int n_kv, int64_t stride, hipStream_t stream) {
-  if (n_kv <= 0) return 0;
-  hipLaunchKernelGGL(zero_rows_kernel, dim3(n_kv), dim3(256), 0, stream, dkv, n_kv, stride, kDqk);
+int launch_zero_rows(float* rows, int n_rows, int64_t stride, int width, hipStream_t stream) {
+  if (n_rows <= 0 || width <= 0) return 0;
+  hipLaunchKernelGGL(zero_rows_kernel, dim3(n_rows), dim3(256), 0, stream, rows, n_rows, stride, width);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -158,6 +158,8 @@ def test_indexer_loss_entry_points_validate_and_size():
     assert bwd(P, P, 16) == _lib.DSA_ERR_WORKSPACE
     assert bwd(P, N, 1 << 30) == _lib.DSA_ERR_WORKSPACE
     assert bwd(N, P, 1 << 30) == _lib.DSA_ERR_INVALID_ARG
+    # no query rows: only dk is needed (written as zeros); without it the call is refused
+    assert lib.dsa_indexer_scores_bwd(N, N, N, N, N, 0, 8, 64, 128, 16, 1, N, N, N, N, 0, N) == _lib.DSA_ERR_INVALID_ARG
     # prologue backward: (T + 64) rows of 256 floats of workspace; limits as the forward
     assert lib.dsa_indexer_prologue_bwd_workspace_size(1000) == (1000 + 64) * 256 * 4
     pb = lambda dq, H, ws_, nbytes, stride=64 * 128: lib.dsa_indexer_prologue_bwd(

@@ -100,6 +100,22 @@ def test_indexer_kl_rows(T, K):
     assert kl[4].item() == 0 and torch.all(d[4] == 0)
 
 
+def test_indexer_scores_bwd_no_query_rows():
+    """No query rows: dq and dw are empty and every key's dk is an empty sum, written as 0."""
+    print("[indexer scores bwd no query rows] Nk=300 Hi=64 K=64", flush=True)
+    k = torch.randn(300, 128, device=DEV).bfloat16()
+    q = torch.empty(0, 64, 128, dtype=torch.bfloat16, device=DEV)
+    w = torch.empty(0, 64, device=DEV)
+    idx = torch.empty(0, 64, dtype=torch.int32, device=DEV)
+    d = torch.empty(0, 64, device=DEV)
+    junk = torch.full((300, 128), float("nan"), device=DEV)
+    del junk
+    dq, dw, dk = ops.indexer_scores_bwd(q, k, w, idx, d, True)
+    torch.cuda.synchronize()
+    assert dq.shape == (0, 64, 128) and dw.shape == (0, 64) and dk.shape == (300, 128)
+    assert torch.equal(dk.cpu(), torch.zeros(300, 128))
+
+
 @pytest.mark.parametrize("T,Hi,K,cu", [(300, 64, 256, [0, 300]), (200, 4, 128, [0, 90, 200]),
                                        (260, 64, 2048, [0, 260]), (150, 33, 96, [0, 150])])
 def test_indexer_selected_scores(T, Hi, K, cu):
