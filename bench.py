@@ -459,6 +459,53 @@ def prefill_fwd_leg(torch, dev, name: str, reps: int = 10):
     return res
 
 
+def int8_staging_leg(torch, lib, _lib, q, kv, qi, ki, w, dout, cu_t, max_seqlen, scale, dkv_bf16, ws, stream,
+                     fl_fwd, fl_bwd, t_fwd, t_bwd, reps: int = 5):
+    """The same cfg3 backward with the per-pair dKV rows staged as int8 with a bf16 scale per 32 dims
+    (DSA_BWD_G_INT8, opt-in): per-stage times and the dkv difference from the default bf16 rows
+    (dkv_bf16 of the timed steps; dq does not depend on the format).  Not the headline: the
+    headline backward is the default bf16 staging."""
+    from mcore_bridge_amd import ops
+    T, H, _ = q.shape
+    N, K = kv.shape[0], 2048
+    idx = ops.indexer_topk(qi, ki, w, K, cu_t, True, max_seqlen)
+    out, lse = ops.sparse_mla_fwd(q, kv, idx, scale, True)
+    need = ops.bwd_workspace_bytes(T, N, H, K, g_int8=True)
+    assert need <= ws.numel()
+    dq = torch.empty_like(q)
+    dkv = torch.empty_like(dkv_bf16)
+    stages = ("bwd_pairs", "bwd_sp", "bwd_dq", "bwd_g", "bwd_dkv_reduce")
+    times = {k: [] for k in stages}
+    for r in range(reps + 1):
+        se = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        for e in se:
+            e.record()
+        arr = (ctypes.c_void_p * 6)(*[e.cuda_event for e in se])
+        _lib.check("dsa_sparse_mla_bwd_ex", lib.dsa_sparse_mla_bwd_ex(
+            q.data_ptr(), kv.data_ptr(), idx.data_ptr(), out.data_ptr(), dout.data_ptr(), lse.data_ptr(), T, N, H,
+            576, 512, K, scale, 1, dq.data_ptr(), dkv.data_ptr(), ops.DSA_BWD_G_INT8,
+            ws.data_ptr(), need, arr, stream))
+        torch.cuda.synchronize()
+        if r:
+            for i, k in enumerate(stages):
+                times[k].append(se[i].elapsed_time(se[i + 1]))
+    t = {k: statistics.mean(v) for k, v in times.items()}
+    t_b = sum(t.values())
+    diff = float((dkv - dkv_bf16).norm() / dkv_bf16.norm())
+    return {
+        "note": "opt-in DSA_BWD_G_INT8 (per-pair dKV rows as int8 + bf16 scale per 32 dims, 640 B/row "
+                "instead of 1152); the headline uses the default bf16 rows",
+        "ms": round(t_b, 3),
+        "breakdown_ms": {k: round(v, 3) for k, v in t.items()},
+        "sparse_bwd_tflops": round(fl_bwd / t_b / 1e9, 2),
+        "sparse_fwd_bwd_frac_bf16_peak": round((fl_fwd + fl_bwd) / (t_fwd + t_b) / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "vs_bf16_rows_ms": round(t_bwd, 3),
+        "dkv_normalised_difference_vs_bf16_rows": round(diff, 5),
+        "workspace_bytes": need,
+        "workspace_bytes_bf16_rows": ops.bwd_workspace_bytes(T, N, H, K),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -559,10 +606,6 @@ def main():
     t = {k: avg_ms(k) for k in ev}
     t_fwd, t_idx = t["sparse_fwd"], t["indexer_topk"]
     t_bwd = sum(t[k] for k in STAGES)
-    # Algorithmic work of each hot kernel (one launch per step) and the roofline that bounds it.
-    #   fwd, B1 (S, dP), B2 (dQ): MFMA flops;  B3 (dKV partial rows), B5 (dKV reduce): HBM bytes
-    #   B3 bytes = G rows N_sel*1152 (write) + P, dS N_sel*H*4 + Q, dO T*H*2176 + idx, pair rows T*K*12
-    #   B5 bytes = G rows N_sel*1152 (read) + dKV N_kv*576*4 (write) + key offsets N_kv*8
     # Algorithmic work of each hot kernel (one launch per step) and the roofline that bounds it:
     # the attention products are bf16 MFMA flops (fwd 2176*H, B1 S+dP 2176*H, B2 dQ 1152*H, B3 dKV
     # rows 2176*H per selected pair); B5 streams the per-pair dKV rows, so HBM bytes.  The
@@ -627,6 +670,10 @@ def main():
                      "ms": round(t[dom], 3)},
         "backward_traffic": bwd_traffic,
     }
+    res["sparse_bwd_int8_staging"] = int8_staging_leg(torch, lib, _lib, q, kv, qi, ki, w, dout, cu_t, max_seqlen,
+                                                      scale, dkv, ws, stream, fl_fwd, fl_bwd, t_fwd, t_bwd)
+    print(f"[bench] int8-staging backward leg done: {res['sparse_bwd_int8_staging']['ms']} ms", file=sys.stderr,
+          flush=True)
     if not args.no_decode:
         res["decode"] = decode_leg(torch, dev)
         print(f"[bench] decode leg done: {res['decode']['attention_us']} us", file=sys.stderr, flush=True)

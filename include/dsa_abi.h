@@ -208,6 +208,29 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Flags of dsa_sparse_mla_bwd_ex.
+ * DSA_BWD_G_INT8: stage the per-(query, key) dKV partial rows as int8 with a bf16 scale per 32
+ *   dims (640 bytes a row instead of 1152 in bf16): ~45% less of the backward's largest memory
+ *   traffic and of that part of the workspace, at a larger dkv rounding error (normalised error
+ *   ~0.5% against ~0.16% with bf16 rows, from the int8 steps of max|g|/127 per 32-dim group).
+ *   dq is unchanged; dkv stays the same bit for bit from run to run. */
+#define DSA_BWD_G_INT8 1
+
+/* Workspace bytes for dsa_sparse_mla_bwd_ex with `flags`: chunk_q == 0 for one pass over all
+ * total_q rows, else passes of chunk_q rows (rounded up to a multiple of 256).  0 for invalid
+ * arguments or unknown flags. */
+size_t dsa_sparse_mla_bwd_workspace_size_ex(int total_q, int n_kv, int n_heads, int topk, int chunk_q, int flags);
+
+/* dsa_sparse_mla_bwd with flags (DSA_BWD_G_INT8 or 0) and optional per-stage timing events (see
+ * dsa_sparse_mla_bwd_timed; NULL = untimed).  No reference counterpart for the flags (torch
+ * autograd has no staging); flags == 0 is dsa_sparse_mla_bwd.  Unknown flags:
+ * DSA_ERR_INVALID_ARG. */
+int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, const void* out,
+                          const void* dout, const float* lse, int total_q, int n_kv, int n_heads,
+                          int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
+                          int flags, void* workspace, size_t workspace_bytes, void* const* stage_events,
+                          void* stream);
+
 /* dsa_sparse_mla_bwd with per-stage timing, for profilers and benchmarks (no reference
  * counterpart; the product path is dsa_sparse_mla_bwd).  stage_events: 6 hipEvent_t the caller
  * created with timing enabled, recorded on `stream` before the pair ordering, then after it and

@@ -25,13 +25,16 @@ struct BwdLayout {
   size_t p_stage, ds_stage, g_stage, pair_pos, offsets, counts, total;
 };
 
-BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
+// G row bytes of a backward's flags (format: dsa_kernels.h)
+size_t g_row_bytes(int flags) { return (flags & DSA_BWD_G_INT8) ? dsa::kGRowBytesI8 : dsa::kGRowBytesBf16; }
+
+BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk, int flags = 0) {
   BwdLayout L{};
   const size_t stage = align_up(sizeof(uint16_t) * (size_t)total_q * n_heads * topk_pad(topk));
   size_t off = 0;
   L.p_stage = off; off += stage;
   L.ds_stage = off; off += stage;
-  L.g_stage = off; off += align_up(sizeof(uint16_t) * ((size_t)total_q * topk + 1) * kDqk);
+  L.g_stage = off; off += align_up(g_row_bytes(flags) * ((size_t)total_q * topk + 1));
   L.pair_pos = off; off += align_up(sizeof(int64_t) * (size_t)total_q * topk);
   L.offsets = off; off += align_up(sizeof(int64_t) * ((size_t)n_kv + 1));
   L.counts = off; off += align_up(sizeof(int32_t) * dsa::csr_count_entries(total_q, n_kv));
@@ -42,12 +45,12 @@ BwdLayout bwd_layout(int total_q, int n_kv, int n_heads, int topk) {
 // Query rows per pass of the sparse backward for a workspace of `bytes`: total_q when the whole
 // layout fits, else the most whole units of kBwdChunkUnit rows whose layout fits (0: none).
 constexpr int kBwdChunkUnit = 256;
-int bwd_chunk_rows(int total_q, int n_kv, int n_heads, int topk, size_t bytes) {
-  if (bwd_layout(total_q, n_kv, n_heads, topk).total <= bytes) return total_q;
+int bwd_chunk_rows(int total_q, int n_kv, int n_heads, int topk, size_t bytes, int flags) {
+  if (bwd_layout(total_q, n_kv, n_heads, topk, flags).total <= bytes) return total_q;
   int lo = 0, hi = total_q / kBwdChunkUnit;   // units; layouts grow with the rows
   while (lo < hi) {
     const int mid = (lo + hi + 1) / 2;
-    if (bwd_layout(mid * kBwdChunkUnit, n_kv, n_heads, topk).total <= bytes) lo = mid;
+    if (bwd_layout(mid * kBwdChunkUnit, n_kv, n_heads, topk, flags).total <= bytes) lo = mid;
     else hi = mid - 1;
   }
   return lo * kBwdChunkUnit;
@@ -343,24 +346,38 @@ size_t dsa_sparse_mla_bwd_workspace_size(int total_q, int n_kv, int n_heads, int
 }
 
 size_t dsa_sparse_mla_bwd_workspace_size_chunked(int total_q, int n_kv, int n_heads, int topk, int chunk_q) {
-  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || chunk_q < 1) return 0;
-  const int rows = std::min(total_q, (chunk_q + kBwdChunkUnit - 1) / kBwdChunkUnit * kBwdChunkUnit);
-  return bwd_layout(rows, n_kv, n_heads, topk).total;
+  return dsa_sparse_mla_bwd_workspace_size_ex(total_q, n_kv, n_heads, topk, chunk_q < 1 ? -1 : chunk_q, 0);
+}
+
+size_t dsa_sparse_mla_bwd_workspace_size_ex(int total_q, int n_kv, int n_heads, int topk, int chunk_q, int flags) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || chunk_q < 0 || (flags & ~DSA_BWD_G_INT8)) return 0;
+  const int rows =
+      chunk_q == 0 ? total_q : std::min(total_q, (chunk_q + kBwdChunkUnit - 1) / kBwdChunkUnit * kBwdChunkUnit);
+  return bwd_layout(rows, n_kv, n_heads, topk, flags).total;
 }
 
 int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
                        const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
                        float sm_scale, int causal, void* dq, float* dkv, void* workspace,
                        size_t workspace_bytes, void* stream) {
-  return dsa_sparse_mla_bwd_timed(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale,
-                                  causal, dq, dkv, workspace, workspace_bytes, nullptr, stream);
+  return dsa_sparse_mla_bwd_ex(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale,
+                               causal, dq, dkv, 0, workspace, workspace_bytes, nullptr, stream);
 }
 
 int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, const void* out,
                              const void* dout, const float* lse, int total_q, int n_kv, int n_heads, int d_qk,
                              int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
                              void* workspace, size_t workspace_bytes, void* const* stage_events, void* stream) {
+  return dsa_sparse_mla_bwd_ex(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale,
+                               causal, dq, dkv, 0, workspace, workspace_bytes, stage_events, stream);
+}
+
+int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
+                          const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
+                          float sm_scale, int causal, void* dq, float* dkv, int flags, void* workspace,
+                          size_t workspace_bytes, void* const* stage_events, void* stream) {
   if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
+  if (flags & ~DSA_BWD_G_INT8) return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (n_heads > 128 || n_heads % 16 != 0) return DSA_ERR_UNSUPPORTED;
   if (!dkv || !aligned16(dkv)) return DSA_ERR_INVALID_ARG;
@@ -375,17 +392,18 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
     return DSA_ERR_INVALID_ARG;
   // query rows per pass: all of them when the whole layout fits the workspace, else the most
   // whole units of kBwdChunkUnit rows whose layout fits (the timed variant needs one pass)
-  const int chunk = bwd_chunk_rows(total_q, n_kv, n_heads, topk, workspace_bytes);
+  const int chunk = bwd_chunk_rows(total_q, n_kv, n_heads, topk, workspace_bytes, flags);
   if (!workspace || chunk == 0 || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
   if (stage_events && chunk < total_q) return DSA_ERR_WORKSPACE;
-  const BwdLayout L = bwd_layout(chunk, n_kv, n_heads, topk);
+  const BwdLayout L = bwd_layout(chunk, n_kv, n_heads, topk, flags);
   char* ws = static_cast<char*>(workspace);
   dsa::SparseBwdParams p{};
   p.kv = static_cast<const dsa::bf16_t*>(kv);
   p.dkv = dkv;
   p.p_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.p_stage);
   p.ds_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.ds_stage);
-  p.g_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.g_stage);
+  p.g_stage = ws + L.g_stage;
+  p.g_int8 = (flags & DSA_BWD_G_INT8) ? 1 : 0;
   p.pair_pos = reinterpret_cast<int64_t*>(ws + L.pair_pos);
   p.csr_offsets = reinterpret_cast<int64_t*>(ws + L.offsets);
   p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);

@@ -23,6 +23,18 @@ struct SparseFwdParams {
   float scale_log2;     // softmax scale * log2(e)
 };
 
+// Per-pair dKV partial rows ("G rows") of the sparse backward, written by B3 and summed per key
+// by B5, in one of two formats:
+//   bf16 (default): the 576 dims as bf16, 1152 bytes.
+//   int8 (DSA_BWD_G_INT8): 640 bytes, five 128-byte lines.  Dims are grouped by 32 (groups
+//     0..15 latent, 16..17 rope), each group with its own scale s = max|g| / 127 rounded up to
+//     bf16, so |g / s| <= 127; a dim is stored as u = rint(g / s) + 128 (offset binary, 1..255)
+//     and read back as (u - 128) * s.  Bytes 0..511: latent dims 0..511.  Bytes 512..639: 8
+//     slots of 16 bytes; slot j holds rope dims 512 + 8j .. +7 (8 bytes), then the bf16 scales
+//     of groups 3j, 3j + 1, 3j + 2 (zero past group 17) and 2 zero bytes.
+constexpr int kGRowBytesBf16 = 1152;
+constexpr int kGRowBytesI8 = 640;
+
 struct SparseBwdParams {
   const bf16_t* q;      // [total_q, n_heads, 576]
   const bf16_t* kv;     // [n_kv, 576]
@@ -35,8 +47,10 @@ struct SparseBwdParams {
   // workspace (carved by the C-ABI from one caller buffer)
   bf16_t* p_stage;      // [total_q, topk_pad/32, n_heads, 32]  P (one contiguous tile per key block)
   bf16_t* ds_stage;     // [total_q, topk_pad/32, n_heads, 32]  scale * dS
-  bf16_t* g_stage;      // [total_q * topk + 1, 576] per-pair dKV partial rows, key-major order
+  char* g_stage;        // [total_q * topk + 1] G rows (g_int8 ? kGRowBytesI8 : kGRowBytesBf16
+                        // bytes each), key-major order
   int64_t g_sink_row;   // last row of g_stage: write target of pairs that select nothing
+  int g_int8;           // G row format: 0 bf16, 1 int8 with per-32-dim scales
   int64_t* pair_pos;    // [total_q, topk] row of G for each pair (-1 = not selected)
   int64_t* csr_offsets; // [n_kv + 1]
   int32_t* csr_counts;  // [csr_count_entries(total_q, n_kv)] scratch of the pair ordering

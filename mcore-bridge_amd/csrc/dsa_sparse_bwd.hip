@@ -635,8 +635,46 @@ struct GSmem {
   int32_t pos[kMaxTopkBwd];                         // G row of every index slot (sink if unselected)
   int32_t idx[kMaxTopkBwd];
   int red[4];
+  // int8 G rows: bf16 group scales of wave w's 8 rows of the tile being stored, laid out as the
+  // rows' tail slots (slot j: scales of groups 3j..3j+2, then a zero)
+  alignas(16) uint16_t gexch[4][8][8][4];
 };
 static_assert(sizeof(GSmem) <= 160 * 1024, "B3 LDS budget");
+
+// ---- int8 G rows (format: dsa_kernels.h) ----
+// Largest |x| of 8 values as a bit pattern (for |x| the integer order of the bits is the float
+// order, and integer max needs no NaN handling).
+DSA_DEV uint32_t absmax_bits8(const f32x4& a, const f32x4& b) {
+  auto m = [](float x) { return __builtin_bit_cast(uint32_t, x) & 0x7fffffffu; };
+  const uint32_t x = max(max(m(a[0]), m(a[1])), m(a[2]));
+  const uint32_t y = max(max(m(a[3]), m(b[0])), m(b[1]));
+  return max(max(m(b[2]), m(b[3])), max(x, y));
+}
+// Largest value over each quad of lanes 4k..4k+3 (two DPP quad permutations).
+DSA_DEV uint32_t quad_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // [2,3,0,1]
+  return v;
+}
+// bf16 bits of a group scale: max / 127 rounded up, so every |g / s| <= 127.
+DSA_DEV uint32_t i8_scale_bits(uint32_t max_bits) {
+  const float f = __builtin_bit_cast(float, max_bits) * (1.0f / 127.0f);
+  return (__builtin_bit_cast(uint32_t, f) + 0xffffu) >> 16;
+}
+// 8 values as offset-binary bytes rint(x * inv) + 128.  Adding 1.5 * 2^23 + 128 in the fma
+// rounds x * inv to the nearest integer (ties to even) in the low mantissa bits, whose low byte
+// is then the code (1..255 for |x * inv| <= 127); v_perm_b32 gathers the low bytes.
+DSA_DEV u32x2 i8_pack8(const f32x4& a, const f32x4& b, float inv) {
+  constexpr float kRound = 12582912.0f + 128.0f;
+  auto c = [&](float x) { return __builtin_bit_cast(uint32_t, fmaf(x, inv, kRound)); };
+  auto pack4 = [&](float x0, float x1, float x2, float x3) {
+    // selector byte k picks byte sel of {src1 bytes 0..3, src0 bytes 4..7}; 0x0c gives zero
+    const uint32_t lo = __builtin_amdgcn_perm(c(x1), c(x0), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(c(x3), c(x2), 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  };
+  return u32x2{pack4(a[0], a[1], a[2], a[3]), pack4(b[0], b[1], b[2], b[3])};
+}
 
 // Chunk slot of fp32 G-tile chunk j (4 dims): consecutive-lane reads of 32-byte pieces and
 // same-column writes of 32 rows are both conflict-free.
@@ -644,7 +682,7 @@ DSA_DEV int gtile_slot(int j) { return j ^ ((j >> 3) & 1); }
 
 // KS = head k-steps run per block (a power of two >= n_heads / 16; steps past n_heads multiply
 // zero Q^T / dO^T fragments).
-template <int KS>
+template <int KS, bool I8>
 __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   constexpr int NW = 4;
   constexpr int G = 2 * kGHeads / 16 / NW;          // 4 copies per wave per block
@@ -656,6 +694,8 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   const int g = lane >> 4, gi = lane & 15;
   const int nks = p.n_heads / 16;
   const int wu = __builtin_amdgcn_readfirstlane(wave);
+  if constexpr (I8)   // slots never written (pads, groups past 17) stay zero
+    *reinterpret_cast<u32x2*>(&sm.gexch[wave][lane >> 3][lane & 7][0]) = u32x2{0, 0};
 
   // ---- setup copies: round r = heads 16r..16r+15 into ring[r % 3]; copy j (1 KB of LDS) is
   // Q bytes 1024j of the round for j < 18, dO bytes 1024(j - 18) after; wave w issues copies
@@ -816,12 +856,31 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
                      *reinterpret_cast<const f32x4*>(r + 16 * gtile_slot(j + 1))};
   };
   auto store_issue = [&](const int32_t (&rpos)[8], int32_t rope_pos, int i, const StoreData& v) {
-    const u32x4 o{pack_bf16x2(v.a[0], v.a[1]), pack_bf16x2(v.a[2], v.a[3]), pack_bf16x2(v.b[0], v.b[1]),
-                  pack_bf16x2(v.b[2], v.b[3])};
-    if (i < 8)
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rpos[i] * kDqk + 8 * lane));
-    else
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))));
+    if constexpr (!I8) {
+      const u32x4 o{pack_bf16x2(v.a[0], v.a[1]), pack_bf16x2(v.a[2], v.a[3]), pack_bf16x2(v.b[0], v.b[1]),
+                    pack_bf16x2(v.b[2], v.b[3])};
+      bf16_t* g = reinterpret_cast<bf16_t*>(p.g_stage);
+      if (i < 8)
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(g + (int64_t)rpos[i] * kDqk + 8 * lane));
+      else
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(g + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))));
+    } else {
+      // one 32-dim group per lane quad: its scale from the quad's largest |g|
+      const uint32_t sb = i8_scale_bits(quad_max_u32(absmax_bits8(v.a, v.b)));
+      const float inv = sb ? __builtin_amdgcn_rcpf(__builtin_bit_cast(float, sb << 16)) : 0.f;
+      const u32x2 q = i8_pack8(v.a, v.b, inv);
+      if (i < 8) {   // latent dims 8*lane..+7 of row 8w + i: group lane / 4
+        const int gq = lane >> 2;
+        if ((lane & 3) == 0) sm.gexch[wave][i][gq / 3][gq % 3] = (uint16_t)sb;
+        __builtin_nontemporal_store(q, reinterpret_cast<u32x2*>(p.g_stage + (int64_t)rpos[i] * kGRowBytesI8 + 8 * lane));
+      } else {       // rope dims 8j..+7 of row 8w + r: group 16 + j / 4, then the row's tail slot j
+        const int r = lane >> 3, j = lane & 7;
+        if ((lane & 3) == 0) sm.gexch[wave][r][5][1 + (j >> 2)] = (uint16_t)sb;
+        const u32x2 sc = *reinterpret_cast<const u32x2*>(&sm.gexch[wave][r][j][0]);   // after every write
+        __builtin_nontemporal_store(u32x4{q[0], q[1], sc[0], sc[1]},
+                                    reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kGRowBytesI8 + 512 + 16 * j));
+      }
+    }
   };
   // k-step of copy c (c < G) and of store i (i < kGStores); stores follow copies in a step
   constexpr auto copy_ks = [](int c) { return c * KS / G; };
@@ -1112,6 +1171,57 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   }
 }
 
+// B5 over int8 G rows (format: dsa_kernels.h): the same per-key sums in the same row order, each
+// value dequantised exactly ((u - 128) * s is a 16-bit product, so the fma is exact).
+__global__ __launch_bounds__(288) void bwd_dkv_reduce_i8_kernel(const char* g_rows, const int64_t* offsets,
+                                                                int n_kv, float* dkv, int64_t dkv_stride,
+                                                                int accumulate) {
+  __shared__ float red[3][kDqk];
+  const int s = blockIdx.x;
+  if (s >= n_kv) return;
+  constexpr int kChunks = kDqk / 8;
+  const int c = threadIdx.x % kChunks, r = threadIdx.x / kChunks;
+  // chunk c (dims 8c..8c+7): its bytes and its group's scale inside a row
+  const int grp = c < 64 ? c >> 2 : 16 + ((c - 64) >> 2);
+  const int data_off = c < 64 ? 8 * c : 512 + 16 * (c - 64);
+  const int scale_off = 512 + 16 * (grp / 3) + 8 + 2 * (grp % 3);
+  const int64_t a = offsets[s], b = offsets[s + 1];
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  struct Row { u32x2 v; uint32_t sb; };
+  auto load_row = [&](int64_t i) {
+    const char* row = g_rows + i * kGRowBytesI8;
+    return Row{__builtin_nontemporal_load(reinterpret_cast<const u32x2*>(row + data_off)),
+               __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(row + scale_off))};
+  };
+  auto add_row = [&](const Row& x) {
+    const float sc = __builtin_bit_cast(float, x.sb << 16), nb = -128.f * sc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += fmaf((float)((x.v[e >> 2] >> (8 * (e & 3))) & 0xffu), sc, nb);
+  };
+  int64_t i = a + r;
+  for (; i + 12 < b; i += 16) {
+    Row v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = load_row(i + 4 * u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add_row(v[u]);
+  }
+  for (; i < b; i += 4) add_row(load_row(i));
+  if (r > 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[r - 1][c * 8 + e] = acc[e];
+  }
+  __syncthreads();
+  if (r == 0) {
+    float* out = dkv + (int64_t)s * dkv_stride + c * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = acc[e] + red[0][c * 8 + e] + red[1][c * 8 + e] + red[2][c * 8 + e];
+      out[e] = accumulate ? out[e] + v : v;
+    }
+  }
+}
+
 // Key gradients of a backward with no query rows: every key's sum is empty.  A fill kernel
 // rather than a memset, so a captured graph holds no memset node.
 __global__ __launch_bounds__(256) void zero_rows_kernel(float* rows, int n_rows, int64_t stride, int width) {
@@ -1169,17 +1279,27 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   mark(3);
   const int nks = p.n_heads / 16;
   const dim3 ggrid(xcd_grid(p.total_q));
-  if (nks > 4)
-    hipLaunchKernelGGL(bwd_g_kernel<8>, ggrid, dim3(256), 0, stream, p);
-  else if (nks > 2)
-    hipLaunchKernelGGL(bwd_g_kernel<4>, ggrid, dim3(256), 0, stream, p);
-  else if (nks > 1)
-    hipLaunchKernelGGL(bwd_g_kernel<2>, ggrid, dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(bwd_g_kernel<1>, ggrid, dim3(256), 0, stream, p);
+  auto launch_g = [&](auto i8) {
+    constexpr bool I8 = decltype(i8)::value;
+    if (nks > 4)
+      hipLaunchKernelGGL((bwd_g_kernel<8, I8>), ggrid, dim3(256), 0, stream, p);
+    else if (nks > 2)
+      hipLaunchKernelGGL((bwd_g_kernel<4, I8>), ggrid, dim3(256), 0, stream, p);
+    else if (nks > 1)
+      hipLaunchKernelGGL((bwd_g_kernel<2, I8>), ggrid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((bwd_g_kernel<1, I8>), ggrid, dim3(256), 0, stream, p);
+  };
+  if (p.g_int8) launch_g(std::true_type{});
+  else launch_g(std::false_type{});
   mark(4);
-  hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets, p.n_kv,
-                     p.dkv, p.dkv_stride, p.dkv_accumulate);
+  if (p.g_int8)
+    hipLaunchKernelGGL(bwd_dkv_reduce_i8_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets,
+                       p.n_kv, p.dkv, p.dkv_stride, p.dkv_accumulate);
+  else
+    hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream,
+                       reinterpret_cast<const bf16_t*>(p.g_stage), p.csr_offsets, p.n_kv, p.dkv, p.dkv_stride,
+                       p.dkv_accumulate);
   mark(5);
   return hipGetLastError() == hipSuccess && marks_ok ? 0 : -4;
 }

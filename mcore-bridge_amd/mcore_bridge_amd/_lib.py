@@ -61,6 +61,10 @@ SIGNATURES = {
     "dsa_sparse_mla_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_void_p,
                                    c_size_t, c_void_p]),
+    "dsa_sparse_mla_bwd_workspace_size_ex": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "dsa_sparse_mla_bwd_ex": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                      c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p, c_int,
+                                      c_void_p, c_size_t, c_void_p, c_void_p]),
     "dsa_sparse_mla_bwd_timed": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                          c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p,
                                          c_void_p, c_size_t, c_void_p, c_void_p]),

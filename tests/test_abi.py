@@ -91,6 +91,31 @@ def test_bwd_workspace_size_formula():
     fixed = 2 * stage + T * K * 576 * 2 + T * K * 8 + (N + 1) * 8 + 257 * N * 4
     assert fixed <= ws < fixed + 4096
     assert lib.dsa_sparse_mla_bwd_workspace_size(-1, N, H, K) == 0
+    # the flags form: one pass (chunk_q = 0) with bf16 rows is the same layout; int8 rows are
+    # 640 bytes (5 lines) instead of 1152; passes round up to 256 rows; unknown flags size 0
+    assert lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, 0, 0) == ws
+    ws8 = lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, 0, 1)
+    assert ws - ws8 == (T * K + 1) * (1152 - 640)
+    assert lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, 300, 0) == \
+        lib.dsa_sparse_mla_bwd_workspace_size_chunked(T, N, H, K, 512)
+    assert lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, 300, 1) < \
+        lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, 300, 0)
+    assert lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, 0, 2) == 0
+    assert lib.dsa_sparse_mla_bwd_workspace_size_ex(T, N, H, K, -1, 0) == 0
+
+
+def test_bwd_flags_validated_before_launch():
+    lib = _lib.load()
+    big = 1 << 40
+    # unknown flag bits, also with no query rows
+    assert lib.dsa_sparse_mla_bwd_ex(P, P, P, P, P, P, 4, 4, 32, 576, 512, 8, 0.1, 1, P, P, 2, P, big, N, N) == \
+        _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_sparse_mla_bwd_ex(N, N, N, N, N, N, 0, 4, 32, 576, 512, 8, 0.1, 1, N, P, 4, N, 0, N, N) == \
+        _lib.DSA_ERR_INVALID_ARG
+    # an int8-row workspace one byte short of the smallest pass is refused
+    need = lib.dsa_sparse_mla_bwd_workspace_size_ex(4, 4, 32, 8, 256, 1)
+    assert lib.dsa_sparse_mla_bwd_ex(P, P, P, P, P, P, 4, 4, 32, 576, 512, 8, 0.1, 1, P, P, 1, P, need - 1, N, N) == \
+        _lib.DSA_ERR_WORKSPACE
 
 
 def test_decode_entry_points_validate_and_size():
