@@ -70,11 +70,19 @@ DSA_DEV float group_sum(float v) {
   v += dpp_mov<kDppXor2>(v);
   return v + dpp_mov<kDppRor8>(v);
 }
-DSA_DEV float group_max(float v) {
-  v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_mov<kDppXor1>(v));
-  v = fmaxf(v, dpp_mov<kDppXor2>(v));
-  return fmaxf(v, dpp_mov<kDppRor8>(v));
+// Largest of non-negative values (|x|): their bit patterns order as unsigned integers, so each
+// step is one v_max_u32 with a DPP source (a float max would first quiet NaNs with an extra
+// v_max per step).
+template <int CTRL>
+DSA_DEV uint32_t dpp_mov_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+DSA_DEV float group_max_nonneg(float x) {
+  uint32_t v = __builtin_bit_cast(uint32_t, x);
+  v = max(v, dpp_mov_u<kDppHalfMirror>(v));
+  v = max(v, dpp_mov_u<kDppXor1>(v));
+  v = max(v, dpp_mov_u<kDppXor2>(v));
+  return __builtin_bit_cast(float, max(v, dpp_mov_u<kDppRor8>(v)));
 }
 
 // The Hadamard's 16-point transform over the lane bits as four butterfly stages on lane masks
@@ -214,14 +222,28 @@ DSA_DEV void store_group_row(float (&v)[2][4], void* out, float* scale_out, int6
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[h][e]));
-  const float amax = group_max(m);
+  const float amax = group_max_nonneg(m);
   if (!valid) return;
-  const float scale = amax > 0.f ? amax / 448.f : 1.f;
+  // scale = RN(amax / 448) and rcp = RN(1 / scale) without IEEE division sequences: amax times
+  // RN(1/448) plus one exact-remainder correction is the correctly rounded quotient, and one fma
+  // Newton step from v_rcp_f32 (within 1 ulp) the correctly rounded reciprocal.  Both hold for
+  // every positive bf16 amax >= 2^-100 (checked exhaustively on the host with exact arithmetic,
+  // reciprocal seeds up to 1 ulp off); smaller rows take the division.
+  float scale, rcp;
+  if (amax >= 0x1p-100f) {
+    constexpr float kInv448 = 1.f / 448.f;
+    const float s0 = amax * kInv448;
+    scale = fmaf(fmaf(-s0, 448.f, amax), kInv448, s0);
+    const float y0 = __builtin_amdgcn_rcpf(scale);
+    rcp = fmaf(fmaf(-scale, y0, 1.f), y0, y0);
+  } else {
+    scale = amax > 0.f ? amax / 448.f : 1.f;
+    rcp = 1.f / scale;
+  }
   // x / scale correctly rounded from the correctly rounded reciprocal plus one exact-remainder
   // correction (Markstein): the remainder x - q0 * scale is exact in an fma, and
   // q0 + rem * (1 / scale) rounds to the nearest quotient -- for |x| >= 2^-100 and normal
   // quotients; below that the remainder underflows and the result may be an ulp off.
-  const float rcp = 1.f / scale;
   uint32_t* dst = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out) + row * kDi);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {

@@ -182,6 +182,52 @@ def test_e4m3_quotient_from_corrected_reciprocal():
         assert np.array_equal(q[normal], exact[normal]), float(amax)
 
 
+def _rn32(x):
+    """Round a rational to the nearest binary32 (ties to even), normals and subnormals."""
+    from fractions import Fraction as F
+    if x == 0:
+        return F(0)
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if F(2) ** e > a:
+        e -= 1
+    e = max(e, -126)
+    q = a / F(2) ** (e - 23)
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > F(1, 2) or (rem == F(1, 2) and n % 2 == 1):
+        n += 1
+    return (1 if x > 0 else -1) * F(n) * F(2) ** (e - 23)
+
+
+def test_e4m3_row_scale_and_reciprocal_without_division():
+    """The fp8 prologue takes a row's scale RN(amax / 448) as fma(fma(-s0, 448, amax), R, s0)
+    with R = RN(1/448) and s0 = RN(amax * R), and its reciprocal RN(1 / scale) as one fma Newton
+    step fma(fma(-scale, y0, 1), y0, y0) from v_rcp_f32's y0 (documented within 1 ulp).  Checked
+    with exact rational arithmetic over every positive finite bf16 amax (the row maxima are bf16
+    values): the scale always equals the correctly rounded quotient, and the reciprocal equals
+    the correctly rounded one for every seed within 1 ulp wherever amax >= 2^-100 (the kernel
+    divides below that)."""
+    import math
+    from fractions import Fraction as F
+    import numpy as np
+    R = _rn32(F(1, 448))
+    assert float(R) == float(np.float32(1.0 / 448.0))
+    vals = (np.arange(1, 0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    for a in vals:
+        amax = F(float(a))
+        s0 = _rn32(amax * R)
+        s = _rn32(_rn32(amax - s0 * 448) * R + s0)
+        assert s == _rn32(amax / 448), float(a)
+        if float(a) < 2.0 ** -100:
+            continue
+        y = _rn32(1 / s)
+        ulp = F(2) ** (math.frexp(float(y))[1] - 24)
+        for k in (-1, 0, 1):
+            y0 = y + k * ulp
+            assert _rn32(_rn32(1 - s * y0) * y0 + y0) == y, (float(a), k)
+
+
 def test_prologue_hadamard_lane_stages():
     """The prologue's 128-point Hadamard: in-lane butterflies on dim bits 0, 1, 6, then four
     cross-lane stages on lane masks 7, 1, 2, 8 (DPP row_half_mirror, quad_perm xor 1 / xor 2,
