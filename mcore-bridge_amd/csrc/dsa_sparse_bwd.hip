@@ -1171,54 +1171,81 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
   }
 }
 
-// B5 over int8 G rows (format: dsa_kernels.h): the same per-key sums in the same row order, each
-// value dequantised exactly ((u - 128) * s is a 16-bit product, so the fma is exact).
-__global__ __launch_bounds__(288) void bwd_dkv_reduce_i8_kernel(const char* g_rows, const int64_t* offsets,
+// B5 over int8 G rows (format: dsa_kernels.h): the same per-key sums in a fixed order, each value
+// dequantised exactly ((u - 128) * s is a 16-bit product, so the fma is exact).  Latent part:
+// one wave per row, lane l dims 8l..8l+7 (8 bytes, group l / 4), wave w rows a + w, a + w + 4, ..
+// (eight in flight), so each 128-byte line is read by one wave (rows cut across waves mid-line
+// were fetched twice).  Rope part (the 128-byte tail line: 8 bytes of slot j = rope dims
+// 512 + 8j.., group 16 + j / 4): thread t takes slot t % 8 of rows a + t / 8, a + t / 8 + 32, ..
+// Then the four waves' latent sums, and the 32 rope partials of each slot, are added in a fixed
+// order.
+__global__ __launch_bounds__(256) void bwd_dkv_reduce_i8_kernel(const char* g_rows, const int64_t* offsets,
                                                                 int n_kv, float* dkv, int64_t dkv_stride,
                                                                 int accumulate) {
-  __shared__ float red[3][kDqk];
+  __shared__ float red[3][512];
+  __shared__ float rred[32][64];
   const int s = blockIdx.x;
   if (s >= n_kv) return;
-  constexpr int kChunks = kDqk / 8;
-  const int c = threadIdx.x % kChunks, r = threadIdx.x / kChunks;
-  // chunk c (dims 8c..8c+7): its bytes and its group's scale inside a row
-  const int grp = c < 64 ? c >> 2 : 16 + ((c - 64) >> 2);
-  const int data_off = c < 64 ? 8 * c : 512 + 16 * (c - 64);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int grp = lane >> 2;
   const int scale_off = 512 + 16 * (grp / 3) + 8 + 2 * (grp % 3);
+  const int rj = tid & 7, rgrp = 16 + (rj >> 2);
+  const int rscale_off = 512 + 16 * (rgrp / 3) + 8 + 2 * (rgrp % 3);
   const int64_t a = offsets[s], b = offsets[s + 1];
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  struct Row { u32x2 v; uint32_t sb; };
-  auto load_row = [&](int64_t i) {
-    const char* row = g_rows + i * kGRowBytesI8;
-    return Row{__builtin_nontemporal_load(reinterpret_cast<const u32x2*>(row + data_off)),
-               __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(row + scale_off))};
-  };
-  auto add_row = [&](const Row& x) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, racc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  struct Part { u32x2 v; uint32_t sb; };
+  auto add8 = [](float (&dst)[8], const Part& x) {
     const float sc = __builtin_bit_cast(float, x.sb << 16), nb = -128.f * sc;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += fmaf((float)((x.v[e >> 2] >> (8 * (e & 3))) & 0xffu), sc, nb);
+    for (int e = 0; e < 8; ++e) dst[e] += fmaf((float)((x.v[e >> 2] >> (8 * (e & 3))) & 0xffu), sc, nb);
   };
-  int64_t i = a + r;
-  for (; i + 12 < b; i += 16) {
-    Row v[4];
+  auto latent = [&](int64_t i) {
+    const char* row = g_rows + i * kGRowBytesI8;
+    return Part{__builtin_nontemporal_load(reinterpret_cast<const u32x2*>(row + 8 * lane)),
+                *reinterpret_cast<const uint16_t*>(row + scale_off)};
+  };
+  auto ropepart = [&](int64_t i) {
+    const char* row = g_rows + i * kGRowBytesI8;
+    return Part{*reinterpret_cast<const u32x2*>(row + 512 + 16 * rj), *reinterpret_cast<const uint16_t*>(row + rscale_off)};
+  };
+  int64_t i = a + w;
+  for (; i + 28 < b; i += 32) {
+    Part v[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = load_row(i + 4 * u);
+    for (int u = 0; u < 8; ++u) v[u] = latent(i + 4 * u);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) add_row(v[u]);
+    for (int u = 0; u < 8; ++u) add8(acc, v[u]);
   }
-  for (; i < b; i += 4) add_row(load_row(i));
-  if (r > 0) {
+  for (; i < b; i += 4) add8(acc, latent(i));
+  int64_t r = a + (tid >> 3);
+  for (; r + 96 < b; r += 128) {
+    Part v[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[r - 1][c * 8 + e] = acc[e];
+    for (int u = 0; u < 4; ++u) v[u] = ropepart(r + 32 * u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) add8(racc, v[u]);
   }
+  for (; r < b; r += 32) add8(racc, ropepart(r));
+  if (w > 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[w - 1][8 * lane + e] = acc[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) rred[tid >> 3][8 * rj + e] = racc[e];
   __syncthreads();
-  if (r == 0) {
-    float* out = dkv + (int64_t)s * dkv_stride + c * 8;
+  float* out = dkv + (int64_t)s * dkv_stride;
+  if (w == 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float v = acc[e] + red[0][c * 8 + e] + red[1][c * 8 + e] + red[2][c * 8 + e];
-      out[e] = accumulate ? out[e] + v : v;
+      const int d = 8 * lane + e;
+      const float v = acc[e] + red[0][d] + red[1][d] + red[2][d];
+      out[d] = accumulate ? out[d] + v : v;
     }
+  } else if (w == 1) {   // rope dim 512 + lane: the 32 row-offset partials in order
+    float v = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < 32; ++k) v += rred[k][lane];
+    out[512 + lane] = accumulate ? out[512 + lane] + v : v;
   }
 }
 
@@ -1294,7 +1321,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   else launch_g(std::false_type{});
   mark(4);
   if (p.g_int8)
-    hipLaunchKernelGGL(bwd_dkv_reduce_i8_kernel, dim3(p.n_kv), dim3(288), 0, stream, p.g_stage, p.csr_offsets,
+    hipLaunchKernelGGL(bwd_dkv_reduce_i8_kernel, dim3(p.n_kv), dim3(256), 0, stream, p.g_stage, p.csr_offsets,
                        p.n_kv, p.dkv, p.dkv_stride, p.dkv_accumulate);
   else
     hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream,
