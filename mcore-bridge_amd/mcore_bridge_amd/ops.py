@@ -466,16 +466,23 @@ def set_backward_staging(g_rows: str) -> None:
     """Format of the per-pair dkv partial rows the autograd backward of ``sparse_mla_fwd`` stages:
     ``"bf16"`` (the default) or ``"int8"`` (a bf16 scale per 32 dims: ~45% less of the backward's
     largest memory traffic and workspace; dkv normalised error ~0.5% instead of ~0.16%, dq
-    unchanged)."""
+    unchanged).  ``sparse_mla_bwd_with_target`` (the indexer loss's target from the backward's P
+    tiles) always stages bf16 rows."""
     if g_rows not in ("bf16", "int8"):
         raise ValueError(f"g_rows must be 'bf16' or 'int8', got {g_rows!r}")
     _BWD_G_INT8[0] = g_rows == "int8"
 
 
+def autograd_backward(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sm_scale: float,
+                      causal: bool) -> Tuple[Tensor, Tensor]:
+    """``sparse_mla_bwd`` with the settings of ``set_backward_workspace_limit`` and
+    ``set_backward_staging``: what every autograd backward over these kernels calls."""
+    return sparse_mla_bwd(q, kv, idx, out, dout, lse, sm_scale, causal, _BWD_WORKSPACE_LIMIT[0], _BWD_G_INT8[0])
+
+
 def _fwd_backward(ctx, dout, dlse):
     q, kv, idx, out, lse = ctx.saved_tensors
-    dq, dkv = sparse_mla_bwd(q, kv, idx, out, dout, lse, ctx.sm_scale, ctx.causal, _BWD_WORKSPACE_LIMIT[0],
-                             _BWD_G_INT8[0])
+    dq, dkv = autograd_backward(q, kv, idx, out, dout, lse, ctx.sm_scale, ctx.causal)
     return dq, dkv.to(kv.dtype), None, None, None
 
 

@@ -62,7 +62,7 @@ class _SinkAttention(torch.autograd.Function):
         q_p, kv_p, idx, out_s, lse_s, sinks = ctx.saved_tensors
         dq = dkv = dsinks = None
         if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-            dq_p, dkv_p = ops.sparse_mla_bwd(q_p, kv_p, idx, out_s, dout.contiguous(), lse_s, ctx.scale, False)
+            dq_p, dkv_p = ops.autograd_backward(q_p, kv_p, idx, out_s, dout.contiguous(), lse_s, ctx.scale, False)
             dq, dkv = dq_p[..., :HEAD_DIM], dkv_p[:, :HEAD_DIM].to(ctx.kv_dtype)
         if ctx.needs_input_grad[2]:
             delta = (dout.float() * out_s.float()).sum(-1)                       # [T, H]
