@@ -123,3 +123,35 @@ def test_int8_staging_through_autograd():
     assert torch.equal(kvg.grad, dkv8.to(torch.bfloat16).float())
     with pytest.raises(ValueError):
         ops.set_backward_staging("fp8")
+
+
+def test_int8_staging_in_the_v4_sink_attention_backward():
+    """The DeepSeek-V4 sink attention's backward runs the same kernels through
+    ops.autograd_backward, so the staging setting reaches it: dq identical to bf16 staging, dkv
+    within the gradient bars of it."""
+    from mcore_bridge_amd import v4
+    T, H, K = 256, 32, 64
+    print(f"[int8 staging v4 sink attention] T={T} H={H} K={K}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    q = (torch.randn(T, H, 512, generator=g) * 0.1).bfloat16().to(DEV)
+    kv = (torch.randn(T, 512, generator=g) * 0.1).bfloat16().to(DEV)
+    sinks = (torch.randn(H, generator=g) * 0.5).to(DEV)
+    idx = torch.full((T, K), -1, dtype=torch.int32)
+    for t in range(T):
+        sel = torch.randperm(t + 1, generator=g)[:K]
+        idx[t, :sel.numel()] = torch.sort(sel).values.to(torch.int32)
+    idx = idx.to(DEV)
+    dout = (torch.randn(T, H, 512, generator=g) * 0.01).bfloat16().to(DEV)
+    grads = {}
+    for fmt in ("bf16", "int8"):
+        ops.set_backward_staging(fmt)
+        try:
+            qg, kg = q.clone().requires_grad_(), kv.clone().requires_grad_()
+            out, _ = v4.sink_attention(qg, kg, sinks, idx, 512 ** -0.5)
+            out.backward(dout)
+        finally:
+            ops.set_backward_staging("bf16")
+        grads[fmt] = (qg.grad, kg.grad)
+    assert torch.equal(grads["int8"][0], grads["bf16"][0])
+    assert not torch.equal(grads["int8"][1], grads["bf16"][1]), "int8 staging did not reach the V4 backward"
+    _close(grads["int8"][1], grads["bf16"][1], name="dkv (int8 vs bf16 rows)")
