@@ -1208,24 +1208,22 @@ __global__ __launch_bounds__(256) void bwd_dkv_reduce_i8_kernel(const char* g_ro
     const char* row = g_rows + i * kGRowBytesI8;
     return Part{*reinterpret_cast<const u32x2*>(row + 512 + 16 * rj), *reinterpret_cast<const uint16_t*>(row + rscale_off)};
   };
-  int64_t i = a + w;
-  for (; i + 28 < b; i += 32) {
+  // Chunks of 32 rows: wave w takes the latent parts of rows c+w, c+w+4, ..., thread t the rope
+  // slot t%8 of row c+t/8.  Both parts of a chunk are loaded together, so the rope loads find the
+  // tail lines the scale loads have just brought into the L2 (a second pass over the key's rows
+  // would fetch every tail line twice).  Each thread still adds its rows in ascending order.
+  int64_t c = a;
+  for (; c + 31 < b; c += 32) {
     Part v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = latent(i + 4 * u);
+    for (int u = 0; u < 8; ++u) v[u] = latent(c + w + 4 * u);
+    const Part rp = ropepart(c + (tid >> 3));
 #pragma unroll
     for (int u = 0; u < 8; ++u) add8(acc, v[u]);
+    add8(racc, rp);
   }
-  for (; i < b; i += 4) add8(acc, latent(i));
-  int64_t r = a + (tid >> 3);
-  for (; r + 96 < b; r += 128) {
-    Part v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = ropepart(r + 32 * u);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) add8(racc, v[u]);
-  }
-  for (; r < b; r += 32) add8(racc, ropepart(r));
+  for (int64_t i = c + w; i < b; i += 4) add8(acc, latent(i));
+  for (int64_t r = c + (tid >> 3); r < b; r += 32) add8(racc, ropepart(r));
   if (w > 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[w - 1][8 * lane + e] = acc[e];
