@@ -181,6 +181,8 @@ struct IdxSelParams {
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
 // ev (nullable): 6 events recorded around the stages B4 | B1 | B2 | B3 | B5.
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev);
+// B3 with int8 G rows (p.g_int8), launched by launch_sparse_mla_bwd.
+void launch_bwd_g_i8(const SparseBwdParams& p, hipStream_t stream);
 int launch_zero_rows(float* rows, int n_rows, int64_t stride, int width, hipStream_t stream);
 int launch_indexer_scores(const IndexerParams& p, hipStream_t stream);
 int launch_topk(const TopkParams& p, hipStream_t stream);
