@@ -12,8 +12,6 @@
 
 namespace dsa {
 
-namespace {
-
 constexpr int kDqk = 576;
 constexpr int kDv = 512;
 constexpr int kBK = kTileKeys;
@@ -28,8 +26,6 @@ DSA_DEV u32x2 lds_read_tr16(const char* p) {
   s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
   return __builtin_bit_cast(u32x2, r);
 }
-
-}  // namespace
 
 // ------------------------------------------------------------------------------------------
 // B3: per-pair dKV partial rows G = (scale*dS)^T Q + P^T dO, contracted over all heads.
