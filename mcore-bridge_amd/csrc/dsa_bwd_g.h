@@ -421,41 +421,41 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
     constexpr int NQ = decltype(nq_c)::value;
     constexpr int S = KS * NQ;                                   // side-work slots per block
     constexpr auto copy_slot = [](int c) { return c * S / G; };
-    constexpr auto st_slot = [](int i) { return i * S / kGStores; };
+    constexpr int NS = 5;                                        // stores per wave per block
+    constexpr auto st_slot = [](int i) { return i * S / NS; };
     constexpr auto piece_ks = [](int piece) { return (piece + 1) * KS / 6; };
     // stores of a block issued after its last copy (a slot issues its copies first)
     constexpr int kAfter = [] {
       int n = 0;
-      for (int i = 0; i < kGStores; ++i) n += (i * S / kGStores) >= ((G - 1) * S / G);
+      for (int i = 0; i < NS; ++i) n += (i * S / NS) >= ((G - 1) * S / G);
       return n;
     }();
     const int key = lane & 31;
-    // store i of a finished tile: latent bytes 8*lane .. +7 of row 8w + i (i < 8), then tail slot
-    // lane % 8 of row 8w + lane / 8
+    // store i of a finished tile: the latent bytes of rows 8w + 2i and 8w + 2i + 1 (i < 4; lanes
+    // 32 * h .. 32 * h + 31 take row 8w + 2i + h, 16 bytes each), then tail slot lane % 8 of row
+    // 8w + lane / 8
     auto st_read = [&](const char* gb, int i) {
-      if (i < 8) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(gb + (8 * wave + i) * kGQPitch + 8 * lane);
-        return u32x4{v[0], v[1], 0u, 0u};
-      }
+      if (i < 4) return *reinterpret_cast<const u32x4*>(gb + (8 * wave + 2 * i + hb) * kGQPitch + 16 * key);
       return *reinterpret_cast<const u32x4*>(gb + rope_row * kGQPitch + 512 + 16 * (lane & 7));
     };
     auto st_issue = [&](const int32_t (&rpos)[8], int32_t rope_pos, int i, const u32x4& v) {
-      if (i < 8)
-        __builtin_nontemporal_store(u32x2{v[0], v[1]},
-                                    reinterpret_cast<u32x2*>(p.g_stage + (int64_t)rpos[i] * kGRowBytesI8 + 8 * lane));
-      else
+      if (i < 4) {
+        const int32_t r = hb ? rpos[2 * i + 1] : rpos[2 * i];
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p.g_stage + (int64_t)r * kGRowBytesI8 + 16 * key));
+      } else {
         __builtin_nontemporal_store(
             v, reinterpret_cast<u32x4*>(p.g_stage + (int64_t)rope_pos * kGRowBytesI8 + 512 + 16 * (lane & 7)));
+      }
     };
     stage(0, 0);
     if (nblk > 1) stage(1, 1);
     for (int blk = 0; blk < nblk; ++blk) {
       // issue order as in the bf16 loop: block blk needs copies(blk); issued after them are block
-      // blk - 2's last kAfter stores, block blk - 1's copies(blk + 1) and its 9 stores
+      // blk - 2's last kAfter stores, block blk - 1's copies(blk + 1) and its NS stores
       if (blk + 1 >= nblk) wait_vmcnt<0>();
       else if (blk <= 1) wait_vmcnt<G>();
-      else if (blk == 2) wait_vmcnt<G + kGStores>();
-      else wait_vmcnt<G + kGStores + kAfter>();
+      else if (blk == 2) wait_vmcnt<G + NS>();
+      else wait_vmcnt<G + NS + kAfter>();
       __syncthreads();
       const bool copy_next = blk + 2 < nblk;
       const bool store_prev = blk > 0;
@@ -534,10 +534,10 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
           }
           if (store_prev) {
 #pragma unroll
-            for (int i = 0; i < kGStores; ++i) {
+            for (int i = 0; i < NS; ++i) {
               if (st_slot(i) == s) {
                 st_issue(rpos, rope_pos, i, sdat);
-                if (i + 1 < kGStores) sdat = st_read(gprev, i + 1);
+                if (i + 1 < NS) sdat = st_read(gprev, i + 1);
               }
             }
           }
@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(nblk - 1) * kBK + 8 * wave + i]);
       const int32_t rope_pos = sm.pos[(nblk - 1) * kBK + rope_row];
 #pragma unroll
-      for (int i = 0; i < kGStores; ++i) st_issue(rpos, rope_pos, i, st_read(gb, i));
+      for (int i = 0; i < NS; ++i) st_issue(rpos, rope_pos, i, st_read(gb, i));
     }
   };
   if constexpr (I8) {
