@@ -415,8 +415,8 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   // LDS buffer blk & 1 in the rows' HBM format, from which block blk + 1 stores whole rows; with
   // two buffers no barrier separates a tile from the stores of the previous one.  The side work
   // of a block is spread over its KS * NQ k-step slots: tile 0's B operands, copies(blk + 2),
-  // the 9 stores of block blk - 1 (each row read from LDS one store ahead) and five
-  // quantisation pieces per tile.
+  // the 5 stores of block blk - 1 (each read from LDS one store ahead) and five quantisation
+  // pieces per tile.
   auto block_loop_i8 = [&](auto nq_c) {
     constexpr int NQ = decltype(nq_c)::value;
     constexpr int S = KS * NQ;                                   // side-work slots per block
