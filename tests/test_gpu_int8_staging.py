@@ -37,9 +37,10 @@ def _case(T, H, K, seed):
     return q, kv, idx, dout
 
 
-@pytest.mark.parametrize("T,H,K", [(300, 64, 256), (160, 128, 128), (120, 16, 64), (77, 48, 96)])
+@pytest.mark.parametrize("T,H,K", [(300, 64, 256), (160, 128, 128), (120, 16, 64), (77, 48, 96), (90, 128, 16)])
 def test_int8_staging_against_fp64_oracle(T, H, K):
-    """H = 48 runs B3's 4-step head loop with a zero last step; T = 77 ends in a partial block."""
+    """H = 48 runs B3's 4-step head loop with a zero last step; T = 77 ends in a partial block;
+    K = 16 gives every query a single key block, stored only after B3's block loop."""
     print(f"[int8 staging vs oracle] T={T} H={H} K={K}", flush=True)
     q, kv, idx, dout = _case(T, H, K, 900 + T)
     qd, kvd, idxd, doutd = q.to(DEV), kv.to(DEV), idx.to(DEV), dout.to(DEV)
