@@ -31,12 +31,18 @@
  *     The valid indices of one row must be distinct (a top-k never repeats a key); ids outside
  *     [0, n_kv) are treated like -1.
  *   - Documents: cu_seqlens [n_seq + 1] int32 on the device, cu[0] = 0, cu[n_seq] = T.
- *   - The caller owns every buffer, including workspaces; the library allocates nothing,
- *     keeps no pointer past the call, and launches everything on `stream` (hipStream_t,
- *     NULL = default stream) without synchronising the host.
+ *   - The caller owns every buffer, including workspaces; the library allocates no memory at
+ *     run time (its one static device array, the 64 MiB scratch of
+ *     dsa_sparse_mla_decode_noalloc, is reserved on each GPU when the library's code object
+ *     is loaded there), keeps no pointer past the call, and launches everything on `stream`
+ *     (hipStream_t, NULL = default stream) without synchronising the host.
  *   - Return 0 on success, a negative dsa_status otherwise; dsa_strerror() explains it.
  *     No C++ exception crosses the ABI.  Argument checks run before any device work, so an
  *     error return means nothing was launched.
+ *   - Every entry point that launches work then checks the current device once per device:
+ *     one that is not gfx950 (or no current device) gives DSA_ERR_DEVICE.  Launch shapes
+ *     follow the device's compute units (the decode key splits fill them; a partitioned MI355X
+ *     exposes fewer) and its XCDs (32 CUs each; the XCD-aware work order of the prefill kernels).
  */
 #ifndef DSA_ABI_H_
 #define DSA_ABI_H_
@@ -157,8 +163,13 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
  * inference); this is the decode restriction of the causal rows of dsa_build_rows. */
 int dsa_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base, int32_t* row_len,
                           void* stream);
-/* Workspace bytes for dsa_sparse_mla_decode (0 when the batch alone fills the device). */
+/* Workspace bytes for dsa_sparse_mla_decode on the current device (0 when the batch alone fills
+ * the device): the key splits are sized by the device's compute units (256 on a whole MI355X;
+ * without a current device, 256 is assumed). */
 size_t dsa_sparse_mla_decode_workspace_size(int batch, int n_heads, int topk);
+/* The same for a device of n_cu compute units (sizing ahead of time, e.g. for a partitioned
+ * MI355X); 0 for n_cu < 1.  No reference counterpart (as dsa_sparse_mla_decode). */
+size_t dsa_sparse_mla_decode_workspace_size_for(int batch, int n_heads, int topk, int n_cu);
 /* Sparse MLA decode: one new query per sequence, q [batch, H, 576] bf16, over its selected rows
  * of the latent cache kv_cache [n_kv, 576] (idx [batch, topk] global cache row ids, -1 pad).
  * out [batch, H, 512] bf16, lse [batch, H] fp32.  Same arithmetic as dsa_sparse_mla_fwd with

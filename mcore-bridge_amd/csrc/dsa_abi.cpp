@@ -6,6 +6,8 @@
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
+#include <cstring>
+#include <mutex>
 
 #include "../../include/dsa_abi.h"
 #include "dsa_kernels.h"
@@ -71,30 +73,83 @@ IdxBwdLayout idx_bwd_layout(int total_q, int n_k, int topk) {
   return L;
 }
 
+// The current device as the launches need it: a gfx950 check, its compute units (the decode
+// key splits fill them) and its XCDs (the XCD-aware grids), looked up once per device.  An
+// MI355X exposes 256 CUs in 8 XCDs of 32; a partitioned one (CPX / DPX modes) fewer of both.
+struct DeviceInfo {
+  int status;   // DSA_OK, or DSA_ERR_DEVICE when there is no current device or it is not gfx950
+  int n_cu, n_xcd;
+};
+constexpr int kMaxDevices = 64;
+constexpr int kCusPerXcd = 32;
+constexpr int kDefaultCus = 256;   // sizing queries on a host without a device
+std::mutex g_dev_mu;
+DeviceInfo g_dev[kMaxDevices];
+bool g_dev_known[kMaxDevices];
+
+int xcds_of(int n_cu) {
+  int x = 1;
+  while (x < 8 && 2 * x * kCusPerXcd <= n_cu) x *= 2;
+  return x;
+}
+
+DeviceInfo current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();   // leave no sticky error behind for the caller's next HIP call
+    return DeviceInfo{DSA_ERR_DEVICE, 0, 0};
+  }
+  std::lock_guard<std::mutex> lock(g_dev_mu);
+  if (!g_dev_known[dev]) {
+    hipDeviceProp_t prop;
+    DeviceInfo d{DSA_ERR_DEVICE, 0, 0};
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+        prop.multiProcessorCount > 0) {
+      d = DeviceInfo{DSA_OK, prop.multiProcessorCount, xcds_of(prop.multiProcessorCount)};
+    } else {
+      (void)hipGetLastError();
+    }
+    g_dev[dev] = d;
+    g_dev_known[dev] = true;
+  }
+  return g_dev[dev];
+}
+
+// CU count that sizes the decode splits: the current device's, or kDefaultCus without one.
+int sizing_cus() {
+  const DeviceInfo d = current_device();
+  return d.status == DSA_OK ? d.n_cu : kDefaultCus;
+}
+
 // Decode key splits: enough (sequence, split) work items to give every CU one workgroup
 // (the forward kernel holds one workgroup per CU), at least 4 key blocks of 32 per split.
 struct DecodeSplit {
   int n_split, split_keys;
 };
 
-DecodeSplit decode_split(int batch, int n_heads, int topk) {
-  constexpr int kCUs = 256;
+DecodeSplit decode_split(int batch, int n_heads, int topk, int n_cu) {
   const int items = batch * ((n_heads + 127) / 128);
   const int blocks = (topk + 31) / 32;
-  int n = (kCUs + items - 1) / items;
+  int n = (std::max(n_cu, 1) + items - 1) / items;
   n = std::max(1, std::min(n, blocks / 4));
   const int per = (blocks + n - 1) / n;                 // blocks per split
   return DecodeSplit{(blocks + per - 1) / per, per * 32};
 }
 
-size_t decode_workspace(int batch, int n_heads, int topk) {
-  const DecodeSplit d = decode_split(batch, n_heads, topk);
+size_t decode_workspace(int batch, int n_heads, int topk, int n_cu) {
+  const DecodeSplit d = decode_split(batch, n_heads, topk, n_cu);
   if (d.n_split == 1) return 0;
   const size_t rows = (size_t)batch * d.n_split * n_heads;
   return align_up(rows * kDv * sizeof(uint16_t)) + align_up(rows * sizeof(float));
 }
 
 }  // namespace
+
+// Every entry point that launches work checks the current device first (after its argument
+// checks, so invalid arguments are reported the same with or without a device).
+#define DSA_CHECK_DEVICE(dev)              \
+  const DeviceInfo dev = current_device(); \
+  if (dev.status != DSA_OK) return dev.status
 
 extern "C" {
 
@@ -117,7 +172,10 @@ const char* dsa_strerror(int status) {
 
 int dsa_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,
                    int32_t* row_len, void* stream) {
-  if (!cu_seqlens || !row_base || !row_len || n_seq < 1 || total_q < 0) return DSA_ERR_INVALID_ARG;
+  if (n_seq < 1 || total_q < 0) return DSA_ERR_INVALID_ARG;
+  if (total_q == 0) return DSA_OK;
+  if (!cu_seqlens || !row_base || !row_len) return DSA_ERR_INVALID_ARG;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_build_rows(cu_seqlens, n_seq, total_q, causal, row_base, row_len, as_stream(stream));
 }
 
@@ -154,6 +212,7 @@ int dsa_indexer_prologue(const void* q_lin, int64_t q_stride_t, const void* k_li
   p.out_fp8 = fp8 ? 1 : 0;
   p.eps = eps; p.mscale = mscale; p.w_scale_heads = w_scale_heads; p.w_scale_softmax = w_scale_softmax;
   p.q_stride_t = q_stride_t; p.k_stride_t = k_stride_t; p.w_stride_t = w_stride_t; p.freqs_stride_t = freqs_stride_t;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_indexer_prologue(p, as_stream(stream));
 }
 
@@ -199,6 +258,7 @@ int dsa_indexer_prologue_bwd(const float* dq, const float* dk, const float* dw, 
   p.eps = eps; p.mscale = mscale; p.w_scale_heads = w_scale_heads; p.w_scale_softmax = w_scale_softmax;
   p.k_stride_t = k_stride_t; p.freqs_stride_t = freqs_stride_t; p.dq_lin_stride_t = dq_lin_stride_t;
   p.dk_lin_stride_t = dk_lin_stride_t; p.dw_lin_stride_t = dw_lin_stride_t;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_indexer_prologue_bwd(p, as_stream(stream));
 }
 
@@ -219,6 +279,7 @@ int dsa_indexer_scores(const void* q, int q_dtype, const float* q_scale, const v
   p.row_base = row_base; p.row_len = row_len; p.scores = scores;
   p.total_q = total_q; p.n_heads = n_heads; p.head_dim = head_dim; p.fp8 = fp8 ? 1 : 0;
   p.max_row_len = max_row_len; p.pitch = pitch; p.fill_masked = fill_masked ? 1 : 0;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_indexer_scores(p, as_stream(stream));
 }
 
@@ -242,6 +303,7 @@ int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const 
     p.cand_key = static_cast<uint32_t*>(workspace);
     p.cand_idx = reinterpret_cast<int32_t*>(p.cand_key + n);
   }
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_topk(p, as_stream(stream));
 }
 
@@ -265,6 +327,8 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
   p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
   p.out_stride_t = (int64_t)n_heads * kDv; p.lse_stride_t = n_heads;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
   return dsa::launch_sparse_mla_fwd(p, as_stream(stream));
 }
 
@@ -272,12 +336,18 @@ int dsa_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_base,
   if (batch < 0) return DSA_ERR_INVALID_ARG;
   if (batch == 0) return DSA_OK;
   if (!cu_cache || !row_base || !row_len) return DSA_ERR_INVALID_ARG;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_build_decode_rows(cu_cache, batch, row_base, row_len, as_stream(stream));
 }
 
 size_t dsa_sparse_mla_decode_workspace_size(int batch, int n_heads, int topk) {
   if (batch < 0 || n_heads < 1 || topk < 1) return 0;
-  return decode_workspace(batch, n_heads, topk);
+  return decode_workspace(batch, n_heads, topk, sizing_cus());
+}
+
+size_t dsa_sparse_mla_decode_workspace_size_for(int batch, int n_heads, int topk, int n_cu) {
+  if (batch < 0 || n_heads < 1 || topk < 1 || n_cu < 1) return 0;
+  return decode_workspace(batch, n_heads, topk, n_cu);
 }
 
 int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* idx, int batch, int n_kv,
@@ -289,10 +359,13 @@ int dsa_sparse_mla_decode(const void* q, const void* kv_cache, const int32_t* id
   if (batch == 0) return DSA_OK;
   if (!q || !kv_cache || !idx || !out || !lse || n_kv < 1) return DSA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(kv_cache) || !aligned16(out)) return DSA_ERR_INVALID_ARG;
-  const DecodeSplit d = decode_split(batch, n_heads, topk);
-  const size_t need = decode_workspace(batch, n_heads, topk);
+  const int n_cu = sizing_cus();
+  const DecodeSplit d = decode_split(batch, n_heads, topk, n_cu);
+  const size_t need = decode_workspace(batch, n_heads, topk, n_cu);
   if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace))) return DSA_ERR_WORKSPACE;
+  DSA_CHECK_DEVICE(dev);
   dsa::SparseFwdParams p{};
+  p.n_xcd = dev.n_xcd;
   p.q = static_cast<const dsa::bf16_t*>(q);
   p.kv = static_cast<const dsa::bf16_t*>(kv_cache);
   p.idx = idx;
@@ -327,7 +400,7 @@ int dsa_sparse_mla_decode_noalloc(const void* q, const void* kv_cache, const int
     return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (batch == 0) return DSA_OK;
-  const size_t need = decode_workspace(batch, n_heads, topk);
+  const size_t need = decode_workspace(batch, n_heads, topk, sizing_cus());
   if (need > dsa::kDecodeScratchBytes) return DSA_ERR_SCRATCH;
   void* scratch = nullptr;
   if (need > 0) {
@@ -385,6 +458,7 @@ int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, con
   // workspace are not touched and may be null; the timed variant has no stages to record)
   if (total_q == 0) {
     if (stage_events) return DSA_ERR_INVALID_ARG;
+    DSA_CHECK_DEVICE(dev0);
     return dsa::launch_zero_rows(dkv, n_kv, kDqk, kDqk, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
   }
   if (!q || !kv || !idx || !out || !dout || !lse || !dq) return DSA_ERR_INVALID_ARG;
@@ -395,9 +469,11 @@ int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, con
   const int chunk = bwd_chunk_rows(total_q, n_kv, n_heads, topk, workspace_bytes, flags);
   if (!workspace || chunk == 0 || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
   if (stage_events && chunk < total_q) return DSA_ERR_WORKSPACE;
+  DSA_CHECK_DEVICE(dev);
   const BwdLayout L = bwd_layout(chunk, n_kv, n_heads, topk, flags);
   char* ws = static_cast<char*>(workspace);
   dsa::SparseBwdParams p{};
+  p.n_xcd = dev.n_xcd;
   p.kv = static_cast<const dsa::bf16_t*>(kv);
   p.dkv = dkv;
   p.p_stage = reinterpret_cast<dsa::bf16_t*>(ws + L.p_stage);
@@ -454,6 +530,8 @@ int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, con
   p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.causal = causal ? 1 : 0;
   p.q_stride_t = (int64_t)n_heads * kDqk; p.idx_stride = topk; p.lse_stride_t = n_heads; p.target_stride = topk;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
   return dsa::launch_indexer_kl_target(p, as_stream(stream));
 }
 
@@ -472,6 +550,7 @@ int dsa_indexer_kl_target_from_bwd(const void* bwd_workspace, size_t bwd_workspa
   p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.topk_pad = topk_pad(topk);
   p.causal = causal ? 1 : 0;
   p.idx_stride = topk; p.target_stride = topk;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_indexer_kl_target_from_p(p, as_stream(stream));
 }
 
@@ -485,6 +564,7 @@ int dsa_indexer_kl_loss(const float* index_sel, const float* target, const int32
   p.total_q = total_q; p.topk = topk; p.n_kv = n_kv; p.causal = causal ? 1 : 0;
   p.index_stride = topk; p.target_stride = topk; p.idx_stride = topk; p.d_stride = topk;
   p.grad_scale = grad_scale;
+  DSA_CHECK_DEVICE(dev);
   return dsa::launch_indexer_kl(p, as_stream(stream));
 }
 
@@ -502,6 +582,8 @@ int dsa_indexer_selected_scores(const void* q, const void* k, const float* w, co
   p.w = w; p.idx = idx; p.scores = scores;
   p.total_q = total_q; p.n_heads = n_heads; p.n_k = n_k; p.topk = topk; p.causal = causal ? 1 : 0;
   p.q_stride_t = (int64_t)n_heads * head_dim; p.idx_stride = topk; p.scores_stride = topk;
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
   return dsa::launch_indexer_selected_scores(p, as_stream(stream));
 }
 
@@ -517,7 +599,10 @@ int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const i
   if (head_dim != 128 || n_heads > 64 || topk > 4096) return DSA_ERR_UNSUPPORTED;
   if (!dk) return DSA_ERR_INVALID_ARG;
   // no query rows: dk = 0 (empty sums); dq and dw are empty, the workspace is not needed
-  if (total_q == 0) return dsa::launch_zero_rows(dk, n_k, head_dim, head_dim, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+  if (total_q == 0) {
+    DSA_CHECK_DEVICE(dev0);
+    return dsa::launch_zero_rows(dk, n_k, head_dim, head_dim, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+  }
   if (!q || !k || !w || !idx || !d_index || !dq || !dw) return DSA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(k) || !aligned16(dq)) return DSA_ERR_INVALID_ARG;
   const IdxBwdLayout L = idx_bwd_layout(total_q, n_k, topk);
@@ -534,6 +619,8 @@ int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const i
   p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);
   p.total_q = total_q; p.n_heads = n_heads; p.n_k = n_k; p.topk = topk; p.causal = causal ? 1 : 0;
   p.q_stride_t = (int64_t)n_heads * head_dim; p.idx_stride = topk; p.d_stride = topk;
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
   return dsa::launch_indexer_scores_bwd(p, as_stream(stream));
 }
 

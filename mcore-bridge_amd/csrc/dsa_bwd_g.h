@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   constexpr int NW = 4;
   constexpr int G = 2 * kGHeads / 16 / NW;          // 4 copies per wave per block
   __shared__ __attribute__((aligned(16))) GSmem sm;
-  const int t = xcd_remap(blockIdx.x);
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5;

@@ -202,23 +202,25 @@ DSA_DEV void wait_vmcnt() {
 DSA_DEV void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // XCD-aware remap of a 1-D grid.  Consecutive workgroup ids are dispatched round-robin over the
-// 8 XCDs; work items are handed out in chunks of kXcdChunk consecutive items, chunk c to XCD
-// c % 8.  The ~32 workgroups an XCD runs at once then work on neighbouring items (neighbouring
-// query tokens share most of their selected KV rows, which stay in that XCD's L2), and every
-// XCD draws items from the whole range: with one contiguous eighth per XCD, the XCDs holding
-// document starts (short causal rows) ran out of work early.  The grid must come from
-// xcd_grid(); a grid of fewer than 8 * kXcdChunk workgroups gives each XCD one contiguous run.
+// device's n_xcd XCDs (8 on a whole MI355X, fewer on a partition); work items are handed out in
+// chunks of kXcdChunk consecutive items, chunk c to XCD c % n_xcd.  The ~32 workgroups an XCD runs
+// at once then work on neighbouring items (neighbouring query tokens share most of their selected
+// KV rows, which stay in that XCD's L2), and every XCD draws items from the whole range: with one
+// contiguous share per XCD, the XCDs holding document starts (short causal rows) ran out of work
+// early.  The grid must come from xcd_grid() with the same n_xcd; a grid of fewer than
+// n_xcd * kXcdChunk workgroups gives each XCD one contiguous run.  With n_xcd = 1 the map is the
+// identity.
 constexpr int kXcdChunk = 64;
-DSA_DEV int xcd_remap(int bid) {
-  const int per = (int)(gridDim.x >> 3);
+DSA_DEV int xcd_remap(int bid, int n_xcd) {
+  const int per = (int)gridDim.x / n_xcd;
   const int c = per < kXcdChunk ? per : kXcdChunk;
-  const int j = bid >> 3, jc = j / c;
-  return (jc * 8 + (bid & 7)) * c + (j - jc * c);
+  const int j = bid / n_xcd, x = bid - j * n_xcd, jc = j / c;
+  return (jc * n_xcd + x) * c + (j - jc * c);
 }
 // Grid size for xcd_remap over n work items (items >= n exit at once).
-inline int xcd_grid(int n) {
-  constexpr int full = 8 * kXcdChunk;
-  return n >= full ? (n + full - 1) / full * full : (n + 7) / 8 * 8;
+inline int xcd_grid(int n, int n_xcd) {
+  const int full = n_xcd * kXcdChunk;
+  return n >= full ? (n + full - 1) / full * full : (n + n_xcd - 1) / n_xcd * n_xcd;
 }
 
 }  // namespace dsa

@@ -84,7 +84,7 @@ static_assert(sizeof(IdxSmem) <= 160 * 1024, "indexer backward LDS budget");
 template <bool kBwd>
 __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
   __shared__ __attribute__((aligned(256))) IdxSmem sm;
-  const int t = xcd_remap(blockIdx.x);
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -462,19 +462,21 @@ __global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stag
 }
 
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream) {
+  if (p.n_xcd < 1) return -1;
   if (p.topk > kMaxTopkIdx || p.n_heads > kHi) return -2;
   if (p.total_q == 0) return 0;
-  hipLaunchKernelGGL(indexer_sel_kernel<false>, dim3(xcd_grid(p.total_q)), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(indexer_sel_kernel<false>, dim3(xcd_grid(p.total_q, p.n_xcd)), dim3(256), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream) {
+  if (p.n_xcd < 1) return -1;
   if (p.topk > kMaxTopkIdx || p.n_heads > kHi) return -2;
   if (p.g_sink_row >= INT32_MAX) return -2;   // staging rows are kept in 32 bits
   if (p.n_k > 0) launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_k, p.causal, 0, p.csr_counts,
                                  p.csr_offsets, p.pair_pos, stream);
   if (p.total_q > 0)
-    hipLaunchKernelGGL(indexer_sel_kernel<true>, dim3(xcd_grid(p.total_q)), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(indexer_sel_kernel<true>, dim3(xcd_grid(p.total_q, p.n_xcd)), dim3(256), 0, stream, p);
   if (p.n_k > 0)
     hipLaunchKernelGGL(idx_dk_reduce_kernel, dim3(p.n_k), dim3(256), 0, stream, p.g_stage, p.csr_offsets, p.n_k, p.dk);
   return hipGetLastError() == hipSuccess ? 0 : -4;

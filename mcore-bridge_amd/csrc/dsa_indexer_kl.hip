@@ -45,7 +45,7 @@ __global__ __launch_bounds__(NW * 64, 1) void indexer_kl_target_kernel(KlTargetP
   constexpr int kCopyEvery = kDqk / 16 / G;
   static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the QK MFMAs");
   __shared__ __attribute__((aligned(128))) KlSmem sm;
-  const int t = xcd_remap(blockIdx.x);
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5, hl = lane & 31;
@@ -259,9 +259,10 @@ int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream) 
 }
 
 int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream) {
+  if (p.n_xcd < 1) return -1;
   if (p.topk > kMaxTopkKl) return -2;
   if (p.total_q == 0) return 0;
-  const dim3 grid(xcd_grid(p.total_q));
+  const dim3 grid(xcd_grid(p.total_q, p.n_xcd));
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   if (nw == 4) hipLaunchKernelGGL(indexer_kl_target_kernel<4>, grid, dim3(256), 0, stream, p);
   else if (nw == 2) hipLaunchKernelGGL(indexer_kl_target_kernel<2>, grid, dim3(128), 0, stream, p);

@@ -21,6 +21,7 @@ struct SparseFwdParams {
   int split_keys;       // index slots per split (multiple of 32 when n_split > 1; = topk otherwise)
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, lse_stride_t;
   float scale_log2;     // softmax scale * log2(e)
+  int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
 };
 
 // Per-pair dKV partial rows ("G rows") of the sparse backward, written by B3 and summed per key
@@ -59,6 +60,7 @@ struct SparseBwdParams {
   int dkv_accumulate;   // 1: B5 adds into dkv (the later chunks of a chunked backward)
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, dout_stride_t, lse_stride_t, dq_stride_t, dkv_stride;
   float scale, scale_log2;
+  int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
 };
 
 struct IndexerParams {
@@ -117,6 +119,7 @@ struct KlTargetParams {
   int total_q, n_heads, n_kv, topk, causal;
   int64_t q_stride_t, idx_stride, lse_stride_t, target_stride;
   float scale_log2;     // softmax scale * log2(e)
+  int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
 };
 
 struct KlFromPParams {
@@ -176,6 +179,7 @@ struct IdxSelParams {
   int32_t* csr_counts;   // [csr_count_entries(total_q, n_k)]
   int total_q, n_heads, n_k, topk, causal;
   int64_t q_stride_t, idx_stride, scores_stride, d_stride;
+  int n_xcd;             // XCDs of the device (xcd_remap / xcd_grid)
 };
 
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   constexpr int kCopyEvery = kDqk / 16 / G;   // S/dP steps per gather copy
   static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the k-steps");
   __shared__ __attribute__((aligned(128))) SpSmem sm;
-  const int t = xcd_remap(blockIdx.x);
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hb = lane >> 5, hl = lane & 31;
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   static_assert(HR / 16 / NW == 2, "two dS copies per wave per block");
   static_assert(DT * NW * 16 == kDqk && DT >= TC, "dims split evenly; one tile copy per dim step");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
-  const int t = xcd_remap(blockIdx.x);
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, gi = lane & 15;
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
   constexpr int G = TC + 2;                      // copies per copy-issuing wave per block
   static_assert(TC <= 2 * HT - 6, "tile copies before the dS copy slots");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
-  const int t = xcd_remap(blockIdx.x);
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(wave);
@@ -871,6 +871,7 @@ void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int to
 }
 
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev) {
+  if (p.n_xcd < 1) return -1;
   if (p.topk > kMaxTopkBwd) return -2;
   if (p.g_sink_row >= INT32_MAX) return -2;   // B3 keeps G row numbers in 32 bits
   bool marks_ok = true;   // a failed event record is reported like a failed launch
@@ -879,7 +880,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   };
   mark(0);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
-  const dim3 grid(xcd_grid(p.total_q), (p.n_heads + 127) / 128);
+  const dim3 grid(xcd_grid(p.total_q, p.n_xcd), (p.n_heads + 127) / 128);
   // B4 first: it only depends on idx.
   launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_kv, p.causal, p.q_offset, p.csr_counts,
                   p.csr_offsets, p.pair_pos, stream);
@@ -900,7 +901,7 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   }
   mark(3);
   const int nks = p.n_heads / 16;
-  const dim3 ggrid(xcd_grid(p.total_q));
+  const dim3 ggrid(xcd_grid(p.total_q, p.n_xcd));
   if (p.g_int8)
     launch_bwd_g_i8(p, stream);
   else if (nks > 4)

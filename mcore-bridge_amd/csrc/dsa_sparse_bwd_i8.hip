@@ -9,7 +9,7 @@ namespace dsa {
 
 void launch_bwd_g_i8(const SparseBwdParams& p, hipStream_t stream) {
   const int nks = p.n_heads / 16;
-  const dim3 grid(xcd_grid(p.total_q));
+  const dim3 grid(xcd_grid(p.total_q, p.n_xcd));
   if (nks > 4)
     hipLaunchKernelGGL((bwd_g_kernel<8, true>), grid, dim3(256), 0, stream, p);
   else if (nks > 2)

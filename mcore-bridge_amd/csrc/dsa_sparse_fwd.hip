@@ -82,7 +82,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   // still fill the chip: split s covers index slots [s*split_keys, (s+1)*split_keys) and writes
   // its normalised partial output and LSE to row t*n_split + s (merged by the combine kernel)
   const int n_items = p.total_q * p.n_split;
-  const int item = xcd_remap(blockIdx.x);
+  const int item = xcd_remap(blockIdx.x, p.n_xcd);
   if (item >= n_items) return;
   const int t = item / p.n_split;
   const int split = item - t * p.n_split;
@@ -405,9 +405,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const bf16_t* part_
 }
 
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
+  if (p.n_xcd < 1) return -1;
   if (p.split_keys > kMaxTopk || p.n_split < 1 || (p.n_split > 1 && p.split_keys % kBK != 0)) return -2;
   if ((int64_t)(p.n_split - 1) * p.split_keys >= p.topk) return -1;   // every split owns >= 1 slot
-  const dim3 grid(xcd_grid(p.total_q * p.n_split), (p.n_heads + 127) / 128);
+  const dim3 grid(xcd_grid(p.total_q * p.n_split, p.n_xcd), (p.n_heads + 127) / 128);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   if (nw == 4)
     hipLaunchKernelGGL(sparse_mla_fwd_kernel<4>, grid, dim3(256), 0, stream, p);

@@ -292,8 +292,14 @@ class _SparseMLAWithIndexerLoss(torch.autograd.Function):
     def backward(ctx, dout):
         q, kv, q_idx, k_idx, w, idx, out, lse = ctx.saved_tensors
         sm_scale, coeff, loss_scale, causal = ctx.args
-        dq, dkv, target = ops.sparse_mla_bwd_with_target(q, kv, idx, out, dout, lse, sm_scale, causal)
-        T = idx.shape[0]
+        T, H = q.shape[0], q.shape[1]
+        if ops.backward_takes_one_pass(T, kv.shape[0], H, idx.shape[1]):
+            dq, dkv, target = ops.sparse_mla_bwd_with_target(q, kv, idx, out, dout, lse, sm_scale, causal)
+        else:
+            # a workspace cap (or int8 row staging) is set: the capped backward cannot keep the P
+            # tiles of every query, so the target is recomputed from the forward LSE instead
+            dq, dkv = ops.autograd_backward(q, kv, idx, out, dout, lse, sm_scale, causal)
+            target = ops.indexer_kl_target(q, kv, idx, lse, sm_scale, causal)
         sel = ops.indexer_selected_scores(q_idx.detach(), k_idx.detach(), w.detach(), idx, causal)
         kl, d = ops.indexer_kl_rows(sel, target, idx, k_idx.shape[0], causal, coeff * loss_scale / max(T, 1))
         ctx.loss_out.copy_(kl.sum() * (coeff / max(T, 1)))
@@ -311,7 +317,9 @@ def sparse_mla_with_indexer_loss(q: Tensor, kv: Tensor, topk_indices: Tensor, q_
     indexer KL loss, the way Megatron's ``DSAIndexerLossAutoScaler`` attaches the indexer loss to
     the attention output: the loss needs no separate backward call.  The target comes from the P
     tiles the attention backward recomputes anyway, so no score product is repeated (the
-    forward-time ``indexer_kl_loss`` recomputes it).
+    forward-time ``indexer_kl_loss`` recomputes it).  Under ``ops.set_backward_workspace_limit``
+    (when the one-pass workspace exceeds the cap) or ``ops.set_backward_staging("int8")`` the
+    backward runs in capped passes / with int8 rows and recomputes the target from the forward LSE.
 
     Returns ``(out [T, H, 512], loss)``: ``loss`` is a 0-dim fp32 tensor that holds ``loss_coeff *
     mean_t KL_t`` once the backward pass has run (for logging); the gradients reaching ``q_idx``,
@@ -559,11 +567,13 @@ class DSAttention(torch.nn.Module):
 
     The attention is causal by construction, as DSA's is: ``attention_mask`` is not read (so it
     is never inspected on the host), and ``attn_mask_type``, when given, must be a causal kind.
-    ``use_sparse_loss=False`` (the reference default) trains the indexer with the dense loss
-    (``indexer_kl_loss_dense``), computed in the forward and applied in the output's backward."""
+    ``use_sparse_loss=False`` (the default, as the reference's ``dsa_indexer_use_sparse_loss``,
+    model_config.py:205) trains the indexer with the dense loss (``indexer_kl_loss_dense``),
+    computed in the forward and applied in the output's backward; ``use_sparse_loss=True`` uses
+    the sparse loss (``sparse_mla_with_indexer_loss``)."""
 
     def __init__(self, indexer: DSAIndexer, softmax_scale: float, loss_coeff: float = 0.0,
-                 use_sparse_loss: bool = True):
+                 use_sparse_loss: bool = False):
         super().__init__()
         self.indexer = indexer
         self.softmax_scale = float(softmax_scale)

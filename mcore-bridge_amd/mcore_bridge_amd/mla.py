@@ -18,6 +18,18 @@ with the indexer KL loss applied in the attention's backward when training with
 ``dsa_indexer_use_sparse_loss`` (model_config.py:204-205).
 ``install_attention(spec)`` makes the swap in a layer spec, the way register.py:158-162 does.
 
+Recompute flags of the base class (set by Megatron's MLA from the recompute config) are honoured
+with non-reentrant activation checkpointing (``torch.utils.checkpoint``):
+- ``checkpoint_core_attention`` (in training, multi_latent_attention.py:250-252): the core
+  attention -- ``W_UK`` absorption, the sparse attention kernels, ``W_UV`` and, when training the
+  indexer, its loss -- is recomputed in the backward instead of keeping its activations.  (The
+  reference's checkpointed path does not pass ``x``/``qr`` to DSA; here the indexer runs before
+  the checkpointed region, so the flag works with DSA.)
+- ``recompute_up_proj`` (multi_latent_attention.py:180-185, 282-285): the reference recomputes the
+  per-head q/k/v up-projection and RoPE.  In the absorbed layout the up-projected tensor the
+  attention keeps is the absorbed query (``H x 576`` per token, larger than the reference's q), so
+  the checkpointed region is the q up-projection, RoPE and the core attention together.
+
 Scope: one tensor-parallel rank holding every head (the kernels' single-GPU share), no
 inference cache (the reference's DSA has none either, patcher.py:256), sbhd or THD packing.
 """
@@ -28,6 +40,7 @@ from typing import Optional
 
 import torch
 from torch import Tensor
+from torch.utils.checkpoint import checkpoint
 
 from .dsa import (IndexerView, _IndexerComputation, _mask_type_is_causal, _split_packed, _thd_docs,
                   absorbed_mla_sparse_attention)
@@ -95,16 +108,21 @@ class _AbsorbedDSAForward:
         kv_c = self.kv_layernorm(kv_c)
         if docs is not None:                     # THD: [t, 1, ...] -> [t, ...] (:88-96)
             q_c, kv_c, k_pe = q_c.squeeze(1), kv_c.squeeze(1), k_pe.squeeze(1)
-        # q up-projection (:104-111); W_UK / W_UV of linear_kv_up_proj are absorbed instead of applied
-        q = _out(self.linear_q_up_proj(q_c)) if cfg.q_lora_rank is not None else _out(self.linear_q_proj(q_c))
         H = self.num_attention_heads_per_partition
-        q = q.view(*q.shape[:-1], H, cfg.qk_head_dim + d_rope)
-        q_nope, q_pe = torch.split(q, [cfg.qk_head_dim, d_rope], dim=-1)
-        # RoPE of the rope parts as the caller applies it (:150-162)
         rope = _rope_fn(type(self))
         cu = docs[0] if docs is not None else None
-        q_pe = rope(q_pe, rotary_pos_emb, config=cfg, cu_seqlens=cu)
-        k_pe = rope(k_pe.unsqueeze(-2), rotary_pos_emb, config=cfg, cu_seqlens=cu).squeeze(-2)
+        add_b = (lambda t: t.unsqueeze(1)) if docs is not None else (lambda t: t)   # THD: one [T, 1] "batch"
+
+        def up_proj(q_c, kv_c, k_pe):
+            # q up-projection (:104-111); W_UK / W_UV of linear_kv_up_proj are absorbed instead of applied
+            q = _out(self.linear_q_up_proj(q_c)) if cfg.q_lora_rank is not None else _out(self.linear_q_proj(q_c))
+            q = q.view(*q.shape[:-1], H, cfg.qk_head_dim + d_rope)
+            q_nope, q_pe = torch.split(q, [cfg.qk_head_dim, d_rope], dim=-1)
+            # RoPE of the rope parts as the caller applies it (:150-162)
+            q_pe = rope(q_pe, rotary_pos_emb, config=cfg, cu_seqlens=cu)
+            k_pe = rope(k_pe.unsqueeze(-2), rotary_pos_emb, config=cfg, cu_seqlens=cu).squeeze(-2)
+            return add_b(q_nope), add_b(q_pe), add_b(kv_c), add_b(k_pe)
+
         # DSA: indexer over (x, q_compressed) (:255-261), causal top-k, absorbed sparse attention
         assert _mask_type_is_causal(getattr(self, "attn_mask_type", None)), "DSA attention is causal"
         ix = self._dsa_indexer()
@@ -115,21 +133,32 @@ class _AbsorbedDSAForward:
         with torch.set_grad_enabled(train_loss):
             ix_out = ix.forward_before_topk(x, q_c, (psp, rotary_pos_emb))
         _, topk = ix.topk_from_outputs(ix_out, None, docs, causal=True, return_scores=False)
-        if docs is not None:                     # one [T, 1] "batch" with global token ids
-            add_b = lambda t: t.unsqueeze(1)
-            q_nope, q_pe, kv_c, k_pe = add_b(q_nope), add_b(q_pe), add_b(kv_c), add_b(k_pe)
+        if docs is not None:
             topk = topk.unsqueeze(0)
             ix_out = tuple(add_b(o) for o in ix_out)
         w_kv = self.linear_kv_up_proj.weight
         scale = self._dsa_softmax_scale()
-        if train_loss:
-            sparse = bool(getattr(cfg, "dsa_indexer_use_sparse_loss", False))
-            out, loss = absorbed_mla_sparse_attention(q_nope, q_pe, kv_c, k_pe, w_kv, topk, scale, True,
-                                                      indexer_loss=(*ix_out, coeff, self.indexer_loss_scale, sparse,
-                                                                    docs))
-            self.last_indexer_loss = loss
+        sparse = bool(getattr(cfg, "dsa_indexer_use_sparse_loss", False))
+
+        def core_attention(q_nope, q_pe, kv_c, k_pe, *ix_t):
+            if not train_loss:
+                return absorbed_mla_sparse_attention(q_nope, q_pe, kv_c, k_pe, w_kv, topk, scale, True), None
+            return absorbed_mla_sparse_attention(q_nope, q_pe, kv_c, k_pe, w_kv, topk, scale, True,
+                                                 indexer_loss=(*ix_t, coeff, self.indexer_loss_scale, sparse, docs))
+
+        # the recompute flags (multi_latent_attention.py:180-185, 250-252): non-reentrant
+        # checkpoints of the up-projection + core attention, or of the core attention alone
+        grad = torch.is_grad_enabled()
+        ix_t = ix_out if train_loss else ()
+        if grad and getattr(self, "recompute_up_proj", False):
+            out, loss = checkpoint(lambda *a: core_attention(*up_proj(*a[:3]), *a[3:]), q_c, kv_c, k_pe, *ix_t,
+                                   use_reentrant=False)
+        elif grad and self.training and getattr(self, "checkpoint_core_attention", False):
+            out, loss = checkpoint(core_attention, *up_proj(q_c, kv_c, k_pe), *ix_t, use_reentrant=False)
         else:
-            out = absorbed_mla_sparse_attention(q_nope, q_pe, kv_c, k_pe, w_kv, topk, scale, True)
+            out, loss = core_attention(*up_proj(q_c, kv_c, k_pe), *ix_t)
+        if train_loss:
+            self.last_indexer_loss = loss
         # output projection (:286-290); THD gives (t, 1, h) like the caller's reshape (:281)
         return self.linear_proj(out)
 

@@ -467,10 +467,21 @@ def set_backward_staging(g_rows: str) -> None:
     ``"bf16"`` (the default) or ``"int8"`` (a bf16 scale per 32 dims: ~45% less of the backward's
     largest memory traffic and workspace; dkv normalised error ~0.5% instead of ~0.16%, dq
     unchanged).  ``sparse_mla_bwd_with_target`` (the indexer loss's target from the backward's P
-    tiles) always stages bf16 rows."""
+    tiles) always stages bf16 rows; the fused attention + indexer loss backward
+    (``dsa.sparse_mla_with_indexer_loss``) therefore switches to ``autograd_backward`` plus a
+    recomputed target when int8 rows are chosen or the one-pass workspace exceeds the cap."""
     if g_rows not in ("bf16", "int8"):
         raise ValueError(f"g_rows must be 'bf16' or 'int8', got {g_rows!r}")
     _BWD_G_INT8[0] = g_rows == "int8"
+
+
+def backward_takes_one_pass(total_q: int, n_kv: int, n_heads: int, topk_: int) -> bool:
+    """True when the settings of ``set_backward_workspace_limit`` and ``set_backward_staging``
+    admit the one-pass bf16-row backward (whose workspace ``sparse_mla_bwd_with_target`` needs)."""
+    if _BWD_G_INT8[0]:
+        return False
+    limit = _BWD_WORKSPACE_LIMIT[0]
+    return limit == 0 or bwd_workspace_bytes(total_q, n_kv, n_heads, topk_) <= limit
 
 
 def autograd_backward(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sm_scale: float,
@@ -640,9 +651,14 @@ def indexer_scores_dense_bwd(q: Tensor, k: Tensor, w: Tensor, row_base: Tensor, 
                              d_scores: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """Gradients of ``indexer_scores`` (bf16, head_dim 128) from ``d_scores [T, pitch]``: only columns
     ``j < row_len[t]`` carry gradient (the rest are constants).  Runs the selected-slot score
-    backward on blocks of ``SCORES_BWD_COLS`` columns and sums them.  ``(dq, dw, dk)`` fp32."""
+    backward on blocks of ``SCORES_BWD_COLS`` columns and sums them.  ``(dq, dw, dk)`` fp32 (zeros
+    when no row has a column, e.g. an empty batch)."""
+    if max_row_len <= 0:
+        return (torch.zeros(q.shape, dtype=torch.float32, device=q.device),
+                torch.zeros(w.shape, dtype=torch.float32, device=q.device),
+                torch.zeros(k.shape, dtype=torch.float32, device=q.device))
     dq = dw = dk = None
-    for c0 in range(0, max(max_row_len, 1), SCORES_BWD_COLS):
+    for c0 in range(0, max_row_len, SCORES_BWD_COLS):
         width = min(SCORES_BWD_COLS, max_row_len - c0)
         idx = dense_row_indices(row_base, row_len, c0, width)
         d = d_scores[:, c0:c0 + width].float()
@@ -673,9 +689,12 @@ torch.library.register_autograd("dsa_amd::indexer_scores", _isc_backward, setup_
 def dense_attention_lse(q: Tensor, kv: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
                         sm_scale: float) -> Tensor:
     """``[T, H]`` natural-log LSE of every query's dense attention over all of its visible keys
-    (the sparse forward over blocks of ``ATTN_COLS`` dense key columns, combined by logaddexp)."""
+    (the sparse forward over blocks of ``ATTN_COLS`` dense key columns, combined by logaddexp;
+    ``-inf`` for every query when no row has a key)."""
+    if max_row_len <= 0:
+        return torch.full((q.shape[0], q.shape[1]), float("-inf"), dtype=torch.float32, device=q.device)
     lse = None
-    for c0 in range(0, max(max_row_len, 1), ATTN_COLS):
+    for c0 in range(0, max_row_len, ATTN_COLS):
         idx = dense_row_indices(row_base, row_len, c0, min(ATTN_COLS, max_row_len - c0))
         _, l = sparse_mla_fwd(q, kv, idx, sm_scale, False)
         lse = l if lse is None else torch.logaddexp(lse, l)
@@ -689,7 +708,7 @@ def dense_attention_target(q: Tensor, kv: Tensor, lse: Tensor, row_base: Tensor,
     dense attention probabilities (``lse`` from ``dense_attention_lse``)."""
     T = q.shape[0]
     tgt = torch.zeros(T, pitch, dtype=torch.float32, device=q.device)
-    for c0 in range(0, max(max_row_len, 1), ATTN_COLS):
+    for c0 in range(0, max(max_row_len, 0), ATTN_COLS):
         width = min(ATTN_COLS, max_row_len - c0)
         idx = dense_row_indices(row_base, row_len, c0, width)
         tgt[:, c0:c0 + width] = indexer_kl_target(q, kv, idx, lse, sm_scale, False)

@@ -210,3 +210,47 @@ def test_indexer_loss_ops_refuse_cpu_tensors():
         ops.indexer_selected_scores(qi, ki, torch.zeros(4, 8), idx, True)
     with pytest.raises(RuntimeError, match="GPU"):
         ops.indexer_kl_rows(torch.zeros(4, 2), torch.zeros(4, 2), idx, 4, True, 1.0)
+
+
+def test_decode_split_follows_the_device_cu_count():
+    """The decode key splits fill the device's compute units: sized for a whole MI355X (256 CUs, also
+    the assumption without a current device) and for partitions with fewer."""
+    lib = _lib.load()
+    f = lib.dsa_sparse_mla_decode_workspace_size_for
+    assert f(64, 128, 2048, 256) == 64 * 4 * 128 * (512 * 2 + 4)
+    if not _has_device():
+        assert lib.dsa_sparse_mla_decode_workspace_size(64, 128, 2048) == f(64, 128, 2048, 256)
+    assert f(64, 128, 2048, 128) == 64 * 2 * 128 * (512 * 2 + 4)   # 128 CUs: 2 splits
+    assert f(64, 128, 2048, 32) == 0                               # 32 CUs: the batch alone fills them
+    assert f(8, 128, 2048, 32) == 8 * 4 * 128 * (512 * 2 + 4)      # 8 sequences on 32 CUs: 4 splits
+    assert f(1, 128, 2048, 32) == 1 * 16 * 128 * (512 * 2 + 4)     # at most one split per 4 key blocks
+    assert f(64, 128, 2048, 0) == 0 and f(-1, 128, 2048, 256) == 0
+
+
+def _has_device():
+    import torch
+    return torch.cuda.device_count() > 0
+
+
+def test_launching_entry_points_report_a_missing_device():
+    """Valid arguments without a usable gfx950 device: every launching entry point returns
+    DSA_ERR_DEVICE (checked once per device, after the argument checks) instead of a launch error."""
+    if _has_device():
+        pytest.skip("a device is present")
+    lib = _lib.load()
+    dev = _lib.DSA_ERR_DEVICE
+    assert lib.dsa_build_rows(P, 1, 4, 1, P, P, N) == dev
+    assert lib.dsa_build_decode_rows(P, 4, P, P, N) == dev
+    assert lib.dsa_sparse_mla_fwd(P, P, P, 4, 4, 16, 576, 512, 8, 0.1, 1, P, P, N) == dev
+    assert lib.dsa_indexer_scores(P, 0, N, P, 0, N, P, P, P, 4, 4, 4, 64, 4, P, 4, 0, N) == dev
+    assert lib.dsa_topk(P, 8, P, P, 4, 2, P, N, N, 0, N) == dev
+    ws = lib.dsa_sparse_mla_bwd_workspace_size(4, 4, 32, 8)
+    assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 32, 576, 512, 8, 0.1, 1, P, P, P, ws, N) == dev
+    assert lib.dsa_sparse_mla_bwd(N, N, N, N, N, N, 0, 4, 32, 576, 512, 8, 0.1, 1, N, P, N, 0, N) == dev
+    need = lib.dsa_sparse_mla_decode_workspace_size(64, 128, 2048)
+    assert lib.dsa_sparse_mla_decode(P, P, P, 64, 100, 128, 576, 512, 2048, 0.1, P, P, P, need, N) == dev
+    assert lib.dsa_sparse_mla_decode_noalloc(P, P, P, 64, 100, 128, 576, 512, 2048, 0.1, P, P, N) == dev
+    # argument errors are still reported as such, ahead of the device check
+    assert lib.dsa_sparse_mla_fwd(N, P, P, 4, 4, 16, 576, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
+    assert lib.dsa_sparse_mla_decode(P, P, P, 64, 100, 128, 576, 512, 2048, 0.1, P, P, P, need - 1, N) == \
+        _lib.DSA_ERR_WORKSPACE

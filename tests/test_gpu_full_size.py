@@ -13,7 +13,7 @@ rtol = atol = 2e-2 (plus normalised error < 1e-2).
 import pytest
 import torch
 
-from gpu_reference import close_on_device, sparse_mla_fwd_fp32
+from gpu_reference import close_on_device, sparse_mla_bwd_fp32, sparse_mla_fwd_fp32
 from oracle import dsa_oracle as O
 from mcore_bridge_amd import ops, workloads as W
 
@@ -29,32 +29,46 @@ def _close(got, ref, rel=1e-2, name="", tol=2e-2):
     assert err < rel, f"{name}: normalised error {err:.3e} >= {rel}"
 
 
-def _topk_every_row_is_a_stable_sort(sc, idx, K, chunk=512):
-    """idx[t] (ascending key ids, -1 pad; one causal document so key id = column) equals the first
-    min(K, t + 1) columns of a stable descending sort of row t of the kernel's scores (columns past
-    the row are -inf)."""
+def _doc_start(t, cu):
+    """First key of query t's document (cu = cumulative document lengths)."""
+    d = next(i for i in range(len(cu) - 1) if cu[i] <= t < cu[i + 1])
+    return cu[d]
+
+
+def _topk_every_row_is_a_stable_sort(sc, idx, K, cu=None, chunk=512):
+    """idx[t] (ascending global key ids, -1 pad) equals the first min(K, t - start + 1) columns of a
+    stable descending sort of row t of the kernel's scores, shifted by the document start (column j
+    of a row is key start + j; columns past the row are -inf), for every row of every document."""
     T = sc.shape[0]
+    cu = list(cu) if cu is not None else [0, T]
     big = torch.iinfo(torch.int64).max
-    for a in range(0, T, chunk):
-        b = min(T, a + chunk)
-        order = torch.sort(sc[a:b], dim=1, descending=True, stable=True).indices[:, :K]
-        n = (torch.arange(a, b, device=sc.device) + 1).clamp(max=K)
-        keep = torch.arange(order.shape[1], device=sc.device)[None] < n[:, None]
-        want = torch.where(keep, order, torch.full_like(order, big)).sort(dim=1).values
-        want = torch.where(want == big, torch.full_like(want, -1), want)
-        if want.shape[1] < K:
-            want = torch.cat([want, want.new_full((b - a, K - want.shape[1]), -1)], 1)
-        bad = (want != idx[a:b].long()).any(dim=1)
-        assert not bad.any(), f"top-k rows {(a + bad.nonzero().flatten()).tolist()[:8]} differ from a stable sort"
+    for s0, s1 in zip(cu[:-1], cu[1:]):
+        for a in range(s0, s1, chunk):
+            b = min(s1, a + chunk)
+            width = b - s0
+            order = torch.sort(sc[a:b, :width], dim=1, descending=True, stable=True).indices[:, :K]
+            n = (torch.arange(a, b, device=sc.device) - s0 + 1).clamp(max=K)
+            keep = torch.arange(order.shape[1], device=sc.device)[None] < n[:, None]
+            want = torch.where(keep, order + s0, torch.full_like(order, big)).sort(dim=1).values
+            want = torch.where(want == big, torch.full_like(want, -1), want)
+            if want.shape[1] < K:
+                want = torch.cat([want, want.new_full((b - a, K - want.shape[1]), -1)], 1)
+            bad = (want != idx[a:b].long()).any(dim=1)
+            assert not bad.any(), f"top-k rows {(a + bad.nonzero().flatten()).tolist()[:8]} differ from a stable sort"
 
 
-def _sampled_rows_against_oracle(q_idx, k_idx, w, sc, idx, rows, K, q_scale=None, k_scale=None, score_tol=1e-4):
+def _sampled_rows_against_oracle(q_idx, k_idx, w, sc, idx, rows, K, q_scale=None, k_scale=None, score_tol=1e-4,
+                                 cu=None):
+    cu = list(cu) if cu is not None else [0, sc.shape[0]]
     rows_t = torch.tensor(rows, device=sc.device)
     sc_rows = sc[rows_t].double().cpu()
     idx_rows = idx[rows_t].long().cpu()
+    starts = [_doc_start(t, cu) for t in rows]
     # bit-exact against the oracle's selection from the kernel's own fp32 scores
     for i, t in enumerate(rows):
-        want = O.topk_indices(sc_rows[i:i + 1, :t + 1], K)[0]
+        s0 = starts[i]
+        want = O.topk_indices(sc_rows[i:i + 1, :t - s0 + 1], K)[0]
+        want = torch.where(want >= 0, want + s0, want)
         want = torch.cat([want, want.new_full((K - want.numel(),), -1)])
         assert torch.equal(idx_rows[i], want), f"row {t}"
     # float64 scores of the same (dequantised) inputs: values and >= 99.9 % overlap
@@ -64,9 +78,11 @@ def _sampled_rows_against_oracle(q_idx, k_idx, w, sc, idx, rows, K, q_scale=None
                                 q_scale=qsc, k_scale=k_scale.cpu() if k_scale is not None else None)
     inter = tot = 0
     for i, t in enumerate(rows):
-        r = ref[i, :t + 1]
-        torch.testing.assert_close(sc_rows[i, :t + 1], r, rtol=score_tol, atol=score_tol, msg=lambda m: f"row {t}: {m}")
-        want = set(O.topk_indices(r[None], K)[0].tolist()) - {-1}
+        s0 = starts[i]
+        r = ref[i, s0:t + 1]
+        torch.testing.assert_close(sc_rows[i, :t - s0 + 1], r, rtol=score_tol, atol=score_tol,
+                                   msg=lambda m: f"row {t}: {m}")
+        want = set((O.topk_indices(r[None], K)[0] + s0).tolist()) - {s0 - 1}
         got = set(idx_rows[i].tolist()) - {-1}
         inter += len(want & got)
         tot += len(want)
@@ -81,12 +97,15 @@ def _forward_checks(q, kv, idx, rows):
     # every row against the fp32 reference
     close_on_device(out, ref_o, name="out (all rows, fp32 reference)")
     torch.testing.assert_close(lse, ref_l, rtol=1e-4, atol=1e-4)
+    del ref_o, ref_l
     # sampled rows against the float64 oracle (which also pins the fp32 reference there)
     si = torch.tensor(rows, device=q.device)
     ro, rl = O.sparse_mla_fwd(q[si].cpu(), kv.cpu(), idx[si].cpu(), W.SM_SCALE)
     _close(out[si].cpu(), ro, name="out (oracle rows)")
     torch.testing.assert_close(lse[si].cpu().double(), rl, rtol=1e-4, atol=1e-4)
-    _close(ref_o[si].cpu(), ro, rel=1e-3, name="fp32 reference vs oracle", tol=5e-3)
+    ref_o, _ = sparse_mla_fwd_fp32(q[si], kv, idx[si], W.SM_SCALE, False)
+    _close(ref_o.cpu(), ro, rel=1e-3, name="fp32 reference vs oracle", tol=5e-3)
+    return out, lse
 
 
 def _sample(S, extra, seed):
@@ -145,3 +164,52 @@ def test_cfg4_full_size_fp8_indexer_topk_sparse_fwd():
     print(f"[cfg4 full size] top-k overlap with float64 selection {ov:.5f}", flush=True)
     del sc
     _forward_checks(x["q"].bfloat16(), x["kv"].bfloat16(), idx, rows)
+
+
+def test_cfg3_full_size_indexer_topk_sparse_fwd_bwd():
+    """cfg3, the bench's headline shape: 16384 packed tokens in 4 causal documents (10363 / 4977 /
+    197 / 847), bf16 indexer 64 x 128, top-k 2048, then the 128-head sparse MLA forward and backward
+    on those indices.  Every row is checked: the top-k of every query (rows up to 10,363 keys, where
+    the top-k kernel sizes its LDS cache per launch) against a stable sort of the kernel's own fp32
+    scores inside its document; out / lse of every query and dq of every query and dkv of every key
+    against the chunked fp32 GPU references.  The float64 oracle checks sampled rows (top-k from
+    the kernel's scores, >= 99.9 % overlap with its own selection, scores, out / lse / dq) and sampled
+    keys (dkv), and pins the fp32 references on them."""
+    print("[cfg3 full size] T=16384 in 4 documents: indexer -> top-k -> sparse fwd + bwd", flush=True)
+    cfg = W.CONFIGS["cfg3"]
+    x = W.make_prefill(cfg, device=DEV, seed=3)
+    T, K, cu = cfg.S, cfg.K, cfg.docs
+    qi, ki, w = x.pop("q_idx").bfloat16(), x.pop("k_idx").bfloat16(), x.pop("w")
+    idx, sc = ops.indexer_topk(qi, ki, w, K, x["cu_seqlens"], causal=True, return_scores=True)
+    assert sc.shape[1] >= max(b - a for a, b in zip(cu[:-1], cu[1:]))
+    _topk_every_row_is_a_stable_sort(sc, idx, K, cu=cu)
+    print("[cfg3 full size] top-k of every row = stable sort of the kernel's scores", flush=True)
+    rows = sorted({0, 1, 31, 2047, 2048, 5000, 10362, cu[1], cu[1] + 2047, cu[1] + 2100, cu[2] + 100,
+                   cu[3] + 5, T - 1} | set(torch.randint(0, T, (8,), generator=torch.Generator().manual_seed(3)).tolist()))
+    ov = _sampled_rows_against_oracle(qi, ki, w, sc, idx, rows, K, cu=cu)
+    print(f"[cfg3 full size] top-k overlap with float64 selection {ov:.5f}", flush=True)
+    del sc, qi, ki, w
+    q, kv, dout = x["q"].bfloat16(), x["kv"].bfloat16(), x["dout"].bfloat16()
+    del x
+    out, lse = _forward_checks(q, kv, idx, rows)
+    print("[cfg3 full size] forward checked", flush=True)
+    dq, dkv = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    ref_dq, ref_dkv = sparse_mla_bwd_fp32(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    torch.cuda.synchronize()
+    close_on_device(dq, ref_dq, name="dq (every query, fp32 reference)")
+    close_on_device(dkv, ref_dkv, name="dkv (every key, fp32 reference)")
+    for name, got, ref in (("dq", dq, ref_dq), ("dkv", dkv, ref_dkv)):
+        err = ((got.float() - ref).norm() / ref.norm()).item()
+        print(f"[cfg3 full size] {name} normalised error vs fp32 reference {err:.2e}", flush=True)
+    # the float64 oracle on sampled queries (dq) and keys (dkv) pins both the kernels and the
+    # fp32 references there
+    si = torch.tensor(rows, device=DEV)
+    kvc = kv.cpu()
+    rdq, _ = O.sparse_mla_bwd(q[si].cpu(), kvc, idx[si].cpu(), out[si].cpu(), dout[si].cpu(), lse[si].cpu(),
+                              W.SM_SCALE)
+    _close(dq[si].cpu(), rdq, name="dq (oracle rows)")
+    _close(ref_dq[si].cpu(), rdq, rel=1e-3, tol=5e-3, name="fp32 dq reference vs oracle")
+    keys = [0, 7, 1000, 2047, 10362, cu[1], cu[2] + 3, cu[3], T - 2048, T - 1]
+    rdkv = O.sparse_mla_bwd_dkv_rows(q.cpu(), kvc, idx.cpu(), out.cpu(), dout.cpu(), lse.cpu(), W.SM_SCALE, keys)
+    _close(dkv[keys].cpu(), rdkv, name="dkv (oracle keys)")
+    _close(ref_dkv[keys].cpu(), rdkv, rel=1e-3, tol=5e-3, name="fp32 dkv reference vs oracle")

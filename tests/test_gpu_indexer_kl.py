@@ -406,7 +406,7 @@ def test_dsattention_module_composes_indexer_attention_and_loss():
             p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(p_.dtype))
         indexer.k_norm.weight.add_(1.0)
     coeff, sc = 0.5, W.SM_SCALE
-    attn = DSAttention(indexer, sc, loss_coeff=coeff)
+    attn = DSAttention(indexer, sc, loss_coeff=coeff, use_sparse_loss=True)
     query = (torch.randn(S, B, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
     key = (torch.randn(S, B, 576, generator=g) * 0.1).bfloat16().to(DEV)
     x = torch.randn(S, B, hidden, generator=g).bfloat16().to(DEV)
@@ -497,7 +497,7 @@ def test_dsattention_thd_packed_equals_per_document():
             p_.copy_((torch.randn(p_.shape, generator=g) * 0.05).to(p_.dtype))
         indexer.k_norm.weight.add_(1.0)
     coeff, sc = 0.5, W.SM_SCALE
-    attn = DSAttention(indexer, sc, loss_coeff=coeff)
+    attn = DSAttention(indexer, sc, loss_coeff=coeff, use_sparse_loss=True)
     query = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
     key = (torch.randn(T, 576, generator=g) * 0.1).bfloat16().to(DEV)
     x = torch.randn(T, 1, hidden, generator=g).bfloat16().to(DEV)
@@ -664,3 +664,58 @@ def test_dsattention_dense_loss_matches_the_separate_op():
                                     q_i.transpose(0, 1).reshape(B * S, Hi, 128), k_i.transpose(0, 1).reshape(B * S, 128),
                                     w.transpose(0, 1).reshape(B * S, Hi), W.SM_SCALE, 0.25, cu, S)
     torch.testing.assert_close(attn.last_indexer_loss, ref, rtol=1e-5, atol=1e-8)
+
+
+def test_fused_attention_with_indexer_loss_honours_the_workspace_cap():
+    """With ops.set_backward_workspace_limit below the one-pass size, the fused attention + indexer
+    loss backward runs the capped passes (target recomputed from the forward LSE) and gives the
+    uncapped result: the same loss and indexer gradients up to the bf16 rounding of the staged P,
+    dq bit-identical, dkv within the rounding of the pass order."""
+    print("[fused attention + indexer loss under a workspace cap]", flush=True)
+    from mcore_bridge_amd.dsa import sparse_mla_with_indexer_loss
+    g = torch.Generator().manual_seed(37)
+    T, H, Hi, K = 700, 64, 64, 128
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    qi, ki, w = (x.to(DEV) for x in _indexer_inputs(T, Hi, g))
+    idx = _idx_case(T, K, g, cu=[0, 400, T]).to(DEV)
+    dout = (torch.randn(T, H, 512, generator=g) * 0.01).bfloat16().to(DEV)
+    sc, coeff = W.SM_SCALE, 0.3
+    cap = ops.bwd_workspace_bytes_chunked(T, T, H, K, 256)
+    assert cap < ops.bwd_workspace_bytes(T, T, H, K)
+    res = []
+    for limit in (0, cap):
+        ops.set_backward_workspace_limit(limit)
+        try:
+            assert ops.backward_takes_one_pass(T, T, H, K) == (limit == 0)
+            leaves = [x.clone().requires_grad_() for x in (q, kv, qi, ki, w)]
+            out, loss = sparse_mla_with_indexer_loss(*leaves[:2], idx, *leaves[2:], sc, coeff, True)
+            (out.float() * dout.float()).sum().backward()
+            torch.cuda.synchronize()
+            res.append((loss.clone(), [x.grad.clone() for x in leaves]))
+        finally:
+            ops.set_backward_workspace_limit(0)
+    (la, ga), (lb, gb) = res
+    torch.testing.assert_close(lb, la, rtol=2e-3, atol=1e-7)
+    assert torch.equal(ga[0], gb[0]), "dq differs under the cap"
+    err = ((gb[1].double() - ga[1].double()).norm() / ga[1].double().norm()).item()
+    assert err < 1e-2, f"dkv: normalised difference {err:.2e}"
+    for name, a, b in zip(("q_idx", "k_idx", "w"), ga[2:], gb[2:]):
+        err = ((b.double() - a.double()).norm() / a.double().norm()).item()
+        assert err < 1e-2, f"{name}: normalised difference {err:.2e}"
+
+
+def test_dense_indexer_loss_of_an_empty_batch_is_zero():
+    """T = 0: the dense indexer loss is 0 and its backward gives empty gradients (no kernel is called
+    with zero key columns)."""
+    print("[dense indexer loss] empty batch", flush=True)
+    from mcore_bridge_amd.dsa import indexer_kl_loss_dense
+    q = torch.empty(0, 16, 576, dtype=torch.bfloat16, device=DEV)
+    kv = torch.empty(0, 576, dtype=torch.bfloat16, device=DEV)
+    qi = torch.empty(0, 64, 128, dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    ki = torch.empty(0, 128, dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    w = torch.empty(0, 64, dtype=torch.float32, device=DEV, requires_grad=True)
+    loss = indexer_kl_loss_dense(q, kv, qi, ki, w, W.SM_SCALE, 0.5)
+    assert float(loss.detach()) == 0.0
+    loss.backward()
+    assert qi.grad.shape == qi.shape and ki.grad.shape == ki.shape and w.grad.shape == w.shape

@@ -116,3 +116,35 @@ def test_absorbed_mla_swap_trains_the_indexer_with_the_sparse_loss():
     assert bool(torch.isfinite(loss_d)) and float(loss_d) > 0
     for n, p in indexer.named_parameters():
         assert p.grad is not None and bool(torch.isfinite(p.grad).all()) and float(p.grad.abs().sum()) > 0, n
+
+
+@pytest.mark.parametrize("flag", ["checkpoint_core_attention", "recompute_up_proj"])
+@pytest.mark.parametrize("sparse", [True, False])
+def test_absorbed_mla_recompute_flags_give_the_same_training_step(flag, sparse):
+    """The reference's recompute flags (multi_latent_attention.py:180-185, 250-252) checkpoint the
+    absorbed attention (and the q up-projection): the kernels run again in the backward and give the
+    same output, indexer loss and gradients as without the flag, bit for bit (the kernels are
+    deterministic)."""
+    print(f"[absorbed MLA swap] {flag}, sparse loss {sparse}", flush=True)
+    res = []
+    for on in (False, True):
+        mod, indexer, g = _build(coeff=0.3, seed=4)
+        mod.config.dsa_indexer_use_sparse_loss = sparse
+        if on:
+            setattr(mod, flag, True)
+        S, B, hidden = 64, 2, 256
+        x = torch.randn(S, B, hidden, generator=g).bfloat16().to(DEV).requires_grad_()
+        rope = (torch.rand(S, 1, 1, 64, generator=g) * 100).to(DEV)
+        mod.train()
+        out, _ = mod(x, None, rotary_pos_emb=rope)
+        (out.float() * 0.01).sum().backward()
+        torch.cuda.synchronize()
+        grads = {n: p.grad.clone() for n, p in list(mod.named_parameters()) + list(indexer.named_parameters(prefix="ix"))
+                 if p.grad is not None}
+        res.append((out.detach(), x.grad.clone(), grads, mod.last_indexer_loss.clone()))
+    (o0, dx0, g0, l0), (o1, dx1, g1, l1) = res
+    assert torch.equal(o0, o1) and torch.equal(dx0, dx1) and torch.equal(l0, l1)
+    assert float(l1) > 0
+    assert g0.keys() == g1.keys()
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n

@@ -662,46 +662,6 @@ def test_sparse_fwd_bwd_no_query_rows():
 
 
 
-def test_sparse_fwd_bwd_cfg3_full_size():
-    """cfg3 at the bench's full size (T = 16384 in 4 documents, H = 128, K = 2048, indices from the
-    indexer + top-k kernels): out/lse and dq of sampled queries against the oracle on those rows,
-    dkv of sampled keys against the oracle's per-key closed form over every query that selected
-    them (each row depends only on its own pairs, so the samples are exact checks)."""
-    print("[sparse fwd+bwd cfg3 full size]", flush=True)
-    cfg = W.CONFIGS["cfg3"]
-    x = W.make_prefill(cfg, device=DEV, seed=3)
-    T, cu = cfg.S, x["cu_seqlens"]
-    idx = ops.indexer_topk(x["q_idx"].bfloat16(), x["k_idx"].bfloat16(), x["w"], cfg.K, cu, causal=True)
-    q = x["q"].bfloat16()
-    kv = x["kv"].bfloat16()
-    dout = x["dout"].bfloat16()
-    del x
-    out, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
-    dq, dkv = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
-    # out / lse of EVERY query against an fp32 reference: the per-key dKV oracle below takes the
-    # kernel's out and lse of every selecting query, so those must be verified rows, not assumed
-    from gpu_reference import close_on_device, sparse_mla_fwd_fp32
-    ref_o, ref_l = sparse_mla_fwd_fp32(q, kv, idx, W.SM_SCALE, True)
-    torch.cuda.synchronize()
-    close_on_device(out, ref_o, name="out (all rows, fp32 reference)")
-    torch.testing.assert_close(lse, ref_l, rtol=1e-4, atol=1e-4)
-    del ref_o, ref_l
-    starts = cfg.docs[:-1]
-    sample = sorted({0, 1, 31, 2047, 2048, 5000, 10362, starts[1], starts[1] + 2100, starts[2] + 100,
-                     starts[3] + 5, T - 1})
-    si = torch.tensor(sample)
-    qs, idxs = q[si.to(DEV)].cpu(), idx[si.to(DEV)].cpu()
-    kvc = kv.cpu()
-    ro, rl = O.sparse_mla_fwd(qs, kvc, idxs, W.SM_SCALE)
-    _close(out[si.to(DEV)].cpu(), ro, name="out")
-    torch.testing.assert_close(lse[si.to(DEV)].cpu().double(), rl, rtol=1e-4, atol=1e-4)
-    rdq, _ = O.sparse_mla_bwd(qs, kvc, idxs, out[si.to(DEV)].cpu(), dout[si.to(DEV)].cpu(), lse[si.to(DEV)].cpu(),
-                              W.SM_SCALE)
-    _close(dq[si.to(DEV)].cpu(), rdq, name="dq")
-    keys = [0, 7, 1000, 10362, starts[1], starts[2] + 3, T - 2048, T - 1]
-    rdkv = O.sparse_mla_bwd_dkv_rows(q.cpu(), kvc, idx.cpu(), out.cpu(), dout.cpu(), lse.cpu(), W.SM_SCALE, keys)
-    _close(dkv[keys].cpu(), rdkv, name="dkv")
-
 def test_sparse_decode_cfg5_full_size():
     """cfg5 at full size: the split decode equals the unsplit non-causal forward kernel on the same
     inputs (a size-independent property), and the oracle on two whole sequences."""
