@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 typedef __bf16 bf16_t;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -76,6 +78,16 @@ DSA_DEV void mfma_acc_drain() {
 }
 
 DSA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// f(std::integral_constant<int, i>) for i = B .. E-1: a loop whose index is a compile-time
+// constant in the body (template arguments such as a copy's LDS offset).
+template <int B, int E, class F>
+DSA_DEV void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // 16-byte LDS / global access helpers.
 DSA_DEV u32x4 lds_load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

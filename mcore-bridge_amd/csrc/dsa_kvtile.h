@@ -110,6 +110,54 @@ DSA_DEV void gather_issue(uint32_t tile, const TileSrc<NW>& src, const char* row
   }
 }
 
+// LDS byte addresses of this wave's share of one tile (wave-uniform): v = the V row of key w
+// (key_row(w) = 2w), rope = its first rope group.  Computed once per tile, so each copy sets M0
+// with a single s_add_u32 of a compile-time offset.
+struct TileDst {
+  uint32_t v, rope;
+};
+template <int NW>
+DSA_DEV TileDst tile_dst(uint32_t tile, uint32_t wsg) {
+  return TileDst{tile + 2u * wsg * kTileVPitch, tile + kTileVBytes + wsg * 1024u};
+}
+
+// copy_row16 with M0 = base + OFF (one SALU instruction; the LDS DMA reads M0 one wait state
+// later: s_nop 0).
+template <uint32_t OFF>
+DSA_DEV void copy_row16_at(uint32_t base, const char* row, uint32_t lane_off) {
+  asm volatile("s_add_u32 m0, %0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3" ::"s"(base), "i"(OFF),
+               "v"(lane_off), "s"(row)
+               : "memory", "m0", "scc");
+}
+template <uint32_t OFF>
+DSA_DEV void copy16_at(const void* gsrc, uint32_t base) {
+  asm volatile("s_add_u32 m0, %0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off" ::"s"(base), "i"(OFF), "v"(gsrc)
+               : "memory", "m0", "scc");
+}
+
+// gather_issue with the wave's TileDst: M0 = an SGPR base plus a constant once k is one (the
+// callers' unrolled loops), no per-copy readfirstlane.
+template <int NW>
+DSA_DEV void gather_issue_dst(const TileDst& d, const TileSrc<NW>& src, const char* row, int lane, int k) {
+  if (k < 32 / NW) {
+    copy_row16(d.v + key_row(NW * k) * kTileVPitch, row, (uint32_t)lane * 16u);
+  } else {
+    const int j = k - 32 / NW;
+    async_copy16_unordered(src.rope[j], d.rope + NW * j * 1024u);
+  }
+}
+
+// gather_issue for a compile-time copy index K with the wave's TileDst.
+template <int NW, int K>
+DSA_DEV void gather_issue_at(const TileDst& d, const TileSrc<NW>& src, const char* row, int lane) {
+  if constexpr (K < 32 / NW) {
+    copy_row16_at<key_row(NW * K) * kTileVPitch>(d.v, row, (uint32_t)lane * 16u);
+  } else {
+    constexpr int j = K - 32 / NW;
+    copy16_at<NW * j * 1024u>(src.rope[j], d.rope);
+  }
+}
+
 // The whole gather of one tile (all of this wave's copies back to back; rows read two copies
 // ahead, the first two behind one explicit 5-wait-state pad).
 template <int NW>

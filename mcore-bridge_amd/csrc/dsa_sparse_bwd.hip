@@ -156,6 +156,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   const uint32_t qk_v = key_row(hl) * kTileVPitch + 16u * hb;
   const uint32_t qk_r = kTileVBytes + hl * 128u + 16u * (hb ^ ((hl >> 1) & 7u));
   const uint32_t tile0 = lds_addr(sm.tile[0]);
+  const uint32_t wsg = __builtin_amdgcn_readfirstlane(wave);
 
   if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
   if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
@@ -181,6 +182,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     const char* next_row = gather_next ? gather_row<NW>(next_src, 0) : nullptr;
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t next_tile = tile0 + st_next;
+    const TileDst nd = tile_dst<NW>(next_tile, wsg);
     const uint32_t tb = tile0 + st_cur;   // 128-byte aligned: the rope XOR stays in its row
     st_cur = st_cur == 2 * kTileBytes ? 0 : st_cur + kTileBytes;
     st_next = st_next == 2 * kTileBytes ? 0 : st_next + kTileBytes;
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         if (ks == 0) mfma32x32x16_acc_first(dp, cur, df[0]);
         else if (ks < kDv / 16) mfma32x32x16_acc(dp, cur, df[ks]);
         if (ks % kCopyEvery == 0 && gather_next) {
-          gather_issue<NW>(next_tile, next_src, next_row, wave, lane, ks / kCopyEvery);
+          gather_issue_dst<NW>(nd, next_src, next_row, lane, ks / kCopyEvery);
           next_row = gather_row<NW>(next_src, ks / kCopyEvery + 1);
         }
         if (ks % 8 == 1 && ks < 32 && store_prev) {

@@ -159,6 +159,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       }
   }
   const uint32_t tile0 = lds_addr(sm.tile[0]);
+  const uint32_t wsg = __builtin_amdgcn_readfirstlane(wave);
 
   // PV, split by latent dims: wave w accumulates O^T[dims DT*32*w .. +DT*32) x all NH*32 heads]
   // (o[m' * NH + n] = dim tile m', head tile n) from its own quarter of the V^T tile and the
@@ -233,8 +234,10 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       const bool gather_next = blk + 1 < nblk;
       TileSrc<NW> next_src;
       if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 1) * kBK, wave, lane);
-      // source row of the next copy, read one copy slot ahead of its issue
-      const char* next_row = gather_next ? gather_row<NW>(next_src, 0) : nullptr;
+      // source rows of the next two copies, each read two copy slots ahead of its issue (with one
+      // wave the copies are one MFMA apart)
+      const char* next_row[2] = {gather_next ? gather_row<NW>(next_src, 0) : nullptr,
+                                 gather_next ? gather_row<NW>(next_src, 1) : nullptr};
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t next_tile = tile0 + st_next;
       // per-block absolute operand addresses (tiles are 128-byte aligned: the rope XOR below
@@ -246,7 +249,9 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       asm volatile("" : "+v"(qv), "+v"(qr));
       const uint32_t vmask = (uint32_t)__ballot(sm.idx[blk * kBK + (lane & 31)] >= 0);
 
-      // ---- S^T[32 keys x 32 heads] = K . Q^T  (A operands prefetched)
+      // ---- S^T[32 keys x 32 heads] = K . Q^T  (A operands prefetched).  Two instances of the
+      // MFMA sequence, with and without block blk+1's gather (the last block has none), so no
+      // copy sits behind a branch; each copy sets M0 with one s_add of a compile-time offset.
       f32x16 s;
       {
         auto qk_addr = [&](int ks) { return lds_ptr(ks < 32 ? (qv + 32u * ks) : (qr ^ (32u * (ks - 32)))); };
@@ -254,18 +259,24 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
 #pragma unroll
         for (int i = 0; i < kPre; ++i) a[i] = lds_load16(qk_addr(i));
         f32x16 sa;
-#pragma unroll
-        for (int ks = 0; ks < kDqk / 16; ++ks) {
-          const u32x4 cur = a[ks % kPre];
-          if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
-          if (ks == 0) mfma32x32x16_cV_first(sa, cur, qf[0]);
-          else mfma32x32x16_cV(sa, cur, qf[ks]);
-          if (ks % kCopyEvery == 0 && gather_next) {
-            gather_issue<NW>(next_tile, next_src, next_row, wave, lane, ks / kCopyEvery);
-            next_row = gather_row<NW>(next_src, ks / kCopyEvery + 1);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        const TileDst nd = tile_dst<NW>(next_tile, wsg);
+        auto qk = [&](auto gather) {
+          static_for<0, kDqk / 16>([&](auto ksc) {
+            constexpr int ks = decltype(ksc)::value;
+            const u32x4 cur = a[ks % kPre];
+            if constexpr (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
+            if constexpr (ks == 0) mfma32x32x16_cV_first(sa, cur, qf[0]);
+            else mfma32x32x16_cV(sa, cur, qf[ks]);
+            if constexpr (decltype(gather)::value && ks % kCopyEvery == 0) {
+              constexpr int k = ks / kCopyEvery;
+              gather_issue_at<NW, k>(nd, next_src, next_row[k & 1], lane);
+              next_row[k & 1] = gather_row<NW>(next_src, k + 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          });
+        };
+        if (gather_next) qk(std::true_type{});
+        else qk(std::false_type{});
         s = sa;
       }
       mfma_acc_drain();
