@@ -20,6 +20,8 @@ The line also carries:
                       e4m3 key cache, and the graph-replayed step;
   "indexer_prologue"  the fused producer of the indexer's inputs at the cfg3 token count (HBM);
   "indexer_kl"        the sparse indexer KL loss and the indexer-score backward at cfg3;
+  "v4"                the DeepSeek-V4 CSA layer core (sink attention fwd + bwd, 512-wide K = V) at
+                      T = 16384, H = 128, window 128 + top-512 compressed entries;
   "cpu_baseline"      the oracle's reference-shaped fp32 compositions timed on the host per config
                       (cfg1 whole; cfg2/cfg3/cfg4 a few query rows, extrapolated by visible keys;
                       cfg5 every sequence) -- a reported baseline, not the target.
@@ -409,6 +411,61 @@ def _time_ms(torch, fn, reps: int, warm: int = 2):
 PEAK_FP8_TFLOPS = 5000.0
 
 
+def v4_leg(torch, dev, reps: int = 5):
+    """DeepSeek-V4 compressed sparse attention layer core (reference deepseek_v4.py:61-328; the core
+    attention of its CSA layers) on the DSA kernels: one document of T = 16384 tokens, H = 128 heads
+    over ONE shared 512-wide K = V head, a 128-token sliding window plus the CSA indexer's top-512
+    of the rate-4 compressed entries (index row width 640), per-head attention sink; forward +
+    backward of v4.sink_attention.  Algorithmic work with the 512-wide keys: forward 2 (512 + 512)
+    H per attended (query, key) pair, backward 2 (3 x 512 + 2 x 512) H.  The kernels run the 576-wide
+    row layout (rope region zero), so `kernels_ms` (the same fwd + bwd on pre-padded inputs) is what
+    the kernels take and `host_composition_ms` the rest: the 512 -> 576 pad copies, the sink fold,
+    the d sink reduction and the gradient slices."""
+    from mcore_bridge_amd import ops, v4
+    T, H, D, Wn, rate, Kc, Hi, Di = 16384, 128, 512, 128, 4, 512, 64, 128
+    cu = [0, T]
+    g = torch.Generator(device=dev).manual_seed(44)
+    q = (torch.randn(T, H, D, generator=g, device=dev) * 0.05).bfloat16()
+    Nc = T // rate
+    keys = (torch.randn(T + Nc, D, generator=g, device=dev)).bfloat16()
+    sinks = torch.randn(H, generator=g, device=dev)
+    qi = (torch.randn(T, Hi, Di, generator=g, device=dev) * 0.1).bfloat16()
+    ck = (torch.randn(Nc, Di, generator=g, device=dev) * 0.1).bfloat16()
+    wi = torch.randn(T, Hi, generator=g, device=dev) / 8
+    sel = v4.indexer_select(qi, ck, wi, cu, rate, Kc, Di)
+    idx = v4.hybrid_indices(cu, Wn, 0, sel, dev)
+    nsel = int((idx >= 0).sum().item())
+    dout = (torch.randn(T, H, D, generator=g, device=dev) * 0.01).bfloat16()
+    scale = D ** -0.5
+    t_sel = _time_ms(torch, lambda: v4.indexer_select(qi, ck, wi, cu, rate, Kc, Di), reps)
+
+    def layer_core():
+        qd, kd, sd = q.detach().requires_grad_(), keys.detach().requires_grad_(), sinks.detach().requires_grad_()
+        out, _ = v4.sink_attention(qd, kd, sd, idx, scale)
+        out.backward(dout)
+
+    qp = torch.nn.functional.pad(q, (0, ops.D_QK - D)).contiguous()
+    kp = torch.nn.functional.pad(keys, (0, ops.D_QK - D)).contiguous()
+
+    def kernels_only():
+        out, lse = ops.sparse_mla_fwd(qp, kp, idx, scale, False)
+        ops.sparse_mla_bwd(qp, kp, idx, out, dout, lse, scale, False)
+
+    t_all = _time_ms(torch, layer_core, reps)
+    t_k = _time_ms(torch, kernels_only, reps)
+    fl = (2 * (D + D) + 2 * (3 * D + 2 * D)) * H * nsel
+    tf = fl / (t_all * 1e-3) / 1e12
+    tfk = fl / (t_k * 1e-3) / 1e12
+    return {"workload": "DeepSeek-V4 CSA layer core: T=16384 (one document), H=128, one shared 512-wide K=V head, "
+                        "window 128 + top-512 of rate-4 compressed entries (indexer 64x128), attention sink; "
+                        "sink_attention fwd+bwd",
+            "n_sel": nsel, "flops": fl, "ms": round(t_all, 3), "tflops": round(tf, 1),
+            "kernels_ms": round(t_k, 3), "kernels_tflops": round(tfk, 1),
+            "host_composition_ms": round(t_all - t_k, 3), "csa_indexer_ms": round(t_sel, 3),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4)}}
+
+
 def prefill_fwd_leg(torch, dev, name: str, reps: int = 10):
     """cfg2 (bf16 indexer) or cfg4 (fp8 e4m3fn indexer with absmax row scales, S = 32768): one
     causal document, indexer scores, top-k 2048 and the bf16 sparse MLA forward (H = 128), each
@@ -686,6 +743,9 @@ def main():
         res["indexer_kl"] = indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale, nsel, ws)
         del idx, lse
         print(f"[bench] indexer KL leg done: {res['indexer_kl']['total_ms']} ms", file=sys.stderr, flush=True)
+    if not args.no_decode:
+        res["v4"] = v4_leg(torch, dev)
+        print(f"[bench] v4 leg done: {res['v4']['ms']} ms", file=sys.stderr, flush=True)
     if not args.no_decode:
         for name in ("cfg2", "cfg4"):
             res[name] = prefill_fwd_leg(torch, dev, name)

@@ -156,6 +156,17 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
                        int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
                        void* out, float* lse, void* stream);
 
+/* dsa_sparse_mla_fwd with a per-head attention sink: sinks [n_heads] fp32 natural-log logits of
+ * a column with no value row, out[t,h] = sum_j p_j kv[idx[t,j], :512] with p_j = exp(a_j) /
+ * (sum_k exp(a_k) + exp(sinks[h])), a_j = sm_scale * q[t,h] . kv[idx[t,j]], and lse[t,h] =
+ * ln(sum_k exp(a_k) + exp(sinks[h])) (a row without a valid index: out = 0, lse = sinks[h]).
+ * Replaces the core attention of the reference's DeepSeek-V4 layers with its
+ * core_attention.attn_sink (src/mcore_bridge/model/gpts/deepseek_v4.py:443; the layer
+ * :61-328, whose core attention is megatron-core's).  sinks == NULL is dsa_sparse_mla_fwd. */
+int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv,
+                            int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
+                            const float* sinks, void* out, float* lse, void* stream);
+
 /* Decode rows for the indexer and top-k: sequence b's new token (position L_b - 1) sees its
  * whole cache, rows [cu_cache[b], cu_cache[b+1]) of the packed cache: row_base[b] = cu_cache[b],
  * row_len[b] = L_b.  cu_cache [batch + 1] int32 on the device.  No reference counterpart: the
@@ -218,6 +229,19 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
                        const void* dout, const float* lse, int total_q, int n_kv, int n_heads,
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward of dsa_sparse_mla_fwd_sink (autograd of the same reference V4 core attention,
+ * deepseek_v4.py:443): dq and dkv as dsa_sparse_mla_bwd given the sink forward's out and lse
+ * (its P and Delta are then the sink softmax's), plus dsinks [n_heads] fp32 = -sum_t
+ * exp(sinks[h] - lse[t,h]) * rowsum(dout[t,h] * out[t,h]), a fixed-order sum (the same bit for
+ * bit from run to run).  The workspace holds the rowsums [total_q, n_heads] fp32 at its end and
+ * the backward's own workspace before them: at least dsa_sparse_mla_bwd_sink_workspace_size()
+ * bytes for one pass (a smaller one runs the passes of dsa_sparse_mla_bwd). */
+size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk);
+int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, const void* out,
+                            const void* dout, const float* lse, const float* sinks, int total_q, int n_kv,
+                            int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq,
+                            float* dkv, float* dsinks, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Flags of dsa_sparse_mla_bwd_ex.
  * DSA_BWD_G_INT8: stage the per-(query, key) dKV partial rows as int8 with a bf16 scale per 32

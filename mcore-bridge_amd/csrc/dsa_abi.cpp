@@ -310,6 +310,13 @@ int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const 
 int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv, int n_heads,
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* out, float* lse,
                        void* stream) {
+  return dsa_sparse_mla_fwd_sink(q, kv, idx, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, nullptr,
+                                 out, lse, stream);
+}
+
+int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv, int n_heads,
+                            int d_qk, int d_v, int topk, float sm_scale, int causal, const float* sinks, void* out,
+                            float* lse, void* stream) {
   if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
     return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
@@ -327,6 +334,7 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
   p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
   p.out_stride_t = (int64_t)n_heads * kDv; p.lse_stride_t = n_heads;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
+  p.sinks = sinks;
   DSA_CHECK_DEVICE(dev);
   p.n_xcd = dev.n_xcd;
   return dsa::launch_sparse_mla_fwd(p, as_stream(stream));
@@ -445,10 +453,14 @@ int dsa_sparse_mla_bwd_timed(const void* q, const void* kv, const int32_t* idx, 
                                causal, dq, dkv, 0, workspace, workspace_bytes, stage_events, stream);
 }
 
-int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
-                          const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
-                          float sm_scale, int causal, void* dq, float* dkv, int flags, void* workspace,
-                          size_t workspace_bytes, void* const* stage_events, void* stream) {
+}  // extern "C"
+
+namespace {
+// The sparse backward; delta_out (nullable) receives rowsum(dO * O) [total_q, n_heads].
+int sparse_bwd(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout, const float* lse,
+               int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq,
+               float* dkv, int flags, void* workspace, size_t workspace_bytes, void* const* stage_events,
+               float* delta_out, void* stream) {
   if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
   if (flags & ~DSA_BWD_G_INT8) return DSA_ERR_INVALID_ARG;
   if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
@@ -507,10 +519,53 @@ int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, con
     p.q_offset = c0;
     p.dkv_accumulate = c0 > 0 ? 1 : 0;
     p.g_sink_row = (int64_t)rows * topk;
+    p.delta_out = delta_out ? delta_out + (int64_t)c0 * n_heads : nullptr;
     const int rc = dsa::launch_sparse_mla_bwd(p, as_stream(stream), reinterpret_cast<hipEvent_t const*>(stage_events));
     if (rc != 0) return rc;
   }
   return DSA_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
+                          const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
+                          float sm_scale, int causal, void* dq, float* dkv, int flags, void* workspace,
+                          size_t workspace_bytes, void* const* stage_events, void* stream) {
+  return sparse_bwd(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, dq, dkv,
+                    flags, workspace, workspace_bytes, stage_events, nullptr, stream);
+}
+
+size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1) return 0;
+  return bwd_layout(total_q, n_kv, n_heads, topk).total + align_up(sizeof(float) * (size_t)total_q * n_heads);
+}
+
+int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
+                            const float* lse, const float* sinks, int total_q, int n_kv, int n_heads, int d_qk,
+                            int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv, float* dsinks,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (total_q < 0 || n_heads < 1) return DSA_ERR_INVALID_ARG;
+  if (!sinks || !dsinks) return DSA_ERR_INVALID_ARG;
+  // Delta [total_q, n_heads] sits at the end of the workspace; the passes take the rest
+  const size_t dbytes = align_up(sizeof(float) * (size_t)total_q * n_heads);
+  if (!workspace || workspace_bytes < dbytes || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  const size_t rest = (workspace_bytes - dbytes) / 256 * 256;
+  float* delta = reinterpret_cast<float*>(static_cast<char*>(workspace) + rest);
+  if (total_q == 0) {
+    const int rc = sparse_bwd(q, kv, idx, out, dout, lse, 0, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, dq,
+                              dkv, 0, workspace, rest, nullptr, nullptr, stream);
+    if (rc != DSA_OK) return rc;
+    return dsa::launch_sink_grad(sinks, lse, delta, 0, n_heads, dsinks, as_stream(stream)) == 0 ? DSA_OK
+                                                                                                : DSA_ERR_LAUNCH;
+  }
+  const int rc = sparse_bwd(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal,
+                            dq, dkv, 0, workspace, rest, nullptr, delta, stream);
+  if (rc != DSA_OK) return rc;
+  return dsa::launch_sink_grad(sinks, lse, delta, total_q, n_heads, dsinks, as_stream(stream)) == 0
+             ? DSA_OK
+             : DSA_ERR_LAUNCH;
 }
 
 int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, const float* lse, int total_q,

@@ -22,6 +22,7 @@ struct SparseFwdParams {
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, lse_stride_t;
   float scale_log2;     // softmax scale * log2(e)
   int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
+  const float* sinks;   // [n_heads] per-head attention-sink logits (natural), or null; n_split == 1
 };
 
 // Per-pair dKV partial rows ("G rows") of the sparse backward, written by B3 and summed per key
@@ -61,6 +62,7 @@ struct SparseBwdParams {
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, dout_stride_t, lse_stride_t, dq_stride_t, dkv_stride;
   float scale, scale_log2;
   int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
+  float* delta_out;     // [total_q, n_heads] rowsum(dO * O) written by B1 (token stride n_heads), or null
 };
 
 struct IndexerParams {
@@ -215,6 +217,11 @@ inline size_t csr_count_entries(int total_q, int n_kv) {
 }
 void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int topk, int n_kv, int causal,
                      int t_offset, int32_t* csr_counts, int64_t* csr_offsets, int64_t* pair_pos, hipStream_t stream);
+// d sinks[h] = -sum_t exp(sinks[h] - lse[t, h]) * delta[t, h] (the gradient of per-head
+// attention-sink logits from the forward's sink-including LSE and B1's Delta), one fixed-order
+// reduction per head.
+int launch_sink_grad(const float* sinks, const float* lse, const float* delta, int total_q, int n_heads,
+                     float* dsinks, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
                           bf16_t* out, float* lse, hipStream_t stream);
 // Static per-device scratch of the allocation-free decode entry point (64 MiB): device address of

@@ -140,6 +140,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     }
   }
   delta = xor32_sum(delta);
+  if (p.delta_out != nullptr && head_ok && hb == 0) p.delta_out[(int64_t)t * p.n_heads + head] = delta;
   const float delta_s = delta * p.scale;
   const float lse = head_ok ? sm.lse[wave][lane] : -INFINITY;
   const float lse2 = lse * kLog2e;
@@ -852,6 +853,32 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* rows, int n_rows,
   const int r = blockIdx.x;
   if (r >= n_rows) return;
   for (int c = threadIdx.x; c < width; c += 256) rows[(int64_t)r * stride + c] = 0.f;
+}
+
+// d sinks: one workgroup per head, a fixed-order sum over the query rows (strided per thread, then
+// a wave and a cross-wave reduction), so the result is the same from run to run.
+__global__ __launch_bounds__(256) void sink_grad_kernel(const float* sinks, const float* lse, const float* delta,
+                                                        int total_q, int n_heads, float* dsinks) {
+  const int h = blockIdx.x;
+  __shared__ float part[4];
+  const float sk = sinks[h];
+  float acc = 0.f;
+  for (int t = threadIdx.x; t < total_q; t += 256) {
+    const float l = lse[(int64_t)t * n_heads + h];
+    if (l != -INFINITY) acc += expf(sk - l) * delta[(int64_t)t * n_heads + h];
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) dsinks[h] = 0.f - ((part[0] + part[1]) + (part[2] + part[3]));
+}
+
+int launch_sink_grad(const float* sinks, const float* lse, const float* delta, int total_q, int n_heads,
+                     float* dsinks, hipStream_t stream) {
+  if (n_heads < 1) return 0;
+  hipLaunchKernelGGL(sink_grad_kernel, dim3(n_heads), dim3(256), 0, stream, sinks, lse, delta, total_q, n_heads,
+                     dsinks);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 int launch_zero_rows(float* rows, int n_rows, int64_t stride, int width, hipStream_t stream) {

@@ -337,6 +337,26 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
     m_ref = xor32_max(m_seen);
   }
   l_run = xor32_sum(l_run);
+  // ---- per-head attention sink (a logit with no value): the row's normaliser gains
+  // exp(sink), O is scaled by 1 / (keys' sum + sink term), the LSE includes it.  Everything is
+  // taken relative to mf = max(key reference, sink) so neither term overflows.
+  float o_scale = l_run > 0.f ? 1.f / l_run : 0.f;
+  float lse_out = -INFINITY;
+  {
+    const float ms = m_set ? m_ref : -INFINITY;
+    if (p.sinks != nullptr) {
+      const float s2 = head_ok ? p.sinks[head] * kLog2e : -INFINITY;
+      const float mf = fmaxf(ms, s2);
+      if (mf != -INFINITY) {
+        const float rel = ms == -INFINITY ? 0.f : fast_exp2(ms - mf);   // keys' sum rescaled to mf
+        const float l_tot = l_run * rel + fast_exp2(s2 - mf);
+        o_scale = rel / l_tot;
+        lse_out = (mf + __log2f(l_tot)) * kLn2;
+      }
+    } else if (l_run > 0.f) {
+      lse_out = ((ms == -INFINITY ? 0.f : ms) + __log2f(l_run)) * kLn2;
+    }
+  }
 
   // ---- epilogue: normalise, store O (bf16) and LSE (natural log).  The output rows go
   // through LDS (the tile ring, P^T slots and index row are dead: every wave passed the
@@ -345,7 +365,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   // Stored straight from the accumulator layout, each store would write 32 rows 16 bytes
   // apart: 8x the L2 requests.
   mfma_acc_drain();
-  if (hb == 0) sm.inv_l[wave * 32 + hl] = l_run > 0.f ? 1.f / l_run : 0.f;
+  if (hb == 0) sm.inv_l[wave * 32 + hl] = o_scale;
   __syncthreads();
   {
 #pragma unroll
@@ -374,10 +394,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       *reinterpret_cast<u32x4*>(obase + (int64_t)r * kDv + 8 * lane) =
           lds_load16(slab + r * (kDv * 2) + 16 * (lane ^ (r & 7)));
   }
-  if (head_ok && hb == 0) {
-    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-    p.lse[orow * p.lse_stride_t + head] = l_run > 0.f ? (m_use + __log2f(l_run)) * kLn2 : -INFINITY;
-  }
+  if (head_ok && hb == 0) p.lse[orow * p.lse_stride_t + head] = lse_out;
 }
 
 // Decode split merge: out[b,h] = sum_s e^{lse_s} O_s / sum_s e^{lse_s} over the n_split
@@ -419,6 +436,7 @@ int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
   if (p.n_xcd < 1) return -1;
   if (p.split_keys > kMaxTopk || p.n_split < 1 || (p.n_split > 1 && p.split_keys % kBK != 0)) return -2;
   if ((int64_t)(p.n_split - 1) * p.split_keys >= p.topk) return -1;   // every split owns >= 1 slot
+  if (p.sinks != nullptr && p.n_split != 1) return -2;                  // a sink joins each row once
   const dim3 grid(xcd_grid(p.total_q * p.n_split, p.n_xcd), (p.n_heads + 127) / 128);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
   if (nw == 4)

@@ -335,6 +335,70 @@ def _(q, kv, idx, sm_scale, causal=False):
     return q.new_empty(T, H, D_V), q.new_empty(T, H, dtype=torch.float32)
 
 
+@torch.library.custom_op("dsa_amd::sparse_mla_fwd_sink", mutates_args=())
+def sparse_mla_fwd_sink(q: Tensor, kv: Tensor, idx: Tensor, sinks: Tensor, sm_scale: float,
+                        causal: bool = False) -> Tuple[Tensor, Tensor]:
+    """``sparse_mla_fwd`` with a per-head attention sink ``sinks [H]`` (a logit with no value row):
+    ``(out [T,H,512] bf16, lse [T,H] fp32)``, the sink counted in the softmax and in ``lse``."""
+    _check_attn(q, kv, idx)
+    _require_gpu(sinks)
+    q = q.contiguous()
+    kv = kv.contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, H, _ = q.shape
+    sk = sinks.to(torch.float32).contiguous()
+    _require(sk.shape == (H,), "sinks must be [H]")
+    out = torch.empty(T, H, D_V, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_sparse_mla_fwd_sink", _p(q), _p(kv), _p(idx), T, kv.shape[0], H, D_QK, D_V, idx.shape[1],
+                  float(sm_scale), int(causal), _p(sk), _p(out), _p(lse), _stream(q.device))
+    return out, lse
+
+
+@sparse_mla_fwd_sink.register_fake
+def _(q, kv, idx, sinks, sm_scale, causal=False):
+    T, H, _ = q.shape
+    return q.new_empty(T, H, D_V), q.new_empty(T, H, dtype=torch.float32)
+
+
+@torch.library.custom_op("dsa_amd::sparse_mla_bwd_sink", mutates_args=())
+def sparse_mla_bwd_sink(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sinks: Tensor,
+                        sm_scale: float, causal: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``sparse_mla_fwd_sink`` from its ``out`` and ``lse``: ``(dq [T,H,576] bf16,
+    dkv [N,576] fp32, dsinks [H] fp32)``.  One pass, or the capped passes of
+    ``set_backward_workspace_limit``."""
+    _check_attn(q, kv, idx)
+    _require_gpu(out, dout, lse, sinks)
+    q, kv, out, lse = q.contiguous(), kv.contiguous(), out.contiguous(), lse.contiguous()
+    dout = dout.to(torch.bfloat16).contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    T, H, _ = q.shape
+    N, K = kv.shape[0], idx.shape[1]
+    sk = sinks.to(torch.float32).contiguous()
+    dq = torch.empty_like(q)
+    dkv = torch.empty(N, D_QK, dtype=torch.float32, device=q.device)
+    dsk = torch.empty(H, dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    ws_bytes = int(lib.dsa_sparse_mla_bwd_sink_workspace_size(T, N, H, K))
+    limit = _BWD_WORKSPACE_LIMIT[0]
+    if 0 < limit < ws_bytes:
+        dbytes = (T * H * 4 + 255) // 256 * 256
+        ws_bytes = max(int(limit), bwd_workspace_bytes_chunked(T, N, H, K, 256) + dbytes)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_sparse_mla_bwd_sink", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), _p(sk), T, N, H,
+                  D_QK, D_V, K, float(sm_scale), int(causal), _p(dq), _p(dkv), _p(dsk), _p(ws), ws.numel(),
+                  _stream(q.device))
+    return dq, dkv, dsk
+
+
+@sparse_mla_bwd_sink.register_fake
+def _(q, kv, idx, out, dout, lse, sinks, sm_scale, causal=False):
+    return (torch.empty_like(q), kv.new_empty(kv.shape[0], D_QK, dtype=torch.float32),
+            sinks.new_empty(q.shape[1], dtype=torch.float32))
+
+
 def decode_workspace_bytes(batch: int, n_heads: int, topk_: int) -> int:
     return int(_lib.load().dsa_sparse_mla_decode_workspace_size(batch, n_heads, topk_))
 

@@ -15,10 +15,11 @@ Kernel mapping (no new arithmetic kernel):
 - every query's key list -- its sliding window over the raw rows, then the compressed entries it
   may see (CSA: the indexer's top-k; HCA: all of them) -- is one index row over the
   concatenation ``[raw rows; compressed entries]``;
-- the sink is a logit with no value: ``lse' = logaddexp(lse, sink_h)``, ``out' = out *
-  exp(lse - lse')``.  The backward of K4 fed ``(out', lse')`` is exactly the sink-augmented
-  attention's (its P and Delta are then the sink softmax's), and ``d sink_h = -sum_t
-  exp(sink_h - lse'[t,h]) * rowsum(dO' * out')``;
+- the sink is a logit with no value, folded into the forward kernel's normaliser (``lse' =
+  logaddexp(lse, sink_h)``, ``out' = out * exp(lse - lse')``, ``dsa_sparse_mla_fwd_sink``).  The
+  backward of K4 fed ``(out', lse')`` is exactly the sink-augmented attention's (its P and Delta
+  are then the sink softmax's), and ``d sink_h = -sum_t exp(sink_h - lse'[t,h]) * Delta[t,h]``
+  from B1's Delta rows (``dsa_sparse_mla_bwd_sink``);
 - the CSA indexer is K1 + K2 over the compressed index keys: query t's row is its document's
   entries ``w < (t - start + 1) // rate``; the scorer's ``softmax_scale`` is folded into the head
   weights (ReLU is positively homogeneous).
@@ -48,26 +49,21 @@ class _SinkAttention(torch.autograd.Function):
     def forward(ctx, q: Tensor, kv: Tensor, sinks: Tensor, idx: Tensor, scale: float):
         q_p = F.pad(q, (0, ops.D_QK - HEAD_DIM)).contiguous()
         kv_p = F.pad(kv, (0, ops.D_QK - HEAD_DIM)).contiguous()
-        out, lse = ops.sparse_mla_fwd(q_p, kv_p, idx, scale, False)
-        lse_s = torch.logaddexp(lse, sinks.float()[None])
-        out_s = (out.float() * torch.exp(lse - lse_s)[..., None]).to(q.dtype)
-        ctx.save_for_backward(q_p, kv_p, idx, out_s, lse_s, sinks)
+        out, lse = ops.sparse_mla_fwd_sink(q_p, kv_p, idx, sinks, scale, False)   # the sink folded in-kernel
+        ctx.save_for_backward(q_p, kv_p, idx, out, lse, sinks)
         ctx.scale = scale
         ctx.kv_dtype = kv.dtype
-        ctx.mark_non_differentiable(lse_s)
-        return out_s, lse_s
+        ctx.mark_non_differentiable(lse)
+        return out, lse
 
     @staticmethod
     def backward(ctx, dout: Tensor, dlse: Tensor):
-        q_p, kv_p, idx, out_s, lse_s, sinks = ctx.saved_tensors
-        dq = dkv = dsinks = None
-        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-            dq_p, dkv_p = ops.autograd_backward(q_p, kv_p, idx, out_s, dout.contiguous(), lse_s, ctx.scale, False)
-            dq, dkv = dq_p[..., :HEAD_DIM], dkv_p[:, :HEAD_DIM].to(ctx.kv_dtype)
-        if ctx.needs_input_grad[2]:
-            delta = (dout.float() * out_s.float()).sum(-1)                       # [T, H]
-            dsinks = -(torch.exp(sinks.float()[None] - lse_s) * delta).sum(0).to(sinks.dtype)
-        return dq, dkv, dsinks, None, None
+        q_p, kv_p, idx, out, lse, sinks = ctx.saved_tensors
+        dq_p, dkv_p, dsinks = ops.sparse_mla_bwd_sink(q_p, kv_p, idx, out, dout.contiguous(), lse, sinks, ctx.scale,
+                                                      False)
+        dq = dq_p[..., :HEAD_DIM] if ctx.needs_input_grad[0] else None
+        dkv = dkv_p[:, :HEAD_DIM].to(ctx.kv_dtype) if ctx.needs_input_grad[1] else None
+        return dq, dkv, dsinks.to(sinks.dtype) if ctx.needs_input_grad[2] else None, None, None
 
 
 def sink_attention(q: Tensor, kv: Tensor, sinks: Tensor, idx: Tensor, scale: float) -> Tuple[Tensor, Tensor]:
@@ -126,11 +122,12 @@ def hybrid_indices(cu_seqlens: Sequence[int], window: int, rate: int = 0, comp_s
 
 
 def indexer_select(q_idx: Tensor, comp_k: Tensor, w: Tensor, cu_seqlens: Sequence[int], rate: int, topk: int,
-                   index_head_dim: int) -> Tensor:
+                   index_head_dim: int, return_scores: bool = False):
     """The CSA lightning indexer on the kernels: ``I[t, s] = sum_h w[t,h] relu(q_idx[t,h] . k[s]) *
     index_head_dim^-0.5`` over the compressed index keys ``comp_k [Nc, Di]`` of t's document with
     ``s < (t - start + 1) // rate``; returns ``[T, topk]`` int32 ids into the compressed array
-    (ascending, ``-1`` pad)."""
+    (ascending, ``-1`` pad) and, with ``return_scores``, the fp32 scores ``[T, pitch]`` the top-k
+    selected from (column j = entry ``doc offset + j``; ``-inf`` past each row)."""
     cu, lens, start = _docs(cu_seqlens, q_idx.device)
     T = cu[-1]
     off = compressed_layout(cu, rate)
@@ -142,8 +139,9 @@ def indexer_select(q_idx: Tensor, comp_k: Tensor, w: Tensor, cu_seqlens: Sequenc
     pitch = (max_len + 3) // 4 * 4
     wf = w.float() * index_head_dim ** -0.5
     sc = ops.indexer_scores(q_idx.contiguous(), comp_k.contiguous(), wf.contiguous(), row_base, row_len, max_len,
-                            pitch, None, None, False)
-    return ops.topk(sc, row_base, row_len, topk)
+                            pitch, None, None, return_scores)
+    idx = ops.topk(sc, row_base, row_len, topk)
+    return (idx, sc) if return_scores else idx
 
 
 # --------------------------------------------------------------------------------------
@@ -264,6 +262,7 @@ class DSv4HybridAttention(torch.nn.Module):
         assert layer_type in ("sliding_attention", "compressed_sparse_attention", "heavily_compressed_attention")
         kw = dict(device=device, dtype=dtype)
         self.layer_type, self.H, self.window, self.eps = layer_type, num_heads, window, eps
+        self.keep_index_scores = False   # CSA: keep the indexer's fp32 scores in last_index_scores
         self.o_groups, self.o_lora_rank = o_groups, o_lora_rank
         self.rope_layer_type = "main" if layer_type == "sliding_attention" else "compress"
         self.mscale = mscale if self.rope_layer_type == "main" else compress_mscale
@@ -329,7 +328,10 @@ class DSv4HybridAttention(torch.nn.Module):
                     ck = rope_interleaved(ix.compressor(x, cu, self.eps), cang, self.mscale)
                     qi = rope_interleaved(ix.linear_wq_b(q_res).view(T, ix.n_heads, ix.head_dim), ang, self.mscale)
                     wi = ix.linear_weights_proj(x).float() * ix.n_heads ** -0.5
-                    comp_sel = indexer_select(qi, ck, wi, cu, self.rate, ix.topk, ix.head_dim)
+                    comp_sel = indexer_select(qi, ck, wi, cu, self.rate, ix.topk, ix.head_dim,
+                                              return_scores=self.keep_index_scores)
+                    if self.keep_index_scores:
+                        comp_sel, self.last_index_scores = comp_sel
                 self.last_indexer_selection = comp_sel
         idx = hybrid_indices(cu, self.window, self.rate if comp_sel is None else 0, comp_sel, dev)
         o, _ = sink_attention(q, keys, ca.attn_sink, idx, HEAD_DIM ** -0.5)
