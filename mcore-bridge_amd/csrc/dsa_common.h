@@ -26,6 +26,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define DSA_DEV __device__ __forceinline__
+#define DSA_HOST_DEV __host__ __device__ __forceinline__
 
 namespace dsa {
 

@@ -10,7 +10,7 @@
 // row-major with column j <-> key row_base + j, which is also the layout of the reference's
 // returned index_scores when there is one document.
 //
-// K1: one wave = one (query, key chunk of 256..2048 keys; shorter chunks when there are few
+// K1: one wave = one (query, key chunk of 256..4096 keys; shorter chunks when there are few
 // queries, e.g. decode, so that enough waves stream keys at once).  Q[64 heads x 128] stays in registers as the A
 // operand (row = head), key rows are the B operand loaded straight from global memory (256 B
 // per key, shared by the 4 waves of a workgroup through L1/L2); C[heads x 32 keys] is reduced
@@ -24,18 +24,29 @@
 // I = k_scale[s] * sum_h (w * q_scale)[t,h] * relu(q8 . k8) -- valid because ReLU is
 // positive-homogeneous and both scales are > 0.
 //
-// K2: one workgroup per row.  4 passes of 8-bit MSB-first radix select over order-preserving
-// uint32 keys (LDS histograms) find the exact K-th largest value; one stable compaction pass
-// (each wave ranks 64 consecutive keys per step with ballots) then emits every larger key plus
-// the lowest-index ties, in ascending key order, -1 padded.  Fewer than 256 rows longer than a slice (decode) are split: a workgroup
+// K2: one workgroup per row, over order-preserving uint32 keys of the fp32 scores.  Rows of
+// 4096 .. 65536 entries with K small against them take the sampled-threshold path
+// (block_select_topk_sampled): a bound from a 2048-entry sample, one streaming pass collecting
+// the ~1.5 K entries above it, the exact K-th largest selected over those candidates, and the
+// selection emitted through a position bitmap.  Other rows (and rows whose bound misses): 4
+// passes of 8-bit MSB-first radix select (LDS histograms, the row cached in LDS when it fits,
+// else a three-pass candidate path over global memory) find the exact K-th largest value; one
+// stable compaction pass (each wave ranks 64 consecutive keys per step with ballots) then emits
+// every larger key plus the lowest-index ties.  Every path emits the same indices: ascending key
+// order, -1 padded.  Fewer than 256 rows longer than a slice (decode) are split: a workgroup
 // per (row, 16384-key slice) keeps the slice's top-K, one per row then selects from those.
+#include <algorithm>
 #include "dsa_common.h"
 #include "dsa_kernels.h"
 
 namespace dsa {
 
 namespace {
-constexpr int kIdxChunkMax = 2048;  // keys per wave work item (prefill)
+// keys per workgroup work item (prefill); 4096 against 2048: cfg4's fp8 scores 4.66 -> 4.39 ms
+// (half the per-workgroup setups: Q, weights and key-scale staging, each a memory round trip)
+constexpr int kIdxChunkMax = 4096;
+// fp8 key-block ring depth (4 KB stages): 4 against 3 measured 4.66 vs 4.89 ms at cfg4 (6: 4.70)
+constexpr int kFp8Stages = 4;
 constexpr int kIdxChunkMin = 256;
 constexpr int kIdxWaveTarget = 8192;   // shrink the chunk until this many work items exist
 constexpr int kRowsMode = 512;      // at most this many queries (128-dim rows): the rows kernels
@@ -154,16 +165,17 @@ DSA_DEV void indexer_block_lds_fp8(const IndexerParams& p, int t, int c0, int c1
     const int r = wu * 8 + (lane >> 3), u = lane & 7;
     const int key = base + min(k0 + r, c1_wg - 1);
     async_copy16_unordered(kbase + (int64_t)key * RB + 16 * (u ^ row_swz<RB>(r)),
-                           __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)((blk % 3) * BLK + wu * 1024)));
+                           __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)((blk % kFp8Stages) * BLK + wu * 1024)));
   };
   const int nb = (c1_wg - c0 + 31) / 32;
-  issue(0, c0);
-  if (nb > 1) issue(1, c0 + 32);
+#pragma unroll
+  for (int b = 0; b < kFp8Stages - 1; ++b)
+    if (b < nb) issue(b, c0 + 32 * b);
   for (int i = 0; i < nb; ++i) {
-    if (i + 1 < nb) wait_vmcnt<1>(); else wait_vmcnt<0>();
+    if (i + kFp8Stages - 2 < nb) wait_vmcnt<kFp8Stages - 2>(); else wait_vmcnt<0>();
     __syncthreads();
-    if (i + 2 < nb) issue(i + 2, c0 + 32 * (i + 2));
-    const char* row = ring + (i % 3) * BLK + hl * RB;
+    if (i + kFp8Stages - 1 < nb) issue(i + kFp8Stages - 1, c0 + 32 * (i + kFp8Stages - 1));
+    const char* row = ring + (i % kFp8Stages) * BLK + hl * RB;
     i32x8 kb[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -236,6 +248,7 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerParams p) {
           }
         }
         wait_vmcnt0();
+        static_assert(kFp8Stages >= 3 && kFp8Stages * 32 * 128 <= (int)sizeof(ring), "fp8 ring stages fit the ring");
         indexer_block_lds_fp8(p, t, c0, c1_wg, c1, base, wr, qa8, ring, ks_s);
         return;
       }
@@ -857,6 +870,358 @@ DSA_DEV bool block_select_topk_long(const float* src, int n, int K, uint32_t* ca
   return true;
 }
 
+// Block-wide min and max of one key per thread (sh: 2 * kTopkThreads/64 ints).
+DSA_DEV void block_minmax(uint32_t vmin, uint32_t vmax, int* sh, uint32_t& omin, uint32_t& omax) {
+  constexpr int NW = kTopkThreads / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    vmin = min(vmin, (uint32_t)__shfl_xor((int)vmin, o, 64));
+    vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, o, 64));
+  }
+  if (lane == 0) {
+    sh[wave] = (int)vmin;
+    sh[NW + wave] = (int)vmax;
+  }
+  __syncthreads();
+  omin = 0xFFFFFFFFu;
+  omax = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    omin = min(omin, (uint32_t)sh[w]);
+    omax = max(omax, (uint32_t)sh[NW + w]);
+  }
+  __syncthreads();
+}
+
+// Exclusive scan of one int per thread over the workgroup; *total = the sum (sh: kTopkThreads/64 ints).
+DSA_DEV int block_excl_scan(int v, int* sh, int* total) {
+  constexpr int NW = kTopkThreads / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) sh[wave] = incl;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    before += w < wave ? sh[w] : 0;
+    tot += sh[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return before + incl - v;
+}
+
+// True when key u lies under `prefix` in the bits at and above hi_shift (all keys when hi_shift = 32).
+DSA_DEV bool under_prefix(uint32_t u, uint32_t prefix, int hi_shift) {
+  return hi_shift >= 32 || (u >> hi_shift) == (prefix >> hi_shift);
+}
+
+// One histogram window of a radix select over the m keys in LDS that lie under `prefix` above
+// hi_shift: bins (u >> shift) & (nb - 1), nb = 2^(hi_shift - shift) <= 2048 (hist: 2048 ints).
+// Returns the bin holding the need-th largest of those keys (need >= 1 of them exist), with
+// *above = their keys in higher bins and *in_bin = the bin's keys.  sel: 3 ints.
+DSA_DEV int window_pass(const uint32_t* keys, int m, uint32_t prefix, int hi_shift, int shift, int need, int* hist,
+                        int* sh, int* sel, int* above, int* in_bin) {
+  constexpr int T = kTopkThreads;
+  const int nb = 1 << (hi_shift - shift);
+  for (int b = threadIdx.x; b < nb; b += T) hist[b] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < m; i += T) {
+    const uint32_t u = keys[i];
+    if (under_prefix(u, prefix, hi_shift)) atomicAdd(&hist[(u >> shift) & (uint32_t)(nb - 1)], 1);
+  }
+  __syncthreads();
+  // bins in descending order, 4 per thread: thread t holds bins nb-1-4t .. nb-4-4t
+  const int b_hi = nb - 1 - 4 * (int)threadIdx.x;
+  int c[4], tot = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    c[q] = b_hi - q >= 0 ? hist[b_hi - q] : 0;
+    tot += c[q];
+  }
+  int all;
+  const int excl = block_excl_scan(tot, sh, &all);
+  if (excl < need && need <= excl + tot) {
+    int ab = excl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (ab + c[q] >= need) {
+        sel[0] = b_hi - q;
+        sel[1] = ab;
+        sel[2] = c[q];
+        break;
+      }
+      ab += c[q];
+    }
+  }
+  __syncthreads();
+  const int bin = sel[0];
+  *above = sel[1];
+  *in_bin = sel[2];
+  __syncthreads();
+  return bin;
+}
+
+// Exact need-th largest of the m keys in LDS (lo <= every key <= hi, need <= m): thr, and how
+// many of the keys equal to it fall within the need largest.  Histogram windows of up to 11
+// bits below the common prefix of lo and hi; once the chosen bin holds at most 64 keys, one
+// wave ranks them directly.
+DSA_DEV void select_exact(const uint32_t* keys, int m, int need, uint32_t lo, uint32_t hi, int* hist, int* sh,
+                          int* sel, uint32_t& thr, int& need_out) {
+  constexpr int T = kTopkThreads;
+  int pb = lo == hi ? 32 : __clz(lo ^ hi);              // bits shared by every key
+  uint32_t prefix = pb >= 32 ? lo : (pb == 0 ? 0u : lo & ~(0xFFFFFFFFu >> pb));
+  while (pb < 32) {
+    const int hi_shift = 32 - pb, shift = max(0, hi_shift - 11);
+    int above, in_bin;
+    const int bin = window_pass(keys, m, prefix, hi_shift, shift, need, hist, sh, sel, &above, &in_bin);
+    prefix |= (uint32_t)bin << shift;
+    need -= above;
+    pb = 32 - shift;
+    if (pb < 32 && in_bin <= 64) {
+      // the bin's keys into hist[0..63], then one wave ranks them
+      if (threadIdx.x == 0) sel[0] = 0;
+      __syncthreads();
+      for (int i = threadIdx.x; i < m; i += T) {
+        const uint32_t u = keys[i];
+        if (under_prefix(u, prefix, 32 - pb)) hist[atomicAdd(&sel[0], 1)] = (int)u;
+      }
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const bool ok = l < in_bin;
+        const uint32_t v = ok ? (uint32_t)hist[l] : 0u;
+        int gt = 0, ge = 0;
+#pragma unroll 8
+        for (int j = 0; j < 64; ++j) {
+          const uint32_t w = (uint32_t)__builtin_amdgcn_readlane((int)v, j);
+          if (j < in_bin) {
+            gt += w > v ? 1 : 0;
+            ge += w >= v ? 1 : 0;
+          }
+        }
+        if (ok && gt < need && need <= ge) {   // every such lane holds the same key
+          sel[1] = (int)v;
+          sel[2] = need - gt;
+        }
+      }
+      __syncthreads();
+      thr = (uint32_t)sel[1];
+      need_out = sel[2];
+      __syncthreads();
+      return;
+    }
+  }
+  thr = prefix;
+  need_out = need;
+}
+
+// Sampled-threshold selection for long rows of fp32 scores in global memory (4096 .. 65536
+// entries): one streaming pass over the row instead of the cached path's LDS passes or the long
+// path's three global ones.
+//   1  order keys of kSampleM entries (64 evenly spaced runs of 32: one 128-byte line each) and
+//      one histogram window below their common prefix give a bound that about
+//      r = ceil(1.5 K M / n) + 8 of the sample reach (the lower edge of the bin holding the
+//      sample's r-th largest), i.e. about 1.5 K of the row's entries;
+//   2  one pass over the row: every entry at or above the bound goes to an LDS candidate list with
+//      its position (wave-aggregated slots: counts bit-sliced over ballots, one LDS atomic per
+//      wave and step);
+//   3  if the list holds between K and `cap` entries, it contains the whole top-K: the exact K-th
+//      largest key thr is selected over the candidates alone (select_exact), the selected
+//      positions (keys above thr, then the lowest-positioned `need` of the keys equal to it) are
+//      marked in an LDS bitmap, and each is emitted at its rank in position order (a scan of the
+//      bitmap's popcounts).
+// The result is the exact selection, the same as the other paths' bit for bit.  Returns false
+// having emitted nothing (the caller then runs another path) for rows out of that range, K large
+// against n, LDS too small, a misaligned row, or a bound that missed (fewer than K or more than
+// cap entries reach it).  LDS: sampled_topk_elems(n, K) 4-byte words of the cache.
+constexpr int kSampleM = 2048;
+constexpr int kSampledMaxN = 65536;   // 16-bit candidate positions
+
+DSA_HOST_DEV int sampled_topk_cap(int n, int K) { return max(kSampleM, 2 * K + 32 * ((n + kSampleM - 1) / kSampleM)); }
+DSA_HOST_DEV int sampled_topk_elems(int n, int K) {
+  return sampled_topk_cap(n, K) + (sampled_topk_cap(n, K) + 1) / 2 + 3 * ((n + 31) / 32);
+}
+DSA_HOST_DEV bool sampled_topk_eligible(int n, int K) {
+  return n >= 2 * kSampleM && n <= kSampledMaxN &&
+         (int)((3LL * K * kSampleM + 2LL * n - 1) / (2LL * n)) + 8 <= kSampleM / 2;
+}
+
+template <class Emit>
+DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t* cache, int cache_cap, int* hist,
+                                       int* sh, uint32_t* sel_prefix, int* sel_need, Emit&& emit) {
+  constexpr int T = kTopkThreads, M = kSampleM;
+  static_assert(M == 4 * T, "one 16-byte sample load per thread");
+  if (!sampled_topk_eligible(n, K)) return false;
+  const int r = (int)((3LL * K * M + 2LL * n - 1) / (2LL * n)) + 8;
+  const int cap = sampled_topk_cap(n, K);
+  const int W = (n + 31) / 32;
+  if (sampled_topk_elems(n, K) > cache_cap || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return false;
+  uint32_t* ckey = cache;                                          // [cap] keys (first the sample's)
+  uint16_t* cpos = reinterpret_cast<uint16_t*>(cache + cap);       // [cap] positions
+  uint32_t* take = cache + cap + (cap + 1) / 2;                    // [W] selected positions
+  uint32_t* eqb = take + W;                                        // [W] candidates equal to thr
+  int* wpre = reinterpret_cast<int*>(eqb + W);                     // [W] selected before each word
+  int* sel = reinterpret_cast<int*>(sel_prefix);   // the launch's 4-int selection slots (sel_need is [1])
+  (void)sel_need;
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt = (1ull << lane) - 1;
+  const uint4* b4 = reinterpret_cast<const uint4*>(src);
+  const uint32_t* bits = reinterpret_cast<const uint32_t*>(src);
+  const int n4 = n >> 2;
+
+  // ---- 1: sample keys, min / max, one window -> bound (workgroup-uniform)
+  uint32_t bound;
+  {
+    const int run = threadIdx.x >> 3, part = threadIdx.x & 7;
+    const int start = (int)(((int64_t)run * (n - 32) / 63) & ~3LL);   // + 31 < n
+    const uint4 sv = b4[(start >> 2) + part];
+    const uint32_t s4[4] = {order_key(__builtin_bit_cast(float, sv.x)), order_key(__builtin_bit_cast(float, sv.y)),
+                            order_key(__builtin_bit_cast(float, sv.z)), order_key(__builtin_bit_cast(float, sv.w))};
+    *reinterpret_cast<uint4*>(ckey + 4 * threadIdx.x) = uint4{s4[0], s4[1], s4[2], s4[3]};
+    for (int w = threadIdx.x; w < W; w += T) { take[w] = 0u; eqb[w] = 0u; }
+    uint32_t smin, smax;
+    block_minmax(min(min(s4[0], s4[1]), min(s4[2], s4[3])), max(max(s4[0], s4[1]), max(s4[2], s4[3])), sh, smin,
+                 smax);
+    bound = smin;
+    if (smin != smax) {
+      const int hi_shift = 32 - __clz(smin ^ smax), shift = max(0, hi_shift - 11);
+      int above, in_bin;
+      const int bin = window_pass(ckey, M, smin, hi_shift, shift, r, hist, sh, sel, &above, &in_bin);
+      bound = (hi_shift >= 32 ? 0u : (smin >> hi_shift) << hi_shift) | ((uint32_t)bin << shift);
+    }
+  }
+  if (threadIdx.x == 0) sel[0] = 0;
+  __syncthreads();
+
+  // ---- 2: candidates (keys >= bound) with their positions, 16 entries per thread and step
+  uint32_t cmax = 0u;
+  for (int g0 = 0; g0 < n4; g0 += 4 * T) {
+    uint4 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int g = g0 + k * T + (int)threadIdx.x;
+      x[k] = g < n4 ? b4[g] : uint4{0u, 0u, 0u, 0u};   // past the row: never counted (ok below)
+    }
+    int c = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool ok = g0 + k * T + (int)threadIdx.x < n4;
+      x[k] = uint4{order_key(__builtin_bit_cast(float, x[k].x)), order_key(__builtin_bit_cast(float, x[k].y)),
+                   order_key(__builtin_bit_cast(float, x[k].z)), order_key(__builtin_bit_cast(float, x[k].w))};
+      const uint32_t e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool in = ok && e[q] >= bound;
+        c += in ? 1 : 0;
+        cmax = in ? max(cmax, e[q]) : cmax;
+      }
+    }
+    // lane prefix of c over the wave from 5 bit-slice ballots (c <= 16)
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int bt = 0; bt < 5; ++bt) {
+      const uint64_t bm = __ballot((c >> bt) & 1);
+      pre += __popcll(bm & lt) << bt;
+      tot += __popcll(bm) << bt;
+    }
+    if (tot == 0) continue;   // wave-uniform
+    int slot0 = 0;
+    if (lane == 0) slot0 = atomicAdd(&sel[0], tot);
+    int slot = __builtin_amdgcn_readfirstlane(slot0) + pre;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int g = g0 + k * T + (int)threadIdx.x;
+      const uint32_t e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (g < n4 && e[q] >= bound) {
+          if (slot < cap) {
+            ckey[slot] = e[q];
+            cpos[slot] = (uint16_t)(4 * g + q);
+          }
+          ++slot;
+        }
+      }
+    }
+  }
+  for (int j = 4 * n4 + (int)threadIdx.x; j < n; j += T) {   // ragged tail (< 4 entries)
+    const uint32_t u = order_key(__builtin_bit_cast(float, bits[j]));
+    if (u >= bound) {
+      cmax = max(cmax, u);
+      const int s = atomicAdd(&sel[0], 1);
+      if (s < cap) { ckey[s] = u; cpos[s] = (uint16_t)j; }
+    }
+  }
+  __syncthreads();
+  const int nc = sel[0];
+  uint32_t kmin_unused, kmax;
+  block_minmax(0xFFFFFFFFu, cmax, sh, kmin_unused, kmax);   // (also every thread has read nc)
+  if (nc < K || nc > cap) return false;
+
+  // ---- 3: exact threshold over the candidates, position bitmap, ranks, emission
+  uint32_t thr;
+  int need;
+  select_exact(ckey, nc, K, bound, kmax, hist, sh, sel, thr, need);
+  int my_eq = 0;
+  for (int i = threadIdx.x; i < nc; i += T) {
+    const uint32_t u = ckey[i], pos = cpos[i];
+    if (u > thr) atomicOr(&take[pos >> 5], 1u << (pos & 31));
+    else if (u == thr) {
+      atomicOr(&eqb[pos >> 5], 1u << (pos & 31));
+      ++my_eq;
+    }
+  }
+  int n_eq;
+  block_excl_scan(my_eq, sh, &n_eq);   // (also the barrier after the marks)
+  const int per = (W + T - 1) / T;
+  const int w0 = min(W, (int)threadIdx.x * per), w1 = min(W, w0 + per);
+  if (n_eq == need) {
+    for (int w = w0; w < w1; ++w) take[w] |= eqb[w];
+  } else {   // keep the `need` lowest-positioned keys equal to thr
+    int s = 0;
+    for (int w = w0; w < w1; ++w) s += __popc(eqb[w]);
+    int t_;
+    int run = block_excl_scan(s, sh, &t_);
+    for (int w = w0; w < w1; ++w) {
+      wpre[w] = run;
+      run += __popc(eqb[w]);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nc; i += T) {
+      const uint32_t pos = cpos[i];
+      if (ckey[i] == thr) {
+        const int rk = wpre[pos >> 5] + __popc(eqb[pos >> 5] & ((1u << (pos & 31)) - 1u));
+        if (rk < need) atomicOr(&take[pos >> 5], 1u << (pos & 31));
+      }
+    }
+    __syncthreads();
+  }
+  {
+    int s = 0;
+    for (int w = w0; w < w1; ++w) s += __popc(take[w]);
+    int t_;
+    int run = block_excl_scan(s, sh, &t_);
+    for (int w = w0; w < w1; ++w) {
+      wpre[w] = run;
+      run += __popc(take[w]);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nc; i += T) {
+    const uint32_t pos = cpos[i];
+    const uint32_t word = take[pos >> 5], bit = 1u << (pos & 31);
+    if (word & bit) emit(wpre[pos >> 5] + __popc(word & (bit - 1u)), (int)pos, ckey[i]);
+  }
+  return true;
+}
+
 // Exact top-k of one list of n > K entries in one workgroup: the K largest under (key desc,
 // position asc), emitted as emit(rank, position, key) with rank ascending in position. Entries are
 // fp32 scores mapped through order_key, or (kKeys) order keys already.
@@ -867,6 +1232,9 @@ DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, i
   auto conv = [](uint32_t x) -> uint32_t { return kKeys ? x : order_key(__builtin_bit_cast(float, x)); };
   const bool cached = n <= cache_cap;
   if constexpr (!kKeys) {
+    if (block_select_topk_sampled(static_cast<const float*>(src), n, K, cache, cache_cap, hist, sh, sel_prefix,
+                                  sel_need, emit))
+      return;
     if (!cached && block_select_topk_long(static_cast<const float*>(src), n, K, cache, cache_cap, hist, sh,
                                           sel_prefix, sel_need, emit))
       return;
@@ -1038,8 +1406,9 @@ DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, i
   extern __shared__ __attribute__((aligned(16))) uint32_t cache[]; /* p.cache_elems */ \
   __shared__ __attribute__((aligned(16))) int hist[256 * kHistCopies]; \
   __shared__ int sh[2 * (kTopkThreads / 64)];         \
-  __shared__ uint32_t sel_prefix;                     \
-  __shared__ int sel_need
+  __shared__ int tk_sel[4];                           \
+  uint32_t& sel_prefix = reinterpret_cast<uint32_t&>(tk_sel[0]); \
+  int& sel_need = tk_sel[1]
 
 // One row in one workgroup: rows of at most K visible keys take them all, -1 padded.
 DSA_DEV void topk_row(const TopkParams& p, int row, int n, uint32_t* cache, int* hist, int* sh,
@@ -1137,17 +1506,34 @@ size_t topk_workspace_size(int rows, int64_t pitch, int topk) {
   return (size_t)rows * n_slices * topk * (sizeof(uint32_t) + sizeof(int32_t));
 }
 
+// LDS cache entries of a launch whose rows hold up to n_max entries: the sampled path's lists
+// for the longest row it can take, the rows too short for it cached whole, at least the long
+// path's 12-bit histogram and 1024 candidates; otherwise rows up to kCacheElems cached whole.
+int topk_cache_elems(int64_t n_max, int K) {
+  const int full = (int)std::min<int64_t>(kCacheElems, (n_max + 3) / 4 * 4);
+  const int n_hi = (int)std::min<int64_t>(n_max, kSampledMaxN);
+  if (!sampled_topk_eligible(n_hi, K)) return full;
+  int n_min = 2 * kSampleM;   // the shortest row the sampled path takes (eligibility grows with n)
+  const int64_t est = (3LL * K * kSampleM + (kSampleM - 16) - 1) / (kSampleM - 16);
+  if (est > n_min) n_min = (int)std::min<int64_t>(est, n_hi);
+  while (n_min > 2 * kSampleM && sampled_topk_eligible(n_min - 1, K)) --n_min;
+  while (!sampled_topk_eligible(n_min, K)) ++n_min;
+  const int need = std::max({sampled_topk_elems(n_hi, K), (n_min + 3) / 4 * 4, kLongBins + 2 * 1024});
+  return std::min(full, need);
+}
+
 int launch_topk(const TopkParams& p_in, hipStream_t stream) {
   if (p_in.rows == 0) return 0;
   TopkParams p = p_in;
-  auto cache_for = [](int64_t n) { return (int)std::min<int64_t>(kCacheElems, (n + 3) / 4 * 4); };
+  auto cache_for = [&](int64_t n) { return topk_cache_elems(n, p.topk); };
   if (p.cand_key && topk_workspace_size(p.rows, p.pitch, p.topk) > 0) {
     p.slice = topk_slice_len(p.topk);
     p.n_slices = (int)((p.pitch + p.slice - 1) / p.slice);
     // rows up to one slice run whole in the slice kernel: its cache covers min(pitch, slice)
     p.cache_elems = cache_for(std::min<int64_t>(p.pitch, p.slice));
     hipLaunchKernelGGL(topk_slice_kernel, dim3(p.rows, p.n_slices), dim3(kTopkThreads), p.cache_elems * 4, stream, p);
-    p.cache_elems = cache_for((int64_t)p.n_slices * p.topk);
+    // the merge selects over order keys (no sampled path): its candidates cached whole
+    p.cache_elems = (int)std::min<int64_t>(kCacheElems, ((int64_t)p.n_slices * p.topk + 3) / 4 * 4);
     hipLaunchKernelGGL(topk_merge_kernel, dim3(p.rows), dim3(kTopkThreads), p.cache_elems * 4, stream, p);
   } else {
     p.cache_elems = cache_for(p.pitch);

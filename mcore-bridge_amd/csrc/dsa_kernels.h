@@ -77,7 +77,7 @@ struct IndexerParams {
   int total_q, n_heads, head_dim, fp8, max_row_len;
   int64_t pitch;
   int fill_masked;      // also write -inf into columns [row_len, pitch)
-  int chunk;            // keys per wave work item (power of two in [256, 2048]); 0 = launcher picks
+  int chunk;            // keys per wave work item (power of two in [256, 4096]); 0 = launcher picks
 };
 
 struct TopkParams {

@@ -92,6 +92,40 @@ def test_topk_one_workgroup_long_rows_bit_exact(n, k):
         assert torch.equal(got[r], ref), r
 
 
+@pytest.mark.parametrize("case", ["random", "quantised", "sample_spikes", "few_values", "rising"])
+@pytest.mark.parametrize("n,k", [(12000, 2048), (40000, 4096), (32768, 2048)])
+def test_topk_sampled_threshold_rows_bit_exact(case, n, k):
+    """Rows the sampled-threshold selection takes (n >= 4096, k small against n): the bound from
+    2048 evenly spaced entries is exact on random rows; quantised rows put many keys at the
+    threshold (only the lowest-positioned `need` of them are taken); rows whose sampled positions
+    hold the largest values make the bound miss low (fewer than k candidates) and rows of few
+    distinct values make it miss high (more than the list holds): both fall back to the exact
+    paths.  Every row equals the oracle's selection."""
+    print(f"[topk sampled threshold] case={case} n={n} k={k}", flush=True)
+    g = torch.Generator().manual_seed(n + k + len(case))
+    rows = 8
+    sc = torch.randn(rows, n, generator=g)
+    if case == "quantised":
+        sc = torch.round(sc * 200) / 200
+    elif case == "sample_spikes":
+        starts = (torch.arange(64, dtype=torch.int64) * (n - 32) // 63) // 4 * 4   # the sampled runs
+        pos = (starts[:, None] + torch.arange(32)).flatten()
+        sc[:, pos] = 10.0 + torch.rand(rows, pos.numel(), generator=g)
+    elif case == "few_values":
+        sc = torch.round(sc * 2) / 2
+    elif case == "rising":
+        sc = sc * 0.1 + torch.linspace(0, 4, n)[None]
+    ln = torch.full((rows,), n, dtype=torch.int32)
+    ln[1::2] = torch.randint(max(k + 1, 4096), n + 1, (rows // 2,), generator=g).to(torch.int32)
+    base = torch.randint(0, 1000, (rows,), generator=g).to(torch.int32)
+    got = ops.topk(sc.to(DEV), base.to(DEV), ln.to(DEV), k).cpu().long()
+    for r in range(rows):
+        row = sc[r].double().clone()
+        row[int(ln[r]):] = float("-inf")
+        ref = O.topk_indices(row[None], k)[0] + int(base[r])
+        assert torch.equal(got[r], ref), r
+
+
 def test_topk_split_equals_one_workgroup_cfg5_full_size():
     """cfg5's 64 cache lengths (up to 65,265 keys): the split selection (slices + merge, through
     the workspace) returns the one-workgroup-per-row selection's indices bit for bit, on scores
