@@ -169,18 +169,22 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     // all before the last copy).  Block blk needs copies(blk) done; issued after them are
     // block blk-1's copies(blk+1) and, from blk = 2 on (block 0 stores nothing), its stores of
     // block blk-2.
-    if (blk + 1 >= nblk) wait_vmcnt<0>();
-    else if (blk <= 1 || !wave_stores) wait_vmcnt<G>();
-    else wait_vmcnt<G + S>();
+    if (blk == 0) {
+      if (nblk > 1) wait_vmcnt<G>(); else wait_vmcnt<0>();
+    } else if (blk == 1 || !wave_stores) {
+      wait_vmcnt<G>();
+    } else {
+      wait_vmcnt<G + S>();
+    }
     __syncthreads();
     const bool store_prev = blk > 0 && head_ok;   // wave_stores => the wave issues all S stores
     const int64_t store_j = (blk - 1) * stage_blk;
-    // block blk+2's gather: one copy per kCopyEvery S/dP steps below
-    const bool gather_next = blk + 2 < nblk;
-    TileSrc<NW> next_src;
-    if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+    // block blk+2's gather, one copy per kCopyEvery S/dP steps below.  Issued every iteration:
+    // the last two re-gather block nblk-1 into the ring slot no block reads any more (so no copy
+    // sits behind a branch); they are retired before the kernel ends.
+    const TileSrc<NW> next_src = tile_sources<NW>(p.kv, sm.idx + min(blk + 2, nblk - 1) * kBK, wave, lane);
     // source row of the next copy, read one copy slot ahead of its issue
-    const char* next_row = gather_next ? gather_row<NW>(next_src, 0) : nullptr;
+    const char* next_row = gather_row<NW>(next_src, 0);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t next_tile = tile0 + st_next;
     const TileDst nd = tile_dst<NW>(next_tile, wsg);
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
         s = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), s);
         if (ks == 0) mfma32x32x16_acc_first(dp, cur, df[0]);
         else if (ks < kDv / 16) mfma32x32x16_acc(dp, cur, df[ks]);
-        if (ks % kCopyEvery == 0 && gather_next) {
+        if (ks % kCopyEvery == 0) {
           gather_issue_dst<NW>(nd, next_src, next_row, lane, ks / kCopyEvery);
           next_row = gather_row<NW>(next_src, ks / kCopyEvery + 1);
         }
@@ -256,6 +260,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
       *reinterpret_cast<u32x4*>(ds_row + j + 16 * pr) = dw[pr];
     }
   }
+  wait_vmcnt0();   // the last re-gathers have landed in LDS before the workgroup ends
 }
 
 // ------------------------------------------------------------------------------------------
@@ -507,12 +512,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
       }
       __syncthreads();
       // block blk+2's copies (copy-issuing waves): tile copy k at half head step k, the dS
-      // copies at half steps 10 and 12; each copy's source row is read one half step ahead
-      const bool copy_next = CP && blk + 2 < nblk;
+      // copies at half steps 10 and 12; each copy's source row is read two copy slots ahead
+      // (the readlanes' SGPRs need 5 wait states before the copy reads them).
+      // Issued every iteration: the last two re-copy block nblk-1 into the ring slot no block
+      // reads any more (so no copy sits behind a branch); retired before the epilogue.
+      const int src_blk = min(blk + 2, nblk - 1);
       const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
       TileSrc<NWC> next_src;
-      if (copy_next) next_src = tile_sources<NWC>(p.kv, sm.idx + (blk + 2) * kBK, wu, lane);
-      const char* next_row = copy_next ? gather_row<NWC>(next_src, 0) : nullptr;
+      if (CP) next_src = tile_sources<NWC>(p.kv, sm.idx + src_blk * kBK, wu, lane);
+      const char* next_row[2] = {CP ? gather_row<NWC>(next_src, 0) : nullptr, CP ? gather_row<NWC>(next_src, 1) : nullptr};
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t next_tile = tile0 + st_next * kTileBytes;
       char* const next_ds = sm.ring.ds[st_next];
@@ -529,12 +537,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
         return u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
       auto copy_slot = [&](int h) {
-        if (!CP || !copy_next) return;
+        if (!CP) return;
         if (h < TC) {
-          gather_issue<NWC>(next_tile, next_src, next_row, wu, lane, h);
-          next_row = gather_row<NWC>(next_src, h + 1);
+          gather_issue<NWC>(next_tile, next_src, next_row[h & 1], wu, lane, h);
+          next_row[h & 1] = gather_row<NWC>(next_src, h + 2);
         }
-        if (h == 10 || h == 12) copy_ds_part(next_ds, blk + 2, (h - 10) >> 1);
+        if (h == 10 || h == 12) copy_ds_part(next_ds, src_blk, (h - 10) >> 1);
       };
       // the wave's K^T fragments stay in registers; dS^T fragments stream in two head tiles ahead
       u32x4 a[ND];
@@ -561,6 +569,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
   };
   if (copier) block_loop(std::integral_constant<int, DTMAX>{}, std::true_type{});
   else block_loop(std::integral_constant<int, DTMAX - 1>{}, std::false_type{});
+  wait_vmcnt0();   // the last re-copies have landed before the epilogue reuses the ring
   mfma_acc_drain();
   // ---- epilogue: dQ rows through LDS (64 heads at a time), then coalesced 16-byte stores.
   bf16_t* dq_t = p.dq + (int64_t)t * p.dq_stride_t;
