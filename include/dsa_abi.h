@@ -231,17 +231,19 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* Backward of dsa_sparse_mla_fwd_sink (autograd of the same reference V4 core attention,
- * deepseek_v4.py:443): dq and dkv as dsa_sparse_mla_bwd given the sink forward's out and lse
- * (its P and Delta are then the sink softmax's), plus dsinks [n_heads] fp32 = -sum_t
- * exp(sinks[h] - lse[t,h]) * rowsum(dout[t,h] * out[t,h]), a fixed-order sum (the same bit for
- * bit from run to run).  The workspace holds the rowsums [total_q, n_heads] fp32 at its end and
- * the backward's own workspace before them: at least dsa_sparse_mla_bwd_sink_workspace_size()
- * bytes for one pass (a smaller one runs the passes of dsa_sparse_mla_bwd). */
-size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk);
+ * deepseek_v4.py:443): dq and dkv as dsa_sparse_mla_bwd_ex (flags: 0 or DSA_BWD_G_INT8, below)
+ * given the sink forward's out and lse (its P and Delta are then the sink softmax's), plus
+ * dsinks [n_heads] fp32 = -sum_t exp(sinks[h] - lse[t,h]) * rowsum(dout[t,h] * out[t,h]), a
+ * fixed-order sum (the same bit for bit from run to run).  The workspace holds the rowsums
+ * [total_q, n_heads] fp32 at its end and the backward's own workspace before them: at least
+ * dsa_sparse_mla_bwd_sink_workspace_size() bytes for one pass (a smaller one runs the passes of
+ * dsa_sparse_mla_bwd).  Unknown flags: DSA_ERR_INVALID_ARG (0 bytes from the size query). */
+size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk, int flags);
 int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, const void* out,
                             const void* dout, const float* lse, const float* sinks, int total_q, int n_kv,
                             int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal, void* dq,
-                            float* dkv, float* dsinks, void* workspace, size_t workspace_bytes, void* stream);
+                            float* dkv, float* dsinks, int flags, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* Flags of dsa_sparse_mla_bwd_ex.
  * DSA_BWD_G_INT8: stage the per-(query, key) dKV partial rows as int8 with a bf16 scale per 32

@@ -537,16 +537,16 @@ int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, con
                     flags, workspace, workspace_bytes, stage_events, nullptr, stream);
 }
 
-size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk) {
-  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1) return 0;
-  return bwd_layout(total_q, n_kv, n_heads, topk).total + align_up(sizeof(float) * (size_t)total_q * n_heads);
+size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk, int flags) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || (flags & ~DSA_BWD_G_INT8)) return 0;
+  return bwd_layout(total_q, n_kv, n_heads, topk, flags).total + align_up(sizeof(float) * (size_t)total_q * n_heads);
 }
 
 int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, const void* out, const void* dout,
                             const float* lse, const float* sinks, int total_q, int n_kv, int n_heads, int d_qk,
                             int d_v, int topk, float sm_scale, int causal, void* dq, float* dkv, float* dsinks,
-                            void* workspace, size_t workspace_bytes, void* stream) {
-  if (total_q < 0 || n_heads < 1) return DSA_ERR_INVALID_ARG;
+                            int flags, void* workspace, size_t workspace_bytes, void* stream) {
+  if (total_q < 0 || n_heads < 1 || (flags & ~DSA_BWD_G_INT8)) return DSA_ERR_INVALID_ARG;
   if (!sinks || !dsinks) return DSA_ERR_INVALID_ARG;
   // Delta [total_q, n_heads] sits at the end of the workspace; the passes take the rest
   const size_t dbytes = align_up(sizeof(float) * (size_t)total_q * n_heads);
@@ -555,13 +555,13 @@ int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, c
   float* delta = reinterpret_cast<float*>(static_cast<char*>(workspace) + rest);
   if (total_q == 0) {
     const int rc = sparse_bwd(q, kv, idx, out, dout, lse, 0, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, dq,
-                              dkv, 0, workspace, rest, nullptr, nullptr, stream);
+                              dkv, flags, workspace, rest, nullptr, nullptr, stream);
     if (rc != DSA_OK) return rc;
     return dsa::launch_sink_grad(sinks, lse, delta, 0, n_heads, dsinks, as_stream(stream)) == 0 ? DSA_OK
                                                                                                 : DSA_ERR_LAUNCH;
   }
   const int rc = sparse_bwd(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal,
-                            dq, dkv, 0, workspace, rest, nullptr, delta, stream);
+                            dq, dkv, flags, workspace, rest, nullptr, delta, stream);
   if (rc != DSA_OK) return rc;
   return dsa::launch_sink_grad(sinks, lse, delta, total_q, n_heads, dsinks, as_stream(stream)) == 0
              ? DSA_OK

@@ -51,10 +51,10 @@ SIGNATURES = {
                                    c_float, c_int, c_void_p, c_void_p, c_void_p]),
     "dsa_sparse_mla_fwd_sink": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                         c_float, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
-    "dsa_sparse_mla_bwd_sink_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "dsa_sparse_mla_bwd_sink_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsa_sparse_mla_bwd_sink": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                         c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_void_p, c_void_p,
-                                        c_void_p, c_void_p, c_size_t, c_void_p]),
+                                        c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
     "dsa_build_decode_rows": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "dsa_sparse_mla_decode_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "dsa_sparse_mla_decode_workspace_size_for": (c_size_t, [c_int, c_int, c_int, c_int]),

@@ -367,7 +367,7 @@ def sparse_mla_bwd_sink(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: T
                         sm_scale: float, causal: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
     """Gradients of ``sparse_mla_fwd_sink`` from its ``out`` and ``lse``: ``(dq [T,H,576] bf16,
     dkv [N,576] fp32, dsinks [H] fp32)``.  One pass, or the capped passes of
-    ``set_backward_workspace_limit``."""
+    ``set_backward_workspace_limit``; dKV partial rows staged as ``set_backward_staging`` says."""
     _check_attn(q, kv, idx)
     _require_gpu(out, dout, lse, sinks)
     q, kv, out, lse = q.contiguous(), kv.contiguous(), out.contiguous(), lse.contiguous()
@@ -380,15 +380,17 @@ def sparse_mla_bwd_sink(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: T
     dkv = torch.empty(N, D_QK, dtype=torch.float32, device=q.device)
     dsk = torch.empty(H, dtype=torch.float32, device=q.device)
     lib = _lib.load()
-    ws_bytes = int(lib.dsa_sparse_mla_bwd_sink_workspace_size(T, N, H, K))
+    g_int8 = _BWD_G_INT8[0]
+    flags = DSA_BWD_G_INT8 if g_int8 else 0
+    ws_bytes = int(lib.dsa_sparse_mla_bwd_sink_workspace_size(T, N, H, K, flags))
     limit = _BWD_WORKSPACE_LIMIT[0]
     if 0 < limit < ws_bytes:
         dbytes = (T * H * 4 + 255) // 256 * 256
-        ws_bytes = max(int(limit), bwd_workspace_bytes_chunked(T, N, H, K, 256) + dbytes)
+        ws_bytes = max(int(limit), bwd_workspace_bytes_chunked(T, N, H, K, 256, g_int8) + dbytes)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         _lib.call("dsa_sparse_mla_bwd_sink", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), _p(sk), T, N, H,
-                  D_QK, D_V, K, float(sm_scale), int(causal), _p(dq), _p(dkv), _p(dsk), _p(ws), ws.numel(),
+                  D_QK, D_V, K, float(sm_scale), int(causal), _p(dq), _p(dkv), _p(dsk), flags, _p(ws), ws.numel(),
                   _stream(q.device))
     return dq, dkv, dsk
 
