@@ -418,9 +418,10 @@ def v4_leg(torch, dev, reps: int = 5):
     of the rate-4 compressed entries (index row width 640), per-head attention sink; forward +
     backward of v4.sink_attention.  Algorithmic work with the 512-wide keys: forward 2 (512 + 512)
     H per attended (query, key) pair, backward 2 (3 x 512 + 2 x 512) H.  The kernels run the 576-wide
-    row layout (rope region zero), so `kernels_ms` (the same fwd + bwd on pre-padded inputs) is what
-    the kernels take and `host_composition_ms` the rest: the 512 -> 576 pad copies, the sink fold,
-    the d sink reduction and the gradient slices."""
+    row layout (rope region zero) and fold the sink in (the forward's epilogue, Delta from B1, one
+    d sink kernel), so `kernels_ms` (the same fwd + bwd on pre-padded inputs, without the sink) is
+    what the attention kernels take and `host_composition_ms` the rest: the 512 -> 576 pad copies,
+    the gradient slices, the sink's epilogue terms and d sink kernel (~0.08 ms), autograd."""
     from mcore_bridge_amd import ops, v4
     T, H, D, Wn, rate, Kc, Hi, Di = 16384, 128, 512, 128, 4, 512, 64, 128
     cu = [0, T]
