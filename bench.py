@@ -417,11 +417,11 @@ def v4_leg(torch, dev, reps: int = 5):
     over ONE shared 512-wide K = V head, a 128-token sliding window plus the CSA indexer's top-512
     of the rate-4 compressed entries (index row width 640), per-head attention sink; forward +
     backward of v4.sink_attention.  Algorithmic work with the 512-wide keys: forward 2 (512 + 512)
-    H per attended (query, key) pair, backward 2 (3 x 512 + 2 x 512) H.  The kernels run the 576-wide
-    row layout (rope region zero) and fold the sink in (the forward's epilogue, Delta from B1, one
-    d sink kernel), so `kernels_ms` (the same fwd + bwd on pre-padded inputs, without the sink) is
-    what the attention kernels take and `host_composition_ms` the rest: the 512 -> 576 pad copies,
-    the gradient slices, the sink's epilogue terms and d sink kernel (~0.08 ms), autograd."""
+    H per attended (query, key) pair, backward 2 (3 x 512 + 2 x 512) H.  The kernels read the
+    512-wide q rows as they are, take the K = V rows in the 576-wide row layout (rope region zero)
+    and fold the sink in (the forward's epilogue, Delta from B1, one d sink kernel), so
+    `kernels_ms` (the sink entry points on pre-padded key rows) is what the kernels take and
+    `host_composition_ms` the rest: the key rows' pad copy, the dkv slice, autograd."""
     from mcore_bridge_amd import ops, v4
     T, H, D, Wn, rate, Kc, Hi, Di = 16384, 128, 512, 128, 4, 512, 64, 128
     cu = [0, T]
@@ -445,12 +445,11 @@ def v4_leg(torch, dev, reps: int = 5):
         out, _ = v4.sink_attention(qd, kd, sd, idx, scale)
         out.backward(dout)
 
-    qp = torch.nn.functional.pad(q, (0, ops.D_QK - D)).contiguous()
     kp = torch.nn.functional.pad(keys, (0, ops.D_QK - D)).contiguous()
 
     def kernels_only():
-        out, lse = ops.sparse_mla_fwd(qp, kp, idx, scale, False)
-        ops.sparse_mla_bwd(qp, kp, idx, out, dout, lse, scale, False)
+        out, lse = ops.sparse_mla_fwd_sink(q, kp, idx, sinks, scale, False)
+        ops.sparse_mla_bwd_sink(q, kp, idx, out, dout, lse, sinks, scale, False)
 
     t_all = _time_ms(torch, layer_core, reps)
     t_k = _time_ms(torch, kernels_only, reps)

@@ -162,7 +162,9 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
  * ln(sum_k exp(a_k) + exp(sinks[h])) (a row without a valid index: out = 0, lse = sinks[h]).
  * Replaces the core attention of the reference's DeepSeek-V4 layers with its
  * core_attention.attn_sink (src/mcore_bridge/model/gpts/deepseek_v4.py:443; the layer
- * :61-328, whose core attention is megatron-core's).  sinks == NULL is dsa_sparse_mla_fwd. */
+ * :61-328, whose core attention is megatron-core's).  sinks == NULL is dsa_sparse_mla_fwd.
+ * d_qk 576, or 512 for V4's 512-wide heads: q [total_q, n_heads, 512] without a rope part (it
+ * counts as zero), kv rows still 576 wide with columns 512..575 zero. */
 int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv,
                             int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
                             const float* sinks, void* out, float* lse, void* stream);
@@ -237,7 +239,9 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* idx, const 
  * fixed-order sum (the same bit for bit from run to run).  The workspace holds the rowsums
  * [total_q, n_heads] fp32 at its end and the backward's own workspace before them: at least
  * dsa_sparse_mla_bwd_sink_workspace_size() bytes for one pass (a smaller one runs the passes of
- * dsa_sparse_mla_bwd).  Unknown flags: DSA_ERR_INVALID_ARG (0 bytes from the size query). */
+ * dsa_sparse_mla_bwd).  Unknown flags: DSA_ERR_INVALID_ARG (0 bytes from the size query).
+ * d_qk 576, or 512 as for dsa_sparse_mla_fwd_sink: q and dq [total_q, n_heads, 512], kv and dkv
+ * rows 576 wide (dkv columns 512..575 then come out zero). */
 size_t dsa_sparse_mla_bwd_sink_workspace_size(int total_q, int n_kv, int n_heads, int topk, int flags);
 int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, const void* out,
                             const void* dout, const float* lse, const float* sinks, int total_q, int n_kv,

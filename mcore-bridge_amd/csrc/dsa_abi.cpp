@@ -310,6 +310,7 @@ int dsa_topk(const float* scores, int64_t pitch, const int32_t* row_base, const 
 int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv, int n_heads,
                        int d_qk, int d_v, int topk, float sm_scale, int causal, void* out, float* lse,
                        void* stream) {
+  if (d_qk != kDqk) return DSA_ERR_UNSUPPORTED;
   return dsa_sparse_mla_fwd_sink(q, kv, idx, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, nullptr,
                                  out, lse, stream);
 }
@@ -319,11 +320,12 @@ int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* idx, i
                             float* lse, void* stream) {
   if (total_q < 0 || n_kv < 0 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
     return DSA_ERR_INVALID_ARG;
-  if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
+  if ((d_qk != kDqk && d_qk != kDv) || d_v != kDv) return DSA_ERR_UNSUPPORTED;
   if (total_q == 0) return DSA_OK;
   if (!q || !kv || !idx || !out || !lse || n_kv < 1) return DSA_ERR_INVALID_ARG;
   if (!aligned16(q) || !aligned16(kv) || !aligned16(out)) return DSA_ERR_INVALID_ARG;
   dsa::SparseFwdParams p{};
+  p.q_dim = d_qk;   // 512: q rows without the rope part
   p.q = static_cast<const dsa::bf16_t*>(q);
   p.kv = static_cast<const dsa::bf16_t*>(kv);
   p.idx = idx;
@@ -331,7 +333,7 @@ int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* idx, i
   p.lse = lse;
   p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.causal = causal ? 1 : 0;
   p.n_split = 1; p.split_keys = topk;
-  p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
+  p.q_stride_t = (int64_t)n_heads * d_qk; p.kv_stride = kDqk; p.idx_stride = topk;
   p.out_stride_t = (int64_t)n_heads * kDv; p.lse_stride_t = n_heads;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.sinks = sinks;
@@ -463,7 +465,7 @@ int sparse_bwd(const void* q, const void* kv, const int32_t* idx, const void* ou
                float* delta_out, void* stream) {
   if (total_q < 0 || n_kv < 1 || n_heads < 1 || topk < 1 || !std::isfinite(sm_scale)) return DSA_ERR_INVALID_ARG;
   if (flags & ~DSA_BWD_G_INT8) return DSA_ERR_INVALID_ARG;
-  if (d_qk != kDqk || d_v != kDv) return DSA_ERR_UNSUPPORTED;
+  if ((d_qk != kDqk && d_qk != kDv) || d_v != kDv) return DSA_ERR_UNSUPPORTED;   // 512: the sink entry only
   if (n_heads > 128 || n_heads % 16 != 0) return DSA_ERR_UNSUPPORTED;
   if (!dkv || !aligned16(dkv)) return DSA_ERR_INVALID_ARG;
   // no query rows: every key's gradient is an empty sum (the per-query buffers and the
@@ -497,9 +499,10 @@ int sparse_bwd(const void* q, const void* kv, const int32_t* idx, const void* ou
   p.csr_counts = reinterpret_cast<int32_t*>(ws + L.counts);
   p.n_heads = n_heads; p.n_kv = n_kv; p.topk = topk; p.topk_pad = topk_pad(topk);
   p.causal = causal ? 1 : 0;
-  p.q_stride_t = (int64_t)n_heads * kDqk; p.kv_stride = kDqk; p.idx_stride = topk;
+  p.q_dim = d_qk;   // 512: q and dq rows without the rope part
+  p.q_stride_t = (int64_t)n_heads * d_qk; p.kv_stride = kDqk; p.idx_stride = topk;
   p.out_stride_t = (int64_t)n_heads * kDv; p.dout_stride_t = (int64_t)n_heads * kDv;
-  p.lse_stride_t = n_heads; p.dq_stride_t = (int64_t)n_heads * kDqk; p.dkv_stride = kDqk;
+  p.lse_stride_t = n_heads; p.dq_stride_t = (int64_t)n_heads * d_qk; p.dkv_stride = kDqk;
   p.scale = sm_scale;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   if (stage_events)
@@ -533,6 +536,7 @@ int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* idx, con
                           const float* lse, int total_q, int n_kv, int n_heads, int d_qk, int d_v, int topk,
                           float sm_scale, int causal, void* dq, float* dkv, int flags, void* workspace,
                           size_t workspace_bytes, void* const* stage_events, void* stream) {
+  if (d_qk != kDqk) return DSA_ERR_UNSUPPORTED;
   return sparse_bwd(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, dq, dkv,
                     flags, workspace, workspace_bytes, stage_events, nullptr, stream);
 }

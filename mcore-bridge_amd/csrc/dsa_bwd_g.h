@@ -13,6 +13,8 @@
 namespace dsa {
 
 constexpr int kDqk = 576;
+// 16 zero bytes in global memory: the LDS-direct source of the rope chunks of 512-wide q rows
+static __device__ __attribute__((aligned(16))) const uint32_t kZero16[4] = {0u, 0u, 0u, 0u};
 constexpr int kDv = 512;
 constexpr int kBK = kTileKeys;
 constexpr int kStages = 3;
@@ -137,6 +139,8 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   // ---- setup copies: round r = heads 16r..16r+15 into ring[r % 3]; copy j (1 KB of LDS) is
   // Q bytes 1024j of the round for j < 18, dO bytes 1024(j - 18) after; wave w issues copies
   // w, w + 4, ... (9 for waves 0-1, 8 for waves 2-3)
+  const bool q_rope = p.q_dim != kDv;   // 512: q rows without the rope part (copied as zeros)
+  const int qd = q_rope ? kDqk : kDv;
   const char* q_t = reinterpret_cast<const char*>(p.q + (int64_t)t * p.q_stride_t);
   const char* o_t = reinterpret_cast<const char*>(p.dout + (int64_t)t * p.dout_stride_t);
   const uint32_t ring0 = lds_addr(sm.ring[0]);
@@ -149,7 +153,9 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         const char* src;
         if (j < kQRound / 1024) {   // 16-byte chunk c of the round's Q rows (72 per row)
           const int c = j * 64 + lane, row = c / (kDqk / 8), slot = c - row * (kDqk / 8);
-          src = q_t + (int64_t)(16 * r + row) * (kDqk * 2) + 16 * (slot ^ (2 * (row & 3)));
+          const int sc = slot ^ (2 * (row & 3));   // source chunk (rope chunks 64..71 stay in 64..71)
+          src = q_t + (int64_t)(16 * r + row) * (2 * qd) + 16 * sc;
+          if (sc >= kDv / 8 && !q_rope) src = reinterpret_cast<const char*>(kZero16);   // q rows of 512
         } else {                    // chunk c of the round's dO rows (64 per row)
           const int c = (j - kQRound / 1024) * 64 + lane, row = c >> 6, slot = c & 63;
           src = o_t + (int64_t)(16 * r + row) * (kDv * 2) + 16 * (slot ^ (2 * (row & 3)));

@@ -10,7 +10,7 @@ namespace dsa {
 typedef __bf16 bf16_t;
 
 struct SparseFwdParams {
-  const bf16_t* q;      // [total_q, n_heads, 576], token stride q_stride_t
+  const bf16_t* q;      // [total_q, n_heads, q_dim], token stride q_stride_t
   const bf16_t* kv;     // [n_kv, 576], row stride kv_stride
   const int32_t* idx;   // [total_q, topk] global kv row ids, -1 = none
   bf16_t* out;          // [total_q, n_heads, 512], token stride out_stride_t
@@ -23,6 +23,8 @@ struct SparseFwdParams {
   float scale_log2;     // softmax scale * log2(e)
   int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
   const float* sinks;   // [n_heads] per-head attention-sink logits (natural), or null; n_split == 1
+  int q_dim;            // 576, or 512: q rows without the rope part (it counts as zero; the kv
+                        // rows' rope region must then be zero too)
 };
 
 // Per-pair dKV partial rows ("G rows") of the sparse backward, written by B3 and summed per key
@@ -38,7 +40,7 @@ constexpr int kGRowBytesBf16 = 1152;
 constexpr int kGRowBytesI8 = 640;
 
 struct SparseBwdParams {
-  const bf16_t* q;      // [total_q, n_heads, 576]
+  const bf16_t* q;      // [total_q, n_heads, q_dim]; dq alike
   const bf16_t* kv;     // [n_kv, 576]
   const int32_t* idx;   // [total_q, topk]
   const bf16_t* out;    // [total_q, n_heads, 512]
@@ -62,6 +64,7 @@ struct SparseBwdParams {
   int64_t q_stride_t, kv_stride, idx_stride, out_stride_t, dout_stride_t, lse_stride_t, dq_stride_t, dkv_stride;
   float scale, scale_log2;
   int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
+  int q_dim;            // 576, or 512 (q and dq rows without the rope part: it counts as zero)
   float* delta_out;     // [total_q, n_heads] rowsum(dO * O) written by B1 (token stride n_heads), or null
 };
 

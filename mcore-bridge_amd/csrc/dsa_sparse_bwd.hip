@@ -108,11 +108,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   }
   // Q (576) and dO (512) fragments, d-contiguous: lane holds [16*ks + 8*hb, +8).
   u32x4 qf[kDqk / 16], df[kDv / 16];
-  const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)hsafe * kDqk + hb * 8;
+  // (q rows of 512: no rope part, its fragments zero)
+  const bool q_rope = p.q_dim != kDv;
+  const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)hsafe * (q_rope ? kDqk : kDv) + hb * 8;
   const bf16_t* drow = p.dout + (int64_t)t * p.dout_stride_t + (int64_t)hsafe * kDv + hb * 8;
 #pragma unroll
   for (int ks = 0; ks < kDqk / 16; ++ks) {
-    const u32x4 v = gload16(qrow + ks * 16);
+    u32x4 v = u32x4{0, 0, 0, 0};
+    if (ks < kDv / 16 || q_rope) v = gload16(qrow + ks * 16);
     qf[ks] = head_ok ? v : u32x4{0, 0, 0, 0};
   }
 #pragma unroll
@@ -427,9 +430,10 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
     }
     __syncthreads();
     const int rows = min(64, hrows - 64 * half);
-    for (int c = threadIdx.x; c < rows * (kDqk / 8); c += NW * 64) {
-      const int r = c / (kDqk / 8), q = c - r * (kDqk / 8);
-      *reinterpret_cast<u32x4*>(dq_t + (int64_t)(h0 + 64 * half + r) * kDqk + 8 * q) =
+    const int qc = (p.q_dim != kDv ? kDqk : kDv) / 8;   // 16-byte chunks of a dq row (512: no rope part)
+    for (int c = threadIdx.x; c < rows * qc; c += NW * 64) {
+      const int r = c / qc, q = c - r * qc;
+      *reinterpret_cast<u32x4*>(dq_t + (int64_t)(h0 + 64 * half + r) * (8 * qc) + 8 * q) =
           lds_load16(sm.out[r] + 16 * q);
     }
   }
@@ -587,9 +591,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
     }
     __syncthreads();
     const int rows = min(64, hrows - 64 * half);
-    for (int c = threadIdx.x; c < rows * (kDqk / 8); c += NW * 64) {
-      const int r = c / (kDqk / 8), q = c - r * (kDqk / 8);
-      *reinterpret_cast<u32x4*>(dq_t + (int64_t)(64 * half + r) * kDqk + 8 * q) = lds_load16(sm.out[r] + 16 * q);
+    const int qc = (p.q_dim != kDv ? kDqk : kDv) / 8;   // 16-byte chunks of a dq row (512: no rope part)
+    for (int c = threadIdx.x; c < rows * qc; c += NW * 64) {
+      const int r = c / qc, q = c - r * qc;
+      *reinterpret_cast<u32x4*>(dq_t + (int64_t)(64 * half + r) * (8 * qc) + 8 * q) = lds_load16(sm.out[r] + 16 * q);
     }
   }
 }

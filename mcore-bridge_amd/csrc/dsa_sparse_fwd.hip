@@ -95,12 +95,16 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   const bool head_ok = head < p.n_heads;
 
   // ---- Q fragments: lane holds q[t, head, 16*ks + 8*hb .. +7] for ks = 0..35
+  // (q rows of 512: no rope part, its fragments zero)
   u32x4 qf[kDqk / 16];
   {
-    const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)(head_ok ? head : 0) * kDqk + hb * 8;
+    const bool q_rope = p.q_dim != kDv;
+    const int qd = q_rope ? kDqk : kDv;
+    const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)(head_ok ? head : 0) * qd + hb * 8;
 #pragma unroll
     for (int ks = 0; ks < kDqk / 16; ++ks) {
-      u32x4 v = gload16(qrow + ks * 16);
+      u32x4 v = u32x4{0, 0, 0, 0};
+      if (ks < kDv / 16 || q_rope) v = gload16(qrow + ks * 16);
       qf[ks] = head_ok ? v : u32x4{0, 0, 0, 0};
     }
   }

@@ -305,9 +305,12 @@ def decode_indexer_topk(q: Tensor, k_cache: Tensor, w: Tensor, index_topk: int, 
 # --------------------------------------------------------------------------------------
 # K3 / K4 sparse MLA
 # --------------------------------------------------------------------------------------
-def _check_attn(q: Tensor, kv: Tensor, idx: Tensor) -> None:
+def _check_attn(q: Tensor, kv: Tensor, idx: Tensor, q512: bool = False) -> None:
     _require_gpu(q, kv, idx)
-    _require(q.dim() == 3 and q.shape[-1] == D_QK, f"q must be [T, H, {D_QK}]")
+    if q512:   # the sink entries also take 512-wide q rows (no rope part) over 576-wide kv rows
+        _require(q.dim() == 3 and q.shape[-1] in (D_QK, D_V), f"q must be [T, H, {D_QK}] or [T, H, {D_V}]")
+    else:
+        _require(q.dim() == 3 and q.shape[-1] == D_QK, f"q must be [T, H, {D_QK}]")
     _require(kv.dim() == 2 and kv.shape[-1] == D_QK, f"kv must be [N, {D_QK}]")
     _require(idx.dim() == 2 and idx.shape[0] == q.shape[0], "idx must be [T, K]")
     _require(q.dtype == torch.bfloat16 and kv.dtype == torch.bfloat16, "q and kv must be bf16")
@@ -339,8 +342,9 @@ def _(q, kv, idx, sm_scale, causal=False):
 def sparse_mla_fwd_sink(q: Tensor, kv: Tensor, idx: Tensor, sinks: Tensor, sm_scale: float,
                         causal: bool = False) -> Tuple[Tensor, Tensor]:
     """``sparse_mla_fwd`` with a per-head attention sink ``sinks [H]`` (a logit with no value row):
-    ``(out [T,H,512] bf16, lse [T,H] fp32)``, the sink counted in the softmax and in ``lse``."""
-    _check_attn(q, kv, idx)
+    ``(out [T,H,512] bf16, lse [T,H] fp32)``, the sink counted in the softmax and in ``lse``.
+    ``q`` may be ``[T,H,512]`` (no rope part; then ``kv``'s columns 512..575 must be zero)."""
+    _check_attn(q, kv, idx, q512=True)
     _require_gpu(sinks)
     q = q.contiguous()
     kv = kv.contiguous()
@@ -351,8 +355,8 @@ def sparse_mla_fwd_sink(q: Tensor, kv: Tensor, idx: Tensor, sinks: Tensor, sm_sc
     out = torch.empty(T, H, D_V, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
     with torch.cuda.device(q.device):
-        _lib.call("dsa_sparse_mla_fwd_sink", _p(q), _p(kv), _p(idx), T, kv.shape[0], H, D_QK, D_V, idx.shape[1],
-                  float(sm_scale), int(causal), _p(sk), _p(out), _p(lse), _stream(q.device))
+        _lib.call("dsa_sparse_mla_fwd_sink", _p(q), _p(kv), _p(idx), T, kv.shape[0], H, q.shape[-1], D_V,
+                  idx.shape[1], float(sm_scale), int(causal), _p(sk), _p(out), _p(lse), _stream(q.device))
     return out, lse
 
 
@@ -365,10 +369,10 @@ def _(q, kv, idx, sinks, sm_scale, causal=False):
 @torch.library.custom_op("dsa_amd::sparse_mla_bwd_sink", mutates_args=())
 def sparse_mla_bwd_sink(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sinks: Tensor,
                         sm_scale: float, causal: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
-    """Gradients of ``sparse_mla_fwd_sink`` from its ``out`` and ``lse``: ``(dq [T,H,576] bf16,
-    dkv [N,576] fp32, dsinks [H] fp32)``.  One pass, or the capped passes of
+    """Gradients of ``sparse_mla_fwd_sink`` from its ``out`` and ``lse``: ``(dq`` (bf16, the shape of
+    ``q``: ``[T,H,576]`` or ``[T,H,512]``), ``dkv [N,576] fp32, dsinks [H] fp32)``.  One pass, or the capped passes of
     ``set_backward_workspace_limit``; dKV partial rows staged as ``set_backward_staging`` says."""
-    _check_attn(q, kv, idx)
+    _check_attn(q, kv, idx, q512=True)
     _require_gpu(out, dout, lse, sinks)
     q, kv, out, lse = q.contiguous(), kv.contiguous(), out.contiguous(), lse.contiguous()
     dout = dout.to(torch.bfloat16).contiguous()
@@ -390,7 +394,7 @@ def sparse_mla_bwd_sink(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: T
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         _lib.call("dsa_sparse_mla_bwd_sink", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), _p(sk), T, N, H,
-                  D_QK, D_V, K, float(sm_scale), int(causal), _p(dq), _p(dkv), _p(dsk), flags, _p(ws), ws.numel(),
+                  q.shape[-1], D_V, K, float(sm_scale), int(causal), _p(dq), _p(dkv), _p(dsk), flags, _p(ws), ws.numel(),
                   _stream(q.device))
     return dq, dkv, dsk
 

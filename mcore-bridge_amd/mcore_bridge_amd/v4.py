@@ -11,7 +11,8 @@ attention (sliding window, CSA compressor + lightning indexer, HCA compressor, a
 Kernel mapping (no new arithmetic kernel):
 - the attention is the absorbed sparse MQA of ``sparse_mla_fwd`` / ``_bwd`` (K3 / K4) with the
   512-wide K = V rows stored in the kernels' 576-wide row layout, rope region zero: the kernels'
-  ``v = kv[:, :512]`` is then the whole key, and the zero region adds nothing to q . k;
+  ``v = kv[:, :512]`` is then the whole key, and the zero region adds nothing to q . k; the
+  512-wide q rows (and dq) are read and written as they are (``d_qk = 512``: no rope part);
 - every query's key list -- its sliding window over the raw rows, then the compressed entries it
   may see (CSA: the indexer's top-k; HCA: all of them) -- is one index row over the
   concatenation ``[raw rows; compressed entries]``;
@@ -47,10 +48,12 @@ ROPE_DIM = 64
 class _SinkAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q: Tensor, kv: Tensor, sinks: Tensor, idx: Tensor, scale: float):
-        q_p = F.pad(q, (0, ops.D_QK - HEAD_DIM)).contiguous()
+        # the kernels take the 512-wide q rows as they are (no rope part) and K = V rows in the
+        # 576-wide row layout with a zero rope region (a copy of the N key rows only)
+        q = q.contiguous()
         kv_p = F.pad(kv, (0, ops.D_QK - HEAD_DIM)).contiguous()
-        out, lse = ops.sparse_mla_fwd_sink(q_p, kv_p, idx, sinks, scale, False)   # the sink folded in-kernel
-        ctx.save_for_backward(q_p, kv_p, idx, out, lse, sinks)
+        out, lse = ops.sparse_mla_fwd_sink(q, kv_p, idx, sinks, scale, False)   # the sink folded in-kernel
+        ctx.save_for_backward(q, kv_p, idx, out, lse, sinks)
         ctx.scale = scale
         ctx.kv_dtype = kv.dtype
         ctx.mark_non_differentiable(lse)
@@ -58,10 +61,10 @@ class _SinkAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout: Tensor, dlse: Tensor):
-        q_p, kv_p, idx, out, lse, sinks = ctx.saved_tensors
-        dq_p, dkv_p, dsinks = ops.sparse_mla_bwd_sink(q_p, kv_p, idx, out, dout.contiguous(), lse, sinks, ctx.scale,
-                                                      False)
-        dq = dq_p[..., :HEAD_DIM] if ctx.needs_input_grad[0] else None
+        q, kv_p, idx, out, lse, sinks = ctx.saved_tensors
+        dq, dkv_p, dsinks = ops.sparse_mla_bwd_sink(q, kv_p, idx, out, dout.contiguous(), lse, sinks, ctx.scale,
+                                                    False)
+        dq = dq if ctx.needs_input_grad[0] else None
         dkv = dkv_p[:, :HEAD_DIM].to(ctx.kv_dtype) if ctx.needs_input_grad[1] else None
         return dq, dkv, dsinks.to(sinks.dtype) if ctx.needs_input_grad[2] else None, None, None
 

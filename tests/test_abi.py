@@ -41,7 +41,7 @@ P = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
 
 def test_invalid_arguments_rejected_before_launch():
     lib = _lib.load()
-    # d_qk must be 576
+    # d_qk must be 576 (512-wide q rows only through the sink entry points)
     assert lib.dsa_sparse_mla_fwd(P, P, P, 4, 4, 16, 512, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_UNSUPPORTED
     # null pointer
     assert lib.dsa_sparse_mla_fwd(N, P, P, 4, 4, 16, 576, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
@@ -69,7 +69,12 @@ def test_invalid_arguments_rejected_before_launch():
     assert lib.dsa_topk_workspace_size(64, 16384, 2048) == 0     # one slice per row
     assert lib.dsa_topk_workspace_size(0, 65268, 2048) == 0
     assert lib.dsa_topk(P, 65268, P, P, 64, 2048, P, N, P, ws - 1, N) == _lib.DSA_ERR_WORKSPACE
-    # backward: heads not a multiple of 16, workspace too small
+    # backward: 512-wide q only through the sink entry points; heads not a multiple of 16,
+    # workspace too small
+    assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 32, 512, 512, 8, 0.1, 1, P, P, P, 1 << 30, N) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_sparse_mla_bwd_sink(P, P, P, P, P, P, P, 4, 4, 32, 448, 512, 8, 0.1, 1, P, P, P, 0, P, 1 << 30,
+                                       N) == _lib.DSA_ERR_UNSUPPORTED
+    assert lib.dsa_sparse_mla_fwd_sink(P, P, P, 4, 4, 16, 448, 512, 8, 0.1, 1, P, P, P, N) == _lib.DSA_ERR_UNSUPPORTED
     assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 24, 576, 512, 8, 0.1, 1, P, P, P, 1 << 30, N) == _lib.DSA_ERR_UNSUPPORTED
     assert lib.dsa_sparse_mla_bwd(P, P, P, P, P, P, 4, 4, 32, 576, 512, 8, 0.1, 1, P, P, P, 16, N) == _lib.DSA_ERR_WORKSPACE
     # no query rows: dkv is still written (must be given), nothing else is needed; no stages to time
