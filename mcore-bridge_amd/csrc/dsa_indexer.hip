@@ -870,7 +870,8 @@ DSA_DEV bool block_select_topk_long(const float* src, int n, int K, uint32_t* ca
   return true;
 }
 
-// Block-wide min and max of one key per thread (sh: 2 * kTopkThreads/64 ints).
+// Block-wide min and max of one key per thread (sh: 2 * kTopkThreads/64 ints).  One barrier; the
+// caller passes another before sh is written again.
 DSA_DEV void block_minmax(uint32_t vmin, uint32_t vmax, int* sh, uint32_t& omin, uint32_t& omax) {
   constexpr int NW = kTopkThreads / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -891,10 +892,10 @@ DSA_DEV void block_minmax(uint32_t vmin, uint32_t vmax, int* sh, uint32_t& omin,
     omin = min(omin, (uint32_t)sh[w]);
     omax = max(omax, (uint32_t)sh[NW + w]);
   }
-  __syncthreads();
 }
 
-// Exclusive scan of one int per thread over the workgroup; *total = the sum (sh: kTopkThreads/64 ints).
+// Exclusive scan of one int per thread over the workgroup; *total = the sum (sh: kTopkThreads/64
+// ints).  One barrier; the caller passes another before sh is written again.
 DSA_DEV int block_excl_scan(int v, int* sh, int* total) {
   constexpr int NW = kTopkThreads / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -912,7 +913,6 @@ DSA_DEV int block_excl_scan(int v, int* sh, int* total) {
     before += w < wave ? sh[w] : 0;
     tot += sh[w];
   }
-  __syncthreads();
   *total = tot;
   return before + incl - v;
 }
@@ -925,7 +925,9 @@ DSA_DEV bool under_prefix(uint32_t u, uint32_t prefix, int hi_shift) {
 // One histogram window of a radix select over the m keys in LDS that lie under `prefix` above
 // hi_shift: bins (u >> shift) & (nb - 1), nb = 2^(hi_shift - shift) <= 2048 (hist: 2048 ints).
 // Returns the bin holding the need-th largest of those keys (need >= 1 of them exist), with
-// *above = their keys in higher bins and *in_bin = the bin's keys.  sel: 3 ints.
+// *above = their keys in higher bins and *in_bin = the bin's keys.  sel: 3 ints, written by one
+// thread between two barriers and read after the second; the caller passes a barrier before
+// sel[0..2], hist or sh is written again.
 DSA_DEV int window_pass(const uint32_t* keys, int m, uint32_t prefix, int hi_shift, int shift, int need, int* hist,
                         int* sh, int* sel, int* above, int* in_bin) {
   constexpr int T = kTopkThreads;
@@ -961,17 +963,16 @@ DSA_DEV int window_pass(const uint32_t* keys, int m, uint32_t prefix, int hi_shi
     }
   }
   __syncthreads();
-  const int bin = sel[0];
   *above = sel[1];
   *in_bin = sel[2];
-  __syncthreads();
-  return bin;
+  return sel[0];
 }
 
 // Exact need-th largest of the m keys in LDS (lo <= every key <= hi, need <= m): thr, and how
 // many of the keys equal to it fall within the need largest.  Histogram windows of up to 11
 // bits below the common prefix of lo and hi; once the chosen bin holds at most 64 keys, one
-// wave ranks them directly.
+// wave ranks them directly (sel[4] must be zero on entry).  The caller passes a barrier before
+// sel, hist or sh is written again.
 DSA_DEV void select_exact(const uint32_t* keys, int m, int need, uint32_t lo, uint32_t hi, int* hist, int* sh,
                           int* sel, uint32_t& thr, int& need_out) {
   constexpr int T = kTopkThreads;
@@ -985,12 +986,11 @@ DSA_DEV void select_exact(const uint32_t* keys, int m, int need, uint32_t lo, ui
     need -= above;
     pb = 32 - shift;
     if (pb < 32 && in_bin <= 64) {
-      // the bin's keys into hist[0..63], then one wave ranks them
-      if (threadIdx.x == 0) sel[0] = 0;
-      __syncthreads();
+      // the bin's keys into hist[0..63] (slots from sel[4], zero on entry), then one wave ranks
+      // them
       for (int i = threadIdx.x; i < m; i += T) {
         const uint32_t u = keys[i];
-        if (under_prefix(u, prefix, 32 - pb)) hist[atomicAdd(&sel[0], 1)] = (int)u;
+        if (under_prefix(u, prefix, 32 - pb)) hist[atomicAdd(&sel[4], 1)] = (int)u;
       }
       __syncthreads();
       if (threadIdx.x < 64) {
@@ -1014,7 +1014,6 @@ DSA_DEV void select_exact(const uint32_t* keys, int m, int need, uint32_t lo, ui
       __syncthreads();
       thr = (uint32_t)sel[1];
       need_out = sel[2];
-      __syncthreads();
       return;
     }
   }
@@ -1068,7 +1067,9 @@ DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t*
   uint32_t* take = cache + cap + (cap + 1) / 2;                    // [W] selected positions
   uint32_t* eqb = take + W;                                        // [W] candidates equal to thr
   int* wpre = reinterpret_cast<int*>(eqb + W);                     // [W] selected before each word
-  int* sel = reinterpret_cast<int*>(sel_prefix);   // the launch's 4-int selection slots (sel_need is [1])
+  // the launch's 8-int selection slots (sel_need is [1]): [0..2] window results, [3] the
+  // candidate count, [4] the exact select's counter
+  int* sel = reinterpret_cast<int*>(sel_prefix);
   (void)sel_need;
   const int lane = threadIdx.x & 63;
   const uint64_t lt = (1ull << lane) - 1;
@@ -1076,6 +1077,10 @@ DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t*
   const uint32_t* bits = reinterpret_cast<const uint32_t*>(src);
   const int n4 = n >> 2;
 
+  if (threadIdx.x == 0) {   // (ordered before their first use by the barriers below)
+    sel[3] = 0;
+    sel[4] = 0;
+  }
   // ---- 1: sample keys, min / max, one window -> bound (workgroup-uniform)
   uint32_t bound;
   {
@@ -1095,10 +1100,10 @@ DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t*
       int above, in_bin;
       const int bin = window_pass(ckey, M, smin, hi_shift, shift, r, hist, sh, sel, &above, &in_bin);
       bound = (hi_shift >= 32 ? 0u : (smin >> hi_shift) << hi_shift) | ((uint32_t)bin << shift);
+    } else {
+      __syncthreads();   // (block_minmax's reads of sh before the collect writes it)
     }
   }
-  if (threadIdx.x == 0) sel[0] = 0;
-  __syncthreads();
 
   // ---- 2: candidates (keys >= bound) with their positions, 16 entries per thread and step
   uint32_t cmax = 0u;
@@ -1133,7 +1138,7 @@ DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t*
     }
     if (tot == 0) continue;   // wave-uniform
     int slot0 = 0;
-    if (lane == 0) slot0 = atomicAdd(&sel[0], tot);
+    if (lane == 0) slot0 = atomicAdd(&sel[3], tot);
     int slot = __builtin_amdgcn_readfirstlane(slot0) + pre;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -1155,14 +1160,23 @@ DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t*
     const uint32_t u = order_key(__builtin_bit_cast(float, bits[j]));
     if (u >= bound) {
       cmax = max(cmax, u);
-      const int s = atomicAdd(&sel[0], 1);
+      const int s = atomicAdd(&sel[3], 1);
       if (s < cap) { ckey[s] = u; cpos[s] = (uint16_t)j; }
     }
   }
+  // the count and the candidates' maximum after one barrier (a fallback path writes neither sel
+  // nor sh before its own barriers)
+  {
+    constexpr int NW = T / 64;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) cmax = max(cmax, (uint32_t)__shfl_xor((int)cmax, o, 64));
+    if (lane == 0) sh[NW + (threadIdx.x >> 6)] = (int)cmax;
+  }
   __syncthreads();
-  const int nc = sel[0];
-  uint32_t kmin_unused, kmax;
-  block_minmax(0xFFFFFFFFu, cmax, sh, kmin_unused, kmax);   // (also every thread has read nc)
+  const int nc = sel[3];
+  uint32_t kmax = 0u;
+#pragma unroll
+  for (int w = 0; w < T / 64; ++w) kmax = max(kmax, (uint32_t)sh[T / 64 + w]);
   if (nc < K || nc > cap) return false;
 
   // ---- 3: exact threshold over the candidates, position bitmap, ranks, emission
@@ -1178,8 +1192,12 @@ DSA_DEV bool block_select_topk_sampled(const float* src, int n, int K, uint32_t*
       ++my_eq;
     }
   }
-  int n_eq;
-  block_excl_scan(my_eq, sh, &n_eq);   // (also the barrier after the marks)
+  my_eq = wave_sum_i(my_eq);
+  if (lane == 0) sh[T / 64 + (threadIdx.x >> 6)] = my_eq;
+  __syncthreads();   // (also the barrier after the marks)
+  int n_eq = 0;
+#pragma unroll
+  for (int w = 0; w < T / 64; ++w) n_eq += sh[T / 64 + w];
   const int per = (W + T - 1) / T;
   const int w0 = min(W, (int)threadIdx.x * per), w1 = min(W, w0 + per);
   if (n_eq == need) {
@@ -1406,7 +1424,7 @@ DSA_DEV void block_select_topk(const void* src, int n, int K, uint32_t* cache, i
   extern __shared__ __attribute__((aligned(16))) uint32_t cache[]; /* p.cache_elems */ \
   __shared__ __attribute__((aligned(16))) int hist[256 * kHistCopies]; \
   __shared__ int sh[2 * (kTopkThreads / 64)];         \
-  __shared__ int tk_sel[4];                           \
+  __shared__ int tk_sel[8];                           \
   uint32_t& sel_prefix = reinterpret_cast<uint32_t&>(tk_sel[0]); \
   int& sel_need = tk_sel[1]
 
