@@ -293,11 +293,12 @@ class _SparseMLAWithIndexerLoss(torch.autograd.Function):
         q, kv, q_idx, k_idx, w, idx, out, lse = ctx.saved_tensors
         sm_scale, coeff, loss_scale, causal = ctx.args
         T, H = q.shape[0], q.shape[1]
-        if ops.backward_takes_one_pass(T, kv.shape[0], H, idx.shape[1]):
+        if ops.backward_takes_one_pass(T, kv.shape[0], H, idx.shape[1], q.device):
             dq, dkv, target = ops.sparse_mla_bwd_with_target(q, kv, idx, out, dout, lse, sm_scale, causal)
         else:
-            # a workspace cap (or int8 row staging) is set: the capped backward cannot keep the P
-            # tiles of every query, so the target is recomputed from the forward LSE instead
+            # a workspace cap applies (set, or the device lacks the one-pass memory) or int8 rows
+            # are staged: the capped backward cannot keep the P tiles of every query, so the
+            # target is recomputed from the forward LSE instead
             dq, dkv = ops.autograd_backward(q, kv, idx, out, dout, lse, sm_scale, causal)
             target = ops.indexer_kl_target(q, kv, idx, lse, sm_scale, causal)
         sel = ops.indexer_selected_scores(q_idx.detach(), k_idx.detach(), w.detach(), idx, causal)

@@ -387,10 +387,10 @@ def sparse_mla_bwd_sink(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: T
     g_int8 = _BWD_G_INT8[0]
     flags = DSA_BWD_G_INT8 if g_int8 else 0
     ws_bytes = int(lib.dsa_sparse_mla_bwd_sink_workspace_size(T, N, H, K, flags))
-    limit = _BWD_WORKSPACE_LIMIT[0]
-    if 0 < limit < ws_bytes:
+    cap = _workspace_cap(_BWD_WORKSPACE_LIMIT[0], ws_bytes, q.device)
+    if 0 < cap < ws_bytes:
         dbytes = (T * H * 4 + 255) // 256 * 256
-        ws_bytes = max(int(limit), bwd_workspace_bytes_chunked(T, N, H, K, 256, g_int8) + dbytes)
+        ws_bytes = max(cap, bwd_workspace_bytes_chunked(T, N, H, K, 256, g_int8) + dbytes)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         _lib.call("dsa_sparse_mla_bwd_sink", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), _p(sk), T, N, H,
@@ -455,7 +455,9 @@ def sparse_mla_bwd(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor
                    causal: bool = False, max_workspace_bytes: int = 0, g_int8: bool = False) -> Tuple[Tensor, Tensor]:
     """Gradients of ``sparse_mla_fwd``: ``(dq [T,H,576] bf16, dkv [N,576] fp32)``.
     ``max_workspace_bytes`` > 0 caps the scratch memory: the backward then runs in passes of as
-    many query rows as fit (at least 256), adding each pass's dkv into the previous ones.
+    many query rows as fit (at least 256), adding each pass's dkv into the previous ones.  With 0
+    it runs one pass if that workspace fits 90 % of the memory the device can still allocate, and
+    passes under that share otherwise.
     ``g_int8`` stages the per-pair dkv partial rows as int8 with a bf16 scale per 32 dims
     (``DSA_BWD_G_INT8``): less memory traffic and workspace, a larger dkv rounding error."""
     _check_attn(q, kv, idx)
@@ -468,8 +470,9 @@ def sparse_mla_bwd(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor
     dq = torch.empty_like(q)
     dkv = torch.empty(N, D_QK, dtype=torch.float32, device=q.device)
     ws_bytes = bwd_workspace_bytes(T, N, H, K, g_int8)
-    if 0 < max_workspace_bytes < ws_bytes:
-        ws_bytes = max(int(max_workspace_bytes), bwd_workspace_bytes_chunked(T, N, H, K, 256, g_int8))
+    cap = _workspace_cap(int(max_workspace_bytes), ws_bytes, q.device)
+    if 0 < cap < ws_bytes:
+        ws_bytes = max(cap, bwd_workspace_bytes_chunked(T, N, H, K, 256, g_int8))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         _lib.call("dsa_sparse_mla_bwd_ex", _p(q), _p(kv), _p(idx), _p(out), _p(dout), _p(lse), T, N, H, D_QK, D_V,
@@ -528,8 +531,30 @@ _BWD_G_INT8 = [False]
 
 def set_backward_workspace_limit(nbytes: int) -> None:
     """Cap the scratch memory of the autograd backward of ``sparse_mla_fwd`` (0 = one pass over all
-    query rows, the fastest; otherwise passes of as many rows as fit, at least 256)."""
+    query rows, the fastest, whenever its workspace fits the memory the device can still give;
+    otherwise passes of as many rows as fit, at least 256)."""
     _BWD_WORKSPACE_LIMIT[0] = max(0, int(nbytes))
+
+
+# share of the allocatable device memory an uncapped backward takes for its workspace before it
+# switches to passes (the rest stays for the allocator's rounding and the caller's tensors)
+_AUTO_CAP_SHARE = 0.9
+
+
+def available_device_bytes(device: torch.device) -> int:
+    """Bytes a new allocation on ``device`` can take: the driver's free memory plus what torch's
+    caching allocator holds reserved but unused."""
+    free, _ = torch.cuda.mem_get_info(device)
+    return int(free + torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device))
+
+
+def _workspace_cap(limit: int, one_pass_bytes: int, device: torch.device) -> int:
+    """The cap a backward runs under: ``limit`` when set (> 0); with no limit, 0 (one pass) if the
+    one-pass workspace fits ``_AUTO_CAP_SHARE`` of the allocatable memory, else that share."""
+    if limit > 0:
+        return limit
+    budget = int(available_device_bytes(device) * _AUTO_CAP_SHARE)
+    return 0 if one_pass_bytes <= budget else max(budget, 1)
 
 
 def set_backward_staging(g_rows: str) -> None:
@@ -545,13 +570,18 @@ def set_backward_staging(g_rows: str) -> None:
     _BWD_G_INT8[0] = g_rows == "int8"
 
 
-def backward_takes_one_pass(total_q: int, n_kv: int, n_heads: int, topk_: int) -> bool:
+def backward_takes_one_pass(total_q: int, n_kv: int, n_heads: int, topk_: int,
+                            device: Optional[torch.device] = None) -> bool:
     """True when the settings of ``set_backward_workspace_limit`` and ``set_backward_staging``
-    admit the one-pass bf16-row backward (whose workspace ``sparse_mla_bwd_with_target`` needs)."""
+    admit the one-pass bf16-row backward (whose workspace ``sparse_mla_bwd_with_target`` needs);
+    with no limit set and a ``device`` given, only if that workspace fits its free memory."""
     if _BWD_G_INT8[0]:
         return False
+    ws = bwd_workspace_bytes(total_q, n_kv, n_heads, topk_)
     limit = _BWD_WORKSPACE_LIMIT[0]
-    return limit == 0 or bwd_workspace_bytes(total_q, n_kv, n_heads, topk_) <= limit
+    if limit == 0 and device is not None:
+        limit = _workspace_cap(0, ws, device)
+    return limit == 0 or ws <= limit
 
 
 def autograd_backward(q: Tensor, kv: Tensor, idx: Tensor, out: Tensor, dout: Tensor, lse: Tensor, sm_scale: float,

@@ -705,6 +705,44 @@ def test_fused_attention_with_indexer_loss_honours_the_workspace_cap():
         assert err < 1e-2, f"{name}: normalised difference {err:.2e}"
 
 
+def test_uncapped_backward_runs_in_passes_when_the_device_is_short(monkeypatch):
+    """With no workspace limit set, a backward whose one-pass workspace exceeds what the device can
+    still allocate runs capped passes instead (the availability probe is patched to report a
+    budget below the one-pass size): dq bit-identical to one pass, dkv within the rounding of the
+    pass order, and the fused indexer-loss backward reports it will not take one pass."""
+    print("[uncapped backward under a short device budget]", flush=True)
+    from mcore_bridge_amd import _lib
+    g = torch.Generator().manual_seed(41)
+    T, H, K = 900, 64, 128
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16().to(DEV)
+    idx = _idx_case(T, K, g, cu=[0, 500, T]).to(DEV)
+    dout = (torch.randn(T, H, 512, generator=g) * 0.01).bfloat16().to(DEV)
+    out, lse = ops.sparse_mla_fwd(q, kv, idx, W.SM_SCALE, True)
+    one = ops.bwd_workspace_bytes(T, T, H, K)
+    dq_a, dkv_a = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    assert ops.backward_takes_one_pass(T, T, H, K, q.device)
+    budget = ops.bwd_workspace_bytes_chunked(T, T, H, K, 256)
+    assert budget < one
+    monkeypatch.setattr(ops, "available_device_bytes", lambda device: int(budget / ops._AUTO_CAP_SHARE) + 1)
+    sizes = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        if name == "dsa_sparse_mla_bwd_ex":
+            sizes.append(args[-3])
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    assert not ops.backward_takes_one_pass(T, T, H, K, q.device)
+    dq_b, dkv_b = ops.sparse_mla_bwd(q, kv, idx, out, dout, lse, W.SM_SCALE, True)
+    torch.cuda.synchronize()
+    assert sizes and sizes[0] < one, f"workspace {sizes} not capped below the one-pass {one}"
+    assert torch.equal(dq_a, dq_b), "dq differs in passes"
+    err = ((dkv_b.double() - dkv_a.double()).norm() / dkv_a.double().norm()).item()
+    assert err < 1e-2, f"dkv: normalised difference {err:.2e}"
+
+
 def test_dense_indexer_loss_of_an_empty_batch_is_zero():
     """T = 0: the dense indexer loss is 0 and its backward gives empty gradients (no kernel is called
     with zero key columns)."""
