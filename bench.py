@@ -418,7 +418,8 @@ def v4_leg(torch, dev, reps: int = 5):
     of the rate-4 compressed entries (index row width 640), per-head attention sink; forward +
     backward of v4.sink_attention.  Algorithmic work with the 512-wide keys: forward 2 (512 + 512)
     H per attended (query, key) pair, backward 2 (3 x 512 + 2 x 512) H.  The kernels read the
-    512-wide q rows as they are, take the K = V rows in the 576-wide row layout (rope region zero)
+    512-wide q rows as they are (their instantiations without the rope part: 512-deep scores,
+    1024-byte G rows), take the K = V rows in the 576-wide row layout (rope region zero)
     and fold the sink in (the forward's epilogue, Delta from B1, one d sink kernel), so
     `kernels_ms` (the sink entry points on pre-padded key rows) is what the kernels take and
     `host_composition_ms` the rest: the key rows' pad copy, the dkv slice, autograd."""

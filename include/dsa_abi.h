@@ -163,8 +163,9 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* idx, int to
  * Replaces the core attention of the reference's DeepSeek-V4 layers with its
  * core_attention.attn_sink (src/mcore_bridge/model/gpts/deepseek_v4.py:443; the layer
  * :61-328, whose core attention is megatron-core's).  sinks == NULL is dsa_sparse_mla_fwd.
- * d_qk 576, or 512 for V4's 512-wide heads: q [total_q, n_heads, 512] without a rope part (it
- * counts as zero), kv rows still 576 wide with columns 512..575 zero. */
+ * d_qk 576, or 512 for V4's 512-wide heads: q [total_q, n_heads, 512] without a rope part, kv
+ * rows still 576 wide with columns 512..575 zero (not read: the scores contract over the 512
+ * latent dims). */
 int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* idx, int total_q, int n_kv,
                             int n_heads, int d_qk, int d_v, int topk, float sm_scale, int causal,
                             const float* sinks, void* out, float* lse, void* stream);

@@ -123,11 +123,16 @@ DSA_DEV uint32_t i8_pack4(const f32x16& a, int o, float inv) {
 DSA_DEV int gtile_slot(int j) { return j ^ ((j >> 3) & 1); }
 
 // KS = head k-steps run per block (a power of two >= n_heads / 16; steps past n_heads multiply
-// zero Q^T / dO^T fragments).
-template <int KS, bool I8>
+// zero Q^T / dO^T fragments).  ROPE = false (512-wide q rows, bf16 G rows only): the G rows are
+// 1024 bytes (no rope part, whose sums would be zero), every wave runs 4 output tiles and 8
+// stores per block.
+template <int KS, bool I8, bool ROPE = true>
 __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
+  static_assert(ROPE || !I8, "int8 G rows keep the 576-dim format");
   constexpr int NW = 4;
   constexpr int G = 2 * kGHeads / 16 / NW;          // 4 copies per wave per block
+  constexpr int NGS = ROPE ? kGStores : kGStores - 1;   // G-tile stores per wave per block
+  constexpr int GW = ROPE ? kDqk : kDv;              // bf16 elements per G row
   __shared__ __attribute__((aligned(16))) GSmem sm;
   const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
@@ -219,7 +224,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) va[i][ks] = u32x4{0, 0, 0, 0};
   }
-  const int nq = wave < 2 ? 5 : 4;
+  const int nq = ROPE && wave < 2 ? 5 : 4;
   // byte address of (row tr_h + dr, latent column tr_c of tile mt) in a round part of row pitch rp
   auto tr_at = [&](uint32_t part, int rp, int mt, int dr) {
     const int cb = 64 * mt + 2 * tr_c;
@@ -313,16 +318,16 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
                   pack_bf16x2(v.b[2], v.b[3])};
     bf16_t* g = reinterpret_cast<bf16_t*>(p.g_stage);
     if (i < 8)
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(g + (int64_t)rpos[i] * kDqk + 8 * lane));
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(g + (int64_t)rpos[i] * GW + 8 * lane));
     else
-      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(g + (int64_t)rope_pos * kDqk + 8 * (64 + (lane & 7))));
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(g + (int64_t)rope_pos * GW + 8 * (64 + (lane & 7))));
   };
-  // k-step of copy c (c < G) and of store i (i < kGStores); stores follow copies in a step
+  // k-step of copy c (c < G) and of store i (i < NGS); stores follow copies in a step
   constexpr auto copy_ks = [](int c) { return c * KS / G; };
-  constexpr auto store_ks = [](int i) { return i * KS / kGStores; };
+  constexpr auto store_ks = [](int i) { return i * KS / NGS; };
   constexpr int kStoresAfterLastCopy = [] {
     int n = 0;
-    for (int i = 0; i < kGStores; ++i) n += (i * KS / kGStores) >= ((G - 1) * KS / G);
+    for (int i = 0; i < NGS; ++i) n += (i * KS / NGS) >= ((G - 1) * KS / G);
     return n;
   }();
 
@@ -338,21 +343,21 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       // b-1's copies(b+1) + stores(b-2).
       if (blk + 1 >= nblk) wait_vmcnt<0>();
       else if (blk <= 1) wait_vmcnt<G>();
-      else if (blk == 2) wait_vmcnt<G + kGStores>();
-      else wait_vmcnt<G + kGStores + kStoresAfterLastCopy>();
+      else if (blk == 2) wait_vmcnt<G + NGS>();
+      else wait_vmcnt<G + NGS + kStoresAfterLastCopy>();
       __syncthreads();
       const bool copy_next = blk + 2 < nblk;
       const bool store_prev = blk > 0;
       // G rows of the previous block's tile: this wave's 8 latent rows (wave-uniform) and the
       // rope row of this lane
       int32_t rpos[8], rope_pos = 0;
-      StoreData sv[kGStores];
+      StoreData sv[NGS];
       if (store_prev) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(blk - 1) * kBK + 8 * wave + i]);
         rope_pos = sm.pos[(blk - 1) * kBK + rope_row];
 #pragma unroll
-        for (int i = 0; i < kGStores; ++i)
+        for (int i = 0; i < NGS; ++i)
           if (store_ks(i) == 0) sv[i] = store_load(i);
       }
       const char* sd = sm.loop.st[blk % kStages][0] + b_off;
@@ -379,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
         }
         if (store_prev) {
 #pragma unroll
-          for (int i = 0; i < kGStores; ++i) {
+          for (int i = 0; i < NGS; ++i) {
             if (store_ks(i) == ks + 1) sv[i] = store_load(i);   // next step's data
             if (store_ks(i) == ks) store_issue(rpos, rope_pos, i, sv[i]);
           }
@@ -412,7 +417,7 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
       for (int i = 0; i < 8; ++i) rpos[i] = __builtin_amdgcn_readfirstlane(sm.pos[(nblk - 1) * kBK + 8 * wave + i]);
       const int32_t rope_pos = sm.pos[(nblk - 1) * kBK + rope_row];
 #pragma unroll
-      for (int i = 0; i < kGStores; ++i) store_issue(rpos, rope_pos, i, store_load(i));
+      for (int i = 0; i < NGS; ++i) store_issue(rpos, rope_pos, i, store_load(i));
     }
   };
   // ---- int8 G rows.  Each wave runs its output tiles one after another (a tile's MFMAs, Q part
@@ -574,9 +579,11 @@ __global__ __launch_bounds__(256, 1) void bwd_g_kernel(SparseBwdParams p) {
   if constexpr (I8) {
     if (nq == 5) block_loop_i8(std::integral_constant<int, 5>{});
     else block_loop_i8(std::integral_constant<int, 4>{});
-  } else {
+  } else if constexpr (ROPE) {
     if (nq == 5) block_loop(std::integral_constant<int, 5>{});
     else block_loop(std::integral_constant<int, 4>{});
+  } else {
+    block_loop(std::integral_constant<int, 4>{});
   }
 }
 

@@ -29,7 +29,8 @@ struct SparseFwdParams {
 
 // Per-pair dKV partial rows ("G rows") of the sparse backward, written by B3 and summed per key
 // by B5, in one of two formats:
-//   bf16 (default): the 576 dims as bf16, 1152 bytes.
+//   bf16 (default): the 576 dims as bf16, 1152 bytes (for 512-wide q rows, q_dim = 512: the 512
+//     latent dims, 1024 bytes; the workspace keeps the 1152-byte sizing).
 //   int8 (DSA_BWD_G_INT8): 640 bytes, five 128-byte lines.  Dims are grouped by 32 (groups
 //     0..15 latent, 16..17 rope), each group with its own scale s = max|g| / 127 rounded up to
 //     bf16, so |g / s| <= 127; a dim is stored as u = rint(g / s) + 128 (offset binary, 1..255)

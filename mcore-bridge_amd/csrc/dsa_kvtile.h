@@ -39,11 +39,12 @@ DSA_DEV uint32_t tile_off(uint32_t k, uint32_t c) {
   return c < 64 ? key_row(k) * kTileVPitch + 16u * c : kTileVBytes + k * 128u + 16u * ((c - 64) ^ ((k >> 1) & 7u));
 }
 
-// Copies issued per wave per tile.
-template <int NW>
+// Copies issued per wave per tile.  ROPE = false: 512-wide score rows (q without a rope part),
+// which never read the rope region, so only the 32 V rows are gathered.
+template <int NW, bool ROPE = true>
 constexpr int tile_copies_per_wave() {
   static_assert(NW == 1 || NW == 2 || NW == 4, "1, 2 or 4 waves");
-  return kTileInstr / NW;
+  return (ROPE ? kTileInstr : kTileKeys) / NW;
 }
 
 // Per-lane gather sources of one wave for one block, from the block's 32 KV row ids in LDS
@@ -60,15 +61,17 @@ DSA_DEV const char* kv_row_addr(const bf16_t* kv, int row) {
   return reinterpret_cast<const char*>(kv) + (int64_t)(row >= 0 ? row : 0) * (kLatent * 2);
 }
 
-template <int NW>
+template <int NW, bool ROPE = true>
 DSA_DEV TileSrc<NW> tile_sources(const bf16_t* kv, const int32_t* idx_blk, int wave, int lane) {
   TileSrc<NW> s;
   s.v = kv_row_addr(kv, idx_blk[wave + NW * (lane % (32 / NW))]);
+  if constexpr (ROPE) {
 #pragma unroll
-  for (int j = 0; j < 4 / NW; ++j) {
-    const int key = 8 * (wave + NW * j) + (lane >> 3);
-    const uint32_t c = (uint32_t)(lane & 7) ^ ((key >> 1) & 7u);
-    s.rope[j] = kv_row_addr(kv, idx_blk[key]) + (64 + c) * 16;
+    for (int j = 0; j < 4 / NW; ++j) {
+      const int key = 8 * (wave + NW * j) + (lane >> 3);
+      const uint32_t c = (uint32_t)(lane & 7) ^ ((key >> 1) & 7u);
+      s.rope[j] = kv_row_addr(kv, idx_blk[key]) + (64 + c) * 16;
+    }
   }
   return s;
 }
@@ -160,10 +163,10 @@ DSA_DEV void gather_issue_at(const TileDst& d, const TileSrc<NW>& src, const cha
 
 // The whole gather of one tile (all of this wave's copies back to back; rows read two copies
 // ahead, the first two behind one explicit 5-wait-state pad).
-template <int NW>
+template <int NW, bool ROPE = true>
 DSA_DEV void gather_tile(uint32_t tile, const bf16_t* kv, const int32_t* idx_blk, int wave, int lane) {
-  constexpr int n = tile_copies_per_wave<NW>();
-  const TileSrc<NW> src = tile_sources<NW>(kv, idx_blk, wave, lane);
+  constexpr int n = tile_copies_per_wave<NW, ROPE>();
+  const TileSrc<NW> src = tile_sources<NW, ROPE>(kv, idx_blk, wave, lane);
   const char* row[2] = {gather_row<NW>(src, 0), gather_row<NW>(src, 1)};
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_nop 4");

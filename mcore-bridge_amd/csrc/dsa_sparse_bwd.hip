@@ -32,6 +32,10 @@
 // global_load_lds copies (see dsa_kvtile.h) completed by explicit s_waitcnt vmcnt + barrier.
 // vmcnt counts every vector-memory instruction of the wave in issue order, so each wave issues
 // a fixed number of copies and stores per block and the waits count them exactly.
+// B1, B2 and B3 have instantiations without the rope part (ROPE = false) for 512-wide q rows
+// (the DeepSeek-V4 sink attention): S contracts over the 512 latent dims only, dQ has 512
+// columns, the KV tiles' rope region is neither gathered nor read, and the bf16 G rows carry the
+// 512 latent dims only (1024 bytes; B5 writes dKV's rope columns as zeros).
 #include <algorithm>
 #include <type_traits>
 
@@ -76,12 +80,13 @@ struct SpSmem {
   int red[4];
 };
 
-template <int NW>
+template <int NW, bool ROPE>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
-  constexpr int G = tile_copies_per_wave<NW>();
+  constexpr int QKS = (ROPE ? kDqk : kDv) / 16;   // S k-steps per block (no rope part: 32)
+  constexpr int G = tile_copies_per_wave<NW, ROPE>();
   constexpr int S = 4;  // staging stores per wave per block (2 x P, 2 x dS)
-  constexpr int kCopyEvery = kDqk / 16 / G;   // S/dP steps per gather copy
-  static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the k-steps");
+  constexpr int kCopyEvery = QKS / G;   // S/dP steps per gather copy
+  static_assert(kCopyEvery * G == QKS, "copies spread evenly over the k-steps");
   __shared__ __attribute__((aligned(128))) SpSmem sm;
   const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
@@ -106,14 +111,14 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
       async_copy16_unordered(o_t + (int64_t)hs * (kDv * 2) + 16 * (lane ^ (i & 7)), ob + 1024u * i);
     }
   }
-  // Q (576) and dO (512) fragments, d-contiguous: lane holds [16*ks + 8*hb, +8).
-  u32x4 qf[kDqk / 16], df[kDv / 16];
-  // (q rows of 512: no rope part, its fragments zero)
+  // Q (576, or 512 without ROPE) and dO (512) fragments, d-contiguous: lane holds [16*ks + 8*hb, +8).
+  u32x4 qf[QKS], df[kDv / 16];
+  // (q rows of 512 under ROPE: no rope part, its fragments zero)
   const bool q_rope = p.q_dim != kDv;
   const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)hsafe * (q_rope ? kDqk : kDv) + hb * 8;
   const bf16_t* drow = p.dout + (int64_t)t * p.dout_stride_t + (int64_t)hsafe * kDv + hb * 8;
 #pragma unroll
-  for (int ks = 0; ks < kDqk / 16; ++ks) {
+  for (int ks = 0; ks < QKS; ++ks) {
     u32x4 v = u32x4{0, 0, 0, 0};
     if (ks < kDv / 16 || q_rope) v = gload16(qrow + ks * 16);
     qf[ks] = head_ok ? v : u32x4{0, 0, 0, 0};
@@ -162,8 +167,8 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
   const uint32_t tile0 = lds_addr(sm.tile[0]);
   const uint32_t wsg = __builtin_amdgcn_readfirstlane(wave);
 
-  if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
-  if (nblk > 1) gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
+  if (nblk > 0) gather_tile<NW, ROPE>(tile0, p.kv, sm.idx, wave, lane);
+  if (nblk > 1) gather_tile<NW, ROPE>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
   uint32_t st_cur = 0, st_next = 2 * kTileBytes;   // ring byte offsets of blocks blk, blk+2
   u32x4 pw[2], dw[2];   // previous block's values, stored right after the next block's barrier
   for (int blk = 0; blk < nblk; ++blk) {
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
     // block blk+2's gather, one copy per kCopyEvery S/dP steps below.  Issued every iteration:
     // the last two re-gather block nblk-1 into the ring slot no block reads any more (so no copy
     // sits behind a branch); they are retired before the kernel ends.
-    const TileSrc<NW> next_src = tile_sources<NW>(p.kv, sm.idx + min(blk + 2, nblk - 1) * kBK, wave, lane);
+    const TileSrc<NW> next_src = tile_sources<NW, ROPE>(p.kv, sm.idx + min(blk + 2, nblk - 1) * kBK, wave, lane);
     // source row of the next copy, read one copy slot ahead of its issue
     const char* next_row = gather_row<NW>(next_src, 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -207,9 +212,9 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_sp_kernel(SparseBwdParams p) {
 #pragma unroll
       for (int i = 0; i < kPre; ++i) a[i] = lds_load16(addr(i));
 #pragma unroll
-      for (int ks = 0; ks < kDqk / 16; ++ks) {
+      for (int ks = 0; ks < QKS; ++ks) {
         const u32x4 cur = a[ks % kPre];
-        if (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(addr(ks + kPre));
+        if (ks + kPre < QKS) a[ks % kPre] = lds_load16(addr(ks + kPre));
         s = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qf[ks]), s);
         if (ks == 0) mfma32x32x16_acc_first(dp, cur, df[0]);
         else if (ks < kDv / 16) mfma32x32x16_acc(dp, cur, df[ks]);
@@ -289,15 +294,16 @@ struct DqSmem {
   int red[8];
 };
 
-template <int NW>
+template <int NW, bool ROPE>
 __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
+  constexpr int DQ = ROPE ? kDqk : kDv;                        // dq row width
   constexpr int HR = 32 * NW;                                  // head rows of the workgroup
   constexpr int HT = HR / 16;                                  // head tiles
-  constexpr int DT = kDqk / 16 / NW;                           // dim tiles per wave
-  constexpr int TC = tile_copies_per_wave<NW>();
+  constexpr int DT = DQ / 16 / NW;                             // dim tiles per wave
+  constexpr int TC = tile_copies_per_wave<NW, ROPE>();
   constexpr int G = TC + HR / 16 / NW;
   static_assert(HR / 16 / NW == 2, "two dS copies per wave per block");
-  static_assert(DT * NW * 16 == kDqk && DT >= TC, "dims split evenly; one tile copy per dim step");
+  static_assert(DT * NW * 16 == DQ && DT >= TC, "dims split evenly; one tile copy per dim step");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
   const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
@@ -355,11 +361,11 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
   mfma_acc_drain();   // zero writes of the accumulators before their first MFMA read
 
   if (nblk > 0) {
-    gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
+    gather_tile<NW, ROPE>(tile0, p.kv, sm.idx, wave, lane);
     copy_ds(sm.ring.ds[0], 0);
   }
   if (nblk > 1) {
-    gather_tile<NW>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
+    gather_tile<NW, ROPE>(tile0 + kTileBytes, p.kv, sm.idx + kBK, wave, lane);
     copy_ds(sm.ring.ds[1], 1);
   }
   int st = 0;   // ring stage of block blk
@@ -370,7 +376,7 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
     const bool copy_next = blk + 2 < nblk;
     const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
     TileSrc<NW> next_src;
-    if (copy_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
+    if (copy_next) next_src = tile_sources<NW, ROPE>(p.kv, sm.idx + (blk + 2) * kBK, wave, lane);
     // source row of the next tile copy, read one copy slot ahead of its issue
     const char* next_row = copy_next ? gather_row<NW>(next_src, 0) : nullptr;
     __builtin_amdgcn_sched_barrier(0);
@@ -446,11 +452,15 @@ __global__ __launch_bounds__(NW * 64, 1) void bwd_dq_kernel(SparseBwdParams p) {
 // wave covers all 8 head tiles: K^T fragments are read once per workgroup.  Per SIMD: 72
 // MFMAs per block.  Accumulators: 5 x 8 tiles of 16 x 16; at two waves per SIMD each register
 // file holds 128 per wave, so dim tiles 0-3 are pinned in AccVGPRs and the 5th in VGPRs.
+// Without ROPE (512-wide dq rows) every wave owns 4 dim tiles: 64 MFMAs per SIMD per block.
+template <bool ROPE>
 __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
   constexpr int NW = 8, NWC = 4;                 // waves; copy-issuing waves
   constexpr int HT = 8;                          // head tiles (128 heads)
-  constexpr int DTMAX = 5;                       // dim tiles per wave (5 for waves 0-3, 4 after)
-  constexpr int TC = tile_copies_per_wave<NWC>();
+  constexpr int DTMAX = ROPE ? 5 : 4;            // dim tiles of a copy-issuing wave
+  constexpr int DTP = 4;                         // dim tiles of the other waves
+  static_assert(NWC * DTMAX + (NW - NWC) * DTP == (ROPE ? kDqk : kDv) / 16, "dims split over the waves");
+  constexpr int TC = tile_copies_per_wave<NWC, ROPE>();
   constexpr int G = TC + 2;                      // copies per copy-issuing wave per block
   static_assert(TC <= 2 * HT - 6, "tile copies before the dS copy slots");
   __shared__ __attribute__((aligned(128))) DqSmem sm;
@@ -484,8 +494,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
     kr[h] = kTileVBytes + key * 128u + 8u * (gi & 1) + 16u * (((gi & 3) >> 1) ^ ((key >> 1) & 7u));
   }
   const uint32_t ds_lane = gi * 64u + 16u * (g ^ ((gi >> 1) & 3));
-  const int d0 = copier ? DTMAX * wu : DTMAX * NWC + (DTMAX - 1) * (wu - NWC);   // first dim tile
-  const int nd = copier ? DTMAX : DTMAX - 1;
+  const int d0 = copier ? DTMAX * wu : DTMAX * NWC + DTP * (wu - NWC);   // first dim tile
+  const int nd = copier ? DTMAX : DTP;
   const uint32_t tile0 = lds_addr(sm.ring.tile[0]);
 
   f32x4 acc[DTMAX][HT];
@@ -499,7 +509,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       if (b < nblk) {
-        gather_tile<NWC>(tile0 + b * kTileBytes, p.kv, sm.idx + b * kBK, wu, lane);
+        gather_tile<NWC, ROPE>(tile0 + b * kTileBytes, p.kv, sm.idx + b * kBK, wu, lane);
         copy_ds_part(sm.ring.ds[b], b, 0);
         copy_ds_part(sm.ring.ds[b], b, 1);
       }
@@ -523,7 +533,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
       const int src_blk = min(blk + 2, nblk - 1);
       const int st_next = st == 0 ? 2 : st - 1;   // (blk + 2) % 3
       TileSrc<NWC> next_src;
-      if (CP) next_src = tile_sources<NWC>(p.kv, sm.idx + src_blk * kBK, wu, lane);
+      if (CP) next_src = tile_sources<NWC, ROPE>(p.kv, sm.idx + src_blk * kBK, wu, lane);
       const char* next_row[2] = {CP ? gather_row<NWC>(next_src, 0) : nullptr, CP ? gather_row<NWC>(next_src, 1) : nullptr};
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t next_tile = tile0 + st_next * kTileBytes;
@@ -572,7 +582,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq8_kernel(SparseBwdParams p) {
     }
   };
   if (copier) block_loop(std::integral_constant<int, DTMAX>{}, std::true_type{});
-  else block_loop(std::integral_constant<int, DTMAX - 1>{}, std::false_type{});
+  else block_loop(std::integral_constant<int, DTP>{}, std::false_type{});
   wait_vmcnt0();   // the last re-copies have landed before the epilogue reuses the ring
   mfma_acc_drain();
   // ---- epilogue: dQ rows through LDS (64 heads at a time), then coalesced 16-byte stores.
@@ -737,15 +747,18 @@ __global__ __launch_bounds__(kCsrThreads) void csr_fill_kernel(const int32_t* id
 
 // ------------------------------------------------------------------------------------------
 // B5: dKV[s] = sum of G rows in s's segment (fp32), or dKV[s] += that sum for the later query
-// chunks of a chunked backward.  One workgroup (288 threads) per key:
-// 4 row lanes x 72 chunks of 8 dims.
+// chunks of a chunked backward.  One workgroup (4 * W / 8 threads) per key: 4 row lanes x W / 8
+// chunks of 8 dims.  W = 576, or 512 for the G rows of 512-wide q rows (dKV's rope columns are
+// then zero).
 // ------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_stage, const int64_t* offsets,
-                                                             int n_kv, float* dkv, int64_t dkv_stride, int accumulate) {
-  __shared__ float red[3][kDqk];
+template <int W>
+__global__ __launch_bounds__(W / 2) void bwd_dkv_reduce_kernel(const bf16_t* g_stage, const int64_t* offsets,
+                                                               int n_kv, float* dkv, int64_t dkv_stride,
+                                                               int accumulate) {
+  __shared__ float red[3][W];
   const int s = blockIdx.x;
   if (s >= n_kv) return;
-  constexpr int kChunks = kDqk / 8;
+  constexpr int kChunks = W / 8;
   const int c = threadIdx.x % kChunks, r = threadIdx.x / kChunks;
   const int64_t a = offsets[s], b = offsets[s + 1];
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -757,7 +770,7 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
     }
   };
   auto load_row = [&](int64_t i) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g_stage + i * kDqk + c * 8));
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g_stage + i * W + c * 8));
   };
   // rows a + r, a + r + 4, ..: four loads in flight per thread, summed in row order (a loop of
   // one load and its adds kept a single 16-byte load per thread in flight)
@@ -782,6 +795,9 @@ __global__ __launch_bounds__(288) void bwd_dkv_reduce_kernel(const bf16_t* g_sta
       const float v = acc[e] + red[0][c * 8 + e] + red[1][c * 8 + e] + red[2][c * 8 + e];
       out[e] = accumulate ? out[e] + v : v;
     }
+  }
+  if constexpr (W < kDqk) {
+    if (!accumulate && (int)threadIdx.x < kDqk - W) dkv[(int64_t)s * dkv_stride + W + threadIdx.x] = 0.f;
   }
 }
 
@@ -928,41 +944,56 @@ int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent
   launch_pair_csr(p.idx, p.idx_stride, p.total_q, p.topk, p.n_kv, p.causal, p.q_offset, p.csr_counts,
                   p.csr_offsets, p.pair_pos, stream);
   mark(1);
-  if (nw == 4) {
-    hipLaunchKernelGGL(bwd_sp_kernel<4>, grid, dim3(256), 0, stream, p);
-    mark(2);
-    if (grid.y == 1) hipLaunchKernelGGL(bwd_dq8_kernel, grid, dim3(512), 0, stream, p);
-    else hipLaunchKernelGGL(bwd_dq_kernel<4>, grid, dim3(256), 0, stream, p);
-  } else if (nw == 2) {
-    hipLaunchKernelGGL(bwd_sp_kernel<2>, grid, dim3(128), 0, stream, p);
-    mark(2);
-    hipLaunchKernelGGL(bwd_dq_kernel<2>, grid, dim3(128), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL(bwd_sp_kernel<1>, grid, dim3(64), 0, stream, p);
-    mark(2);
-    hipLaunchKernelGGL(bwd_dq_kernel<1>, grid, dim3(64), 0, stream, p);
-  }
+  // B1, B2: 512-wide q rows (no rope part) take the instantiations without the rope k-steps
+  auto launch_sp_dq = [&](auto rope_c) {
+    constexpr bool R = decltype(rope_c)::value;
+    if (nw == 4) {
+      hipLaunchKernelGGL((bwd_sp_kernel<4, R>), grid, dim3(256), 0, stream, p);
+      mark(2);
+      if (grid.y == 1) hipLaunchKernelGGL((bwd_dq8_kernel<R>), grid, dim3(512), 0, stream, p);
+      else hipLaunchKernelGGL((bwd_dq_kernel<4, R>), grid, dim3(256), 0, stream, p);
+    } else if (nw == 2) {
+      hipLaunchKernelGGL((bwd_sp_kernel<2, R>), grid, dim3(128), 0, stream, p);
+      mark(2);
+      hipLaunchKernelGGL((bwd_dq_kernel<2, R>), grid, dim3(128), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((bwd_sp_kernel<1, R>), grid, dim3(64), 0, stream, p);
+      mark(2);
+      hipLaunchKernelGGL((bwd_dq_kernel<1, R>), grid, dim3(64), 0, stream, p);
+    }
+  };
+  if (p.q_dim == kDv) launch_sp_dq(std::false_type{});
+  else launch_sp_dq(std::true_type{});
   mark(3);
   const int nks = p.n_heads / 16;
   const dim3 ggrid(xcd_grid(p.total_q, p.n_xcd));
-  if (p.g_int8)
-    launch_bwd_g_i8(p, stream);
-  else if (nks > 4)
-    hipLaunchKernelGGL((bwd_g_kernel<8, false>), ggrid, dim3(256), 0, stream, p);
-  else if (nks > 2)
-    hipLaunchKernelGGL((bwd_g_kernel<4, false>), ggrid, dim3(256), 0, stream, p);
-  else if (nks > 1)
-    hipLaunchKernelGGL((bwd_g_kernel<2, false>), ggrid, dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((bwd_g_kernel<1, false>), ggrid, dim3(256), 0, stream, p);
+  // bf16 G rows of 512-wide q rows are 1024 bytes (no rope part); int8 rows keep their format
+  const bool g512 = !p.g_int8 && p.q_dim == kDv;
+  auto launch_g = [&](auto rope_c) {
+    constexpr bool R = decltype(rope_c)::value;
+    if (nks > 4)
+      hipLaunchKernelGGL((bwd_g_kernel<8, false, R>), ggrid, dim3(256), 0, stream, p);
+    else if (nks > 2)
+      hipLaunchKernelGGL((bwd_g_kernel<4, false, R>), ggrid, dim3(256), 0, stream, p);
+    else if (nks > 1)
+      hipLaunchKernelGGL((bwd_g_kernel<2, false, R>), ggrid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((bwd_g_kernel<1, false, R>), ggrid, dim3(256), 0, stream, p);
+  };
+  if (p.g_int8) launch_bwd_g_i8(p, stream);
+  else if (g512) launch_g(std::false_type{});
+  else launch_g(std::true_type{});
   mark(4);
+  const bf16_t* g_rows = reinterpret_cast<const bf16_t*>(p.g_stage);
   if (p.g_int8)
     hipLaunchKernelGGL(bwd_dkv_reduce_i8_kernel, dim3(p.n_kv), dim3(256), 0, stream, p.g_stage, p.csr_offsets,
                        p.n_kv, p.dkv, p.dkv_stride, p.dkv_accumulate);
+  else if (g512)
+    hipLaunchKernelGGL(bwd_dkv_reduce_kernel<kDv>, dim3(p.n_kv), dim3(kDv / 2), 0, stream, g_rows, p.csr_offsets,
+                       p.n_kv, p.dkv, p.dkv_stride, p.dkv_accumulate);
   else
-    hipLaunchKernelGGL(bwd_dkv_reduce_kernel, dim3(p.n_kv), dim3(288), 0, stream,
-                       reinterpret_cast<const bf16_t*>(p.g_stage), p.csr_offsets, p.n_kv, p.dkv, p.dkv_stride,
-                       p.dkv_accumulate);
+    hipLaunchKernelGGL(bwd_dkv_reduce_kernel<kDqk>, dim3(p.n_kv), dim3(kDqk / 2), 0, stream, g_rows, p.csr_offsets,
+                       p.n_kv, p.dkv, p.dkv_stride, p.dkv_accumulate);
   mark(5);
   return hipGetLastError() == hipSuccess && marks_ok ? 0 : -4;
 }

@@ -71,11 +71,14 @@ struct FwdSmem {
 
 }  // namespace
 
-template <int NW>
+// ROPE = false: q rows of 512 (no rope part): the scores contract over the 512 latent dims only
+// (32 QK MFMAs per block instead of 36) and the tiles' rope region is neither gathered nor read.
+template <int NW, bool ROPE>
 __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdParams p) {
-  constexpr int G = tile_copies_per_wave<NW>();
-  constexpr int kCopyEvery = kDqk / 16 / G;   // QK MFMAs per gather copy (36 MFMAs per block)
-  static_assert(kCopyEvery * G == kDqk / 16, "copies spread evenly over the QK MFMAs");
+  constexpr int QKS = (ROPE ? kDqk : kDv) / 16;   // QK MFMAs (16-deep k-steps) per block
+  constexpr int G = tile_copies_per_wave<NW, ROPE>();
+  constexpr int kCopyEvery = QKS / G;             // QK MFMAs per gather copy
+  static_assert(kCopyEvery * G == QKS, "copies spread evenly over the QK MFMAs");
   __shared__ __attribute__((aligned(128))) FwdSmem sm;
 
   // work item = (query t, key split); n_split > 1 only for decode, where a few queries must
@@ -94,15 +97,15 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
   const int head = blockIdx.y * 128 + wave * 32 + hl;
   const bool head_ok = head < p.n_heads;
 
-  // ---- Q fragments: lane holds q[t, head, 16*ks + 8*hb .. +7] for ks = 0..35
-  // (q rows of 512: no rope part, its fragments zero)
-  u32x4 qf[kDqk / 16];
+  // ---- Q fragments: lane holds q[t, head, 16*ks + 8*hb .. +7] for ks < QKS (q rows of 512 under
+  // ROPE: no rope part, its fragments zero)
+  u32x4 qf[QKS];
   {
     const bool q_rope = p.q_dim != kDv;
     const int qd = q_rope ? kDqk : kDv;
     const bf16_t* qrow = p.q + (int64_t)t * p.q_stride_t + (int64_t)(head_ok ? head : 0) * qd + hb * 8;
 #pragma unroll
-    for (int ks = 0; ks < kDqk / 16; ++ks) {
+    for (int ks = 0; ks < QKS; ++ks) {
       u32x4 v = u32x4{0, 0, 0, 0};
       if (ks < kDv / 16 || q_rope) v = gload16(qrow + ks * 16);
       qf[ks] = head_ok ? v : u32x4{0, 0, 0, 0};
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
     for (int m = 0; m < kDv / 32; ++m) o[m] = f32x16{};
     mfma_acc_drain();
     l_run = 0.f;
-    if (nblk > 0) gather_tile<NW>(tile0, p.kv, sm.idx, wave, lane);
+    if (nblk > 0) gather_tile<NW, ROPE>(tile0, p.kv, sm.idx, wave, lane);
     // block -1's P^T slot holds zeros (iteration 0 multiplies tile 0 by it)
     lds_store16(pf_addr(1, wave, 0), u32x4{0, 0, 0, 0});
     lds_store16(pf_addr(1, wave, 1), u32x4{0, 0, 0, 0});
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
       // block blk+1's gather is issued one copy per kCopyEvery QK MFMAs below
       const bool gather_next = blk + 1 < nblk;
       TileSrc<NW> next_src;
-      if (gather_next) next_src = tile_sources<NW>(p.kv, sm.idx + (blk + 1) * kBK, wave, lane);
+      if (gather_next) next_src = tile_sources<NW, ROPE>(p.kv, sm.idx + (blk + 1) * kBK, wave, lane);
       // source rows of the next two copies, each read two copy slots ahead of its issue (with one
       // wave the copies are one MFMA apart)
       const char* next_row[2] = {gather_next ? gather_row<NW>(next_src, 0) : nullptr,
@@ -265,10 +268,10 @@ __global__ __launch_bounds__(NW * 64, 1) void sparse_mla_fwd_kernel(SparseFwdPar
         f32x16 sa;
         const TileDst nd = tile_dst<NW>(next_tile, wsg);
         auto qk = [&](auto gather) {
-          static_for<0, kDqk / 16>([&](auto ksc) {
+          static_for<0, QKS>([&](auto ksc) {
             constexpr int ks = decltype(ksc)::value;
             const u32x4 cur = a[ks % kPre];
-            if constexpr (ks + kPre < kDqk / 16) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
+            if constexpr (ks + kPre < QKS) a[ks % kPre] = lds_load16(qk_addr(ks + kPre));
             if constexpr (ks == 0) mfma32x32x16_cV_first(sa, cur, qf[0]);
             else mfma32x32x16_cV(sa, cur, qf[ks]);
             if constexpr (decltype(gather)::value && ks % kCopyEvery == 0) {
@@ -443,12 +446,20 @@ int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream) {
   if (p.sinks != nullptr && p.n_split != 1) return -2;                  // a sink joins each row once
   const dim3 grid(xcd_grid(p.total_q * p.n_split, p.n_xcd), (p.n_heads + 127) / 128);
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
-  if (nw == 4)
-    hipLaunchKernelGGL(sparse_mla_fwd_kernel<4>, grid, dim3(256), 0, stream, p);
-  else if (nw == 2)
-    hipLaunchKernelGGL(sparse_mla_fwd_kernel<2>, grid, dim3(128), 0, stream, p);
-  else
-    hipLaunchKernelGGL(sparse_mla_fwd_kernel<1>, grid, dim3(64), 0, stream, p);
+  if (p.q_dim == kDv) {   // 512-wide q: the rope-free instantiation
+    if (nw == 4)
+      hipLaunchKernelGGL((sparse_mla_fwd_kernel<4, false>), grid, dim3(256), 0, stream, p);
+    else if (nw == 2)
+      hipLaunchKernelGGL((sparse_mla_fwd_kernel<2, false>), grid, dim3(128), 0, stream, p);
+    else
+      hipLaunchKernelGGL((sparse_mla_fwd_kernel<1, false>), grid, dim3(64), 0, stream, p);
+  } else if (nw == 4) {
+    hipLaunchKernelGGL((sparse_mla_fwd_kernel<4, true>), grid, dim3(256), 0, stream, p);
+  } else if (nw == 2) {
+    hipLaunchKernelGGL((sparse_mla_fwd_kernel<2, true>), grid, dim3(128), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((sparse_mla_fwd_kernel<1, true>), grid, dim3(64), 0, stream, p);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

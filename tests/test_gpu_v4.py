@@ -303,3 +303,42 @@ def test_sink_entry_points_empty_rows_and_capped_backward():
     assert torch.equal(dq0, dq1) and torch.equal(ds0, ds1)
     err = ((dkv1 - dkv0).norm() / dkv0.norm()).item()
     assert err < 1e-6, err
+
+
+@pytest.mark.parametrize("H", [128, 48])
+def test_sink_entry_points_512_rows_equal_the_576_path_with_zero_rope(H):
+    """The sink entry points on 512-wide q rows run the kernels' rope-free instantiations (32
+    score k-steps, no rope gathers, 1024-byte G rows).  With the rope part zero, the 576-wide
+    path computes the same sums plus zero products, so both give the same bits: out, lse, dq's
+    512 columns, d sink and dkv (whose rope columns are 0), in one pass and in capped passes."""
+    print(f"[v4 sink entry points] 512 vs 576 rows, H={H}", flush=True)
+    from mcore_bridge_amd import ops
+    g = torch.Generator().manual_seed(23 + H)
+    T, K = 600, 160
+    q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
+    kv = (torch.randn(T, 576, generator=g) * 0.5).bfloat16()
+    q[..., 512:] = 0
+    kv[:, 512:] = 0
+    sinks = torch.randn(H, generator=g).to(DEV)
+    idx = torch.stack([torch.randperm(T, generator=g)[:K].sort().values for _ in range(T)]).to(torch.int32)
+    idx[:3] = -1
+    idx[5, ::3] = -1
+    q, kv, idx = q.to(DEV), kv.to(DEV), idx.to(DEV)
+    q512 = q[..., :512].contiguous()
+    dout = (torch.randn(T, H, 512, generator=g) * 0.05).bfloat16().to(DEV)
+    o576, l576 = ops.sparse_mla_fwd_sink(q, kv, idx, sinks, W_SCALE, False)
+    o512, l512 = ops.sparse_mla_fwd_sink(q512, kv, idx, sinks, W_SCALE, False)
+    assert torch.equal(o512, o576) and torch.equal(l512, l576)
+    for cap in (0, 1):
+        ops.set_backward_workspace_limit(cap)
+        try:
+            dq576, dkv576, ds576 = ops.sparse_mla_bwd_sink(q, kv, idx, o576, dout, l576, sinks, W_SCALE, False)
+            dq512, dkv512, ds512 = ops.sparse_mla_bwd_sink(q512, kv, idx, o512, dout, l512, sinks, W_SCALE, False)
+        finally:
+            ops.set_backward_workspace_limit(0)
+        torch.cuda.synchronize()
+        assert dq512.shape == (T, H, 512)
+        assert torch.equal(dq512, dq576[..., :512]), f"dq differs (cap {cap})"
+        assert torch.equal(ds512, ds576), f"d sink differs (cap {cap})"
+        assert torch.equal(dkv512, dkv576), f"dkv differs (cap {cap})"
+        assert (dkv512[:, 512:] == 0).all()
