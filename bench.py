@@ -394,18 +394,22 @@ def indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale: float, nsel: i
     return res
 
 
-def _time_ms(torch, fn, reps: int, warm: int = 2):
-    """Average ms of fn() over `reps` calls, HIP events on torch's current stream (every op here
-    launches on it)."""
+def _time_ms(torch, fn, reps: int, warm: int = 2, windows: int = 3):
+    """ms per fn() call: the median over `windows` timed windows of the average of `reps` calls,
+    HIP events on torch's current stream (every op here launches on it).  One slow window (seen
+    once: a 5-call window at 1.5x the others) then does not set the figure."""
     for _ in range(warm):
         fn()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        fn()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    per = []
+    for _ in range(windows):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / reps)
+    return sorted(per)[len(per) // 2]
 
 
 PEAK_FP8_TFLOPS = 5000.0
