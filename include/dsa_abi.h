@@ -305,6 +305,26 @@ int dsa_indexer_kl_target_from_bwd(const void* bwd_workspace, size_t bwd_workspa
                                    int total_q, int n_kv, int n_heads, int topk, int causal, float* target,
                                    void* stream);
 
+/* ---- Dense indexer loss statistics (dsa_indexer_loss_coeff > 0 with
+ * dsa_indexer_use_sparse_loss = False, the reference default, src/mcore_bridge/config/
+ * model_config.py:204-205: megatron-core's compute_dsa_indexer_loss targets the head-summed dense
+ * attention of each query over every key of its document).  Query t's keys are the kv rows
+ * row_base[t] .. row_base[t] + row_len[t] - 1 (dsa_build_rows; a row with row_base outside kv is
+ * empty, lengths are clipped to kv).  q [total_q, n_heads, 576] bf16, kv [n_kv, 576] bf16;
+ * n_heads <= 128; any row length (no index row). ---- */
+
+/* lse[t, h] = ln sum_j exp(sm_scale * q[t,h] . kv[row_base[t] + j]) over the query's keys (-inf
+ * for an empty row), [total_q, n_heads] fp32. */
+int dsa_dense_attention_lse(const void* q, const void* kv, const int32_t* row_base, const int32_t* row_len,
+                            int total_q, int n_kv, int n_heads, int d_qk, float sm_scale, float* lse, void* stream);
+
+/* target[t, j] = (1/H) sum_h exp(sm_scale * q[t,h] . kv[row_base[t] + j] - lse[t,h]) for j <
+ * min(row_len[t], pitch), 0 for the other j < pitch; [total_q, pitch] fp32, lse from
+ * dsa_dense_attention_lse. */
+int dsa_dense_attention_target(const void* q, const void* kv, const float* lse, const int32_t* row_base,
+                               const int32_t* row_len, int total_q, int n_kv, int n_heads, int d_qk, int pitch,
+                               float sm_scale, float* target, void* stream);
+
 /* Per-query KL of the sparse indexer loss and its gradient: with pI = softmax of index_sel over
  * the valid slots of row t, kl[t] = sum_j target (ln(target + 1e-10) - ln(pI + 1e-10)) and
  * d_index[t, j] = grad_scale * d kl[t] / d index_sel[t, j] (0 at invalid slots).  The loss of the

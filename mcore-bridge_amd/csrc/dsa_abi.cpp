@@ -594,6 +594,50 @@ int dsa_indexer_kl_target(const void* q, const void* kv, const int32_t* idx, con
   return dsa::launch_indexer_kl_target(p, as_stream(stream));
 }
 
+static int dense_kl_params(const void* q, const void* kv, const int32_t* row_base, const int32_t* row_len, int total_q,
+                    int n_kv, int n_heads, int d_qk, float sm_scale, dsa::DenseKlParams& p) {
+  if (total_q < 0 || n_kv < 0 || n_heads < 1 || !std::isfinite(sm_scale) || !(sm_scale > 0.f))
+    return DSA_ERR_INVALID_ARG;
+  if (d_qk != kDqk) return DSA_ERR_UNSUPPORTED;
+  if (n_heads > 128) return DSA_ERR_UNSUPPORTED;
+  if (total_q == 0) return DSA_OK;
+  if (!q || !kv || !row_base || !row_len || n_kv < 1) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(kv)) return DSA_ERR_INVALID_ARG;
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.kv = static_cast<const dsa::bf16_t*>(kv);
+  p.row_base = row_base; p.row_len = row_len;
+  p.total_q = total_q; p.n_heads = n_heads; p.n_kv = n_kv;
+  p.q_stride_t = (int64_t)n_heads * kDqk;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  return DSA_OK;
+}
+
+int dsa_dense_attention_lse(const void* q, const void* kv, const int32_t* row_base, const int32_t* row_len,
+                            int total_q, int n_kv, int n_heads, int d_qk, float sm_scale, float* lse, void* stream) {
+  dsa::DenseKlParams p{};
+  const int rc = dense_kl_params(q, kv, row_base, row_len, total_q, n_kv, n_heads, d_qk, sm_scale, p);
+  if (rc != DSA_OK || total_q == 0) return rc;
+  if (!lse) return DSA_ERR_INVALID_ARG;
+  p.lse_out = lse;
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
+  return dsa::launch_dense_lse(p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+int dsa_dense_attention_target(const void* q, const void* kv, const float* lse, const int32_t* row_base,
+                               const int32_t* row_len, int total_q, int n_kv, int n_heads, int d_qk, int pitch,
+                               float sm_scale, float* target, void* stream) {
+  dsa::DenseKlParams p{};
+  if (pitch < 1) return DSA_ERR_INVALID_ARG;
+  const int rc = dense_kl_params(q, kv, row_base, row_len, total_q, n_kv, n_heads, d_qk, sm_scale, p);
+  if (rc != DSA_OK || total_q == 0) return rc;
+  if (!lse || !target) return DSA_ERR_INVALID_ARG;
+  p.lse = lse; p.target = target; p.pitch = pitch; p.target_stride = pitch;
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
+  return dsa::launch_dense_target(p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
 int dsa_indexer_kl_target_from_bwd(const void* bwd_workspace, size_t bwd_workspace_bytes, const int32_t* idx,
                                    int total_q, int n_kv, int n_heads, int topk, int causal, float* target,
                                    void* stream) {

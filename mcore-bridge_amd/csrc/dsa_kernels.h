@@ -128,6 +128,22 @@ struct KlTargetParams {
   int n_xcd;            // XCDs of the device (xcd_remap / xcd_grid)
 };
 
+// Dense attention statistics of the dense indexer loss (dsa_dense_kl.hip): query t's keys are
+// the kv rows row_base[t] .. row_base[t] + row_len[t] - 1.
+struct DenseKlParams {
+  const bf16_t* q;          // [total_q, n_heads, 576], token stride q_stride_t
+  const bf16_t* kv;         // [n_kv, 576]
+  const int32_t* row_base;  // [total_q]
+  const int32_t* row_len;   // [total_q]
+  const float* lse;         // target: [total_q, n_heads] natural-log dense LSE
+  float* lse_out;           // LSE: [total_q, n_heads]
+  float* target;            // target: [total_q, pitch] (row stride target_stride)
+  int total_q, n_heads, n_kv, pitch;
+  int64_t q_stride_t, target_stride;
+  float scale_log2;         // softmax scale * log2(e)
+  int n_xcd;                // XCDs of the device (xcd_remap / xcd_grid)
+};
+
 struct KlFromPParams {
   const bf16_t* p_stage;  // the sparse backward's staged P tiles [total_q][topk_pad / 32][n_heads][32]
   const int32_t* idx;     // [total_q, topk]
@@ -203,6 +219,8 @@ int launch_indexer_prologue_bwd(const PrologueBwdParams& p, hipStream_t stream);
 int launch_indexer_kl_target(const KlTargetParams& p, hipStream_t stream);
 int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
 int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream);
+int launch_dense_lse(const DenseKlParams& p, hipStream_t stream);
+int launch_dense_target(const DenseKlParams& p, hipStream_t stream);
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream);
 // Key-major order of the selected (query, slot) pairs, ascending in query inside each key

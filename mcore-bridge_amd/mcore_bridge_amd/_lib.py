@@ -79,6 +79,10 @@ SIGNATURES = {
                                       c_float, c_int, c_void_p, c_void_p]),
     "dsa_indexer_kl_target_from_bwd": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                                c_void_p, c_void_p]),
+    "dsa_dense_attention_lse": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float,
+                                        c_void_p, c_void_p]),
+    "dsa_dense_attention_target": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                           c_int, c_int, c_float, c_void_p, c_void_p]),
     "dsa_indexer_kl_loss": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "dsa_indexer_selected_scores": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

@@ -736,7 +736,6 @@ torch.library.register_autograd("dsa_amd::indexer_selected_scores", _sel_backwar
 # dense indexer loss), through the kernels above in blocks of key columns
 # --------------------------------------------------------------------------------------
 SCORES_BWD_COLS = 4096   # key columns per call of the selected-slot score backward
-ATTN_COLS = 8192         # key columns per call of the sparse forward / KL target
 
 
 def dense_row_indices(row_base: Tensor, row_len: Tensor, start: int, width: int) -> Tensor:
@@ -786,18 +785,30 @@ def _isc_backward(ctx, d_scores):
 torch.library.register_autograd("dsa_amd::indexer_scores", _isc_backward, setup_context=_isc_setup)
 
 
+def _check_dense(q: Tensor, kv: Tensor, row_base: Tensor, row_len: Tensor) -> None:
+    _require_gpu(q, kv, row_base, row_len)
+    _require(q.dim() == 3 and q.shape[-1] == D_QK, f"q must be [T, H, {D_QK}]")
+    _require(kv.dim() == 2 and kv.shape[-1] == D_QK, f"kv must be [N, {D_QK}]")
+    _require(q.dtype == torch.bfloat16 and kv.dtype == torch.bfloat16, "q and kv must be bf16")
+    _require(row_base.shape == (q.shape[0],) and row_len.shape == (q.shape[0],), "row_base / row_len must be [T]")
+
+
 def dense_attention_lse(q: Tensor, kv: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
                         sm_scale: float) -> Tensor:
-    """``[T, H]`` natural-log LSE of every query's dense attention over all of its visible keys
-    (the sparse forward over blocks of ``ATTN_COLS`` dense key columns, combined by logaddexp;
-    ``-inf`` for every query when no row has a key)."""
-    if max_row_len <= 0:
-        return torch.full((q.shape[0], q.shape[1]), float("-inf"), dtype=torch.float32, device=q.device)
-    lse = None
-    for c0 in range(0, max_row_len, ATTN_COLS):
-        idx = dense_row_indices(row_base, row_len, c0, min(ATTN_COLS, max_row_len - c0))
-        _, l = sparse_mla_fwd(q, kv, idx, sm_scale, False)
-        lse = l if lse is None else torch.logaddexp(lse, l)
+    """``[T, H]`` natural-log LSE of every query's dense attention over all of its visible keys, the
+    kv rows ``row_base[t] .. row_base[t] + row_len[t] - 1`` (``dsa_dense_attention_lse``: the QK
+    product alone over each contiguous key range, no index rows; ``-inf`` for an empty row).
+    ``max_row_len`` is part of the call contract; the kernel reads the rows themselves."""
+    _check_dense(q, kv, row_base, row_len)
+    q, kv = q.contiguous(), kv.contiguous()
+    T, H, _ = q.shape
+    lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    if T == 0 or max_row_len <= 0:
+        return lse.fill_(float("-inf"))
+    rb, rl = row_base.to(torch.int32).contiguous(), row_len.to(torch.int32).contiguous()
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_dense_attention_lse", _p(q), _p(kv), _p(rb), _p(rl), T, kv.shape[0], H, D_QK,
+                  float(sm_scale), _p(lse), _stream(q.device))
     return lse
 
 
@@ -805,11 +816,17 @@ def dense_attention_target(q: Tensor, kv: Tensor, lse: Tensor, row_base: Tensor,
                            pitch: int, sm_scale: float) -> Tensor:
     """Target of the dense indexer loss, ``[T, pitch]`` fp32: column j = key ``row_base[t] + j`` holds
     ``(1/H) sum_h exp(sm_scale * q[t,h] . kv[key] - lse[t,h])`` (0 past the row), the head-mean of the
-    dense attention probabilities (``lse`` from ``dense_attention_lse``)."""
-    T = q.shape[0]
-    tgt = torch.zeros(T, pitch, dtype=torch.float32, device=q.device)
-    for c0 in range(0, max(max_row_len, 0), ATTN_COLS):
-        width = min(ATTN_COLS, max_row_len - c0)
-        idx = dense_row_indices(row_base, row_len, c0, width)
-        tgt[:, c0:c0 + width] = indexer_kl_target(q, kv, idx, lse, sm_scale, False)
+    dense attention probabilities (``lse`` from ``dense_attention_lse``; ``dsa_dense_attention_target``)."""
+    _check_dense(q, kv, row_base, row_len)
+    q, kv = q.contiguous(), kv.contiguous()
+    T, H, _ = q.shape
+    _require(lse.shape == (T, H), "lse must be [T, H]")
+    tgt = torch.empty(T, pitch, dtype=torch.float32, device=q.device)
+    if T == 0 or max_row_len <= 0:
+        return tgt.zero_()
+    rb, rl = row_base.to(torch.int32).contiguous(), row_len.to(torch.int32).contiguous()
+    lse = lse.to(torch.float32).contiguous()
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_dense_attention_target", _p(q), _p(kv), _p(lse), _p(rb), _p(rl), T, kv.shape[0], H, D_QK,
+                  int(pitch), float(sm_scale), _p(tgt), _stream(q.device))
     return tgt

@@ -598,12 +598,11 @@ def test_dense_indexer_loss_matches_float64_autograd(cols, monkeypatch):
     """The dense indexer loss (the reference default, dsa_indexer_use_sparse_loss=False) over packed
     documents: loss and gradients of q_idx, k_idx, w against float64 autograd through the oracle's
     dense scores and compute_dsa_indexer_loss(sparse_loss=False), document by document (the
-    reference's mean over tokens); ``cols`` shrinks every column block of the dense path."""
+    reference's mean over tokens); ``cols`` shrinks the column blocks of the dense score backward."""
     print(f"[dense indexer loss] cols={cols}", flush=True)
     from mcore_bridge_amd.dsa import indexer_kl_loss_dense
     if cols:
         monkeypatch.setattr(ops, "SCORES_BWD_COLS", cols)
-        monkeypatch.setattr(ops, "ATTN_COLS", cols)
     g = torch.Generator().manual_seed(41)
     cu = [0, 130, 300, 301, 420]
     T, H, Hi, coeff = cu[-1], 16, 64, 0.4
