@@ -20,6 +20,8 @@ The line also carries:
                       e4m3 key cache, and the graph-replayed step;
   "indexer_prologue"  the fused producer of the indexer's inputs at the cfg3 token count (HBM);
   "indexer_kl"        the sparse indexer KL loss and the indexer-score backward at cfg3;
+  "indexer_kl_dense"  the dense indexer KL loss (the reference default) at cfg3: its LSE and target
+                      kernels and the whole loss forward + backward;
   "v4"                the DeepSeek-V4 CSA layer core (sink attention fwd + bwd, 512-wide K = V) at
                       T = 16384, H = 128, window 128 + top-512 compressed entries;
   "cpu_baseline"      the oracle's reference-shaped fp32 compositions timed on the host per config
@@ -415,6 +417,40 @@ def _time_ms(torch, fn, reps: int, warm: int = 2, windows: int = 3):
 PEAK_FP8_TFLOPS = 5000.0
 
 
+def indexer_kl_dense_leg(torch, dev, q, kv, qi, ki, w, cu_t, max_seqlen: int, scale: float, npairs: int,
+                         reps: int = 5):
+    """Dense indexer KL loss at the cfg3 size (the reference default: dsa_indexer_loss_coeff with
+    dsa_indexer_use_sparse_loss = False, model_config.py:204-205; the target is the head-summed
+    dense attention of each query over EVERY visible key): the dense LSE and target kernels alone,
+    then the whole loss forward + backward through autograd (LSE, target, dense index scores, KL
+    rows, score backward).  LSE and target each cost 2*576*H flops per visible pair (QK only)."""
+    from mcore_bridge_amd import ops, dsa
+    T, H, _ = q.shape
+    base, ln = ops.build_rows(cu_t, T, True)
+    pitch = max(4, (max_seqlen + 3) // 4 * 4)
+    lse = ops.dense_attention_lse(q, kv, base, ln, max_seqlen, scale)
+    t_lse = _time_ms(torch, lambda: ops.dense_attention_lse(q, kv, base, ln, max_seqlen, scale), reps)
+    t_tgt = _time_ms(torch, lambda: ops.dense_attention_target(q, kv, lse, base, ln, max_seqlen, pitch, scale), reps)
+    qd, kd, wd = (x.detach().requires_grad_() for x in (qi, ki, w))
+    loss_val = [0.0]
+
+    def loss_step():
+        loss = dsa.indexer_kl_loss_dense(q, kv, qd, kd, wd, scale, 1.0, cu_t, max_seqlen)
+        loss.backward()
+        loss_val[0] = loss
+
+    t_all = _time_ms(torch, loss_step, reps)
+    fl = 2 * 576 * H * npairs
+    tf_lse = fl / (t_lse * 1e-3) / 1e12
+    return {"workload": f"dense indexer KL loss at cfg3 size: T={T} in 4 causal documents, H={H}, Hi={qi.shape[1]}, "
+                        f"{npairs} visible (query, key) pairs",
+            "lse_ms": round(t_lse, 3), "target_ms": round(t_tgt, 3), "loss_fwd_bwd_ms": round(t_all, 3),
+            "lse_tflops": round(tf_lse, 1), "target_tflops": round(fl / (t_tgt * 1e-3) / 1e12, 1),
+            "loss": round(float(loss_val[0].detach().item()), 6),
+            "roofline": {"bound": "mfma", "kernel": "dense_lse_kernel", "achieved": round(tf_lse, 1),
+                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf_lse / PEAK_BF16_TFLOPS, 4)}}
+
+
 def v4_leg(torch, dev, reps: int = 5):
     """DeepSeek-V4 compressed sparse attention layer core (reference deepseek_v4.py:61-328; the core
     attention of its CSA layers) on the DSA kernels: one document of T = 16384 tokens, H = 128 heads
@@ -748,6 +784,10 @@ def main():
         res["indexer_kl"] = indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale, nsel, ws)
         del idx, lse
         print(f"[bench] indexer KL leg done: {res['indexer_kl']['total_ms']} ms", file=sys.stderr, flush=True)
+        res["indexer_kl_dense"] = indexer_kl_dense_leg(torch, dev, q, kv, qi, ki, w, cu_t, max_seqlen, scale,
+                                                       W.n_pairs(cu))
+        print(f"[bench] dense indexer KL leg done: {res['indexer_kl_dense']['loss_fwd_bwd_ms']} ms", file=sys.stderr,
+              flush=True)
     if not args.no_decode:
         res["v4"] = v4_leg(torch, dev)
         print(f"[bench] v4 leg done: {res['v4']['ms']} ms", file=sys.stderr, flush=True)

@@ -325,6 +325,22 @@ int dsa_dense_attention_target(const void* q, const void* kv, const float* lse, 
                                const int32_t* row_len, int total_q, int n_kv, int n_heads, int d_qk, int pitch,
                                float sm_scale, float* target, void* stream);
 
+/* Backward of the dense index scores (the [B, S, S] scores of fused_qk_topk_naive, patcher.py:338-376,
+ * over every visible key, through which the dense indexer loss trains the indexer; the reference
+ * runs torch autograd through them): with I[t, j] = sum_h w[t,h] relu(q[t,h] . k[row_base[t] + j])
+ * and d_scores [total_q, pitch] = dL/dI (columns j >= min(row_len[t], pitch) are ignored),
+ *   dq[t,h] = w[t,h] sum_j dI 1[z>0] k,   dw[t,h] = sum_j dI relu(z),
+ *   dk[s]   = sum over (t, h) seeing s of dI w[t,h] 1[z>0] q[t,h]                     (all fp32).
+ * Rows as for dsa_dense_attention_lse (k [n_k, 128]), and monotone: row_base[t] and row_base[t] +
+ * row_len[t] nondecreasing in t (what dsa_build_rows and dsa_build_decode_rows give).  q
+ * [total_q, n_heads, 128] bf16, w [total_q, n_heads] fp32; n_heads <= 64.  Deterministic (no
+ * atomics: per-chunk partial dk tiles in the workspace, summed in a fixed order). */
+size_t dsa_dense_indexer_scores_bwd_workspace_size(int total_q, int n_k);
+int dsa_dense_indexer_scores_bwd(const void* q, const void* k, const float* w, const int32_t* row_base,
+                                 const int32_t* row_len, int total_q, int n_k, int n_heads, int head_dim,
+                                 const float* d_scores, int pitch, float* dq, float* dw, float* dk, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* Per-query KL of the sparse indexer loss and its gradient: with pI = softmax of index_sel over
  * the valid slots of row t, kl[t] = sum_j target (ln(target + 1e-10) - ln(pI + 1e-10)) and
  * d_index[t, j] = grad_scale * d kl[t] / d index_sel[t, j] (0 at invalid slots).  The loss of the

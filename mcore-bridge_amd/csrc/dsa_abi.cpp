@@ -695,6 +695,44 @@ size_t dsa_indexer_scores_bwd_workspace_size(int total_q, int n_k, int topk) {
   return idx_bwd_layout(total_q, n_k, topk).total;
 }
 
+static size_t dense_scores_bwd_chunks(int total_q) {
+  return ((size_t)total_q + dsa::kDenseQChunk - 1) / dsa::kDenseQChunk;
+}
+
+size_t dsa_dense_indexer_scores_bwd_workspace_size(int total_q, int n_k) {
+  if (total_q <= 0 || n_k <= 0) return 0;
+  const size_t tiles = ((size_t)n_k + dsa::kDenseDkKeys - 1) / dsa::kDenseDkKeys;
+  return align_up(tiles * dense_scores_bwd_chunks(total_q) * dsa::kDenseDkKeys * 128 * sizeof(float));
+}
+
+int dsa_dense_indexer_scores_bwd(const void* q, const void* k, const float* w, const int32_t* row_base,
+                                 const int32_t* row_len, int total_q, int n_k, int n_heads, int head_dim,
+                                 const float* d_scores, int pitch, float* dq, float* dw, float* dk, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (total_q < 0 || n_k < 1 || n_heads < 1 || pitch < 1) return DSA_ERR_INVALID_ARG;
+  if (head_dim != 128 || n_heads > 64) return DSA_ERR_UNSUPPORTED;
+  if (!dk) return DSA_ERR_INVALID_ARG;
+  if (total_q == 0) {   // no rows: dk = 0 (empty sums); dq and dw are empty
+    DSA_CHECK_DEVICE(dev0);
+    return dsa::launch_zero_rows(dk, n_k, head_dim, head_dim, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+  }
+  if (!q || !k || !w || !row_base || !row_len || !d_scores || !dq || !dw) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(dq) || !aligned16(dk)) return DSA_ERR_INVALID_ARG;
+  const size_t need = dsa_dense_indexer_scores_bwd_workspace_size(total_q, n_k);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  dsa::DenseIdxBwdParams p{};
+  p.q = static_cast<const dsa::bf16_t*>(q);
+  p.k = static_cast<const dsa::bf16_t*>(k);
+  p.w = w; p.row_base = row_base; p.row_len = row_len; p.d_scores = d_scores;
+  p.dq = dq; p.dw = dw; p.dk = dk; p.dk_part = static_cast<float*>(workspace);
+  p.total_q = total_q; p.n_heads = n_heads; p.n_k = n_k; p.pitch = pitch;
+  p.n_tiles = (n_k + dsa::kDenseDkKeys - 1) / dsa::kDenseDkKeys;
+  p.max_chunks = (int)dense_scores_bwd_chunks(total_q);
+  DSA_CHECK_DEVICE(dev);
+  p.n_xcd = dev.n_xcd;
+  return dsa::launch_dense_scores_bwd(p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
 int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const int32_t* idx, const float* d_index,
                            int total_q, int n_k, int n_heads, int head_dim, int topk, int causal, float* dq,
                            float* dw, float* dk, void* workspace, size_t workspace_bytes, void* stream) {

@@ -461,6 +461,426 @@ __global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stag
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// Dense score backward: the gradients of I[t, j] = sum_h w relu(q[t,h] . k[row_base[t] + j]) over
+// EVERY key of each row (the dense indexer loss backpropagates through the [T, pitch] scores).  A
+// row's keys are one contiguous range, so neither kernel needs index rows or a pair order, and dk
+// needs no staged per-pair rows:
+//   dense_scores_dq_kernel  query-major (one workgroup per query, wave w takes blocks w, w + 4, ..
+//       through its own double-buffered K tile and dI slot): Z^T = K . Q^T (lane = head) gives
+//       G^T = dI 1[z>0] and dw += dI relu(z); dq^T += K^T . G^T; dq = w * the sum over the waves.
+//   dense_scores_dk_kernel  key-major: a workgroup holds 128 consecutive keys (wave w: 32, their K^T
+//       fragments in registers for the whole run) and streams the queries that see them, each
+//       query's Q rows, weights and dI through a double-buffered LDS slot: Z = Q . K^T (lane = key)
+//       gives G = dI w 1[z>0]; dk^T += Q^T . G (Q^T by transposing LDS reads).  A key tile's
+//       queries are cut into chunks of kDenseQChunk, one workgroup each, so no workgroup runs a
+//       whole document's queries; the chunks' partial dk tiles are summed in chunk order by
+//       dense_dk_reduce_kernel (the same bits every run).
+// Rows are monotone (row_base and row_base + row_len nondecreasing in t), so the queries that see
+// a key tile are one range, found by binary search.
+// ------------------------------------------------------------------------------------------
+namespace {
+
+// Row t's keys clipped to k and to the score pitch: [base, base + len).
+DSA_DEV void dense_row(const DenseIdxBwdParams& p, int t, int& base, int& len) {
+  base = p.row_base[t];
+  len = p.row_len[t];
+  if (base < 0 || base >= p.n_k || len < 0) len = 0;
+  else len = min(min(len, p.n_k - base), p.pitch);
+}
+
+// Queries [lo, hi) that may see a key of key tile `tile`: lo = the first row ending past the
+// tile's first key, hi = the first row starting past its last key.
+DSA_DEV void dense_tile_queries(const DenseIdxBwdParams& p, int tile, int& lo, int& hi) {
+  const int s0 = tile * kDenseDkKeys;
+  const int s1 = min(s0 + kDenseDkKeys, p.n_k) - 1;
+  int a = 0, b = p.total_q;
+  while (a < b) {
+    const int m = (a + b) >> 1;
+    if (p.row_base[m] + p.row_len[m] > s0) b = m; else a = m + 1;
+  }
+  lo = a;
+  b = p.total_q;
+  while (a < b) {
+    const int m = (a + b) >> 1;
+    if (p.row_base[m] > s1) b = m; else a = m + 1;
+  }
+  hi = a;
+}
+
+struct DenseDqSmem {
+  union {
+    struct {
+      char tile[4][2][kKTile];   // per-wave double-buffered K tiles
+      float di[4][2][64];        // per-wave dI of the block (64 copied, 32 used)
+    };
+    float part[4][kHi][68];      // epilogue: per-wave dq partials of 64 dims
+  };
+  float dwp[4][kHi];
+};
+
+struct DenseDkSmem {
+  char q[2][kHi * kRowB];          // Q[t] rows (head r, 16-byte chunk c at slot c ^ swz(r))
+  float w[2][kHi];
+  float di[2][kDenseDkKeys];       // dI[t, s - row_base[t]] of the tile's keys (masked in-register)
+  int32_t rb[kDenseQChunk];        // row_base / row_len of the work item's queries
+  int32_t rl[kDenseQChunk];
+};
+
+}  // namespace
+
+__global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdParams p) {
+  __shared__ __attribute__((aligned(256))) DenseDqSmem sm;
+  const int t = xcd_remap(blockIdx.x, p.n_xcd);
+  if (t >= p.total_q) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hb = lane >> 5, hl = lane & 31;
+  int base, len;
+  dense_row(p, t, base, len);
+  const int nblk = (len + 31) / 32;
+  // Q fragments (B of Z^T): head 32 mh + hl, dims 16 ks + 8 hb .. +7
+  const bf16_t* qt_row = p.q + (int64_t)t * p.n_heads * kDi;
+  u32x4 qf[2][8];
+#pragma unroll
+  for (int mh = 0; mh < 2; ++mh) {
+    const int head = 32 * mh + hl;
+    const bool ok = head < p.n_heads;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const u32x4 v = gload16(qt_row + (ok ? head : 0) * kDi + 16 * ks + 8 * hb);
+      qf[mh][ks] = ok ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+  wait_vmcnt0();   // compiler-visible loads retired before the asynchronous copies start
+  const float* drow = p.d_scores + (int64_t)t * p.pitch;
+  const uint32_t tiles = lds_addr(sm.tile[wave][0]);
+  const uint32_t dis = lds_addr(sm.di[wave][0]);
+  // block blk into slot `slot`: K rows of keys base + 32 blk + kk (past the row: its last key,
+  // masked), copy r moving keys 4r .. 4r+3 (lane l: slot l & 15 of key 4r + l/16 from chunk
+  // (l & 15) ^ swz(key)); then 64 dI values from column 32 blk (clamped to the row's pitch)
+  auto gather = [&](int slot, int blk) {
+    const int kk0 = lane >> 4;
+    const uint32_t sl = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int kk = 4 * r + kk0;
+      const int j = min(32 * blk + kk, len - 1);
+      const char* src = reinterpret_cast<const char*>(p.k) + (int64_t)(base + j) * kRowB + 16u * (sl ^ swz(kk));
+      async_copy16_unordered(src, tiles + slot * kKTile + 1024u * r);
+    }
+    async_copy4_unordered(drow + min(32 * blk + lane, p.pitch - 1), dis + slot * 256u);
+  };
+  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz(hl));
+  uint32_t troff[2][2][2];
+  {
+    const int g = lane >> 4, gi = lane & 15;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int m1 = 0; m1 < 2; ++m1) {
+          const uint32_t key = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
+          const uint32_t cp = 2 * (g & 1) + ((gi >> 1) & 1);
+          troff[a][h][m1] = key * kRowB + 16u * ((4u * m1) ^ cp ^ swz(key)) + 8u * (gi & 1);
+        }
+  }
+  f32x16 dqa[4][2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int n = 0; n < 2; ++n) dqa[m][n] = f32x16{};
+  float dwacc[2] = {0.f, 0.f};
+
+  if (wave < nblk) gather(0, wave);
+  int it = 0;
+  for (int blk = wave; blk < nblk; blk += 4, ++it) {
+    const int slot = it & 1;
+    const uint32_t tb = tiles + slot * kKTile;
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    if (blk + 4 < nblk) gather(slot ^ 1, blk + 4);
+    // ---- Z^T = K . Q^T (lane = head, rows = keys (i/4)*8 + 4 hb + i%4)
+    f32x16 zt[2];
+    {
+      uint32_t zb = tb + zoff;
+      asm volatile("" : "+v"(zb));
+      u32x4 kf[kPreI];
+#pragma unroll
+      for (int i = 0; i < kPreI; ++i) kf[i] = lds_load16(lds_ptr(zb ^ (32u * i)));
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const u32x4 cur = kf[ks % kPreI];
+        if (ks + kPreI < 8) kf[ks % kPreI] = lds_load16(lds_ptr(zb ^ (32u * (ks + kPreI))));
+        if (ks == 0) {
+          mfma32x32x16_cV_first(zt[0], cur, qf[0][0]);
+          mfma32x32x16_cV_first(zt[1], cur, qf[1][0]);
+        } else {
+          mfma32x32x16_cV(zt[0], cur, qf[0][ks]);
+          mfma32x32x16_cV(zt[1], cur, qf[1][ks]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    mfma_acc_drain();
+    // ---- G^T = dI 1[z>0] (0 past the row) and dw
+    const int nvalid = len - 32 * blk;
+    float dr[16];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sm.di[wave][slot][gq * 8 + 4 * hb]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dr[4 * gq + e] = gq * 8 + 4 * hb + e < nvalid ? v[e] : 0.f;
+    }
+    u32x4 gt[2][2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      float dws = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const float a0 = zt[n][i] > 0.f ? dr[i] : 0.f, a1 = zt[n][i + 1] > 0.f ? dr[i + 1] : 0.f;
+        gt[n][i >> 3][(i & 7) >> 1] = pack_bf16x2(a0, a1);
+        dws = __builtin_fmaf(dr[i], relu_bits(zt[n][i]), dws);
+        dws = __builtin_fmaf(dr[i + 1], relu_bits(zt[n][i + 1]), dws);
+      }
+      dwacc[n] += dws;
+    }
+    // ---- dq^T[dims x heads] += K^T . G^T
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        const uint32_t o = 128u * (mm >> 1);
+        const u32x2 lo = lds_read_tr16(tb + troff[a][0][mm & 1] + o);
+        const u32x2 hi = lds_read_tr16(tb + troff[a][1][mm & 1] + o);
+        const u32x4 kt = u32x4{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int n = 0; n < 2; ++n) mfma32x32x16_cA(dqa[mm][n], kt, gt[n][a]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  }
+
+  // ---- epilogue: dw and dq summed over the four waves (the tiles' union is reused)
+  mfma_acc_drain();
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const float v = xor32_sum(dwacc[n]);
+    if (hb == 0) sm.dwp[wave][32 * n + hl] = v;
+  }
+  __syncthreads();
+  const float* wrow = p.w + (int64_t)t * p.n_heads;
+  const int h_red = threadIdx.x >> 2;
+  const float w_red = h_red < p.n_heads ? wrow[h_red] : 0.f;
+  float* dq_row = p.dq + ((int64_t)t * p.n_heads + h_red) * kDi;
+#pragma unroll
+  for (int ph = 0; ph < 2; ++ph) {
+#pragma unroll
+    for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const f32x16& a = dqa[2 * ph + m2][n];
+          *reinterpret_cast<f32x4*>(&sm.part[wave][32 * n + hl][32 * m2 + 8 * gq + 4 * hb]) =
+              f32x4{a[4 * gq], a[4 * gq + 1], a[4 * gq + 2], a[4 * gq + 3]};
+        }
+    __syncthreads();
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int dd = 16 * (threadIdx.x & 3) + 4 * q4;
+      f32x4 sacc = *reinterpret_cast<const f32x4*>(&sm.part[0][h_red][dd]);
+#pragma unroll
+      for (int w = 1; w < 4; ++w) sacc += *reinterpret_cast<const f32x4*>(&sm.part[w][h_red][dd]);
+      if (h_red < p.n_heads) *reinterpret_cast<f32x4*>(dq_row + 64 * ph + dd) = sacc * w_red;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < p.n_heads) {
+    const int h = threadIdx.x;
+    p.dw[(int64_t)t * p.n_heads + h] = sm.dwp[0][h] + sm.dwp[1][h] + sm.dwp[2][h] + sm.dwp[3][h];
+  }
+}
+
+// Work item (key tile, query chunk): chunk-major ids, so the workgroups running at once share
+// their queries' rows through the caches.
+__global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdParams p) {
+  __shared__ __attribute__((aligned(256))) DenseDkSmem sm;
+  const int item = xcd_remap(blockIdx.x, p.n_xcd);
+  if (item >= p.n_tiles * p.max_chunks) return;
+  const int chunk = item / p.n_tiles, tile = item - chunk * p.n_tiles;
+  int lo, hi;
+  dense_tile_queries(p, tile, lo, hi);
+  const int t_begin = lo + chunk * kDenseQChunk;
+  if (t_begin >= hi) return;   // the tile's queries end before this chunk: no partial (the reduce knows)
+  const int nq = min(kDenseQChunk, hi - t_begin);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hb = lane >> 5, hl = lane & 31;
+  const int s0 = tile * kDenseDkKeys;
+  const int s = s0 + 32 * wave + hl;                     // this lane's key (Z column)
+  // K^T fragments (B of Z = Q . K^T): key s, dims 16 ks + 8 hb .. +7
+  u32x4 kf[8];
+  {
+    const bf16_t* krow = p.k + (int64_t)min(s, p.n_k - 1) * kDi + 8 * hb;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kf[ks] = gload16(krow + 16 * ks);
+  }
+  // the work item's row descriptors
+  for (int i = threadIdx.x; i < nq; i += 256) {
+    int b, l;
+    dense_row(p, t_begin + i, b, l);
+    sm.rb[i] = b;
+    sm.rl[i] = l;
+  }
+  wait_vmcnt0();
+  __syncthreads();
+  const uint32_t qs0 = lds_addr(sm.q[0]), ws0 = lds_addr(sm.w[0]), ds0 = lds_addr(sm.di[0]);
+  // query i's rows into slot `slot`: Q (16 copies of 4 head rows, 4 per wave; rows past n_heads
+  // re-read head 0, never used), weights (wave 1), the tile's 128 dI columns (wave 0, two copies;
+  // columns outside the row clamped into it and masked by the caller)
+  auto issue = [&](int slot, int i) {
+    const int tq = t_begin + i;
+    const bf16_t* qrow = p.q + (int64_t)tq * p.n_heads * kDi;
+    const uint32_t sl = lane & 15;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int r = 4 * wave + r4;
+      const int h = 4 * r + (lane >> 4);
+      const char* src = reinterpret_cast<const char*>(qrow + (h < p.n_heads ? h : 0) * kDi) + 16u * (sl ^ swz(h));
+      async_copy16_unordered(src, qs0 + slot * (kHi * kRowB) + 1024u * r);
+    }
+    if (wave == 1) async_copy4_unordered(p.w + (int64_t)tq * p.n_heads + min(lane, p.n_heads - 1), ws0 + slot * 256u);
+    if (wave == 0) {
+      const float* drow = p.d_scores + (int64_t)tq * p.pitch;
+      const int base_q = sm.rb[i];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int j = min(max(s0 + 64 * c + lane - base_q, 0), p.pitch - 1);
+        async_copy4_unordered(drow + j, ds0 + slot * 512u + 256u * c);
+      }
+    }
+  };
+  // Z operand (A = Q rows): head 32 n + hl, chunk 2 ks + hb; transposing reads of Q^T (A of dk^T)
+  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz(hl));
+  uint32_t troff[2][2][2];
+  {
+    const int g = lane >> 4, gi = lane & 15;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int m1 = 0; m1 < 2; ++m1) {
+          const uint32_t r = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
+          const uint32_t cp = 2 * (g & 1) + ((gi >> 1) & 1);
+          troff[a][h][m1] = r * kRowB + 16u * ((4u * m1) ^ cp ^ swz(r)) + 8u * (gi & 1);
+        }
+  }
+  f32x16 dka[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) dka[m] = f32x16{};
+
+  issue(0, 0);
+  for (int i = 0; i < nq; ++i) {
+    const int slot = i & 1;
+    const int base_t = sm.rb[i], len_t = sm.rl[i];
+    wait_vmcnt<0>();
+    __syncthreads();   // query i's rows are in; every wave is done with slot ^ 1
+    if (i + 1 < nq) issue(slot ^ 1, i + 1);
+    const uint32_t qb = qs0 + slot * (kHi * kRowB);
+    // ---- Z[heads x keys] = Q . K^T (lane = key s, element i = head 32 n + (i/4)*8 + 4 hb + i%4)
+    f32x16 z[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      uint32_t zb = qb + n * kKTile + zoff;
+      asm volatile("" : "+v"(zb));
+      u32x4 qa[kPreI];
+#pragma unroll
+      for (int u = 0; u < kPreI; ++u) qa[u] = lds_load16(lds_ptr(zb ^ (32u * u)));
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const u32x4 cur = qa[ks % kPreI];
+        if (ks + kPreI < 8) qa[ks % kPreI] = lds_load16(lds_ptr(zb ^ (32u * (ks + kPreI))));
+        if (ks == 0) mfma32x32x16_cV_first(z[n], cur, kf[0]);
+        else mfma32x32x16_cV(z[n], cur, kf[ks]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    mfma_acc_drain();
+    // ---- G = dI w 1[z>0] (0 where the query does not see key s)
+    const bool vis = s >= base_t && s < base_t + len_t;
+    const float dv = vis ? sm.di[slot][32 * wave + hl] : 0.f;
+    u32x4 gz[2][2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(&sm.w[slot][32 * n + 8 * gq + 4 * hb]);
+        float g4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int h = 32 * n + 8 * gq + 4 * hb + e;
+          g4[e] = (z[n][4 * gq + e] > 0.f && h < p.n_heads) ? dv * wv[e] : 0.f;
+        }
+        gz[n][gq >> 1][2 * (gq & 1)] = pack_bf16x2(g4[0], g4[1]);
+        gz[n][gq >> 1][2 * (gq & 1) + 1] = pack_bf16x2(g4[2], g4[3]);
+      }
+    // ---- dk^T[dims x keys] += Q^T . G: four independent dim-tile chains
+#pragma unroll
+    for (int mh = 0; mh < 2; ++mh)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const uint32_t b = qb + mh * kKTile + 128u * (mt >> 1);
+          const u32x2 lo2 = lds_read_tr16(b + troff[s2][0][mt & 1]);
+          const u32x2 hi2 = lds_read_tr16(b + troff[s2][1][mt & 1]);
+          mfma32x32x16_cV(dka[mt], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, gz[mh][s2]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+  }
+  mfma_acc_drain();
+  // ---- the partial tile: key 32 w + hl, dims 32 mt + 8 q + 4 hb .. +3
+  float* part = p.dk_part + ((int64_t)tile * p.max_chunks + chunk) * (kDenseDkKeys * kDi) + (32 * wave + hl) * kDi;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f32x4*>(part + 32 * mt + 8 * q + 4 * hb) =
+          f32x4{dka[mt][4 * q], dka[mt][4 * q + 1], dka[mt][4 * q + 2], dka[mt][4 * q + 3]};
+}
+
+// dk of key tile `blockIdx.x`: the sum of its chunks' partial tiles, in chunk order.
+__global__ __launch_bounds__(256) void dense_dk_reduce_kernel(DenseIdxBwdParams p) {
+  const int tile = blockIdx.x;
+  int lo, hi;
+  dense_tile_queries(p, tile, lo, hi);
+  const int nch = min(hi > lo ? (hi - lo + kDenseQChunk - 1) / kDenseQChunk : 0, p.max_chunks);
+  const int s0 = tile * kDenseDkKeys;
+  const f32x4* part = reinterpret_cast<const f32x4*>(p.dk_part + (int64_t)tile * p.max_chunks * (kDenseDkKeys * kDi));
+  constexpr int kVec = kDenseDkKeys * kDi / 4;   // f32x4 per tile
+  for (int v = threadIdx.x; v < kVec; v += 256) {
+    const int key = v / (kDi / 4);
+    if (s0 + key >= p.n_k) break;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nch; ++c) acc += part[(int64_t)c * kVec + v];
+    *reinterpret_cast<f32x4*>(p.dk + (int64_t)(s0 + key) * kDi + 4 * (v % (kDi / 4))) = acc;
+  }
+}
+
+int launch_dense_scores_bwd(const DenseIdxBwdParams& p, hipStream_t stream) {
+  if (p.n_xcd < 1) return -1;
+  if (p.n_heads > kHi || p.n_heads < 1) return -2;
+  if (p.total_q > 0)
+    hipLaunchKernelGGL(dense_scores_dq_kernel, dim3(xcd_grid(p.total_q, p.n_xcd)), dim3(256), 0, stream, p);
+  if (p.total_q > 0 && p.n_tiles > 0)
+    hipLaunchKernelGGL(dense_scores_dk_kernel, dim3(xcd_grid(p.n_tiles * p.max_chunks, p.n_xcd)), dim3(256), 0,
+                       stream, p);
+  if (p.n_tiles > 0) hipLaunchKernelGGL(dense_dk_reduce_kernel, dim3(p.n_tiles), dim3(256), 0, stream, p);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream) {
   if (p.n_xcd < 1) return -1;
   if (p.topk > kMaxTopkIdx || p.n_heads > kHi) return -2;

@@ -204,6 +204,28 @@ struct IdxSelParams {
   int n_xcd;             // XCDs of the device (xcd_remap / xcd_grid)
 };
 
+// Dense score backward (every visible key of each query, dsa_indexer_bwd.hip): query t's keys are
+// the k rows row_base[t] .. row_base[t] + row_len[t] - 1, with row_base and row_base + row_len
+// nondecreasing in t (document rows, decode rows, compressed-entry rows).
+constexpr int kDenseDkKeys = 128;   // keys per key tile of the dk kernel
+constexpr int kDenseQChunk = 512;   // queries per work item of the dk kernel
+struct DenseIdxBwdParams {
+  const bf16_t* q;            // [total_q, n_heads, 128]
+  const bf16_t* k;            // [n_k, 128]
+  const float* w;             // [total_q, n_heads]
+  const int32_t* row_base;    // [total_q]
+  const int32_t* row_len;     // [total_q]
+  const float* d_scores;      // [total_q, pitch]: column j of row t = key row_base[t] + j
+  float* dq;                  // [total_q, n_heads, 128]
+  float* dw;                  // [total_q, n_heads]
+  float* dk;                  // [n_k, 128]
+  float* dk_part;             // [n_tiles, max_chunks, 128 keys, 128 dims] partial dk tiles
+  int total_q, n_heads, n_k, pitch;
+  int n_tiles, max_chunks;
+  int n_xcd;
+};
+int launch_dense_scores_bwd(const DenseIdxBwdParams& p, hipStream_t stream);
+
 int launch_sparse_mla_fwd(const SparseFwdParams& p, hipStream_t stream);
 // ev (nullable): 6 events recorded around the stages B4 | B1 | B2 | B3 | B5.
 int launch_sparse_mla_bwd(const SparseBwdParams& p, hipStream_t stream, hipEvent_t const* ev);

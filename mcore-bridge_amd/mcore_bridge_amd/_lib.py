@@ -83,6 +83,10 @@ SIGNATURES = {
                                         c_void_p, c_void_p]),
     "dsa_dense_attention_target": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                            c_int, c_int, c_float, c_void_p, c_void_p]),
+    "dsa_dense_indexer_scores_bwd_workspace_size": (c_size_t, [c_int, c_int]),
+    "dsa_dense_indexer_scores_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                             c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                             c_void_p]),
     "dsa_indexer_kl_loss": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "dsa_indexer_selected_scores": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

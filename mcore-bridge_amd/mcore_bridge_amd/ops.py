@@ -733,11 +733,8 @@ torch.library.register_autograd("dsa_amd::indexer_selected_scores", _sel_backwar
 
 # --------------------------------------------------------------------------------------
 # dense rows: every visible key of each query (the reference's [B, S, S] index scores and its
-# dense indexer loss), through the kernels above in blocks of key columns
+# dense indexer loss): kernels over each row's contiguous key range
 # --------------------------------------------------------------------------------------
-SCORES_BWD_COLS = 4096   # key columns per call of the selected-slot score backward
-
-
 def dense_row_indices(row_base: Tensor, row_len: Tensor, start: int, width: int) -> Tensor:
     """``[T, width]`` int32: key id ``row_base[t] + start + j`` where ``start + j < row_len[t]``, else -1
     (column block ``[start, start + width)`` of the dense rows)."""
@@ -746,24 +743,37 @@ def dense_row_indices(row_base: Tensor, row_len: Tensor, start: int, width: int)
     return torch.where(j[None] < row_len.to(torch.int32)[:, None], ids, torch.full_like(ids, -1))
 
 
+def dense_scores_bwd_workspace_bytes(T: int, N: int) -> int:
+    return int(_lib.load().dsa_dense_indexer_scores_bwd_workspace_size(T, N))
+
+
 def indexer_scores_dense_bwd(q: Tensor, k: Tensor, w: Tensor, row_base: Tensor, row_len: Tensor, max_row_len: int,
                              d_scores: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
     """Gradients of ``indexer_scores`` (bf16, head_dim 128) from ``d_scores [T, pitch]``: only columns
-    ``j < row_len[t]`` carry gradient (the rest are constants).  Runs the selected-slot score
-    backward on blocks of ``SCORES_BWD_COLS`` columns and sums them.  ``(dq, dw, dk)`` fp32 (zeros
-    when no row has a column, e.g. an empty batch)."""
-    if max_row_len <= 0:
+    ``j < row_len[t]`` carry gradient (the rest are constants).  ``dsa_dense_indexer_scores_bwd``: a
+    query-major kernel for dq / dw and a key-major one for dk over each row's contiguous keys (rows
+    monotone in t, as ``build_rows`` / ``build_decode_rows`` give).  ``(dq, dw, dk)`` fp32 (zeros when
+    no row has a column, e.g. an empty batch)."""
+    T, Hi, D = q.shape
+    N = k.shape[0]
+    if max_row_len <= 0 or T == 0:
         return (torch.zeros(q.shape, dtype=torch.float32, device=q.device),
                 torch.zeros(w.shape, dtype=torch.float32, device=q.device),
                 torch.zeros(k.shape, dtype=torch.float32, device=q.device))
-    dq = dw = dk = None
-    for c0 in range(0, max_row_len, SCORES_BWD_COLS):
-        width = min(SCORES_BWD_COLS, max_row_len - c0)
-        idx = dense_row_indices(row_base, row_len, c0, width)
-        d = d_scores[:, c0:c0 + width].float()
-        d = torch.where(idx >= 0, d, torch.zeros_like(d)).contiguous()
-        a, b, c = indexer_scores_bwd(q, k, w, idx, d, False)
-        dq, dw, dk = (a, b, c) if dq is None else (dq + a, dw + b, dk + c)
+    _require_gpu(q, k, w, row_base, row_len, d_scores)
+    _require(D == 128 and k.shape[-1] == 128, "indexer head_dim must be 128")
+    q, k = q.to(torch.bfloat16).contiguous(), k.to(torch.bfloat16).contiguous()
+    w = w.to(torch.float32).contiguous()
+    d = d_scores.to(torch.float32).contiguous()
+    rb, rl = row_base.to(torch.int32).contiguous(), row_len.to(torch.int32).contiguous()
+    dq = torch.empty(T, Hi, 128, dtype=torch.float32, device=q.device)
+    dw = torch.empty(T, Hi, dtype=torch.float32, device=q.device)
+    dk = torch.empty(N, 128, dtype=torch.float32, device=q.device)
+    ws_bytes = dense_scores_bwd_workspace_bytes(T, N)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.call("dsa_dense_indexer_scores_bwd", _p(q), _p(k), _p(w), _p(rb), _p(rl), T, N, Hi, 128, _p(d),
+                  d.shape[1], _p(dq), _p(dw), _p(dk), _p(ws), ws.numel(), _stream(q.device))
     return dq, dw, dk
 
 

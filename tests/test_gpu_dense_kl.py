@@ -134,3 +134,81 @@ def test_dense_statistics_of_rows_longer_than_the_index_rows():
         idx = ops.dense_row_indices(base, ln, c0, w)
         t_ref = ops.indexer_kl_target(q, kv, idx, lse, W.SM_SCALE, False)
         torch.testing.assert_close(tgt[:, c0:c0 + w], t_ref, rtol=1e-4, atol=1e-9)
+
+
+def _column_block_scores_bwd(q, k, w, base, ln, max_len, d, cols=4096):
+    """The dense score backward as the selected-slot score backward (pinned to the oracle in
+    test_gpu_indexer_kl.py) over blocks of dense columns, summed."""
+    dq = dw = dk = None
+    for c0 in range(0, max_len, cols):
+        width = min(cols, max_len - c0)
+        idx = ops.dense_row_indices(base, ln, c0, width)
+        dd = torch.where(idx >= 0, d[:, c0:c0 + width], torch.zeros_like(d[:, c0:c0 + width])).contiguous()
+        a, b, c = ops.indexer_scores_bwd(q, k, w, idx, dd, False)
+        dq, dw, dk = (a, b, c) if dq is None else (dq + a, dw + b, dk + c)
+    return dq, dw, dk
+
+
+def _nerr(a, b):
+    return float((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30))
+
+
+def test_dense_scores_bwd_matches_the_oracle():
+    """dq, dw, dk of the dense index scores over packed causal documents (one row of 1 key, key tiles
+    straddling documents) against the float64 oracle's score backward over the dense index rows."""
+    print("[dense score bwd] oracle", flush=True)
+    g = torch.Generator().manual_seed(12)
+    cu = [0, 130, 300, 301, 700]
+    T, Hi = cu[-1], 64
+    q = (torch.randn(T, Hi, 128, generator=g) * 0.1).bfloat16()
+    k = (torch.randn(T, 128, generator=g) * 0.1).bfloat16()
+    w = torch.randn(T, Hi, generator=g) / 8
+    base, ln, maxlen = _rows(cu)
+    pitch = maxlen + 5
+    d = torch.randn(T, pitch, generator=g)
+    dq, dw, dk = ops.indexer_scores_dense_bwd(q.to(DEV), k.to(DEV), w.to(DEV), base, ln, maxlen, d.to(DEV))
+    idx = ops.dense_row_indices(base, ln, 0, pitch).cpu()
+    dq_r, dk_r, dw_r = O.indexer_scores_bwd(q, k, w, idx, d)
+    for name, a, r in (("dq", dq, dq_r), ("dw", dw, dw_r), ("dk", dk, dk_r)):
+        torch.testing.assert_close(a.cpu().double(), r, rtol=2e-2, atol=2e-2, msg=lambda m: f"{name}: {m}")
+        assert _nerr(a.cpu(), r) < 5e-3, (name, _nerr(a.cpu(), r))
+
+
+@pytest.mark.parametrize("case", ["cfg3", "decode"])
+def test_dense_scores_bwd_matches_the_column_block_path(case):
+    """At the cfg3 size (16384 tokens in 4 causal documents, Hi = 64: every row) and over decode rows
+    (one query per sequence over its own cache rows: keys that are not the query tokens), the dense
+    score backward equals the selected-slot score backward over 4096-column blocks: dq and dw to
+    fp32 summation order, dk to the bf16 rounding of its per-pair gradient (w folded into G here, into
+    Q there)."""
+    print(f"[dense score bwd] column-block path, {case}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    Hi = 64
+    if case == "cfg3":
+        cfg = W.CONFIGS["cfg3"]
+        cu = torch.tensor(cfg.cu_seqlens, dtype=torch.int32, device=DEV)
+        T = N = cfg.S
+        base, ln = ops.build_rows(cu, T, True)
+        maxlen = max(b - a for a, b in zip(cfg.cu_seqlens[:-1], cfg.cu_seqlens[1:]))
+    else:
+        lens = [5000, 1, 777, 12000, 64, 3001]
+        cc = [0]
+        for x in lens:
+            cc.append(cc[-1] + x)
+        T, N = len(lens), cc[-1]
+        base, ln = ops.build_decode_rows(torch.tensor(cc, dtype=torch.int32, device=DEV))
+        maxlen = max(lens)
+    q = (torch.randn(T, Hi, 128, generator=g, device=DEV) * 0.1).bfloat16()
+    k = (torch.randn(N, 128, generator=g, device=DEV) * 0.1).bfloat16()
+    w = torch.randn(T, Hi, generator=g, device=DEV) / 8
+    pitch = (maxlen + 3) // 4 * 4
+    d = torch.randn(T, pitch, generator=g, device=DEV) * 1e-3
+    dq, dw, dk = ops.indexer_scores_dense_bwd(q, k, w, base, ln, maxlen, d)
+    dq_r, dw_r, dk_r = _column_block_scores_bwd(q, k, w, base, ln, maxlen, d)
+    torch.testing.assert_close(dq, dq_r, rtol=1e-4, atol=1e-7)
+    torch.testing.assert_close(dw, dw_r, rtol=1e-4, atol=1e-7)
+    assert _nerr(dk, dk_r) < 1e-2, _nerr(dk, dk_r)
+    torch.testing.assert_close(dk, dk_r, rtol=5e-2, atol=1e-4)
+    # deterministic: a second call gives the same bits
+    dq2, dw2, dk2 = ops.indexer_scores_dense_bwd(q, k, w, base, ln, maxlen, d)
+    assert torch.equal(dq, dq2) and torch.equal(dw, dw2) and torch.equal(dk, dk2)

@@ -566,17 +566,15 @@ def test_dsattention_thd_packed_equals_per_document():
         _close(grads_p[n].cpu(), grads_d[n].cpu(), rel=2e-2, name=f"indexer {n}")
 
 
-@pytest.mark.parametrize("cols", [None, 96])
-def test_fused_qk_topk_naive_scores_are_differentiable(cols, monkeypatch):
+@pytest.mark.parametrize("S,B", [(200, 2), (1100, 1)])
+def test_fused_qk_topk_naive_scores_are_differentiable(S, B):
     """The [B, S, S] index scores of the drop-in carry the dense score backward (what the reference's
     dense indexer loss backpropagates through): gradients of q, k, weights against float64 autograd
-    of the oracle's scores, with the causal triu mask and without; ``cols`` shrinks the column
-    blocks of the dense backward so that several blocks run."""
-    print(f"[index scores autograd] cols={cols}", flush=True)
-    if cols:
-        monkeypatch.setattr(ops, "SCORES_BWD_COLS", cols)
+    of the oracle's scores, with the causal triu mask and without; S = 1100 puts more than one
+    512-query chunk on the dk kernel's key tiles."""
+    print(f"[index scores autograd] S={S} B={B}", flush=True)
     g = torch.Generator().manual_seed(31)
-    S, B, Hi = 200, 2, 64
+    Hi = 64
     q = (torch.randn(S, B, Hi, 128, generator=g) * 0.1).bfloat16()
     k = (torch.randn(S, B, 128, generator=g) * 0.1).bfloat16()
     w = torch.randn(S, B, Hi, generator=g) / 8
@@ -593,18 +591,15 @@ def test_fused_qk_topk_naive_scores_are_differentiable(cols, monkeypatch):
             _close(a.cpu(), r, name=f"{name} (mask={m is not None}, causal={causal})")
 
 
-@pytest.mark.parametrize("cols", [None, 64])
-def test_dense_indexer_loss_matches_float64_autograd(cols, monkeypatch):
+@pytest.mark.parametrize("cu", [[0, 130, 300, 301, 420], [0, 1100, 1230]])
+def test_dense_indexer_loss_matches_float64_autograd(cu):
     """The dense indexer loss (the reference default, dsa_indexer_use_sparse_loss=False) over packed
     documents: loss and gradients of q_idx, k_idx, w against float64 autograd through the oracle's
     dense scores and compute_dsa_indexer_loss(sparse_loss=False), document by document (the
-    reference's mean over tokens); ``cols`` shrinks the column blocks of the dense score backward."""
-    print(f"[dense indexer loss] cols={cols}", flush=True)
+    reference's mean over tokens); the 1100-token document gives key tiles of several query chunks."""
+    print(f"[dense indexer loss] cu={cu}", flush=True)
     from mcore_bridge_amd.dsa import indexer_kl_loss_dense
-    if cols:
-        monkeypatch.setattr(ops, "SCORES_BWD_COLS", cols)
     g = torch.Generator().manual_seed(41)
-    cu = [0, 130, 300, 301, 420]
     T, H, Hi, coeff = cu[-1], 16, 64, 0.4
     q = (torch.randn(T, H, 576, generator=g) * 0.1).bfloat16()
     kv = (torch.randn(T, 576, generator=g) * 0.1).bfloat16()
