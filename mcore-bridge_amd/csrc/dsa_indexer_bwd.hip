@@ -467,19 +467,28 @@ __global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stag
 // row's keys are one contiguous range, so neither kernel needs index rows or a pair order, and dk
 // needs no staged per-pair rows:
 //   dense_scores_dq_kernel  query-major (one workgroup per query, wave w takes blocks w, w + 4, ..
-//       through its own double-buffered K tile and dI slot): Z^T = K . Q^T (lane = head) gives
+//       through its own double-buffered K tile and dI slot, rows swizzled by swz16 below): Z^T = K . Q^T (lane = head) gives
 //       G^T = dI 1[z>0] and dw += dI relu(z); dq^T += K^T . G^T; dq = w * the sum over the waves.
 //   dense_scores_dk_kernel  key-major: a workgroup holds 128 consecutive keys (wave w: 32, their K^T
 //       fragments in registers for the whole run) and streams the queries that see them, each
 //       query's Q rows, weights and dI through a double-buffered LDS slot: Z = Q . K^T (lane = key)
-//       gives G = dI w 1[z>0]; dk^T += Q^T . G (Q^T by transposing LDS reads).  A key tile's
-//       queries are cut into chunks of kDenseQChunk, one workgroup each, so no workgroup runs a
-//       whole document's queries; the chunks' partial dk tiles are summed in chunk order by
-//       dense_dk_reduce_kernel (the same bits every run).
+//       gives G = dI w 1[z>0]; dk^T += Q^T . G (Q^T by transposing LDS reads).  The queries are
+//       cut into fixed chunks of kDenseQChunk (chunk c = queries 256c .. 256c + 255), one work item
+//       per (key tile, chunk) that holds queries seeing the tile, so no workgroup runs a whole
+//       document's queries and the items of one chunk stream the same Q rows at the same time
+//       (chunk-major item order: they share them through L2); the chunks' partial dk tiles are
+//       summed in chunk order by dense_dk_reduce_kernel (the same bits every run).
 // Rows are monotone (row_base and row_base + row_len nondecreasing in t), so the queries that see
 // a key tile are one range, found by binary search.
 // ------------------------------------------------------------------------------------------
 namespace {
+
+// Dense kernels' 256-byte LDS rows: 16-byte chunk c of row r at slot c ^ swz16(r), swz16(r) =
+// 2 (r & 3) + ((r >> 2) & 1) + (r & 8).  ds_read_b128 serves 16 lanes per LDS cycle: the operand
+// read (16 consecutive rows, one chunk) then meets 16 distinct slots, and the transposing read
+// (4 consecutive rows x 2 chunks per 16 lanes) 8 distinct slots.  (swz, 3 bits, gives the
+// operand read 8.)  Adding 128 bytes to a chunk address is an XOR on bit 7 of the byte address.
+DSA_DEV constexpr uint32_t swz16(uint32_t r) { return ((r & 3u) << 1) | ((r >> 2) & 1u) | (r & 8u); }
 
 // Row t's keys clipped to k and to the score pitch: [base, base + len).
 DSA_DEV void dense_row(const DenseIdxBwdParams& p, int t, int& base, int& len) {
@@ -519,10 +528,12 @@ struct DenseDqSmem {
   float dwp[4][kHi];
 };
 
+constexpr int kDkSlots = 3;        // query slots of the dk kernel's ring (rows of query i + 2 copied during i)
 struct DenseDkSmem {
-  char q[2][kHi * kRowB];          // Q[t] rows (head r, 16-byte chunk c at slot c ^ swz(r))
-  float w[2][kHi];
-  float di[2][kDenseDkKeys];       // dI[t, s - row_base[t]] of the tile's keys (masked in-register)
+  char q[kDkSlots][kHi * kRowB];   // Q[t] rows (head r, 16-byte chunk c at slot c ^ swz16(r))
+  float w[kDkSlots][kHi];
+  float di[kDkSlots][kDenseDkKeys];  // dI[t, s - row_base[t]] of the tile's keys (masked in-register)
+  float wpad[kHi];                 // target of wave 3's balancing copy (never read)
   int32_t rb[kDenseQChunk];        // row_base / row_len of the work item's queries
   int32_t rl[kDenseQChunk];
 };
@@ -558,20 +569,33 @@ __global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdPara
   const uint32_t dis = lds_addr(sm.di[wave][0]);
   // block blk into slot `slot`: K rows of keys base + 32 blk + kk (past the row: its last key,
   // masked), copy r moving keys 4r .. 4r+3 (lane l: slot l & 15 of key 4r + l/16 from chunk
-  // (l & 15) ^ swz(key)); then 64 dI values from column 32 blk (clamped to the row's pitch)
-  auto gather = [&](int slot, int blk) {
-    const int kk0 = lane >> 4;
-    const uint32_t sl = lane & 15;
+  // (l & 15) ^ swz16(key)); then 64 dI values from column 32 blk (clamped to the row's pitch)
+  // Keys of a block past the row's end are gathered too (masked) as long as they are k rows: then
+  // copy r reads 1 KB from the scalar address of key base + 32 blk + 4r plus a per-lane offset
+  // (swz16(4r + lane/16) depends on r & 3 only: four offsets serve all eight copies).
+  uint32_t voff[4];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int kk = 4 * r + kk0;
-      const int j = min(32 * blk + kk, len - 1);
-      const char* src = reinterpret_cast<const char*>(p.k) + (int64_t)(base + j) * kRowB + 16u * (sl ^ swz(kk));
-      async_copy16_unordered(src, tiles + slot * kKTile + 1024u * r);
+  for (int v = 0; v < 4; ++v) voff[v] = (lane >> 4) * kRowB + 16u * ((lane & 15) ^ swz16(4 * v + (lane >> 4)));
+  auto gather = [&](int slot, int blk) {
+    if (base + 32 * blk + 32 <= p.n_k) {
+      const char* kb = reinterpret_cast<const char*>(p.k) + (int64_t)(base + 32 * blk) * kRowB;
+      asm volatile("s_nop 4");   // any VALU-written SGPR of the address: 5 wait states before the DMA
+#pragma unroll
+      for (int r = 0; r < 8; ++r) copy_row16(tiles + slot * kKTile + 1024u * r, kb + 1024 * r, voff[r & 3]);
+    } else {   // the last rows of k: clamp each key to the row
+      const int kk0 = lane >> 4;
+      const uint32_t sl = lane & 15;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int kk = 4 * r + kk0;
+        const int j = min(32 * blk + kk, len - 1);
+        const char* src = reinterpret_cast<const char*>(p.k) + (int64_t)(base + j) * kRowB + 16u * (sl ^ swz16(kk));
+        async_copy16_unordered(src, tiles + slot * kKTile + 1024u * r);
+      }
     }
     async_copy4_unordered(drow + min(32 * blk + lane, p.pitch - 1), dis + slot * 256u);
   };
-  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz(hl));
+  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz16(hl));
   uint32_t troff[2][2][2];
   {
     const int g = lane >> 4, gi = lane & 15;
@@ -583,7 +607,7 @@ __global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdPara
         for (int m1 = 0; m1 < 2; ++m1) {
           const uint32_t key = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
           const uint32_t cp = 2 * (g & 1) + ((gi >> 1) & 1);
-          troff[a][h][m1] = key * kRowB + 16u * ((4u * m1) ^ cp ^ swz(key)) + 8u * (gi & 1);
+          troff[a][h][m1] = key * kRowB + 16u * ((4u * m1) ^ cp ^ swz16(key)) + 8u * (gi & 1);
         }
   }
   f32x16 dqa[4][2];
@@ -601,6 +625,10 @@ __global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdPara
     wait_vmcnt<0>();
     asm volatile("" ::: "memory");
     if (blk + 4 < nblk) gather(slot ^ 1, blk + 4);
+    // dI of the lane's 16 keys (read before the MFMAs, used after them)
+    f32x4 dv4[4];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) dv4[gq] = *reinterpret_cast<const f32x4*>(&sm.di[wave][slot][gq * 8 + 4 * hb]);
     // ---- Z^T = K . Q^T (lane = head, rows = keys (i/4)*8 + 4 hb + i%4)
     f32x16 zt[2];
     {
@@ -623,15 +651,31 @@ __global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdPara
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    auto ktr = [&](int f) {
+      const int a = f >> 2, mm = f & 3;
+      const uint32_t o = 128u * (mm >> 1);
+      const u32x2 lo = lds_read_tr16((tb + troff[a][0][mm & 1]) ^ o);
+      const u32x2 hi = lds_read_tr16((tb + troff[a][1][mm & 1]) ^ o);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    constexpr int kPreT = 3;
+    u32x4 kt[kPreT];
+#pragma unroll
+    for (int f = 0; f < kPreT; ++f) kt[f] = ktr(f);
     mfma_acc_drain();
     // ---- G^T = dI 1[z>0] (0 past the row) and dw
     const int nvalid = len - 32 * blk;
     float dr[16];
+    if (nvalid >= 32) {
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&sm.di[wave][slot][gq * 8 + 4 * hb]);
+      for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dr[4 * gq + e] = gq * 8 + 4 * hb + e < nvalid ? v[e] : 0.f;
+        for (int e = 0; e < 4; ++e) dr[4 * gq + e] = dv4[gq][e];
+    } else {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dr[4 * gq + e] = gq * 8 + 4 * hb + e < nvalid ? dv4[gq][e] : 0.f;
     }
     u32x4 gt[2][2];
 #pragma unroll
@@ -646,19 +690,16 @@ __global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdPara
       }
       dwacc[n] += dws;
     }
-    // ---- dq^T[dims x heads] += K^T . G^T
+    // ---- dq^T[dims x heads] += K^T . G^T (K^T fragment f = 4 a + mm, read kPreT fragments ahead;
+    // the first ones before G^T is formed)
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int f = 0; f < 8; ++f) {
+      const u32x4 cur = kt[f % kPreT];
+      if (f + kPreT < 8) kt[f % kPreT] = ktr(f + kPreT);
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm) {
-        const uint32_t o = 128u * (mm >> 1);
-        const u32x2 lo = lds_read_tr16(tb + troff[a][0][mm & 1] + o);
-        const u32x2 hi = lds_read_tr16(tb + troff[a][1][mm & 1] + o);
-        const u32x4 kt = u32x4{lo[0], lo[1], hi[0], hi[1]};
-#pragma unroll
-        for (int n = 0; n < 2; ++n) mfma32x32x16_cA(dqa[mm][n], kt, gt[n][a]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int n = 0; n < 2; ++n) mfma32x32x16_cA(dqa[f & 3][n], cur, gt[n][f >> 2]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   // ---- epilogue: dw and dq summed over the four waves (the tiles' union is reused)
@@ -702,8 +743,8 @@ __global__ __launch_bounds__(256, 1) void dense_scores_dq_kernel(DenseIdxBwdPara
   }
 }
 
-// Work item (key tile, query chunk): chunk-major ids, so the workgroups running at once share
-// their queries' rows through the caches.
+// Work item (key tile, query chunk): chunk-major ids, so the workgroups running at once stream the
+// same queries' rows.
 __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdParams p) {
   __shared__ __attribute__((aligned(256))) DenseDkSmem sm;
   const int item = xcd_remap(blockIdx.x, p.n_xcd);
@@ -711,9 +752,9 @@ __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdPara
   const int chunk = item / p.n_tiles, tile = item - chunk * p.n_tiles;
   int lo, hi;
   dense_tile_queries(p, tile, lo, hi);
-  const int t_begin = lo + chunk * kDenseQChunk;
-  if (t_begin >= hi) return;   // the tile's queries end before this chunk: no partial (the reduce knows)
-  const int nq = min(kDenseQChunk, hi - t_begin);
+  const int t_begin = max(lo, chunk * kDenseQChunk);
+  const int nq = min(hi, (chunk + 1) * kDenseQChunk) - t_begin;
+  if (nq <= 0) return;   // no query of this chunk sees the tile: no partial (the reduce knows)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hb = lane >> 5, hl = lane & 31;
@@ -736,33 +777,47 @@ __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdPara
   wait_vmcnt0();
   __syncthreads();
   const uint32_t qs0 = lds_addr(sm.q[0]), ws0 = lds_addr(sm.w[0]), ds0 = lds_addr(sm.di[0]);
-  // query i's rows into slot `slot`: Q (16 copies of 4 head rows, 4 per wave; rows past n_heads
-  // re-read head 0, never used), weights (wave 1), the tile's 128 dI columns (wave 0, two copies;
-  // columns outside the row clamped into it and masked by the caller)
+  const uint32_t wpad0 = lds_addr(sm.wpad);
+  // query i's rows into slot `slot`, five copies per wave (so every wave's waits count the same):
+  // Q (16 copies of 4 head rows, 4 per wave; rows past n_heads re-read head 0, never used), the
+  // tile's 128 dI columns (waves 0 and 1, 64 each; columns outside the row clamped into it and
+  // masked by the caller), the weights (wave 2) and a copy of them into an unread pad (wave 3)
+  // with 64 heads, copy r reads 1 KB from the scalar address of head 4r plus a per-lane offset
+  // (swz16(4r + lane/16) depends on r & 3 only)
+  uint32_t voff[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) voff[v] = (lane >> 4) * kRowB + 16u * ((lane & 15) ^ swz16(4 * v + (lane >> 4)));
   auto issue = [&](int slot, int i) {
     const int tq = t_begin + i;
     const bf16_t* qrow = p.q + (int64_t)tq * p.n_heads * kDi;
-    const uint32_t sl = lane & 15;
+    if (p.n_heads == kHi) {
+      const char* qb0 = reinterpret_cast<const char*>(qrow);
+      asm volatile("s_nop 4");   // any VALU-written SGPR of the address: 5 wait states before the DMA
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int r = 4 * wave + r4;
-      const int h = 4 * r + (lane >> 4);
-      const char* src = reinterpret_cast<const char*>(qrow + (h < p.n_heads ? h : 0) * kDi) + 16u * (sl ^ swz(h));
-      async_copy16_unordered(src, qs0 + slot * (kHi * kRowB) + 1024u * r);
-    }
-    if (wave == 1) async_copy4_unordered(p.w + (int64_t)tq * p.n_heads + min(lane, p.n_heads - 1), ws0 + slot * 256u);
-    if (wave == 0) {
-      const float* drow = p.d_scores + (int64_t)tq * p.pitch;
-      const int base_q = sm.rb[i];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int j = min(max(s0 + 64 * c + lane - base_q, 0), p.pitch - 1);
-        async_copy4_unordered(drow + j, ds0 + slot * 512u + 256u * c);
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int r = 4 * wave + r4;
+        copy_row16(qs0 + slot * (kHi * kRowB) + 1024u * r, qb0 + 1024 * r, voff[r4]);
       }
+    } else {
+      const uint32_t sl = lane & 15;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int r = 4 * wave + r4;
+        const int h = 4 * r + (lane >> 4);
+        const char* src = reinterpret_cast<const char*>(qrow + (h < p.n_heads ? h : 0) * kDi) + 16u * (sl ^ swz16(h));
+        async_copy16_unordered(src, qs0 + slot * (kHi * kRowB) + 1024u * r);
+      }
+    }
+    if (wave < 2) {
+      const int j = min(max(s0 + 64 * wave + lane - sm.rb[i], 0), p.pitch - 1);
+      async_copy4_unordered(p.d_scores + (int64_t)tq * p.pitch + j, ds0 + slot * 512u + 256u * wave);
+    } else {
+      async_copy4_unordered(p.w + (int64_t)tq * p.n_heads + min(lane, p.n_heads - 1),
+                            wave == 2 ? ws0 + slot * 256u : wpad0);
     }
   };
   // Z operand (A = Q rows): head 32 n + hl, chunk 2 ks + hb; transposing reads of Q^T (A of dk^T)
-  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz(hl));
+  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz16(hl));
   uint32_t troff[2][2][2];
   {
     const int g = lane >> 4, gi = lane & 15;
@@ -774,7 +829,7 @@ __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdPara
         for (int m1 = 0; m1 < 2; ++m1) {
           const uint32_t r = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
           const uint32_t cp = 2 * (g & 1) + ((gi >> 1) & 1);
-          troff[a][h][m1] = r * kRowB + 16u * ((4u * m1) ^ cp ^ swz(r)) + 8u * (gi & 1);
+          troff[a][h][m1] = r * kRowB + 16u * ((4u * m1) ^ cp ^ swz16(r)) + 8u * (gi & 1);
         }
   }
   f32x16 dka[4];
@@ -782,15 +837,26 @@ __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdPara
   for (int m = 0; m < 4; ++m) dka[m] = f32x16{};
 
   issue(0, 0);
+  if (nq > 1) issue(1, 1);
+  int slot = 0, slot2 = 2;   // query i's slot and query i + 2's
   for (int i = 0; i < nq; ++i) {
-    const int slot = i & 1;
     const int base_t = sm.rb[i], len_t = sm.rl[i];
-    wait_vmcnt<0>();
-    __syncthreads();   // query i's rows are in; every wave is done with slot ^ 1
-    if (i + 1 < nq) issue(slot ^ 1, i + 1);
+    if (i + 1 < nq) wait_vmcnt<5>(); else wait_vmcnt<0>();   // query i's five copies (i + 1's may fly)
+    __syncthreads();   // query i's rows are in; every wave is done with query i - 1's slot
+    if (i + 2 < nq) issue(slot2, i + 2);
     const uint32_t qb = qs0 + slot * (kHi * kRowB);
-    // ---- Z[heads x keys] = Q . K^T (lane = key s, element i = head 32 n + (i/4)*8 + 4 hb + i%4)
+    // weights and dI of query i (read before the MFMAs, used after them)
+    const bool vis = s >= base_t && s < base_t + len_t;
+    const float dv = vis ? sm.di[slot][32 * wave + hl] : 0.f;
+    f32x4 wv[2][4];
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) wv[n][gq] = *reinterpret_cast<const f32x4*>(&sm.w[slot][32 * n + 8 * gq + 4 * hb]);
+    // ---- Z[heads x keys] = Q . K^T (lane = key s, element i = head 32 n + (i/4)*8 + 4 hb + i%4);
+    // dI w of the lane's 32 (head, key) values (0 for heads past n_heads), two per MFMA
     f32x16 z[2];
+    float dvw[2][16];
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       uint32_t zb = qb + n * kKTile + zoff;
@@ -804,41 +870,45 @@ __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdPara
         if (ks + kPreI < 8) qa[ks % kPreI] = lds_load16(lds_ptr(zb ^ (32u * (ks + kPreI))));
         if (ks == 0) mfma32x32x16_cV_first(z[n], cur, kf[0]);
         else mfma32x32x16_cV(z[n], cur, kf[ks]);
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const int i2 = 2 * ks + e2, h = 32 * n + 8 * (i2 >> 2) + 4 * hb + (i2 & 3);
+          dvw[n][i2] = h < p.n_heads ? dv * wv[n][i2 >> 2][i2 & 3] : 0.f;
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    // Q^T fragment f of the dk^T product (f = 8 mh + 4 s2 + mt): the first kPreT are read before
+    // G is formed, the others kPreT MFMAs ahead of their use
+    auto qtr = [&](int f) {
+      const int mh = f >> 3, s2 = (f >> 2) & 1, mt = f & 3;
+      const uint32_t b = qb + mh * kKTile, o = 128u * (mt >> 1);
+      const u32x2 lo2 = lds_read_tr16((b + troff[s2][0][mt & 1]) ^ o);
+      const u32x2 hi2 = lds_read_tr16((b + troff[s2][1][mt & 1]) ^ o);
+      return u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+    };
+    constexpr int kPreT = 4;
+    u32x4 qt[kPreT];
+#pragma unroll
+    for (int f = 0; f < kPreT; ++f) qt[f] = qtr(f);
     mfma_acc_drain();
     // ---- G = dI w 1[z>0] (0 where the query does not see key s)
-    const bool vis = s >= base_t && s < base_t + len_t;
-    const float dv = vis ? sm.di[slot][32 * wave + hl] : 0.f;
     u32x4 gz[2][2];
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const f32x4 wv = *reinterpret_cast<const f32x4*>(&sm.w[slot][32 * n + 8 * gq + 4 * hb]);
-        float g4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int h = 32 * n + 8 * gq + 4 * hb + e;
-          g4[e] = (z[n][4 * gq + e] > 0.f && h < p.n_heads) ? dv * wv[e] : 0.f;
-        }
-        gz[n][gq >> 1][2 * (gq & 1)] = pack_bf16x2(g4[0], g4[1]);
-        gz[n][gq >> 1][2 * (gq & 1) + 1] = pack_bf16x2(g4[2], g4[3]);
-      }
+      for (int i = 0; i < 16; i += 2)
+        gz[n][i >> 3][(i & 7) >> 1] = pack_bf16x2(z[n][i] > 0.f ? dvw[n][i] : 0.f, z[n][i + 1] > 0.f ? dvw[n][i + 1] : 0.f);
     // ---- dk^T[dims x keys] += Q^T . G: four independent dim-tile chains
 #pragma unroll
-    for (int mh = 0; mh < 2; ++mh)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const uint32_t b = qb + mh * kKTile + 128u * (mt >> 1);
-          const u32x2 lo2 = lds_read_tr16(b + troff[s2][0][mt & 1]);
-          const u32x2 hi2 = lds_read_tr16(b + troff[s2][1][mt & 1]);
-          mfma32x32x16_cV(dka[mt], u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, gz[mh][s2]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int f = 0; f < 16; ++f) {
+      const u32x4 cur = qt[f % kPreT];
+      if (f + kPreT < 16) qt[f % kPreT] = qtr(f + kPreT);
+      mfma32x32x16_cV(dka[f & 3], cur, gz[f >> 3][(f >> 2) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    slot = slot == kDkSlots - 1 ? 0 : slot + 1;
+    slot2 = slot2 == kDkSlots - 1 ? 0 : slot2 + 1;
   }
   mfma_acc_drain();
   // ---- the partial tile: key 32 w + hl, dims 32 mt + 8 q + 4 hb .. +3
@@ -856,7 +926,8 @@ __global__ __launch_bounds__(256) void dense_dk_reduce_kernel(DenseIdxBwdParams 
   const int tile = blockIdx.x;
   int lo, hi;
   dense_tile_queries(p, tile, lo, hi);
-  const int nch = min(hi > lo ? (hi - lo + kDenseQChunk - 1) / kDenseQChunk : 0, p.max_chunks);
+  // chunks c0 .. c1 hold the tile's queries [lo, hi) (each of them some)
+  const int c0 = lo / kDenseQChunk, c1 = hi > lo ? min((hi - 1) / kDenseQChunk, p.max_chunks - 1) : c0 - 1;
   const int s0 = tile * kDenseDkKeys;
   const f32x4* part = reinterpret_cast<const f32x4*>(p.dk_part + (int64_t)tile * p.max_chunks * (kDenseDkKeys * kDi));
   constexpr int kVec = kDenseDkKeys * kDi / 4;   // f32x4 per tile
@@ -864,7 +935,7 @@ __global__ __launch_bounds__(256) void dense_dk_reduce_kernel(DenseIdxBwdParams 
     const int key = v / (kDi / 4);
     if (s0 + key >= p.n_k) break;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < nch; ++c) acc += part[(int64_t)c * kVec + v];
+    for (int c = c0; c <= c1; ++c) acc += part[(int64_t)c * kVec + v];
     *reinterpret_cast<f32x4*>(p.dk + (int64_t)(s0 + key) * kDi + 4 * (v % (kDi / 4))) = acc;
   }
 }

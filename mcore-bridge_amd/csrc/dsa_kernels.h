@@ -208,7 +208,7 @@ struct IdxSelParams {
 // the k rows row_base[t] .. row_base[t] + row_len[t] - 1, with row_base and row_base + row_len
 // nondecreasing in t (document rows, decode rows, compressed-entry rows).
 constexpr int kDenseDkKeys = 128;   // keys per key tile of the dk kernel
-constexpr int kDenseQChunk = 512;   // queries per work item of the dk kernel
+constexpr int kDenseQChunk = 256;   // queries per work item of the dk kernel
 struct DenseIdxBwdParams {
   const bf16_t* q;            // [total_q, n_heads, 128]
   const bf16_t* k;            // [n_k, 128]
