@@ -610,7 +610,10 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-decode", action="store_true", help="skip the cfg5 decode leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip every leg after the cfg3 step")
+    ap.add_argument("--legs", default="all",
+                    help="comma list of the legs after the cfg3 step to run: int8, decode, prologue, indexer_kl, "
+                         "indexer_kl_dense, v4, cfg2, cfg4 (default all)")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="only copy a 1 GiB tensor (known HBM bytes) to calibrate FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
@@ -768,31 +771,37 @@ def main():
                      "ms": round(t[dom], 3)},
         "backward_traffic": bwd_traffic,
     }
-    res["sparse_bwd_int8_staging"] = int8_staging_leg(torch, lib, _lib, q, kv, qi, ki, w, dout, cu_t, max_seqlen,
-                                                      scale, dkv, ws, stream, fl_fwd, fl_bwd, t_fwd, t_bwd)
-    print(f"[bench] int8-staging backward leg done: {res['sparse_bwd_int8_staging']['ms']} ms", file=sys.stderr,
-          flush=True)
-    if not args.no_decode:
+    legs = set(args.legs.split(",")) if args.legs != "all" else None
+
+    def want(name):
+        return not args.no_decode and (legs is None or name in legs)
+
+    if legs is None or "int8" in legs:
+        res["sparse_bwd_int8_staging"] = int8_staging_leg(torch, lib, _lib, q, kv, qi, ki, w, dout, cu_t, max_seqlen,
+                                                          scale, dkv, ws, stream, fl_fwd, fl_bwd, t_fwd, t_bwd)
+        print(f"[bench] int8-staging backward leg done: {res['sparse_bwd_int8_staging']['ms']} ms", file=sys.stderr,
+              flush=True)
+    if want("decode"):
         res["decode"] = decode_leg(torch, dev)
         print(f"[bench] decode leg done: {res['decode']['attention_us']} us", file=sys.stderr, flush=True)
-    if not args.no_decode:
+    if want("prologue"):
         res["indexer_prologue"] = prologue_leg(torch, dev)
         print(f"[bench] prologue leg done: {res['indexer_prologue']['bf16']['us']} us", file=sys.stderr, flush=True)
-    if not args.no_decode:
+    if want("indexer_kl"):
         idx = ops.indexer_topk(qi, ki, w, K, cu_t, True, max_seqlen)
         _, lse = ops.sparse_mla_fwd(q, kv, idx, scale, True)
         res["indexer_kl"] = indexer_kl_leg(torch, dev, q, kv, idx, lse, qi, ki, w, scale, nsel, ws)
         del idx, lse
         print(f"[bench] indexer KL leg done: {res['indexer_kl']['total_ms']} ms", file=sys.stderr, flush=True)
-        res["indexer_kl_dense"] = indexer_kl_dense_leg(torch, dev, q, kv, qi, ki, w, cu_t, max_seqlen, scale,
-                                                       W.n_pairs(cu))
+    if want("indexer_kl_dense"):
+        res["indexer_kl_dense"] = indexer_kl_dense_leg(torch, dev, q, kv, qi, ki, w, cu_t, max_seqlen, scale, npairs)
         print(f"[bench] dense indexer KL leg done: {res['indexer_kl_dense']['loss_fwd_bwd_ms']} ms", file=sys.stderr,
               flush=True)
-    if not args.no_decode:
+    if want("v4"):
         res["v4"] = v4_leg(torch, dev)
         print(f"[bench] v4 leg done: {res['v4']['ms']} ms", file=sys.stderr, flush=True)
-    if not args.no_decode:
-        for name in ("cfg2", "cfg4"):
+    for name in ("cfg2", "cfg4"):
+        if want(name):
             res[name] = prefill_fwd_leg(torch, dev, name)
             print(f"[bench] {name} leg done: chain {res[name]['chain_ms']} ms", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:

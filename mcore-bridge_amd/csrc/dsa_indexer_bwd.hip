@@ -921,9 +921,10 @@ __global__ __launch_bounds__(256, 2) void dense_scores_dk_kernel(DenseIdxBwdPara
           f32x4{dka[mt][4 * q], dka[mt][4 * q + 1], dka[mt][4 * q + 2], dka[mt][4 * q + 3]};
 }
 
-// dk of key tile `blockIdx.x`: the sum of its chunks' partial tiles, in chunk order.
+// dk of 32 keys (quarter blockIdx.x & 3 of key tile blockIdx.x / 4): the sum of the tile's chunks'
+// partial rows, in chunk order.
 __global__ __launch_bounds__(256) void dense_dk_reduce_kernel(DenseIdxBwdParams p) {
-  const int tile = blockIdx.x;
+  const int tile = blockIdx.x >> 2, quarter = blockIdx.x & 3;
   int lo, hi;
   dense_tile_queries(p, tile, lo, hi);
   // chunks c0 .. c1 hold the tile's queries [lo, hi) (each of them some)
@@ -931,7 +932,7 @@ __global__ __launch_bounds__(256) void dense_dk_reduce_kernel(DenseIdxBwdParams 
   const int s0 = tile * kDenseDkKeys;
   const f32x4* part = reinterpret_cast<const f32x4*>(p.dk_part + (int64_t)tile * p.max_chunks * (kDenseDkKeys * kDi));
   constexpr int kVec = kDenseDkKeys * kDi / 4;   // f32x4 per tile
-  for (int v = threadIdx.x; v < kVec; v += 256) {
+  for (int v = quarter * (kVec / 4) + threadIdx.x; v < (quarter + 1) * (kVec / 4); v += 256) {
     const int key = v / (kDi / 4);
     if (s0 + key >= p.n_k) break;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -948,7 +949,7 @@ int launch_dense_scores_bwd(const DenseIdxBwdParams& p, hipStream_t stream) {
   if (p.total_q > 0 && p.n_tiles > 0)
     hipLaunchKernelGGL(dense_scores_dk_kernel, dim3(xcd_grid(p.n_tiles * p.max_chunks, p.n_xcd)), dim3(256), 0,
                        stream, p);
-  if (p.n_tiles > 0) hipLaunchKernelGGL(dense_dk_reduce_kernel, dim3(p.n_tiles), dim3(256), 0, stream, p);
+  if (p.n_tiles > 0) hipLaunchKernelGGL(dense_dk_reduce_kernel, dim3(4 * p.n_tiles), dim3(256), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
