@@ -25,9 +25,10 @@
 // forward (scores only) runs the Z product alone.
 //
 // LDS rows are 256 bytes (one key or one head, 128 bf16); 16-byte chunk c of row r sits at slot
-// c ^ swz(r), swz(r) = 2 (r & 3) + ((r >> 2) & 1): the Z operand read (8 consecutive keys, one
-// chunk) and the transposing read (4 consecutive keys x 2 chunks per 16 lanes) are then
-// conflict free.
+// c ^ swz16(r), swz16(r) = 2 (r & 3) + ((r >> 2) & 1) + (r & 8).  ds_read_b128 serves 16 lanes per
+// LDS cycle: the operand read (16 consecutive rows, one chunk) then meets 16 distinct slots, and
+// the transposing read (4 consecutive rows x 2 chunks per 16 lanes) 8.  Adding 128 bytes to a
+// chunk address is an XOR on bit 7 of the (256-byte aligned) row address.
 #include "dsa_common.h"
 #include "dsa_kernels.h"
 #include "dsa_kvtile.h"
@@ -52,7 +53,7 @@ DSA_DEV u32x2 lds_read_tr16(uint32_t a) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-DSA_DEV constexpr uint32_t swz(uint32_t r) { return ((r & 3u) << 1) | ((r >> 2) & 1u); }
+DSA_DEV constexpr uint32_t swz16(uint32_t r) { return ((r & 3u) << 1) | ((r >> 2) & 1u) | (r & 8u); }
 
 // C += A * B with A in AccVGPRs (loop-invariant operand), B and C in VGPRs; hazards as the other
 // asm forms (dsa_common.h).
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
       u32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(wh4[r] * bf16_lo(qv4[r][e]), wh4[r] * bf16_hi(qv4[r][e]));
-      lds_store16(&sm.qw[h * kRowB + 16 * (c ^ swz(h))], o);
+      lds_store16(&sm.qw[h * kRowB + 16 * (c ^ swz16(h))], o);
     }
   }
   last = wave_max_i(last);
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
   const uint32_t tiles = lds_addr(sm.tile[wave][0]);
   const uint32_t qw0 = lds_addr(sm.qw);
   // gather of block blk into the tile at LDS address buf: copy r moves keys 4r .. 4r+3, lane l
-  // filling slot l & 15 of key 4r + l / 16 from that key's chunk (l & 15) ^ swz(key)
+  // filling slot l & 15 of key 4r + l / 16 from that key's chunk (l & 15) ^ swz16(key)
   auto gather = [&](uint32_t buf, int blk) {
     const int kk0 = lane >> 4;
     const uint32_t sl = lane & 15;
@@ -190,12 +191,12 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
       const int kk = 4 * r + kk0;
       const int row = sm.idx[blk * 32 + kk];
       const char* src = reinterpret_cast<const char*>(p.k) + (int64_t)(row >= 0 ? row : 0) * kRowB +
-                        16u * (sl ^ swz(kk));
+                        16u * (sl ^ swz16(kk));
       async_copy16_unordered(src, buf + 1024u * r);
     }
   };
   // Z operand: key hl, chunk 2 ks + hb -> (tile + zoff) ^ 32 ks
-  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz(hl));
+  const uint32_t zoff = hl * kRowB + 16u * (hb ^ swz16(hl));
   // transposing reads (A of dq^T / c^T): 16-lane group g, lane gi feeds row 16a + 8h + 4(g/2) +
   // gi/4 (the C-layout row order of Z^T / Z) and dims 32m + 16(g%2) + 4(gi%4); m&1 selects the
   // precomputed slot, m>>1 adds 128 bytes
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
         for (int m1 = 0; m1 < 2; ++m1) {
           const uint32_t key = 16 * a + 8 * h + 4 * (g >> 1) + (gi >> 2);
           const uint32_t cp = 2 * (g & 1) + ((gi >> 1) & 1);
-          troff[a][h][m1] = key * kRowB + 16u * ((4u * m1) ^ cp ^ swz(key)) + 8u * (gi & 1);
+          troff[a][h][m1] = key * kRowB + 16u * ((4u * m1) ^ cp ^ swz16(key)) + 8u * (gi & 1);
         }
   }
 
@@ -223,9 +224,9 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
       for (int mh = 0; mh < 2; ++mh)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const uint32_t base = qw0 + mh * kKTile + 128u * (mt >> 1);
-          const u32x2 lo = lds_read_tr16(base + troff[s2][0][mt & 1]);
-          const u32x2 hi = lds_read_tr16(base + troff[s2][1][mt & 1]);
+          const uint32_t base = qw0 + mh * kKTile, o = 128u * (mt >> 1);
+          const u32x2 lo = lds_read_tr16((base + troff[s2][0][mt & 1]) ^ o);
+          const u32x2 hi = lds_read_tr16((base + troff[s2][1][mt & 1]) ^ o);
           qt[mt][mh][s2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
   }
@@ -278,6 +279,18 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    auto ktr = [&](int f) {
+      const uint32_t o = 128u * ((f & 3) >> 1);
+      const u32x2 lo = lds_read_tr16((tb + troff[f >> 2][0][f & 1]) ^ o);
+      const u32x2 hi = lds_read_tr16((tb + troff[f >> 2][1][f & 1]) ^ o);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    constexpr int kPreT = 3;
+    u32x4 kt[kPreT];
+    if (kBwd) {
+#pragma unroll
+      for (int f = 0; f < kPreT; ++f) kt[f] = ktr(f);
+    }
     mfma_acc_drain();
 
     if (!kBwd) {
@@ -316,19 +329,16 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
       dwacc[n] += dws;
     }
 
-    // ---- dq^T[dims x heads] += K^T . G^T
+    // ---- dq^T[dims x heads] += K^T . G^T (K^T fragment f = 4 a + mm, read kPreT fragments ahead;
+    // the first ones before G^T is formed)
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int f = 0; f < 8; ++f) {
+      const u32x4 cur = kt[f % kPreT];
+      if (f + kPreT < 8) kt[f % kPreT] = ktr(f + kPreT);
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm) {
-        const uint32_t o = 128u * (mm >> 1);
-        const u32x2 lo = lds_read_tr16(tb + troff[a][0][mm & 1] + o);
-        const u32x2 hi = lds_read_tr16(tb + troff[a][1][mm & 1] + o);
-        const u32x4 kt = u32x4{lo[0], lo[1], hi[0], hi[1]};
-#pragma unroll
-        for (int n = 0; n < 2; ++n) mfma32x32x16_cA(dqa[mm][n], kt, gt[n][a]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int n = 0; n < 2; ++n) mfma32x32x16_cA(dqa[f & 3][n], cur, gt[n][f >> 2]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     // ---- c^T[dims x keys] = (wQ)^T . G: four independent dim-tile chains, then staged as 256-byte
     // key rows in this block's tile
@@ -352,7 +362,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
           const u32x2 v = u32x2{pack_bf16x2(c[mt][4 * gq], c[mt][4 * gq + 1]),
                                 pack_bf16x2(c[mt][4 * gq + 2], c[mt][4 * gq + 3])};
           *reinterpret_cast<u32x2*>(const_cast<char*>(
-              lds_ptr(tb + hl * kRowB + 16u * ((4u * mt + gq) ^ swz(hl)) + 8u * hb))) = v;
+              lds_ptr(tb + hl * kRowB + 16u * ((4u * mt + gq) ^ swz16(hl)) + 8u * hb))) = v;
         }
     }
     // ---- key rows out: copy s writes keys 4s .. 4s+3, 16 lanes per 256-byte row
@@ -363,7 +373,7 @@ __global__ __launch_bounds__(256, 1) void indexer_sel_kernel(IdxSelParams p) {
         const int r = 4 * s + (lane >> 4);
         const u32x4 v = lds_load16(lds_ptr(tb + r * kRowB + 16u * sl));
         const int64_t grow = sm.pos[blk * 32 + r];
-        *reinterpret_cast<u32x4*>(p.g_stage + grow * kDi + 8 * (sl ^ swz(r))) = v;
+        *reinterpret_cast<u32x4*>(p.g_stage + grow * kDi + 8 * (sl ^ swz16(r))) = v;
       }
     }
   }
@@ -467,7 +477,7 @@ __global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stag
 // row's keys are one contiguous range, so neither kernel needs index rows or a pair order, and dk
 // needs no staged per-pair rows:
 //   dense_scores_dq_kernel  query-major (one workgroup per query, wave w takes blocks w, w + 4, ..
-//       through its own double-buffered K tile and dI slot, rows swizzled by swz16 below): Z^T = K . Q^T (lane = head) gives
+//       through its own double-buffered K tile and dI slot, rows swizzled by swz16): Z^T = K . Q^T (lane = head) gives
 //       G^T = dI 1[z>0] and dw += dI relu(z); dq^T += K^T . G^T; dq = w * the sum over the waves.
 //   dense_scores_dk_kernel  key-major: a workgroup holds 128 consecutive keys (wave w: 32, their K^T
 //       fragments in registers for the whole run) and streams the queries that see them, each
@@ -482,13 +492,6 @@ __global__ __launch_bounds__(256) void idx_dk_reduce_kernel(const bf16_t* g_stag
 // a key tile are one range, found by binary search.
 // ------------------------------------------------------------------------------------------
 namespace {
-
-// Dense kernels' 256-byte LDS rows: 16-byte chunk c of row r at slot c ^ swz16(r), swz16(r) =
-// 2 (r & 3) + ((r >> 2) & 1) + (r & 8).  ds_read_b128 serves 16 lanes per LDS cycle: the operand
-// read (16 consecutive rows, one chunk) then meets 16 distinct slots, and the transposing read
-// (4 consecutive rows x 2 chunks per 16 lanes) 8 distinct slots.  (swz, 3 bits, gives the
-// operand read 8.)  Adding 128 bytes to a chunk address is an XOR on bit 7 of the byte address.
-DSA_DEV constexpr uint32_t swz16(uint32_t r) { return ((r & 3u) << 1) | ((r >> 2) & 1u) | (r & 8u); }
 
 // Row t's keys clipped to k and to the score pitch: [base, base + len).
 DSA_DEV void dense_row(const DenseIdxBwdParams& p, int t, int& base, int& len) {
