@@ -1,5 +1,6 @@
 """Full-size GPU parity of the prefill configurations cfg2 (bf16, S = 4096) and cfg4 (fp8 indexer,
-S = 32768): the whole chain indexer -> top-k -> sparse MLA forward at the bench's shapes.
+S = 32768): the whole chain indexer -> top-k -> sparse MLA forward at the bench's shapes; and of
+cfg5's decode indexer (64 sequences over caches of up to 65,265 keys, bf16 and e4m3 key caches).
 
 Every row is checked where a size-independent check exists:
   - top-k of every row equals a stable descending sort of the kernel's own fp32 scores (ties to
@@ -213,3 +214,62 @@ def test_cfg3_full_size_indexer_topk_sparse_fwd_bwd():
     rdkv = O.sparse_mla_bwd_dkv_rows(q.cpu(), kvc, idx.cpu(), out.cpu(), dout.cpu(), lse.cpu(), W.SM_SCALE, keys)
     _close(dkv[keys].cpu(), rdkv, name="dkv (oracle keys)")
     _close(ref_dkv[keys].cpu(), rdkv, rel=1e-3, tol=5e-3, name="fp32 dkv reference vs oracle")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_decode_indexer_cfg5_full_size(fp8):
+    """cfg5 at full size (64 sequences, the cache-length fixture up to 65,265 keys, Hi = 64, Di = 128,
+    K = 2048) through ops.decode_indexer_topk: every row's selection equals a stable descending sort
+    of the kernel's own fp32 scores, bit for bit; every score matches an fp32 GPU reference of the
+    same (dequantised) inputs; on sampled sequences the scores match the float64 oracle and the
+    selection overlaps the float64 selection by >= 99.9 %.  fp8: e4m3fn q and key cache with one
+    fp32 absmax scale per row."""
+    cfg = W.CONFIGS["cfg5"]
+    print(f"[decode indexer cfg5 full size] fp8={fp8}", flush=True)
+    d = W.make_decode(cfg, device=DEV, seed=17)
+    lens = [int(x) for x in cfg.decode_lens]
+    B, K = len(lens), cfg.K
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32, device=DEV)
+    q, k, w = d["q_idx"], d["k_cache"], d["w"]
+    del d
+    if fp8:
+        q8, qs = W.quantize_e4m3_rows(q * 10)
+        k8, ks = W.quantize_e4m3_rows(k * 10)
+        idx, sc = ops.decode_indexer_topk(q8, k8, w, K, cu, max(lens), qs, ks, return_scores=True)
+        qd, kd = q8.float() * qs[..., None], k8.float() * ks[:, None]
+    else:
+        qb, kb = q.bfloat16(), k.bfloat16()
+        idx, sc = ops.decode_indexer_topk(qb, kb, w, K, cu, max(lens), return_scores=True)
+        qd, kd = qb.float(), kb.float()
+    # every row: bit-exact selection from the kernel's own scores (ascending ids, ties to the lower key)
+    off = cu[:-1].long()
+    for b, L in enumerate(lens):
+        order = torch.sort(sc[b, :L], descending=True, stable=True).indices[:K]
+        want = (order.long() + off[b]).sort().values
+        got = idx[b].long()
+        n = min(K, L)
+        assert torch.equal(got[:n], want) and bool((got[n:] == -1).all()), f"row {b}"
+    # every score against an fp32 GPU reference
+    for b, L in enumerate(lens):
+        o = int(off[b])
+        ref = (torch.relu(qd[b] @ kd[o:o + L].T) * w[b][:, None]).sum(0)
+        torch.testing.assert_close(sc[b, :L], ref, rtol=2e-3 if fp8 else 1e-4, atol=2e-3 if fp8 else 1e-5,
+                                   msg=lambda m: f"scores row {b}: {m}")
+    # sampled sequences against the float64 oracle (the longest, the shortest and one more)
+    rows = sorted({int(torch.tensor(lens).argmax()), int(torch.tensor(lens).argmin()), 7})
+    inter = tot = 0
+    for b in rows:
+        o, L = int(off[b]), lens[b]
+        qo = (q8 if fp8 else qb)[b:b + 1].cpu()
+        ko = (k8 if fp8 else kb)[o:o + L].cpu()
+        kw = dict(q_scale=qs[b:b + 1].cpu(), k_scale=ks[o:o + L].cpu()) if fp8 else {}
+        ref64 = O.decode_indexer_scores(qo.float() if fp8 else qo, ko.float() if fp8 else ko, w[b:b + 1].cpu(),
+                                        torch.tensor([0]), torch.tensor([L]), **kw)[0]
+        torch.testing.assert_close(sc[b, :L].double().cpu(), ref64, rtol=2e-3 if fp8 else 1e-4,
+                                   atol=2e-3 if fp8 else 1e-5)
+        exact = set((O.topk_indices(ref64[None], K)[0] + o).tolist())
+        exact.discard(o - 1)
+        got = set(idx[b][idx[b] >= 0].tolist())
+        inter += len(got & exact)
+        tot += len(exact)
+    assert inter / tot >= 0.999, inter / tot
