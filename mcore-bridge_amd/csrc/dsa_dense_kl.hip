@@ -16,7 +16,7 @@
 //       headroom, the sparse forward's scheme) each element costs one fma, one exp2, one add
 //       and one max; the whole query is recomputed with its exact maximum if a score overshoots.
 //       That work for block b-1 runs in the issue slots between block b's QK MFMAs.
-//   dense_target_kernel  S = Q . K^T (lane = key, 16 heads per lane): exp2(scale*s - lse) summed
+//   attn_target_kernel   S = Q . K^T (lane = key, 16 heads per lane): exp2(scale*s - lse) summed
 //       over the lane's heads, its half-wave partner's and (through LDS) the other waves'.  Block
 //       b-1's exps again run between block b's MFMAs, and its cross-wave sum is stored after the
 //       barrier of block b+1: one barrier per block.
@@ -45,8 +45,28 @@ constexpr float kHeadroom = 64.0f;      // log2 headroom above the reference max
 struct DenseSmem {
   char tile[kStages][kTileBytes];
   float red[3][4][32];   // target: per-wave head sums of the keys of the last three blocks
+  int32_t ids[3][64];    // sparse target: index-row slices of blocks b, b + 1, b + 2 (32 used)
   int flag;
 };
+
+// Gather sources of one block from a slice of an index row in LDS (ids[k] = kv row of key k of the
+// block; entries outside kv load row 0 and are masked by the caller).
+template <int NW>
+DSA_DEV TileSrc<NW> index_sources(const bf16_t* kv, const int32_t* ids, int n_kv, int wave, int lane) {
+  auto row = [&](int k) {
+    const int x = ids[k];
+    return x >= 0 && x < n_kv ? x : 0;
+  };
+  TileSrc<NW> s;
+  s.v = kv_row_addr(kv, row(wave + NW * (lane % (32 / NW))));
+#pragma unroll
+  for (int j = 0; j < 4 / NW; ++j) {
+    const int key = 8 * (wave + NW * j) + (lane >> 3);
+    const uint32_t c = (uint32_t)(lane & 7) ^ ((key >> 1) & 7u);
+    s.rope[j] = kv_row_addr(kv, row(key)) + (64 + c) * 16;
+  }
+  return s;
+}
 
 // Gather sources of one block of a contiguous key range: key k of the block is kv row row0 + k
 // for k < nvalid; the others (past the row's end) load row0 and are masked by the caller.
@@ -245,11 +265,13 @@ __global__ __launch_bounds__(NW * 64, kWgPerCu) void dense_lse_kernel(DenseKlPar
 }
 
 // ------------------------------------------------------------------------------------------
-// Target: target[t, j] = (1/H) sum_h exp(scale * s - lse[t,h]) for j < min(row_len, pitch), 0 for
-// the other columns j < pitch.
+// Target: target[t, j] = (1/H) sum_h exp(scale * s - lse[t,h]) over the keys of row t: IDX = false,
+// the dense row (key row_base[t] + j for j < min(row_len, pitch), 0 for the other columns j <
+// pitch); IDX = true, the index row (key idx[t, j], 0 at entries that are none).  The index row is
+// read in 32-entry slices, each copied into a 3-slot LDS ring two blocks before its tile's gather.
 // ------------------------------------------------------------------------------------------
-template <int NW>
-__global__ __launch_bounds__(NW * 64, kWgPerCu) void dense_target_kernel(DenseKlParams p) {
+template <int NW, bool IDX>
+__global__ __launch_bounds__(NW * 64, kWgPerCu) void attn_target_kernel(DenseKlParams p) {
   __shared__ __attribute__((aligned(128))) DenseSmem sm;
   const int t = xcd_remap(blockIdx.x, p.n_xcd);
   if (t >= p.total_q) return;
@@ -257,10 +279,39 @@ __global__ __launch_bounds__(NW * 64, kWgPerCu) void dense_target_kernel(DenseKl
   const int hb = lane >> 5, hl = lane & 31;
   const int head = wave * 32 + hl;
   const bool head_ok = head < p.n_heads;
-  int row0, len;
-  query_range(p, t, row0, len);
-  const int ncols = min(len, p.pitch);
-  const int nblk = (ncols + kBK - 1) / kBK;
+  int row0 = 0, ncols;
+  const int32_t* irow = nullptr;
+  auto entry_ok = [&](int x) { return x >= 0 && x < p.n_kv && (!p.causal || x <= t); };
+  if constexpr (IDX) {
+    // the row's blocks end with its last entry that is a key: every load issued before any is used
+    irow = p.idx + (int64_t)t * p.idx_stride;
+    constexpr int kBatch = 8;
+    int last = -1;
+    for (int j0 = threadIdx.x; j0 < p.pitch; j0 += kBatch * NW * 64) {
+      int v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int j = j0 + i * NW * 64;
+        v[i] = j < p.pitch ? irow[j] : -1;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i)
+        if (entry_ok(v[i])) last = j0 + i * NW * 64;
+    }
+    last = wave_max_i(last);
+    if (lane == 0) sm.red[0][wave][0] = __builtin_bit_cast(float, last);
+    __syncthreads();
+    last = -1;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) last = max(last, __builtin_bit_cast(int, sm.red[0][w][0]));
+    __syncthreads();
+    ncols = last + 1;
+  } else {
+    int len;
+    query_range(p, t, row0, len);
+    ncols = min(len, p.pitch);
+  }
+  const int nblk = __builtin_amdgcn_readfirstlane((ncols + kBK - 1) / kBK);
   float* trow = p.target + (int64_t)t * p.target_stride;
   for (int j = nblk * kBK + threadIdx.x; j < p.pitch; j += NW * 64) trow[j] = 0.f;
   if (nblk == 0) return;
@@ -278,17 +329,32 @@ __global__ __launch_bounds__(NW * 64, kWgPerCu) void dense_target_kernel(DenseKl
   wait_vmcnt0();   // Q and LSE retired before the copies
 
   const uint32_t tile0 = lds_addr(sm.tile[0]);
+  const uint32_t ids0 = lds_addr(sm.ids[0]);
   const uint32_t wsg = __builtin_amdgcn_readfirstlane(wave);
   const float c2 = p.scale_log2;
   const float inv_h = 1.f / (float)p.n_heads;
-  gather_range<NW>(tile0, range_sources<NW>(p.kv, row0, ncols, wave, lane), wave, lane);
+  // index-row slice of block b into ring slot b % 3 (wave 0; entries 32b .. 32b + 63, clamped)
+  auto copy_ids = [&](int b) {
+    if (wave == 0) async_copy4_unordered(irow + min(kBK * b + lane, p.pitch - 1), ids0 + (b % 3) * 256u);
+  };
+  auto sources = [&](int b) {
+    if constexpr (IDX) return index_sources<NW>(p.kv, sm.ids[b % 3], p.n_kv, wave, lane);
+    else return range_sources<NW>(p.kv, row0 + b * kBK, ncols - b * kBK, wave, lane);
+  };
+  if constexpr (IDX) {
+    copy_ids(0);
+    if (nblk > 1) copy_ids(1);
+    wait_vmcnt0();
+    __syncthreads();
+  }
+  gather_range<NW>(tile0, sources(0), wave, lane);
   // block b's per-wave sums (key hl of the block) go to slot b % 3 in iteration b + 1; wave 0 stores
   // the block's columns after the barrier of iteration b + 2 (every wave's sum is in), and block
   // b + 3 reuses the slot only after the barrier of iteration b + 3 (or in the tail, after the
   // last iteration's barrier): each slot access is ordered by a barrier
-  auto publish = [&](int b, float r) {
+  auto publish = [&](int b, float r, bool key_ok) {
     r = xor32_sum(r);
-    if (b * kBK + hl >= ncols) r = 0.f;
+    if (b * kBK + hl >= ncols || !key_ok) r = 0.f;
     if (hb == 0) sm.red[b % 3][wave][hl] = r;
   };
   auto store = [&](int b) {
@@ -301,14 +367,23 @@ __global__ __launch_bounds__(NW * 64, kWgPerCu) void dense_target_kernel(DenseKl
   };
   f32x16 sp = f32x16{};   // S of the previous block
   float r = 0.f;
+  bool ok_prev = true;    // IDX: key hl of the previous block is a key
   uint32_t st_cur = 0, st_next = kTileBytes;
   for (int blk = 0; blk < nblk; ++blk) {
-    wait_vmcnt<0>();   // block blk's copies (and wave 0's earlier stores)
+    wait_vmcnt<0>();   // block blk's copies, block blk + 1's index slice (and wave 0's earlier stores)
     __syncthreads();
     if (blk >= 2) store(blk - 2);
+    bool ok_cur = true;
+    if constexpr (IDX) {
+      // this block's entry of key hl, read before the slot is refilled (three iterations on)
+      const int x = sm.ids[blk % 3][hl];
+      ok_cur = entry_ok(x);
+      asm volatile("" ::"v"(ok_cur ? 1 : 0));
+      if (blk + 2 < nblk) copy_ids(blk + 2);
+    }
     const bool gather_next = blk + 1 < nblk;
     TileSrc<NW> nsrc{};
-    if (gather_next) nsrc = range_sources<NW>(p.kv, row0 + (blk + 1) * kBK, ncols - (blk + 1) * kBK, wave, lane);
+    if (gather_next) nsrc = sources(blk + 1);
     const TileDst nd = tile_dst<NW>(tile0 + st_next, wsg);
     const uint32_t tb = tile0 + st_cur;
     st_cur ^= kTileBytes;
@@ -326,14 +401,15 @@ __global__ __launch_bounds__(NW * 64, kWgPerCu) void dense_target_kernel(DenseKl
     } else {
       s = gather_next ? qk_block<NW, false, true>(tb, qf, nd, nsrc, lane, step)
                       : qk_block<NW, false, false>(tb, qf, nd, nsrc, lane, step);
-      publish(blk - 1, r);
+      publish(blk - 1, r, ok_prev);
       r = 0.f;
     }
     sp = s;
+    ok_prev = ok_cur;
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e) r += fast_exp2(__builtin_fmaf(sp[e], c2, -lse2[e]));
-  publish(nblk - 1, r);
+  publish(nblk - 1, r, ok_prev);
   __syncthreads();
   if (nblk >= 2) store(nblk - 2);
   store(nblk - 1);
@@ -350,15 +426,19 @@ int launch_dense_lse(const DenseKlParams& p, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int launch_dense_target(const DenseKlParams& p, hipStream_t stream) {
+template <bool IDX>
+static int launch_target(const DenseKlParams& p, hipStream_t stream) {
   if (p.n_xcd < 1) return -1;
   if (p.total_q == 0) return 0;
   const dim3 grid(xcd_grid(p.total_q, p.n_xcd));
   const int nw = p.n_heads > 64 ? 4 : (p.n_heads > 32 ? 2 : 1);
-  if (nw == 4) hipLaunchKernelGGL(dense_target_kernel<4>, grid, dim3(256), 0, stream, p);
-  else if (nw == 2) hipLaunchKernelGGL(dense_target_kernel<2>, grid, dim3(128), 0, stream, p);
-  else hipLaunchKernelGGL(dense_target_kernel<1>, grid, dim3(64), 0, stream, p);
+  if (nw == 4) hipLaunchKernelGGL((attn_target_kernel<4, IDX>), grid, dim3(256), 0, stream, p);
+  else if (nw == 2) hipLaunchKernelGGL((attn_target_kernel<2, IDX>), grid, dim3(128), 0, stream, p);
+  else hipLaunchKernelGGL((attn_target_kernel<1, IDX>), grid, dim3(64), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
+
+int launch_dense_target(const DenseKlParams& p, hipStream_t stream) { return launch_target<false>(p, stream); }
+int launch_sparse_target(const DenseKlParams& p, hipStream_t stream) { return launch_target<true>(p, stream); }
 
 }  // namespace dsa

@@ -142,6 +142,11 @@ struct DenseKlParams {
   int64_t q_stride_t, target_stride;
   float scale_log2;         // softmax scale * log2(e)
   int n_xcd;                // XCDs of the device (xcd_remap / xcd_grid)
+  // sparse target (index rows instead of key ranges): idx [total_q, pitch] kv row ids, -1 = none;
+  // entries outside kv or (causal) after the query are none too
+  const int32_t* idx;
+  int64_t idx_stride;
+  int causal;
 };
 
 struct KlFromPParams {
@@ -243,6 +248,7 @@ int launch_indexer_kl(const KlLossParams& p, hipStream_t stream);
 int launch_indexer_kl_target_from_p(const KlFromPParams& p, hipStream_t stream);
 int launch_dense_lse(const DenseKlParams& p, hipStream_t stream);
 int launch_dense_target(const DenseKlParams& p, hipStream_t stream);
+int launch_sparse_target(const DenseKlParams& p, hipStream_t stream);
 int launch_indexer_selected_scores(const IdxSelParams& p, hipStream_t stream);
 int launch_indexer_scores_bwd(const IdxSelParams& p, hipStream_t stream);
 // Key-major order of the selected (query, slot) pairs, ascending in query inside each key

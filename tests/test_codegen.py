@@ -173,8 +173,8 @@ def _violations(asm_text):
     return bad
 
 
-@pytest.mark.parametrize("src", ["dsa_sparse_fwd.hip", "dsa_sparse_bwd.hip", "dsa_indexer.hip", "dsa_indexer_kl.hip",
-                                 "dsa_indexer_bwd.hip", "dsa_dense_kl.hip"])
+@pytest.mark.parametrize("src", ["dsa_sparse_fwd.hip", "dsa_sparse_bwd.hip", "dsa_indexer.hip", "dsa_indexer_bwd.hip",
+                                 "dsa_dense_kl.hip"])
 def test_no_valu_write_right_before_mfma(src, tmp_path):
     out = tmp_path / (src + ".s")
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
