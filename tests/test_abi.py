@@ -259,3 +259,58 @@ def test_launching_entry_points_report_a_missing_device():
     assert lib.dsa_sparse_mla_fwd(N, P, P, 4, 4, 16, 576, 512, 8, 0.1, 1, P, P, N) == _lib.DSA_ERR_INVALID_ARG
     assert lib.dsa_sparse_mla_decode(P, P, P, 64, 100, 128, 576, 512, 2048, 0.1, P, P, P, need - 1, N) == \
         _lib.DSA_ERR_WORKSPACE
+
+
+def test_dense_loss_entry_points_validate_and_size():
+    """The dense indexer-loss entry points: d_qk 576 and at most 128 heads for the attention
+    statistics, head_dim 128 and at most 64 heads for the score backward, a pitch of at least one
+    column, aligned rows, a workspace of the documented size; empty work is a no-op."""
+    lib = _lib.load()
+    lse = lambda q, dqk, H, sc, T=4: lib.dsa_dense_attention_lse(q, P, P, P, T, 8, H, dqk, sc, P, N)
+    assert lse(P, 512, 16, 0.1) == _lib.DSA_ERR_UNSUPPORTED
+    assert lse(P, 576, 129, 0.1) == _lib.DSA_ERR_UNSUPPORTED
+    assert lse(N, 576, 16, 0.1) == _lib.DSA_ERR_INVALID_ARG
+    assert lse(ctypes.c_void_p(4100), 576, 16, 0.1) == _lib.DSA_ERR_INVALID_ARG
+    assert lse(P, 576, 16, float("nan")) == _lib.DSA_ERR_INVALID_ARG
+    assert lse(P, 576, 16, -1.0) == _lib.DSA_ERR_INVALID_ARG
+    assert lse(N, 576, 16, 0.1, T=0) == _lib.DSA_OK
+    assert lib.dsa_dense_attention_lse(P, P, P, P, 4, 8, 16, 576, 0.1, N, N) == _lib.DSA_ERR_INVALID_ARG
+    tgt = lambda pitch, lse_, T=4: lib.dsa_dense_attention_target(P, P, lse_, P, P, T, 8, 16, 576, pitch, 0.1, P, N)
+    assert tgt(0, P) == _lib.DSA_ERR_INVALID_ARG
+    assert tgt(8, N) == _lib.DSA_ERR_INVALID_ARG
+    assert tgt(8, N, T=0) == _lib.DSA_OK
+    # score backward: one 64 KB partial dk tile per (128-key tile, 256-query chunk)
+    T, Nk = 16384, 16384
+    ws = lib.dsa_dense_indexer_scores_bwd_workspace_size(T, Nk)
+    assert ws == (Nk // 128) * (T // 256) * 128 * 128 * 4
+    assert lib.dsa_dense_indexer_scores_bwd_workspace_size(0, Nk) == 0
+    assert lib.dsa_dense_indexer_scores_bwd_workspace_size(T, 0) == 0
+    bwd = lambda H, D, pitch, ws_, nbytes, dq=P: lib.dsa_dense_indexer_scores_bwd(
+        P, P, P, P, P, 4, 8, H, D, P, pitch, dq, P, P, ws_, nbytes, N)
+    need = lib.dsa_dense_indexer_scores_bwd_workspace_size(4, 8)
+    assert bwd(65, 128, 8, P, need) == _lib.DSA_ERR_UNSUPPORTED
+    assert bwd(64, 64, 8, P, need) == _lib.DSA_ERR_UNSUPPORTED
+    assert bwd(64, 128, 0, P, need) == _lib.DSA_ERR_INVALID_ARG
+    assert bwd(64, 128, 8, P, need, dq=N) == _lib.DSA_ERR_INVALID_ARG
+    assert bwd(64, 128, 8, P, need - 1) == _lib.DSA_ERR_WORKSPACE
+    assert bwd(64, 128, 8, N, need) == _lib.DSA_ERR_WORKSPACE
+    # no query rows: only dk is needed (written as zeros); without it the call is refused
+    assert lib.dsa_dense_indexer_scores_bwd(N, N, N, N, N, 0, 8, 64, 128, N, 8, N, N, N, N, 0, N) == \
+        _lib.DSA_ERR_INVALID_ARG
+    if not _has_device():
+        assert lib.dsa_dense_attention_lse(P, P, P, P, 4, 8, 16, 576, 0.1, P, N) == _lib.DSA_ERR_DEVICE
+        assert lib.dsa_dense_indexer_scores_bwd(P, P, P, P, P, 4, 8, 64, 128, P, 8, P, P, P, P, need, N) == \
+            _lib.DSA_ERR_DEVICE
+
+
+def test_dense_loss_ops_refuse_cpu_tensors():
+    import torch
+    from mcore_bridge_amd import ops
+    q = torch.zeros(4, 16, 576, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 576, dtype=torch.bfloat16)
+    rows = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.dense_attention_lse(q, kv, rows, rows + 1, 1, 0.1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.indexer_scores_dense_bwd(torch.zeros(4, 8, 128, dtype=torch.bfloat16), torch.zeros(4, 128, dtype=torch.bfloat16),
+                                     torch.zeros(4, 8), rows, rows + 1, 1, torch.zeros(4, 4))
