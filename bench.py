@@ -23,7 +23,8 @@ The line also carries:
   "indexer_kl_dense"  the dense indexer KL loss (the reference default) at cfg3: its LSE and target
                       kernels and the whole loss forward + backward;
   "v4"                the DeepSeek-V4 CSA layer core (sink attention fwd + bwd, 512-wide K = V) at
-                      T = 16384, H = 128, window 128 + top-512 compressed entries;
+                      T = 16384, H = 128, window 128 + top-512 compressed entries, and the layer's
+                      main compressor (pooling + norm kernels, forward and forward + backward);
   "cpu_baseline"      the oracle's reference-shaped fp32 compositions timed on the host per config
                       (cfg1 whole; cfg2/cfg3/cfg4 a few query rows, extrapolated by visible keys;
                       cfg5 every sequence) -- a reported baseline, not the target.
@@ -462,7 +463,9 @@ def v4_leg(torch, dev, reps: int = 5):
     1024-byte G rows), take the K = V rows in the 576-wide row layout (rope region zero)
     and fold the sink in (the forward's epilogue, Delta from B1, one d sink kernel), so
     `kernels_ms` (the sink entry points on pre-padded key rows) is what the kernels take and
-    `host_composition_ms` the rest: the key rows' pad copy, the dkv slice, autograd."""
+    `host_composition_ms` the rest: the key rows' pad copy, the dkv slice, autograd.
+    `csa_compressor_*_ms`: the CSA main compressor (rate 4, overlapping windows, 2 x 512-channel
+    kv / gate rows of the T tokens) through v4.compress, host calls and autograd included."""
     from mcore_bridge_amd import ops, v4
     T, H, D, Wn, rate, Kc, Hi, Di = 16384, 128, 512, 128, 4, 512, 64, 128
     cu = [0, T]
@@ -494,6 +497,22 @@ def v4_leg(torch, dev, reps: int = 5):
 
     t_all = _time_ms(torch, layer_core, reps)
     t_k = _time_ms(torch, kernels_only, reps)
+    # the CSA layer's main compressor (kv / gate projections of the T tokens, rate 4, overlapping
+    # windows of 2 x 512 channels) through v4.compress on the HIP kernels, host calls included
+    C = 2 * D
+    ckv = torch.randn(T, C, generator=g, device=dev).bfloat16()
+    cgt = (torch.randn(T, C, generator=g, device=dev) * 2).bfloat16()
+    cape = (torch.randn(rate, C, generator=g, device=dev) * 0.5).bfloat16()
+    cnw = torch.ones(D, device=dev, dtype=torch.bfloat16)
+    cdo = (torch.randn(T // rate, D, generator=g, device=dev) * 0.1).bfloat16()
+
+    def comp_fwd_bwd():
+        leaves = [t.detach().requires_grad_() for t in (ckv, cgt, cape, cnw)]
+        v4.compress(*leaves, cu, rate, 1e-6, True).backward(cdo)
+
+    with torch.no_grad():
+        t_cf = _time_ms(torch, lambda: v4.compress(ckv, cgt, cape, cnw, cu, rate, 1e-6, True), reps)
+    t_cfb = _time_ms(torch, comp_fwd_bwd, reps)
     fl = (2 * (D + D) + 2 * (3 * D + 2 * D)) * H * nsel
     tf = fl / (t_all * 1e-3) / 1e12
     tfk = fl / (t_k * 1e-3) / 1e12
@@ -503,6 +522,7 @@ def v4_leg(torch, dev, reps: int = 5):
             "n_sel": nsel, "flops": fl, "ms": round(t_all, 3), "tflops": round(tf, 1),
             "kernels_ms": round(t_k, 3), "kernels_tflops": round(tfk, 1),
             "host_composition_ms": round(t_all - t_k, 3), "csa_indexer_ms": round(t_sel, 3),
+            "csa_compressor_fwd_ms": round(t_cf, 3), "csa_compressor_fwd_bwd_ms": round(t_cfb, 3),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / PEAK_BF16_TFLOPS, 4)}}
 

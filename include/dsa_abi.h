@@ -250,6 +250,41 @@ int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, c
                             float* dkv, float* dsinks, int flags, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* DeepSeek-V4 compressor (the compressed layers' `core_attention.compressor` and the CSA
+ * indexer's compressor, parameters ape / linear_wkv / linear_wgate / norm mapped at
+ * src/mcore_bridge/model/gpts/deepseek_v4.py:447-464; the module itself lives in megatron-core,
+ * outside the reference): every complete window of `rate` tokens of each document becomes one
+ * entry, out[e] = RMSNorm(sum_s softmax_s(gate[t_s] + ape[s]) * kv[t_s]) * norm_w, the softmax
+ * per channel over the window's slots; with overlap (CSA) kv and gate are 2 * dim wide and
+ * entry e pools the previous window's first halves and its own second halves (a document's
+ * first window: its own only).  Pooled sums are rounded to bf16 before the norm, the normalised
+ * row to bf16 before the weight (the module's dtype steps).
+ *   kv, gate: [total_tokens, channels] bf16, row strides kv_stride / gate_stride (elements, even
+ *     multiples of 8); channels = 2 * dim (overlap) or dim; dim in {64, 128, 256, 512};
+ *   ape [rate, channels] bf16, norm_w [dim] bf16, out [n_entries, dim] bf16 (document order);
+ *   doc_table: device int32 [3, n_docs + 1] -- cu_seqlens, entry offsets (prefix sums of
+ *     len / rate, the last one n_entries) and item offsets (prefix sums of ceil(len / rate), the
+ *     last one n_items); cu_seqlens[n_docs] = total_tokens.  A window whose rows fall outside
+ *     [0, total_tokens) (a table that breaks these rules) yields a zero entry and no gradient.
+ * No reference counterpart in this repository (its compressor runs in megatron-core); the
+ * computation follows transformers' DeepseekV4 compressor, which the CPU oracle restates. */
+int dsa_v4_compress_fwd(const void* kv, const void* gate, int64_t kv_stride, int64_t gate_stride, const void* ape,
+                        const void* norm_w, const int32_t* doc_table, int n_docs, int total_tokens, int n_entries,
+                        int channels, int dim, int rate, int overlap, float eps, void* out, void* stream);
+
+/* Workspace bytes for dsa_v4_compress_bwd. */
+size_t dsa_v4_compress_bwd_workspace_size(int n_entries, int n_items, int channels, int dim, int rate);
+
+/* Backward of dsa_v4_compress_fwd given dout [n_entries, dim] bf16: dkv and dgate [total_tokens,
+ * channels] bf16 (row strides dkv_stride / dgate_stride; every element of every row written,
+ * zero where a token feeds no entry), dape [rate, channels] and dnorm_w [dim] fp32.  The pooling
+ * is recomputed from kv and gate; deterministic (fixed-order sums, no atomics). */
+int dsa_v4_compress_bwd(const void* kv, const void* gate, int64_t kv_stride, int64_t gate_stride, const void* ape,
+                        const void* norm_w, const int32_t* doc_table, int n_docs, int total_tokens, int n_entries,
+                        int n_items, int channels, int dim, int rate, int overlap, float eps, const void* dout,
+                        void* dkv, void* dgate, int64_t dkv_stride, int64_t dgate_stride, float* dape,
+                        float* dnorm_w, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Flags of dsa_sparse_mla_bwd_ex.
  * DSA_BWD_G_INT8: stage the per-(query, key) dKV partial rows as int8 with a bf16 scale per 32
  *   dims (640 bytes a row instead of 1152 in bf16): ~45% less of the backward's largest memory

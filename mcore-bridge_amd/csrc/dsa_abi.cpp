@@ -765,4 +765,80 @@ int dsa_indexer_scores_bwd(const void* q, const void* k, const float* w, const i
   return dsa::launch_indexer_scores_bwd(p, as_stream(stream));
 }
 
+// ---- DeepSeek-V4 compressor
+static int compress_params(const void* kv, const void* gate, int64_t kv_stride, int64_t gate_stride, const void* ape,
+                           const void* norm_w, const int32_t* doc_table, int n_docs, int total_tokens, int n_entries,
+                           int n_items, int channels, int dim, int rate, int overlap, float eps,
+                           dsa::CompressParams& p) {
+  if (n_docs < 1 || total_tokens < 0 || n_entries < 0 || n_items < 0 || rate < 1 || !std::isfinite(eps) || eps < 0.f)
+    return DSA_ERR_INVALID_ARG;
+  if (dim != 64 && dim != 128 && dim != 256 && dim != 512) return DSA_ERR_UNSUPPORTED;
+  if (channels != (overlap ? 2 * dim : dim)) return DSA_ERR_INVALID_ARG;
+  if ((int64_t)n_entries * rate > total_tokens || n_items > total_tokens || n_entries > n_items)
+    return DSA_ERR_INVALID_ARG;
+  if (kv_stride < channels || gate_stride < channels || kv_stride % 8 || gate_stride % 8) return DSA_ERR_INVALID_ARG;
+  if (!kv || !gate || !ape || !norm_w || !doc_table) return DSA_ERR_INVALID_ARG;
+  if (!aligned16(kv) || !aligned16(gate) || !aligned16(ape) || !aligned16(norm_w)) return DSA_ERR_INVALID_ARG;
+  p.kv = static_cast<const dsa::bf16_t*>(kv);
+  p.gate = static_cast<const dsa::bf16_t*>(gate);
+  p.ape = static_cast<const dsa::bf16_t*>(ape);
+  p.norm_w = static_cast<const dsa::bf16_t*>(norm_w);
+  p.doc_table = doc_table;
+  p.n_docs = n_docs; p.total_tokens = total_tokens; p.n_entries = n_entries; p.n_items = n_items;
+  p.channels = channels; p.dim = dim; p.rate = rate; p.overlap = overlap ? 1 : 0; p.eps = eps;
+  p.kv_stride = kv_stride; p.gate_stride = gate_stride;
+  return DSA_OK;
+}
+
+int dsa_v4_compress_fwd(const void* kv, const void* gate, int64_t kv_stride, int64_t gate_stride, const void* ape,
+                        const void* norm_w, const int32_t* doc_table, int n_docs, int total_tokens, int n_entries,
+                        int channels, int dim, int rate, int overlap, float eps, void* out, void* stream) {
+  dsa::CompressParams p{};
+  // the forward has no items of its own: n_items = n_entries passes the item checks
+  const int rc = compress_params(kv, gate, kv_stride, gate_stride, ape, norm_w, doc_table, n_docs, total_tokens,
+                                 n_entries, n_entries, channels, dim, rate, overlap, eps, p);
+  if (rc != DSA_OK) return rc;
+  if (n_entries == 0) return DSA_OK;
+  if (!out || !aligned16(out)) return DSA_ERR_INVALID_ARG;
+  p.out = static_cast<dsa::bf16_t*>(out);
+  DSA_CHECK_DEVICE(dev);
+  return dsa::launch_v4_compress_fwd(p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+size_t dsa_v4_compress_bwd_workspace_size(int n_entries, int n_items, int channels, int dim, int rate) {
+  if (n_entries < 0 || n_items < 0 || channels < 1 || dim < 1 || rate < 1) return 0;
+  const dsa::CompressBwdGrid g = dsa::compress_bwd_grid(n_entries, n_items, channels, dim, rate);
+  return align_up(sizeof(float) * (size_t)g.dnorm_floats) + align_up(sizeof(float) * (size_t)g.dape_floats) +
+         align_up(sizeof(int32_t) * (size_t)g.entry_ints);
+}
+
+int dsa_v4_compress_bwd(const void* kv, const void* gate, int64_t kv_stride, int64_t gate_stride, const void* ape,
+                        const void* norm_w, const int32_t* doc_table, int n_docs, int total_tokens, int n_entries,
+                        int n_items, int channels, int dim, int rate, int overlap, float eps, const void* dout,
+                        void* dkv, void* dgate, int64_t dkv_stride, int64_t dgate_stride, float* dape,
+                        float* dnorm_w, void* workspace, size_t workspace_bytes, void* stream) {
+  dsa::CompressParams p{};
+  const int rc = compress_params(kv, gate, kv_stride, gate_stride, ape, norm_w, doc_table, n_docs, total_tokens,
+                                 n_entries, n_items, channels, dim, rate, overlap, eps, p);
+  if (rc != DSA_OK) return rc;
+  if (!dape || !dnorm_w || !dkv || !dgate || (n_entries > 0 && !dout)) return DSA_ERR_INVALID_ARG;
+  if (dkv_stride < channels || dgate_stride < channels || dkv_stride % 8 || dgate_stride % 8)
+    return DSA_ERR_INVALID_ARG;
+  if (!aligned16(dkv) || !aligned16(dgate) || (dout && !aligned16(dout))) return DSA_ERR_INVALID_ARG;
+  const size_t need = dsa_v4_compress_bwd_workspace_size(n_entries, n_items, channels, dim, rate);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return DSA_ERR_WORKSPACE;
+  const dsa::CompressBwdGrid g = dsa::compress_bwd_grid(n_entries, n_items, channels, dim, rate);
+  char* ws = static_cast<char*>(workspace);
+  p.dout = static_cast<const dsa::bf16_t*>(dout);
+  p.dkv = static_cast<dsa::bf16_t*>(dkv);
+  p.dgate = static_cast<dsa::bf16_t*>(dgate);
+  p.dkv_stride = dkv_stride; p.dgate_stride = dgate_stride;
+  p.dnorm_part = reinterpret_cast<float*>(ws);
+  const size_t dape_off = align_up(sizeof(float) * (size_t)g.dnorm_floats);
+  p.dape_part = reinterpret_cast<float*>(ws + dape_off);
+  p.entry_tok = reinterpret_cast<int32_t*>(ws + dape_off + align_up(sizeof(float) * (size_t)g.dape_floats));
+  DSA_CHECK_DEVICE(dev);
+  return dsa::launch_v4_compress_bwd(p, dape, dnorm_w, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
 }  // extern "C"

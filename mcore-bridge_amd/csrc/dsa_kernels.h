@@ -284,4 +284,35 @@ int launch_build_decode_rows(const int32_t* cu_cache, int batch, int32_t* row_ba
 int launch_build_rows(const int32_t* cu_seqlens, int n_seq, int total_q, int causal, int32_t* row_base,
                       int32_t* row_len, hipStream_t stream);
 
+// DeepSeek-V4 compressor (dsa_v4_compress.hip): softmax-gated pooling of each complete window of
+// `rate` tokens + RMS norm.  doc_table = device int32 [3][n_docs + 1]: token offsets, entry offsets
+// (prefix sums of len / rate), backward item offsets (prefix sums of ceil(len / rate)).
+struct CompressParams {
+  const bf16_t* kv;         // [total_tokens, channels], row stride kv_stride
+  const bf16_t* gate;       // [total_tokens, channels], row stride gate_stride
+  const bf16_t* ape;        // [rate, channels]
+  const bf16_t* norm_w;     // [dim]
+  const int32_t* doc_table;
+  int n_docs, total_tokens, n_entries, n_items, channels, dim, rate, overlap;
+  float eps;
+  int64_t kv_stride, gate_stride;
+  bf16_t* out;              // forward: [n_entries, dim]
+  const bf16_t* dout;       // backward: [n_entries, dim]
+  bf16_t* dkv;              // backward: [total_tokens, channels], row stride dkv_stride
+  bf16_t* dgate;            // backward: [total_tokens, channels], row stride dgate_stride
+  int64_t dkv_stride, dgate_stride;
+  float* dnorm_part;        // backward workspace: [bwd_wg, dim]
+  float* dape_part;         // backward workspace: [ape_chunks, rate, channels]
+  int32_t* entry_tok;       // backward workspace: [n_entries] first token of each entry's window
+};
+struct CompressBwdGrid {
+  int bwd_wg, ape_chunks, entries_per_chunk;
+  int64_t dnorm_floats, dape_floats;   // workspace floats of the two partial buffers
+  int64_t entry_ints;                  // workspace int32 of the entry_tok row
+};
+CompressBwdGrid compress_bwd_grid(int n_entries, int n_items, int channels, int dim, int rate);
+int launch_v4_compress_fwd(const CompressParams& p, hipStream_t stream);
+// dape [rate, channels] and dnorm [dim] fp32 outputs
+int launch_v4_compress_bwd(const CompressParams& p, float* dape, float* dnorm, hipStream_t stream);
+
 }  // namespace dsa

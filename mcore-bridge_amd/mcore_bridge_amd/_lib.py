@@ -87,6 +87,12 @@ SIGNATURES = {
     "dsa_dense_indexer_scores_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                              c_int, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
                                              c_void_p]),
+    "dsa_v4_compress_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                    c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p]),
+    "dsa_v4_compress_bwd_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "dsa_v4_compress_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                    c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p,
+                                    c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsa_indexer_kl_loss": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "dsa_indexer_selected_scores": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

@@ -840,3 +840,91 @@ def dense_attention_target(q: Tensor, kv: Tensor, lse: Tensor, row_base: Tensor,
         _lib.call("dsa_dense_attention_target", _p(q), _p(kv), _p(lse), _p(rb), _p(rl), T, kv.shape[0], H, D_QK,
                   int(pitch), float(sm_scale), _p(tgt), _stream(q.device))
     return tgt
+
+
+# --------------------------------------------------------------------------------------
+# DeepSeek-V4 compressor (softmax-gated window pooling + RMS norm)
+# --------------------------------------------------------------------------------------
+_DOC_TABLES: dict = {}   # (cu, rate, device) -> table: layers re-use their documents' table
+
+
+def compress_doc_table(cu_seqlens, rate: int, device) -> Tuple[Tensor, int, int]:
+    """Document table of the V4 compressor entry points: int32 ``[3, n_docs + 1]`` on ``device``
+    (token offsets, entry offsets = prefix sums of ``len // rate``, backward item offsets = prefix
+    sums of ``ceil(len / rate)``), the number of entries and of backward items.  Tables are kept
+    per (documents, rate, device), at most 64 of them, so repeated calls copy nothing."""
+    cu = [int(x) for x in cu_seqlens]
+    key = (tuple(cu), int(rate), str(torch.device(device)))
+    hit = _DOC_TABLES.get(key)
+    if hit is not None:
+        return hit
+    _require(len(cu) >= 2 and cu[0] == 0 and all(b >= a for a, b in zip(cu[:-1], cu[1:])),
+             "cu_seqlens must start at 0 and be non-decreasing")
+    _require(rate >= 1, "rate must be >= 1")
+    coff, ioff = [0], [0]
+    for a, b in zip(cu[:-1], cu[1:]):
+        coff.append(coff[-1] + (b - a) // rate)
+        ioff.append(ioff[-1] + (b - a + rate - 1) // rate)
+    tab = torch.tensor([cu, coff, ioff], dtype=torch.int32).to(device)
+    if len(_DOC_TABLES) >= 64:
+        _DOC_TABLES.pop(next(iter(_DOC_TABLES)))
+    _DOC_TABLES[key] = (tab, coff[-1], ioff[-1])
+    return tab, coff[-1], ioff[-1]
+
+
+def _check_compress(kv: Tensor, gate: Tensor, ape: Tensor, norm_w: Tensor, table: Tensor, rate: int,
+                    overlap: bool) -> Tuple[int, int]:
+    _require_gpu(kv, gate, ape, norm_w, table)
+    D = norm_w.numel()
+    C = 2 * D if overlap else D
+    _require(D in (64, 128, 256, 512), "compressor dim must be 64, 128, 256 or 512")
+    for name, t in (("kv", kv), ("gate", gate)):
+        _require(t.dim() == 2 and t.shape[1] == C and t.dtype == torch.bfloat16,
+                 f"{name} must be [T, {C}] bf16")
+        _require(t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0,
+                 f"{name} rows must be unit-stride, 16-byte aligned, row stride a multiple of 8")
+    _require(kv.shape[0] == gate.shape[0], "kv and gate must have the same rows")
+    _require(ape.shape == (rate, C) and ape.dtype == torch.bfloat16, f"ape must be [{rate}, {C}] bf16")
+    _require(norm_w.dtype == torch.bfloat16, "norm weight must be bf16")
+    _require(table.dtype == torch.int32 and table.dim() == 2 and table.shape[0] == 3, "doc table must be int32 [3, n+1]")
+    return C, D
+
+
+def v4_compress_fwd(kv: Tensor, gate: Tensor, ape: Tensor, norm_w: Tensor, table: Tensor, n_entries: int,
+                    rate: int, eps: float, overlap: bool) -> Tensor:
+    """Compressed entries ``[n_entries, D]`` bf16 (``dsa_v4_compress_fwd``): every complete window of
+    ``rate`` tokens of each document (``table`` from ``compress_doc_table``), softmax(gate + ape)-pooled
+    per channel (overlap: the previous window's first halves and this window's second halves), RMS
+    norm with ``norm_w``.  ``kv``, ``gate [T, C]`` bf16, ``ape [rate, C]``."""
+    C, D = _check_compress(kv, gate, ape, norm_w, table, rate, overlap)
+    T = kv.shape[0]
+    ape, norm_w = ape.contiguous(), norm_w.contiguous()
+    out = torch.empty(n_entries, D, dtype=torch.bfloat16, device=kv.device)
+    with torch.cuda.device(kv.device):
+        _lib.call("dsa_v4_compress_fwd", _p(kv), _p(gate), kv.stride(0), gate.stride(0), _p(ape), _p(norm_w),
+                  _p(table), table.shape[1] - 1, T, int(n_entries), C, D, int(rate), int(bool(overlap)), float(eps),
+                  _p(out), _stream(kv.device))
+    return out
+
+
+def v4_compress_bwd(kv: Tensor, gate: Tensor, ape: Tensor, norm_w: Tensor, table: Tensor, n_entries: int,
+                    n_items: int, rate: int, eps: float, overlap: bool, dout: Tensor):
+    """Backward of ``v4_compress_fwd`` (``dsa_v4_compress_bwd``): ``(dkv, dgate)`` bf16 ``[T, C]`` and
+    ``(dape [rate, C], dnorm_w [D])`` fp32, the pooling recomputed from ``kv`` and ``gate``."""
+    C, D = _check_compress(kv, gate, ape, norm_w, table, rate, overlap)
+    T = kv.shape[0]
+    _require(dout.shape == (n_entries, D) and dout.dtype == torch.bfloat16, f"dout must be [{n_entries}, {D}] bf16")
+    _require_gpu(dout)
+    ape, norm_w, dout = ape.contiguous(), norm_w.contiguous(), dout.contiguous()
+    dkv = torch.empty(T, C, dtype=torch.bfloat16, device=kv.device)
+    dgate = torch.empty(T, C, dtype=torch.bfloat16, device=kv.device)
+    dape = torch.empty(rate, C, dtype=torch.float32, device=kv.device)
+    dnorm = torch.empty(D, dtype=torch.float32, device=kv.device)
+    ws_bytes = int(_lib.load().dsa_v4_compress_bwd_workspace_size(int(n_entries), int(n_items), C, D, int(rate)))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=kv.device)
+    with torch.cuda.device(kv.device):
+        _lib.call("dsa_v4_compress_bwd", _p(kv), _p(gate), kv.stride(0), gate.stride(0), _p(ape), _p(norm_w),
+                  _p(table), table.shape[1] - 1, T, int(n_entries), int(n_items), C, D, int(rate),
+                  int(bool(overlap)), float(eps), _p(dout), _p(dkv), _p(dgate), C, C, _p(dape), _p(dnorm), _p(ws),
+                  ws.numel(), _stream(kv.device))
+    return dkv, dgate, dape, dnorm

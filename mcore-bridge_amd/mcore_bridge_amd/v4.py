@@ -148,7 +148,7 @@ def indexer_select(q_idx: Tensor, comp_k: Tensor, w: Tensor, cu_seqlens: Sequenc
 
 
 # --------------------------------------------------------------------------------------
-# host-side pieces of the layer (projections, norms, RoPE, compressors): torch
+# host-side pieces of the layer (projections, norms, RoPE): torch; the compressors' pooling: HIP
 # --------------------------------------------------------------------------------------
 def rope_interleaved(x: Tensor, angles: Tensor, mscale: float = 1.0, inverse: bool = False) -> Tensor:
     """Interleaved RoPE on the trailing ``2 * angles.shape[-1]`` dims of ``x [N, ..., D]`` with
@@ -171,31 +171,36 @@ def rms_norm(x: Tensor, weight: Optional[Tensor], eps: float) -> Tensor:
     return y if weight is None else y * weight
 
 
+class _Compress(torch.autograd.Function):
+    """The compressor's pooling + norm on the HIP kernels (``ops.v4_compress_fwd`` / ``_bwd``); the
+    backward recomputes the pooling from ``kv`` and ``gate``."""
+
+    @staticmethod
+    def forward(ctx, kv, gate, ape, norm_w, table, n_entries, n_items, rate, eps, overlap):
+        out = ops.v4_compress_fwd(kv, gate, ape, norm_w, table, n_entries, rate, eps, overlap)
+        ctx.save_for_backward(kv, gate, ape, norm_w, table)
+        ctx.meta = (n_entries, n_items, rate, eps, overlap)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        kv, gate, ape, norm_w, table = ctx.saved_tensors
+        dkv, dgate, dape, dnorm = ops.v4_compress_bwd(kv, gate, ape, norm_w, table, *ctx.meta,
+                                                      dout.to(torch.bfloat16).contiguous())
+        return dkv, dgate, dape.to(ape.dtype), dnorm.to(norm_w.dtype), None, None, None, None, None, None
+
+
 def compress(kv: Tensor, gate: Tensor, ape: Tensor, norm_w: Tensor, cu_seqlens: Sequence[int], rate: int, eps: float,
              overlap: bool) -> Tensor:
     """Compressed entries of every document (concatenated in document order): softmax-gated pooling
     of each complete ``rate``-token window (CSA: ``overlap``, ``2 * rate`` slots over the previous
-    window's first halves and this window's second halves), RMS norm.  ``kv``, ``gate [T, C]``,
-    ``ape [rate, C]``.  Returns ``[Nc, D]`` (before RoPE)."""
-    outs = []
+    window's first halves and this window's second halves), RMS norm -- one HIP kernel each way
+    (``dsa_v4_compress_fwd`` / ``dsa_v4_compress_bwd``).  ``kv``, ``gate [T, C]`` bf16, ``ape [rate, C]``.
+    Returns ``[Nc, D]`` (before RoPE)."""
     cu = [int(x) for x in cu_seqlens]
-    for a, b in zip(cu[:-1], cu[1:]):
-        n = (b - a) // rate
-        if n == 0:
-            continue
-        k = kv[a:a + n * rate].float().view(n, rate, -1)
-        g = gate[a:a + n * rate].float().view(n, rate, -1) + ape.float()
-        if overlap:
-            D = k.shape[-1] // 2
-            pk = torch.zeros_like(k[..., D:])
-            pg = torch.full_like(g[..., D:], float("-inf"))
-            pk[1:], pg[1:] = k[:-1, :, :D], g[:-1, :, :D]
-            k = torch.cat([pk, k[..., D:]], dim=1)
-            g = torch.cat([pg, g[..., D:]], dim=1)
-        outs.append((k * torch.softmax(g, dim=1)).sum(1))
-    D = norm_w.numel()
-    pooled = torch.cat(outs) if outs else kv.new_zeros((0, D), dtype=torch.float32)
-    return rms_norm(pooled.to(kv.dtype), norm_w, eps)
+    ops._require(cu[-1] == kv.shape[0], "cu_seqlens must end at the token count")
+    table, n_entries, n_items = ops.compress_doc_table(cu, rate, kv.device)
+    return _Compress.apply(kv, gate, ape, norm_w, table, n_entries, n_items, rate, eps, overlap)
 
 
 def compressed_positions(cu_seqlens: Sequence[int], rate: int, device) -> Tensor:

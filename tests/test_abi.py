@@ -314,3 +314,59 @@ def test_dense_loss_ops_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         ops.indexer_scores_dense_bwd(torch.zeros(4, 8, 128, dtype=torch.bfloat16), torch.zeros(4, 128, dtype=torch.bfloat16),
                                      torch.zeros(4, 8), rows, rows + 1, 1, torch.zeros(4, 4))
+
+
+def test_v4_compressor_entry_points_validate_and_size():
+    """The V4 compressor entry points: dim 64 / 128 / 256 / 512, channels = 2 * dim with overlap
+    (dim without), row strides of at least the channels in multiples of 8, entry and item counts
+    that the token count can hold, a workspace of the documented size; no entries is a no-op
+    forward."""
+    lib = _lib.load()
+    fwd = lambda C, D, ov, T=16, ne=4, stride=None, eps=1e-6, kv=P, out=P: lib.dsa_v4_compress_fwd(
+        kv, P, stride or C, stride or C, P, P, P, 1, T, ne, C, D, 4, ov, eps, out, N)
+    assert fwd(200, 100, 1) == _lib.DSA_ERR_UNSUPPORTED
+    assert fwd(512, 512, 1) == _lib.DSA_ERR_INVALID_ARG          # overlap needs 2 * dim channels
+    assert fwd(1024, 512, 0) == _lib.DSA_ERR_INVALID_ARG
+    assert fwd(1024, 512, 1, stride=1028) == _lib.DSA_ERR_INVALID_ARG
+    assert fwd(1024, 512, 1, ne=5) == _lib.DSA_ERR_INVALID_ARG   # 5 windows of 4 in 16 tokens
+    assert fwd(1024, 512, 1, eps=float("nan")) == _lib.DSA_ERR_INVALID_ARG
+    assert fwd(1024, 512, 1, kv=N) == _lib.DSA_ERR_INVALID_ARG
+    assert fwd(1024, 512, 1, kv=ctypes.c_void_p(4100)) == _lib.DSA_ERR_INVALID_ARG
+    assert fwd(1024, 512, 1, ne=0, out=N) == _lib.DSA_OK
+    assert fwd(1024, 512, 1, out=N) == _lib.DSA_ERR_INVALID_ARG
+    # workspace: dnorm partials (one row per backward workgroup, at most 1024) + dape partials
+    # (entry chunks x rate x channels, at most 256 chunks) + each entry's first token; CSA main
+    # compressor at T = 16384, rate 4
+    ws = lib.dsa_v4_compress_bwd_workspace_size(4096, 4096, 1024, 512, 4)
+    assert ws == 1024 * 512 * 4 + 256 * 4 * 1024 * 4 + 4096 * 4
+    assert lib.dsa_v4_compress_bwd_workspace_size(-1, 0, 1024, 512, 4) == 0
+    bwd = lambda ws_, nbytes, dkv=P, dout=P, ni=4: lib.dsa_v4_compress_bwd(
+        P, P, 1024, 1024, P, P, P, 1, 16, 4, ni, 1024, 512, 4, 1, 1e-6, dout, dkv, P, 1024, 1024, P, P, ws_, nbytes, N)
+    need = lib.dsa_v4_compress_bwd_workspace_size(4, 4, 1024, 512, 4)
+    assert need > 0
+    assert bwd(P, need, ni=3) == _lib.DSA_ERR_INVALID_ARG        # fewer items than entries
+    assert bwd(P, need, dkv=N) == _lib.DSA_ERR_INVALID_ARG
+    assert bwd(P, need, dout=N) == _lib.DSA_ERR_INVALID_ARG
+    assert bwd(P, need - 1) == _lib.DSA_ERR_WORKSPACE
+    assert bwd(N, need) == _lib.DSA_ERR_WORKSPACE
+    if not _has_device():
+        assert fwd(1024, 512, 1) == _lib.DSA_ERR_DEVICE
+        assert bwd(P, need) == _lib.DSA_ERR_DEVICE
+
+
+def test_v4_compressor_doc_table():
+    """compress_doc_table: token offsets, entry offsets (complete windows) and item offsets
+    (complete windows plus each partial tail) per document; bad offsets are refused."""
+    import torch
+    from mcore_bridge_amd import ops
+    tab, ne, ni = ops.compress_doc_table([0, 10, 10, 13, 21], 4, "cpu")
+    assert tab.dtype == torch.int32 and tab.tolist() == [[0, 10, 10, 13, 21], [0, 2, 2, 2, 4], [0, 3, 3, 4, 6]]
+    assert (ne, ni) == (4, 6)
+    with pytest.raises(AssertionError):
+        ops.compress_doc_table([0, 5, 3], 4, "cpu")
+    with pytest.raises(AssertionError):
+        ops.compress_doc_table([1, 5], 4, "cpu")
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.v4_compress_fwd(torch.zeros(8, 256, dtype=torch.bfloat16), torch.zeros(8, 256, dtype=torch.bfloat16),
+                            torch.zeros(4, 256, dtype=torch.bfloat16), torch.ones(128, dtype=torch.bfloat16), tab, 2, 4,
+                            1e-6, True)
