@@ -465,7 +465,9 @@ def v4_leg(torch, dev, reps: int = 5):
     `kernels_ms` (the sink entry points on pre-padded key rows) is what the kernels take and
     `host_composition_ms` the rest: the key rows' pad copy, the dkv slice, autograd.
     `csa_compressor_*_ms`: the CSA main compressor (rate 4, overlapping windows, 2 x 512-channel
-    kv / gate rows of the T tokens) through v4.compress, host calls and autograd included."""
+    kv / gate rows of the T tokens) through v4.compress, host calls and autograd included.
+    `csa_layer_fwd_bwd_ms`: the whole DSv4HybridAttention CSA layer (hidden 4096, q_lora_rank
+    1024, 8 output groups of rank 1024, random weights) forward + backward, library GEMMs included."""
     from mcore_bridge_amd import ops, v4
     T, H, D, Wn, rate, Kc, Hi, Di = 16384, 128, 512, 128, 4, 512, 64, 128
     cu = [0, T]
@@ -513,6 +515,28 @@ def v4_leg(torch, dev, reps: int = 5):
     with torch.no_grad():
         t_cf = _time_ms(torch, lambda: v4.compress(ckv, cgt, cape, cnw, cu, rate, 1e-6, True), reps)
     t_cfb = _time_ms(torch, comp_fwd_bwd, reps)
+    # the whole CSA layer mirror (hidden 4096, q_lora_rank 1024, 8 output groups of rank 1024,
+    # random weights): projections, norms and RoPE, both compressors, the indexer's top-k, the
+    # sink attention and the grouped output projection, forward + backward
+    layer = v4.DSv4HybridAttention("compressed_sparse_attention", 4096, H, 1024, o_groups=8, o_lora_rank=1024,
+                                   window=Wn, compress_rates=(rate, 128), index_n_heads=Hi, index_head_dim=Di,
+                                   index_topk=Kc, device=dev)
+    with torch.no_grad():
+        for prm in layer.parameters():
+            if prm.dim() >= 2:
+                prm.normal_(0, 0.02, generator=g)
+    lx = torch.randn(T, 1, 4096, generator=g, device=dev).bfloat16()
+    ldo = (torch.randn(T, 1, 4096, generator=g, device=dev) * 0.01).bfloat16()
+    inv_f = 1.0 / (10000 ** (torch.arange(0, 64, 2, device=dev).float() / 64))
+    tab = torch.outer(torch.arange(T, device=dev).float(), inv_f).repeat(1, 2).view(T, 1, 1, 64)
+
+    def layer_fwd_bwd():
+        xx = lx.detach().requires_grad_()
+        out, _ = layer(xx, None, rotary_pos_emb={"main": tab, "compress": tab})
+        out.backward(ldo)
+
+    t_layer = _time_ms(torch, layer_fwd_bwd, 3)
+    del layer
     fl = (2 * (D + D) + 2 * (3 * D + 2 * D)) * H * nsel
     tf = fl / (t_all * 1e-3) / 1e12
     tfk = fl / (t_k * 1e-3) / 1e12
@@ -523,6 +547,7 @@ def v4_leg(torch, dev, reps: int = 5):
             "kernels_ms": round(t_k, 3), "kernels_tflops": round(tfk, 1),
             "host_composition_ms": round(t_all - t_k, 3), "csa_indexer_ms": round(t_sel, 3),
             "csa_compressor_fwd_ms": round(t_cf, 3), "csa_compressor_fwd_bwd_ms": round(t_cfb, 3),
+            "csa_layer_fwd_bwd_ms": round(t_layer, 3),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / PEAK_BF16_TFLOPS, 4)}}
 

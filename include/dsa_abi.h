@@ -285,6 +285,32 @@ int dsa_v4_compress_bwd(const void* kv, const void* gate, int64_t kv_stride, int
                         void* dkv, void* dgate, int64_t dkv_stride, int64_t dgate_stride, float* dape,
                         float* dnorm_w, void* workspace, size_t workspace_bytes, void* stream);
 
+/* DeepSeek-V4 per-head row transforms around the core attention (deepseek_v4.py:114-142, the q
+ * path's weightless per-head RMS norm and RoPE; :287-318, the output's inverse RoPE and the
+ * grouped output projection's [G, T, H * dim / G] view; the torch ops of those lines, one pass
+ * each here).  RoPE is interleaved on the last rope_dim dims of each row: pairs (2i, 2i + 1)
+ * rotate by (cos, sin)[t, i] of the row's token t (tables [tokens, angle_stride] fp32, the
+ * attention mscale already applied; inverse = 1 negates sin).  dim in {64, 128, 256, 512},
+ * rope_dim a multiple of 8 up to dim.
+ * dsa_v4_norm_rope: x, out [rows, dim] bf16, rows = tokens * n_heads (token t = row / n_heads);
+ *   norm = 1: y = bf16(x * rsqrt(mean x^2 + eps)) before the rotation, norm = 0: rotation only.
+ * dsa_v4_norm_rope_bwd: dx [rows, dim] bf16 from dout (and x when norm = 1). */
+int dsa_v4_norm_rope(const void* x, int64_t rows, int n_heads, int dim, int rope_dim, const float* cos,
+                     const float* sin, int64_t angle_stride, int norm, float eps, int inverse, void* out,
+                     void* stream);
+int dsa_v4_norm_rope_bwd(const void* x, const void* dout, int64_t rows, int n_heads, int dim, int rope_dim,
+                         const float* cos, const float* sin, int64_t angle_stride, int norm, float eps, int inverse,
+                         void* dx, void* stream);
+/* dsa_v4_out_rope_group: o [tokens, n_heads, dim] bf16 -> og [groups, tokens, (n_heads / groups) *
+ *   dim] bf16 with each row rotated (inverse = 1: the output's inverse RoPE); n_heads divisible by
+ *   groups.  dsa_v4_out_rope_group_bwd: d_o [tokens, n_heads, dim] from dog in og's layout. */
+int dsa_v4_out_rope_group(const void* o, int tokens, int n_heads, int dim, int rope_dim, int groups,
+                          const float* cos, const float* sin, int64_t angle_stride, int inverse, void* og,
+                          void* stream);
+int dsa_v4_out_rope_group_bwd(const void* dog, int tokens, int n_heads, int dim, int rope_dim, int groups,
+                              const float* cos, const float* sin, int64_t angle_stride, int inverse, void* d_o,
+                              void* stream);
+
 /* Flags of dsa_sparse_mla_bwd_ex.
  * DSA_BWD_G_INT8: stage the per-(query, key) dKV partial rows as int8 with a bf16 scale per 32
  *   dims (640 bytes a row instead of 1152 in bf16): ~45% less of the backward's largest memory

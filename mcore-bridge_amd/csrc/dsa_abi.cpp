@@ -841,4 +841,84 @@ int dsa_v4_compress_bwd(const void* kv, const void* gate, int64_t kv_stride, int
   return dsa::launch_v4_compress_bwd(p, dape, dnorm_w, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
 }
 
+
+// ---- DeepSeek-V4 row transforms
+static int rope_params(int64_t rows, int n_heads, int dim, int rope_dim, const float* cos, const float* sin,
+                       int64_t angle_stride, int inverse, dsa::RopeParams& p) {
+  if (rows < 0 || n_heads < 1 || rows % n_heads != 0 || rope_dim < 0 || rope_dim > dim || rope_dim % 8 ||
+      rows / n_heads > INT32_MAX)
+    return DSA_ERR_INVALID_ARG;
+  if (dim != 64 && dim != 128 && dim != 256 && dim != 512) return DSA_ERR_UNSUPPORTED;
+  if (rope_dim > 0 && (!cos || !sin || angle_stride < rope_dim / 2)) return DSA_ERR_INVALID_ARG;
+  p.rows = rows; p.n_heads = n_heads; p.tokens = (int)(rows / n_heads); p.dim = dim; p.rope_dim = rope_dim;
+  p.cos = cos; p.sin = sin; p.angle_stride = angle_stride; p.inverse = inverse ? 1 : 0; p.groups = 1;
+  return DSA_OK;
+}
+
+int dsa_v4_norm_rope(const void* x, int64_t rows, int n_heads, int dim, int rope_dim, const float* cos,
+                     const float* sin, int64_t angle_stride, int norm, float eps, int inverse, void* out,
+                     void* stream) {
+  dsa::RopeParams p{};
+  const int rc = rope_params(rows, n_heads, dim, rope_dim, cos, sin, angle_stride, inverse, p);
+  if (rc != DSA_OK) return rc;
+  if (norm && (!std::isfinite(eps) || eps < 0.f)) return DSA_ERR_INVALID_ARG;
+  if (rows == 0) return DSA_OK;
+  if (!x || !out || !aligned16(x) || !aligned16(out)) return DSA_ERR_INVALID_ARG;
+  p.x = static_cast<const dsa::bf16_t*>(x);
+  p.out = static_cast<dsa::bf16_t*>(out);
+  p.norm = norm ? 1 : 0; p.eps = eps;
+  DSA_CHECK_DEVICE(dev);
+  return dsa::launch_v4_rope(0, p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+int dsa_v4_norm_rope_bwd(const void* x, const void* dout, int64_t rows, int n_heads, int dim, int rope_dim,
+                         const float* cos, const float* sin, int64_t angle_stride, int norm, float eps, int inverse,
+                         void* dx, void* stream) {
+  dsa::RopeParams p{};
+  const int rc = rope_params(rows, n_heads, dim, rope_dim, cos, sin, angle_stride, inverse, p);
+  if (rc != DSA_OK) return rc;
+  if (norm && (!std::isfinite(eps) || eps < 0.f)) return DSA_ERR_INVALID_ARG;
+  if (rows == 0) return DSA_OK;
+  if (!dout || !dx || !aligned16(dout) || !aligned16(dx) || (norm && (!x || !aligned16(x))))
+    return DSA_ERR_INVALID_ARG;
+  p.x = static_cast<const dsa::bf16_t*>(x);
+  p.dout = static_cast<const dsa::bf16_t*>(dout);
+  p.dx = static_cast<dsa::bf16_t*>(dx);
+  p.norm = norm ? 1 : 0; p.eps = eps;
+  DSA_CHECK_DEVICE(dev);
+  return dsa::launch_v4_rope(1, p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+int dsa_v4_out_rope_group(const void* o, int tokens, int n_heads, int dim, int rope_dim, int groups,
+                          const float* cos, const float* sin, int64_t angle_stride, int inverse, void* og,
+                          void* stream) {
+  dsa::RopeParams p{};
+  if (tokens < 0 || groups < 1 || n_heads % groups != 0) return DSA_ERR_INVALID_ARG;
+  const int rc = rope_params((int64_t)tokens * n_heads, n_heads, dim, rope_dim, cos, sin, angle_stride, inverse, p);
+  if (rc != DSA_OK) return rc;
+  if (tokens == 0) return DSA_OK;
+  if (!o || !og || !aligned16(o) || !aligned16(og)) return DSA_ERR_INVALID_ARG;
+  p.x = static_cast<const dsa::bf16_t*>(o);
+  p.out = static_cast<dsa::bf16_t*>(og);
+  p.groups = groups;
+  DSA_CHECK_DEVICE(dev);
+  return dsa::launch_v4_rope(2, p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
+int dsa_v4_out_rope_group_bwd(const void* dog, int tokens, int n_heads, int dim, int rope_dim, int groups,
+                              const float* cos, const float* sin, int64_t angle_stride, int inverse, void* d_o,
+                              void* stream) {
+  dsa::RopeParams p{};
+  if (tokens < 0 || groups < 1 || n_heads % groups != 0) return DSA_ERR_INVALID_ARG;
+  const int rc = rope_params((int64_t)tokens * n_heads, n_heads, dim, rope_dim, cos, sin, angle_stride, inverse, p);
+  if (rc != DSA_OK) return rc;
+  if (tokens == 0) return DSA_OK;
+  if (!dog || !d_o || !aligned16(dog) || !aligned16(d_o)) return DSA_ERR_INVALID_ARG;
+  p.dout = static_cast<const dsa::bf16_t*>(dog);
+  p.dx = static_cast<dsa::bf16_t*>(d_o);
+  p.groups = groups;
+  DSA_CHECK_DEVICE(dev);
+  return dsa::launch_v4_rope(3, p, as_stream(stream)) == 0 ? DSA_OK : DSA_ERR_LAUNCH;
+}
+
 }  // extern "C"

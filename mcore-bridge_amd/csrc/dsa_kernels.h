@@ -312,6 +312,23 @@ struct CompressBwdGrid {
 };
 CompressBwdGrid compress_bwd_grid(int n_entries, int n_items, int channels, int dim, int rate);
 int launch_v4_compress_fwd(const CompressParams& p, hipStream_t stream);
+
+// DeepSeek-V4 row transforms (dsa_v4_rope.hip): weightless RMS norm + interleaved RoPE of q rows,
+// and the output's inverse RoPE written in the grouped projection's layout.
+struct RopeParams {
+  const bf16_t* x;      // norm_rope: rows [rows, dim] (forward input; backward: the forward's input)
+                        // out_rope_group forward: o [tokens, n_heads, dim]
+  const bf16_t* dout;   // norm_rope backward: [rows, dim]; out_rope_group backward: [groups, tokens, HG*dim]
+  bf16_t* out;          // norm_rope forward: [rows, dim]; out_rope_group forward: [groups, tokens, HG*dim]
+  bf16_t* dx;           // backward: [rows, dim]
+  const float* cos;     // [tokens, angle_stride] (first rope_dim / 2 used), mscale applied
+  const float* sin;
+  int64_t rows, angle_stride;
+  int tokens, n_heads, dim, rope_dim, groups, norm, inverse;
+  float eps;
+};
+// which: 0 norm_rope forward, 1 norm_rope backward, 2 out_rope_group forward, 3 its backward
+int launch_v4_rope(int which, const RopeParams& p, hipStream_t stream);
 // dape [rate, channels] and dnorm [dim] fp32 outputs
 int launch_v4_compress_bwd(const CompressParams& p, float* dape, float* dnorm, hipStream_t stream);
 

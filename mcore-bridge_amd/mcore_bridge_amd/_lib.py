@@ -93,6 +93,14 @@ SIGNATURES = {
     "dsa_v4_compress_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                     c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p,
                                     c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "dsa_v4_norm_rope": (c_int, [c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int, c_float,
+                                 c_int, c_void_p, c_void_p]),
+    "dsa_v4_norm_rope_bwd": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_int64,
+                                     c_int, c_float, c_int, c_void_p, c_void_p]),
+    "dsa_v4_out_rope_group": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int,
+                                      c_void_p, c_void_p]),
+    "dsa_v4_out_rope_group_bwd": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64,
+                                          c_int, c_void_p, c_void_p]),
     "dsa_indexer_kl_loss": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "dsa_indexer_selected_scores": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

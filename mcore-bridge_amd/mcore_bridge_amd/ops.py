@@ -928,3 +928,69 @@ def v4_compress_bwd(kv: Tensor, gate: Tensor, ape: Tensor, norm_w: Tensor, table
                   int(bool(overlap)), float(eps), _p(dout), _p(dkv), _p(dgate), C, C, _p(dape), _p(dnorm), _p(ws),
                   ws.numel(), _stream(kv.device))
     return dkv, dgate, dape, dnorm
+
+
+# --------------------------------------------------------------------------------------
+# DeepSeek-V4 row transforms: per-head RMS norm + RoPE of q rows, the output's RoPE in the grouped
+# projection's layout
+# --------------------------------------------------------------------------------------
+def _check_rope(x: Tensor, cos: Tensor, sin: Tensor, rope_dim: int) -> None:
+    _require_gpu(x, cos, sin)
+    _require(x.dtype == torch.bfloat16 and x.is_contiguous(), "rows must be contiguous bf16")
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32 and cos.shape == sin.shape,
+             "cos / sin must be fp32 tables of one shape")
+    _require(cos.dim() == 2 and cos.stride(1) == 1 and sin.stride(0) == cos.stride(0) and cos.shape[1] >= rope_dim // 2,
+             "cos / sin must be [tokens, >= rope_dim / 2] with unit column stride")
+
+
+def v4_norm_rope(x: Tensor, cos: Tensor, sin: Tensor, rope_dim: int, norm: bool, eps: float,
+                 inverse: bool = False) -> Tensor:
+    """``x [T, H, D]`` bf16 -> per-row weightless RMS norm (``norm``) then interleaved RoPE on the last
+    ``rope_dim`` dims with token t's ``cos / sin [T, >= rope_dim/2]`` (``dsa_v4_norm_rope``)."""
+    _check_rope(x, cos, sin, rope_dim)
+    T, H, D = x.shape
+    _require(cos.shape[0] == T, "one cos / sin row per token")
+    out = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        _lib.call("dsa_v4_norm_rope", _p(x), T * H, H, D, int(rope_dim), _p(cos), _p(sin), cos.stride(0), int(bool(norm)),
+                  float(eps), int(bool(inverse)), _p(out), _stream(x.device))
+    return out
+
+
+def v4_norm_rope_bwd(x: Tensor, dout: Tensor, cos: Tensor, sin: Tensor, rope_dim: int, norm: bool, eps: float,
+                     inverse: bool = False) -> Tensor:
+    """Gradient of ``v4_norm_rope`` with respect to ``x`` (``dsa_v4_norm_rope_bwd``)."""
+    _check_rope(dout, cos, sin, rope_dim)
+    _require(x.shape == dout.shape and x.dtype == torch.bfloat16 and x.is_contiguous(), "x must match dout")
+    T, H, D = dout.shape
+    dx = torch.empty_like(dout)
+    with torch.cuda.device(dout.device):
+        _lib.call("dsa_v4_norm_rope_bwd", _p(x), _p(dout), T * H, H, D, int(rope_dim), _p(cos), _p(sin), cos.stride(0),
+                  int(bool(norm)), float(eps), int(bool(inverse)), _p(dx), _stream(dout.device))
+    return dx
+
+
+def v4_out_rope_group(o: Tensor, cos: Tensor, sin: Tensor, rope_dim: int, groups: int, inverse: bool) -> Tensor:
+    """``o [T, H, D]`` -> ``[groups, T, H * D / groups]`` with each row RoPE-rotated (``inverse``: the
+    output's inverse rotation; ``dsa_v4_out_rope_group``)."""
+    _check_rope(o, cos, sin, rope_dim)
+    T, H, D = o.shape
+    _require(H % groups == 0 and cos.shape[0] == T, "heads must split into the groups; one cos / sin row per token")
+    og = torch.empty(groups, T, H * D // groups, dtype=o.dtype, device=o.device)
+    with torch.cuda.device(o.device):
+        _lib.call("dsa_v4_out_rope_group", _p(o), T, H, D, int(rope_dim), int(groups), _p(cos), _p(sin), cos.stride(0),
+                  int(bool(inverse)), _p(og), _stream(o.device))
+    return og
+
+
+def v4_out_rope_group_bwd(dog: Tensor, n_heads: int, cos: Tensor, sin: Tensor, rope_dim: int, inverse: bool) -> Tensor:
+    """Gradient of ``v4_out_rope_group``: ``dog [G, T, H * D / G]`` -> ``do [T, H, D]``."""
+    _check_rope(dog, cos, sin, rope_dim)
+    G, T, W = dog.shape
+    _require((W * G) % n_heads == 0, "the grouped rows must hold whole heads")
+    D = W * G // n_heads
+    d_o = torch.empty(T, n_heads, D, dtype=dog.dtype, device=dog.device)
+    with torch.cuda.device(dog.device):
+        _lib.call("dsa_v4_out_rope_group_bwd", _p(dog), T, n_heads, D, int(rope_dim), G, _p(cos), _p(sin),
+                  cos.stride(0), int(bool(inverse)), _p(d_o), _stream(dog.device))
+    return d_o

@@ -36,7 +36,6 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import ops
-from .dsa import _HeadwiseMatmul
 
 HEAD_DIM = 512
 ROPE_DIM = 64
@@ -148,27 +147,88 @@ def indexer_select(q_idx: Tensor, comp_k: Tensor, w: Tensor, cu_seqlens: Sequenc
 
 
 # --------------------------------------------------------------------------------------
-# host-side pieces of the layer (projections, norms, RoPE): torch; the compressors' pooling: HIP
+# host-side pieces of the layer: projections and their norms in torch; per-head norm + RoPE, the
+# output's RoPE + grouped layout and the compressors' pooling on HIP kernels
 # --------------------------------------------------------------------------------------
-def rope_interleaved(x: Tensor, angles: Tensor, mscale: float = 1.0, inverse: bool = False) -> Tensor:
-    """Interleaved RoPE on the trailing ``2 * angles.shape[-1]`` dims of ``x [N, ..., D]`` with
-    per-token ``angles [N, rd/2]`` (fp32 math, result in x's dtype)."""
-    rd = 2 * angles.shape[-1]
-    shape = [angles.shape[0]] + [1] * (x.dim() - 2) + [angles.shape[-1]]
-    cos = (torch.cos(angles) * mscale).view(shape)
-    sin = (torch.sin(angles) * mscale).view(shape)
-    if inverse:
-        sin = -sin
-    nope, rope = x[..., :-rd], x[..., -rd:].float()
-    a, b = rope[..., 0::2], rope[..., 1::2]
-    out = torch.stack((a * cos - b * sin, b * cos + a * sin), dim=-1).flatten(-2)
-    return torch.cat([nope, out.to(x.dtype)], dim=-1)
+class _NormRope(torch.autograd.Function):
+    """Per-row weightless RMS norm (``norm``) then interleaved RoPE on the last ``rope_dim`` dims of
+    rows ``x [T, H, D]`` (``ops.v4_norm_rope`` / ``_bwd``: one HBM pass each way)."""
+
+    @staticmethod
+    def forward(ctx, x, cos, sin, rope_dim, norm, eps, inverse):
+        x = x.contiguous()
+        ctx.save_for_backward(x if norm else None, cos, sin)
+        ctx.cfg = (rope_dim, norm, eps, inverse)
+        return ops.v4_norm_rope(x, cos, sin, rope_dim, norm, eps, inverse)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, cos, sin = ctx.saved_tensors
+        rope_dim, norm, eps, inverse = ctx.cfg
+        g = g.contiguous()
+        dx = ops.v4_norm_rope_bwd(x if norm else g, g, cos, sin, rope_dim, norm, eps, inverse)
+        return dx, None, None, None, None, None, None
 
 
-def rms_norm(x: Tensor, weight: Optional[Tensor], eps: float) -> Tensor:
-    y = x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps)
-    y = y.to(x.dtype)
-    return y if weight is None else y * weight
+def norm_rope(x: Tensor, cos: Tensor, sin: Tensor, norm: bool, eps: float = 0.0, inverse: bool = False) -> Tensor:
+    """``x [N, ..., D]`` rows: optional weightless RMS norm, then the interleaved RoPE of the last
+    ``ROPE_DIM`` dims with row n's token angles (``cos / sin [N, ROPE_DIM / 2]``, mscale applied)."""
+    shape = x.shape
+    y = _NormRope.apply(x.reshape(shape[0], -1, shape[-1]), cos, sin, ROPE_DIM, norm, eps, inverse)
+    return y.view(shape)
+
+
+def rope_tables(angles: Tensor, mscale: float) -> Tuple[Tensor, Tensor]:
+    """fp32 ``cos / sin [N, ROPE_DIM / 2]`` of the RoPE angles, times the attention mscale."""
+    a = angles.float()
+    return (torch.cos(a) * mscale).contiguous(), (torch.sin(a) * mscale).contiguous()
+
+
+class _OutRopeGroup(torch.autograd.Function):
+    """The output's inverse RoPE, written in the grouped projection's layout ``[G, T, H * D / G]``
+    (``ops.v4_out_rope_group`` / ``_bwd``)."""
+
+    @staticmethod
+    def forward(ctx, o, cos, sin, groups):
+        ctx.save_for_backward(cos, sin)
+        ctx.n_heads = o.shape[1]
+        return ops.v4_out_rope_group(o.contiguous(), cos, sin, ROPE_DIM, groups, True)
+
+    @staticmethod
+    def backward(ctx, g):
+        cos, sin = ctx.saved_tensors
+        return ops.v4_out_rope_group_bwd(g.contiguous(), ctx.n_heads, cos, sin, ROPE_DIM, True), None, None, None
+
+
+class _GroupedProj(torch.autograd.Function):
+    """``out[t, g*N:(g+1)*N] = a[g, t] @ w[g]^T`` for ``a [G, T, K]`` and ``w [G, N, K]`` (the
+    grouped output projection ``wo_a``, ``deepseek_v4.py:313-318``), written straight into the
+    ``[T, G * N]`` rows the output projection reads; one library GEMM per group each way, on the
+    operands as they lie (no transposed copies)."""
+
+    @staticmethod
+    def forward(ctx, a, w):
+        G, T, _ = a.shape
+        N = w.shape[1]
+        ctx.save_for_backward(a, w)
+        out = torch.empty(T, G * N, dtype=a.dtype, device=a.device)
+        for g in range(G):
+            out[:, g * N:(g + 1) * N] = torch.mm(a[g], w[g].t())
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        a, w = ctx.saved_tensors
+        G, N = w.shape[0], w.shape[1]
+        da = torch.empty_like(a) if ctx.needs_input_grad[0] else None
+        dw = torch.empty_like(w) if ctx.needs_input_grad[1] else None
+        for g in range(G):
+            gg = grad[:, g * N:(g + 1) * N]
+            if da is not None:
+                torch.mm(gg, w[g], out=da[g])
+            if dw is not None:
+                torch.mm(gg.t(), a[g], out=dw[g])
+        return da, dw
 
 
 class _Compress(torch.autograd.Function):
@@ -315,26 +375,26 @@ class DSv4HybridAttention(torch.nn.Module):
         angles_tab = angles_tab[:, : ROPE_DIM // 2].float()
         _, _, start = _docs(cu, dev)
         pos = torch.arange(T, device=dev) - start                              # position inside the document
-        ang = angles_tab[pos]
+        cs, sn = rope_tables(angles_tab[pos], self.mscale)
         # q path (deepseek_v4.py:114-142): down, norm, up, per-head weightless RMS norm, RoPE
         q_res = self.q_layernorm(self.linear_q_down_proj(x))
         q = self.linear_q_up_proj(q_res).view(T, self.H, HEAD_DIM)
-        q = rope_interleaved(rms_norm(q, None, self.eps), ang, self.mscale)
+        q = norm_rope(q, cs, sn, True, self.eps)
         # the one K = V head (:144-198)
-        kv = rope_interleaved(self.kv_layernorm(self.linear_kv_proj(x)), ang, self.mscale)
+        kv = norm_rope(self.kv_layernorm(self.linear_kv_proj(x)), cs, sn, False)
         comp_sel = None
         keys = kv
         ca = self.core_attention
         if ca.compressor is not None:
             comp = ca.compressor(x, cu, self.eps)
-            cang = angles_tab[compressed_positions(cu, self.rate, dev)]
-            comp = rope_interleaved(comp, cang, self.mscale)
+            ccs, csn = rope_tables(angles_tab[compressed_positions(cu, self.rate, dev)], self.mscale)
+            comp = norm_rope(comp, ccs, csn, False)
             keys = torch.cat([kv, comp])
             if ca.indexer is not None:
                 ix = ca.indexer
                 with torch.no_grad():
-                    ck = rope_interleaved(ix.compressor(x, cu, self.eps), cang, self.mscale)
-                    qi = rope_interleaved(ix.linear_wq_b(q_res).view(T, ix.n_heads, ix.head_dim), ang, self.mscale)
+                    ck = norm_rope(ix.compressor(x, cu, self.eps), ccs, csn, False)
+                    qi = norm_rope(ix.linear_wq_b(q_res).view(T, ix.n_heads, ix.head_dim), cs, sn, False)
                     wi = ix.linear_weights_proj(x).float() * ix.n_heads ** -0.5
                     comp_sel = indexer_select(qi, ck, wi, cu, self.rate, ix.topk, ix.head_dim,
                                               return_scores=self.keep_index_scores)
@@ -344,10 +404,9 @@ class DSv4HybridAttention(torch.nn.Module):
         idx = hybrid_indices(cu, self.window, self.rate if comp_sel is None else 0, comp_sel, dev)
         o, _ = sink_attention(q, keys, ca.attn_sink, idx, HEAD_DIM ** -0.5)
         # inverse RoPE on the rope slice of each head's output (:287-311), grouped output (:313-318)
-        o = rope_interleaved(o, ang, self.mscale, inverse=True)
-        og = o.reshape(T, self.o_groups, -1).transpose(0, 1)                   # [G, T, H*D/G]
-        wo_a = self.linear_o_group_proj.view(self.o_groups, self.o_lora_rank, -1).transpose(1, 2)
-        o = _HeadwiseMatmul.apply(og, wo_a).transpose(0, 1).reshape(T, -1)     # [T, G * o_lora_rank]
+        og = _OutRopeGroup.apply(o, cs, sn, self.o_groups)                     # [G, T, H*D/G]
+        wo_a = self.linear_o_group_proj.view(self.o_groups, self.o_lora_rank, -1)
+        o = _GroupedProj.apply(og, wo_a)                                       # [T, G * o_lora_rank]
         out = self.linear_proj(o)
         if thd:
             return out.view(T, 1, -1), None

@@ -370,3 +370,31 @@ def test_v4_compressor_doc_table():
         ops.v4_compress_fwd(torch.zeros(8, 256, dtype=torch.bfloat16), torch.zeros(8, 256, dtype=torch.bfloat16),
                             torch.zeros(4, 256, dtype=torch.bfloat16), torch.ones(128, dtype=torch.bfloat16), tab, 2, 4,
                             1e-6, True)
+
+
+def test_v4_row_transform_entry_points_validate():
+    """The V4 row transforms: dim 64 / 128 / 256 / 512, rope_dim a multiple of 8 up to dim, rows a
+    whole number of tokens, angle tables wide enough, heads that split into the groups."""
+    lib = _lib.load()
+    nr = lambda rows=64, H=4, D=512, rd=64, stride=32, cos=P, x=P, norm=1, eps=1e-6: lib.dsa_v4_norm_rope(
+        x, rows, H, D, rd, cos, P, stride, norm, eps, 0, P, N)
+    assert nr(D=96) == _lib.DSA_ERR_UNSUPPORTED
+    assert nr(rows=66) == _lib.DSA_ERR_INVALID_ARG       # not a whole number of tokens
+    assert nr(rd=60) == _lib.DSA_ERR_INVALID_ARG
+    assert nr(rd=520) == _lib.DSA_ERR_INVALID_ARG
+    assert nr(stride=31) == _lib.DSA_ERR_INVALID_ARG
+    assert nr(cos=N) == _lib.DSA_ERR_INVALID_ARG
+    assert nr(x=ctypes.c_void_p(4100)) == _lib.DSA_ERR_INVALID_ARG
+    assert nr(eps=float("nan")) == _lib.DSA_ERR_INVALID_ARG
+    assert nr(rows=0, x=N) == _lib.DSA_OK
+    bwd = lambda x=P, norm=1: lib.dsa_v4_norm_rope_bwd(x, P, 64, 4, 512, 64, P, P, 32, norm, 1e-6, 0, P, N)
+    assert bwd(x=N) == _lib.DSA_ERR_INVALID_ARG          # the norm's backward needs the forward input
+    og = lambda H=8, G=3, T=4: lib.dsa_v4_out_rope_group(P, T, H, 512, 64, G, P, P, 32, 1, P, N)
+    assert og() == _lib.DSA_ERR_INVALID_ARG              # 8 heads do not split into 3 groups
+    assert og(T=-1, G=4) == _lib.DSA_ERR_INVALID_ARG
+    assert og(T=0, G=4) == _lib.DSA_OK
+    assert lib.dsa_v4_out_rope_group_bwd(P, 4, 8, 512, 64, 0, P, P, 32, 1, P, N) == _lib.DSA_ERR_INVALID_ARG
+    if not _has_device():
+        assert nr(rd=0, cos=N) == _lib.DSA_ERR_DEVICE     # no rope part: no angle tables needed
+        assert og(G=4) == _lib.DSA_ERR_DEVICE
+        assert bwd() == _lib.DSA_ERR_DEVICE
