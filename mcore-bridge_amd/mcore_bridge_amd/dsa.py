@@ -333,23 +333,68 @@ def sparse_mla_with_indexer_loss(q: Tensor, kv: Tensor, topk_indices: Tensor, q_
     return out, loss
 
 
-class _HeadwiseMatmul(torch.autograd.Function):
-    """``out[h] = a[h] @ b[h]`` for ``a [H, M, K]``, ``b [H, K, N]``, with every batched product in
-    forward and backward fed contiguous operands (no transposed views reach ``torch.bmm``)."""
+def _rows_by_head(x: Tensor, H: int, width: int, lo: int = 0) -> Tensor:
+    """``[H, N, width]`` view of the columns ``lo .. lo + width`` of each head's row in ``x`` (rows of
+    ``H`` heads, token-major, unit column stride): a strided batch for the library GEMMs, no copy."""
+    return x.reshape(-1, H, x.shape[-1])[..., lo:lo + width].permute(1, 0, 2)
+
+
+class _AbsorbQuery(torch.autograd.Function):
+    """``query [S, B, H, dc + dr] = [q_no_pe_h W_UK_h, q_pos_emb]``: the per-head products written
+    straight into the query rows (one strided batched GEMM, heads as the batch), the rope part
+    copied beside them.  ``w_uk [H, dn, dc]``."""
 
     @staticmethod
-    def forward(ctx, a: Tensor, b: Tensor) -> Tensor:
-        a, b = a.contiguous(), b.contiguous()
-        ctx.save_for_backward(a, b)
-        return torch.bmm(a, b)
+    def forward(ctx, q_no_pe: Tensor, q_pos_emb: Tensor, w_uk: Tensor) -> Tensor:
+        S, B, H, dn = q_no_pe.shape
+        dc, dr = w_uk.shape[-1], q_pos_emb.shape[-1]
+        q_no_pe = q_no_pe.contiguous()
+        wk = w_uk.contiguous()
+        query = torch.empty(S, B, H, dc + dr, dtype=q_no_pe.dtype, device=q_no_pe.device)
+        torch.bmm(_rows_by_head(q_no_pe, H, dn), wk, out=_rows_by_head(query, H, dc))
+        query[..., dc:] = q_pos_emb
+        ctx.save_for_backward(q_no_pe, wk)
+        return query
+
+    @staticmethod
+    def backward(ctx, dquery: Tensor):
+        q_no_pe, wk = ctx.saved_tensors
+        H, dn, dc = wk.shape
+        dquery = dquery.contiguous()
+        dq_lat = _rows_by_head(dquery, H, dc)                                # [H, N, dc] strided
+        d_qn = torch.empty_like(q_no_pe)
+        torch.bmm(dq_lat, wk.transpose(1, 2).contiguous(), out=_rows_by_head(d_qn, H, dn))
+        d_wk = torch.bmm(_rows_by_head(q_no_pe, H, dn).transpose(1, 2).contiguous(), dq_lat)
+        return d_qn, dquery[..., dc:].contiguous(), d_wk
+
+
+class _AbsorbOutput(torch.autograd.Function):
+    """``out [S, B, H * dv]``: each head's latent output row times ``W_UV_h^T`` (``w_uv_t [H, dc,
+    dv]``), one strided batched GEMM reading the attention's rows and writing the output rows."""
+
+    @staticmethod
+    def forward(ctx, o_lat: Tensor, w_uv_t: Tensor) -> Tensor:
+        S, B = o_lat.shape[0], o_lat.shape[1]
+        H, dc, dv = w_uv_t.shape
+        o_lat = o_lat.contiguous()
+        wv = w_uv_t.contiguous()
+        out = torch.empty(S, B, H * dv, dtype=o_lat.dtype, device=o_lat.device)
+        torch.bmm(_rows_by_head(o_lat.view(S, B, H, dc), H, dc), wv, out=_rows_by_head(out.view(S, B, H, dv), H, dv))
+        ctx.save_for_backward(o_lat, wv)
+        return out
 
     @staticmethod
     def backward(ctx, g: Tensor):
-        a, b = ctx.saved_tensors
+        o_lat, wv = ctx.saved_tensors
+        H, dc, dv = wv.shape
+        S, B = o_lat.shape[0], o_lat.shape[1]
         g = g.contiguous()
-        ga = torch.bmm(g, b.transpose(1, 2).contiguous()) if ctx.needs_input_grad[0] else None
-        gb = torch.bmm(a.transpose(1, 2).contiguous(), g) if ctx.needs_input_grad[1] else None
-        return ga, gb
+        gh = _rows_by_head(g.view(S, B, H, dv), H, dv)                        # [H, N, dv] strided
+        d_o = torch.empty_like(o_lat)
+        torch.bmm(gh, wv.transpose(1, 2).contiguous(), out=_rows_by_head(d_o.view(S, B, H, dc), H, dc))
+        # d W_UV_h^T = o_h^T g_h, formed as (g_h^T o_h)^T: the transposed copy is of the dv-wide rows
+        d_wv = torch.bmm(gh.transpose(1, 2).contiguous(), _rows_by_head(o_lat.view(S, B, H, dc), H, dc))
+        return d_o, d_wv.transpose(1, 2)
 
 
 def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compressed: Tensor, k_pos_emb: Tensor,
@@ -379,9 +424,7 @@ def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compres
     dv = W.shape[1] - dn
     w_uk = W[:, :dn]                                                   # [H, dn, dc]
     w_uv_t = W[:, dn:].transpose(1, 2)                                 # [H, dc, dv]
-    qn = q_no_pe.permute(2, 0, 1, 3).reshape(H, S * B, dn)
-    q_lat = _HeadwiseMatmul.apply(qn, w_uk)                            # [H, S*B, dc]
-    query = torch.cat([q_lat.view(H, S, B, dc).permute(1, 2, 0, 3), q_pos_emb], dim=-1)
+    query = _AbsorbQuery.apply(q_no_pe, q_pos_emb, w_uk)               # [S, B, H, dc + 64]
     kv = torch.cat([kv_compressed, k_pos_emb.reshape(S, B, -1)], dim=-1)
     loss = None
     if indexer_loss is None:
@@ -410,9 +453,7 @@ def absorbed_mla_sparse_attention(q_no_pe: Tensor, q_pos_emb: Tensor, kv_compres
             o_thd = attach_indexer_loss(o_thd, loss, loss_scale)
             loss = loss.detach()
         o_lat = o_thd.reshape(B, S, H * ops.D_V).transpose(0, 1)
-    o = o_lat.reshape(S, B, H, dc).permute(2, 0, 1, 3).reshape(H, S * B, dc)
-    out = _HeadwiseMatmul.apply(o, w_uv_t)                             # [H, S*B, dv]
-    out = out.view(H, S, B, dv).permute(1, 2, 0, 3).reshape(S, B, H * dv)
+    out = _AbsorbOutput.apply(o_lat.reshape(S, B, H * dc), w_uv_t)    # [S, B, H * dv]
     return out if indexer_loss is None else (out, loss)
 
 
