@@ -22,6 +22,8 @@ The line also carries:
   "indexer_kl"        the sparse indexer KL loss and the indexer-score backward at cfg3;
   "indexer_kl_dense"  the dense indexer KL loss (the reference default) at cfg3: its LSE and target
                       kernels and the whole loss forward + backward;
+  "mla"               the absorbed MLA path of the layer-spec swap (W_UK into q, the sparse kernels,
+                      W_UV after) forward + backward at T = 16384, H = 128, top-k 2048;
   "v4"                the DeepSeek-V4 CSA layer core (sink attention fwd + bwd, 512-wide K = V) at
                       T = 16384, H = 128, window 128 + top-512 compressed entries, and the layer's
                       main compressor (pooling + norm kernels, forward and forward + backward);
@@ -552,6 +554,56 @@ def v4_leg(torch, dev, reps: int = 5):
                          "frac": round(tf / PEAK_BF16_TFLOPS, 4)}}
 
 
+def mla_leg(torch, dev, qi, ki, w, reps: int = 3):
+    """The absorbed MLA path of the layer-spec swap (absorbed_mla_sparse_attention, the core of
+    reference multi_latent_attention.py:262-270 on MLASelfAttention's un-absorbed tensors) at one
+    causal document of T = 16384 tokens: H = 128, qk_nope = v_head = 128, kv_lora_rank 512, rope
+    64, top-k 2048 from the bench's indexer inputs over that document.  `ms` is the autograd path
+    forward + backward (W_UK folded into q, the sparse kernels, W_UV after, every gradient incl. the
+    up-projection weight's); `attention_ms` the same sparse forward + backward on the prepared
+    query / kv alone, so `ms - attention_ms` is what the absorption costs.  Algorithmic work: the
+    sparse attention's 7680*H per selected pair plus the absorption products, 2*T*H*(dn*512 +
+    512*dv) forward and twice that backward."""
+    from mcore_bridge_amd import dsa, ops
+    T, H, dn, dv, K = qi.shape[0], 128, 128, 128, 2048
+    g = torch.Generator(device=dev).manual_seed(55)
+    q_no_pe = (torch.randn(T, 1, H, dn, generator=g, device=dev) * 0.1).bfloat16()
+    q_pe = (torch.randn(T, 1, H, 64, generator=g, device=dev) * 0.1).bfloat16()
+    kvc = (torch.randn(T, 1, 512, generator=g, device=dev) * 0.1).bfloat16()
+    kpe = (torch.randn(T, 1, 64, generator=g, device=dev) * 0.1).bfloat16()
+    wkv = (torch.randn(H * (dn + dv), 512, generator=g, device=dev) * 0.02).bfloat16()
+    dout = (torch.randn(T, 1, H * dv, generator=g, device=dev) * 0.01).bfloat16()
+    cu1 = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    idx = ops.indexer_topk(qi, ki, w, K, cu1, True, T).view(1, T, K)
+    nsel = int((idx >= 0).sum().item())
+    scale = 192 ** -0.5
+
+    def absorbed():
+        ls = [x.detach().requires_grad_() for x in (q_no_pe, q_pe, kvc, kpe, wkv)]
+        dsa.absorbed_mla_sparse_attention(*ls, idx, scale).backward(dout)
+
+    with torch.no_grad():
+        q_lat = torch.bmm(q_no_pe[:, 0].permute(1, 0, 2).float().contiguous(),
+                          wkv.view(H, dn + dv, 512)[:, :dn].float().contiguous())        # [H, T, 512]
+        qq = torch.cat([q_lat.permute(1, 0, 2).unsqueeze(1).bfloat16(), q_pe], -1).contiguous()
+        kk = torch.cat([kvc, kpe], -1).contiguous()
+    do_lat = (torch.randn(T, 1, H * 512, generator=g, device=dev) * 0.01).bfloat16()
+
+    def attention_only():
+        a, b = qq.detach().requires_grad_(), kk.detach().requires_grad_()
+        dsa.sparse_mla_attention(a, b, idx, scale).backward(do_lat)
+
+    t_all = _time_ms(torch, absorbed, reps)
+    t_att = _time_ms(torch, attention_only, reps)
+    fl = 7680 * H * nsel + 3 * 2 * T * H * (dn * 512 + 512 * dv)
+    return {"workload": "absorbed MLA (layer-spec swap) core: T=16384 one causal document, H=128, qk_nope=v=128, "
+                        "kv_lora 512 + rope 64, top-k 2048; forward + backward incl. W_UK / W_UV and their gradients",
+            "n_sel": nsel, "ms": round(t_all, 3), "attention_ms": round(t_att, 3),
+            "absorption_ms": round(t_all - t_att, 3), "tflops": round(fl / (t_all * 1e-3) / 1e12, 1),
+            "roofline": {"bound": "mfma", "achieved": round(fl / (t_all * 1e-3) / 1e12, 1), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(fl / (t_all * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}}
+
+
 def prefill_fwd_leg(torch, dev, name: str, reps: int = 10):
     """cfg2 (bf16 indexer) or cfg4 (fp8 e4m3fn indexer with absmax row scales, S = 32768): one
     causal document, indexer scores, top-k 2048 and the bf16 sparse MLA forward (H = 128), each
@@ -658,7 +710,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip every leg after the cfg3 step")
     ap.add_argument("--legs", default="all",
                     help="comma list of the legs after the cfg3 step to run: int8, decode, prologue, indexer_kl, "
-                         "indexer_kl_dense, v4, cfg2, cfg4 (default all)")
+                         "indexer_kl_dense, mla, v4, cfg2, cfg4 (default all)")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="only copy a 1 GiB tensor (known HBM bytes) to calibrate FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
@@ -842,6 +894,9 @@ def main():
         res["indexer_kl_dense"] = indexer_kl_dense_leg(torch, dev, q, kv, qi, ki, w, cu_t, max_seqlen, scale, npairs)
         print(f"[bench] dense indexer KL leg done: {res['indexer_kl_dense']['loss_fwd_bwd_ms']} ms", file=sys.stderr,
               flush=True)
+    if want("mla"):
+        res["mla"] = mla_leg(torch, dev, qi, ki, w)
+        print(f"[bench] mla leg done: {res['mla']['ms']} ms", file=sys.stderr, flush=True)
     if want("v4"):
         res["v4"] = v4_leg(torch, dev)
         print(f"[bench] v4 leg done: {res['v4']['ms']} ms", file=sys.stderr, flush=True)
