@@ -185,3 +185,46 @@ def test_v4_compress_many_entries_grid_stride(T, D, rate):
         eg = _err(g_got, leaf.grad)
         print(f"  {name}: normalised error {eg:.2e}", flush=True)
         assert eg < 1e-2, f"{name}: normalised error {eg:.3e}"
+
+
+@pytest.mark.parametrize("draw", range(12))
+def test_v4_compress_seeded_sweep(draw):
+    """Seeded draws (inputs from the seed alone): dim 64..512, rate 1..20, with and without
+    overlap, 1..4 documents of 0..70 tokens (empty ones, ones shorter than a window, partial
+    tails); forward and gradients against float64, gradients zero where a token feeds no entry."""
+    r = torch.Generator().manual_seed(1000 + draw)
+    D = [64, 128, 256, 512][int(torch.randint(0, 4, (1,), generator=r))]
+    rate = int(torch.randint(1, 21, (1,), generator=r))
+    overlap = bool(torch.randint(0, 2, (1,), generator=r))
+    lens = [int(x) for x in torch.randint(0, 71, (int(torch.randint(1, 5, (1,), generator=r)),), generator=r)]
+    if sum(n // rate for n in lens) == 0:
+        lens.append(rate * 2 + 1)
+    print(f"[v4 compress sweep] draw {draw}: D={D} rate={rate} overlap={overlap} lens={lens}", flush=True)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    T, C = cu[-1], (2 * D if overlap else D)
+    kv, gate, ape, norm_w = _inputs(T, D, rate, overlap, seed=2000 + draw)
+    leaves = [t.to(DEV).requires_grad_() for t in (kv, gate, ape, norm_w)]
+    out = v4.compress(*leaves, cu, rate, EPS, overlap)
+    n_ent = sum(n // rate for n in lens)
+    dout = (torch.randn(n_ent, D, generator=r) * 0.1).bfloat16()
+    out.backward(dout.to(DEV))
+    ref_l = [t.double().requires_grad_() for t in (kv, gate, ape, norm_w)]
+    ref = _oracle(*ref_l, cu, rate, overlap)
+    ref.backward(dout.double())
+    e = _err(out.detach(), ref.detach())
+    assert e < 1e-2, f"forward {e:.3e}"
+    for name, got, leaf in zip(("dkv", "dgate", "dape", "dnorm_w"), (t.grad for t in leaves), ref_l):
+        eg = _err(got, leaf.grad)
+        assert eg < 1e-2, f"{name}: {eg:.3e}"
+    covered = torch.zeros(T, C, dtype=torch.bool)
+    for a, b in zip(cu[:-1], cu[1:]):
+        n = (b - a) // rate
+        if overlap:
+            covered[a:a + n * rate, C // 2:] = True
+            covered[a:a + max(n - 1, 0) * rate, :C // 2] = True
+        else:
+            covered[a:a + n * rate] = True
+    for got in (leaves[0].grad, leaves[1].grad):
+        assert torch.count_nonzero(got.cpu()[~covered]) == 0

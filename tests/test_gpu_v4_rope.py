@@ -138,3 +138,44 @@ def test_grouped_projection_matches_float64():
         e = _err(got, r.detach())
         assert e < 1e-2 and torch.allclose(got.double(), r.detach(), rtol=2e-2, atol=2e-2 * r.abs().max().item()), \
             f"{name}: {e:.3e}"
+
+
+@pytest.mark.parametrize("draw", range(12))
+def test_norm_rope_seeded_sweep(draw):
+    """Seeded draws: dim 64..512, rope_dim 0..dim in steps of 8, 1..130 heads, norm on / off,
+    inverse or not, mscale 0.5..1.5: forward and backward of the HIP rows against the torch
+    composition (bit-exact without the norm) and float64 autograd (with it)."""
+    r = torch.Generator().manual_seed(3000 + draw)
+    D = [64, 128, 256, 512][int(torch.randint(0, 4, (1,), generator=r))]
+    rd = 8 * int(torch.randint(0, D // 8 + 1, (1,), generator=r))
+    H = int(torch.randint(1, 131, (1,), generator=r))
+    T = int(torch.randint(1, 90, (1,), generator=r))
+    norm = bool(torch.randint(0, 2, (1,), generator=r))
+    inverse = bool(torch.randint(0, 2, (1,), generator=r))
+    mscale = 0.5 + float(torch.rand(1, generator=r))
+    print(f"[v4 rope sweep] draw {draw}: T={T} H={H} D={D} rope={rd} norm={norm} inverse={inverse}", flush=True)
+    inv = 1.0 / (10000 ** (torch.arange(0, max(rd, 2), 2).double() / max(rd, 2)))
+    ang = torch.outer(torch.randint(0, 20000, (T,), generator=r).double(), inv).float().to(DEV)
+    cos, sin = v4.rope_tables(ang, mscale)
+    x = (torch.randn(T, H, D, generator=r) * 2).bfloat16().to(DEV)
+    dy = torch.randn(T, H, D, generator=r).bfloat16().to(DEV)
+    xa = x.clone().requires_grad_()
+    ya = v4._NormRope.apply(xa, cos, sin, rd, norm, 1e-6, inverse)
+    ya.backward(dy)
+    # float64 composition
+    xd = x.double().requires_grad_()
+    yd = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6) if norm else xd
+    if rd:
+        c, s = cos.double()[:, : rd // 2].view(T, 1, -1), sin.double()[:, : rd // 2].view(T, 1, -1)
+        if inverse:
+            s = -s
+        a, b = yd[..., D - rd:][..., 0::2], yd[..., D - rd:][..., 1::2]
+        yd = torch.cat([yd[..., :D - rd], torch.stack((a * c - b * s, b * c + a * s), -1).flatten(-2)], -1)
+    yd.backward(dy.double())
+    assert _err(ya, yd.detach()) < 1e-2
+    assert _err(xa.grad, xd.grad) < 1e-2
+    if not norm and rd == RD:   # the rotation alone: the fp32 torch composition bit for bit
+        xb = x.clone().requires_grad_()
+        yb = _torch_rope(xb, cos[:, : rd // 2].contiguous(), sin[:, : rd // 2].contiguous(), inverse)
+        yb.backward(dy)
+        assert torch.equal(ya, yb) and torch.equal(xa.grad, xb.grad)
