@@ -213,7 +213,7 @@ class _GroupedProj(torch.autograd.Function):
         ctx.save_for_backward(a, w)
         out = torch.empty(T, G * N, dtype=a.dtype, device=a.device)
         for g in range(G):
-            out[:, g * N:(g + 1) * N] = torch.mm(a[g], w[g].t())
+            torch.mm(a[g], w[g].t(), out=out[:, g * N:(g + 1) * N])
         return out
 
     @staticmethod
