@@ -704,7 +704,7 @@ def int8_staging_leg(torch, lib, _lib, q, kv, qi, ki, w, dout, cu_t, max_seqlen,
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip every leg after the cfg3 step")
