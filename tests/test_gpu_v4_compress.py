@@ -228,3 +228,17 @@ def test_v4_compress_seeded_sweep(draw):
             covered[a:a + n * rate] = True
     for got in (leaves[0].grad, leaves[1].grad):
         assert torch.count_nonzero(got.cpu()[~covered]) == 0
+
+
+def test_v4_compress_no_complete_window():
+    """Documents all shorter than a window: no entry, and every gradient zero (dkv, dgate, dape,
+    dnorm_w) -- the backward still runs its partial-tail items and column sums."""
+    print("[v4 compress] no complete window", flush=True)
+    cu, rate, D = [0, 3, 3, 6], 4, 128
+    kv, gate, ape, norm_w = _inputs(6, D, rate, True, seed=9)
+    leaves = [t.to(DEV).requires_grad_() for t in (kv, gate, ape, norm_w)]
+    out = v4.compress(*leaves, cu, rate, EPS, True)
+    assert out.shape == (0, D)
+    out.backward(torch.zeros(0, D, dtype=torch.bfloat16, device=DEV))
+    for t in leaves:
+        assert t.grad is not None and torch.count_nonzero(t.grad) == 0
