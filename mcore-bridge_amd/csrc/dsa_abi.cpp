@@ -849,7 +849,8 @@ static int rope_params(int64_t rows, int n_heads, int dim, int rope_dim, const f
       rows / n_heads > INT32_MAX)
     return DSA_ERR_INVALID_ARG;
   if (dim != 64 && dim != 128 && dim != 256 && dim != 512) return DSA_ERR_UNSUPPORTED;
-  if (rope_dim > 0 && (!cos || !sin || angle_stride < rope_dim / 2)) return DSA_ERR_INVALID_ARG;
+  if (rope_dim > 0 && angle_stride < rope_dim / 2) return DSA_ERR_INVALID_ARG;
+  if (rows > 0 && rope_dim > 0 && (!cos || !sin)) return DSA_ERR_INVALID_ARG;   // no rows: nothing is read
   p.rows = rows; p.n_heads = n_heads; p.tokens = (int)(rows / n_heads); p.dim = dim; p.rope_dim = rope_dim;
   p.cos = cos; p.sin = sin; p.angle_stride = angle_stride; p.inverse = inverse ? 1 : 0; p.groups = 1;
   return DSA_OK;

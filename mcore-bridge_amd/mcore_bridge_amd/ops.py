@@ -951,6 +951,8 @@ def v4_norm_rope(x: Tensor, cos: Tensor, sin: Tensor, rope_dim: int, norm: bool,
     T, H, D = x.shape
     _require(cos.shape[0] == T, "one cos / sin row per token")
     out = torch.empty_like(x)
+    if out.numel() == 0:
+        return out
     with torch.cuda.device(x.device):
         _lib.call("dsa_v4_norm_rope", _p(x), T * H, H, D, int(rope_dim), _p(cos), _p(sin), cos.stride(0), int(bool(norm)),
                   float(eps), int(bool(inverse)), _p(out), _stream(x.device))
@@ -964,6 +966,8 @@ def v4_norm_rope_bwd(x: Tensor, dout: Tensor, cos: Tensor, sin: Tensor, rope_dim
     _require(x.shape == dout.shape and x.dtype == torch.bfloat16 and x.is_contiguous(), "x must match dout")
     T, H, D = dout.shape
     dx = torch.empty_like(dout)
+    if dx.numel() == 0:
+        return dx
     with torch.cuda.device(dout.device):
         _lib.call("dsa_v4_norm_rope_bwd", _p(x), _p(dout), T * H, H, D, int(rope_dim), _p(cos), _p(sin), cos.stride(0),
                   int(bool(norm)), float(eps), int(bool(inverse)), _p(dx), _stream(dout.device))

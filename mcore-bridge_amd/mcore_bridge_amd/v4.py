@@ -132,6 +132,11 @@ def indexer_select(q_idx: Tensor, comp_k: Tensor, w: Tensor, cu_seqlens: Sequenc
     selected from (column j = entry ``doc offset + j``; ``-inf`` past each row)."""
     cu, lens, start = _docs(cu_seqlens, q_idx.device)
     T = cu[-1]
+    if comp_k.shape[0] == 0:   # no document holds a complete window: nothing to select
+        idx = torch.full((T, topk), -1, dtype=torch.int32, device=q_idx.device)
+        if not return_scores:
+            return idx
+        return idx, torch.full((T, 4), float("-inf"), dtype=torch.float32, device=q_idx.device)
     off = compressed_layout(cu, rate)
     offs = torch.repeat_interleave(torch.tensor(off[:-1], device=q_idx.device), lens)
     t = torch.arange(T, device=q_idx.device)
@@ -174,8 +179,8 @@ def norm_rope(x: Tensor, cos: Tensor, sin: Tensor, norm: bool, eps: float = 0.0,
     """``x [N, ..., D]`` rows: optional weightless RMS norm, then the interleaved RoPE of the last
     ``ROPE_DIM`` dims with row n's token angles (``cos / sin [N, ROPE_DIM / 2]``, mscale applied)."""
     shape = x.shape
-    y = _NormRope.apply(x.reshape(shape[0], -1, shape[-1]), cos, sin, ROPE_DIM, norm, eps, inverse)
-    return y.view(shape)
+    rows = x.reshape(shape[0], math.prod(shape[1:-1]), shape[-1])    # [N, heads, D] (N may be 0)
+    return _NormRope.apply(rows, cos, sin, ROPE_DIM, norm, eps, inverse).view(shape)
 
 
 def rope_tables(angles: Tensor, mscale: float) -> Tuple[Tensor, Tensor]:

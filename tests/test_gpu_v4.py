@@ -227,6 +227,42 @@ def test_v4_layer_mirror_thd_equals_per_document():
             _close(out_p[a:b], out_d, name=f"document {a}:{b}")
 
 
+@pytest.mark.parametrize("layer_type", ["compressed_sparse_attention", "heavily_compressed_attention"])
+def test_v4_layer_mirror_thd_backward_equals_per_document(layer_type):
+    """Packed THD forward + backward against one call per document: input gradients per document,
+    parameter gradients summed over the documents (the compressors' ragged tails and the row
+    transforms' per-document positions included; documents shorter than a window among them)."""
+    print(f"[v4 layer] THD backward vs per document: {layer_type}", flush=True)
+    m, g = _layer(layer_type, 9)
+    lens = [70, 3, 96, 41] if layer_type == "compressed_sparse_attention" else [70, 10, 96, 41]
+    cu = [0] + [sum(lens[:i + 1]) for i in range(len(lens))]
+    T, hidden = cu[-1], 256
+    x = torch.randn(T, 1, hidden, generator=g).bfloat16().to(DEV)
+    dy = (torch.randn(T, 1, hidden, generator=g) * 0.1).bfloat16().to(DEV)
+    rope, _ = _rope_tables(max(lens), DEV)
+    psp = types.SimpleNamespace(qkv_format="thd", cu_seqlens_q=torch.tensor(cu, dtype=torch.int32, device=DEV))
+    params = [p for p in m.parameters() if p.requires_grad]
+    xp = x.clone().requires_grad_()
+    out_p, _ = m(xp, None, rotary_pos_emb=rope, packed_seq_params=psp)
+    out_p.backward(dy)
+    grads_p = [None if p.grad is None else p.grad.clone() for p in params]
+    m.zero_grad(set_to_none=True)
+    dx_d = []
+    for a, b in zip(cu[:-1], cu[1:]):
+        xd = x[a:b].clone().requires_grad_()
+        out_d, _ = m(xd, None, rotary_pos_emb=rope)
+        out_d.backward(dy[a:b])
+        dx_d.append(xd.grad)
+    _close(xp.grad, torch.cat(dx_d), name="d input")
+    names = [n for n, p in m.named_parameters() if p.requires_grad]
+    for n, gp, p in zip(names, grads_p, params):
+        if gp is None or p.grad is None:
+            assert gp is None and p.grad is None, n
+            continue
+        scale = p.grad.double().abs().max().clamp_min(1e-30)
+        _close(gp / scale, p.grad / scale, name=n)
+
+
 @pytest.mark.parametrize("layer_type", ["sliding_attention", "compressed_sparse_attention",
                                         "heavily_compressed_attention"])
 def test_v4_layer_mirror_backward_matches_oracle(layer_type):
