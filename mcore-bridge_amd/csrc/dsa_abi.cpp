@@ -561,13 +561,19 @@ int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* idx, c
     const int rc = sparse_bwd(q, kv, idx, out, dout, lse, 0, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal, dq,
                               dkv, flags, workspace, rest, nullptr, nullptr, stream);
     if (rc != DSA_OK) return rc;
-    return dsa::launch_sink_grad(sinks, lse, delta, 0, n_heads, dsinks, as_stream(stream)) == 0 ? DSA_OK
-                                                                                                : DSA_ERR_LAUNCH;
+    return dsa::launch_sink_grad(sinks, lse, delta, 0, n_heads, dsinks, nullptr, 0, as_stream(stream)) == 0
+               ? DSA_OK
+               : DSA_ERR_LAUNCH;
   }
   const int rc = sparse_bwd(q, kv, idx, out, dout, lse, total_q, n_kv, n_heads, d_qk, d_v, topk, sm_scale, causal,
                             dq, dkv, flags, workspace, rest, nullptr, delta, stream);
   if (rc != DSA_OK) return rc;
-  return dsa::launch_sink_grad(sinks, lse, delta, total_q, n_heads, dsinks, as_stream(stream)) == 0
+  // the backward's part of the workspace is free again: the sums' partials go just below Delta (the
+  // pair-order scratch there is not read after the backward; the staged P tiles at its head stay)
+  const size_t pbytes = align_up(dsa::sink_grad_scratch_bytes(n_heads));
+  float* scratch = rest >= pbytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) + rest - pbytes) : nullptr;
+  return dsa::launch_sink_grad(sinks, lse, delta, total_q, n_heads, dsinks, scratch, scratch ? pbytes : 0,
+                               as_stream(stream)) == 0
              ? DSA_OK
              : DSA_ERR_LAUNCH;
 }

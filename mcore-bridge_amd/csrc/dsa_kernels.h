@@ -270,8 +270,11 @@ void launch_pair_csr(const int32_t* idx, int64_t idx_stride, int total_q, int to
 // d sinks[h] = -sum_t exp(sinks[h] - lse[t, h]) * delta[t, h] (the gradient of per-head
 // attention-sink logits from the forward's sink-including LSE and B1's Delta), one fixed-order
 // reduction per head.
+// scratch (at least sink_grad_scratch_bytes(n_heads), or null for the one-level form) holds the
+// partial sums of long batches
+size_t sink_grad_scratch_bytes(int n_heads);
 int launch_sink_grad(const float* sinks, const float* lse, const float* delta, int total_q, int n_heads,
-                     float* dsinks, hipStream_t stream);
+                     float* dsinks, float* scratch, size_t scratch_bytes, hipStream_t stream);
 int launch_decode_combine(const bf16_t* part_o, const float* part_lse, int batch, int n_heads, int n_split,
                           bf16_t* out, float* lse, hipStream_t stream);
 // Static per-device scratch of the allocation-free decode entry point (64 MiB): device address of

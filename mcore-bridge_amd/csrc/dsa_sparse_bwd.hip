@@ -886,7 +886,8 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(float* rows, int n_rows,
 }
 
 // d sinks: one workgroup per head, a fixed-order sum over the query rows (strided per thread, then
-// a wave and a cross-wave reduction), so the result is the same from run to run.
+// a wave and a cross-wave reduction), so the result is the same from run to run (short batches
+// and callers without scratch; longer ones take the two-level form below).
 __global__ __launch_bounds__(256) void sink_grad_kernel(const float* sinks, const float* lse, const float* delta,
                                                         int total_q, int n_heads, float* dsinks) {
   const int h = blockIdx.x;
@@ -903,11 +904,68 @@ __global__ __launch_bounds__(256) void sink_grad_kernel(const float* sinks, cons
   if (threadIdx.x == 0) dsinks[h] = 0.f - ((part[0] + part[1]) + (part[2] + part[3]));
 }
 
+// Long batches: the same sums in two fixed-order levels over coalesced rows.  Workgroup (chunk,
+// 64-head tile): lane = head, its 4 waves take every 4th row of the chunk; then one workgroup per
+// head tile adds the chunks' partials, its 16 waves every 16th chunk, and the waves in order.
+constexpr int kSinkChunks = 256;
+__global__ __launch_bounds__(256) void sink_grad_partial_kernel(const float* sinks, const float* lse,
+                                                                const float* delta, int total_q, int n_heads,
+                                                                int rows_per_chunk, float* part) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = blockIdx.y * 64 + lane;
+  const int t0 = blockIdx.x * rows_per_chunk, t1 = min(total_q, t0 + rows_per_chunk);
+  float acc = 0.f;
+  if (h < n_heads) {
+    const float sk = sinks[h];
+#pragma unroll 4
+    for (int t = t0 + wave; t < t1; t += 4) {
+      const float l = lse[(int64_t)t * n_heads + h];
+      if (l != -INFINITY) acc += expf(sk - l) * delta[(int64_t)t * n_heads + h];
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && h < n_heads)
+    part[(int64_t)blockIdx.x * n_heads + h] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+}
+
+__global__ __launch_bounds__(1024) void sink_grad_final_kernel(const float* part, int chunks, int n_heads,
+                                                               float* dsinks) {
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = blockIdx.x * 64 + lane;
+  float acc = 0.f;
+  if (h < n_heads) {
+#pragma unroll 4
+    for (int c = wave; c < chunks; c += 16) acc += part[(int64_t)c * n_heads + h];
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && h < n_heads) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) s += red[w][lane];
+    dsinks[h] = 0.f - s;
+  }
+}
+
+size_t sink_grad_scratch_bytes(int n_heads) { return sizeof(float) * (size_t)kSinkChunks * (size_t)n_heads; }
+
 int launch_sink_grad(const float* sinks, const float* lse, const float* delta, int total_q, int n_heads,
-                     float* dsinks, hipStream_t stream) {
+                     float* dsinks, float* scratch, size_t scratch_bytes, hipStream_t stream) {
   if (n_heads < 1) return 0;
-  hipLaunchKernelGGL(sink_grad_kernel, dim3(n_heads), dim3(256), 0, stream, sinks, lse, delta, total_q, n_heads,
-                     dsinks);
+  if (scratch != nullptr && scratch_bytes >= sink_grad_scratch_bytes(n_heads) && total_q >= 4 * kSinkChunks) {
+    const int rows = (total_q + kSinkChunks - 1) / kSinkChunks;
+    const int chunks = (total_q + rows - 1) / rows;
+    const int tiles = (n_heads + 63) / 64;
+    hipLaunchKernelGGL(sink_grad_partial_kernel, dim3(chunks, tiles), dim3(256), 0, stream, sinks, lse, delta,
+                       total_q, n_heads, rows, scratch);
+    hipLaunchKernelGGL(sink_grad_final_kernel, dim3(tiles), dim3(1024), 0, stream, scratch, chunks, n_heads, dsinks);
+  } else {
+    hipLaunchKernelGGL(sink_grad_kernel, dim3(n_heads), dim3(256), 0, stream, sinks, lse, delta, total_q, n_heads,
+                       dsinks);
+  }
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
